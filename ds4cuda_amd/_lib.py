@@ -1,0 +1,61 @@
+"""ctypes binding of libds4hip.so (the C-ABI declared in include/ds4hip.h).
+
+The library is loaded from the package directory only; there is no fallback:
+if it is missing, every call raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libds4hip.so"
+
+_vp, _i, _ll, _sz = C.c_void_p, C.c_int, C.c_longlong, C.c_size_t
+
+# name -> argtypes (all return int)
+SIGNATURES: dict[str, list] = {
+    "ds4hip_get_last_error": [],
+    "ds4hip_set_last_error": [_i],
+    "ds4hip_version": [],
+    "ds4hip_fp8_kv_quantize_round_trip_f32": [_vp, _vp, _i, _i, _i, _vp],
+    "ds4hip_fp8_kv_quantize_append": [_vp, _i, _i, _i, _vp, _vp, _vp, _ll, _vp, _vp],
+    "ds4hip_flash_attn_decode_raw_f32": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp],
+    "ds4hip_flash_attn_decode_mixed_f32": [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp],
+    "ds4hip_flash_attn_decode_fp8_workspace_size": [_vp, _i, C.POINTER(_sz)],
+    "ds4hip_flash_attn_decode_fp8": [
+        _vp, _i, _ll, _vp, _ll, _vp, _ll, _vp, _vp, _vp, _vp, _i, _vp, _ll, _vp, _ll, _vp, _i,
+        _i, _i, _i, _i, _vp, _sz, _i, _vp],
+}
+
+_lib = None
+
+
+class Ds4HipError(RuntimeError):
+    def __init__(self, name: str, code: int):
+        kind = "invalid argument" if code == -22 else (
+            f"hip error {-1000 - code}" if code <= -1000 else "error")
+        super().__init__(f"{name} failed: {code} ({kind})")
+        self.code = code
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -m ds4cuda_amd.build` "
+                "(there is no CPU fallback)")
+        l = C.CDLL(str(LIB_PATH))
+        for name, args in SIGNATURES.items():
+            fn = getattr(l, name)
+            fn.argtypes = args
+            fn.restype = C.c_int
+        _lib = l
+    return _lib
+
+
+def call(name: str, *args) -> int:
+    rc = getattr(lib(), name)(*args)
+    if rc != 0:
+        raise Ds4HipError(name, rc)
+    return rc

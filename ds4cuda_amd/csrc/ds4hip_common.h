@@ -1,0 +1,128 @@
+// ds4hip_common.h — shared device helpers for the gfx950 attention-path
+// kernels: vector types, the exact E4M3FN encoder, the power-of-two scale
+// rule, bf16/f16 conversions and the C-ABI error plumbing.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ds4hip {
+
+typedef _Float16 half_t;
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int uint4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int uint2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kEINVAL = -22;
+constexpr int kHipErrBase = -1000;   // returned as kHipErrBase - hipError_t
+
+// ---- scale rule -------------------------------------------------------------
+// The reference picks scale = 2^ceil(log2(amax/448)) per 64-element block
+// (cuda/fp8_kv.cu:174-176). With log2 evaluated as a correctly rounded fp32
+// function of the fp32 quotient y = fl(amax/448), ceil(fl(log2 y)) equals
+//   k       when y = 2^k exactly,
+//   k       when y = 2^k (1 + M 2^-23) and log2(1 + M 2^-23) is below half the
+//           fp32 spacing next to k (fl(k + t) rounds back to k),
+//   k + 1   otherwise.
+// The rounding-back case only happens for a few mantissas M just above a power
+// of two. For y in [2^-126, 2^127) the bound M <= limit(s) with
+// s = -log2(half spacing) is the integer part of (2^(2^-s) - 1) 2^23:
+//   s=18 -> 22, s=19 -> 11, s=20 -> 5, s=21 -> 2, s=22 -> 1, s>=23 -> 0.
+// tests/test_fp8_rule.py checks this rule against ceil(float(log2(double y)))
+// for every fp32 y in [2^-30, 2^30).
+__host__ __device__ inline int floor_log2_u32(uint32_t a) {
+    int r = 0;
+    while (a >>= 1) ++r;
+    return r;
+}
+
+__host__ __device__ inline int ceil_log2_cr(float y) {
+    uint32_t u;
+    __builtin_memcpy(&u, &y, 4);
+    const int k = (int)((u >> 23) & 0xFF) - 127;
+    const uint32_t M = u & 0x7FFFFFu;
+    if (M == 0) return k;
+    if (k == 0) return 1;
+    int s;
+    if (k > 0) {
+        s = 24 - floor_log2_u32((uint32_t)k);
+    } else {
+        const uint32_t a = (uint32_t)(-k);
+        const int fl = floor_log2_u32(a);
+        s = ((a & (a - 1)) == 0) ? 25 - fl : 24 - fl;
+    }
+    uint32_t limit = 0;
+    switch (s) {
+    case 18: limit = 22; break;
+    case 19: limit = 11; break;
+    case 20: limit = 5; break;
+    case 21: limit = 2; break;
+    case 22: limit = 1; break;
+    default: limit = s < 18 ? 0xFFFFFFFFu : 0; break;   // s < 18 unreachable for y < 2^127
+    }
+    return (M <= limit) ? k : k + 1;
+}
+
+// Scale exponent of one 64-block from its max |x| (floor 1e-4, fp8_kv.cu:175).
+__host__ __device__ inline int fp8_block_exp(float amax) {
+    const float a = amax > 1.0e-4f ? amax : 1.0e-4f;
+    // fl(a / 448): the double quotient rounded to fp32 equals the fp32 quotient
+    // because a / 7 never lies within 2^-53 of an fp32 rounding midpoint.
+    const float y = (float)((double)a / 448.0);
+    return ceil_log2_cr(y);
+}
+
+// ---- E4M3FN encoder -------------------------------------------------------------
+// Nearest E4M3FN code of v, |v| <= 448, ties to the even code (the picker of
+// cuda/fp8_kv.cu:102-131 is round-to-nearest-even in code space). Sign bit set
+// when v < 0 (the reference takes the sign from v < 0, so -0 encodes as +0).
+__host__ __device__ inline uint32_t e4m3_encode(float v) {
+    uint32_t u;
+    __builtin_memcpy(&u, &v, 4);
+    const uint32_t sign = (v < 0.0f) ? 0x80u : 0u;
+    const uint32_t au = u & 0x7FFFFFFFu;
+    float av;
+    __builtin_memcpy(&av, &au, 4);
+    uint32_t mag;
+    if (au < 0x3C800000u) {                    // |v| < 2^-6: subnormal codes m * 2^-9
+        mag = (uint32_t)__builtin_rintf(av * 512.0f);   // exact scaling, RNE
+    } else {
+        const uint32_t e8 = au >> 23;          // >= 121
+        const uint32_t m = au & 0x7FFFFFu;
+        uint32_t r = m >> 20;
+        const uint32_t rem = m & 0xFFFFFu;
+        if (rem > 0x80000u || (rem == 0x80000u && (r & 1u))) ++r;
+        mag = ((e8 - 120u) << 3) + r;          // carry of r into the exponent is intended
+    }
+    return sign | mag;
+}
+
+// ---- conversions ------------------------------------------------------------
+__host__ __device__ inline float bf16_to_f32(uint16_t h) {
+    const uint32_t u = (uint32_t)h << 16;
+    float f;
+    __builtin_memcpy(&f, &u, 4);
+    return f;
+}
+
+__device__ inline uint16_t f32_to_f16_bits(float x) {
+    const half_t h = (half_t)x;                // v_cvt_f16_f32, RNE
+    uint16_t b;
+    __builtin_memcpy(&b, &h, 2);
+    return b;
+}
+
+__device__ inline float f16_bits_to_f32(uint16_t b) {
+    half_t h;
+    __builtin_memcpy(&h, &b, 2);
+    return (float)h;
+}
+
+__host__ inline int hip_status(hipError_t e) { return e == hipSuccess ? 0 : kHipErrBase - (int)e; }
+
+}  // namespace ds4hip
+
+// Records the last failing status for the void-returning C++ shims.
+extern "C" int ds4hip_set_last_error(int code);

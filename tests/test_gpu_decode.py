@@ -1,0 +1,131 @@
+"""Decode attention on the GPU vs the oracle. Outputs must satisfy
+max|gpu - oracle| <= 2e-3 * RMS(oracle output) (fp32 accumulation)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from ds4cuda_amd import ops, synth
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+def check(got, ref, tol=TOL):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    rms = np.sqrt(np.mean(ref ** 2))
+    err = np.abs(got - ref).max()
+    assert np.isfinite(got).all()
+    assert err <= tol * rms, f"max err {err:.3e} > {tol} * rms {rms:.3e}"
+
+
+def make_cache(n_rows, seed, device, outlier=0.01):
+    x = synth.kv_rows(seed, 1, n_rows, outlier_frac=outlier)
+    codes, sexp, tail, _ = O.fp8_quant_rows(x)
+    cache = ops.Fp8KVCache.empty(n_rows, device=device)
+    cache.append(torch.from_numpy(x).to(device))
+    return cache, (codes, sexp, tail)
+
+
+def q_bf16(seed, n_prob):
+    bits = synth.to_bf16_bits(synth.normal(seed, 2, n_prob * 64 * 512)).reshape(n_prob, 64, 512)
+    return bits, synth.bf16_bits_to_f32(bits)
+
+
+def sinks_for(seed, n_prob):
+    return synth.normal(seed, 3, n_prob * 64).reshape(n_prob, 64)
+
+
+@pytest.mark.parametrize("n_kv", [1, 17, 32, 33, 100, 1000, 4096])
+def test_fp8_single_problem(gpu, n_kv):
+    cache, (codes, sexp, tail) = make_cache(n_kv, 11, gpu)
+    bits, qf = q_bf16(12, 1)
+    sinks = sinks_for(13, 1)
+    out = torch.zeros((1, 64, 512), dtype=torch.float32, device=gpu)
+    q = torch.from_numpy(bits.view(np.int16)).to(gpu).view(torch.bfloat16)
+    ops.flash_attn_decode_fp8(q, torch.from_numpy(sinks).to(gpu), out, cache, [n_kv])
+    torch.cuda.synchronize()
+    ref = O.attn_decode_fp8(qf[0], codes, sexp, tail, np.arange(n_kv), sinks[0])
+    check(out[0].cpu().numpy(), ref)
+
+
+def test_fp8_multi_problem_layers_and_fp32_q(gpu):
+    counts = [300, 0, 64, 1025, 7]
+    base = np.concatenate([[0], np.cumsum(counts)[:-1]]) + 3
+    total = int(sum(counts)) + 3
+    cache, (codes, sexp, tail) = make_cache(total, 21, gpu)
+    n = len(counts)
+    qf = synth.normal(22, 2, n * 64 * 512).reshape(n, 64, 512) * 2.0
+    sinks = sinks_for(23, n)
+    sinks[1, :5] = -np.inf
+    out = torch.zeros((n, 64, 512), dtype=torch.float32, device=gpu)
+    ops.flash_attn_decode_fp8(torch.from_numpy(qf).to(gpu), torch.from_numpy(sinks).to(gpu), out,
+                              cache, counts, row_base=torch.from_numpy(base.astype(np.int64)).to(gpu))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    for p in range(n):
+        ref = O.attn_decode_fp8(qf[p], codes, sexp, tail, base[p] + np.arange(counts[p]), sinks[p])
+        if counts[p] == 0:
+            assert (got[p] == 0).all()
+        else:
+            check(got[p], ref)
+
+
+def test_fp8_sparse_rows_and_pages(gpu):
+    n_rows = 4096
+    cache, (codes, sexp, tail) = make_cache(n_rows, 31, gpu)
+    rng = np.random.default_rng(32)
+    # two sequences, each with a page table over the cache (256-row pages)
+    pt = np.stack([rng.permutation(16), rng.permutation(16)]).astype(np.int32)
+    idx = np.stack([np.sort(rng.choice(4096, 700, replace=False)),
+                    np.sort(rng.choice(4096, 700, replace=False))]).astype(np.int32)
+    counts = [700, 513]
+    bits, qf = q_bf16(33, 2)
+    sinks = sinks_for(34, 2)
+    out = torch.zeros((2, 64, 512), dtype=torch.float32, device=gpu)
+    q = torch.from_numpy(bits.view(np.int16)).to(gpu).view(torch.bfloat16)
+    ops.flash_attn_decode_fp8(q, torch.from_numpy(sinks).to(gpu), out, cache, counts,
+                              row_idx=torch.from_numpy(idx).to(gpu),
+                              page_table=torch.from_numpy(pt).to(gpu), page_rows=256)
+    torch.cuda.synchronize()
+    for p in range(2):
+        pos = idx[p, :counts[p]]
+        phys = pt[p][pos // 256] * 256 + pos % 256
+        ref = O.attn_decode_fp8(qf[p], codes, sexp, tail, phys, sinks[p])
+        check(out[p].cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("n_kv", [1, 10, 128, 300])
+def test_raw_f32_launcher(gpu, n_kv):
+    K = synth.kv_rows(41, 1, n_kv) * 1.5
+    Q = synth.normal(42, 2, 64 * 512).reshape(64, 512)
+    sinks = sinks_for(43, 1)[0]
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(gpu)
+    out = torch.zeros((64, 512), dtype=torch.float32, device=gpu)
+    Kt = t(K)
+    ops.launch_flash_attn_decode_raw_f32(t(Q), Kt, Kt, t(sinks), out, 64, n_kv, 512)
+    torch.cuda.synchronize()
+    ref = O.attn_decode_mixed_f32(Q, K, None, None, sinks)
+    check(out.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("n_raw,n_comp", [(128, 0), (0, 50), (128, 300), (5, 1000)])
+def test_mixed_f32_launcher(gpu, n_raw, n_comp):
+    raw = synth.kv_rows(51, 1, max(n_raw, 1))[:n_raw]
+    comp = synth.kv_rows(52, 1, max(n_comp, 1))[:n_comp] * 0.7
+    mask = (synth.uniform(53, 1, n_comp) < 0.5).astype(np.int32)
+    Q = synth.normal(54, 2, 64 * 512).reshape(64, 512)
+    sinks = sinks_for(55, 1)[0]
+    t = lambda a, dt=np.float32: torch.from_numpy(np.ascontiguousarray(a, dt)).to(gpu)
+    for use_mask in (True, False):
+        out = torch.zeros((64, 512), dtype=torch.float32, device=gpu)
+        ops.launch_flash_attn_decode_mixed_f32(
+            t(Q), t(raw) if n_raw else None, t(comp) if n_comp else None,
+            t(mask, np.int32) if (use_mask and n_comp) else None, t(sinks), out, 64, n_raw,
+            n_comp, 512)
+        torch.cuda.synchronize()
+        ref = O.attn_decode_mixed_f32(Q, raw if n_raw else None, comp if n_comp else None,
+                                      mask if use_mask else None, sinks)
+        check(out.cpu().numpy(), ref)

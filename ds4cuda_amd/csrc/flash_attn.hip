@@ -231,7 +231,7 @@ __device__ inline void stage_start(const DecodeArgs &A, long long *s_start) {
     // DecodeArgs is the only kernel argument, so it sits at offset 0 of the
     // kernarg segment and the table can be read through a plain pointer.
     const long long *tab = reinterpret_cast<const long long *>(
-        static_cast<const char *>(__builtin_amdgcn_kernarg_segment_ptr()) +
+        (const char *)__builtin_amdgcn_kernarg_segment_ptr() +
         offsetof(DecodeArgs, start));
     for (int i = threadIdx.x; i <= kMaxProb; i += blockDim.x) s_start[i] = tab[i];
     __syncthreads();

@@ -154,7 +154,7 @@ def main():
                    "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "decode_partial_kernel<fp8, bf16 q>",
+                     "kernel": "decode_fp8_kernel<bf16 q>",
                      "kernel_ms": round(k_ms, 4), "bytes_per_launch": step_bytes},
     }
     if not args.no_cpu_baseline:

@@ -39,11 +39,31 @@ def _compile(src: Path) -> Path:
     return obj
 
 
+# Kernels whose copy ring counts outstanding vector-memory operations: a
+# register spill (scratch store) would break that count, so the build refuses it.
+NO_SPILL_KERNELS = ("decode_fp8_kernelILb0E",)
+
+
+def check_spills(src: Path) -> None:
+    cmd = [HIPCC, *FLAGS, "-I", str(ROOT / "include"), "--cuda-device-only", "-c", str(src),
+           "-o", os.devnull, "-Rpass-analysis=kernel-resource-usage"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    name = None
+    for line in r.stderr.splitlines():
+        if "Function Name:" in line:
+            name = line.split("Function Name:")[1].split("[")[0].strip()
+        elif "VGPRs Spill:" in line and name and any(k in name for k in NO_SPILL_KERNELS):
+            n = int(line.split("VGPRs Spill:")[1].split("[")[0])
+            if n:
+                raise RuntimeError(f"{name} spills {n} VGPRs; its copy-ring waits require none")
+
+
 def build_lib(verbose: bool = False) -> Path:
     OBJ.mkdir(exist_ok=True)
     srcs = sorted(CSRC.glob("*.hip"))
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
         objs = list(ex.map(_compile, srcs))
+    check_spills(CSRC / "flash_attn.hip")
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     r = subprocess.run(cmd, capture_output=True, text=True)

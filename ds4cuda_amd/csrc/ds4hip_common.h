@@ -14,6 +14,7 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef unsigned int uint4_t __attribute__((ext_vector_type(4)));
 typedef unsigned int uint2_t __attribute__((ext_vector_type(2)));
+typedef short short4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kEINVAL = -22;
 constexpr int kHipErrBase = -1000;   // returned as kHipErrBase - hipError_t

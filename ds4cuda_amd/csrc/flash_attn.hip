@@ -13,17 +13,19 @@
 // each problem with the sink. Each workgroup covers all 64 heads: wave w owns
 // heads [16w, 16w+16), so every KV row is dequantized and used by 4 waves.
 //
-// Per 32-row tile, per wave:
-//   S^T[32 rows x 16 heads] = K[32 x 512] . Q^T  — v_mfma_f32_16x16x32_f16,
-//     A = K fragments loaded straight from HBM into registers (lane = row,
-//     16 consecutive dims), dequantized with v_cvt_scalef32_pk_f16_fp8;
-//     B = Q^T held in registers for the whole chunk;
-//   online softmax in the exp2 domain, P kept in registers: the S^T output
+// FP8 kernel, per 32-row tile:
+//   * the tile's raw bytes (codes, f16 tail, exponents: 584 B/row) are copied
+//     HBM -> LDS by global_load_lds_dwordx4, three tiles ahead of use (4-stage
+//     ring), so HBM latency is covered without holding registers;
+//   * S^T[32 rows x 16 heads] = K[32 x 512] . Q^T per wave with
+//     v_mfma_f32_16x16x32_f16: A = K fragments read from the stage (lane = row,
+//     16 dims = one 16-byte chunk) and dequantized with
+//     v_cvt_scalef32_pk_f16_fp8; B = Q^T held in registers for the segment;
+//   * online softmax in the exp2 domain; P stays in registers: the S^T output
 //     layout (lane = head, 4+4 rows) is already the A layout of P . V;
-//   O[16 heads x 512] += P[16 x 32] . V[32 x 512] — B = V^T fragments read
-//     from LDS as 16-byte vectors. The V^T tile is written once per workgroup:
-//     wave w transposes dims [128w, 128w+128) from the registers it already
-//     holds.
+//   * O[16 heads x 512] += P[16 x 32] . V[32 x 512] with B = V^T fragments
+//     read from LDS as 16-byte vectors. Wave w writes V^T for dims
+//     [128w, 128w+128) from the registers it already holds.
 // Rows inside a V^T line are stored in the order the P fragment uses
 // (row 4a+c of half-tile t at position 8a+4t+c), so each B fragment is one
 // contiguous 16-byte LDS read.
@@ -47,6 +49,7 @@ constexpr int kTile = 32;        // rows per tile
 constexpr int kVtStride = 40;    // halves per V^T line (32 rows + 8 pad)
 constexpr int kMaxProb = 128;
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kFp8WgPerCu = 1;   // the FP8 kernel's LDS ring allows one workgroup per CU
 
 struct DecodeArgs {
     const void *q;
@@ -112,50 +115,6 @@ __device__ inline long long phys_row(const DecodeArgs &A, int p, long long r) {
         return (page << A.page_shift) | (pos & ((1LL << A.page_shift) - 1));
     }
     return (A.row_base ? A.row_base[p] : (long long)p * A.row_base_stride) + pos;
-}
-
-// Raw registers of one half-tile (16 rows) for one lane: its row's 16-dim
-// slice of each of the 7 code blocks, the matching 16 tail dims, and the
-// row's 8 scale exponents.
-struct Fp8Frag {
-    uint4_t c[7];
-    uint4_t t0, t1;
-    uint2_t e;
-};
-
-__device__ inline void load_fp8_frag(const DecodeArgs &A, long long phys, int q, bool valid,
-                                     Fp8Frag &f) {
-    if (valid) {
-        const uint4_t *cp = reinterpret_cast<const uint4_t *>(A.codes + phys * kNope + 16 * q);
-#pragma unroll
-        for (int b = 0; b < 7; ++b) f.c[b] = __builtin_nontemporal_load(cp + 4 * b);
-        const uint4_t *tp = reinterpret_cast<const uint4_t *>(A.tail + phys * kRot + 16 * q);
-        f.t0 = __builtin_nontemporal_load(tp);
-        f.t1 = __builtin_nontemporal_load(tp + 1);
-        f.e = *reinterpret_cast<const uint2_t *>(A.sexp + phys * 8);
-    } else {
-#pragma unroll
-        for (int b = 0; b < 7; ++b) f.c[b] = uint4_t{0, 0, 0, 0};
-        f.t0 = f.t1 = uint4_t{0, 0, 0, 0};
-        f.e = uint2_t{0, 0};
-    }
-}
-
-// Dequantized A fragments for block b (dims 64b+16q+[0,8) and +[8,16)).
-__device__ inline void dequant_fp8(const Fp8Frag &f, int b, half8_t &a0, half8_t &a1) {
-    if (b < 7) {
-        const uint32_t ew = b < 4 ? f.e[0] : f.e[1];
-        const int e = (int)(int8_t)((ew >> (8 * (b & 3))) & 0xFF);
-        const float s = pow2f(e);
-        const uint4_t c = f.c[b];
-        a0 = make_half8(cvt_fp8x2<false>(c[0], s), cvt_fp8x2<true>(c[0], s),
-                        cvt_fp8x2<false>(c[1], s), cvt_fp8x2<true>(c[1], s));
-        a1 = make_half8(cvt_fp8x2<false>(c[2], s), cvt_fp8x2<true>(c[2], s),
-                        cvt_fp8x2<false>(c[3], s), cvt_fp8x2<true>(c[3], s));
-    } else {
-        a0 = __builtin_bit_cast(half8_t, f.t0);
-        a1 = __builtin_bit_cast(half8_t, f.t1);
-    }
 }
 
 // fp32 rows (reference launchers): the lane's 16-dim slice of block b,
@@ -237,23 +196,586 @@ __device__ inline void stage_start(const DecodeArgs &A, long long *s_start) {
     __syncthreads();
 }
 
-template <bool kFp8, bool kQf32>
-__global__ __launch_bounds__(256) void decode_partial_kernel(const DecodeArgs A) {
+// max / sum over lanes l, l^16, l^32, l^48 with VALU lane swaps (no LDS).
+__device__ inline float xmax_16_32(float v) {
+    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ inline float xsum_16_32(float v) {
+    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// Barrier for this kernel's LDS pipeline: waits for this wave's LDS
+// operations, then s_barrier. Unlike __syncthreads() it does not wait for
+// outstanding global->LDS copies (vmcnt), which keeps the prefetch in flight.
+__device__ inline void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+struct SegState {
+    float m_run;
+    float l_run;
+    float4_t o[32];
+};
+
+// Online softmax of one 32-row tile (S^T accumulators acc[t][r] = row
+// 16t+4q+r, head j) and the P fragment for P . V. row_ok(t, r) says whether
+// that row takes part.
+template <typename RowOk>
+__device__ inline half8_t softmax_tile(const float4_t *acc, float kq_log2, int q, SegState &S,
+                                       RowOk row_ok) {
+    float s[2][4];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            s[t][r] = row_ok(t, r) ? acc[t][r] * kq_log2 : -INFINITY;
+            tmax = fmaxf(tmax, s[t][r]);
+        }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const float m_new = fmaxf(S.m_run, tmax);
+    const bool none = m_new == -INFINITY;
+    const float alpha = none ? 1.0f : __builtin_amdgcn_exp2f(S.m_run - m_new);
+    half8_t pf;
+    float psum = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float pv = none ? 0.0f : __builtin_amdgcn_exp2f(s[t][r] - m_new);
+            psum += pv;
+            pf[4 * t + r] = (half_t)pv;
+        }
+    S.l_run = S.l_run * alpha + psum;
+    S.m_run = m_new;
+    if (__any(alpha != 1.0f)) {
+        // O rows are heads 16w+4q+r; their alpha sits in lanes 4q+r
+        float ar[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ar[r] = __shfl(alpha, 4 * q + r);
+#pragma unroll
+        for (int n = 0; n < 32; ++n)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) S.o[n][r] *= ar[r];
+    }
+    return pf;
+}
+
+__device__ inline void pv_tile(const half_t *vt, half8_t pf, int j, int q, SegState &S) {
+#pragma unroll
+    for (int n = 0; n < 32; ++n) {
+        const half8_t vb = *reinterpret_cast<const half8_t *>(&vt[(16 * n + j) * kVtStride + 8 * q]);
+        S.o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf, vb, S.o[n], 0, 0, 0);
+    }
+}
+
+// Writes this wave's V^T slice (dims 64b+16q .. +15 of row `prow`).
+__device__ inline void vt_write(half_t *vt, int b, int q, int prow, half8_t a0, half8_t a1) {
+    const int d0 = 64 * b + 16 * q;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        vt[(d0 + i) * kVtStride + prow] = a0[i];
+        vt[(d0 + 8 + i) * kVtStride + prow] = a1[i];
+    }
+}
+
+__device__ inline void emit_partial(const DecodeArgs &A, long long slot, int wave, int j, int q,
+                                    int head, int p, SegState &S) {
+    float l = S.l_run;
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    float *wo = A.ws_o + slot * (kH * kD) + (wave * 16 + 4 * q) * kD + j;
+    // keep the 128 store addresses from being hoisted out of the tile loop
+    asm volatile("" : "+v"(wo));
+#pragma unroll
+    for (int n = 0; n < 32; ++n)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) wo[r * kD + 16 * n] = S.o[n][r];
+    if (q == 0) {
+        A.ws_ml[slot * 2 * kH + head] = S.m_run;
+        A.ws_ml[slot * 2 * kH + kH + head] = l;
+    }
+    if (threadIdx.x == 0) A.ws_prob[slot] = p;
+}
+
+__device__ inline void seg_init(SegState &S) {
+    S.m_run = -INFINITY;
+    S.l_run = 0.0f;
+#pragma unroll
+    for (int n = 0; n < 32; ++n) S.o[n] = float4_t{0, 0, 0, 0};
+}
+
+// ---- FP8 cache kernel ------------------------------------------------------------------
+//
+// Copy ring. Each 32-row tile is copied HBM -> LDS by global_load_lds three
+// tiles ahead of use (4-stage ring). Copy instruction i < 18 moves 64-dim
+// block i>>1 (blocks 0..6 = codes, 7..8 = the f16 tail) of the 16 rows of
+// half-tile i&1: lane L fetches 16-byte chunk (L&3) ^ ((L>>4)&3)... of row
+// L>>2, so every row contributes one whole 64-byte segment per instruction
+// and the chunk order inside the LDS segment is XOR-swizzled by the row,
+// which makes the fragment reads below bank-conflict free. Instruction 18
+// copies the 32 rows' scale exponents; instruction 19 is a filler that
+// keeps every wave at 5 copies per stage.
+//
+// Work split inside a workgroup (4 waves): wave w owns head dims
+// [128w, 128w+128) — code blocks 2w, 2w+1 (wave 3: block 6 and the tail) —
+// and heads [16w, 16w+16) for the softmax. Per tile:
+//   1. partial scores over the wave's dims for all 64 heads,
+//      S_w^T[32 rows x 64 heads] (v_mfma_f32_16x16x32_f16, A = the wave's own
+//      dequantized K fragments, B = Q^T slice in registers);
+//   2. reduce-scatter through LDS: wave w sums the four partials of its 16
+//      heads, runs the online softmax and publishes P (f16) and the rescale
+//      factors of its heads;
+//   3. O_w[64 heads x 128 dims] += P . V_w with V_w the wave's own f16 slice,
+//      kept row-major in LDS and read as MFMA B fragments with
+//      ds_read_b64_tr_b16 (transposing 16-bit load).
+// Every KV element is dequantized once and read from HBM once.
+
+constexpr int kStages = 4;
+constexpr int kStageBytes = 18 * 1024 + 256 + 256;
+constexpr int kSexpOff = 18 * 1024;
+constexpr int kCopiesPerWave = 5;
+constexpr int kVRowBytes = 288;                  // 128 dims f16 + 32 B pad (bank spread)
+constexpr int kVTileBytes = kTile * kVRowBytes;  // per wave
+
+__device__ inline uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+// LDS byte offset of 16-byte chunk c (0..3) of row k (0..15) in copy region
+// `region` (= 2*block + half) of a stage.
+__device__ inline int stage_off(int region, int k, int c) {
+    return region * 1024 + 64 * k + 16 * (c ^ ((k >> 1) & 3));
+}
+
+__device__ inline void issue_stage(const DecodeArgs &A, uint8_t *stage, long long ph, int lane,
+                                   int wave) {
+    // ph = physical row of tile row (lane & 31)
+    const int k = lane >> 2;
+    const long long ph_h0 = __shfl(ph, k);          // tile row k
+    const long long ph_h1 = __shfl(ph, 16 + k);     // tile row 16 + k
+    const long long ph_e = __shfl(ph, lane >> 1);   // exponent copy: tile row lane>>1
+    const int c = (lane & 3) ^ ((k >> 1) & 3);
+#pragma unroll
+    for (int kk = 0; kk < kCopiesPerWave; ++kk) {
+        const int i = wave * kCopiesPerWave + kk;
+        if (i < 18) {
+            const int blk = i >> 1;
+            const long long row = (i & 1) ? ph_h1 : ph_h0;
+            const uint8_t *g = blk < 7
+                ? A.codes + row * kNope + blk * 64 + c * 16
+                : reinterpret_cast<const uint8_t *>(A.tail) + row * (2 * kRot) + (blk - 7) * 64 + c * 16;
+            __builtin_amdgcn_global_load_lds(g, stage + i * 1024, 16, 0, 0);
+        } else {
+            const uint8_t *g = reinterpret_cast<const uint8_t *>(A.sexp) + ph_e * 8 + (lane & 1) * 4;
+            __builtin_amdgcn_global_load_lds(g, stage + kSexpOff + (i - 18) * 256, 4, 0, 0);
+        }
+    }
+}
+
+// Waits until at most `pending_stages` stages of this wave's copies are in flight.
+__device__ inline void wait_copies(int pending_stages) {
+    switch (pending_stages) {
+    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    case 1: asm volatile("s_waitcnt vmcnt(5)" ::: "memory"); break;
+    case 2: asm volatile("s_waitcnt vmcnt(10)" ::: "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(15)" ::: "memory"); break;
+    }
+}
+
+// LDS accessors used inside the copy-ring loop. They are inline assembly so
+// that the compiler does not make them wait for the outstanding global->LDS
+// copies (it cannot tell the ring apart from the other LDS buffers and would
+// insert vmcnt(0), draining the ring every tile). Reads return without
+// waiting; lds_wait() completes them and ties the results to the wait.
+template <typename T>
+__device__ inline void lds_st128(uint32_t a, T v) {
+    asm volatile("ds_write_b128 %0, %1" ::"v"(a), "v"(v) : "memory");
+}
+__device__ inline void lds_st32(uint32_t a, float v) {
+    asm volatile("ds_write_b32 %0, %1" ::"v"(a), "v"(v) : "memory");
+}
+// Eight 16-byte LDS reads at a + off[i] completed by one lgkmcnt wait in the
+// same statement (a separate wait would let the compiler copy a destination
+// register before its load has landed).
+template <int O0, int O1, int O2, int O3, int O4, int O5, int O6, int O7, typename T>
+__device__ inline void lds_ld128x8(uint32_t a, T *v) {
+    asm volatile(
+        "ds_read_b128 %0, %8 offset:%9\n\tds_read_b128 %1, %8 offset:%10\n\t"
+        "ds_read_b128 %2, %8 offset:%11\n\tds_read_b128 %3, %8 offset:%12\n\t"
+        "ds_read_b128 %4, %8 offset:%13\n\tds_read_b128 %5, %8 offset:%14\n\t"
+        "ds_read_b128 %6, %8 offset:%15\n\tds_read_b128 %7, %8 offset:%16\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]),
+          "=&v"(v[6]), "=&v"(v[7])
+        : "v"(a), "n"(O0), "n"(O1), "n"(O2), "n"(O3), "n"(O4), "n"(O5), "n"(O6), "n"(O7));
+}
+
+// Four 16-byte reads at a + 64*i and four at b + 1024*i, one wait.
+__device__ inline void lds_ld_alpha_p(uint32_t a, uint32_t b, float4_t *ar, half8_t *pa) {
+    asm volatile(
+        "ds_read_b128 %0, %8\n\tds_read_b128 %1, %8 offset:64\n\t"
+        "ds_read_b128 %2, %8 offset:128\n\tds_read_b128 %3, %8 offset:192\n\t"
+        "ds_read_b128 %4, %9\n\tds_read_b128 %5, %9 offset:1024\n\t"
+        "ds_read_b128 %6, %9 offset:2048\n\tds_read_b128 %7, %9 offset:3072\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(ar[0]), "=&v"(ar[1]), "=&v"(ar[2]), "=&v"(ar[3]), "=&v"(pa[0]), "=&v"(pa[1]),
+          "=&v"(pa[2]), "=&v"(pa[3])
+        : "v"(a), "v"(b));
+}
+
+// The wave's raw fragment of one half-tile row: two 16-byte chunks (its two
+// 64-dim blocks, 16 dims each) and the row's exponents. Issued from inline
+// assembly because the compiler would otherwise make each read wait for all
+// outstanding global->LDS copies; the trailing lgkmcnt wait makes the outputs
+// valid when the statement completes.
+__device__ inline void read_wave_frag(const uint8_t *st, int wave, int h2, int j, int q,
+                                      uint4_t &c0, uint4_t &c1, uint2_t &e) {
+    uint32_t a0, a1;
+    if (wave < 3) {
+        a0 = lds_addr(st) + stage_off(2 * (2 * wave) + h2, j, q);
+        a1 = lds_addr(st) + stage_off(2 * (2 * wave + 1) + h2, j, q);
+    } else {
+        // block 6 codes, then tail dims 16q..16q+15 = f16 chunks 2q, 2q+1 of the
+        // tail, i.e. chunk (2q)&3 of tail block 7 + (q>>1) (two 16 B chunks)
+        a0 = lds_addr(st) + stage_off(2 * 6 + h2, j, q);
+        a1 = lds_addr(st) + stage_off(2 * (7 + (q >> 1)) + h2, j, (2 * q) & 3);
+    }
+    const uint32_t ae = lds_addr(st) + kSexpOff + (16 * h2 + j) * 8;
+    asm volatile(
+        "ds_read_b128 %0, %3\n\t"
+        "ds_read_b128 %1, %4\n\t"
+        "ds_read_b64 %2, %5\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(c0), "=&v"(c1), "=&v"(e)
+        : "v"(a0), "v"(a1), "v"(ae));
+}
+
+// Second tail chunk of wave 3 (f16 chunk 2q+1).
+__device__ inline uint4_t read_tail_hi(const uint8_t *st, int h2, int j, int q) {
+    uint4_t v;
+    const uint32_t a = lds_addr(st) + stage_off(2 * (7 + (q >> 1)) + h2, j, (2 * q + 1) & 3);
+    asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(a));
+    return v;
+}
+
+__device__ inline void dequant16(uint4_t c, float sc, half8_t &a0, half8_t &a1) {
+    a0 = make_half8(cvt_fp8x2<false>(c[0], sc), cvt_fp8x2<true>(c[0], sc),
+                    cvt_fp8x2<false>(c[1], sc), cvt_fp8x2<true>(c[1], sc));
+    a1 = make_half8(cvt_fp8x2<false>(c[2], sc), cvt_fp8x2<true>(c[2], sc),
+                    cvt_fp8x2<false>(c[3], sc), cvt_fp8x2<true>(c[3], sc));
+}
+
+__device__ inline float block_scale(uint2_t e, int b) {
+    const uint32_t w = b < 4 ? e[0] : e[1];
+    return pow2f((int)(int8_t)((w >> (8 * (b & 3))) & 0xFF));
+}
+
+// Q^T B fragments for the dim-split: hb = head block, ks = k-step over the
+// wave's 128 dims; dims 64*(2w + (ks>>1)) + 16q + 8(ks&1) + [0,8).
+template <bool kQf32>
+__device__ inline void load_q_split(const DecodeArgs &A, int p, int wave, int j, int q,
+                                    half8_t (*qh)[4], half8_t (*ql)[4]) {
+#pragma unroll
+    for (int hb = 0; hb < 4; ++hb)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const int d = 64 * (2 * wave + (ks >> 1)) + 16 * q + 8 * (ks & 1);
+            const long long off = (long long)p * A.q_stride + (long long)(16 * hb + j) * kD + d;
+            if (kQf32) {
+                const float *src = static_cast<const float *>(A.q) + off;
+                const float4_t x0 = *reinterpret_cast<const float4_t *>(src);
+                const float4_t x1 = *reinterpret_cast<const float4_t *>(src + 4);
+                half8_t hi, lo;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    hi[i] = (half_t)x0[i];
+                    lo[i] = (half_t)(x0[i] - (float)hi[i]);
+                    hi[4 + i] = (half_t)x1[i];
+                    lo[4 + i] = (half_t)(x1[i] - (float)hi[4 + i]);
+                }
+                qh[hb][ks] = hi;
+                ql[hb][ks] = lo;
+            } else {
+                const uint4_t v = *reinterpret_cast<const uint4_t *>(
+                    static_cast<const uint16_t *>(A.q) + off);
+                half8_t h;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    h[2 * i] = (half_t)bf16_to_f32((uint16_t)(v[i] & 0xFFFF));
+                    h[2 * i + 1] = (half_t)bf16_to_f32((uint16_t)(v[i] >> 16));
+                }
+                qh[hb][ks] = h;
+            }
+        }
+}
+
+struct SplitState {
+    float m_run;        // owner-side softmax state of head 16w + j
+    float l_run;
+    float4_t o[4][8];   // O_w[head block][dim block]: heads 16mb+4q+r, dims 128w+16nb+j
+};
+
+// O_w += P . V_w for one tile: B fragments (rows R(8q + 4h + s/4) =
+// 16h + 4q + s/4, dims 16nb + 4(s&3)) come from the wave's V slice via
+// transposing reads, all 16 behind one wait.
+__device__ inline void pv_split(uint32_t vt_base, int j, int q, const half8_t *pa,
+                                float4_t (*o)[8]) {
+            uint2_t tb[16];
+            {
+                const uint32_t ab = vt_base + (4 * q + (j >> 2)) * kVRowBytes + 8 * (j & 3);
+                asm volatile(
+                    "ds_read_b64_tr_b16 %0, %16\n\tds_read_b64_tr_b16 %1, %16 offset:4608\n\t"
+                    "ds_read_b64_tr_b16 %2, %16 offset:32\n\tds_read_b64_tr_b16 %3, %16 offset:4640\n\t"
+                    "ds_read_b64_tr_b16 %4, %16 offset:64\n\tds_read_b64_tr_b16 %5, %16 offset:4672\n\t"
+                    "ds_read_b64_tr_b16 %6, %16 offset:96\n\tds_read_b64_tr_b16 %7, %16 offset:4704\n\t"
+                    "ds_read_b64_tr_b16 %8, %16 offset:128\n\tds_read_b64_tr_b16 %9, %16 offset:4736\n\t"
+                    "ds_read_b64_tr_b16 %10, %16 offset:160\n\tds_read_b64_tr_b16 %11, %16 offset:4768\n\t"
+                    "ds_read_b64_tr_b16 %12, %16 offset:192\n\tds_read_b64_tr_b16 %13, %16 offset:4800\n\t"
+                    "ds_read_b64_tr_b16 %14, %16 offset:224\n\tds_read_b64_tr_b16 %15, %16 offset:4832\n\t"
+                    "s_waitcnt lgkmcnt(0)"
+                    : "=&v"(tb[0]), "=&v"(tb[1]), "=&v"(tb[2]), "=&v"(tb[3]), "=&v"(tb[4]),
+                      "=&v"(tb[5]), "=&v"(tb[6]), "=&v"(tb[7]), "=&v"(tb[8]), "=&v"(tb[9]),
+                      "=&v"(tb[10]), "=&v"(tb[11]), "=&v"(tb[12]), "=&v"(tb[13]), "=&v"(tb[14]),
+                      "=&v"(tb[15])
+                    : "v"(ab));
+            }
+            static_assert(16 * kVRowBytes == 4608, "tr-read offsets assume 288-byte V rows");
+#pragma unroll
+            for (int nb = 0; nb < 8; ++nb) {
+                const half8_t vb = __builtin_bit_cast(
+                    half8_t, uint4_t{tb[2 * nb][0], tb[2 * nb][1], tb[2 * nb + 1][0], tb[2 * nb + 1][1]});
+#pragma unroll
+                for (int mb = 0; mb < 4; ++mb)
+                    o[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[mb], vb, o[mb][nb], 0, 0, 0);
+            }
+}
+
+template <bool kQf32>
+__global__ __launch_bounds__(256) void decode_fp8_kernel(const DecodeArgs A) {
+    static_assert(kStages == 4 && kCopiesPerWave == 5, "wait_copies encodes these counts");
+    __shared__ __attribute__((aligned(16))) uint8_t stages[kStages][kStageBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t vtile[4][kVTileBytes];
+    __shared__ __attribute__((aligned(16))) float4_t sx[4][4][2][64];   // [owner][writer][h2][lane]
+    __shared__ __attribute__((aligned(16))) half8_t pbuf[4][64];        // [head block][lane]
+    __shared__ __attribute__((aligned(16))) float alpha_s[kH];
+    __shared__ long long s_start[kMaxProb + 1];
+    stage_start(A, s_start);
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int j = lane & 15;
+    const int q = lane >> 4;
+    const uint32_t vt_base = lds_addr(vtile[wave]);
+
+    long long g0 = (long long)blockIdx.x * A.chunk;
+    const long long g1 = min(g0 + (long long)A.chunk, A.total);
+    int p = 0;
+    int slot_s = 0;
+
+    while (g0 < g1) {
+        while (s_start[p + 1] <= g0) ++p;
+        const long long seg_end = min(g1, s_start[p + 1]);
+        const long long r0 = g0 - s_start[p];
+        const long long r1 = seg_end - s_start[p];
+        const int n_tiles = (int)((r1 - r0 + kTile - 1) / kTile);
+        const long long seg_base =
+            (A.row_base ? A.row_base[p] : (long long)p * A.row_base_stride);
+        const bool direct = !A.row_idx && !A.page_table;
+        // physical row of tile row (lane & 31); rows past the segment end copy
+        // the segment's first row (finite filler, masked in the softmax)
+        auto lane_phys = [&](int t) {
+            long long r = r0 + (long long)t * kTile + (lane & 31);
+            if (r >= r1) r = r0;
+            return direct ? seg_base + r : phys_row(A, p, r);
+        };
+
+        half8_t qh[4][4], ql[kQf32 ? 4 : 1][4];
+        load_q_split<kQf32>(A, p, wave, j, q, qh, ql);
+        for (int s = 0; s < kStages - 1 && s < n_tiles; ++s)
+            issue_stage(A, stages[s], lane_phys(s), lane, wave);
+        SplitState S;
+        S.m_run = -INFINITY;
+        S.l_run = 0.0f;
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+            for (int nb = 0; nb < 8; ++nb) S.o[mb][nb] = float4_t{0, 0, 0, 0};
+
+        float4_t ar[4];
+        half8_t pa[4];
+        int t = 0;
+        while (t < n_tiles) {
+        for (; t < n_tiles; ++t) {
+            if (t + kStages - 1 < n_tiles)
+                issue_stage(A, stages[(t + kStages - 1) % kStages], lane_phys(t + kStages - 1),
+                            lane, wave);
+            // The fp32-Q variant spills registers; spill stores share the vmcnt
+            // counter with the copies, so it waits for the whole ring.
+            wait_copies(kQf32 ? 0 : min(kStages - 1, n_tiles - 1 - t));
+            lds_barrier();   // B1: tile t landed; last tile's P/alpha/S slots are consumed
+
+            const uint8_t *st = stages[t % kStages];
+            const long long rb = r0 + (long long)t * kTile;
+
+            // ---- 1. partial S^T over this wave's dims; V_w slice to LDS ----------
+            float4_t acc[2][4];
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2) {
+                uint4_t c0, c1;
+                uint2_t e;
+                read_wave_frag(st, wave, h2, j, q, c0, c1, e);
+                half8_t a[4];
+                dequant16(c0, block_scale(e, 2 * wave), a[0], a[1]);
+                if (wave < 3) {
+                    dequant16(c1, block_scale(e, 2 * wave + 1), a[2], a[3]);
+                } else {
+                    a[2] = __builtin_bit_cast(half8_t, c1);
+                    a[3] = __builtin_bit_cast(half8_t, read_tail_hi(st, h2, j, q));
+                }
+                // V_w row 16h2+j, dims 64*bb + 16q .. +15 (bb = 0,1 within the wave)
+                const uint32_t vrow = vt_base + (16 * h2 + j) * kVRowBytes + 32 * q;
+                asm volatile("ds_write_b128 %0, %1\n\tds_write_b128 %0, %2 offset:16\n\t"
+                             "ds_write_b128 %0, %3 offset:128\n\tds_write_b128 %0, %4 offset:144"
+                             :: "v"(vrow), "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]) : "memory");
+#pragma unroll
+                for (int hb = 0; hb < 4; ++hb) {
+                    float4_t c = float4_t{0, 0, 0, 0};
+#pragma unroll
+                    for (int ks = 0; ks < 4; ++ks) {
+                        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[ks], qh[hb][ks], c, 0, 0, 0);
+                        if (kQf32)
+                            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[ks], ql[hb][ks], c, 0, 0, 0);
+                    }
+                    acc[h2][hb] = c;
+                }
+            }
+            // ---- 2. reduce-scatter S, softmax of the wave's heads ----------------
+            // sx layout: [owner][writer][h2][lane] float4
+            const uint32_t sx_base = lds_addr(sx);
+#pragma unroll
+            for (int hb = 0; hb < 4; ++hb)
+#pragma unroll
+                for (int h2 = 0; h2 < 2; ++h2)
+                    lds_st128(sx_base + (((hb * 4 + wave) * 2 + h2) * 64 + lane) * 16, acc[h2][hb]);
+            lds_barrier();   // B2: partials visible
+            float4_t part[8];   // [w2*2 + h2]
+            lds_ld128x8<0, 1024, 2048, 3072, 4096, 5120, 6144, 7168>(
+                sx_base + ((wave * 8) * 64 + lane) * 16, part);
+            float4_t sacc[2];
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2)   // sum in writer order 0..3
+                sacc[h2] = ((part[h2] + part[2 + h2]) + part[4 + h2]) + part[6 + h2];
+            float s[2][4];
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const bool ok = rb + 16 * h2 + 4 * q + r < r1;
+                    s[h2][r] = ok ? sacc[h2][r] * A.kq_log2 : -INFINITY;
+                    tmax = fmaxf(tmax, s[h2][r]);
+                }
+            tmax = xmax_16_32(tmax);
+            // Lazy rescale: the reference point m_run moves only when the tile max
+            // exceeds it by more than 8 (log2 units); otherwise p <= 2^8, which f16
+            // P and the fp32 sums carry exactly as well.
+            const bool bump = tmax > S.m_run + 8.0f;
+            const float m_new = bump ? tmax : S.m_run;
+            const bool none = m_new == -INFINITY;
+            const float alpha = (bump && S.m_run != -INFINITY) ? __builtin_amdgcn_exp2f(S.m_run - m_new) : 1.0f;
+            half8_t pf;
+            float psum = 0.0f;
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float pv = none ? 0.0f : __builtin_amdgcn_exp2f(s[h2][r] - m_new);
+                    psum += pv;
+                    pf[4 * h2 + r] = (half_t)pv;
+                }
+            S.l_run = S.l_run * alpha + psum;
+            S.m_run = m_new;
+            const uint32_t pbuf_base = lds_addr(pbuf);
+            const uint32_t alpha_base = lds_addr(alpha_s);
+            lds_st128(pbuf_base + (wave * 64 + lane) * 16, pf);
+            if (q == 0) lds_st32(alpha_base + (16 * wave + j) * 4, alpha);
+            lds_barrier();   // B3: P and rescale factors of all heads visible
+
+            // ---- 3. O_w += P . V_w --------------------------------------------------
+            lds_ld_alpha_p(alpha_base + 16 * q, pbuf_base + lane * 16, ar, pa);
+            bool need_rescale = false;
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb)
+                need_rescale |= ar[mb][0] != 1.0f || ar[mb][1] != 1.0f || ar[mb][2] != 1.0f ||
+                                ar[mb][3] != 1.0f;
+            need_rescale = __any(need_rescale);
+            if (need_rescale) break;   // rare: the rescale runs outside the hot loop
+            pv_split(vt_base, j, q, pa, S.o);
+        }
+        if (t < n_tiles) {
+            // a softmax reference point moved: rescale O, then finish tile t
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+                for (int nb = 0; nb < 8; ++nb) S.o[mb][nb] *= ar[mb];
+            pv_split(vt_base, j, q, pa, S.o);
+            ++t;
+        }
+        }
+
+        // ---- emit: O_w rows of all heads over the wave's dims; m, l by owners ------
+        {
+            const float l = xsum_16_32(S.l_run);
+            const long long slot = (long long)blockIdx.x * A.s_max + slot_s;
+            float *wo = A.ws_o + slot * (kH * kD) + (4 * q) * kD + 128 * wave + j;
+            asm volatile("" : "+v"(wo));
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+                for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) wo[(16 * mb + r) * kD + 16 * nb] = S.o[mb][nb][r];
+            if (q == 0) {
+                A.ws_ml[slot * 2 * kH + 16 * wave + j] = S.m_run;
+                A.ws_ml[slot * 2 * kH + kH + 16 * wave + j] = l;
+            }
+            if (threadIdx.x == 0) A.ws_prob[slot] = p;
+        }
+        ++slot_s;
+        g0 = seg_end;
+        lds_barrier();   // the next segment's copies reuse the ring
+    }
+    if (threadIdx.x == 0)
+        for (int s2 = slot_s; s2 < A.s_max; ++s2) A.ws_prob[(long long)blockIdx.x * A.s_max + s2] = -1;
+}
+
+// ---- fp32-row kernel (reference launchers): fragments straight from global -----------
+__global__ __launch_bounds__(256) void decode_f32_kernel(const DecodeArgs A) {
     __shared__ half_t vt[kD * kVtStride];
     __shared__ long long s_start[kMaxProb + 1];
     stage_start(A, s_start);
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int j = lane & 15;          // row (A/K loads) or head / dim column (outputs)
-    const int q = lane >> 4;          // k-group
-    const int head = wave * 16 + j;   // head owned by this lane in S^T / Q layout
+    const int j = lane & 15;
+    const int q = lane >> 4;
+    const int head = wave * 16 + j;
 
     long long g0 = (long long)blockIdx.x * A.chunk;
     const long long g1 = min(g0 + (long long)A.chunk, A.total);
     int p = 0;
     int slot_s = 0;
-    const int wg = blockIdx.x;
+    auto row_allowed = [&](long long row) {
+        return row < A.f32_n_raw || !A.f32_allowed || A.f32_allowed[row - A.f32_n_raw] != 0;
+    };
 
     while (g0 < g1) {
         while (s_start[p + 1] <= g0) ++p;
@@ -261,144 +783,46 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(const DecodeArgs A)
         const long long r0 = g0 - s_start[p];
         const long long r1 = seg_end - s_start[p];
 
-        half8_t qh[16], ql[kQf32 ? 16 : 1];
-        load_q<kQf32>(A, p, head, q, qh, ql);
-
-        float m_run = -INFINITY;
-        float l_run = 0.0f;
-        float4_t o[32];
-#pragma unroll
-        for (int n = 0; n < 32; ++n) o[n] = float4_t{0, 0, 0, 0};
+        half8_t qh[16], ql[16];
+        load_q<true>(A, p, head, q, qh, ql);
+        SegState S;
+        seg_init(S);
 
         for (long long rb = r0; rb < r1; rb += kTile) {
-            // ---- issue this tile's loads -------------------------------------
-            Fp8Frag fr[2];
-            const float *frow[2] = {nullptr, nullptr};
-            bool lvalid[2];
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                const long long r = rb + 16 * t + j;
-                lvalid[t] = r < r1;
-                if (kFp8) {
-                    const long long ph = lvalid[t] ? phys_row(A, p, r) : 0;
-                    load_fp8_frag(A, ph, q, lvalid[t], fr[t]);
-                } else if (lvalid[t]) {
-                    if (r < A.f32_n_raw) {
-                        frow[t] = A.f32_raw + r * kD;
-                    } else {
-                        const long long rc = r - A.f32_n_raw;
-                        if (A.f32_allowed && A.f32_allowed[rc] == 0) lvalid[t] = false;
-                        frow[t] = A.f32_comp + rc * kD;
-                    }
-                }
-            }
-
             __syncthreads();   // previous tile's P.V reads of vt are done
-
-            // ---- S^T = K . Q^T, and this wave's quarter of V^T -------------------
             float4_t acc[2];
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                acc[t] = float4_t{0, 0, 0, 0};
-                const int prow = vt_pos(16 * t + j);
+            for (int h2 = 0; h2 < 2; ++h2) {
+                acc[h2] = float4_t{0, 0, 0, 0};
+                const long long r = rb + 16 * h2 + j;
+                const bool valid = r < r1 && row_allowed(r);
+                const float *frow = r < A.f32_n_raw ? A.f32_raw + r * kD
+                                                    : A.f32_comp + (r - A.f32_n_raw) * kD;
+                const int prow = vt_pos(16 * h2 + j);
 #pragma unroll
                 for (int b = 0; b < 8; ++b) {
                     half8_t a0, a1;
-                    if (kFp8) dequant_fp8(fr[t], b, a0, a1);
-                    else load_f32_block(frow[t], b, q, lvalid[t], a0, a1);
-                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qh[2 * b], acc[t], 0, 0, 0);
-                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qh[2 * b + 1], acc[t], 0, 0, 0);
-                    if (kQf32) {
-                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, ql[2 * b], acc[t], 0, 0, 0);
-                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, ql[2 * b + 1], acc[t], 0, 0, 0);
-                    }
-                    if ((b >> 1) == wave) {
-                        const int d0 = 64 * b + 16 * q;
-#pragma unroll
-                        for (int i = 0; i < 8; ++i) {
-                            vt[(d0 + i) * kVtStride + prow] = a0[i];
-                            vt[(d0 + 8 + i) * kVtStride + prow] = a1[i];
-                        }
-                    }
+                    load_f32_block(frow, b, q, valid, a0, a1);
+                    acc[h2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qh[2 * b], acc[h2], 0, 0, 0);
+                    acc[h2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qh[2 * b + 1], acc[h2], 0, 0, 0);
+                    acc[h2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, ql[2 * b], acc[h2], 0, 0, 0);
+                    acc[h2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, ql[2 * b + 1], acc[h2], 0, 0, 0);
+                    if ((b >> 1) == wave) vt_write(vt, b, q, prow, a0, a1);
                 }
             }
-
-            // ---- online softmax (exp2 domain) ------------------------------------
-            float s[2][4];
-            float tmax = -INFINITY;
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const long long row = rb + 16 * t + 4 * q + r;
-                    bool ok = row < r1;
-                    if (!kFp8 && ok && row >= A.f32_n_raw && A.f32_allowed)
-                        ok = A.f32_allowed[row - A.f32_n_raw] != 0;
-                    s[t][r] = ok ? acc[t][r] * A.kq_log2 : -INFINITY;
-                    tmax = fmaxf(tmax, s[t][r]);
-                }
-            }
-            tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-            tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-            const float m_new = fmaxf(m_run, tmax);
-            const bool none = m_new == -INFINITY;
-            const float alpha = none ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-            half8_t pf;
-            float psum = 0.0f;
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float pv = none ? 0.0f : __builtin_amdgcn_exp2f(s[t][r] - m_new);
-                    psum += pv;
-                    pf[4 * t + r] = (half_t)pv;
-                }
-            }
-            l_run = l_run * alpha + psum;
-            m_run = m_new;
-            if (__any(alpha != 1.0f)) {
-                // O rows are heads 16w+4q+r; their alpha sits in lanes 4q+r
-                float ar[4];
-#pragma unroll
-                for (int r = 0; r < 4; ++r) ar[r] = __shfl(alpha, 4 * q + r);
-#pragma unroll
-                for (int n = 0; n < 32; ++n)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) o[n][r] *= ar[r];
-            }
-
+            const half8_t pf = softmax_tile(acc, A.kq_log2, q, S, [&](int h2, int r) {
+                const long long row = rb + 16 * h2 + 4 * q + r;
+                return row < r1 && row_allowed(row);
+            });
             __syncthreads();   // V^T tile complete
-
-            // ---- O += P . V -----------------------------------------------------
-#pragma unroll
-            for (int n = 0; n < 32; ++n) {
-                const half8_t vb =
-                    *reinterpret_cast<const half8_t *>(&vt[(16 * n + j) * kVtStride + 8 * q]);
-                o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf, vb, o[n], 0, 0, 0);
-            }
+            pv_tile(vt, pf, j, q, S);
         }
-
-        // ---- emit this segment's partial ------------------------------------------
-        l_run += __shfl_xor(l_run, 16);
-        l_run += __shfl_xor(l_run, 32);
-        const long long slot = (long long)wg * A.s_max + slot_s;
-        float *wo = A.ws_o + slot * (kH * kD) + (wave * 16 + 4 * q) * kD + j;
-        // keep the 128 store addresses from being hoisted out of the tile loop
-        asm volatile("" : "+v"(wo));
-#pragma unroll
-        for (int n = 0; n < 32; ++n)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) wo[r * kD + 16 * n] = o[n][r];
-        if (q == 0) {
-            A.ws_ml[slot * 2 * kH + head] = m_run;
-            A.ws_ml[slot * 2 * kH + kH + head] = l_run;
-        }
-        if (threadIdx.x == 0) A.ws_prob[slot] = p;
+        emit_partial(A, (long long)blockIdx.x * A.s_max + slot_s, wave, j, q, head, p, S);
         ++slot_s;
         g0 = seg_end;
     }
     if (threadIdx.x == 0)
-        for (int s2 = slot_s; s2 < A.s_max; ++s2) A.ws_prob[(long long)wg * A.s_max + s2] = -1;
+        for (int s2 = slot_s; s2 < A.s_max; ++s2) A.ws_prob[(long long)blockIdx.x * A.s_max + s2] = -1;
 }
 
 // One block per (problem, head): combine the partials with the sink.
@@ -506,7 +930,10 @@ int launch(DecodeArgs &A, const Plan &pl, hipStream_t st, int phases = 3) {
     A.s_max = pl.s_max;
     A.kq_log2 = kLog2e / sqrtf((float)kD);
     if ((phases & 1) && pl.n_wg > 0) {
-        hipLaunchKernelGGL((decode_partial_kernel<kFp8, kQf32>), dim3(pl.n_wg), dim3(256), 0, st, A);
+        if (kFp8)
+            hipLaunchKernelGGL(decode_fp8_kernel<kQf32>, dim3(pl.n_wg), dim3(256), 0, st, A);
+        else
+            hipLaunchKernelGGL(decode_f32_kernel, dim3(pl.n_wg), dim3(256), 0, st, A);
         const int e = hip_status(hipGetLastError());
         if (e) return e;
     }
@@ -526,7 +953,7 @@ extern "C" int ds4hip_flash_attn_decode_fp8_workspace_size(const long long *n_ro
         if (n_rows_per_prob[p] < 0) return kEINVAL;
         start[p + 1] = start[p] + n_rows_per_prob[p];
     }
-    *bytes = make_plan(start, n_prob, 2).ws_bytes;
+    *bytes = make_plan(start, n_prob, kFp8WgPerCu).ws_bytes;
     return 0;
 }
 
@@ -552,7 +979,7 @@ extern "C" int ds4hip_flash_attn_decode_fp8(
         if (n_rows_per_prob[p] < 0) return ds4hip_set_last_error(kEINVAL);
         A.start[p + 1] = A.start[p] + n_rows_per_prob[p];
     }
-    const Plan pl = make_plan(A.start, n_prob, 2);
+    const Plan pl = make_plan(A.start, n_prob, kFp8WgPerCu);
     if (workspace_bytes < pl.ws_bytes) return ds4hip_set_last_error(kEINVAL);
     A.q = q;
     A.q_stride = q_stride;

@@ -25,7 +25,30 @@ SIGNATURES: dict[str, list] = {
     "ds4hip_flash_attn_decode_fp8": [
         _vp, _i, _ll, _vp, _ll, _vp, _ll, _vp, _vp, _vp, _vp, _i, _vp, _ll, _vp, _ll, _vp, _i,
         _i, _i, _i, _i, _vp, _sz, _i, _vp],
+    "ds4hip_tail_rope_yarn_f32": [_vp, _vp, _i, _i, _i, _i, _i, _vp],
+    "ds4hip_tail_rope_yarn_inverse_f32": [_vp, _vp, _i, _i, _i, _i, _i, _vp],
+    "ds4hip_mul_mv_f16_f32": [_vp, _vp, _vp, _i, _i, _vp],
+    "ds4hip_mul_mv_q8_0_q8_0_grouped_f32": [_vp, _vp, _vp, _i, _i, _i, _vp],
+    "ds4hip_mul_mv_q8_0_q8_0_grouped_f32_prealloc": [_vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp],
+    "ds4hip_mul_mv_q8_0_q8_0_f32_prealloc": [_vp, _vp, _vp, _i, _i, _vp, _vp, _vp],
+    "ds4hip_mul_mm_bf16_f32": [_vp, _vp, _vp, _i, _i, _i, _vp],
+    "ds4hip_indexer_allowed_short_circuit_i32": [_vp, _i, _i, _vp],
+    "ds4hip_scale_inplace_f32": [_vp, _i, C.c_float, _vp],
+    "ds4hip_indexer_score_topk_i32": [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp],
+    "ds4hip_indexer_score_topk_f32_i32": [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp],
+    "ds4hip_indexer_select_scratch_bytes": [_i],
+    "ds4hip_indexer_topk_positions": [_vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp,
+                                      _vp],
+    "ds4hip_compressor_decode_step_f32_prealloc": [_i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i,
+                                                   _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
+    "ds4hip_compressor_decode_step_f32": [_i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp,
+                                          _vp, _vp, _vp, _vp],
+    "ds4hip_compressor_decode_step_w32": [_i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp,
+                                          _vp, _vp, _vp, _vp],
 }
+
+# entry points that return a value rather than a status
+RESTYPES = {"ds4hip_indexer_select_scratch_bytes": C.c_size_t}
 
 _lib = None
 
@@ -49,7 +72,7 @@ def lib() -> C.CDLL:
         for name, args in SIGNATURES.items():
             fn = getattr(l, name)
             fn.argtypes = args
-            fn.restype = C.c_int
+            fn.restype = RESTYPES.get(name, C.c_int)
         _lib = l
     return _lib
 

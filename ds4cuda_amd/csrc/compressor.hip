@@ -1,0 +1,284 @@
+// compressor.hip — streaming KV compressor, one decode step
+// (cuda/compressor.cu:64-429; spec ds4.c compressor_decode_one).
+//
+// Step kernel: both projections (kv and gate, f16 or fp32 weights) in one
+// launch, one wave per output row over the LDS-staged input; the gate row gets
+// its APE bias and both rows are written straight into the state row
+// (ratio + pos % ratio for ratio 4, pos % ratio otherwise) and into the
+// caller's projection scratch.
+// Emit kernel (only when (pos + 1) % ratio == 0, decided on the host): one
+// workgroup pools the state per column (softmax over 8 or 128 rows),
+// RMSNorm-s the pooled row, applies tail RoPE at pos + 1 - ratio, FP8
+// round-trips the non-RoPE prefix (attention compressor only), and then —
+// after a barrier, since the pool read the state — shifts the ratio-4 ring.
+
+#include "ds4hip_common.h"
+#include "../../include/ds4hip.h"
+
+#include <cmath>
+
+using namespace ds4hip;
+
+namespace {
+
+constexpr float kNegInf = -1.0e30f;   // cuda/compressor.cu:53
+constexpr float kRmsEps = 1.0e-6f;    // cuda/compressor.cu:54
+constexpr int kNRot = 64;             // cuda/compressor.cu:55
+constexpr int kMaxIn = 8192;
+
+template <bool kW32>
+__global__ __launch_bounds__(256) void comp_project_kernel(
+        const float *__restrict__ x, const void *__restrict__ w_kv, const void *__restrict__ w_gate,
+        const uint16_t *__restrict__ w_ape, int in_dim, int width, int ratio, int pos_mod,
+        float *__restrict__ state_kv, float *__restrict__ state_score, float *__restrict__ kv_cur,
+        float *__restrict__ sc_cur) {
+    __shared__ float xs[kMaxIn];
+    for (int i = threadIdx.x; i < in_dim; i += 256) xs[i] = x[i];
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);   // [0, 2*width)
+    if (r >= 2 * width) return;
+    const bool gate = r >= width;
+    const int o = gate ? r - width : r;
+    float acc = 0.0f;
+    if (kW32) {
+        const float *wr = static_cast<const float *>(gate ? w_gate : w_kv) + (size_t)o * in_dim;
+        for (int i = lane * 4; i < in_dim; i += 256) {
+            const float4_t v = *reinterpret_cast<const float4_t *>(wr + i);
+            acc = fmaf(v[0], xs[i], acc);
+            acc = fmaf(v[1], xs[i + 1], acc);
+            acc = fmaf(v[2], xs[i + 2], acc);
+            acc = fmaf(v[3], xs[i + 3], acc);
+        }
+    } else {
+        const uint16_t *wr = static_cast<const uint16_t *>(gate ? w_gate : w_kv) + (size_t)o * in_dim;
+        for (int i = lane * 8; i < in_dim; i += 512) {
+            const uint4_t v = *reinterpret_cast<const uint4_t *>(wr + i);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                acc = fmaf(f16_bits_to_f32((uint16_t)(v[k] & 0xFFFF)), xs[i + 2 * k], acc);
+                acc = fmaf(f16_bits_to_f32((uint16_t)(v[k] >> 16)), xs[i + 2 * k + 1], acc);
+            }
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+    if (lane == 0) {
+        const int row = ratio == 4 ? ratio + pos_mod : pos_mod;   // cuda/compressor.cu:85
+        const size_t off = (size_t)row * width + o;
+        if (gate) {
+            const float s = acc + f16_bits_to_f32(w_ape[(size_t)pos_mod * width + o]);
+            state_score[off] = s;
+            if (sc_cur) sc_cur[o] = s;
+        } else {
+            state_kv[off] = acc;
+            if (kv_cur) kv_cur[o] = acc;
+        }
+    }
+}
+
+struct RopeArgs {
+    float theta_scale, freq_scale, ext_factor, attn_factor, corr_low, corr_high;
+    int pos;
+};
+
+// cuda/rope.cu:214-250 (host) for n_rot = 64
+RopeArgs rope_args(int il, int pos) {
+    const bool compressed = il >= 2;
+    RopeArgs R;
+    const float base = compressed ? 160000.0f : 10000.0f;
+    R.freq_scale = compressed ? 1.0f / 16.0f : 1.0f;
+    R.ext_factor = compressed ? 1.0f : 0.0f;
+    R.attn_factor = 1.0f;
+    if (R.ext_factor != 0.0f) R.attn_factor /= 1.0f + 0.1f * logf(1.0f / R.freq_scale);
+    R.corr_low = R.corr_high = 0.0f;
+    if (R.ext_factor != 0.0f) {
+        const float pi = 3.14159265358979323846f;
+        auto corr_dim = [&](float t) {
+            return (float)kNRot * logf(65536.0f / (t * 2.0f * pi)) / (2.0f * logf(base));
+        };
+        R.corr_low = fmaxf(0.0f, floorf(corr_dim(32.0f)));
+        R.corr_high = fminf((float)(kNRot - 1), ceilf(corr_dim(1.0f)));
+    }
+    R.theta_scale = powf(base, -2.0f / (float)kNRot);
+    R.pos = pos;
+    return R;
+}
+
+// One workgroup of 512 threads; thread j owns column j (< head_dim <= 512).
+__global__ __launch_bounds__(512) void comp_emit_kernel(float *__restrict__ state_kv,
+                                                        float *__restrict__ state_score,
+                                                        const float *__restrict__ w_norm,
+                                                        float *__restrict__ emit_out, int head_dim,
+                                                        int ratio, int is_attn, RopeArgs R) {
+    __shared__ float pooled[512];
+    __shared__ float red[8];
+    const int j = threadIdx.x;
+    const int coff = ratio == 4 ? 2 : 1;
+    const int width = coff * head_dim;
+    // ---- pool (cuda/compressor.cu:107-164)
+    float v = 0.0f;
+    if (j < head_dim) {
+        float mx = kNegInf;
+        if (ratio == 4) {
+            for (int r = 0; r < 4; ++r) {
+                mx = fmaxf(mx, state_score[(size_t)r * width + j]);
+                mx = fmaxf(mx, state_score[(size_t)(4 + r) * width + head_dim + j]);
+            }
+        } else {
+            for (int r = 0; r < ratio; ++r) mx = fmaxf(mx, state_score[(size_t)r * width + j]);
+        }
+        if (mx > kNegInf * 0.5f) {
+            float den = 0.0f, sum = 0.0f;
+            if (ratio == 4) {
+                for (int r = 0; r < 4; ++r) {
+                    const float wp = expf(state_score[(size_t)r * width + j] - mx);
+                    const float wc = expf(state_score[(size_t)(4 + r) * width + head_dim + j] - mx);
+                    den += wp + wc;
+                    sum += wp * state_kv[(size_t)r * width + j];
+                    sum += wc * state_kv[(size_t)(4 + r) * width + head_dim + j];
+                }
+            } else {
+                for (int r = 0; r < ratio; ++r) {
+                    const float w = expf(state_score[(size_t)r * width + j] - mx);
+                    den += w;
+                    sum += w * state_kv[(size_t)r * width + j];
+                }
+            }
+            v = den > 0.0f ? sum / den : 0.0f;
+        }
+    }
+    // ---- RMSNorm (cuda/compressor.cu:174-219)
+    float ss = v * v;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+    if ((j & 63) == 0) red[j >> 6] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+    for (int w = 0; w < 8; ++w) tot += red[w];
+    const float scale = 1.0f / sqrtf(tot / (float)head_dim + kRmsEps);
+    if (j < head_dim) pooled[j] = v * scale * w_norm[j];
+    __syncthreads();
+    // ---- tail RoPE at the window start (cuda/compressor.cu:325-331, rope.cu:136-201)
+    const int n_nope = head_dim - kNRot;
+    float out = j < head_dim ? pooled[j] : 0.0f;
+    if (j >= n_nope && j < head_dim) {
+        const int p = (j - n_nope) >> 1;   // pair index
+        float te = (float)R.pos;
+        for (int k = 0; k < p; ++k) te *= R.theta_scale;
+        const float ti = R.freq_scale * te;
+        float theta = ti, ms = R.attn_factor;
+        if (R.ext_factor != 0.0f) {
+            const float y = ((float)p - R.corr_low) / fmaxf(0.001f, R.corr_high - R.corr_low);
+            const float mix = (1.0f - fminf(1.0f, fmaxf(0.0f, y))) * R.ext_factor;
+            theta = ti * (1.0f - mix) + te * mix;
+            ms *= 1.0f + 0.1f * logf(1.0f / R.freq_scale);
+        }
+        const float c = cosf(theta) * ms, s = sinf(theta) * ms;
+        const float x0 = pooled[n_nope + 2 * p], x1 = pooled[n_nope + 2 * p + 1];
+        out = ((j - n_nope) & 1) ? x0 * s + x1 * c : x0 * c - x1 * s;
+    }
+    // ---- FP8 round trip of the non-RoPE prefix (attention compressor only)
+    if (is_attn && j < n_nope) {
+        float a = fabsf(out);
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) a = fmaxf(a, __shfl_xor(a, off));
+        const int e = fp8_block_exp(a);
+        float q = fminf(fmaxf(ldexpf(out, -e), -448.0f), 448.0f);
+        const uint32_t code = e4m3_encode(q);
+        const uint32_t mag = code & 0x7Fu;
+        float val;
+        if (mag < 8) {
+            val = (float)mag * 0.001953125f;
+        } else {
+            const uint32_t bits = ((mag >> 3) + 120u) << 23 | (mag & 7u) << 20;
+            val = __uint_as_float(bits);
+        }
+        out = ldexpf((code & 0x80u) ? -val : val, e);
+    }
+    if (j < head_dim) emit_out[j] = out;
+    // ---- ring shift, ratio 4 (cuda/compressor.cu:230-249); the pool above
+    // finished reading the state
+    __syncthreads();
+    if (ratio == 4) {
+        for (int i = j; i < 4 * width; i += 512) {
+            const int r = i / width, c = i % width;
+            const size_t top = (size_t)(4 + r) * width + c, bot = (size_t)r * width + c;
+            const float kv = state_kv[top], sc = state_score[top];
+            state_kv[bot] = kv;
+            state_score[bot] = sc;
+        }
+    }
+}
+
+int comp_step(bool is_attn, const float *x, const void *w_kv, const void *w_gate, bool w32,
+              const uint16_t *w_ape, const float *w_norm, int in_dim, int head_dim_out, int ratio,
+              int pos, int il, float *state_kv, float *state_score, float *emit_out,
+              int *emitted_out_host, float *kv_cur, float *sc_cur, hipStream_t st) {
+    if (!x || !w_kv || !w_gate || !w_ape || !w_norm || !state_kv || !state_score || !emit_out ||
+        in_dim <= 0 || in_dim > kMaxIn || (in_dim % 8) || head_dim_out <= kNRot ||
+        head_dim_out > 512 || (head_dim_out % 64) || (ratio != 4 && ratio != 128) || pos < 0)
+        return kEINVAL;
+    const int coff = ratio == 4 ? 2 : 1;
+    const int width = coff * head_dim_out;
+    const int pos_mod = pos % ratio;
+    const bool emit = ((pos + 1) % ratio) == 0;
+    const dim3 grid((2 * width + 3) / 4);
+    if (w32)
+        hipLaunchKernelGGL(comp_project_kernel<true>, grid, dim3(256), 0, st, x, w_kv, w_gate,
+                           w_ape, in_dim, width, ratio, pos_mod, state_kv, state_score, kv_cur, sc_cur);
+    else
+        hipLaunchKernelGGL(comp_project_kernel<false>, grid, dim3(256), 0, st, x, w_kv, w_gate,
+                           w_ape, in_dim, width, ratio, pos_mod, state_kv, state_score, kv_cur, sc_cur);
+    int rc = hip_status(hipGetLastError());
+    if (emitted_out_host) *emitted_out_host = emit ? 1 : 0;   // cuda/compressor.cu:304
+    if (rc || !emit) return rc;
+    hipLaunchKernelGGL(comp_emit_kernel, dim3(1), dim3(512), 0, st, state_kv, state_score, w_norm,
+                       emit_out, head_dim_out, ratio, is_attn ? 1 : 0,
+                       rope_args(il, pos + 1 - ratio));
+    return hip_status(hipGetLastError());
+}
+
+}  // namespace
+
+extern "C" int ds4hip_compressor_decode_step_f32_prealloc(
+        int is_attn, const float *x_f32, const uint16_t *w_kv_f16, const uint16_t *w_gate_f16,
+        const uint16_t *w_ape_f16, const float *w_norm_f32, int in_dim, int head_dim_out,
+        int compress_ratio, int pos, int il, float *state_kv, float *state_score,
+        float *emit_out, int *emitted_out_host, float *scratch_kv_cur, float *scratch_sc_cur,
+        void *stream) {
+    return ds4hip_set_last_error(comp_step(
+        is_attn != 0, x_f32, w_kv_f16, w_gate_f16, false, w_ape_f16, w_norm_f32, in_dim,
+        head_dim_out, compress_ratio, pos, il, state_kv, state_score, emit_out, emitted_out_host,
+        scratch_kv_cur, scratch_sc_cur, (hipStream_t)stream));
+}
+
+extern "C" int ds4hip_compressor_decode_step_f32(int is_attn, const float *x_f32,
+                                                 const uint16_t *w_kv_f16,
+                                                 const uint16_t *w_gate_f16,
+                                                 const uint16_t *w_ape_f16,
+                                                 const float *w_norm_f32, int in_dim,
+                                                 int head_dim_out, int compress_ratio, int pos,
+                                                 int il, float *state_kv, float *state_score,
+                                                 float *emit_out, int *emitted_out_host,
+                                                 void *stream) {
+    // The projection results live only in the state rows; no scratch needed.
+    return ds4hip_set_last_error(comp_step(
+        is_attn != 0, x_f32, w_kv_f16, w_gate_f16, false, w_ape_f16, w_norm_f32, in_dim,
+        head_dim_out, compress_ratio, pos, il, state_kv, state_score, emit_out, emitted_out_host,
+        nullptr, nullptr, (hipStream_t)stream));
+}
+
+extern "C" int ds4hip_compressor_decode_step_w32(int is_attn, const float *x_f32,
+                                                 const float *w_kv_f32, const float *w_gate_f32,
+                                                 const uint16_t *w_ape_f16,
+                                                 const float *w_norm_f32, int in_dim,
+                                                 int head_dim_out, int compress_ratio, int pos,
+                                                 int il, float *state_kv, float *state_score,
+                                                 float *emit_out, int *emitted_out_host,
+                                                 void *stream) {
+    return ds4hip_set_last_error(comp_step(
+        is_attn != 0, x_f32, w_kv_f32, w_gate_f32, true, w_ape_f16, w_norm_f32, in_dim,
+        head_dim_out, compress_ratio, pos, il, state_kv, state_score, emit_out, emitted_out_host,
+        nullptr, nullptr, (hipStream_t)stream));
+}

@@ -1,0 +1,462 @@
+// indexer.hip — lightning-indexer scores and exact top-k selection.
+//
+// Scores (cuda/indexer_allowed.cu:68-171): score[c] = sum_h w[h] relu(q_h . k_c).
+// The reference reduces in a warp-shuffle order and accepts ULP drift at the
+// top-k boundary (cuda/indexer_allowed.cuh:64-66). Here the order is fixed so
+// that the selected set is reproducible bit for bit: dot_h is an fma chain
+// over d ascending from +0, then score = fma(w[h], relu(dot_h), score) over h
+// ascending from +0. One thread scores one key: the key row (up to 128 dims)
+// sits in registers as fp32, the 64 x 128 query in LDS (broadcast reads).
+//
+// Selection (cuda/indexer_allowed.cu:200-279): top_k rounds of argmax with
+// ties to the lowest index select exactly the top_k entries in
+// (score desc, index asc) order. This is computed as an exact radix select on
+// order-preserving 32-bit keys (11 + 11 + 10 bits; histograms built by all
+// workgroups with LDS + global atomics), which yields the threshold key T,
+// the number above it and how many ties at T to take; one workgroup then
+// walks the candidates in index order and emits the 0/1 mask or the
+// ascending position list.
+
+#include "ds4hip_common.h"
+#include "../../include/ds4hip.h"
+
+using namespace ds4hip;
+
+namespace {
+
+constexpr int kMaxHeads = 64;
+constexpr int kMaxDim = 128;
+constexpr int kBins = 2048;
+
+__device__ inline unsigned ord_key(float s) {
+    unsigned u = __float_as_uint(s);
+    if (u == 0x80000000u) u = 0;                 // -0 ranks as +0
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+template <int kKind>   // 0 f32, 1 f16, 2 bf16
+__device__ inline float key_elem(const void *keys, size_t i) {
+    if (kKind == 0) return static_cast<const float *>(keys)[i];
+    if (kKind == 1) return f16_bits_to_f32(static_cast<const uint16_t *>(keys)[i]);
+    return bf16_to_f32(static_cast<const uint16_t *>(keys)[i]);
+}
+
+// 256 threads, one key per thread. hist (optional): top-11-bit histogram of
+// the ordered keys of positions [0, n_cand).
+template <int kKind>
+__global__ __launch_bounds__(256) void score_kernel(const float *__restrict__ q,
+                                                    const float *__restrict__ w,
+                                                    const void *__restrict__ keys, int n_comp,
+                                                    int n_head, int head_dim,
+                                                    float *__restrict__ scores,
+                                                    unsigned *__restrict__ hist, int n_cand) {
+    __shared__ float qs[kMaxHeads * kMaxDim];
+    __shared__ float ws[kMaxHeads];
+    __shared__ unsigned lh[kBins];
+    for (int i = threadIdx.x; i < n_head * head_dim; i += 256) qs[i] = q[i];
+    for (int i = threadIdx.x; i < n_head; i += 256) ws[i] = w[i];
+    if (hist)
+        for (int i = threadIdx.x; i < kBins; i += 256) lh[i] = 0;
+    __syncthreads();
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c < n_comp) {
+        float k[kMaxDim];
+        if (head_dim == kMaxDim && kKind != 0) {
+            // 16-bit keys of the common 128-dim shape: 16 x 16-byte loads
+            const uint4_t *src = reinterpret_cast<const uint4_t *>(
+                static_cast<const uint16_t *>(keys) + (size_t)c * kMaxDim);
+#pragma unroll
+            for (int v = 0; v < kMaxDim / 8; ++v) {
+                const uint4_t u = src[v];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const uint16_t h = (uint16_t)((u[e >> 1] >> (16 * (e & 1))) & 0xFFFF);
+                    k[8 * v + e] = kKind == 1 ? f16_bits_to_f32(h) : bf16_to_f32(h);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int d = 0; d < kMaxDim; ++d)
+                k[d] = d < head_dim ? key_elem<kKind>(keys, (size_t)c * head_dim + d) : 0.0f;
+        }
+        float s = 0.0f;
+        for (int h = 0; h < n_head; ++h) {
+            const float *qh = qs + h * head_dim;
+            float dot = 0.0f;
+#pragma unroll
+            for (int d = 0; d < kMaxDim; ++d)
+                if (d < head_dim) dot = fmaf(qh[d], k[d], dot);
+            s = fmaf(ws[h], dot > 0.0f ? dot : 0.0f, s);
+        }
+        scores[c] = s;
+        if (hist && c < n_cand) atomicAdd(&lh[ord_key(s) >> 21], 1u);
+    }
+    if (hist) {
+        __syncthreads();
+        for (int i = threadIdx.x; i < kBins; i += 256)
+            if (lh[i]) atomicAdd(&hist[i], lh[i]);
+    }
+}
+
+__global__ void zero_u32_kernel(unsigned *p, int n) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0;
+}
+
+// Finds, in histogram h (nb bins, high bin = larger keys), the bin holding the
+// need-th largest key (need >= 1; need == 0 returns the top bin with nothing
+// above). Called by every thread of a workgroup of >= 256 threads.
+__device__ void find_bin(const unsigned *h, int nb, unsigned need, unsigned *s_bin,
+                         unsigned *s_above, unsigned *scratch) {
+    const int t = threadIdx.x;
+    const int per = nb / 256;
+    if (t < 256) {
+        unsigned local = 0;
+        for (int i = 0; i < per; ++i) local += h[nb - 1 - (t * per + i)];
+        scratch[t] = local;
+    }
+    __syncthreads();
+    if (t == 0) {
+        unsigned run = 0;
+        int tt = 0;
+        for (; tt < 255; ++tt) {
+            if (run + scratch[tt] >= need) break;
+            run += scratch[tt];
+        }
+        int bin = nb - 1 - tt * per;
+        for (int i = 0; i < per - 1; ++i, --bin) {
+            if (run + h[bin] >= need) break;
+            run += h[bin];
+        }
+        *s_bin = (unsigned)bin;
+        *s_above = run;
+    }
+    __syncthreads();
+}
+
+// Threshold key T (the need0-th largest candidate key) and the number of
+// candidates equal to T that are taken (lowest indices first).
+__device__ void threshold(const unsigned *hists, unsigned need0, unsigned *T, unsigned *need_eq,
+                          unsigned *scratch, unsigned *s_bin, unsigned *s_above) {
+    unsigned need = need0;
+    find_bin(hists, kBins, need, s_bin, s_above, scratch);
+    unsigned t = *s_bin << 21;
+    need -= *s_above;
+    __syncthreads();
+    find_bin(hists + kBins, kBins, need, s_bin, s_above, scratch);
+    t |= *s_bin << 10;
+    need -= *s_above;
+    __syncthreads();
+    find_bin(hists + 2 * kBins, 1024, need, s_bin, s_above, scratch);
+    t |= *s_bin;
+    need -= *s_above;
+    *T = t;
+    *need_eq = need;
+}
+
+// Stage 2 / 3 histogram: recompute the selection state from the previous
+// histograms, then histogram the next bit field of keys matching the prefix.
+template <int kStage>
+__global__ __launch_bounds__(256) void hist_next_kernel(const float *__restrict__ scores,
+                                                        int n_cand, unsigned need0,
+                                                        unsigned *__restrict__ hists) {
+    __shared__ unsigned lh[kBins];
+    __shared__ unsigned scratch[256];
+    __shared__ unsigned s_bin, s_above;
+    unsigned *h1 = hists, *h2 = hists + kBins, *h3 = hists + 2 * kBins;
+    find_bin(h1, kBins, need0, &s_bin, &s_above, scratch);
+    unsigned prefix = s_bin << 21, need = need0 - s_above;
+    int shift = 10, nb = kBins;
+    if (kStage == 3) {
+        __syncthreads();
+        find_bin(h2, kBins, need, &s_bin, &s_above, scratch);
+        prefix |= s_bin << 10;
+        shift = 0;
+        nb = 1024;
+    }
+    for (int i = threadIdx.x; i < nb; i += 256) lh[i] = 0;
+    __syncthreads();
+    const unsigned mask_hi = kStage == 2 ? 0xFFE00000u : 0xFFFFFC00u;
+    for (int c = blockIdx.x * 256 + threadIdx.x; c < n_cand; c += gridDim.x * 256) {
+        const unsigned k = ord_key(scores[c]);
+        if ((k & mask_hi) == prefix) atomicAdd(&lh[(k >> shift) & (nb - 1)], 1u);
+    }
+    __syncthreads();
+    unsigned *dst = kStage == 2 ? h2 : h3;
+    for (int i = threadIdx.x; i < nb; i += 256)
+        if (lh[i]) atomicAdd(&dst[i], lh[i]);
+}
+
+constexpr int kChunk = 1024;   // positions per emit workgroup (256 threads x 4)
+
+// Per chunk: candidates strictly above T and equal to T.
+__global__ __launch_bounds__(256) void count_kernel(const float *__restrict__ scores, int n_cand,
+                                                    unsigned need0,
+                                                    const unsigned *__restrict__ hists,
+                                                    unsigned *__restrict__ chunk_gt,
+                                                    unsigned *__restrict__ chunk_eq) {
+    __shared__ unsigned scratch[256];
+    __shared__ unsigned s_bin, s_above, red[2][4];
+    unsigned T, need_eq;
+    threshold(hists, need0, &T, &need_eq, scratch, &s_bin, &s_above);
+    unsigned gt = 0, eq = 0;
+    for (int i = 0; i < 4; ++i) {
+        const int c = blockIdx.x * kChunk + i * 256 + threadIdx.x;
+        if (c < n_cand) {
+            const unsigned k = ord_key(scores[c]);
+            gt += k > T;
+            eq += k == T;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        gt += __shfl_xor(gt, off);
+        eq += __shfl_xor(eq, off);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        red[0][threadIdx.x >> 6] = gt;
+        red[1][threadIdx.x >> 6] = eq;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        chunk_gt[blockIdx.x] = red[0][0] + red[0][1] + red[0][2] + red[0][3];
+        chunk_eq[blockIdx.x] = red[1][0] + red[1][1] + red[1][2] + red[1][3];
+    }
+}
+
+// Block-wide exclusive scan of 256 values (one per thread); returns the total.
+__device__ unsigned block_excl_scan(unsigned v, unsigned *buf, unsigned *excl) {
+    const int t = threadIdx.x;
+    buf[t] = v;
+    __syncthreads();
+    for (int off = 1; off < 256; off <<= 1) {
+        const unsigned u = t >= off ? buf[t - off] : 0;
+        __syncthreads();
+        buf[t] += u;
+        __syncthreads();
+    }
+    *excl = buf[t] - v;
+    const unsigned total = buf[255];
+    __syncthreads();
+    return total;
+}
+
+// Per chunk: every candidate above T, ties at T in index order while the
+// global tie rank < need_eq, and every position >= n_cand (the forced recent
+// window). Writes the 0/1 mask and/or the ascending position list.
+__global__ __launch_bounds__(256) void emit_kernel(const float *__restrict__ scores, int n_comp,
+                                                   int n_cand, unsigned need0,
+                                                   const unsigned *__restrict__ hists,
+                                                   const unsigned *__restrict__ chunk_gt,
+                                                   const unsigned *__restrict__ chunk_eq,
+                                                   int32_t *__restrict__ mask,
+                                                   int32_t *__restrict__ pos_out) {
+    __shared__ unsigned scratch[256], buf[256];
+    __shared__ unsigned s_bin, s_above, s_sel_before, s_eq_before;
+    unsigned T, need_eq;
+    threshold(hists, need0, &T, &need_eq, scratch, &s_bin, &s_above);
+    // selections and ties of the earlier chunks
+    unsigned sel_b = 0, eq_b = 0;
+    for (int c2 = threadIdx.x; c2 < (int)blockIdx.x; c2 += 256) {
+        eq_b += chunk_eq[c2];
+        sel_b += chunk_gt[c2];
+    }
+    unsigned ex;
+    const unsigned eq_before = block_excl_scan(eq_b, buf, &ex);
+    const unsigned gt_before = block_excl_scan(sel_b, buf, &ex);
+    // ties taken by earlier chunks = min(need_eq, ties before)
+    const unsigned ties_taken_before = eq_before < need_eq ? eq_before : need_eq;
+    const unsigned sel_before = gt_before + ties_taken_before;
+    // this thread's 4 consecutive positions
+    const int base = blockIdx.x * kChunk + threadIdx.x * 4;
+    unsigned k4[4];
+    unsigned my_eq = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int c = base + i;
+        k4[i] = (c < n_cand) ? ord_key(scores[c]) : 0;
+        my_eq += (c < n_cand) && k4[i] == T;
+    }
+    unsigned eq_ex;
+    block_excl_scan(my_eq, buf, &eq_ex);
+    unsigned rank = eq_before + eq_ex;
+    bool take[4];
+    unsigned my_sel = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int c = base + i;
+        bool t = false;
+        if (c < n_cand) {
+            if (k4[i] > T) t = true;
+            else if (k4[i] == T) { t = rank < need_eq; ++rank; }
+        } else if (c < n_comp) {
+            t = true;
+        }
+        take[i] = t;
+        my_sel += t;
+    }
+    unsigned sel_ex;
+    block_excl_scan(my_sel, buf, &sel_ex);
+    unsigned o = sel_before + sel_ex;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int c = base + i;
+        if (c >= n_comp) break;
+        if (mask) mask[c] = take[i] ? 1 : 0;
+        if (take[i] && pos_out) pos_out[o] = c;
+        o += take[i];
+    }
+}
+
+__global__ void fill_kernel(int32_t *out, int n, int32_t v, int iota) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+        out[i] = iota ? i : v;
+}
+
+__global__ void scale_kernel(float *y, int n, float s) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] *= s;
+}
+
+int launch_scores(const float *q, const float *w, const void *keys, int kind, int n_comp,
+                  int n_head, int head_dim, float *scores, unsigned *hist, int n_cand,
+                  hipStream_t st) {
+    const dim3 grid((n_comp + 255) / 256);
+    switch (kind) {
+    case 0: hipLaunchKernelGGL(score_kernel<0>, grid, dim3(256), 0, st, q, w, keys, n_comp, n_head, head_dim, scores, hist, n_cand); break;
+    case 1: hipLaunchKernelGGL(score_kernel<1>, grid, dim3(256), 0, st, q, w, keys, n_comp, n_head, head_dim, scores, hist, n_cand); break;
+    default: hipLaunchKernelGGL(score_kernel<2>, grid, dim3(256), 0, st, q, w, keys, n_comp, n_head, head_dim, scores, hist, n_cand); break;
+    }
+    return hip_status(hipGetLastError());
+}
+
+// scores + selection. mask and/or pos_out; n_recent trailing positions are
+// always selected and take part in no comparison.
+size_t select_scratch_bytes(int n_comp) {
+    const size_t chunks = (size_t)(n_comp > 0 ? n_comp : 1) / kChunk + 1;
+    return (3 * kBins + 2 * chunks) * sizeof(unsigned);
+}
+
+int score_select(const float *q, const float *w, const void *keys, int kind, int n_comp,
+                 int n_head, int head_dim, int top_k, int n_recent, float *scores,
+                 unsigned *scratch, int32_t *mask, int32_t *pos_out, hipStream_t st) {
+    if (!q || !w || !keys || !scores || !scratch || n_head <= 0 || n_head > kMaxHeads ||
+        head_dim <= 0 || head_dim > kMaxDim || n_recent < 0 || (!mask && !pos_out))
+        return kEINVAL;
+    if (n_comp <= 0) return 0;
+    if (top_k <= 0) {
+        if (mask) hipLaunchKernelGGL(fill_kernel, dim3((n_comp + 255) / 256), dim3(256), 0, st, mask, n_comp, 0, 0);
+        return hip_status(hipGetLastError());
+    }
+    if (n_comp <= top_k) {
+        int rc = launch_scores(q, w, keys, kind, n_comp, n_head, head_dim, scores, nullptr, 0, st);
+        if (rc) return rc;
+        if (mask) hipLaunchKernelGGL(fill_kernel, dim3((n_comp + 255) / 256), dim3(256), 0, st, mask, n_comp, 1, 0);
+        if (pos_out) hipLaunchKernelGGL(fill_kernel, dim3((n_comp + 255) / 256), dim3(256), 0, st, pos_out, n_comp, 0, 1);
+        return hip_status(hipGetLastError());
+    }
+    const int recent = n_recent < top_k ? n_recent : top_k;
+    const int n_cand = n_comp - recent;
+    const unsigned need0 = (unsigned)(top_k - recent);
+    const int n_chunks = (n_comp + kChunk - 1) / kChunk;
+    unsigned *hists = scratch;
+    unsigned *chunk_gt = scratch + 3 * kBins;
+    unsigned *chunk_eq = chunk_gt + n_chunks;
+    hipLaunchKernelGGL(zero_u32_kernel, dim3(24), dim3(256), 0, st, hists, 3 * kBins);
+    int rc = launch_scores(q, w, keys, kind, n_comp, n_head, head_dim, scores, hists, n_cand, st);
+    if (rc) return rc;
+    const int g = (n_cand + 256 * 8 - 1) / (256 * 8) + 1;
+    hipLaunchKernelGGL(hist_next_kernel<2>, dim3(g), dim3(256), 0, st, scores, n_cand, need0, hists);
+    hipLaunchKernelGGL(hist_next_kernel<3>, dim3(g), dim3(256), 0, st, scores, n_cand, need0, hists);
+    hipLaunchKernelGGL(count_kernel, dim3(n_chunks), dim3(256), 0, st, scores, n_cand, need0, hists,
+                       chunk_gt, chunk_eq);
+    hipLaunchKernelGGL(emit_kernel, dim3(n_chunks), dim3(256), 0, st, scores, n_comp, n_cand, need0,
+                       hists, chunk_gt, chunk_eq, mask, pos_out);
+    return hip_status(hipGetLastError());
+}
+
+}  // namespace
+
+extern "C" int ds4hip_indexer_allowed_short_circuit_i32(int32_t *out_i32, int n_comp, int top_k,
+                                                        void *stream) {
+    // cuda/indexer_allowed.cu:283-305: n_comp <= 0 -> nothing; n_comp > top_k
+    // is a caller error (the reference aborts; here it is reported).
+    if (n_comp <= 0) return 0;
+    if (!out_i32 || n_comp > top_k) return ds4hip_set_last_error(kEINVAL);
+    hipLaunchKernelGGL(fill_kernel, dim3((n_comp + 127) / 128), dim3(128), 0, (hipStream_t)stream,
+                       out_i32, n_comp, 1, 0);
+    return ds4hip_set_last_error(hip_status(hipGetLastError()));
+}
+
+extern "C" int ds4hip_scale_inplace_f32(float *y, int n, float scale, void *stream) {
+    if (n <= 0) return 0;
+    if (!y) return ds4hip_set_last_error(kEINVAL);
+    hipLaunchKernelGGL(scale_kernel, dim3((n + 63) / 64), dim3(64), 0, (hipStream_t)stream, y, n, scale);
+    return ds4hip_set_last_error(hip_status(hipGetLastError()));
+}
+
+extern "C" size_t ds4hip_indexer_select_scratch_bytes(int n_comp) { return select_scratch_bytes(n_comp); }
+
+// The reference launchers take only a score scratch; the selection
+// histograms are stream-ordered allocations here.
+static int with_hists(int (*fn)(unsigned *, void *), void *ctx, int n_comp, hipStream_t st) {
+    void *h = nullptr;
+    hipError_t e = hipMallocAsync(&h, select_scratch_bytes(n_comp), st);
+    if (e != hipSuccess) return hip_status(e);
+    int rc = fn(static_cast<unsigned *>(h), ctx);
+    e = hipFreeAsync(h, st);
+    return rc ? rc : hip_status(e);
+}
+
+struct TopkCall {
+    const float *q, *w;
+    const void *keys;
+    int kind, n_comp, n_head, head_dim, top_k;
+    int32_t *allowed;
+    float *scores;
+    hipStream_t st;
+};
+
+extern "C" int ds4hip_indexer_score_topk_i32(const float *q, const float *weights,
+                                             const uint16_t *index_comp, int n_comp, int n_head,
+                                             int head_dim, int top_k, int32_t *allowed_out,
+                                             float *scratch_scores, void *stream) {
+    if (n_comp <= 0 || n_head <= 0 || head_dim <= 0) return 0;   // cuda/indexer_allowed.cu:330-331
+    TopkCall c{q, weights, index_comp, 1, n_comp, n_head, head_dim, top_k, allowed_out,
+               scratch_scores, (hipStream_t)stream};
+    return ds4hip_set_last_error(with_hists(
+        [](unsigned *h, void *p) {
+            auto *c = static_cast<TopkCall *>(p);
+            return score_select(c->q, c->w, c->keys, c->kind, c->n_comp, c->n_head, c->head_dim,
+                                c->top_k, 0, c->scores, h, c->allowed, nullptr, c->st);
+        },
+        &c, n_comp, (hipStream_t)stream));
+}
+
+extern "C" int ds4hip_indexer_score_topk_f32_i32(const float *q, const float *weights,
+                                                 const float *index_comp_f32, int n_comp,
+                                                 int n_head, int head_dim, int top_k,
+                                                 int32_t *allowed_out, float *scratch_scores,
+                                                 void *stream) {
+    if (n_comp <= 0 || n_head <= 0 || head_dim <= 0) return 0;
+    TopkCall c{q, weights, index_comp_f32, 0, n_comp, n_head, head_dim, top_k, allowed_out,
+               scratch_scores, (hipStream_t)stream};
+    return ds4hip_set_last_error(with_hists(
+        [](unsigned *h, void *p) {
+            auto *c = static_cast<TopkCall *>(p);
+            return score_select(c->q, c->w, c->keys, c->kind, c->n_comp, c->n_head, c->head_dim,
+                                c->top_k, 0, c->scores, h, c->allowed, nullptr, c->st);
+        },
+        &c, n_comp, (hipStream_t)stream));
+}
+
+extern "C" int ds4hip_indexer_topk_positions(const float *q, const float *weights,
+                                             const void *keys, int key_kind, int n_comp,
+                                             int n_head, int head_dim, int top_k, int n_recent,
+                                             float *scratch_scores, void *scratch_select,
+                                             int32_t *allowed_mask, int32_t *positions_out,
+                                             void *stream) {
+    if (key_kind < 0 || key_kind > 2) return ds4hip_set_last_error(kEINVAL);
+    return ds4hip_set_last_error(score_select(
+        q, weights, keys, key_kind, n_comp, n_head, head_dim, top_k, n_recent, scratch_scores,
+        static_cast<unsigned *>(scratch_select), allowed_mask, positions_out, (hipStream_t)stream));
+}

@@ -1,0 +1,369 @@
+// rope_matvec.hip — tail RoPE YaRN (forward / inverse) and the matvecs of the
+// attention path: f16 x fp32 (compressor / indexer projections), Q8_0 x Q8_0
+// grouped and dense (attention output chain), bf16 x fp32 batched (the
+// forward_batch output projection).
+//
+// RoPE (cuda/rope.cu:114-259, cuda/attn_out.cu:54-107,207-251): the per-layer
+// YaRN parameters and theta_scale = powf(base, -2/n_rot) are computed on the
+// host, so every caller sees the same fp32 constants; each pair thread then
+// forms theta_extrap = pos * theta_scale^k by the same sequential fp32
+// multiplications as the reference. One 64-lane wave rotates one head's
+// 32 pairs (lanes 32..63 copy the untouched dims when out != in).
+//
+// Matvecs are weight-bandwidth bound: one wave per output row, 16-byte
+// loads, activations staged once per workgroup in LDS, fp32 accumulation and
+// a wave reduction. The Q8_0 dot products use v_dot4_i32_iu8 on int8 pairs,
+// exact in int32, scaled per 32-element block as the reference does.
+
+#include "ds4hip_common.h"
+#include "../../include/ds4hip.h"
+
+#include <algorithm>
+#include <cmath>
+
+using namespace ds4hip;
+
+namespace {
+
+// ---- tail RoPE YaRN ---------------------------------------------------------------
+
+struct RopeParams {
+    float theta_scale;
+    float freq_scale;
+    float ext_factor;
+    float attn_factor;
+    float corr_low;
+    float corr_high;
+    float sin_sign;
+};
+
+// cuda/rope.cu:123-126
+int compress_ratio_of(int il) { return il < 2 ? 0 : ((il & 1) == 0 ? 4 : 128); }
+
+// cuda/rope.cu:214-250 (host-side parameter routing)
+RopeParams rope_params(int n_rot, int il, bool inverse) {
+    constexpr float kFreqBase = 10000.0f, kScale = 16.0f, kBetaFast = 32.0f, kBetaSlow = 1.0f;
+    constexpr float kCompressBase = 160000.0f;
+    constexpr int kOrigCtx = 65536;
+    const bool compressed = compress_ratio_of(il) != 0;
+    RopeParams P;
+    const float freq_base = compressed ? kCompressBase : kFreqBase;
+    P.freq_scale = compressed ? 1.0f / kScale : 1.0f;
+    P.ext_factor = compressed ? 1.0f : 0.0f;
+    P.attn_factor = 1.0f;
+    if (P.ext_factor != 0.0f) P.attn_factor /= 1.0f + 0.1f * logf(1.0f / P.freq_scale);
+    P.corr_low = P.corr_high = 0.0f;
+    if (P.ext_factor != 0.0f) {
+        const float pi = 3.14159265358979323846f;
+        auto corr_dim = [&](float target) {
+            return (float)n_rot * logf((float)kOrigCtx / (target * 2.0f * pi)) /
+                   (2.0f * logf(freq_base));
+        };
+        P.corr_low = fmaxf(0.0f, floorf(corr_dim(kBetaFast)));
+        P.corr_high = fminf((float)(n_rot - 1), ceilf(corr_dim(kBetaSlow)));
+    }
+    P.theta_scale = powf(freq_base, -2.0f / (float)n_rot);
+    P.sin_sign = inverse ? -1.0f : 1.0f;
+    return P;
+}
+
+__global__ __launch_bounds__(64) void rope_tail_kernel(const float *__restrict__ x_in,
+                                                       float *__restrict__ x_out, int head_dim,
+                                                       int n_rot, int pos, RopeParams P) {
+    const int head = blockIdx.x;
+    const int t = threadIdx.x;
+    const int n_nope = head_dim - n_rot;
+    const float *xi = x_in + (size_t)head * head_dim;
+    float *xo = x_out + (size_t)head * head_dim;
+    const int half = n_rot / 2;
+    if (xi != xo)
+        for (int d = t; d < n_nope; d += 64) xo[d] = xi[d];
+    if (t >= half) return;
+    float theta_extrap = (float)pos;
+    for (int k = 0; k < t; ++k) theta_extrap *= P.theta_scale;   // running product (rope.cu:172-177)
+    const float theta_interp = P.freq_scale * theta_extrap;
+    float theta = theta_interp;
+    float mscale = P.attn_factor;
+    if (P.ext_factor != 0.0f) {
+        // cuda/rope.cu:130-133 ramp, then the YaRN mix
+        const float y = ((float)((2 * t) / 2) - P.corr_low) / fmaxf(0.001f, P.corr_high - P.corr_low);
+        const float ramp_mix = (1.0f - fminf(1.0f, fmaxf(0.0f, y))) * P.ext_factor;
+        theta = theta_interp * (1.0f - ramp_mix) + theta_extrap * ramp_mix;
+        mscale *= 1.0f + 0.1f * logf(1.0f / P.freq_scale);
+    }
+    const float c = cosf(theta) * mscale;
+    const float s = P.sin_sign * sinf(theta) * mscale;
+    const float x0 = xi[n_nope + 2 * t], x1 = xi[n_nope + 2 * t + 1];
+    xo[n_nope + 2 * t] = x0 * c - x1 * s;
+    xo[n_nope + 2 * t + 1] = x0 * s + x1 * c;
+}
+
+int launch_rope(const float *x_in, float *x_out, int n_heads, int head_dim, int n_rot, int pos,
+                int il, bool inverse, hipStream_t st) {
+    if (!x_in || !x_out || n_heads < 0 || head_dim <= 0 || n_rot <= 0 || n_rot > 128 ||
+        (n_rot & 1) || n_rot > head_dim)
+        return kEINVAL;
+    if (n_heads == 0) return 0;
+    const RopeParams P = rope_params(n_rot, il, inverse);
+    hipLaunchKernelGGL(rope_tail_kernel, dim3(n_heads), dim3(64), 0, st, x_in, x_out, head_dim,
+                       n_rot, pos, P);
+    return hip_status(hipGetLastError());
+}
+
+// ---- wave reduction helpers ----------------------------------------------------------
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+// ---- f16 x fp32 matvec (cuda/router.cu:69-97) -----------------------------------------
+// 256 threads = 4 waves, 2 rows per wave; x staged in LDS as fp32.
+constexpr int kMvMaxIn = 16384;
+
+__global__ __launch_bounds__(256) void mv_f16_kernel(const uint16_t *__restrict__ w,
+                                                     const float *__restrict__ x,
+                                                     float *__restrict__ y, int out_dim,
+                                                     int in_dim) {
+    extern __shared__ float xs[];
+    for (int i = threadIdx.x; i < in_dim; i += 256) xs[i] = x[i];
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    for (int rr = 0; rr < 2; ++rr) {
+        const int row = (blockIdx.x * 4 + wave) * 2 + rr;
+        if (row >= out_dim) return;
+        const uint16_t *wr = w + (size_t)row * in_dim;
+        float acc = 0.0f;
+        if ((in_dim & 7) == 0) {
+            for (int i = lane * 8; i < in_dim; i += 512) {
+                const uint4_t v = *reinterpret_cast<const uint4_t *>(wr + i);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    acc = fmaf(f16_bits_to_f32((uint16_t)(v[k] & 0xFFFF)), xs[i + 2 * k], acc);
+                    acc = fmaf(f16_bits_to_f32((uint16_t)(v[k] >> 16)), xs[i + 2 * k + 1], acc);
+                }
+            }
+        } else {
+            for (int i = lane; i < in_dim; i += 64) acc = fmaf(f16_bits_to_f32(wr[i]), xs[i], acc);
+        }
+        acc = wave_sum(acc);
+        if (lane == 0) y[row] = acc;
+    }
+}
+
+// ---- Q8_0 activation quantization (cuda/attn_out.cu:119-145, dense_q8.cu) ---------------
+// One 32-lane half-wave per 32-element block: amax, d = amax/127, id = 1/d,
+// q = clamp(rint(x*id), -128, 127); the scale is kept fp32 as the reference does.
+__global__ __launch_bounds__(256) void q8_quant_kernel(const float *__restrict__ x,
+                                                       int8_t *__restrict__ xq,
+                                                       float *__restrict__ xscale, int n_blocks) {
+    const int b = (blockIdx.x * 256 + threadIdx.x) >> 5;
+    const int l = threadIdx.x & 31;
+    if (b >= n_blocks) return;
+    const float v = x[(size_t)b * 32 + l];
+    float a = fabsf(v);
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, 32));
+    const float d = a / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    int q = (int)__builtin_rintf(v * id);
+    q = q > 127 ? 127 : (q < -128 ? -128 : q);
+    xq[(size_t)b * 32 + l] = (int8_t)q;
+    if (l == 0) xscale[b] = d;
+}
+
+// ---- Q8_0 x Q8_0 matvec --------------------------------------------------------------------
+// Weight rows of n_blocks 34-byte blocks (f16 d + 32 int8). Lane l of a wave
+// handles blocks l, l+64, ...: it reads the 34 bytes with 2-byte-aligned
+// loads, the quantized activations from LDS, and accumulates
+// sum_b (d_w * d_x) * isum_b with isum_b an exact int32 dot product.
+// Rows of group g = row / rank read activation group g (cuda/attn_out.cu:171-174).
+__device__ inline int dot4(int a, int b, int c) {
+    return __builtin_amdgcn_sdot4(a, b, c, false);
+}
+
+__global__ __launch_bounds__(256) void mv_q8_kernel(const uint8_t *__restrict__ W,
+                                                    const int8_t *__restrict__ xq,
+                                                    const float *__restrict__ xscale,
+                                                    float *__restrict__ y, int n_rows,
+                                                    int n_blocks, int rank, int grouped) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int row = blockIdx.x * 4 + wave;
+    if (row >= n_rows) return;
+    const int g = grouped ? row / rank : 0;
+    const int8_t *xg = xq + (size_t)g * n_blocks * 32;
+    const float *sg = xscale + (size_t)g * n_blocks;
+    const uint8_t *wr = W + (size_t)row * n_blocks * 34;
+    float acc = 0.0f;
+    for (int b = lane; b < n_blocks; b += 64) {
+        const uint16_t *blk = reinterpret_cast<const uint16_t *>(wr + (size_t)b * 34);
+        const float dw = f16_bits_to_f32(blk[0]);
+        int isum = 0;
+        const int *xb = reinterpret_cast<const int *>(xg + (size_t)b * 32);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t wv = (uint32_t)blk[1 + 2 * k] | ((uint32_t)blk[2 + 2 * k] << 16);
+            isum = dot4((int)wv, xb[k], isum);
+        }
+        acc = fmaf(dw * sg[b], (float)isum, acc);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) y[row] = acc;
+}
+
+int launch_q8(const uint8_t *W, const float *x, float *y, int n_groups, int group_dim, int rank,
+              int8_t *xq, float *xs, bool grouped, hipStream_t st) {
+    const int bpg = group_dim / 32;
+    const int nb_total = n_groups * bpg;
+    hipLaunchKernelGGL(q8_quant_kernel, dim3((nb_total * 32 + 255) / 256), dim3(256), 0, st, x,
+                       xq, xs, nb_total);
+    int e = hip_status(hipGetLastError());
+    if (e) return e;
+    const int n_rows = grouped ? n_groups * rank : rank;
+    hipLaunchKernelGGL(mv_q8_kernel, dim3((n_rows + 3) / 4), dim3(256), 0, st, W, xq, xs, y,
+                       n_rows, bpg, rank, grouped ? 1 : 0);
+    return hip_status(hipGetLastError());
+}
+
+// ---- bf16 batched matvec / skinny GEMM: Y[b][r] = sum_c W[r][c] X[b][c] -----------------
+// For the forward_batch output projection (16 sequences x 32768 -> 4096). Each
+// wave owns 16 output rows; v_mfma_f32_16x16x32_bf16 with A = W rows (16 rows
+// x 32 cols per step, read straight from HBM) and B = X^T from LDS. X is split
+// into bf16 hi + lo parts (two MFMAs) so the activations keep ~16 mantissa
+// bits. Column chunks (split-K) are summed with fp32 atomics into a zeroed Y.
+// n_batch <= 16, n_cols % 32 == 0.
+typedef short bf16x8_t __attribute__((ext_vector_type(8)));
+constexpr int kMmCols = 2048;
+
+__device__ inline uint16_t f32_to_bf16_rne(float v) {
+    const uint32_t u = __float_as_uint(v);
+    return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+__global__ __launch_bounds__(256) void zero_kernel(float *__restrict__ y, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+        y[i] = 0.0f;
+}
+
+__global__ __launch_bounds__(256) void mm_bf16_kernel(const uint16_t *__restrict__ W,
+                                                      const float *__restrict__ X,
+                                                      float *__restrict__ Y, int n_rows,
+                                                      int n_cols, int n_batch) {
+    __shared__ uint16_t xh[16 * kMmCols];
+    __shared__ uint16_t xl[16 * kMmCols];
+    const int c0 = blockIdx.y * kMmCols;
+    const int nc = min(kMmCols, n_cols - c0);
+    for (int idx = threadIdx.x; idx < 16 * nc; idx += 256) {
+        const int b = idx / nc, c = idx % nc;
+        const float v = b < n_batch ? X[(size_t)b * n_cols + c0 + c] : 0.0f;
+        const uint16_t hi = f32_to_bf16_rne(v);
+        xh[b * kMmCols + c] = hi;
+        xl[b * kMmCols + c] = f32_to_bf16_rne(v - bf16_to_f32(hi));
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int r0 = (blockIdx.x * 4 + wave) * 16;
+    if (r0 >= n_rows) return;
+    const int i = lane & 15, q = lane >> 4;
+    const int row = min(r0 + i, n_rows - 1);
+    const uint16_t *wr = W + (size_t)row * n_cols + c0;
+    float4_t acc = float4_t{0, 0, 0, 0};
+    for (int k = 0; k < nc; k += 32) {
+        const bf16x8_t a = *reinterpret_cast<const bf16x8_t *>(wr + k + 8 * q);
+        const bf16x8_t bh = *reinterpret_cast<const bf16x8_t *>(&xh[i * kMmCols + k + 8 * q]);
+        const bf16x8_t bl = *reinterpret_cast<const bf16x8_t *>(&xl[i * kMmCols + k + 8 * q]);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bh, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bl, acc, 0, 0, 0);
+    }
+    // D[row 4q+r][batch i]
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int rr = r0 + 4 * q + r;
+        if (rr < n_rows && i < n_batch) atomicAdd(&Y[(size_t)i * n_rows + rr], acc[r]);
+    }
+}
+
+}  // namespace
+
+extern "C" int ds4hip_tail_rope_yarn_f32(const float *x_in, float *x_out, int n_heads,
+                                         int head_dim, int n_rot, int pos, int il, void *stream) {
+    return ds4hip_set_last_error(
+        launch_rope(x_in, x_out, n_heads, head_dim, n_rot, pos, il, false, (hipStream_t)stream));
+}
+
+extern "C" int ds4hip_tail_rope_yarn_inverse_f32(const float *x_in, float *x_out, int n_heads,
+                                                 int head_dim, int n_rot, int pos, int il,
+                                                 void *stream) {
+    return ds4hip_set_last_error(
+        launch_rope(x_in, x_out, n_heads, head_dim, n_rot, pos, il, true, (hipStream_t)stream));
+}
+
+extern "C" int ds4hip_mul_mv_f16_f32(const uint16_t *w_f16, const float *x_f32, float *y_f32,
+                                     int out_dim, int in_dim, void *stream) {
+    if (!w_f16 || !x_f32 || !y_f32 || out_dim < 0 || in_dim <= 0 || in_dim > kMvMaxIn)
+        return ds4hip_set_last_error(kEINVAL);
+    if (out_dim == 0) return 0;
+    hipLaunchKernelGGL(mv_f16_kernel, dim3((out_dim + 7) / 8), dim3(256), in_dim * sizeof(float),
+                       (hipStream_t)stream, w_f16, x_f32, y_f32, out_dim, in_dim);
+    return ds4hip_set_last_error(hip_status(hipGetLastError()));
+}
+
+extern "C" int ds4hip_mul_mv_q8_0_q8_0_grouped_f32_prealloc(const void *W, const float *x,
+                                                            float *y, int n_groups,
+                                                            int group_dim, int rank,
+                                                            int8_t *scratch_xq,
+                                                            float *scratch_xscale, void *stream) {
+    if (!W || !x || !y || !scratch_xq || !scratch_xscale || n_groups <= 0 || rank <= 0 ||
+        group_dim <= 0 || group_dim % 32)
+        return ds4hip_set_last_error(kEINVAL);
+    return ds4hip_set_last_error(launch_q8(static_cast<const uint8_t *>(W), x, y, n_groups,
+                                           group_dim, rank, scratch_xq, scratch_xscale, true,
+                                           (hipStream_t)stream));
+}
+
+extern "C" int ds4hip_mul_mv_q8_0_q8_0_grouped_f32(const void *W, const float *x, float *y,
+                                                   int n_groups, int group_dim, int rank,
+                                                   void *stream) {
+    if (!W || !x || !y || n_groups <= 0 || rank <= 0 || group_dim <= 0 || group_dim % 32)
+        return ds4hip_set_last_error(kEINVAL);
+    const hipStream_t st = (hipStream_t)stream;
+    const size_t n = (size_t)n_groups * group_dim;
+    void *xq = nullptr, *xs = nullptr;
+    hipError_t e = hipMallocAsync(&xq, n, st);
+    if (e == hipSuccess) e = hipMallocAsync(&xs, n / 32 * sizeof(float), st);
+    if (e != hipSuccess) return ds4hip_set_last_error(hip_status(e));
+    int rc = launch_q8(static_cast<const uint8_t *>(W), x, y, n_groups, group_dim, rank,
+                       static_cast<int8_t *>(xq), static_cast<float *>(xs), true, st);
+    const hipError_t e1 = hipFreeAsync(xq, st), e2 = hipFreeAsync(xs, st);
+    if (!rc) rc = hip_status(e1 != hipSuccess ? e1 : e2);
+    return ds4hip_set_last_error(rc);
+}
+
+extern "C" int ds4hip_mul_mv_q8_0_q8_0_f32_prealloc(const void *W, const float *x, float *y,
+                                                    int n_rows, int n_cols, int8_t *scratch_xq,
+                                                    float *scratch_xscale, void *stream) {
+    if (!W || !x || !y || !scratch_xq || !scratch_xscale || n_rows <= 0 || n_cols <= 0 ||
+        n_cols % 32)
+        return ds4hip_set_last_error(kEINVAL);
+    return ds4hip_set_last_error(launch_q8(static_cast<const uint8_t *>(W), x, y, 1, n_cols,
+                                           n_rows, scratch_xq, scratch_xscale, false,
+                                           (hipStream_t)stream));
+}
+
+extern "C" int ds4hip_mul_mm_bf16_f32(const uint16_t *W, const float *X, float *Y, int n_rows,
+                                      int n_cols, int n_batch, void *stream) {
+    if (!W || !X || !Y || n_rows <= 0 || n_cols <= 0 || n_cols % 32 || n_batch <= 0 ||
+        n_batch > 16)
+        return ds4hip_set_last_error(kEINVAL);
+    const hipStream_t st = (hipStream_t)stream;
+    const size_t ny = (size_t)n_batch * n_rows;
+    hipLaunchKernelGGL(zero_kernel, dim3((unsigned)std::min<size_t>((ny + 255) / 256, 1024)),
+                       dim3(256), 0, st, Y, ny);
+    const dim3 grid((n_rows + 63) / 64, (n_cols + kMmCols - 1) / kMmCols);
+    hipLaunchKernelGGL(mm_bf16_kernel, grid, dim3(256), 0, st, W, X, Y, n_rows, n_cols, n_batch);
+    return ds4hip_set_last_error(hip_status(hipGetLastError()));
+}

@@ -144,3 +144,151 @@ def flash_attn_decode_fp8(q, sinks, out, cache: Fp8KVCache, n_rows_per_prob, *, 
          page_table.shape[-1] if page_table is not None else 0, int(page_rows), N_HEAD,
          HEAD_DIM, N_ROT, _ptr(workspace), workspace.numel(), int(phases), _stream(stream))
     return workspace
+
+
+# ---- tail RoPE (cuda/rope.cuh:51, cuda/attn_out.cuh:52) ----------------------------------
+
+def launch_tail_rope_yarn_f32(x_in, x_out, n_heads, head_dim, n_rot, pos, il, stream=None):
+    _check(x_in, torch.float32, n_heads * head_dim, "x_in")
+    _check(x_out, torch.float32, n_heads * head_dim, "x_out")
+    call("ds4hip_tail_rope_yarn_f32", _ptr(x_in), _ptr(x_out), n_heads, head_dim, n_rot, pos, il,
+         _stream(stream))
+
+
+def launch_tail_rope_yarn_inverse_f32(x_in, x_out, n_heads, head_dim, n_rot, pos, il,
+                                      stream=None):
+    _check(x_in, torch.float32, n_heads * head_dim, "x_in")
+    _check(x_out, torch.float32, n_heads * head_dim, "x_out")
+    call("ds4hip_tail_rope_yarn_inverse_f32", _ptr(x_in), _ptr(x_out), n_heads, head_dim, n_rot,
+         pos, il, _stream(stream))
+
+
+# ---- matvecs (cuda/router.cuh:62, cuda/attn_out.cuh:86,98, cuda/dense_q8.cuh:62) ----------
+
+def launch_mul_mv_f16_f32(w_f16, x_f32, y_f32, out_dim, in_dim, stream=None):
+    _check(w_f16, torch.int16, out_dim * in_dim, "w_f16")
+    _check(x_f32, torch.float32, in_dim, "x")
+    _check(y_f32, torch.float32, out_dim, "y")
+    call("ds4hip_mul_mv_f16_f32", _ptr(w_f16), _ptr(x_f32), _ptr(y_f32), out_dim, in_dim,
+         _stream(stream))
+
+
+def launch_mul_mv_q8_0_q8_0_grouped_f32(W, x, y, n_groups, group_dim, rank, stream=None):
+    _check(W, torch.uint8, n_groups * rank * (group_dim // 32) * 34, "W")
+    _check(x, torch.float32, n_groups * group_dim, "x")
+    _check(y, torch.float32, n_groups * rank, "y")
+    call("ds4hip_mul_mv_q8_0_q8_0_grouped_f32", _ptr(W), _ptr(x), _ptr(y), n_groups, group_dim,
+         rank, _stream(stream))
+
+
+def launch_mul_mv_q8_0_q8_0_grouped_f32_prealloc(W, x, y, n_groups, group_dim, rank, scratch_xq,
+                                                 scratch_xscale, stream=None):
+    _check(W, torch.uint8, n_groups * rank * (group_dim // 32) * 34, "W")
+    _check(scratch_xq, torch.int8, n_groups * group_dim, "scratch_xq")
+    _check(scratch_xscale, torch.float32, n_groups * group_dim // 32, "scratch_xscale")
+    call("ds4hip_mul_mv_q8_0_q8_0_grouped_f32_prealloc", _ptr(W), _ptr(x), _ptr(y), n_groups,
+         group_dim, rank, _ptr(scratch_xq), _ptr(scratch_xscale), _stream(stream))
+
+
+def launch_mul_mv_q8_0_q8_0_f32_prealloc(W, x, y, n_rows, n_cols, scratch_xq, scratch_xscale,
+                                         stream=None):
+    _check(W, torch.uint8, n_rows * (n_cols // 32) * 34, "W")
+    _check(scratch_xq, torch.int8, n_cols, "scratch_xq")
+    _check(scratch_xscale, torch.float32, n_cols // 32, "scratch_xscale")
+    call("ds4hip_mul_mv_q8_0_q8_0_f32_prealloc", _ptr(W), _ptr(x), _ptr(y), n_rows, n_cols,
+         _ptr(scratch_xq), _ptr(scratch_xscale), _stream(stream))
+
+
+def mul_mm_bf16_f32(W, X, Y, n_rows, n_cols, n_batch, stream=None):
+    _check(W, torch.bfloat16, n_rows * n_cols, "W")
+    _check(X, torch.float32, n_batch * n_cols, "X")
+    _check(Y, torch.float32, n_batch * n_rows, "Y")
+    call("ds4hip_mul_mm_bf16_f32", _ptr(W), _ptr(X), _ptr(Y), n_rows, n_cols, n_batch,
+         _stream(stream))
+
+
+# ---- indexer (cuda/indexer_allowed.cuh:33,67,83,97) ----------------------------------------
+
+def launch_indexer_allowed_short_circuit_i32(out_i32, n_comp, top_k, stream=None):
+    call("ds4hip_indexer_allowed_short_circuit_i32", _ptr(out_i32), n_comp, top_k,
+         _stream(stream))
+
+
+def launch_scale_inplace_f32(y, n, scale, stream=None):
+    _check(y, torch.float32, n, "y")
+    call("ds4hip_scale_inplace_f32", _ptr(y), n, float(scale), _stream(stream))
+
+
+def launch_indexer_score_topk_i32(q, weights, index_comp, n_comp, n_head, head_dim, top_k,
+                                  allowed_out, scratch_scores, stream=None):
+    _check(index_comp, torch.int16, n_comp * head_dim, "index_comp")
+    call("ds4hip_indexer_score_topk_i32", _ptr(q), _ptr(weights), _ptr(index_comp), n_comp,
+         n_head, head_dim, top_k, _ptr(allowed_out), _ptr(scratch_scores), _stream(stream))
+
+
+def launch_indexer_score_topk_f32_i32(q, weights, index_comp_f32, n_comp, n_head, head_dim,
+                                      top_k, allowed_out, scratch_scores, stream=None):
+    _check(index_comp_f32, torch.float32, n_comp * head_dim, "index_comp_f32")
+    call("ds4hip_indexer_score_topk_f32_i32", _ptr(q), _ptr(weights), _ptr(index_comp_f32),
+         n_comp, n_head, head_dim, top_k, _ptr(allowed_out), _ptr(scratch_scores),
+         _stream(stream))
+
+
+_KEY_KIND = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+
+
+def indexer_topk_positions(q, weights, keys, top_k, n_recent, *, scores=None, select=None,
+                           mask=None, positions=None, stream=None):
+    """keys [n_comp, head_dim] fp32/f16/bf16; returns (positions, mask, scores)."""
+    n_comp, head_dim = keys.shape
+    n_head = q.numel() // head_dim
+    dev = keys.device
+    if scores is None:
+        scores = torch.empty(n_comp, dtype=torch.float32, device=dev)
+    if select is None:
+        from ._lib import lib
+        nb = lib().ds4hip_indexer_select_scratch_bytes(n_comp)
+        select = torch.empty(nb, dtype=torch.uint8, device=dev)
+    if positions is None:
+        positions = torch.empty(min(top_k, n_comp), dtype=torch.int32, device=dev)
+    call("ds4hip_indexer_topk_positions", _ptr(q), _ptr(weights), _ptr(keys),
+         _KEY_KIND[keys.dtype], n_comp, n_head, head_dim, top_k, n_recent, _ptr(scores),
+         _ptr(select), _ptr(mask), _ptr(positions), _stream(stream))
+    return positions, mask, scores
+
+
+# ---- compressor (cuda/compressor.cuh:78,102) -------------------------------------------------
+
+def launch_compressor_decode_step_f32_prealloc(is_attn, x_f32, w_kv_f16, w_gate_f16, w_ape_f16,
+                                               w_norm_f32, in_dim, head_dim_out, compress_ratio,
+                                               pos, il, state_kv, state_score, emit_out,
+                                               scratch_kv_cur, scratch_sc_cur, stream=None):
+    """Returns `emitted` (the reference's *emitted_out_host)."""
+    emitted = C.c_int(0)
+    call("ds4hip_compressor_decode_step_f32_prealloc", int(bool(is_attn)), _ptr(x_f32),
+         _ptr(w_kv_f16), _ptr(w_gate_f16), _ptr(w_ape_f16), _ptr(w_norm_f32), in_dim,
+         head_dim_out, compress_ratio, pos, il, _ptr(state_kv), _ptr(state_score), _ptr(emit_out),
+         C.byref(emitted), _ptr(scratch_kv_cur), _ptr(scratch_sc_cur), _stream(stream))
+    return emitted.value
+
+
+def launch_compressor_decode_step_f32(is_attn, x_f32, w_kv_f16, w_gate_f16, w_ape_f16,
+                                      w_norm_f32, in_dim, head_dim_out, compress_ratio, pos, il,
+                                      state_kv, state_score, emit_out, stream=None):
+    emitted = C.c_int(0)
+    call("ds4hip_compressor_decode_step_f32", int(bool(is_attn)), _ptr(x_f32), _ptr(w_kv_f16),
+         _ptr(w_gate_f16), _ptr(w_ape_f16), _ptr(w_norm_f32), in_dim, head_dim_out,
+         compress_ratio, pos, il, _ptr(state_kv), _ptr(state_score), _ptr(emit_out),
+         C.byref(emitted), _stream(stream))
+    return emitted.value
+
+
+def compressor_decode_step_w32(is_attn, x_f32, w_kv_f32, w_gate_f32, w_ape_f16, w_norm_f32,
+                               in_dim, head_dim_out, compress_ratio, pos, il, state_kv,
+                               state_score, emit_out, stream=None):
+    emitted = C.c_int(0)
+    call("ds4hip_compressor_decode_step_w32", int(bool(is_attn)), _ptr(x_f32), _ptr(w_kv_f32),
+         _ptr(w_gate_f32), _ptr(w_ape_f16), _ptr(w_norm_f32), in_dim, head_dim_out,
+         compress_ratio, pos, il, _ptr(state_kv), _ptr(state_score), _ptr(emit_out),
+         C.byref(emitted), _stream(stream))
+    return emitted.value

@@ -109,6 +109,134 @@ int ds4hip_flash_attn_decode_fp8(const void *q, int q_is_f32, long long q_stride
                                  int n_rot, void *workspace, size_t workspace_bytes,
                                  int phases, void *stream);
 
+/* ---- tail RoPE YaRN --------------------------------------------------------------- */
+
+/* Replaces ds4cuda::launch_tail_rope_yarn_f32 (cuda/rope.cuh:51): rotates the
+ * last n_rot dims of each of n_heads rows of head_dim floats with the layer
+ * il's YaRN parameters at position pos; the other dims are copied. In-place
+ * safe. n_rot even, <= 128. */
+int ds4hip_tail_rope_yarn_f32(const float *x_in, float *x_out, int n_heads, int head_dim,
+                              int n_rot, int pos, int il, void *stream);
+
+/* Replaces ds4cuda::launch_tail_rope_yarn_inverse_f32 (cuda/attn_out.cuh:52):
+ * the same rotation with the sine negated. */
+int ds4hip_tail_rope_yarn_inverse_f32(const float *x_in, float *x_out, int n_heads,
+                                      int head_dim, int n_rot, int pos, int il, void *stream);
+
+/* ---- matvecs ------------------------------------------------------------------------ */
+
+/* Replaces ds4cuda::launch_mul_mv_f16_f32 (cuda/router.cuh:62): y[o] =
+ * sum_i f16(w[o*in_dim + i]) * x[i], fp32 accumulation. in_dim <= 16384. */
+int ds4hip_mul_mv_f16_f32(const uint16_t *w_f16, const float *x_f32, float *y_f32, int out_dim,
+                          int in_dim, void *stream);
+
+/* Replaces ds4cuda::launch_mul_mv_q8_0_q8_0_grouped_f32 (cuda/attn_out.cuh:86).
+ * W: n_groups*rank rows of group_dim/32 block_q8_0 records (34 bytes: f16 d,
+ * 32 int8). x: n_groups*group_dim fp32, quantized per 32 elements
+ * (d = amax/127, fp32 scale). Row r reads group r / rank. Activation scratch is
+ * stream-ordered (hipMallocAsync). */
+int ds4hip_mul_mv_q8_0_q8_0_grouped_f32(const void *W, const float *x, float *y, int n_groups,
+                                        int group_dim, int rank, void *stream);
+
+/* Replaces ds4cuda::launch_mul_mv_q8_0_q8_0_grouped_f32_prealloc
+ * (cuda/attn_out.cuh:98): caller scratch int8 [n_groups*group_dim] and
+ * fp32 [n_groups*group_dim/32]; allocates nothing. */
+int ds4hip_mul_mv_q8_0_q8_0_grouped_f32_prealloc(const void *W, const float *x, float *y,
+                                                 int n_groups, int group_dim, int rank,
+                                                 int8_t *scratch_xq, float *scratch_xscale,
+                                                 void *stream);
+
+/* Replaces ds4cuda::launch_mul_mv_q8_0_q8_0_f32_prealloc (cuda/dense_q8.cuh:62):
+ * dense Q8_0 x Q8_0, W n_rows x n_cols. */
+int ds4hip_mul_mv_q8_0_q8_0_f32_prealloc(const void *W, const float *x, float *y, int n_rows,
+                                         int n_cols, int8_t *scratch_xq, float *scratch_xscale,
+                                         void *stream);
+
+/* Batched bf16 projection (additive; the forward_batch form of the attention
+ * output projection): Y[b][r] = sum_c W[r][c] X[b][c] for n_batch <= 16 rows
+ * of X, W bf16 [n_rows][n_cols], n_cols % 32 == 0. Y is overwritten. */
+int ds4hip_mul_mm_bf16_f32(const uint16_t *W, const float *X, float *Y, int n_rows, int n_cols,
+                           int n_batch, void *stream);
+
+/* ---- indexer --------------------------------------------------------------------------- */
+
+/* Replaces ds4cuda::launch_indexer_allowed_short_circuit_i32
+ * (cuda/indexer_allowed.cuh:33): out[0..n_comp) = 1. n_comp <= 0 is a no-op;
+ * n_comp > top_k returns -22 (the reference aborts). */
+int ds4hip_indexer_allowed_short_circuit_i32(int32_t *out_i32, int n_comp, int top_k,
+                                             void *stream);
+
+/* Replaces ds4cuda::launch_scale_inplace_f32 (cuda/indexer_allowed.cuh:97). */
+int ds4hip_scale_inplace_f32(float *y, int n, float scale, void *stream);
+
+/* Replaces ds4cuda::launch_indexer_score_topk_i32 (cuda/indexer_allowed.cuh:67):
+ * scores score[c] = sum_h w[h] relu(q_h . k_c) over f16 keys into
+ * scratch_scores, then allowed[c] = 1 for the top_k (score desc, index asc),
+ * 0 otherwise; n_comp <= top_k -> all ones; top_k <= 0 -> all zeros;
+ * n_comp <= 0 or n_head/head_dim <= 0 -> nothing. n_head <= 64, head_dim <= 128.
+ * Scores use a fixed fma order (dot over d ascending, then heads ascending) so
+ * the selection is reproducible exactly. Selection scratch is stream-ordered. */
+int ds4hip_indexer_score_topk_i32(const float *q, const float *weights,
+                                  const uint16_t *index_comp, int n_comp, int n_head,
+                                  int head_dim, int top_k, int32_t *allowed_out,
+                                  float *scratch_scores, void *stream);
+
+/* Replaces ds4cuda::launch_indexer_score_topk_f32_i32 (cuda/indexer_allowed.cuh:83):
+ * the same over fp32 keys. */
+int ds4hip_indexer_score_topk_f32_i32(const float *q, const float *weights,
+                                      const float *index_comp_f32, int n_comp, int n_head,
+                                      int head_dim, int top_k, int32_t *allowed_out,
+                                      float *scratch_scores, void *stream);
+
+/* Bytes of selection scratch ds4hip_indexer_topk_positions needs for n_comp keys. */
+size_t ds4hip_indexer_select_scratch_bytes(int n_comp);
+
+/* Sparse-decode selection (additive; generalizes cuda/indexer_allowed.cu:200-279).
+ * keys: key_kind 0 = fp32, 1 = f16, 2 = bf16, [n_comp][head_dim]. The last
+ * n_recent positions are always selected; of the rest the best
+ * top_k - n_recent by (score desc, index asc). allowed_mask [n_comp] (0/1)
+ * and/or positions_out [min(top_k, n_comp)] (ascending) may be NULL. */
+int ds4hip_indexer_topk_positions(const float *q, const float *weights, const void *keys,
+                                  int key_kind, int n_comp, int n_head, int head_dim, int top_k,
+                                  int n_recent, float *scratch_scores, void *scratch_select,
+                                  int32_t *allowed_mask, int32_t *positions_out, void *stream);
+
+/* ---- compressor ------------------------------------------------------------------------ */
+
+/* Replaces ds4cuda::launch_compressor_decode_step_f32_prealloc
+ * (cuda/compressor.cuh:102): one streaming-compressor step for token pos of
+ * layer il. is_attn != 0 FP8 round-trips the emitted row. *emitted_out_host
+ * (host int, may be NULL) is set from pos: 1 when (pos + 1) % ratio == 0.
+ * ratio 4 or 128; head_dim_out <= 512; in_dim <= 8192. */
+int ds4hip_compressor_decode_step_f32_prealloc(int is_attn, const float *x_f32,
+                                               const uint16_t *w_kv_f16,
+                                               const uint16_t *w_gate_f16,
+                                               const uint16_t *w_ape_f16,
+                                               const float *w_norm_f32, int in_dim,
+                                               int head_dim_out, int compress_ratio, int pos,
+                                               int il, float *state_kv, float *state_score,
+                                               float *emit_out, int *emitted_out_host,
+                                               float *scratch_kv_cur, float *scratch_sc_cur,
+                                               void *stream);
+
+/* Replaces ds4cuda::launch_compressor_decode_step_f32 (cuda/compressor.cuh:78);
+ * needs no scratch (the projections go straight into the state rows). */
+int ds4hip_compressor_decode_step_f32(int is_attn, const float *x_f32, const uint16_t *w_kv_f16,
+                                      const uint16_t *w_gate_f16, const uint16_t *w_ape_f16,
+                                      const float *w_norm_f32, int in_dim, int head_dim_out,
+                                      int compress_ratio, int pos, int il, float *state_kv,
+                                      float *state_score, float *emit_out,
+                                      int *emitted_out_host, void *stream);
+
+/* The same step with fp32 projection weights (additive; the batched-decode
+ * configuration states fp32 compressor weights). */
+int ds4hip_compressor_decode_step_w32(int is_attn, const float *x_f32, const float *w_kv_f32,
+                                      const float *w_gate_f32, const uint16_t *w_ape_f16,
+                                      const float *w_norm_f32, int in_dim, int head_dim_out,
+                                      int compress_ratio, int pos, int il, float *state_kv,
+                                      float *state_score, float *emit_out,
+                                      int *emitted_out_host, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

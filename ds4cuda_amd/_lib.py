@@ -16,6 +16,7 @@ _vp, _i, _ll, _sz = C.c_void_p, C.c_int, C.c_longlong, C.c_size_t
 SIGNATURES: dict[str, list] = {
     "ds4hip_get_last_error": [],
     "ds4hip_set_last_error": [_i],
+    "ds4hip_clear_last_error": [],
     "ds4hip_version": [],
     "ds4hip_fp8_kv_quantize_round_trip_f32": [_vp, _vp, _i, _i, _i, _vp],
     "ds4hip_fp8_kv_quantize_append": [_vp, _i, _i, _i, _vp, _vp, _vp, _ll, _vp, _vp],
@@ -45,10 +46,21 @@ SIGNATURES: dict[str, list] = {
                                           _vp, _vp, _vp, _vp],
     "ds4hip_compressor_decode_step_w32": [_i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp,
                                           _vp, _vp, _vp, _vp],
+    "ds4hip_swa_push_f32": [_vp, C.POINTER(_i), _i, _vp, _i, _vp],
+    "ds4hip_comp_push_f32": [_vp, C.POINTER(_i), _i, _vp, _i, _vp],
+    "ds4hip_session_state_arena_bytes": [_i],
+    "ds4hip_session_state_alloc": [_vp, _i],
+    "ds4hip_session_state_free": [_vp],
+    "ds4hip_session_state_reset": [_vp, _vp],
+    "ds4hip_session_push_raw": [_vp, _i, _vp, _vp],
+    "ds4hip_session_push_comp": [_vp, _i, _vp, _vp],
+    "ds4hip_session_push_index_comp": [_vp, _i, _vp, _vp],
+    "ds4hip_session_layer_rows": [_vp, _i, _i, C.POINTER(_vp), C.POINTER(_ll), C.POINTER(_vp)],
 }
 
 # entry points that return a value rather than a status
-RESTYPES = {"ds4hip_indexer_select_scratch_bytes": C.c_size_t}
+RESTYPES = {"ds4hip_indexer_select_scratch_bytes": C.c_size_t,
+            "ds4hip_session_state_arena_bytes": C.c_size_t}
 
 _lib = None
 

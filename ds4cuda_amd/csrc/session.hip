@@ -1,0 +1,347 @@
+// session.hip — KV push / SWA eviction and the per-session KV arena.
+//
+// Two forms:
+//  * The reference's fp32 row layout (ds4hip_swa_push_f32 / ds4hip_comp_push_f32):
+//    the raw sliding window is a linear array, oldest row first; when it is full
+//    the rows move down by one and the new row goes last (memmove semantics,
+//    cuda/forward_layer.cu:159-190,941-972); every stored element is
+//    f16-rounded. Compressed rows append with no eviction; a full cache is an
+//    error (cuda/forward_layer.cu:1021-1034).
+//  * The FP8 session (ds4hip_session_state_*): every layer owns a range of FP8
+//    cache rows, compressed rows first ([0, cap_comp)) then a 128-row SWA ring
+//    ([cap_comp, cap_comp + 128)). The ring is a true ring: a push overwrites
+//    the oldest slot, so eviction costs one row write instead of a 127-row move.
+//    Attention is order-free over its rows, so the window's set of rows is all
+//    that matters; a constant per-layer row list (ring slots in reverse, then
+//    the compressed rows in order) makes "the n_raw valid ring rows followed by
+//    the first n_comp compressed rows" one contiguous slice of that list, which
+//    the decode kernel reads as its row-index array.
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+
+#include "../../include/ds4hip_session.h"
+#include "ds4hip_common.h"
+
+using namespace ds4hip;
+
+namespace {
+
+constexpr int kShiftChunk = 16;
+
+// f16 round trip of one fp32 value (round to nearest even), as stored rows are.
+__device__ inline float f16_round(float v) { return __half2float(__float2half(v)); }
+
+// Moves rows [1, n_rows) of a [n_rows][head_dim] fp32 array down by one, in
+// place, f16-rounding on the way. One thread owns one column and walks it from
+// low to high rows; each chunk of kShiftChunk rows is loaded before any of it
+// is stored, and only rows at or below the last loaded one are stored.
+__global__ __launch_bounds__(256) void swa_shift_kernel(float *__restrict__ base, int head_dim,
+                                                        int n_rows) {
+    const int col = blockIdx.x * blockDim.x + threadIdx.x;
+    if (col >= head_dim) return;
+    float *p = base + col;
+    for (int r0 = 0; r0 + 1 < n_rows; r0 += kShiftChunk) {
+        float v[kShiftChunk];
+#pragma unroll
+        for (int i = 0; i < kShiftChunk; ++i)
+            if (r0 + 1 + i < n_rows) v[i] = p[(size_t)(r0 + 1 + i) * head_dim];
+#pragma unroll
+        for (int i = 0; i < kShiftChunk; ++i)
+            if (r0 + 1 + i < n_rows) p[(size_t)(r0 + i) * head_dim] = f16_round(v[i]);
+    }
+}
+
+__global__ __launch_bounds__(256) void row_write_kernel(float *__restrict__ dst,
+                                                        const float *__restrict__ src, int n,
+                                                        int round_f16) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) dst[i] = round_f16 ? f16_round(src[i]) : src[i];
+}
+
+__global__ __launch_bounds__(256) void fill_f32_kernel(float *__restrict__ p, size_t n, float v) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x)
+        p[i] = v;
+}
+
+__global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t *__restrict__ p, size_t n,
+                                                       uint32_t v) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x)
+        p[i] = v;
+}
+
+// Row list of one layer: [cap_raw - 1 - k + cap_comp for k < cap_raw] then
+// [c for c < cap_comp] (row numbers relative to the layer's first row).
+__global__ __launch_bounds__(256) void row_list_kernel(int32_t *__restrict__ list, int cap_raw,
+                                                       int cap_comp) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < cap_raw) list[i] = cap_comp + cap_raw - 1 - i;
+    else if (i < cap_raw + cap_comp) list[i] = i - cap_raw;
+}
+
+inline unsigned fill_grid(size_t n) {
+    size_t g = (n + 255) / 256;
+    return (unsigned)(g < 2048 ? (g ? g : 1) : 2048);
+}
+
+int layer_ratio(int il) { return il < 2 ? 0 : ((il & 1) == 0 ? 4 : 128); }
+
+size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+
+struct Plan {
+    int cap_raw;
+    int cap_comp[DS4HIP_N_LAYER];
+    long long row_base[DS4HIP_N_LAYER];
+    long long n_rows;
+    size_t off_codes, off_sexp, off_tail, off_lists, off_state, bytes;
+    size_t list_off[DS4HIP_N_LAYER];
+    size_t state_off[DS4HIP_N_LAYER];  // attn kv, attn score, idx comp, idx kv, idx score
+};
+
+size_t attn_state_cells(int ratio) {
+    const int coff = ratio == 4 ? 2 : 1;
+    return (size_t)coff * ratio * coff * DS4HIP_HEAD_DIM;
+}
+size_t index_state_cells() { return (size_t)2 * 4 * 2 * DS4HIP_INDEXER_HEAD_DIM; }
+
+size_t layer_state_bytes(int ratio, int cap_comp) {
+    if (ratio == 0) return 0;
+    size_t b = 2 * align256(attn_state_cells(ratio) * 4);
+    if (ratio == 4)
+        b += align256((size_t)cap_comp * DS4HIP_INDEXER_HEAD_DIM * 4) +
+             2 * align256(index_state_cells() * 4);
+    return b;
+}
+
+Plan make_plan(int max_context) {
+    Plan P{};
+    P.cap_raw = max_context < DS4HIP_N_SWA ? max_context : DS4HIP_N_SWA;
+    long long rows = 0;
+    for (int il = 0; il < DS4HIP_N_LAYER; ++il) {
+        const int r = layer_ratio(il);
+        P.cap_comp[il] = r ? max_context / r + 2 : 0;  // cuda/session_state.cu:137
+        P.row_base[il] = rows;
+        rows += P.cap_comp[il] + P.cap_raw;
+    }
+    P.n_rows = rows;
+    size_t off = 0;
+    P.off_codes = off;
+    off += align256((size_t)rows * DS4HIP_FP8_CODES);
+    P.off_sexp = off;
+    off += align256((size_t)rows * DS4HIP_FP8_SEXP);
+    P.off_tail = off;
+    off += align256((size_t)rows * DS4HIP_FP8_TAIL * 2);
+    P.off_lists = off;
+    for (int il = 0; il < DS4HIP_N_LAYER; ++il) {
+        P.list_off[il] = off;
+        off += align256((size_t)(P.cap_raw + P.cap_comp[il]) * 4);
+    }
+    P.off_state = off;
+    for (int il = 0; il < DS4HIP_N_LAYER; ++il) {
+        P.state_off[il] = off;
+        off += layer_state_bytes(layer_ratio(il), P.cap_comp[il]);
+    }
+    P.bytes = off;
+    return P;
+}
+
+int fill(float *p, size_t n, float v, hipStream_t st) {
+    if (!p || !n) return 0;
+    hipLaunchKernelGGL(fill_f32_kernel, dim3(fill_grid(n)), dim3(256), 0, st, p, n, v);
+    return hip_status(hipGetLastError());
+}
+
+int init_buffers(ds4hip_session_state *s, hipStream_t st) {
+    s->pos = 0;
+    s->n_tokens_processed = 0;
+    int rc = 0;
+    // Cache rows are zeroed so a stale row never holds NaN bit patterns.
+    const size_t cache_words = (s->codes_bytes + 3) / 4;
+    hipLaunchKernelGGL(fill_u32_kernel, dim3(fill_grid(cache_words)), dim3(256), 0, st,
+                       (uint32_t *)s->arena_base, cache_words, 0u);
+    if ((rc = hip_status(hipGetLastError()))) return rc;
+    for (int il = 0; il < DS4HIP_N_LAYER; ++il) {
+        ds4hip_layer_state *L = &s->layers[il];
+        L->n_raw = L->raw_head = L->n_comp = L->n_index_comp = 0;
+        // The compressed part may hold an indexer selection from the last sequence.
+        const int nl = L->cap_raw + L->cap_comp;
+        hipLaunchKernelGGL(row_list_kernel, dim3((nl + 255) / 256), dim3(256), 0, st, L->row_list,
+                           L->cap_raw, L->cap_comp);
+        if ((rc = hip_status(hipGetLastError()))) return rc;
+        if (!L->compress_ratio) continue;
+        const size_t cells = attn_state_cells(L->compress_ratio);
+        if ((rc = fill(L->attn_state_kv, cells, 0.f, st))) return rc;
+        if ((rc = fill(L->attn_state_score, cells, -INFINITY, st))) return rc;
+        if (L->has_indexer) {
+            if ((rc = fill(L->index_comp_kv, (size_t)L->cap_comp * DS4HIP_INDEXER_HEAD_DIM, 0.f,
+                           st)))
+                return rc;
+            if ((rc = fill(L->index_state_kv, index_state_cells(), 0.f, st))) return rc;
+            if ((rc = fill(L->index_state_score, index_state_cells(), -INFINITY, st))) return rc;
+        }
+    }
+    return 0;
+}
+
+bool layer_ok(const ds4hip_session_state *s, int il) {
+    return s && s->arena_base && il >= 0 && il < DS4HIP_N_LAYER;
+}
+
+}  // namespace
+
+// ---- reference fp32 layout ------------------------------------------------------------------
+
+extern "C" int ds4hip_swa_push_f32(float *raw_kv, int *n_raw_host, int cap_raw,
+                                   const float *kv_cur, int head_dim, void *stream) {
+    if (!raw_kv || !n_raw_host || !kv_cur || cap_raw <= 0 || head_dim <= 0 || *n_raw_host < 0 ||
+        *n_raw_host > cap_raw)
+        return ds4hip_set_last_error(kEINVAL);
+    const hipStream_t st = (hipStream_t)stream;
+    int slot = *n_raw_host;
+    if (slot == cap_raw) {
+        hipLaunchKernelGGL(swa_shift_kernel, dim3((head_dim + 255) / 256), dim3(256), 0, st,
+                           raw_kv, head_dim, cap_raw);
+        slot = cap_raw - 1;
+    }
+    hipLaunchKernelGGL(row_write_kernel, dim3((head_dim + 255) / 256), dim3(256), 0, st,
+                       raw_kv + (size_t)slot * head_dim, kv_cur, head_dim, 1);
+    const int rc = ds4hip_set_last_error(hip_status(hipGetLastError()));
+    if (!rc) *n_raw_host = slot + 1;
+    return rc;
+}
+
+extern "C" int ds4hip_comp_push_f32(float *comp_kv, int *n_comp_host, int cap_comp,
+                                    const float *row, int head_dim, void *stream) {
+    if (!comp_kv || !n_comp_host || !row || head_dim <= 0 || *n_comp_host < 0)
+        return ds4hip_set_last_error(kEINVAL);
+    if (*n_comp_host >= cap_comp) return ds4hip_set_last_error(DS4HIP_ENOSPC);
+    hipLaunchKernelGGL(row_write_kernel, dim3((head_dim + 255) / 256), dim3(256), 0,
+                       (hipStream_t)stream, comp_kv + (size_t)*n_comp_host * head_dim, row,
+                       head_dim, 0);
+    const int rc = ds4hip_set_last_error(hip_status(hipGetLastError()));
+    if (!rc) ++*n_comp_host;
+    return rc;
+}
+
+// ---- FP8 session --------------------------------------------------------------------------
+
+extern "C" size_t ds4hip_session_state_arena_bytes(int max_context) {
+    if (max_context <= 0) return 0;
+    return make_plan(max_context).bytes;
+}
+
+extern "C" int ds4hip_session_state_alloc(ds4hip_session_state *out, int max_context) {
+    if (!out || max_context <= 0) return ds4hip_set_last_error(kEINVAL);
+    std::memset(out, 0, sizeof(*out));
+    const Plan P = make_plan(max_context);
+    void *base = nullptr;
+    int rc = hip_status(hipMalloc(&base, P.bytes));
+    if (rc) return ds4hip_set_last_error(rc);
+    uint8_t *b = (uint8_t *)base;
+    out->max_context = max_context;
+    out->arena_base = base;
+    out->arena_bytes = P.bytes;
+    out->codes = b + P.off_codes;
+    out->sexp = (int8_t *)(b + P.off_sexp);
+    out->tail = (uint16_t *)(b + P.off_tail);
+    out->n_cache_rows = P.n_rows;
+    out->codes_bytes = P.off_lists;
+    for (int il = 0; il < DS4HIP_N_LAYER; ++il) {
+        ds4hip_layer_state *L = &out->layers[il];
+        const int r = layer_ratio(il);
+        L->il = il;
+        L->compress_ratio = r;
+        L->has_indexer = r == 4;
+        L->cap_raw = P.cap_raw;
+        L->cap_comp = P.cap_comp[il];
+        L->row_base = P.row_base[il];
+        L->row_list = (int32_t *)(b + P.list_off[il]);
+        if (!r) continue;
+        uint8_t *p = b + P.state_off[il];
+        const size_t sb = align256(attn_state_cells(r) * 4);
+        L->attn_state_kv = (float *)p;
+        L->attn_state_score = (float *)(p + sb);
+        p += 2 * sb;
+        if (r == 4) {
+            L->index_comp_kv = (float *)p;
+            p += align256((size_t)L->cap_comp * DS4HIP_INDEXER_HEAD_DIM * 4);
+            const size_t ib = align256(index_state_cells() * 4);
+            L->index_state_kv = (float *)p;
+            L->index_state_score = (float *)(p + ib);
+        }
+    }
+    rc = hip_status(hipGetLastError());
+    if (!rc) rc = init_buffers(out, 0);
+    if (!rc) rc = hip_status(hipStreamSynchronize(0));
+    if (rc) {
+        (void)hipFree(base);
+        std::memset(out, 0, sizeof(*out));
+        return ds4hip_set_last_error(rc);
+    }
+    return 0;
+}
+
+extern "C" int ds4hip_session_state_free(ds4hip_session_state *s) {
+    if (!s) return 0;
+    int rc = 0;
+    if (s->arena_base) rc = hip_status(hipFree(s->arena_base));
+    std::memset(s, 0, sizeof(*s));
+    return rc ? ds4hip_set_last_error(rc) : 0;
+}
+
+extern "C" int ds4hip_session_state_reset(ds4hip_session_state *s, void *stream) {
+    if (!s || !s->arena_base) return ds4hip_set_last_error(kEINVAL);
+    return ds4hip_set_last_error(init_buffers(s, (hipStream_t)stream));
+}
+
+extern "C" int ds4hip_session_push_raw(ds4hip_session_state *s, int il, const float *kv_cur,
+                                       void *stream) {
+    if (!layer_ok(s, il) || !kv_cur) return ds4hip_set_last_error(kEINVAL);
+    ds4hip_layer_state *L = &s->layers[il];
+    const long long row = L->row_base + L->cap_comp + L->raw_head;
+    const int rc = ds4hip_fp8_kv_quantize_append(kv_cur, 1, DS4HIP_HEAD_DIM, DS4HIP_N_ROT, s->codes,
+                                                 s->sexp, s->tail, row, nullptr, stream);
+    if (rc) return rc;
+    L->raw_head = (L->raw_head + 1) % L->cap_raw;
+    if (L->n_raw < L->cap_raw) ++L->n_raw;
+    return 0;
+}
+
+extern "C" int ds4hip_session_push_comp(ds4hip_session_state *s, int il, const float *row,
+                                        void *stream) {
+    if (!layer_ok(s, il) || !row) return ds4hip_set_last_error(kEINVAL);
+    ds4hip_layer_state *L = &s->layers[il];
+    if (!L->compress_ratio) return ds4hip_set_last_error(kEINVAL);
+    if (L->n_comp >= L->cap_comp) return ds4hip_set_last_error(DS4HIP_ENOSPC);
+    const int rc = ds4hip_fp8_kv_quantize_append(row, 1, DS4HIP_HEAD_DIM, DS4HIP_N_ROT, s->codes,
+                                                 s->sexp, s->tail, L->row_base + L->n_comp,
+                                                 nullptr, stream);
+    if (!rc) ++L->n_comp;
+    return rc;
+}
+
+extern "C" int ds4hip_session_push_index_comp(ds4hip_session_state *s, int il, const float *row,
+                                              void *stream) {
+    if (!layer_ok(s, il) || !row) return ds4hip_set_last_error(kEINVAL);
+    ds4hip_layer_state *L = &s->layers[il];
+    if (!L->has_indexer) return ds4hip_set_last_error(kEINVAL);
+    return ds4hip_comp_push_f32(L->index_comp_kv, &L->n_index_comp, L->cap_comp, row,
+                                DS4HIP_INDEXER_HEAD_DIM, stream);
+}
+
+extern "C" int ds4hip_session_layer_rows(const ds4hip_session_state *s, int il, int n_selected,
+                                         const int32_t **row_idx, long long *n_rows,
+                                         int32_t **selected_out) {
+    if (!layer_ok(s, il) || !row_idx || !n_rows) return ds4hip_set_last_error(kEINVAL);
+    const ds4hip_layer_state *L = &s->layers[il];
+    const int n_sel = n_selected < 0 ? L->n_comp : n_selected;
+    if (n_sel > L->cap_comp) return ds4hip_set_last_error(kEINVAL);
+    *row_idx = L->row_list + (L->cap_raw - L->n_raw);
+    *n_rows = (long long)L->n_raw + n_sel;
+    if (selected_out) *selected_out = L->row_list + L->cap_raw;
+    return 0;
+}

@@ -32,6 +32,9 @@ extern "C" {
  * for the void-returning C++ shims. Reading it does not clear it. */
 int ds4hip_get_last_error(void);
 int ds4hip_set_last_error(int code);
+/* Returns the last non-zero status and resets it to 0 (the analogue of
+ * hipGetLastError for this library). */
+int ds4hip_clear_last_error(void);
 /* Library version, (major << 16) | minor. */
 int ds4hip_version(void);
 

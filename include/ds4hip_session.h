@@ -1,0 +1,130 @@
+/* ds4hip_session.h — KV push / SWA eviction and the per-session KV arena.
+ *
+ * Same status convention as ds4hip.h (0, -22, -28 = cache full,
+ * -1000 - hipError_t). Counters passed as host ints are updated only when the
+ * call succeeds.
+ */
+#ifndef DS4HIP_SESSION_H
+#define DS4HIP_SESSION_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "ds4hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DS4HIP_N_LAYER 43
+#define DS4HIP_N_SWA 128
+#define DS4HIP_HEAD_DIM 512
+#define DS4HIP_N_ROT 64
+#define DS4HIP_INDEXER_HEAD_DIM 128
+#define DS4HIP_FP8_CODES 448 /* bytes of E4M3 codes per cache row */
+#define DS4HIP_FP8_SEXP 8    /* scale exponents per cache row (7 used) */
+#define DS4HIP_FP8_TAIL 64   /* f16 tail elements per cache row */
+#define DS4HIP_ENOSPC (-28)
+
+/* ---- reference fp32 row layout --------------------------------------------------- */
+
+/* Raw sliding-window push (cuda/forward_layer.cu:941-972 with the kernels at
+ * :159-190). raw_kv is [cap_raw][head_dim] fp32, rows [0, *n_raw_host) valid,
+ * oldest first. If *n_raw_host < cap_raw the f16-rounded kv_cur goes to row
+ * *n_raw_host and the count grows; otherwise rows 1..cap_raw-1 move down one
+ * (f16-rounded, memmove order) and kv_cur goes to the last row. */
+int ds4hip_swa_push_f32(float *raw_kv, int *n_raw_host, int cap_raw, const float *kv_cur,
+                        int head_dim, void *stream);
+
+/* Compressed-row append (cuda/forward_layer.cu:1021-1034): copies row to
+ * comp_kv[*n_comp_host] and increments the count; -28 when the cache is full
+ * (there is no eviction). */
+int ds4hip_comp_push_f32(float *comp_kv, int *n_comp_host, int cap_comp, const float *row,
+                         int head_dim, void *stream);
+
+/* ---- FP8 session arena ------------------------------------------------------------ */
+
+/* FP8 form of struct ds4_layer_state (include/ds4cuda.h:310-360): the KV rows
+ * live in the session's FP8 cache (codes/sexp/tail, layout of ds4hip.h); the
+ * layer owns rows [row_base, row_base + cap_comp + cap_raw): compressed rows
+ * first, then the SWA ring. Compressor and indexer state stay fp32. */
+typedef struct ds4hip_layer_state {
+    int il;
+    int compress_ratio; /* 0 (il < 2), 4 (even il >= 2), 128 (odd il >= 3) */
+    int has_indexer;    /* compress_ratio == 4 */
+    int cap_raw;        /* min(128, max_context) */
+    int n_raw;          /* valid ring rows */
+    int raw_head;       /* next ring slot to write (the oldest row once full) */
+    int cap_comp;       /* max_context / ratio + 2 (cuda/session_state.cu:137) */
+    int n_comp;
+    int n_index_comp;
+    long long row_base;
+    /* device int32 [cap_raw + cap_comp]: cap_comp + cap_raw - 1 - k for the
+     * ring part, then 0..cap_comp-1 (compressed rows in order, or the
+     * indexer's selection written there); values are relative to row_base. */
+    int32_t *row_list;
+    float *attn_state_kv;     /* [coff*ratio][coff*512], coff = 2 for ratio 4 */
+    float *attn_state_score;  /* same shape, -inf after reset */
+    float *index_comp_kv;     /* [cap_comp][128] (ratio 4 only) */
+    float *index_state_kv;    /* [8][256] */
+    float *index_state_score; /* [8][256], -inf after reset */
+} ds4hip_layer_state;
+
+/* FP8 form of struct ds4_session_state (include/ds4cuda.h:392-425): one
+ * device allocation carved into the FP8 cache, the row lists and the
+ * compressor state. The hyper-connection residual and activation arena of the
+ * reference belong to the rest of the layer and are not part of it. */
+typedef struct ds4hip_session_state {
+    int max_context;
+    int pos;
+    int n_tokens_processed;
+    ds4hip_layer_state layers[DS4HIP_N_LAYER];
+    uint8_t *codes;  /* [n_cache_rows][448] */
+    int8_t *sexp;    /* [n_cache_rows][8] */
+    uint16_t *tail;  /* [n_cache_rows][64] f16 */
+    long long n_cache_rows;
+    size_t codes_bytes; /* bytes of the cache region at the start of the arena */
+    void *arena_base;
+    size_t arena_bytes;
+} ds4hip_session_state;
+
+/* Device bytes ds4hip_session_state_alloc takes for max_context tokens (pure
+ * size calculation; cuda/session_state.cu:147 for the fp32 form). */
+size_t ds4hip_session_state_arena_bytes(int max_context);
+
+/* One hipMalloc, carved; cache rows zeroed, compressor scores -inf, counters
+ * 0 (cuda/session_state.cu:110-256). Synchronizes the null stream once. */
+int ds4hip_session_state_alloc(ds4hip_session_state *out, int max_context);
+
+/* Frees the arena and zeroes *s; a zeroed struct is a no-op. */
+int ds4hip_session_state_free(ds4hip_session_state *s);
+
+/* Re-initializes buffers and counters for a new sequence, on stream. */
+int ds4hip_session_state_reset(ds4hip_session_state *s, void *stream);
+
+/* Quantizes kv_cur [512] fp32 into layer il's SWA ring (overwriting the
+ * oldest row once the ring is full). */
+int ds4hip_session_push_raw(ds4hip_session_state *s, int il, const float *kv_cur, void *stream);
+
+/* Quantizes an emitted compressed row [512] into the next compressed slot;
+ * -28 when full, -22 on a layer without compression. */
+int ds4hip_session_push_comp(ds4hip_session_state *s, int il, const float *row, void *stream);
+
+/* Appends an indexer key row [128] fp32; -28 when full. */
+int ds4hip_session_push_index_comp(ds4hip_session_state *s, int il, const float *row,
+                                   void *stream);
+
+/* Rows for layer il's decode attention: *row_idx (device) and *n_rows are
+ * the row_idx / n_rows arguments of ds4hip_flash_attn_decode_fp8 with
+ * row_base = layers[il].row_base: the valid ring rows, then n_selected
+ * compressed rows (n_selected < 0: all n_comp in order). *selected_out
+ * (may be NULL) receives where a caller writes the n_selected compressed row
+ * numbers (for example ds4hip_indexer_topk_positions' positions_out). */
+int ds4hip_session_layer_rows(const ds4hip_session_state *s, int il, int n_selected,
+                              const int32_t **row_idx, long long *n_rows, int32_t **selected_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DS4HIP_SESSION_H */

@@ -26,6 +26,9 @@ SIGNATURES: dict[str, list] = {
     "ds4hip_flash_attn_decode_fp8": [
         _vp, _i, _ll, _vp, _ll, _vp, _ll, _vp, _vp, _vp, _vp, _i, _vp, _ll, _vp, _ll, _vp, _i,
         _i, _i, _i, _i, _vp, _sz, _i, _vp],
+    "ds4hip_flash_attn_prefill_fp8_workspace_size": [_i],
+    "ds4hip_flash_attn_prefill_fp8": [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _sz,
+                                      _vp],
     "ds4hip_tail_rope_yarn_f32": [_vp, _vp, _i, _i, _i, _i, _i, _vp],
     "ds4hip_tail_rope_yarn_inverse_f32": [_vp, _vp, _i, _i, _i, _i, _i, _vp],
     "ds4hip_mul_mv_f16_f32": [_vp, _vp, _vp, _i, _i, _vp],
@@ -60,6 +63,7 @@ SIGNATURES: dict[str, list] = {
 
 # entry points that return a value rather than a status
 RESTYPES = {"ds4hip_indexer_select_scratch_bytes": C.c_size_t,
+            "ds4hip_flash_attn_prefill_fp8_workspace_size": C.c_size_t,
             "ds4hip_session_state_arena_bytes": C.c_size_t}
 
 _lib = None

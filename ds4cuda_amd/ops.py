@@ -146,6 +146,29 @@ def flash_attn_decode_fp8(q, sinks, out, cache: Fp8KVCache, n_rows_per_prob, *, 
     return workspace
 
 
+def flash_attn_prefill_fp8(q, sinks, out, cache: Fp8KVCache, n_q, n_cached, row0=0,
+                           workspace=None, stream=None):
+    """Causal chunked prefill: q [n_q, 64, 512] bf16, out [n_q, 64, 512] fp32;
+    the sequence's rows start at cache row row0 and the chunk's own rows
+    (n_cached .. n_cached + n_q - 1) are already appended."""
+    _check(q, torch.bfloat16, n_q * N_HEAD * HEAD_DIM, "q")
+    _check(sinks, torch.float32, N_HEAD, "sinks")
+    _check(out, torch.float32, n_q * N_HEAD * HEAD_DIM, "out")
+    if row0 + n_cached + n_q > cache.n_rows:
+        raise Ds4HipError("prefill rows past the end of the cache", -22)
+    c = cache.codes[row0:]
+    s = cache.sexp[row0:]
+    t = cache.tail[row0:]
+    from ._lib import lib
+    need = lib().ds4hip_flash_attn_prefill_fp8_workspace_size(n_q)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    call("ds4hip_flash_attn_prefill_fp8", _ptr(q), _ptr(sinks), _ptr(out), _ptr(c), _ptr(s),
+         _ptr(t), n_q, n_cached, N_HEAD, HEAD_DIM, N_ROT, _ptr(workspace), workspace.numel(),
+         _stream(stream))
+    return workspace
+
+
 # ---- tail RoPE (cuda/rope.cuh:51, cuda/attn_out.cuh:52) ----------------------------------
 
 def launch_tail_rope_yarn_f32(x_in, x_out, n_heads, head_dim, n_rot, pos, il, stream=None):

@@ -112,6 +112,25 @@ int ds4hip_flash_attn_decode_fp8(const void *q, int q_is_f32, long long q_stride
                                  int n_rot, void *workspace, size_t workspace_bytes,
                                  int phases, void *stream);
 
+/* ---- chunked prefill ------------------------------------------------------------- */
+
+/* Causal chunked-prefill attention over the FP8 cache (additive: the
+ * reference runs prefill token by token through the decode launchers,
+ * cuda/forward_batch.cu:264-284; this is the batched form of the same math,
+ * cuda/flash_attn.cuh:9-26). Query t (0 <= t < n_q) of the chunk sits at
+ * position n_cached + t and attends cache rows [0, n_cached + t]; the chunk's
+ * own rows must already be in the cache (rows n_cached .. n_cached+n_q-1).
+ * q [n_q][64][512] bf16 bits, sinks [64] fp32, out [n_q][64][512] fp32;
+ * codes/sexp/tail point at the sequence's row 0. workspace holds
+ * ds4hip_flash_attn_prefill_fp8_workspace_size(n_q) bytes (one flag per query
+ * pair: pairs whose softmax range outgrows the fast kernel are redone by a
+ * second, rescaling kernel in the same call). */
+size_t ds4hip_flash_attn_prefill_fp8_workspace_size(int n_q);
+int ds4hip_flash_attn_prefill_fp8(const void *q, const float *sinks, float *out,
+                                  const uint8_t *codes, const int8_t *sexp, const uint16_t *tail,
+                                  int n_q, int n_cached, int n_head, int head_dim, int n_rot,
+                                  void *workspace, size_t workspace_bytes, void *stream);
+
 /* ---- tail RoPE YaRN --------------------------------------------------------------- */
 
 /* Replaces ds4cuda::launch_tail_rope_yarn_f32 (cuda/rope.cuh:51): rotates the

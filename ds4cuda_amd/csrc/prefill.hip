@@ -90,30 +90,26 @@ __device__ inline float xsum_16_32(float v) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-// Raw FP8 bytes of one tile held by one thread: row tid/8, 64-dim block
-// j = tid%8 (j < 7: 64 codes and the block exponent) and tail granule j.
+// Raw FP8 bytes of one tile held by one thread: row tid/8 of the tile, code
+// bytes [56j, 56j+56) (j = tid%8, seven 8-byte groups, each inside one
+// 64-dim block), the row's 8 scale exponents and tail granule j (f16 dims
+// 448+8j .. +8). Rows past the end of the sequence repeat its last row, so
+// every LDS row stays finite (those keys are masked).
 struct Raw {
-    uint4_t c[4];
+    uint2_t c[7];
+    uint2_t e;
     uint4_t t;
-    int e;
 };
 
 __device__ inline void load_raw(const PrefillArgs &A, int tile, int n_all, int tid, Raw &R) {
-    const int row = tile * kTile + (tid >> 3), j = tid & 7;
-    if (row < n_all) {
-        const uint8_t *cp = A.codes + (long long)row * kNope + 64 * j;
-        if (j < 7) {
+    int row = tile * kTile + (tid >> 3);
+    row = row < n_all ? row : n_all - 1;
+    const int j = tid & 7;
+    const uint8_t *cp = A.codes + (long long)row * kNope + 56 * j;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) R.c[i] = *reinterpret_cast<const uint4_t *>(cp + 16 * i);
-            R.e = A.sexp[(long long)row * 8 + j];
-        }
-        R.t = *reinterpret_cast<const uint4_t *>(A.tail + (long long)row * kRot + 8 * j);
-    } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) R.c[i] = uint4_t{0, 0, 0, 0};
-        R.t = uint4_t{0, 0, 0, 0};
-        R.e = 0;
-    }
+    for (int i = 0; i < 7; ++i) R.c[i] = *reinterpret_cast<const uint2_t *>(cp + 8 * i);
+    R.e = *reinterpret_cast<const uint2_t *>(A.sexp + (long long)row * 8);
+    R.t = *reinterpret_cast<const uint4_t *>(A.tail + (long long)row * kRot + 8 * j);
 }
 
 template <bool kHi>
@@ -125,47 +121,41 @@ __device__ inline half2_t cvt2(uint32_t w, float scale) {
 __device__ inline void store_tile(uint8_t *stage, int tid, const Raw &R) {
     const int row = tid >> 3, j = tid & 7;
     uint8_t *rp = stage + row * kRowB;
-    if (j < 7) {
-        const float sc = __uint_as_float((uint32_t)(R.e + 127) << 23);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            // 16 codes -> two 8-half chunks
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const uint32_t w0 = R.c[i][2 * h], w1 = R.c[i][2 * h + 1];
-                const half2_t a = cvt2<false>(w0, sc), b = cvt2<true>(w0, sc);
-                const half2_t c = cvt2<false>(w1, sc), d = cvt2<true>(w1, sc);
-                const half8_t v{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
-                *reinterpret_cast<half8_t *>(rp + kBlkB * j + 32 * i + 16 * h) = v;
-            }
-        }
+    for (int i = 0; i < 7; ++i) {
+        const int d = 56 * j + 8 * i;       // first dim of the group
+        const int b = d >> 6;                       // its 64-dim block
+        const uint32_t ew = b < 4 ? R.e[0] : R.e[1];
+        const int e = (int)(int8_t)(ew >> (8 * (b & 3)));
+        const float sc = __uint_as_float((uint32_t)(e + 127) << 23);
+        const half2_t h0 = cvt2<false>(R.c[i][0], sc), h1 = cvt2<true>(R.c[i][0], sc);
+        const half2_t h2 = cvt2<false>(R.c[i][1], sc), h3 = cvt2<true>(R.c[i][1], sc);
+        *reinterpret_cast<half8_t *>(rp + kBlkB * b + 2 * (d & 63)) =
+            half8_t{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
     }
     *reinterpret_cast<uint4_t *>(rp + kBlkB * 7 + 16 * j) = R.t;
 }
 
-// V^T fragments of the wave's 8 dim tiles: vb[dt] holds, for lane (n, g),
-// V[pi(4g+r)][128w+16dt+n] then V[pi(16+4g+r)][...], r = 0..3.
-__device__ inline void read_vt(uint32_t a0, uint32_t a1, half8_t *vb) {
-    uint2_t tb[16];
+// V^T fragments of 4 of the wave's dim tiles (DT0 .. DT0+3): vb[i] holds,
+// for lane (n, g), V[pi(4g+r)][128w+16(DT0+i)+n] then V[pi(16+4g+r)][...].
+template <int DT0>
+__device__ inline void read_vt4(uint32_t a0, uint32_t a1, half8_t *vb) {
+    static_assert(kBlkB == 144, "tr-read offsets assume 144-byte blocks");
+    constexpr int o0 = kBlkB * (DT0 / 4);
+    uint2_t tb[8];
     asm volatile(
-        "ds_read_b64_tr_b16 %0, %16\n\tds_read_b64_tr_b16 %1, %17\n\t"
-        "ds_read_b64_tr_b16 %2, %16 offset:32\n\tds_read_b64_tr_b16 %3, %17 offset:32\n\t"
-        "ds_read_b64_tr_b16 %4, %16 offset:64\n\tds_read_b64_tr_b16 %5, %17 offset:64\n\t"
-        "ds_read_b64_tr_b16 %6, %16 offset:96\n\tds_read_b64_tr_b16 %7, %17 offset:96\n\t"
-        "ds_read_b64_tr_b16 %8, %16 offset:144\n\tds_read_b64_tr_b16 %9, %17 offset:144\n\t"
-        "ds_read_b64_tr_b16 %10, %16 offset:176\n\tds_read_b64_tr_b16 %11, %17 offset:176\n\t"
-        "ds_read_b64_tr_b16 %12, %16 offset:208\n\tds_read_b64_tr_b16 %13, %17 offset:208\n\t"
-        "ds_read_b64_tr_b16 %14, %16 offset:240\n\tds_read_b64_tr_b16 %15, %17 offset:240\n\t"
+        "ds_read_b64_tr_b16 %0, %8 offset:%10\n\tds_read_b64_tr_b16 %1, %9 offset:%10\n\t"
+        "ds_read_b64_tr_b16 %2, %8 offset:%11\n\tds_read_b64_tr_b16 %3, %9 offset:%11\n\t"
+        "ds_read_b64_tr_b16 %4, %8 offset:%12\n\tds_read_b64_tr_b16 %5, %9 offset:%12\n\t"
+        "ds_read_b64_tr_b16 %6, %8 offset:%13\n\tds_read_b64_tr_b16 %7, %9 offset:%13\n\t"
         "s_waitcnt lgkmcnt(0)"
         : "=&v"(tb[0]), "=&v"(tb[1]), "=&v"(tb[2]), "=&v"(tb[3]), "=&v"(tb[4]), "=&v"(tb[5]),
-          "=&v"(tb[6]), "=&v"(tb[7]), "=&v"(tb[8]), "=&v"(tb[9]), "=&v"(tb[10]), "=&v"(tb[11]),
-          "=&v"(tb[12]), "=&v"(tb[13]), "=&v"(tb[14]), "=&v"(tb[15])
-        : "v"(a0), "v"(a1));
-    static_assert(kBlkB == 144, "tr-read offsets assume 144-byte blocks");
+          "=&v"(tb[6]), "=&v"(tb[7])
+        : "v"(a0), "v"(a1), "i"(o0), "i"(o0 + 32), "i"(o0 + 64), "i"(o0 + 96));
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
-        vb[dt] = __builtin_bit_cast(
-            half8_t, uint4_t{tb[2 * dt][0], tb[2 * dt][1], tb[2 * dt + 1][0], tb[2 * dt + 1][1]});
+    for (int i = 0; i < 4; ++i)
+        vb[i] = __builtin_bit_cast(
+            half8_t, uint4_t{tb[2 * i][0], tb[2 * i][1], tb[2 * i + 1][0], tb[2 * i + 1][1]});
 }
 
 __device__ inline void load_q(const PrefillArgs &A, int qi, int w, int n16, int g,
@@ -190,17 +180,37 @@ __device__ inline void load_q(const PrefillArgs &A, int qi, int w, int n16, int 
 
 // One P . V step: O[rt8][dt] += P_hi . V + P_lo . V for the 8 row tiles of
 // all waves, over this wave's 8 dim tiles (V^T read in two halves of 4).
+// The P fragments are read one row tile ahead of their MFMAs, and a
+// scheduling barrier closes every row tile so the compiler cannot hoist all
+// reads to the front (which would need 64 more VGPRs than exist).
 __device__ inline void pv_step(const half8_t (*phi)[64], const half8_t (*plo)[64], int lane,
                                uint32_t a0, uint32_t a1, float4_t (*o)[8]) {
-    half8_t vb[8];
-    read_vt(a0, a1, vb);
 #pragma unroll
-    for (int rt8 = 0; rt8 < 8; ++rt8) {
-        const half8_t ph = phi[rt8][lane], pl = plo[rt8][lane];
+    for (int half = 0; half < 2; ++half) {
+        half8_t vb[4];
+        if (half == 0)
+            read_vt4<0>(a0, a1, vb);
+        else
+            read_vt4<4>(a0, a1, vb);
+        half8_t ph[2], pl[2];
+        ph[0] = phi[0][lane];
+        pl[0] = plo[0][lane];
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) {
-            o[rt8][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, vb[dt], o[rt8][dt], 0, 0, 0);
-            o[rt8][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, vb[dt], o[rt8][dt], 0, 0, 0);
+        for (int rt8 = 0; rt8 < 8; ++rt8) {
+            if (rt8 < 7) {
+                ph[(rt8 + 1) & 1] = phi[rt8 + 1][lane];
+                pl[(rt8 + 1) & 1] = plo[rt8 + 1][lane];
+            }
+            // hi products of the 4 dim tiles, then lo: dependent MFMAs 4 apart
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                o[rt8][4 * half + i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    ph[rt8 & 1], vb[i], o[rt8][4 * half + i], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                o[rt8][4 * half + i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    pl[rt8 & 1], vb[i], o[rt8][4 * half + i], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 }
@@ -406,6 +416,201 @@ __global__ __launch_bounds__(256) void prefill_fp8_kernel(const PrefillArgs A) {
     }
 }
 
+// QK^T of one tile for the wave's 32 rows: acc[kt][rt] = S^T[keys pi(16kt+4g+r)][row 16rt+n16].
+__device__ inline void qk_tile(const uint8_t *st, const uint32_t *ka, const half8_t (*qf)[16],
+                               float4_t (*acc)[2]) {
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) acc[a][b] = float4_t{0, 0, 0, 0};
+    half8_t k0[2], k1[2];
+    k0[0] = *reinterpret_cast<const half8_t *>(st + ka[0]);
+    k1[0] = *reinterpret_cast<const half8_t *>(st + ka[1]);
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+        if (s < 15) {
+            const int off = kBlkB * ((s + 1) >> 1) + 64 * ((s + 1) & 1);
+            k0[(s + 1) & 1] = *reinterpret_cast<const half8_t *>(st + ka[0] + off);
+            k1[(s + 1) & 1] = *reinterpret_cast<const half8_t *>(st + ka[1] + off);
+        }
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+            acc[0][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0[s & 1], qf[rt][s], acc[0][rt], 0, 0, 0);
+            acc[1][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1[s & 1], qf[rt][s], acc[1][rt], 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// Softmax of one tile with the reference max fixed (set on the first tile):
+// writes P hi/lo for the wave's two row tiles and accumulates l. A score more
+// than 2^kLazy above the reference marks the wave failed.
+template <bool kFirst>
+__device__ inline void softmax_fixed(const float4_t (*acc)[2], float kq_log2, int key0, int qpos,
+                                     int g, float *m_use, float *l_part, bool &failed,
+                                     half8_t *hi_out, half8_t *lo_out) {
+    const bool edge = key0 + kTile - 1 > qpos;
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+        float s2[2][4];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float v = acc[kt][rt][r] * kq_log2;
+                s2[kt][r] = (edge && key0 + pi_key(16 * kt + 4 * g + r) > qpos) ? -INFINITY : v;
+            }
+        if (kFirst) {
+            float mx = fmaxf(fmaxf(fmaxf(s2[0][0], s2[0][1]), fmaxf(s2[0][2], s2[0][3])),
+                             fmaxf(fmaxf(s2[1][0], s2[1][1]), fmaxf(s2[1][2], s2[1][3])));
+            m_use[rt] = xmax_16_32(mx);
+        }
+        const float m = m_use[rt];
+        half8_t hi, lo;
+        float lsum = 0.0f;
+        bool big = false;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float x = s2[kt][r] - m;
+                big |= x > kLazy;
+                const float p = s2[kt][r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(x);
+                lsum += p;
+                const half_t h = (half_t)p;
+                hi[4 * kt + r] = h;
+                lo[4 * kt + r] = (half_t)(p - (float)h);
+            }
+        l_part[rt] += lsum;
+        failed |= big;
+        hi_out[rt] = hi;
+        lo_out[rt] = lo;
+    }
+}
+
+// The fast kernel: software-pipelined over tiles with one barrier per tile.
+// Iteration t: [barrier] S(t) = K(t) Q^T | dequantize tile t+1 (fetched one
+// iteration earlier), fetch tile t+2 | softmax(t) | O += P(t-1) V(t-1). Three f16 stages (t-1 for V, t for K,
+// t+1 being written) and two P buffers make every LDS hazard one barrier apart.
+__global__ __launch_bounds__(256) void prefill_fast_kernel(const PrefillArgs A) {
+    __shared__ __attribute__((aligned(16))) uint8_t stages[3][kStageB];
+    __shared__ __attribute__((aligned(16))) half8_t pb[2][2][8][64];   // [buf][hi,lo][row tile][lane]
+    __shared__ __attribute__((aligned(16))) int flag_s[4];
+    __shared__ __attribute__((aligned(16))) float fin_s[2][kRows];
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int n16 = lane & 15, g = lane >> 4;
+    const int pair = (int)gridDim.x - 1 - (int)blockIdx.x;
+    const int q0 = 2 * pair;
+    const int qi = q0 + (w >> 1);
+    const bool q_ok = qi < A.n_q;
+    const int qpos = q_ok ? A.n_cached + qi : -1;
+    const int n_all = A.n_cached + (q0 + 2 < A.n_q ? q0 + 2 : A.n_q);
+    const int n_tiles = (n_all + kTile - 1) / kTile;
+
+    half8_t qf[2][16];
+    load_q(A, q_ok ? qi : 0, w, n16, g, qf);
+    float4_t o[8][8];
+#pragma unroll
+    for (int a = 0; a < 8; ++a)
+#pragma unroll
+        for (int b = 0; b < 8; ++b) o[a][b] = float4_t{0, 0, 0, 0};
+    float m_use[2], l_part[2] = {0.f, 0.f};
+    bool failed = false;
+
+    uint32_t ka[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) ka[kt] = pi_key(16 * kt + n16) * kRowB + 16 * g;
+    uint32_t va[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+        va[h] = pi_key(16 * h + 4 * g + (n16 >> 2)) * kRowB + kBlkB * 2 * w + 8 * (n16 & 3);
+
+    Raw R;
+    load_raw(A, 0, n_all, tid, R);
+    store_tile(stages[0], tid, R);
+    load_raw(A, 1, n_all, tid, R);
+    lds_barrier();
+    {
+        float4_t acc[2][2];
+        qk_tile(stages[0], ka, qf, acc);
+        store_tile(stages[1], tid, R);
+        load_raw(A, 2, n_all, tid, R);
+        half8_t hi[2], lo[2];
+        softmax_fixed<true>(acc, A.kq_log2, 0, qpos, g, m_use, l_part, failed, hi, lo);
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+            pb[0][0][2 * w + rt][lane] = hi[rt];
+            pb[0][1][2 * w + rt][lane] = lo[rt];
+        }
+    }
+    int sp = 0, sc = 1, sn = 2;   // stages of tiles t-1, t, t+1
+    for (int t = 1; t < n_tiles; ++t) {
+        lds_barrier();
+        float4_t acc[2][2];
+        qk_tile(stages[sc], ka, qf, acc);
+        // tile t+1 (fetched one iteration ago) is dequantized; t+2 is fetched
+        store_tile(stages[sn], tid, R);
+        load_raw(A, t + 2, n_all, tid, R);
+        half8_t hi[2], lo[2];
+        softmax_fixed<false>(acc, A.kq_log2, t * kTile, qpos, g, m_use, l_part, failed, hi, lo);
+        const int pbuf = (t - 1) & 1;
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+            pb[pbuf ^ 1][0][2 * w + rt][lane] = hi[rt];
+            pb[pbuf ^ 1][1][2 * w + rt][lane] = lo[rt];
+        }
+        pv_step(pb[pbuf][0], pb[pbuf][1], lane, lds_addr(stages[sp]) + va[0],
+                lds_addr(stages[sp]) + va[1], o);
+        const int tmp = sp;
+        sp = sc;
+        sc = sn;
+        sn = tmp;
+    }
+    lds_barrier();
+    {
+        const int pbuf = (n_tiles - 1) & 1;
+        pv_step(pb[pbuf][0], pb[pbuf][1], lane, lds_addr(stages[sp]) + va[0],
+                lds_addr(stages[sp]) + va[1], o);
+    }
+
+    // ---- finish ----
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+        const float l = xsum_16_32(l_part[rt]);
+        if (g == 0) {
+            fin_s[0][32 * w + 16 * rt + n16] = m_use[rt];
+            fin_s[1][32 * w + 16 * rt + n16] = l;
+        }
+    }
+    const bool wf = __any(failed);
+    if (lane == 0) flag_s[w] = wf ? 1 : 0;
+    lds_barrier();
+    const int4 fl = *reinterpret_cast<const int4 *>(flag_s);
+    if (fl.x | fl.y | fl.z | fl.w) {
+        if (tid == 0) A.fail[pair] = 1;
+        return;
+    }
+#pragma unroll
+    for (int rt8 = 0; rt8 < 8; ++rt8) {
+        const int qq = q0 + (rt8 >> 2);
+        if (qq >= A.n_q) continue;
+        float inv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = 16 * rt8 + 4 * g + r;
+            const float m = fin_s[0][row], l = fin_s[1][row];
+            const float sk = A.sinks[row & 63] * kLog2e;
+            inv[r] = m == -INFINITY ? 0.0f : 1.0f / (l + __builtin_amdgcn_exp2f(sk - m));
+        }
+        float *dst = A.out + ((long long)qq * kH + ((16 * rt8) & 63) + 4 * g) * kD + 128 * w + n16;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) dst[r * kD + 16 * dt] = o[rt8][dt][r] * inv[r];
+    }
+}
+
 __global__ void zero_i32_kernel(int *p, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) p[i] = 0;
@@ -443,7 +648,7 @@ extern "C" int ds4hip_flash_attn_prefill_fp8(const void *q, const float *sinks, 
     const hipStream_t st = (hipStream_t)stream;
     hipLaunchKernelGGL(zero_i32_kernel, dim3((n_pairs + 255) / 256), dim3(256), 0, st, A.fail,
                        n_pairs);
-    hipLaunchKernelGGL(prefill_fp8_kernel<false>, dim3(n_pairs), dim3(256), 0, st, A);
+    hipLaunchKernelGGL(prefill_fast_kernel, dim3(n_pairs), dim3(256), 0, st, A);
     hipLaunchKernelGGL(prefill_fp8_kernel<true>, dim3(n_pairs), dim3(256), 0, st, A);
     return ds4hip_set_last_error(hip_status(hipGetLastError()));
 }

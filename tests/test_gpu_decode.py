@@ -129,3 +129,29 @@ def test_mixed_f32_launcher(gpu, n_raw, n_comp):
         ref = O.attn_decode_mixed_f32(Q, raw if n_raw else None, comp if n_comp else None,
                                       mask if use_mask else None, sinks)
         check(out.cpu().numpy(), ref)
+
+
+def test_fp8_cfg2_scale_long_chunks(gpu):
+    # the batch-1 decode shape (43 layers x 32768 rows): each workgroup walks
+    # ~170 tiles, so the softmax reference max is set long before the chunk's
+    # largest score; two layers are checked against the oracle
+    n_layer, n_kv = 43, 32768
+    x = torch.randn(n_layer * n_kv, 512, device=gpu, generator=torch.Generator(gpu).manual_seed(5))
+    pick = torch.rand(n_layer * n_kv, device=gpu, generator=torch.Generator(gpu).manual_seed(6)) < 0.01
+    x[pick] *= 8
+    cache = ops.Fp8KVCache.empty(n_layer * n_kv, device=gpu)
+    cache.append(x)
+    bits, qf = q_bf16(41, n_layer)
+    sinks = sinks_for(42, n_layer)
+    out = torch.zeros((n_layer, 64, 512), dtype=torch.float32, device=gpu)
+    q = torch.from_numpy(bits.view(np.int16)).to(gpu).view(torch.bfloat16)
+    ops.flash_attn_decode_fp8(q, torch.from_numpy(sinks).to(gpu), out, cache, [n_kv] * n_layer,
+                              row_base_stride=n_kv)
+    torch.cuda.synchronize()
+    codes = cache.codes.cpu().numpy()
+    sexp = cache.sexp.cpu().numpy()
+    tail = cache.tail.cpu().numpy().view(np.uint16)
+    for p in (0, 42):
+        rows = p * n_kv + np.arange(n_kv)
+        ref = O.attn_decode_fp8(qf[p], codes, sexp, tail, rows, sinks[p], n_threads=8)
+        check(out[p].cpu().numpy(), ref)

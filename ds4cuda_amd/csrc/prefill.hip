@@ -21,11 +21,11 @@
 //     ds_read_b64_tr_b16.
 // The FP8 tile (32 rows x 584 B) is loaded into registers one tile ahead,
 // dequantized once per workgroup (v_cvt_scalef32_pk_f16_fp8) and written to a
-// double-buffered f16 LDS tile. Row layout in LDS: eight 64-dim blocks of
-// 128 B, each followed by 16 B of padding, plus 16 B per row (1168 B per
-// row), so 16 lanes reading the same block column of 16 rows, 8 lanes writing
-// the eight blocks of one row, and the transposing reads of 4 rows all fall in
-// distinct banks. Inside a tile the keys are taken in the order pi (below):
+// double-buffered f16 LDS tile. Rows are stored linearly with a 16-byte pad
+// (1040 B per row): ds_read/write_b128 resolve banks per 8 lanes over 256 B,
+// so the 8 threads storing one row (16-byte chunks 7j + i), 8 lanes reading
+// one column chunk of 8 rows, and the transposing reads of 4 rows x 32 B all
+// hit distinct banks. Inside a tile the keys are taken in the order pi (below):
 // the S^T rows of an MFMA, the P fragment and the V^T fragment then agree
 // without any register shuffling.
 
@@ -42,8 +42,7 @@ constexpr int kD = 512;
 constexpr int kRot = 64;
 constexpr int kNope = kD - kRot;
 constexpr int kTile = 32;            // keys per tile
-constexpr int kBlkB = 144;           // 128 B of a 64-dim f16 block + 16 B pad
-constexpr int kRowB = 8 * kBlkB + 16;
+constexpr int kRowB = 2 * kD + 16;   // one f16 row + 16 B
 constexpr int kStageB = kTile * kRowB;
 constexpr int kRows = 128;           // query rows (2 queries x 64 heads) per workgroup
 constexpr float kLog2e = 1.4426950408889634f;
@@ -130,18 +129,17 @@ __device__ inline void store_tile(uint8_t *stage, int tid, const Raw &R) {
         const float sc = __uint_as_float((uint32_t)(e + 127) << 23);
         const half2_t h0 = cvt2<false>(R.c[i][0], sc), h1 = cvt2<true>(R.c[i][0], sc);
         const half2_t h2 = cvt2<false>(R.c[i][1], sc), h3 = cvt2<true>(R.c[i][1], sc);
-        *reinterpret_cast<half8_t *>(rp + kBlkB * b + 2 * (d & 63)) =
+        *reinterpret_cast<half8_t *>(rp + 2 * d) =
             half8_t{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
     }
-    *reinterpret_cast<uint4_t *>(rp + kBlkB * 7 + 16 * j) = R.t;
+    *reinterpret_cast<uint4_t *>(rp + 2 * kNope + 16 * j) = R.t;
 }
 
 // V^T fragments of 4 of the wave's dim tiles (DT0 .. DT0+3): vb[i] holds,
 // for lane (n, g), V[pi(4g+r)][128w+16(DT0+i)+n] then V[pi(16+4g+r)][...].
 template <int DT0>
 __device__ inline void read_vt4(uint32_t a0, uint32_t a1, half8_t *vb) {
-    static_assert(kBlkB == 144, "tr-read offsets assume 144-byte blocks");
-    constexpr int o0 = kBlkB * (DT0 / 4);
+    constexpr int o0 = 32 * DT0;
     uint2_t tb[8];
     asm volatile(
         "ds_read_b64_tr_b16 %0, %8 offset:%10\n\tds_read_b64_tr_b16 %1, %9 offset:%10\n\t"
@@ -262,7 +260,7 @@ __global__ __launch_bounds__(256) void prefill_fp8_kernel(const PrefillArgs A) {
     uint32_t va[2];           // V^T supplier rows (half h), dims 128w + 4(n16&3)
 #pragma unroll
     for (int h = 0; h < 2; ++h)
-        va[h] = pi_key(16 * h + 4 * g + (n16 >> 2)) * kRowB + kBlkB * 2 * w + 8 * (n16 & 3);
+        va[h] = pi_key(16 * h + 4 * g + (n16 >> 2)) * kRowB + 256 * w + 8 * (n16 & 3);
 
     Raw R;
     load_raw(A, 0, n_all, tid, R);
@@ -287,7 +285,7 @@ __global__ __launch_bounds__(256) void prefill_fp8_kernel(const PrefillArgs A) {
                 for (int b = 0; b < 2; ++b) acc[a][b] = float4_t{0, 0, 0, 0};
 #pragma unroll
             for (int s = 0; s < 16; ++s) {
-                const int off = kBlkB * (s >> 1) + 64 * (s & 1);
+                const int off = 64 * s;
                 const half8_t k0 = *reinterpret_cast<const half8_t *>(st + ka[0] + off);
                 const half8_t k1 = *reinterpret_cast<const half8_t *>(st + ka[1] + off);
 #pragma unroll
@@ -429,7 +427,7 @@ __device__ inline void qk_tile(const uint8_t *st, const uint32_t *ka, const half
 #pragma unroll
     for (int s = 0; s < 16; ++s) {
         if (s < 15) {
-            const int off = kBlkB * ((s + 1) >> 1) + 64 * ((s + 1) & 1);
+            const int off = 64 * (s + 1);
             k0[(s + 1) & 1] = *reinterpret_cast<const half8_t *>(st + ka[0] + off);
             k1[(s + 1) & 1] = *reinterpret_cast<const half8_t *>(st + ka[1] + off);
         }
@@ -524,7 +522,7 @@ __global__ __launch_bounds__(256) void prefill_fast_kernel(const PrefillArgs A) 
     uint32_t va[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h)
-        va[h] = pi_key(16 * h + 4 * g + (n16 >> 2)) * kRowB + kBlkB * 2 * w + 8 * (n16 & 3);
+        va[h] = pi_key(16 * h + 4 * g + (n16 >> 2)) * kRowB + 256 * w + 8 * (n16 & 3);
 
     Raw R;
     load_raw(A, 0, n_all, tid, R);

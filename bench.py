@@ -31,6 +31,7 @@ def log(*a):
 N_LAYERS, N_KV, N_HEAD, HEAD_DIM = 43, 32768, 64, 512
 ROW_BYTES = 584                                   # FP8 cache row: 448 codes + 8 exps + 128 tail
 HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0                          # dense f16 / bf16
 
 
 def bytes_per_layer():
@@ -66,12 +67,102 @@ def cpu_baseline(seed=0):
                       f"({b / t1 / 1e9:.3f} GB/s)"}
 
 
+def time_ms(fn, steps, warmup, stream):
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def bench_prefill(dev, stream, steps):
+    """2048 new queries over 8192 cached rows + causal
+    self, 64 heads, head_dim 512, bf16 Q, FP8 KV."""
+    import torch
+    from ds4cuda_amd import ops
+    n_cached, n_q = 8192, 2048
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    cache = ops.Fp8KVCache.empty(n_cached + n_q, device=dev)
+    cache.append(torch.randn((n_cached + n_q, HEAD_DIM), generator=g, device=dev))
+    q = torch.randn((n_q, N_HEAD, HEAD_DIM), generator=g, device=dev).to(torch.bfloat16)
+    sinks = torch.randn((N_HEAD,), generator=g, device=dev)
+    out = torch.empty((n_q, N_HEAD, HEAD_DIM), device=dev)
+    ws = ops.flash_attn_prefill_fp8(q, sinks, out, cache, n_q, n_cached, stream=stream)
+    ms = time_ms(lambda: ops.flash_attn_prefill_fp8(q, sinks, out, cache, n_q, n_cached,
+                                                    workspace=ws, stream=stream),
+                 steps, 2, stream)
+    causal = 4 * N_HEAD * HEAD_DIM * sum(n_cached + i + 1 for i in range(n_q))
+    full = 4 * N_HEAD * HEAD_DIM * n_q * (n_cached + n_q)
+    tf = causal / (ms * 1e-3) / 1e12
+    return {"workload": "chunked prefill: 2048 queries over 8192 cached + causal self, 64 heads, "
+                        "head_dim 512, bf16 Q, FP8 KV (BASELINE configs[3])",
+            "ms": round(ms, 4), "tflops_causal": round(tf, 1),
+            "tflops_nomask_credit": round(full / (ms * 1e-3) / 1e12, 1),
+            "flops_causal": causal, "peak_tflops": MFMA_PEAK_TFLOPS,
+            "frac": round(tf / MFMA_PEAK_TFLOPS, 4)}
+
+
+def bench_sparse(dev, stream, steps):
+    """indexer over 131072 bf16 index keys (64 heads x
+    128), top-2048 incl. the last 128, then decode over the 2048 gathered FP8
+    rows of a 131072-row cache."""
+    import torch
+    from ds4cuda_amd import ops
+    n, top_k, recent = 131072, 2048, 128
+    g = torch.Generator(device=dev)
+    g.manual_seed(4)
+    keys = torch.randn((n, 128), generator=g, device=dev).to(torch.bfloat16)
+    qi = torch.randn((N_HEAD, 128), generator=g, device=dev).to(torch.bfloat16).float()
+    w = torch.randn((N_HEAD,), generator=g, device=dev) / float(np.sqrt(128 * N_HEAD))
+    cache = ops.Fp8KVCache.empty(n, device=dev)
+    for r0 in range(0, n, 32768):
+        cache.append(torch.randn((32768, HEAD_DIM), generator=g, device=dev), row0=r0)
+    q = torch.randn((1, N_HEAD, HEAD_DIM), generator=g, device=dev).to(torch.bfloat16)
+    sinks = torch.randn((1, N_HEAD), generator=g, device=dev)
+    out = torch.empty((1, N_HEAD, HEAD_DIM), device=dev)
+    from ds4cuda_amd._lib import lib
+    scores = torch.empty(n, device=dev)
+    select = torch.empty(lib().ds4hip_indexer_select_scratch_bytes(n), dtype=torch.uint8,
+                         device=dev)
+    pos = torch.empty((1, top_k), dtype=torch.int32, device=dev)
+    ws = torch.empty(ops.decode_fp8_workspace_bytes([top_k]), dtype=torch.uint8, device=dev)
+
+    def step():
+        ops.indexer_topk_positions(qi, w, keys, top_k, recent, scores=scores, select=select,
+                                   positions=pos[0], stream=stream)
+        ops.flash_attn_decode_fp8(q, sinks, out, cache, [top_k], row_idx=pos, workspace=ws,
+                                  stream=stream)
+
+    def sel_only():
+        ops.indexer_topk_positions(qi, w, keys, top_k, recent, scores=scores, select=select,
+                                   positions=pos[0], stream=stream)
+
+    ms = time_ms(step, steps, 3, stream)
+    ms_idx = time_ms(sel_only, steps, 3, stream)
+    b = n * 128 * 2 + N_HEAD * 128 * 4 + N_HEAD * 4 + 2 * n * 4 + top_k * (ROW_BYTES + 4) \
+        + N_HEAD * HEAD_DIM * 6 + N_HEAD * 4
+    return {"workload": "sparse decode: indexer over 131072 bf16 keys (64 heads x 128), top-2048 "
+                        "incl. last 128, decode over the gathered FP8 rows (BASELINE configs[2])",
+            "us": round(ms * 1e3, 2), "us_indexer": round(ms_idx * 1e3, 2),
+            "bytes": b, "gbs": round(b / (ms * 1e-3) / 1e9, 1),
+            "frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="skip the prefill / sparse-decode / batched-block figures")
     args = ap.parse_args()
     if args.gpus != 1:
         log("bench.py measures the single-GPU path only: the attention path has no "
@@ -157,6 +248,10 @@ def main():
                      "kernel": "decode_fp8_kernel<bf16 q>",
                      "kernel_ms": round(k_ms, 4), "bytes_per_launch": step_bytes},
     }
+    if not args.no_secondary:
+        log("secondary configs: chunked prefill, sparse decode")
+        res["secondary"] = {"prefill": bench_prefill(dev, stream, max(3, args.steps // 10)),
+                            "sparse_decode": bench_sparse(dev, stream, args.steps)}
     if not args.no_cpu_baseline:
         log("timing the CPU baseline (oracle) on one layer")
         res["cpu_baseline"] = cpu_baseline()

@@ -48,6 +48,7 @@ constexpr int kNope = kD - kRot; // 448 FP8-coded dims, 7 scale blocks
 constexpr int kTile = 32;        // rows per tile
 constexpr int kVtStride = 40;    // halves per V^T line (32 rows + 8 pad)
 constexpr int kMaxProb = 128;
+constexpr int kMinChunk = 4 * kTile;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kFp8WgPerCu = 1;   // the FP8 kernel's LDS ring allows one workgroup per CU
 
@@ -826,42 +827,63 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(const DecodeArgs A) {
 }
 
 // One block per (problem, head): combine the partials with the sink.
+// One workgroup per (problem, head). The partial slots of the problem are
+// spread over the 4 waves (slot i -> wave i % 4), so their loads are
+// independent; each lane covers 8 of the 512 dims. The max over the slots
+// (and the sink) is taken first, then every wave accumulates its slots
+// rescaled to that max, and the 4 wave sums are added in LDS in wave order.
 __global__ __launch_bounds__(256) void decode_merge_kernel(const DecodeArgs A) {
     __shared__ long long s_start[kMaxProb + 1];
+    __shared__ float red_m[4];
+    __shared__ float red_l[4];
+    __shared__ float4_t red_o[4][128];
     stage_start(A, s_start);
-    if (threadIdx.x >= 128) return;
     const int p = blockIdx.x;
     const int h = blockIdx.y;
-    const int d = threadIdx.x * 4;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const float sink = A.sinks[(long long)p * A.sinks_stride + h] * kLog2e;
-    float mx = sink;
     const long long b0 = s_start[p], b1 = s_start[p + 1];
-    long long w0 = 0, w1 = -1;
+    long long s0 = 0, n_slot = 0;
     if (b1 > b0) {
-        w0 = b0 / A.chunk;
-        w1 = (b1 - 1) / A.chunk;
+        s0 = (b0 / A.chunk) * A.s_max;
+        n_slot = ((b1 - 1) / A.chunk) * A.s_max + A.s_max - s0;
     }
-    for (long long w = w0; w <= w1; ++w)
-        for (int s = 0; s < A.s_max; ++s) {
-            const long long slot = w * A.s_max + s;
-            if (A.ws_prob[slot] == p) mx = fmaxf(mx, A.ws_ml[slot * 2 * kH + h]);
-        }
-    float denom = __builtin_amdgcn_exp2f(sink - mx);
-    float4_t acc = float4_t{0, 0, 0, 0};
-    for (long long w = w0; w <= w1; ++w)
-        for (int s = 0; s < A.s_max; ++s) {
-            const long long slot = w * A.s_max + s;
-            if (A.ws_prob[slot] != p) continue;
-            const float m = A.ws_ml[slot * 2 * kH + h];
-            if (m == -INFINITY) continue;
-            const float sc = __builtin_amdgcn_exp2f(m - mx);
-            denom += A.ws_ml[slot * 2 * kH + kH + h] * sc;
-            const float4_t v =
-                *reinterpret_cast<const float4_t *>(A.ws_o + slot * (kH * kD) + h * kD + d);
-            acc += v * sc;
-        }
-    const float inv = 1.0f / denom;
-    *reinterpret_cast<float4_t *>(A.out + (long long)p * A.out_stride + h * kD + d) = acc * inv;
+    // max over this problem's partials
+    float mx = -INFINITY;
+    for (long long i = tid; i < n_slot; i += 256) {
+        const long long slot = s0 + i;
+        if (A.ws_prob[slot] == p) mx = fmaxf(mx, A.ws_ml[slot * 2 * kH + h]);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if (lane == 0) red_m[wv] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3])), sink);
+    // weighted sums, slots strided over the waves
+    float4_t acc0 = float4_t{0, 0, 0, 0}, acc1 = acc0;
+    float den = 0.0f;
+    for (long long i = wv; i < n_slot; i += 4) {
+        const long long slot = s0 + i;
+        if (A.ws_prob[slot] != p) continue;
+        const float m = A.ws_ml[slot * 2 * kH + h];
+        if (m == -INFINITY) continue;
+        const float sc = __builtin_amdgcn_exp2f(m - mx);
+        den += A.ws_ml[slot * 2 * kH + kH + h] * sc;
+        const float4_t *src = reinterpret_cast<const float4_t *>(A.ws_o + slot * (kH * kD) + h * kD) + lane;
+        acc0 += src[0] * sc;
+        acc1 += src[64] * sc;
+    }
+    red_o[wv][lane] = acc0;
+    red_o[wv][64 + lane] = acc1;
+    if (lane == 0) red_l[wv] = den;
+    __syncthreads();
+    if (tid < 128) {
+        const float denom = __builtin_amdgcn_exp2f(sink - mx) + ((red_l[0] + red_l[1]) + red_l[2]) + red_l[3];
+        const float4_t o = ((red_o[0][tid] + red_o[1][tid]) + red_o[2][tid]) + red_o[3][tid];
+        // lane t of the first 64 holds dims 4t..4t+3, the next 64 dims 256+4t..
+        *reinterpret_cast<float4_t *>(A.out + (long long)p * A.out_stride + h * kD + 4 * tid) =
+            o * (1.0f / denom);
+    }
 }
 
 // ---- host-side planning -----------------------------------------------------------
@@ -888,15 +910,17 @@ struct Plan {
 
 size_t slot_bytes() { return (size_t)kH * kD * 4 + 2 * kH * 4 + 4; }
 
-// Chunk the concatenated rows so that ~2 workgroups run per CU, each chunk a
-// whole number of tiles; s_max bounds the problems one chunk can touch.
+// Chunk the concatenated rows so that about wg_per_cu workgroups run per CU,
+// each chunk a whole number of tiles and at least kMinChunk rows (small
+// steps get fewer, longer workgroups and fewer partials to merge); s_max
+// bounds the problems one chunk can touch.
 Plan make_plan(const long long *start, int n_prob, int wg_per_cu) {
     Plan pl;
     const long long total = start[n_prob];
     const long long target = (long long)num_cus() * wg_per_cu;
     long long chunk = total > 0 ? (total + target - 1) / target : kTile;
     chunk = ((chunk + kTile - 1) / kTile) * kTile;
-    if (chunk < kTile) chunk = kTile;
+    if (chunk < kMinChunk) chunk = kMinChunk;
     pl.chunk = (int)chunk;
     pl.n_wg = total > 0 ? (int)((total + chunk - 1) / chunk) : 0;
     int smax = 1;

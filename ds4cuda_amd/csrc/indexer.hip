@@ -41,8 +41,79 @@ __device__ inline float key_elem(const void *keys, size_t i) {
     return bf16_to_f32(static_cast<const uint16_t *>(keys)[i]);
 }
 
-// 256 threads, one key per thread. hist (optional): top-11-bit histogram of
-// the ordered keys of positions [0, n_cand).
+// 256 threads, one key per thread. The query and the weights are read with
+// uniform addresses, so they come through the scalar cache into SGPRs and
+// every multiply-add is one VALU instruction with no memory operand.
+// hist (optional): top-11-bit histogram of the ordered keys of positions
+// [0, n_cand).
+template <int kKind, int kDim>
+__device__ inline float score_one(const float *__restrict__ q, const float *__restrict__ w,
+                                  const void *__restrict__ keys, int c, int n_head) {
+    float k[kDim];
+    if (kKind != 0 && kDim % 8 == 0) {
+        const uint4_t *src = reinterpret_cast<const uint4_t *>(
+            static_cast<const uint16_t *>(keys) + (size_t)c * kDim);
+#pragma unroll
+        for (int v = 0; v < kDim / 8; ++v) {
+            const uint4_t u = src[v];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint16_t h = (uint16_t)((u[e >> 1] >> (16 * (e & 1))) & 0xFFFF);
+                k[8 * v + e] = kKind == 1 ? f16_bits_to_f32(h) : bf16_to_f32(h);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int d = 0; d < kDim; ++d) k[d] = key_elem<kKind>(keys, (size_t)c * kDim + d);
+    }
+    // two heads at a time: their dot chains are independent, so the two
+    // interleaved chains keep the VALU busy; the chains and the head sum keep
+    // the canonical order
+    float s = 0.0f;
+    int h = 0;
+    for (; h + 1 < n_head; h += 2) {
+        const float *q0 = q + h * kDim;
+        const float *q1 = q0 + kDim;
+        float d0 = 0.0f, d1 = 0.0f;
+#pragma unroll
+        for (int d = 0; d < kDim; ++d) {
+            d0 = fmaf(q0[d], k[d], d0);
+            d1 = fmaf(q1[d], k[d], d1);
+        }
+        s = fmaf(w[h], d0 > 0.0f ? d0 : 0.0f, s);
+        s = fmaf(w[h + 1], d1 > 0.0f ? d1 : 0.0f, s);
+    }
+    if (h < n_head) {
+        const float *qh = q + h * kDim;
+        float dot = 0.0f;
+#pragma unroll
+        for (int d = 0; d < kDim; ++d) dot = fmaf(qh[d], k[d], dot);
+        s = fmaf(w[h], dot > 0.0f ? dot : 0.0f, s);
+    }
+    return s;
+}
+
+// Any head_dim <= 128: the key row is zero-padded to 128 in registers and
+// the query is read with the same padding from LDS.
+template <int kKind>
+__device__ inline float score_any(const float *qs, const float *ws, const void *keys, int c,
+                                  int n_head, int head_dim) {
+    float k[kMaxDim];
+#pragma unroll
+    for (int d = 0; d < kMaxDim; ++d)
+        k[d] = d < head_dim ? key_elem<kKind>(keys, (size_t)c * head_dim + d) : 0.0f;
+    float s = 0.0f;
+    for (int h = 0; h < n_head; ++h) {
+        const float *qh = qs + h * head_dim;
+        float dot = 0.0f;
+#pragma unroll
+        for (int d = 0; d < kMaxDim; ++d)
+            if (d < head_dim) dot = fmaf(qh[d], k[d], dot);
+        s = fmaf(ws[h], dot > 0.0f ? dot : 0.0f, s);
+    }
+    return s;
+}
+
 template <int kKind>
 __global__ __launch_bounds__(256) void score_kernel(const float *__restrict__ q,
                                                     const float *__restrict__ w,
@@ -50,48 +121,25 @@ __global__ __launch_bounds__(256) void score_kernel(const float *__restrict__ q,
                                                     int n_head, int head_dim,
                                                     float *__restrict__ scores,
                                                     unsigned *__restrict__ hist, int n_cand) {
-    __shared__ float qs[kMaxHeads * kMaxDim];
-    __shared__ float ws[kMaxHeads];
     __shared__ unsigned lh[kBins];
-    for (int i = threadIdx.x; i < n_head * head_dim; i += 256) qs[i] = q[i];
-    for (int i = threadIdx.x; i < n_head; i += 256) ws[i] = w[i];
     if (hist)
         for (int i = threadIdx.x; i < kBins; i += 256) lh[i] = 0;
-    __syncthreads();
     const int c = blockIdx.x * 256 + threadIdx.x;
-    if (c < n_comp) {
-        float k[kMaxDim];
-        if (head_dim == kMaxDim && kKind != 0) {
-            // 16-bit keys of the common 128-dim shape: 16 x 16-byte loads
-            const uint4_t *src = reinterpret_cast<const uint4_t *>(
-                static_cast<const uint16_t *>(keys) + (size_t)c * kMaxDim);
-#pragma unroll
-            for (int v = 0; v < kMaxDim / 8; ++v) {
-                const uint4_t u = src[v];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const uint16_t h = (uint16_t)((u[e >> 1] >> (16 * (e & 1))) & 0xFFFF);
-                    k[8 * v + e] = kKind == 1 ? f16_bits_to_f32(h) : bf16_to_f32(h);
-                }
-            }
-        } else {
-#pragma unroll
-            for (int d = 0; d < kMaxDim; ++d)
-                k[d] = d < head_dim ? key_elem<kKind>(keys, (size_t)c * head_dim + d) : 0.0f;
-        }
-        float s = 0.0f;
-        for (int h = 0; h < n_head; ++h) {
-            const float *qh = qs + h * head_dim;
-            float dot = 0.0f;
-#pragma unroll
-            for (int d = 0; d < kMaxDim; ++d)
-                if (d < head_dim) dot = fmaf(qh[d], k[d], dot);
-            s = fmaf(ws[h], dot > 0.0f ? dot : 0.0f, s);
-        }
-        scores[c] = s;
-        if (hist && c < n_cand) atomicAdd(&lh[ord_key(s) >> 21], 1u);
+    float s = 0.0f;
+    if (head_dim == kMaxDim) {
+        if (c < n_comp) s = score_one<kKind, kMaxDim>(q, w, keys, c, n_head);
+    } else {
+        __shared__ float qs[kMaxHeads * kMaxDim];
+        __shared__ float ws[kMaxHeads];
+        for (int i = threadIdx.x; i < n_head * head_dim; i += 256) qs[i] = q[i];
+        for (int i = threadIdx.x; i < n_head; i += 256) ws[i] = w[i];
+        __syncthreads();
+        if (c < n_comp) s = score_any<kKind>(qs, ws, keys, c, n_head, head_dim);
     }
+    if (c < n_comp) scores[c] = s;
     if (hist) {
+        __syncthreads();
+        if (c < n_cand) atomicAdd(&lh[ord_key(s) >> 21], 1u);
         __syncthreads();
         for (int i = threadIdx.x; i < kBins; i += 256)
             if (lh[i]) atomicAdd(&hist[i], lh[i]);
@@ -102,27 +150,44 @@ __global__ void zero_u32_kernel(unsigned *p, int n) {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0;
 }
 
+// Inclusive prefix sum over the 256 threads of a workgroup (4 waves).
+__device__ inline unsigned block_incl_scan(unsigned v, unsigned *wsum) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const unsigned u = __shfl_up(v, off);
+        if (lane >= off) v += u;
+    }
+    if (lane == 63) wsum[wv] = v;
+    __syncthreads();
+    unsigned before = 0;
+    for (int i = 0; i < wv; ++i) before += wsum[i];
+    __syncthreads();
+    return v + before;
+}
+
 // Finds, in histogram h (nb bins, high bin = larger keys), the bin holding the
-// need-th largest key (need >= 1; need == 0 returns the top bin with nothing
-// above). Called by every thread of a workgroup of >= 256 threads.
+// need-th largest key and the count strictly above that bin (need == 0:
+// the top bin, nothing above).
+// Called by every thread of a 256-thread workgroup: thread t sums bins
+// [nb-1-t*per, nb-1-(t+1)*per), a block scan finds the thread whose range
+// crosses need, and that thread walks its <= 8 bins.
 __device__ void find_bin(const unsigned *h, int nb, unsigned need, unsigned *s_bin,
                          unsigned *s_above, unsigned *scratch) {
     const int t = threadIdx.x;
     const int per = nb / 256;
-    if (t < 256) {
-        unsigned local = 0;
-        for (int i = 0; i < per; ++i) local += h[nb - 1 - (t * per + i)];
-        scratch[t] = local;
-    }
-    __syncthreads();
-    if (t == 0) {
-        unsigned run = 0;
-        int tt = 0;
-        for (; tt < 255; ++tt) {
-            if (run + scratch[tt] >= need) break;
-            run += scratch[tt];
+    unsigned local = 0;
+    for (int i = 0; i < per; ++i) local += h[nb - 1 - (t * per + i)];
+    const unsigned incl = block_incl_scan(local, scratch);
+    const unsigned excl = incl - local;
+    if (need == 0) {
+        if (t == 0) {
+            *s_bin = (unsigned)(nb - 1);
+            *s_above = 0;
         }
-        int bin = nb - 1 - tt * per;
+    } else if (excl < need && incl >= need) {
+        unsigned run = excl;
+        int bin = nb - 1 - t * per;
         for (int i = 0; i < per - 1; ++i, --bin) {
             if (run + h[bin] >= need) break;
             run += h[bin];

@@ -49,6 +49,12 @@ SIGNATURES: dict[str, list] = {
                                           _vp, _vp, _vp, _vp],
     "ds4hip_compressor_decode_step_w32": [_i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp,
                                           _vp, _vp, _vp, _vp],
+    "ds4hip_mul_mm_f32_f32": [_vp, _vp, _vp, _i, _i, _i, _vp],
+    "ds4hip_tail_rope_yarn_batch_f32": [_vp, _vp, _i, _i, _i, _i, _vp, _i, _i, _vp],
+    "ds4hip_indexer_topk_positions_batch": [_vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _i, _i, _vp,
+                                            _vp, _i, _vp],
+    "ds4hip_compressor_decode_step_batch_w32": [_i, _i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp,
+                                                _vp, _i, _vp, _vp, _ll, _vp, _vp, _vp, _vp],
     "ds4hip_swa_push_f32": [_vp, C.POINTER(_i), _i, _vp, _i, _vp],
     "ds4hip_comp_push_f32": [_vp, C.POINTER(_i), _i, _vp, _i, _vp],
     "ds4hip_session_state_arena_bytes": [_i],

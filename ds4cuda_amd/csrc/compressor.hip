@@ -106,11 +106,9 @@ RopeArgs rope_args(int il, int pos) {
 }
 
 // One workgroup of 512 threads; thread j owns column j (< head_dim <= 512).
-__global__ __launch_bounds__(512) void comp_emit_kernel(float *__restrict__ state_kv,
-                                                        float *__restrict__ state_score,
-                                                        const float *__restrict__ w_norm,
-                                                        float *__restrict__ emit_out, int head_dim,
-                                                        int ratio, int is_attn, RopeArgs R) {
+__device__ inline void emit_body(float *__restrict__ state_kv, float *__restrict__ state_score,
+                                 const float *__restrict__ w_norm, float *__restrict__ emit_out,
+                                 int head_dim, int ratio, int is_attn, RopeArgs R) {
     __shared__ float pooled[512];
     __shared__ float red[8];
     const int j = threadIdx.x;
@@ -211,6 +209,47 @@ __global__ __launch_bounds__(512) void comp_emit_kernel(float *__restrict__ stat
     }
 }
 
+__global__ __launch_bounds__(512) void comp_emit_kernel(float *__restrict__ state_kv,
+                                                        float *__restrict__ state_score,
+                                                        const float *__restrict__ w_norm,
+                                                        float *__restrict__ emit_out, int head_dim,
+                                                        int ratio, int is_attn, RopeArgs R) {
+    emit_body(state_kv, state_score, w_norm, emit_out, head_dim, ratio, is_attn, R);
+}
+
+// ---- batched step: n_seq sequences, one position each ----------------------------------
+
+// Y = [kv | gate] projections, [2][n_seq][width]; writes each sequence's
+// state row (cuda/compressor.cu:85) with the APE bias on the gate.
+__global__ __launch_bounds__(256) void comp_batch_update_kernel(
+        const float *__restrict__ Y, const uint16_t *__restrict__ w_ape,
+        const int *__restrict__ pos, int n_seq, int width, int ratio, float *__restrict__ state_kv,
+        float *__restrict__ state_score, long long state_stride) {
+    const int b = blockIdx.y;
+    const int o = blockIdx.x * 256 + threadIdx.x;
+    if (o >= width) return;
+    const int pm = pos[b] % ratio;
+    const int row = ratio == 4 ? ratio + pm : pm;
+    const size_t off = (size_t)b * state_stride + (size_t)row * width + o;
+    state_kv[off] = Y[(size_t)b * width + o];
+    state_score[off] = Y[((size_t)n_seq + b) * width + o] +
+                       f16_bits_to_f32(w_ape[(size_t)pm * width + o]);
+}
+
+// One workgroup per sequence; sequences whose position does not close a
+// window return at once.
+__global__ __launch_bounds__(512) void comp_batch_emit_kernel(
+        float *__restrict__ state_kv, float *__restrict__ state_score, long long state_stride,
+        const float *__restrict__ w_norm, float *__restrict__ emit_out, int head_dim, int ratio,
+        int is_attn, RopeArgs R, const int *__restrict__ pos) {
+    const int b = blockIdx.x;
+    const int p = pos[b];
+    if ((p + 1) % ratio) return;
+    R.pos = p + 1 - ratio;
+    emit_body(state_kv + (size_t)b * state_stride, state_score + (size_t)b * state_stride, w_norm,
+              emit_out + (size_t)b * head_dim, head_dim, ratio, is_attn, R);
+}
+
 int comp_step(bool is_attn, const float *x, const void *w_kv, const void *w_gate, bool w32,
               const uint16_t *w_ape, const float *w_norm, int in_dim, int head_dim_out, int ratio,
               int pos, int il, float *state_kv, float *state_score, float *emit_out,
@@ -281,4 +320,44 @@ extern "C" int ds4hip_compressor_decode_step_w32(int is_attn, const float *x_f32
         is_attn != 0, x_f32, w_kv_f32, w_gate_f32, true, w_ape_f16, w_norm_f32, in_dim,
         head_dim_out, compress_ratio, pos, il, state_kv, state_score, emit_out, emitted_out_host,
         nullptr, nullptr, (hipStream_t)stream));
+}
+
+int ds4hip_mm_f32(const float *W, const float *X, float *Y, int n_rows, int n_cols, int n_batch,
+                  hipStream_t st);
+
+extern "C" int ds4hip_compressor_decode_step_batch_w32(
+        int is_attn, int n_seq, const float *x_f32, const float *w_kv_f32,
+        const float *w_gate_f32, const uint16_t *w_ape_f16, const float *w_norm_f32, int in_dim,
+        int head_dim_out, int compress_ratio, const int *pos_host, const int *pos_dev, int il,
+        float *state_kv, float *state_score, long long state_stride, float *emit_out,
+        int *emitted_out_host, float *scratch, void *stream) {
+    const int ratio = compress_ratio;
+    if (n_seq <= 0 || n_seq > 16 || !x_f32 || !w_kv_f32 || !w_gate_f32 || !w_ape_f16 ||
+        !w_norm_f32 || !pos_host || !pos_dev || !state_kv || !state_score || !emit_out ||
+        !scratch || in_dim <= 0 || (in_dim % 16) || head_dim_out <= kNRot || head_dim_out > 512 ||
+        (head_dim_out % 64) || (ratio != 4 && ratio != 128))
+        return ds4hip_set_last_error(kEINVAL);
+    const int coff = ratio == 4 ? 2 : 1;
+    const int width = coff * head_dim_out;
+    if (state_stride < (long long)coff * ratio * width) return ds4hip_set_last_error(kEINVAL);
+    bool any = false;
+    for (int b = 0; b < n_seq; ++b) {
+        if (pos_host[b] < 0) return ds4hip_set_last_error(kEINVAL);
+        const bool e = ((pos_host[b] + 1) % ratio) == 0;
+        if (emitted_out_host) emitted_out_host[b] = e ? 1 : 0;
+        any |= e;
+    }
+    const hipStream_t st = (hipStream_t)stream;
+    int rc = ds4hip_mm_f32(w_kv_f32, x_f32, scratch, width, in_dim, n_seq, st);
+    if (!rc) rc = ds4hip_mm_f32(w_gate_f32, x_f32, scratch + (size_t)n_seq * width, width, in_dim,
+                                n_seq, st);
+    if (rc) return ds4hip_set_last_error(rc);
+    hipLaunchKernelGGL(comp_batch_update_kernel, dim3((width + 255) / 256, n_seq), dim3(256), 0,
+                       st, scratch, w_ape_f16, pos_dev, n_seq, width, ratio, state_kv,
+                       state_score, state_stride);
+    if (any)
+        hipLaunchKernelGGL(comp_batch_emit_kernel, dim3(n_seq), dim3(512), 0, st, state_kv,
+                           state_score, state_stride, w_norm_f32, emit_out, head_dim_out, ratio,
+                           is_attn ? 1 : 0, rope_args(il, 0), pos_dev);
+    return ds4hip_set_last_error(hip_status(hipGetLastError()));
 }

@@ -525,3 +525,204 @@ extern "C" int ds4hip_indexer_topk_positions(const float *q, const float *weight
         q, weights, keys, key_kind, n_comp, n_head, head_dim, top_k, n_recent, scratch_scores,
         static_cast<unsigned *>(scratch_select), allowed_mask, positions_out, (hipStream_t)stream));
 }
+
+// ---- batched selection (several sequences, one launch per phase) -------------------------
+//
+// Scores: the key rows of all sequences are concatenated; block ranges per
+// sequence come from a prefix table in the kernel arguments, so each block
+// scores keys of one sequence with that sequence's query and weights.
+// Selection: one 1024-thread workgroup per sequence holds the ordered keys of
+// its candidates in LDS (up to kSelMax) and runs a 4 x 8-bit radix select,
+// then emits the positions in ascending order (same rule as above: the top
+// (score desc, index asc) plus the forced recent window).
+
+namespace {
+
+constexpr int kMaxSeq = 16;
+constexpr int kSelMax = 16384;
+
+struct BatchArgs {
+    const float *q;            // [n_seq][n_head][128]
+    const float *w;            // [n_seq][n_head]
+    const void *keys;          // key rows, sequence s at row key0[s]
+    float *scores;             // same indexing as the key rows
+    int32_t *pos_out;          // [n_seq][pos_stride]
+    int n_seq, n_head, top_k, n_recent, pos_stride;
+    long long key0[kMaxSeq];
+    int n_comp[kMaxSeq];
+    int blk0[kMaxSeq + 1];     // first score block of each sequence
+};
+
+template <int kKind>
+__global__ __launch_bounds__(256) void score_batch_kernel(const BatchArgs A) {
+    int s = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxSeq; ++i)
+        if (i < A.n_seq && (int)blockIdx.x >= A.blk0[i]) s = i;
+    int n = 0;
+    long long k0 = 0;
+#pragma unroll
+    for (int i = 0; i < kMaxSeq; ++i)
+        if (i == s) {
+            n = A.n_comp[i];
+            k0 = A.key0[i];
+        }
+    int first = 0;
+#pragma unroll
+    for (int i = 0; i < kMaxSeq; ++i)
+        if (i == s) first = A.blk0[i];
+    const int c = ((int)blockIdx.x - first) * 256 + threadIdx.x;
+    if (c >= n) return;
+    const float *qs = A.q + (size_t)s * A.n_head * kMaxDim;
+    const float *ws = A.w + (size_t)s * A.n_head;
+    A.scores[k0 + c] = score_one<kKind, kMaxDim>(qs, ws, A.keys, (int)(k0 + c), A.n_head);
+}
+
+__device__ inline unsigned scan1024_excl(unsigned v, unsigned *wsum, unsigned *total) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    unsigned x = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const unsigned u = __shfl_up(x, off);
+        if (lane >= off) x += u;
+    }
+    if (lane == 63) wsum[wv] = x;
+    __syncthreads();
+    unsigned before = 0, tot = 0;
+    for (int i = 0; i < 16; ++i) {
+        const unsigned t = wsum[i];
+        before += i < wv ? t : 0;
+        tot += t;
+    }
+    __syncthreads();
+    *total = tot;
+    return before + x - v;
+}
+
+__global__ __launch_bounds__(1024) void select_batch_kernel(const BatchArgs A) {
+    __shared__ unsigned keys[kSelMax];
+    __shared__ unsigned hist[256];
+    __shared__ unsigned wsum[16];
+    __shared__ unsigned s_bin, s_above;
+    const int s = blockIdx.x;
+    int n = 0;
+    long long k0 = 0;
+#pragma unroll
+    for (int i = 0; i < kMaxSeq; ++i)
+        if (i == s) {
+            n = A.n_comp[i];
+            k0 = A.key0[i];
+        }
+    int32_t *out = A.pos_out + (size_t)s * A.pos_stride;
+    const int t = threadIdx.x;
+    if (n <= A.top_k) {
+        for (int i = t; i < n; i += 1024) out[i] = i;
+        return;
+    }
+    const int recent = A.n_recent < A.top_k ? A.n_recent : A.top_k;
+    const int n_cand = n - recent;
+    const unsigned need0 = (unsigned)(A.top_k - recent);
+    for (int i = t; i < n_cand; i += 1024) keys[i] = ord_key(A.scores[k0 + i]);
+    // radix select of the need0-th largest key, 8 bits at a time
+    unsigned prefix = 0, pmask = 0, need = need0;
+    for (int shift = 24; shift >= 0 && need > 0; shift -= 8) {
+        if (t < 256) hist[t] = 0;
+        __syncthreads();
+        for (int i = t; i < n_cand; i += 1024) {
+            const unsigned k = keys[i];
+            if ((k & pmask) == prefix) atomicAdd(&hist[(k >> shift) & 255], 1u);
+        }
+        __syncthreads();
+        // bins from the top: thread b < 256 owns bin 255 - b
+        const unsigned v = t < 256 ? hist[255 - t] : 0;
+        unsigned tot;
+        const unsigned ex = scan1024_excl(v, wsum, &tot);
+        if (t < 256 && ex < need && ex + v >= need) {
+            s_bin = 255 - t;
+            s_above = ex;
+        }
+        __syncthreads();
+        prefix |= s_bin << shift;
+        pmask |= 255u << shift;
+        need -= s_above;
+        __syncthreads();
+    }
+    // need0 == 0 leaves T above every key
+    const unsigned T = need0 ? prefix : 0xFFFFFFFFu;
+    const unsigned need_eq = need0 ? need : 0;
+    // emit in index order: thread t owns a contiguous range
+    const int per = (n_cand + 1023) / 1024;
+    const int b0 = t * per, b1 = min(b0 + per, n_cand);
+    unsigned n_eq = 0;
+    for (int i = b0; i < b1; ++i) n_eq += keys[i] == T;
+    unsigned tot_eq;
+    unsigned eq_rank = scan1024_excl(n_eq, wsum, &tot_eq);
+    unsigned n_sel = 0;
+    {
+        unsigned r = eq_rank;
+        for (int i = b0; i < b1; ++i) {
+            const unsigned k = keys[i];
+            if (k > T) ++n_sel;
+            else if (k == T) { n_sel += r < need_eq; ++r; }
+        }
+    }
+    unsigned tot_sel;
+    unsigned o = scan1024_excl(n_sel, wsum, &tot_sel);
+    {
+        unsigned r = eq_rank;
+        for (int i = b0; i < b1; ++i) {
+            const unsigned k = keys[i];
+            bool take = k > T;
+            if (k == T) { take = r < need_eq; ++r; }
+            if (take) out[o++] = i;
+        }
+    }
+    for (int i = t; i < recent; i += 1024) out[tot_sel + i] = n_cand + i;
+}
+
+}  // namespace
+
+extern "C" int ds4hip_indexer_topk_positions_batch(
+        const float *q, const float *weights, const void *keys, int key_kind,
+        const long long *key_row0_host, const int *n_comp_host, int n_seq, int n_head,
+        int head_dim, int top_k, int n_recent, float *scratch_scores, int32_t *positions_out,
+        int pos_stride, void *stream) {
+    if (!q || !weights || !keys || !key_row0_host || !n_comp_host || !scratch_scores ||
+        !positions_out || key_kind < 0 || key_kind > 2 || n_seq <= 0 || n_seq > kMaxSeq ||
+        n_head <= 0 || n_head > kMaxHeads || head_dim != kMaxDim || top_k <= 0 || n_recent < 0 ||
+        pos_stride < top_k)
+        return ds4hip_set_last_error(kEINVAL);
+    BatchArgs A;
+    A.q = q;
+    A.w = weights;
+    A.keys = keys;
+    A.scores = scratch_scores;
+    A.pos_out = positions_out;
+    A.n_seq = n_seq;
+    A.n_head = n_head;
+    A.top_k = top_k;
+    A.n_recent = n_recent;
+    A.pos_stride = pos_stride;
+    int blk = 0;
+    for (int s = 0; s < kMaxSeq; ++s) {
+        const int n = s < n_seq ? n_comp_host[s] : 0;
+        if (n < 0 || (n > top_k && n - (n_recent < top_k ? n_recent : top_k) > kSelMax))
+            return ds4hip_set_last_error(kEINVAL);
+        A.n_comp[s] = n;
+        A.key0[s] = s < n_seq ? key_row0_host[s] : 0;
+        A.blk0[s] = blk;
+        // only sequences that need a selection are scored
+        if (s < n_seq && n > top_k) blk += (n + 255) / 256;
+    }
+    A.blk0[kMaxSeq] = blk;
+    const hipStream_t st = (hipStream_t)stream;
+    if (blk > 0) {
+        switch (key_kind) {
+        case 0: hipLaunchKernelGGL(score_batch_kernel<0>, dim3(blk), dim3(256), 0, st, A); break;
+        case 1: hipLaunchKernelGGL(score_batch_kernel<1>, dim3(blk), dim3(256), 0, st, A); break;
+        default: hipLaunchKernelGGL(score_batch_kernel<2>, dim3(blk), dim3(256), 0, st, A); break;
+        }
+    }
+    hipLaunchKernelGGL(select_batch_kernel, dim3(n_seq), dim3(1024), 0, st, A);
+    return ds4hip_set_last_error(hip_status(hipGetLastError()));
+}

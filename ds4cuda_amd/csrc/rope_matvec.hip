@@ -67,11 +67,15 @@ RopeParams rope_params(int n_rot, int il, bool inverse) {
     return P;
 }
 
+// pos_dev (optional): position per group of heads_per_pos consecutive heads.
 __global__ __launch_bounds__(64) void rope_tail_kernel(const float *__restrict__ x_in,
                                                        float *__restrict__ x_out, int head_dim,
-                                                       int n_rot, int pos, RopeParams P) {
+                                                       int n_rot, int pos, RopeParams P,
+                                                       const int *__restrict__ pos_dev,
+                                                       int heads_per_pos) {
     const int head = blockIdx.x;
     const int t = threadIdx.x;
+    if (pos_dev) pos = pos_dev[head / heads_per_pos];
     const int n_nope = head_dim - n_rot;
     const float *xi = x_in + (size_t)head * head_dim;
     float *xo = x_out + (size_t)head * head_dim;
@@ -99,14 +103,15 @@ __global__ __launch_bounds__(64) void rope_tail_kernel(const float *__restrict__
 }
 
 int launch_rope(const float *x_in, float *x_out, int n_heads, int head_dim, int n_rot, int pos,
-                int il, bool inverse, hipStream_t st) {
+                int il, bool inverse, hipStream_t st, const int *pos_dev = nullptr,
+                int heads_per_pos = 1) {
     if (!x_in || !x_out || n_heads < 0 || head_dim <= 0 || n_rot <= 0 || n_rot > 128 ||
         (n_rot & 1) || n_rot > head_dim)
         return kEINVAL;
     if (n_heads == 0) return 0;
     const RopeParams P = rope_params(n_rot, il, inverse);
     hipLaunchKernelGGL(rope_tail_kernel, dim3(n_heads), dim3(64), 0, st, x_in, x_out, head_dim,
-                       n_rot, pos, P);
+                       n_rot, pos, P, pos_dev, heads_per_pos);
     return hip_status(hipGetLastError());
 }
 
@@ -287,7 +292,74 @@ __global__ __launch_bounds__(256) void mm_bf16_kernel(const uint16_t *__restrict
     }
 }
 
+// fp32 weights: v_mfma_f32_16x16x4_f32 (exact fp32 products). One wave owns
+// 16 rows and a column slice of kMmF32Cols; lane (i, k) loads W[row i][c+4k ..
+// c+4k+3] and X[batch i][same] as float4 and feeds element j to MFMA step j,
+// so A and B agree on the reduction index. Column slices add into Y with
+// atomics (Y zeroed first).
+constexpr int kMmF32Cols = 512;
+
+__global__ __launch_bounds__(256) void mm_f32_kernel(const float *__restrict__ W,
+                                                     const float *__restrict__ X,
+                                                     float *__restrict__ Y, int n_rows,
+                                                     int n_cols, int n_batch) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r0 = (blockIdx.x * 4 + wave) * 16;
+    if (r0 >= n_rows) return;
+    const int i = lane & 15, k = lane >> 4;
+    const int c0 = blockIdx.y * kMmF32Cols;
+    const int c1 = min(c0 + kMmF32Cols, n_cols);
+    const int row = min(r0 + i, n_rows - 1);
+    const float *wr = W + (size_t)row * n_cols;
+    const bool bok = i < n_batch;
+    const float *xr = X + (size_t)(bok ? i : 0) * n_cols;
+    float4_t acc = float4_t{0, 0, 0, 0};
+    for (int c = c0 + 4 * k; c < c1; c += 16) {
+        const float4_t a = *reinterpret_cast<const float4_t *>(wr + c);
+        float4_t b = *reinterpret_cast<const float4_t *>(xr + c);
+        if (!bok) b = float4_t{0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j], b[j], acc, 0, 0, 0);
+    }
+    // D[row 4k+r][batch i]
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int rr = r0 + 4 * k + r;
+        if (rr < n_rows && bok) atomicAdd(&Y[(size_t)i * n_rows + rr], acc[r]);
+    }
+}
+
 }  // namespace
+
+int ds4hip_mm_f32(const float *W, const float *X, float *Y, int n_rows, int n_cols, int n_batch,
+                  hipStream_t st) {
+    if (!W || !X || !Y || n_rows <= 0 || n_cols <= 0 || n_cols % 16 || n_batch <= 0 ||
+        n_batch > 16)
+        return kEINVAL;
+    const size_t ny = (size_t)n_batch * n_rows;
+    hipLaunchKernelGGL(zero_kernel, dim3((unsigned)std::min<size_t>((ny + 255) / 256, 1024)),
+                       dim3(256), 0, st, Y, ny);
+    const dim3 grid((n_rows + 63) / 64, (n_cols + kMmF32Cols - 1) / kMmF32Cols);
+    hipLaunchKernelGGL(mm_f32_kernel, grid, dim3(256), 0, st, W, X, Y, n_rows, n_cols, n_batch);
+    return hip_status(hipGetLastError());
+}
+
+extern "C" int ds4hip_mul_mm_f32_f32(const float *W, const float *X, float *Y, int n_rows,
+                                     int n_cols, int n_batch, void *stream) {
+    return ds4hip_set_last_error(ds4hip_mm_f32(W, X, Y, n_rows, n_cols, n_batch,
+                                               (hipStream_t)stream));
+}
+
+extern "C" int ds4hip_tail_rope_yarn_batch_f32(const float *x_in, float *x_out, int n_seq,
+                                               int n_heads, int head_dim, int n_rot,
+                                               const int *pos_dev, int il, int inverse,
+                                               void *stream) {
+    if (n_seq < 0 || !pos_dev) return ds4hip_set_last_error(kEINVAL);
+    return ds4hip_set_last_error(launch_rope(x_in, x_out, n_seq * n_heads, head_dim, n_rot, 0, il,
+                                             inverse != 0, (hipStream_t)stream, pos_dev,
+                                             n_heads > 0 ? n_heads : 1));
+}
 
 extern "C" int ds4hip_tail_rope_yarn_f32(const float *x_in, float *x_out, int n_heads,
                                          int head_dim, int n_rot, int pos, int il, void *stream) {

@@ -315,3 +315,54 @@ def compressor_decode_step_w32(is_attn, x_f32, w_kv_f32, w_gate_f32, w_ape_f16, 
          compress_ratio, pos, il, _ptr(state_kv), _ptr(state_score), _ptr(emit_out),
          C.byref(emitted), _stream(stream))
     return emitted.value
+
+
+# ---- batched forms (the batched-decode attention block) ------------------------------------
+
+def mul_mm_f32_f32(W, X, Y, n_rows, n_cols, n_batch, stream=None):
+    _check(W, torch.float32, n_rows * n_cols, "W")
+    _check(X, torch.float32, n_batch * n_cols, "X")
+    _check(Y, torch.float32, n_batch * n_rows, "Y")
+    call("ds4hip_mul_mm_f32_f32", _ptr(W), _ptr(X), _ptr(Y), n_rows, n_cols, n_batch,
+         _stream(stream))
+
+
+def tail_rope_yarn_batch_f32(x_in, x_out, n_seq, n_heads, head_dim, n_rot, pos_dev, il,
+                             inverse=False, stream=None):
+    _check(x_in, torch.float32, n_seq * n_heads * head_dim, "x_in")
+    _check(x_out, torch.float32, n_seq * n_heads * head_dim, "x_out")
+    _check(pos_dev, torch.int32, n_seq, "pos")
+    call("ds4hip_tail_rope_yarn_batch_f32", _ptr(x_in), _ptr(x_out), n_seq, n_heads, head_dim,
+         n_rot, _ptr(pos_dev), il, int(inverse), _stream(stream))
+
+
+def indexer_topk_positions_batch(q, weights, keys, key_row0, n_comp, top_k, n_recent, scores,
+                                 positions, stream=None):
+    """q [n_seq, n_head, 128] fp32, weights [n_seq, n_head], keys [rows, 128]
+    (fp32 / f16 / bf16), key_row0 / n_comp host ints per sequence, scores
+    [rows] fp32 scratch, positions [n_seq, stride] int32."""
+    n_seq = len(n_comp)
+    n_head = q.shape[1]
+    r0 = (C.c_longlong * n_seq)(*[int(x) for x in key_row0])
+    nc = (C.c_int * n_seq)(*[int(x) for x in n_comp])
+    _check(positions, torch.int32, n_seq * positions.shape[-1], "positions")
+    call("ds4hip_indexer_topk_positions_batch", _ptr(q), _ptr(weights), _ptr(keys),
+         _KEY_KIND[keys.dtype], C.cast(r0, C.c_void_p), C.cast(nc, C.c_void_p), n_seq, n_head,
+         keys.shape[-1], top_k, n_recent, _ptr(scores), _ptr(positions), positions.shape[-1],
+         _stream(stream))
+
+
+def compressor_decode_step_batch_w32(is_attn, x, w_kv, w_gate, w_ape, w_norm, in_dim,
+                                     head_dim_out, ratio, pos, pos_dev, il, state_kv,
+                                     state_score, state_stride, emit_out, scratch, stream=None):
+    """One compressor step for len(pos) sequences; returns the host emit flags."""
+    n = len(pos)
+    ph = (C.c_int * n)(*[int(p) for p in pos])
+    em = (C.c_int * n)()
+    _check(pos_dev, torch.int32, n, "pos_dev")
+    call("ds4hip_compressor_decode_step_batch_w32", int(is_attn), n, _ptr(x), _ptr(w_kv),
+         _ptr(w_gate), _ptr(w_ape), _ptr(w_norm), in_dim, head_dim_out, ratio,
+         C.cast(ph, C.c_void_p), _ptr(pos_dev), il, _ptr(state_kv), _ptr(state_score),
+         int(state_stride), _ptr(emit_out), C.cast(em, C.c_void_p), _ptr(scratch),
+         _stream(stream))
+    return list(em)

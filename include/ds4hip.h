@@ -180,6 +180,19 @@ int ds4hip_mul_mv_q8_0_q8_0_f32_prealloc(const void *W, const float *x, float *y
 int ds4hip_mul_mm_bf16_f32(const uint16_t *W, const float *X, float *Y, int n_rows, int n_cols,
                            int n_batch, void *stream);
 
+/* Batched fp32 projection (additive; the batched-decode compressor
+ * projection): Y[b][r] = sum_c W[r][c] X[b][c], W fp32 [n_rows][n_cols],
+ * n_batch <= 16, n_cols % 16 == 0. Y is overwritten. */
+int ds4hip_mul_mm_f32_f32(const float *W, const float *X, float *Y, int n_rows, int n_cols,
+                          int n_batch, void *stream);
+
+/* Tail RoPE for n_seq sequences at their own positions (additive; batched form
+ * of ds4hip_tail_rope_yarn_f32 / _inverse_f32): x [n_seq][n_heads][head_dim],
+ * pos_dev device int [n_seq]; inverse != 0 negates the sine. In-place safe. */
+int ds4hip_tail_rope_yarn_batch_f32(const float *x_in, float *x_out, int n_seq, int n_heads,
+                                    int head_dim, int n_rot, const int *pos_dev, int il,
+                                    int inverse, void *stream);
+
 /* ---- indexer --------------------------------------------------------------------------- */
 
 /* Replaces ds4cuda::launch_indexer_allowed_short_circuit_i32
@@ -223,6 +236,21 @@ int ds4hip_indexer_topk_positions(const float *q, const float *weights, const vo
                                   int n_recent, float *scratch_scores, void *scratch_select,
                                   int32_t *allowed_mask, int32_t *positions_out, void *stream);
 
+/* Sparse-decode selection for up to 16 sequences in one launch pair
+ * (additive). Sequence s scores its n_comp_host[s] key rows starting at key
+ * row key_row0_host[s] of `keys` (key_kind as above, head_dim 128) with query
+ * q[s] [n_head][128] and weights[s] [n_head], into scratch_scores (same row
+ * indexing as keys), and writes its selected positions, ascending, to
+ * positions_out + s * pos_stride: all n positions when n <= top_k, else the
+ * last n_recent plus the best top_k - n_recent of the rest (score desc, index
+ * asc). Candidates per sequence <= 16384. */
+int ds4hip_indexer_topk_positions_batch(const float *q, const float *weights, const void *keys,
+                                        int key_kind, const long long *key_row0_host,
+                                        const int *n_comp_host, int n_seq, int n_head,
+                                        int head_dim, int top_k, int n_recent,
+                                        float *scratch_scores, int32_t *positions_out,
+                                        int pos_stride, void *stream);
+
 /* ---- compressor ------------------------------------------------------------------------ */
 
 /* Replaces ds4cuda::launch_compressor_decode_step_f32_prealloc
@@ -258,6 +286,22 @@ int ds4hip_compressor_decode_step_w32(int is_attn, const float *x_f32, const flo
                                       int compress_ratio, int pos, int il, float *state_kv,
                                       float *state_score, float *emit_out,
                                       int *emitted_out_host, void *stream);
+
+/* One compressor step for n_seq <= 16 sequences at once, fp32 weights read once
+ * for all of them (additive; batched form of
+ * ds4hip_compressor_decode_step_w32). x [n_seq][in_dim]; sequence b is at
+ * position pos_host[b] (pos_dev: the same array in device memory) with state
+ * at state_kv / state_score + b * state_stride floats; emit_out row b is
+ * written when (pos + 1) % ratio == 0, and emitted_out_host[b] (host, may be
+ * NULL) says so. scratch: 2 * n_seq * coff * head_dim_out floats. */
+int ds4hip_compressor_decode_step_batch_w32(int is_attn, int n_seq, const float *x_f32,
+                                            const float *w_kv_f32, const float *w_gate_f32,
+                                            const uint16_t *w_ape_f16, const float *w_norm_f32,
+                                            int in_dim, int head_dim_out, int compress_ratio,
+                                            const int *pos_host, const int *pos_dev, int il,
+                                            float *state_kv, float *state_score,
+                                            long long state_stride, float *emit_out,
+                                            int *emitted_out_host, float *scratch, void *stream);
 
 #ifdef __cplusplus
 }

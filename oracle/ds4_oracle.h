@@ -123,6 +123,12 @@ int orc_compressor_step(int is_attn, const float *x, const uint16_t *w_kv,
                         const float *w_norm, int in_dim, int head_dim_out,
                         int ratio, int pos, int il, float *state_kv,
                         float *state_score, float *emit_out);
+// The same step with fp32 projection weights (fp64 accumulation).
+int orc_compressor_step_w32(int is_attn, const float *x, const float *w_kv,
+                            const float *w_gate, const uint16_t *w_ape,
+                            const float *w_norm, int in_dim, int head_dim_out,
+                            int ratio, int pos, int il, float *state_kv,
+                            float *state_score, float *emit_out);
 
 #ifdef __cplusplus
 }

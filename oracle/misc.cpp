@@ -159,18 +159,56 @@ extern "C" void orc_bf16_matvec(const uint16_t *W, const float *x, float *y, int
 }
 
 // cuda/compressor.cu:64-349 (launch_compressor_decode_step_f32).
+// The step after the two projections (kv, sc: the W x products).
+static int compressor_after_projection(int is_attn, const float *kv_in, const float *sc_in,
+                                       const uint16_t *w_ape, const float *w_norm,
+                                       int head_dim_out, int ratio, int pos, int il,
+                                       float *state_kv, float *state_score, float *emit_out);
+
 extern "C" int orc_compressor_step(int is_attn, const float *x, const uint16_t *w_kv,
                                    const uint16_t *w_gate, const uint16_t *w_ape,
                                    const float *w_norm, int in_dim, int head_dim_out,
                                    int ratio, int pos, int il, float *state_kv,
                                    float *state_score, float *emit_out) {
+    const int width = (ratio == 4 ? 2 : 1) * head_dim_out;
+    std::vector<float> kv((size_t)width), sc((size_t)width);
+    orc_mul_mv_f16_f32(w_kv, x, kv.data(), width, in_dim);
+    orc_mul_mv_f16_f32(w_gate, x, sc.data(), width, in_dim);
+    return compressor_after_projection(is_attn, kv.data(), sc.data(), w_ape, w_norm,
+                                       head_dim_out, ratio, pos, il, state_kv, state_score,
+                                       emit_out);
+}
+
+// The same step with fp32 projection weights (fp64 accumulation).
+extern "C" int orc_compressor_step_w32(int is_attn, const float *x, const float *w_kv,
+                                       const float *w_gate, const uint16_t *w_ape,
+                                       const float *w_norm, int in_dim, int head_dim_out,
+                                       int ratio, int pos, int il, float *state_kv,
+                                       float *state_score, float *emit_out) {
+    const int width = (ratio == 4 ? 2 : 1) * head_dim_out;
+    std::vector<float> kv((size_t)width), sc((size_t)width);
+    for (int o = 0; o < width; ++o) {
+        double a = 0.0, b = 0.0;
+        for (int i = 0; i < in_dim; ++i) {
+            a += (double)w_kv[(size_t)o * in_dim + i] * x[i];
+            b += (double)w_gate[(size_t)o * in_dim + i] * x[i];
+        }
+        kv[o] = (float)a;
+        sc[o] = (float)b;
+    }
+    return compressor_after_projection(is_attn, kv.data(), sc.data(), w_ape, w_norm,
+                                       head_dim_out, ratio, pos, il, state_kv, state_score,
+                                       emit_out);
+}
+
+static int compressor_after_projection(int is_attn, const float *kv, const float *sc,
+                                       const uint16_t *w_ape, const float *w_norm,
+                                       int head_dim_out, int ratio, int pos, int il,
+                                       float *state_kv, float *state_score, float *emit_out) {
     const int coff = ratio == 4 ? 2 : 1;
     const int width = coff * head_dim_out;
     const int pos_mod = pos % ratio;
     const bool emit = ((pos + 1) % ratio) == 0;
-    std::vector<float> kv((size_t)width), sc((size_t)width);
-    orc_mul_mv_f16_f32(w_kv, x, kv.data(), width, in_dim);
-    orc_mul_mv_f16_f32(w_gate, x, sc.data(), width, in_dim);
     // compressor.cu:64-90: APE add and state-row write.
     const int row = ratio == 4 ? ratio + pos_mod : pos_mod;
     for (int j = 0; j < width; ++j) {

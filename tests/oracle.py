@@ -37,6 +37,7 @@ def lib():
         _o.orc_fp8_deq.argtypes = [C.c_uint8, C.c_int]
         _o.orc_topk_positions.restype = C.c_int
         _o.orc_compressor_step.restype = C.c_int
+        _o.orc_compressor_step_w32.restype = C.c_int
     return _o
 
 

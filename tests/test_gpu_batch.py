@@ -1,0 +1,111 @@
+"""Batched forms used by the batched-decode attention block: fp32 projection,
+per-sequence tail RoPE, compressor step for 16 sequences and the batched
+sparse selection — each against the oracle run one sequence at a time."""
+import ctypes as C
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from oracle import P
+from ds4cuda_amd import ops, synth
+from test_gpu_ops import close, t
+from test_oracle_misc import rope
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("n_rows,n_cols,nb", [(1024, 4096, 16), (256, 4096, 3), (100, 48, 1)])
+def test_mul_mm_f32(gpu, n_rows, n_cols, nb):
+    W = synth.normal(51, 1, n_rows * n_cols).reshape(n_rows, n_cols) * 0.02
+    X = synth.normal(51, 2, nb * n_cols).reshape(nb, n_cols)
+    Y = torch.full((nb, n_rows), 7.0, device=gpu)
+    ops.mul_mm_f32_f32(t(W, gpu), t(X, gpu), Y, n_rows, n_cols, nb)
+    torch.cuda.synchronize()
+    close(Y.cpu().numpy(), X.astype(np.float64) @ W.astype(np.float64).T, 1e-5)
+
+
+def test_rope_batch_inverse(gpu):
+    n_seq, n_heads = 5, 64
+    pos = np.array([3, 1000, 16383, 0, 77], np.int32)
+    x = synth.normal(52, 1, n_seq * n_heads * 512).reshape(n_seq, n_heads, 512)
+    xt = t(x, gpu)
+    ops.tail_rope_yarn_batch_f32(xt, xt, n_seq, n_heads, 512, 64, t(pos, gpu), 2, inverse=True)
+    torch.cuda.synchronize()
+    got = xt.cpu().numpy()
+    for b in range(n_seq):
+        close(got[b], rope(x[b], int(pos[b]), 2, inverse=True), 1e-5)
+
+
+def test_compressor_batch_matches_per_sequence(gpu):
+    n_seq, in_dim, hd, ratio, il = 16, 4096, 512, 4, 2
+    width = 2 * hd
+    rows = 2 * ratio
+    wkv = (synth.normal(53, 1, width * in_dim) * 0.02).reshape(width, in_dim)
+    wg = (synth.normal(53, 2, width * in_dim) * 0.02).reshape(width, in_dim)
+    ape = np.ascontiguousarray((synth.normal(53, 3, ratio * width) * 0.1).astype(np.float16)
+                               .view(np.uint16).reshape(ratio, width))
+    wn = (1 + 0.1 * synth.normal(53, 4, hd)).astype(np.float32)
+    stride = rows * width
+    skv = np.zeros((n_seq, rows, width), np.float32)
+    ssc = np.full((n_seq, rows, width), -np.inf, np.float32)
+    g_kv, g_sc = t(skv, gpu), t(ssc, gpu)
+    g_wkv, g_wg, g_ape, g_wn = t(wkv, gpu), t(wg, gpu), t(ape.view(np.int16), gpu), t(wn, gpu)
+    emit = torch.zeros((n_seq, hd), device=gpu)
+    scratch = torch.empty(2 * n_seq * width, device=gpu)
+    start = np.arange(n_seq) * 3 + 1          # sequences at different phases of the window
+    for step in range(6):
+        pos = (start + step).astype(np.int32)
+        x = synth.normal(54, step, n_seq * in_dim).reshape(n_seq, in_dim)
+        flags = ops.compressor_decode_step_batch_w32(
+            True, t(x, gpu), g_wkv, g_wg, g_ape, g_wn, in_dim, hd, ratio, pos, t(pos, gpu), il,
+            g_kv, g_sc, stride, emit, scratch)
+        torch.cuda.synchronize()
+        got_e = emit.cpu().numpy()
+        for b in range(n_seq):
+            ref_e = np.zeros(hd, np.float32)
+            r = O.lib().orc_compressor_step_w32(
+                C.c_int(1), P(x[b]), P(wkv), P(wg), P(ape), P(wn), C.c_int(in_dim), C.c_int(hd),
+                C.c_int(ratio), C.c_int(int(pos[b])), C.c_int(il), P(skv[b]), P(ssc[b]),
+                P(ref_e))
+            assert flags[b] == r
+            if r:
+                close(got_e[b], ref_e, 3e-2)
+        close(g_kv.cpu().numpy(), skv, 1e-5)
+        fin = np.isfinite(ssc)
+        got_sc = g_sc.cpu().numpy()
+        assert np.array_equal(np.isfinite(got_sc), fin)
+        close(got_sc[fin], ssc[fin], 1e-5)
+
+
+def test_indexer_batch_positions(gpu):
+    n_seq, top_k, recent = 6, 512, 64
+    n_comp = [100, 512, 513, 2000, 4000, 3]
+    row0 = np.concatenate([[0], np.cumsum(n_comp)[:-1]]) + 10
+    n_rows = int(row0[-1] + n_comp[-1])
+    keys = synth.to_bf16_bits(synth.normal(55, 1, n_rows * 128)).reshape(n_rows, 128)
+    keys[row0[3] + 200: row0[3] + 260] = keys[row0[3] + 5]       # tied scores
+    q = synth.normal(55, 2, n_seq * 64 * 128).reshape(n_seq, 64, 128)
+    w = synth.normal(55, 3, n_seq * 64).reshape(n_seq, 64) / np.float32(np.sqrt(128 * 64))
+    scores = torch.zeros(n_rows, device=gpu)
+    pos = torch.full((n_seq, top_k + 7), -1, dtype=torch.int32, device=gpu)
+    ops.indexer_topk_positions_batch(t(q, gpu), t(w, gpu),
+                                     t(keys.view(np.int16), gpu).view(torch.bfloat16),
+                                     row0, n_comp, top_k, recent, scores, pos)
+    torch.cuda.synchronize()
+    got = pos.cpu().numpy()
+    for s in range(n_seq):
+        n = n_comp[s]
+        if n <= top_k:
+            assert np.array_equal(got[s, :n], np.arange(n))
+            continue
+        ks = np.ascontiguousarray(keys[row0[s]:row0[s] + n])
+        sc = np.zeros(n, np.float32)
+        O.lib().orc_indexer_scores(P(q[s]), P(w[s]), P(ks), C.c_int(2), C.c_int(n), C.c_int(64),
+                                   C.c_int(128), P(sc))
+        assert np.array_equal(scores.cpu().numpy()[row0[s]:row0[s] + n].view(np.uint32),
+                              sc.view(np.uint32))
+        ref = np.zeros(top_k, np.int32)
+        O.lib().orc_topk_positions(P(sc), C.c_int(n), C.c_int(top_k), C.c_int(recent), P(ref))
+        assert np.array_equal(got[s, :top_k], ref), s

@@ -164,3 +164,32 @@ def test_compressor_invariants(ratio):
                 assert np.array_equal(skv[:4], skv[4:])      # ring shift duplicated the rows
             assert np.isclose(np.sqrt((e.astype(np.float64) ** 2).mean()), 1.0, rtol=1e-3)
     assert len(emits) == 2
+
+
+def test_compressor_w32_matches_f16_on_f16_weights():
+    # fp32 weights holding f16-representable values give the f16 step's result
+    rng = np.random.default_rng(6)
+    in_dim, hd, ratio = 256, 128, 4
+    width = 2 * hd
+    wkv16 = (rng.standard_normal((width, in_dim)) * 0.05).astype(np.float16)
+    wg16 = (rng.standard_normal((width, in_dim)) * 0.05).astype(np.float16)
+    ape = np.ascontiguousarray((rng.standard_normal((ratio, width)) * 0.1).astype(np.float16)
+                               .view(np.uint16))
+    wn = np.ones(hd, np.float32)
+    st = [(np.zeros((2 * ratio, width), np.float32), np.full((2 * ratio, width), -np.inf, np.float32))
+          for _ in range(2)]
+    for pos in range(8):
+        x = rng.standard_normal(in_dim).astype(np.float32)
+        e16 = np.zeros(hd, np.float32)
+        e32 = np.zeros(hd, np.float32)
+        r16 = O.lib().orc_compressor_step(
+            C.c_int(1), P(x), P(np.ascontiguousarray(wkv16.view(np.uint16))),
+            P(np.ascontiguousarray(wg16.view(np.uint16))), P(ape), P(wn), C.c_int(in_dim),
+            C.c_int(hd), C.c_int(ratio), C.c_int(pos), C.c_int(2), P(st[0][0]), P(st[0][1]), P(e16))
+        r32 = O.lib().orc_compressor_step_w32(
+            C.c_int(1), P(x), P(np.ascontiguousarray(wkv16.astype(np.float32))),
+            P(np.ascontiguousarray(wg16.astype(np.float32))), P(ape), P(wn), C.c_int(in_dim),
+            C.c_int(hd), C.c_int(ratio), C.c_int(pos), C.c_int(2), P(st[1][0]), P(st[1][1]), P(e32))
+        assert r16 == r32
+        assert np.array_equal(st[0][0], st[1][0]) and np.array_equal(st[0][1], st[1][1])
+        assert np.array_equal(e16, e32)

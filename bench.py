@@ -155,6 +155,116 @@ def bench_sparse(dev, stream, steps):
             "frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def bench_batch(dev, stream, steps):
+    """the attention block of one layer for 16 sequences
+    in batched decode (contexts ~U[1024, 16384], seeded): compressor (ratio
+    4, fp32 weights) for the attention and the indexer keys, FP8 quantize +
+    append into a 256-row paged cache, sparse top-2048 selection, decode
+    attention, inverse tail RoPE and the bf16 attn_out projection
+    32768 -> 4096."""
+    import torch
+    from ds4cuda_amd import ops
+    B, IN, PAGE, TOPK, SWA = 16, 4096, 256, 2048, 128
+    rng = np.random.default_rng(5)
+    ctx = rng.integers(1024, 16385, size=B)
+    n_comp = (ctx // 4).astype(int)
+    cmax = int(n_comp.max()) + 8
+    lrows = cmax + SWA                               # logical rows per sequence
+    pages_per = (lrows + PAGE - 1) // PAGE
+    g = torch.Generator(device=dev)
+    g.manual_seed(6)
+    perm = torch.randperm(B * pages_per, generator=g, device=dev).to(torch.int32)
+    page_table = perm.reshape(B, pages_per).contiguous()
+    pt_host = page_table.cpu().numpy()
+    trash = B * pages_per * PAGE                     # one spare row for rows not emitted
+    cache = ops.Fp8KVCache.empty(trash + 1, device=dev)
+
+    def phys(b, lrow):
+        return int(pt_host[b][lrow // PAGE]) * PAGE + lrow % PAGE
+
+    # fill every sequence's compressed rows and its full sliding window
+    for b in range(B):
+        rows = list(range(int(n_comp[b]))) + list(range(cmax, cmax + SWA))
+        dst = torch.tensor([phys(b, r) for r in rows], dtype=torch.int64, device=dev)
+        cache.append(torch.randn((len(rows), HEAD_DIM), generator=g, device=dev), dst_rows=dst)
+    # index keys (fp32, as the indexer compressor emits them), concatenated
+    key_row0 = np.concatenate([[0], np.cumsum(n_comp)[:-1]]).astype(np.int64)
+    keys = torch.randn((int(n_comp.sum()), 128), generator=g, device=dev)
+    # row lists: the window (reversed) then the selected compressed rows
+    rowlist = torch.empty((B, SWA + TOPK), dtype=torch.int32, device=dev)
+    rowlist[:, :SWA] = torch.arange(cmax + SWA - 1, cmax - 1, -1, dtype=torch.int32, device=dev)
+    counts = [SWA + min(int(n), TOPK) for n in n_comp]
+    ws = torch.empty(ops.decode_fp8_workspace_bytes(counts), dtype=torch.uint8, device=dev)
+    # weights and per-step inputs
+    w_kv = torch.randn((1024, IN), generator=g, device=dev) * 0.02
+    w_gate = torch.randn((1024, IN), generator=g, device=dev) * 0.02
+    wi_kv = torch.randn((256, IN), generator=g, device=dev) * 0.02
+    wi_gate = torch.randn((256, IN), generator=g, device=dev) * 0.02
+    ape = (torch.randn((4, 1024), generator=g, device=dev) * 0.02).half().view(torch.int16)
+    ape_i = (torch.randn((4, 256), generator=g, device=dev) * 0.02).half().view(torch.int16)
+    wn = torch.ones(512, device=dev)
+    wn_i = torch.ones(128, device=dev)
+    w_out = (torch.randn((4096, N_HEAD * HEAD_DIM), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    st_kv = torch.zeros((B, 8, 1024), device=dev)
+    st_sc = torch.full((B, 8, 1024), float("-inf"), device=dev)
+    sti_kv = torch.zeros((B, 8, 256), device=dev)
+    sti_sc = torch.full((B, 8, 256), float("-inf"), device=dev)
+    emit = torch.empty((B, 512), device=dev)
+    emit_i = torch.empty((B, 128), device=dev)
+    scratch = torch.empty(2 * B * 1024, device=dev)
+    x = torch.randn((B, IN), generator=g, device=dev)
+    kv_cur = torch.randn((B, HEAD_DIM), generator=g, device=dev)
+    q = torch.randn((B, N_HEAD, HEAD_DIM), generator=g, device=dev).to(torch.bfloat16)
+    q_idx = torch.randn((B, N_HEAD, 128), generator=g, device=dev)
+    w_idx = torch.randn((B, N_HEAD), generator=g, device=dev) / float(np.sqrt(128 * N_HEAD))
+    sinks = torch.randn((B, N_HEAD), generator=g, device=dev)
+    pos = (ctx - 1).astype(np.int32)                  # the token being decoded
+    pos_dev = torch.from_numpy(pos).to(dev)
+    scores = torch.empty(int(n_comp.sum()), device=dev)
+    out = torch.empty((B, N_HEAD, HEAD_DIM), device=dev)
+    y = torch.empty((B, 4096), device=dev)
+    # raw-row destinations (window slot pos % 128); emitted compressed rows go
+    # to the next compressed slot of their sequence
+    emits = [(pos[b] + 1) % 4 == 0 for b in range(B)]
+    dst_raw = torch.tensor([phys(b, cmax + int(pos[b]) % SWA) for b in range(B)],
+                           dtype=torch.int64, device=dev)
+    dst_emit = torch.tensor([phys(b, min(int(n_comp[b]), cmax - 1)) if emits[b] else trash
+                             for b in range(B)], dtype=torch.int64, device=dev)
+
+    def step():
+        ops.compressor_decode_step_batch_w32(True, x, w_kv, w_gate, ape, wn, IN, 512, 4, pos,
+                                             pos_dev, 2, st_kv, st_sc, 8 * 1024, emit, scratch,
+                                             stream=stream)
+        ops.compressor_decode_step_batch_w32(False, x, wi_kv, wi_gate, ape_i, wn_i, IN, 128, 4,
+                                             pos, pos_dev, 2, sti_kv, sti_sc, 8 * 256, emit_i,
+                                             scratch, stream=stream)
+        cache.append(kv_cur, dst_rows=dst_raw, stream=stream)
+        cache.append(emit, dst_rows=dst_emit, stream=stream)
+        ops.indexer_topk_positions_batch(q_idx, w_idx, keys, key_row0, n_comp, TOPK, 0, scores,
+                                         rowlist, pos_offset=SWA, stream=stream)
+        ops.flash_attn_decode_fp8(q, sinks, out, cache, counts, row_idx=rowlist,
+                                  page_table=page_table, page_rows=PAGE, workspace=ws,
+                                  stream=stream)
+        ops.tail_rope_yarn_batch_f32(out, out, B, N_HEAD, HEAD_DIM, 64, pos_dev, 2, inverse=True,
+                                     stream=stream)
+        ops.mul_mm_bf16_f32(w_out, out, y, 4096, N_HEAD * HEAD_DIM, B, stream=stream)
+
+    ms = time_ms(step, steps, 3, stream)
+    sel = [min(int(n), TOPK) for n in n_comp]
+    b = (w_out.numel() * 2 + (w_kv.numel() + w_gate.numel() + wi_kv.numel() + wi_gate.numel()) * 4
+         + int(sum(n_comp[i] * 512 for i in range(B) if n_comp[i] > TOPK))
+         + sum((SWA + s) * ROW_BYTES for s in sel) + B * (IN * 4 + N_HEAD * HEAD_DIM * (2 + 4 + 4)
+                                                         + 4096 * 4))
+    return {"workload": "batched-decode attention block, one layer: 16 sequences, ctx ~U[1024,16384] "
+                        "(seed 5), compressor ratio 4 (fp32 W), FP8 append into 256-row pages, "
+                        "top-2048 selection, decode, inverse RoPE, bf16 attn_out 32768->4096 "
+                        "(BASELINE configs[4])",
+            "us_per_step_layer": round(ms * 1e3, 2), "bytes": b,
+            "gbs": round(b / (ms * 1e-3) / 1e9, 1),
+            "frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "contexts": [int(c) for c in ctx]}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -249,9 +359,10 @@ def main():
                      "kernel_ms": round(k_ms, 4), "bytes_per_launch": step_bytes},
     }
     if not args.no_secondary:
-        log("secondary configs: chunked prefill, sparse decode")
+        log("secondary configs: chunked prefill, sparse decode, batched block")
         res["secondary"] = {"prefill": bench_prefill(dev, stream, max(3, args.steps // 10)),
-                            "sparse_decode": bench_sparse(dev, stream, args.steps)}
+                            "sparse_decode": bench_sparse(dev, stream, args.steps),
+                            "batched_block": bench_batch(dev, stream, args.steps)}
     if not args.no_cpu_baseline:
         log("timing the CPU baseline (oracle) on one layer")
         res["cpu_baseline"] = cpu_baseline()

@@ -322,8 +322,6 @@ extern "C" int ds4hip_compressor_decode_step_w32(int is_attn, const float *x_f32
         nullptr, nullptr, (hipStream_t)stream));
 }
 
-int ds4hip_mm_f32(const float *W, const float *X, float *Y, int n_rows, int n_cols, int n_batch,
-                  hipStream_t st);
 
 extern "C" int ds4hip_compressor_decode_step_batch_w32(
         int is_attn, int n_seq, const float *x_f32, const float *w_kv_f32,
@@ -334,7 +332,7 @@ extern "C" int ds4hip_compressor_decode_step_batch_w32(
     const int ratio = compress_ratio;
     if (n_seq <= 0 || n_seq > 16 || !x_f32 || !w_kv_f32 || !w_gate_f32 || !w_ape_f16 ||
         !w_norm_f32 || !pos_host || !pos_dev || !state_kv || !state_score || !emit_out ||
-        !scratch || in_dim <= 0 || (in_dim % 16) || head_dim_out <= kNRot || head_dim_out > 512 ||
+        !scratch || in_dim <= 0 || (in_dim % 32) || head_dim_out <= kNRot || head_dim_out > 512 ||
         (head_dim_out % 64) || (ratio != 4 && ratio != 128))
         return ds4hip_set_last_error(kEINVAL);
     const int coff = ratio == 4 ? 2 : 1;
@@ -348,9 +346,10 @@ extern "C" int ds4hip_compressor_decode_step_batch_w32(
         any |= e;
     }
     const hipStream_t st = (hipStream_t)stream;
-    int rc = ds4hip_mm_f32(w_kv_f32, x_f32, scratch, width, in_dim, n_seq, st);
-    if (!rc) rc = ds4hip_mm_f32(w_gate_f32, x_f32, scratch + (size_t)n_seq * width, width, in_dim,
-                                n_seq, st);
+    int rc = ds4hip_zero_f32(scratch, (size_t)2 * n_seq * width, st);
+    if (!rc)
+        rc = ds4hip_mm_f32(w_kv_f32, x_f32, scratch, width, in_dim, n_seq, st, false, w_gate_f32,
+                           scratch + (size_t)n_seq * width);
     if (rc) return ds4hip_set_last_error(rc);
     hipLaunchKernelGGL(comp_batch_update_kernel, dim3((width + 255) / 256, n_seq), dim3(256), 0,
                        st, scratch, w_ape_f16, pos_dev, n_seq, width, ratio, state_kv,

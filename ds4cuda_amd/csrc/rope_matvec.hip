@@ -253,102 +253,171 @@ __global__ __launch_bounds__(256) void zero_kernel(float *__restrict__ y, size_t
         y[i] = 0.0f;
 }
 
-__global__ __launch_bounds__(256) void mm_bf16_kernel(const uint16_t *__restrict__ W,
-                                                      const float *__restrict__ X,
-                                                      float *__restrict__ Y, int n_rows,
-                                                      int n_cols, int n_batch) {
-    __shared__ uint16_t xh[16 * kMmCols];
-    __shared__ uint16_t xl[16 * kMmCols];
-    const int c0 = blockIdx.y * kMmCols;
-    const int nc = min(kMmCols, n_cols - c0);
-    for (int idx = threadIdx.x; idx < 16 * nc; idx += 256) {
-        const int b = idx / nc, c = idx % nc;
-        const float v = b < n_batch ? X[(size_t)b * n_cols + c0 + c] : 0.0f;
-        const uint16_t hi = f32_to_bf16_rne(v);
-        xh[b * kMmCols + c] = hi;
-        xl[b * kMmCols + c] = f32_to_bf16_rne(v - bf16_to_f32(hi));
-    }
-    __syncthreads();
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int r0 = (blockIdx.x * 4 + wave) * 16;
-    if (r0 >= n_rows) return;
-    const int i = lane & 15, q = lane >> 4;
-    const int row = min(r0 + i, n_rows - 1);
-    const uint16_t *wr = W + (size_t)row * n_cols + c0;
-    float4_t acc = float4_t{0, 0, 0, 0};
-    for (int k = 0; k < nc; k += 32) {
-        const bf16x8_t a = *reinterpret_cast<const bf16x8_t *>(wr + k + 8 * q);
-        const bf16x8_t bh = *reinterpret_cast<const bf16x8_t *>(&xh[i * kMmCols + k + 8 * q]);
-        const bf16x8_t bl = *reinterpret_cast<const bf16x8_t *>(&xl[i * kMmCols + k + 8 * q]);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bh, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bl, acc, 0, 0, 0);
-    }
-    // D[row 4q+r][batch i]
+// Batched projection Y[b][r] = sum_c W[r][c] X[b][c] for n_batch <= 16,
+// streamed: weight-bandwidth bound, every weight is read once. One wave owns
+// 64 rows (4 MFMA row tiles) and a k-range of kslice columns; lane (i, q)
+// loads 8 consecutive columns of W row 16t+i and of X row i per 32-column
+// step, so the four row tiles share one B fragment. bf16 W: X is split into
+// bf16 hi + lo on the fly and multiplied with v_mfma_f32_16x16x32_bf16 twice
+// (~16 bits of X kept); fp32 W: v_mfma_f32_16x16x4f32 on the exact fp32 values,
+// element j of the 8 columns feeding MFMA step j. k-ranges add into Y with
+// atomics (Y zeroed first).
+template <bool kF32W>
+struct MmFrag {
+    float4_t xa, xb;           // X[batch i][8 columns]
+    float4_t wa[4], wb[4];     // fp32 W: 8 columns of the 4 rows
+    bf16x8_t w[4];             // bf16 W: 8 columns of the 4 rows
+};
+
+template <bool kF32W>
+__device__ inline void mm_load(MmFrag<kF32W> &f, const void *Wv, const float *xr,
+                               const size_t *roff, int k) {
+    f.xa = *reinterpret_cast<const float4_t *>(xr + k);
+    f.xb = *reinterpret_cast<const float4_t *>(xr + k + 4);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int rr = r0 + 4 * q + r;
-        if (rr < n_rows && i < n_batch) atomicAdd(&Y[(size_t)i * n_rows + rr], acc[r]);
+    for (int t = 0; t < 4; ++t) {
+        if (kF32W) {
+            const float *W = static_cast<const float *>(Wv) + roff[t] + k;
+            f.wa[t] = *reinterpret_cast<const float4_t *>(W);
+            f.wb[t] = *reinterpret_cast<const float4_t *>(W + 4);
+        } else {
+            f.w[t] = *reinterpret_cast<const bf16x8_t *>(static_cast<const uint16_t *>(Wv) +
+                                                         roff[t] + k);
+        }
     }
 }
 
-// fp32 weights: v_mfma_f32_16x16x4_f32 (exact fp32 products). One wave owns
-// 16 rows and a column slice of kMmF32Cols; lane (i, k) loads W[row i][c+4k ..
-// c+4k+3] and X[batch i][same] as float4 and feeds element j to MFMA step j,
-// so A and B agree on the reduction index. Column slices add into Y with
-// atomics (Y zeroed first).
-constexpr int kMmF32Cols = 512;
+template <bool kF32W>
+__device__ inline void mm_compute(const MmFrag<kF32W> &f, bool bok, float4_t *acc) {
+    const float4_t xa = bok ? f.xa : float4_t{0, 0, 0, 0};
+    const float4_t xb = bok ? f.xb : float4_t{0, 0, 0, 0};
+    if (kF32W) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(f.wa[t][j], xa[j], acc[t], 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(f.wb[t][j], xb[j], acc[t], 0, 0, 0);
+        }
+    } else {
+        bf16x8_t xh, xl;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float v = e < 4 ? xa[e] : xb[e - 4];
+            const uint16_t h = f32_to_bf16_rne(v);
+            xh[e] = (short)h;
+            xl[e] = (short)f32_to_bf16_rne(v - bf16_to_f32(h));
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.w[t], xh, acc[t], 0, 0, 0);
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.w[t], xl, acc[t], 0, 0, 0);
+        }
+    }
+}
 
-__global__ __launch_bounds__(256) void mm_f32_kernel(const float *__restrict__ W,
-                                                     const float *__restrict__ X,
-                                                     float *__restrict__ Y, int n_rows,
-                                                     int n_cols, int n_batch) {
+// grid.z selects one of two (W, Y) pairs with the same shape and X.
+template <bool kF32W>
+__global__ __launch_bounds__(256) void mm_stream_kernel(const void *__restrict__ Wv0,
+                                                        const void *__restrict__ Wv1,
+                                                        const float *__restrict__ X,
+                                                        float *__restrict__ Y0,
+                                                        float *__restrict__ Y1, int n_rows,
+                                                        int n_cols, int n_batch, int kslice) {
+    constexpr int kDepth = 4;   // 32-column steps in flight
+    const void *Wv = blockIdx.z ? Wv1 : Wv0;
+    float *Y = blockIdx.z ? Y1 : Y0;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int r0 = (blockIdx.x * 4 + wave) * 16;
+    const int r0 = (blockIdx.x * 4 + wave) * 64;
     if (r0 >= n_rows) return;
-    const int i = lane & 15, k = lane >> 4;
-    const int c0 = blockIdx.y * kMmF32Cols;
-    const int c1 = min(c0 + kMmF32Cols, n_cols);
-    const int row = min(r0 + i, n_rows - 1);
-    const float *wr = W + (size_t)row * n_cols;
+    const int i = lane & 15, q = lane >> 4;
+    const int k0 = blockIdx.y * kslice;
+    const int k1 = min(k0 + kslice, n_cols);
     const bool bok = i < n_batch;
-    const float *xr = X + (size_t)(bok ? i : 0) * n_cols;
-    float4_t acc = float4_t{0, 0, 0, 0};
-    for (int c = c0 + 4 * k; c < c1; c += 16) {
-        const float4_t a = *reinterpret_cast<const float4_t *>(wr + c);
-        float4_t b = *reinterpret_cast<const float4_t *>(xr + c);
-        if (!bok) b = float4_t{0, 0, 0, 0};
+    const float *xr = X + (size_t)(bok ? i : 0) * n_cols + 8 * q;
+    size_t roff[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j], b[j], acc, 0, 0, 0);
-    }
-    // D[row 4k+r][batch i]
+    for (int t = 0; t < 4; ++t) roff[t] = (size_t)min(r0 + 16 * t + i, n_rows - 1) * n_cols + 8 * q;
+    float4_t acc[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int rr = r0 + 4 * k + r;
-        if (rr < n_rows && bok) atomicAdd(&Y[(size_t)i * n_rows + rr], acc[r]);
+    for (int t = 0; t < 4; ++t) acc[t] = float4_t{0, 0, 0, 0};
+    // steps past k1 re-read the last step (never used)
+    auto clampk = [&](int k) { return k < k1 ? k : k1 - 32; };
+    MmFrag<kF32W> f[kDepth];
+#pragma unroll
+    for (int u = 0; u < kDepth; ++u) mm_load(f[u], Wv, xr, roff, clampk(k0 + 32 * u));
+    for (int k = k0; k < k1; k += 32 * kDepth) {
+#pragma unroll
+        for (int u = 0; u < kDepth; ++u) {
+            // past k1 the fragment is a re-read of the last step: X is zeroed
+            // instead of branching, so the load pipeline never drains
+            mm_compute(f[u], bok && k + 32 * u < k1, acc);
+            mm_load(f[u], Wv, xr, roff, clampk(k + 32 * (u + kDepth)));
+        }
     }
+    // D[row 4q+r of tile t][batch i]
+    if (!bok) return;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int rr = r0 + 16 * t + 4 * q + r;
+            if (rr < n_rows) atomicAdd(&Y[(size_t)i * n_rows + rr], acc[t][r]);
+        }
+}
+
+// k-slice so that the launch has about 2048 waves (two per SIMD; a multiple
+// of 128 columns).
+int mm_kslice(int n_rows, int n_cols, int n_mats) {
+    const long long groups = (long long)n_mats * ((n_rows + 63) / 64);
+    long long ks = (long long)n_cols * groups / 2048;
+    ks = ((ks + 127) / 128) * 128;
+    if (ks < 128) ks = 128;
+    if (ks > n_cols) ks = ((n_cols + 31) / 32) * 32;
+    return (int)ks;
+}
+
+template <bool kF32W>
+int mm_launch(const void *W, const float *X, float *Y, int n_rows, int n_cols, int n_batch,
+              bool zero, hipStream_t st, const void *W2 = nullptr, float *Y2 = nullptr) {
+    const int n_mats = W2 ? 2 : 1;
+    if (zero) {
+        const size_t ny = (size_t)n_batch * n_rows;
+        hipLaunchKernelGGL(zero_kernel, dim3((unsigned)std::min<size_t>((ny + 255) / 256, 1024)),
+                           dim3(256), 0, st, Y, ny);
+        if (Y2)
+            hipLaunchKernelGGL(zero_kernel, dim3((unsigned)std::min<size_t>((ny + 255) / 256, 1024)),
+                               dim3(256), 0, st, Y2, ny);
+    }
+    const int ks = mm_kslice(n_rows, n_cols, n_mats);
+    const dim3 grid((n_rows + 255) / 256, (n_cols + ks - 1) / ks, n_mats);
+    hipLaunchKernelGGL(mm_stream_kernel<kF32W>, grid, dim3(256), 0, st, W, W2 ? W2 : W, X, Y,
+                       Y2 ? Y2 : Y, n_rows, n_cols, n_batch, ks);
+    return hip_status(hipGetLastError());
 }
 
 }  // namespace
 
 int ds4hip_mm_f32(const float *W, const float *X, float *Y, int n_rows, int n_cols, int n_batch,
-                  hipStream_t st) {
-    if (!W || !X || !Y || n_rows <= 0 || n_cols <= 0 || n_cols % 16 || n_batch <= 0 ||
-        n_batch > 16)
+                  hipStream_t st, bool zero, const float *W2, float *Y2) {
+    if (!W || !X || !Y || n_rows <= 0 || n_cols <= 0 || n_cols % 32 || n_batch <= 0 ||
+        n_batch > 16 || (!W2 != !Y2))
         return kEINVAL;
-    const size_t ny = (size_t)n_batch * n_rows;
-    hipLaunchKernelGGL(zero_kernel, dim3((unsigned)std::min<size_t>((ny + 255) / 256, 1024)),
-                       dim3(256), 0, st, Y, ny);
-    const dim3 grid((n_rows + 63) / 64, (n_cols + kMmF32Cols - 1) / kMmF32Cols);
-    hipLaunchKernelGGL(mm_f32_kernel, grid, dim3(256), 0, st, W, X, Y, n_rows, n_cols, n_batch);
+    return mm_launch<true>(W, X, Y, n_rows, n_cols, n_batch, zero, st, W2, Y2);
+}
+
+int ds4hip_zero_f32(float *y, size_t n, hipStream_t st) {
+    hipLaunchKernelGGL(zero_kernel, dim3((unsigned)std::min<size_t>((n + 255) / 256, 1024)),
+                       dim3(256), 0, st, y, n);
     return hip_status(hipGetLastError());
 }
 
 extern "C" int ds4hip_mul_mm_f32_f32(const float *W, const float *X, float *Y, int n_rows,
                                      int n_cols, int n_batch, void *stream) {
     return ds4hip_set_last_error(ds4hip_mm_f32(W, X, Y, n_rows, n_cols, n_batch,
-                                               (hipStream_t)stream));
+                                               (hipStream_t)stream, true));
 }
 
 extern "C" int ds4hip_tail_rope_yarn_batch_f32(const float *x_in, float *x_out, int n_seq,
@@ -431,11 +500,6 @@ extern "C" int ds4hip_mul_mm_bf16_f32(const uint16_t *W, const float *X, float *
     if (!W || !X || !Y || n_rows <= 0 || n_cols <= 0 || n_cols % 32 || n_batch <= 0 ||
         n_batch > 16)
         return ds4hip_set_last_error(kEINVAL);
-    const hipStream_t st = (hipStream_t)stream;
-    const size_t ny = (size_t)n_batch * n_rows;
-    hipLaunchKernelGGL(zero_kernel, dim3((unsigned)std::min<size_t>((ny + 255) / 256, 1024)),
-                       dim3(256), 0, st, Y, ny);
-    const dim3 grid((n_rows + 63) / 64, (n_cols + kMmCols - 1) / kMmCols);
-    hipLaunchKernelGGL(mm_bf16_kernel, grid, dim3(256), 0, st, W, X, Y, n_rows, n_cols, n_batch);
-    return ds4hip_set_last_error(hip_status(hipGetLastError()));
+    return ds4hip_set_last_error(
+        mm_launch<false>(W, X, Y, n_rows, n_cols, n_batch, true, (hipStream_t)stream));
 }

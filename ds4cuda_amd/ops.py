@@ -337,19 +337,23 @@ def tail_rope_yarn_batch_f32(x_in, x_out, n_seq, n_heads, head_dim, n_rot, pos_d
 
 
 def indexer_topk_positions_batch(q, weights, keys, key_row0, n_comp, top_k, n_recent, scores,
-                                 positions, stream=None):
+                                 positions, pos_offset=0, stream=None):
     """q [n_seq, n_head, 128] fp32, weights [n_seq, n_head], keys [rows, 128]
     (fp32 / f16 / bf16), key_row0 / n_comp host ints per sequence, scores
-    [rows] fp32 scratch, positions [n_seq, stride] int32."""
+    [rows] fp32 scratch, positions [n_seq, stride] int32; sequence s writes at
+    positions[s, pos_offset:]."""
     n_seq = len(n_comp)
     n_head = q.shape[1]
     r0 = (C.c_longlong * n_seq)(*[int(x) for x in key_row0])
     nc = (C.c_int * n_seq)(*[int(x) for x in n_comp])
     _check(positions, torch.int32, n_seq * positions.shape[-1], "positions")
+    stride = positions.shape[-1]
+    if pos_offset + top_k > stride:
+        raise Ds4HipError("positions rows too short", -22)
     call("ds4hip_indexer_topk_positions_batch", _ptr(q), _ptr(weights), _ptr(keys),
          _KEY_KIND[keys.dtype], C.cast(r0, C.c_void_p), C.cast(nc, C.c_void_p), n_seq, n_head,
-         keys.shape[-1], top_k, n_recent, _ptr(scores), _ptr(positions), positions.shape[-1],
-         _stream(stream))
+         keys.shape[-1], top_k, n_recent, _ptr(scores),
+         C.c_void_p(positions.data_ptr() + 4 * pos_offset), stride, _stream(stream))
 
 
 def compressor_decode_step_batch_w32(is_attn, x, w_kv, w_gate, w_ape, w_norm, in_dim,

@@ -182,7 +182,7 @@ int ds4hip_mul_mm_bf16_f32(const uint16_t *W, const float *X, float *Y, int n_ro
 
 /* Batched fp32 projection (additive; the batched-decode compressor
  * projection): Y[b][r] = sum_c W[r][c] X[b][c], W fp32 [n_rows][n_cols],
- * n_batch <= 16, n_cols % 16 == 0. Y is overwritten. */
+ * n_batch <= 16, n_cols % 32 == 0. Y is overwritten. */
 int ds4hip_mul_mm_f32_f32(const float *W, const float *X, float *Y, int n_rows, int n_cols,
                           int n_batch, void *stream);
 

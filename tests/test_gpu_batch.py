@@ -16,7 +16,7 @@ from test_oracle_misc import rope
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("n_rows,n_cols,nb", [(1024, 4096, 16), (256, 4096, 3), (100, 48, 1)])
+@pytest.mark.parametrize("n_rows,n_cols,nb", [(1024, 4096, 16), (256, 4096, 3), (100, 64, 1), (4096, 32768, 16)])
 def test_mul_mm_f32(gpu, n_rows, n_cols, nb):
     W = synth.normal(51, 1, n_rows * n_cols).reshape(n_rows, n_cols) * 0.02
     X = synth.normal(51, 2, nb * n_cols).reshape(nb, n_cols)

@@ -77,6 +77,9 @@ struct DecodeArgs {
     const int32_t *page_table;       // per problem page lists, or null
     int page_table_stride;
     int page_shift;
+    // gathered rows (row_idx or page_table): physical row of every logical
+    // row, resolved by phys_kernel before the partial kernel
+    long long *phys;
     // schedule
     int n_prob;
     int chunk;
@@ -342,6 +345,7 @@ __device__ inline void seg_init(SegState &S) {
 constexpr int kStages = 4;
 constexpr int kStageBytes = 18 * 1024 + 256 + 256;
 constexpr int kSexpOff = 18 * 1024;
+constexpr int kPhysOff = kSexpOff + 256;         // 32 x int64 physical rows (gathered modes)
 constexpr int kCopiesPerWave = 5;
 constexpr int kVRowBytes = 288;                  // 128 dims f16 + 32 B pad (bank spread)
 constexpr int kVTileBytes = kTile * kVRowBytes;  // per wave
@@ -356,13 +360,16 @@ __device__ inline int stage_off(int region, int k, int c) {
     return region * 1024 + 64 * k + 16 * (c ^ ((k >> 1) & 3));
 }
 
-__device__ inline void issue_stage(const DecodeArgs &A, uint8_t *stage, long long ph, int lane,
-                                   int wave) {
-    // ph = physical row of tile row (lane & 31)
+// Issues the 5 copies of this wave for one tile. ph_h0 / ph_h1: physical rows
+// of tile rows lane>>2 and 16 + (lane>>2); ph_e: tile row lane>>1 (exponent
+// copy). The wave-3 spare copy carries, when phys_src != null, the physical
+// rows of the tile kStages ahead of this one (32 x int64 from phys_src,
+// lanes 0..15) into the stage's phys slot; otherwise it repeats the exponent
+// copy so every wave issues the same number of copies.
+__device__ inline void issue_stage(const DecodeArgs &A, uint8_t *stage, long long ph_h0,
+                                   long long ph_h1, long long ph_e, const long long *phys_src,
+                                   int lane, int wave) {
     const int k = lane >> 2;
-    const long long ph_h0 = __shfl(ph, k);          // tile row k
-    const long long ph_h1 = __shfl(ph, 16 + k);     // tile row 16 + k
-    const long long ph_e = __shfl(ph, lane >> 1);   // exponent copy: tile row lane>>1
     const int c = (lane & 3) ^ ((k >> 1) & 3);
 #pragma unroll
     for (int kk = 0; kk < kCopiesPerWave; ++kk) {
@@ -374,9 +381,12 @@ __device__ inline void issue_stage(const DecodeArgs &A, uint8_t *stage, long lon
                 ? A.codes + row * kNope + blk * 64 + c * 16
                 : reinterpret_cast<const uint8_t *>(A.tail) + row * (2 * kRot) + (blk - 7) * 64 + c * 16;
             __builtin_amdgcn_global_load_lds(g, stage + i * 1024, 16, 0, 0);
-        } else {
+        } else if (i == 18 || !phys_src) {
             const uint8_t *g = reinterpret_cast<const uint8_t *>(A.sexp) + ph_e * 8 + (lane & 1) * 4;
-            __builtin_amdgcn_global_load_lds(g, stage + kSexpOff + (i - 18) * 256, 4, 0, 0);
+            __builtin_amdgcn_global_load_lds(g, stage + kSexpOff, 4, 0, 0);
+        } else if (lane < 16) {
+            // 16 lanes x 16 bytes = the 32 int64 rows (one copy, partial exec)
+            __builtin_amdgcn_global_load_lds(phys_src + 2 * lane, stage + kPhysOff, 16, 0, 0);
         }
     }
 }
@@ -399,6 +409,24 @@ __device__ inline void wait_copies(int pending_stages) {
 template <typename T>
 __device__ inline void lds_st128(uint32_t a, T v) {
     asm volatile("ds_write_b128 %0, %1" ::"v"(a), "v"(v) : "memory");
+}
+// Eight 16-byte stores of MFMA results at a + off[i]. The compiler does not
+// insert the wait states that a read of an MFMA destination register needs
+// when the read is inside inline assembly, so the statement starts with them
+// (16, more than the 16x16x32 f16 MFMA needs) and ends with two for the
+// store-data hazard of a following write of those registers.
+template <int O0, int O1, int O2, int O3, int O4, int O5, int O6, int O7>
+__device__ inline void lds_st128x8_mfma(uint32_t a, const float4_t *v) {
+    asm volatile(
+        "s_nop 7\n\ts_nop 7\n\t"
+        "ds_write_b128 %0, %1 offset:%9\n\tds_write_b128 %0, %2 offset:%10\n\t"
+        "ds_write_b128 %0, %3 offset:%11\n\tds_write_b128 %0, %4 offset:%12\n\t"
+        "ds_write_b128 %0, %5 offset:%13\n\tds_write_b128 %0, %6 offset:%14\n\t"
+        "ds_write_b128 %0, %7 offset:%15\n\tds_write_b128 %0, %8 offset:%16\n\t"
+        "s_nop 1"
+        :: "v"(a), "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]), "v"(v[5]), "v"(v[6]),
+           "v"(v[7]), "n"(O0), "n"(O1), "n"(O2), "n"(O3), "n"(O4), "n"(O5), "n"(O6), "n"(O7)
+        : "memory");
 }
 __device__ inline void lds_st32(uint32_t a, float v) {
     asm volatile("ds_write_b32 %0, %1" ::"v"(a), "v"(v) : "memory");
@@ -437,6 +465,19 @@ __device__ inline void lds_ld_alpha_p(uint32_t a, uint32_t b, float4_t *ar, half
 // assembly because the compiler would otherwise make each read wait for all
 // outstanding global->LDS copies; the trailing lgkmcnt wait makes the outputs
 // valid when the statement completes.
+// The three physical rows a lane needs from a phys slot (rows a, 16 + a and b).
+__device__ inline void lds_ld_phys3(uint32_t slot, int a, int b, long long &h0, long long &h1,
+                                    long long &e) {
+    uint2_t x, y, z;
+    asm volatile("ds_read_b64 %0, %3\n\tds_read_b64 %1, %3 offset:128\n\tds_read_b64 %2, %4\n\t"
+                 "s_waitcnt lgkmcnt(0)"
+                 : "=&v"(x), "=&v"(y), "=&v"(z)
+                 : "v"(slot + 8 * a), "v"(slot + 8 * b));
+    h0 = (long long)(((unsigned long long)x[1] << 32) | x[0]);
+    h1 = (long long)(((unsigned long long)y[1] << 32) | y[0]);
+    e = (long long)(((unsigned long long)z[1] << 32) | z[0]);
+}
+
 __device__ inline void read_wave_frag(const uint8_t *st, int wave, int h2, int j, int q,
                                       uint4_t &c0, uint4_t &c1, uint2_t &e) {
     uint32_t a0, a1;
@@ -457,6 +498,39 @@ __device__ inline void read_wave_frag(const uint8_t *st, int wave, int h2, int j
         "s_waitcnt lgkmcnt(0)"
         : "=&v"(c0), "=&v"(c1), "=&v"(e)
         : "v"(a0), "v"(a1), "v"(ae));
+}
+
+// Both half-tiles at once (one LDS round trip): c[h2][0..1] and e[h2] as
+// read_wave_frag; for wave 3, th[h2] is the second tail chunk (f16 chunk
+// 2q+1), otherwise untouched.
+__device__ inline void read_wave_frags(const uint8_t *st, int wave, int j, int q, uint4_t (*c)[2],
+                                       uint2_t *e, uint4_t *th) {
+    const uint32_t ae0 = lds_addr(st) + kSexpOff + j * 8;
+    if (wave < 3) {
+        const uint32_t a0 = lds_addr(st) + stage_off(2 * (2 * wave), j, q);
+        const uint32_t a1 = lds_addr(st) + stage_off(2 * (2 * wave + 1), j, q);
+        // half 1 is the next 1 KB region of each block
+        asm volatile(
+            "ds_read_b128 %0, %6\n\tds_read_b128 %1, %7\n\tds_read_b64 %4, %8\n\t"
+            "ds_read_b128 %2, %6 offset:1024\n\tds_read_b128 %3, %7 offset:1024\n\t"
+            "ds_read_b64 %5, %8 offset:128\n\ts_waitcnt lgkmcnt(0)"
+            : "=&v"(c[0][0]), "=&v"(c[0][1]), "=&v"(c[1][0]), "=&v"(c[1][1]), "=&v"(e[0]),
+              "=&v"(e[1])
+            : "v"(a0), "v"(a1), "v"(ae0));
+    } else {
+        const uint32_t a0 = lds_addr(st) + stage_off(2 * 6, j, q);
+        const uint32_t a1 = lds_addr(st) + stage_off(2 * (7 + (q >> 1)), j, (2 * q) & 3);
+        const uint32_t a2 = lds_addr(st) + stage_off(2 * (7 + (q >> 1)), j, (2 * q + 1) & 3);
+        asm volatile(
+            "ds_read_b128 %0, %8\n\tds_read_b128 %1, %9\n\tds_read_b128 %6, %10\n\t"
+            "ds_read_b64 %4, %11\n\t"
+            "ds_read_b128 %2, %8 offset:1024\n\tds_read_b128 %3, %9 offset:1024\n\t"
+            "ds_read_b128 %7, %10 offset:1024\n\tds_read_b64 %5, %11 offset:128\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(c[0][0]), "=&v"(c[0][1]), "=&v"(c[1][0]), "=&v"(c[1][1]), "=&v"(e[0]),
+              "=&v"(e[1]), "=&v"(th[0]), "=&v"(th[1])
+            : "v"(a0), "v"(a1), "v"(a2), "v"(ae0));
+    }
 }
 
 // Second tail chunk of wave 3 (f16 chunk 2q+1).
@@ -568,10 +642,13 @@ __global__ __launch_bounds__(256) void decode_fp8_kernel(const DecodeArgs A) {
     __shared__ __attribute__((aligned(16))) half8_t pbuf[4][64];        // [head block][lane]
     __shared__ __attribute__((aligned(16))) float alpha_s[kH];
     __shared__ long long s_start[kMaxProb + 1];
+    __shared__ long long s_rowbase[kMaxProb];   // LDS, so the ring loop issues no row loads
+    for (int i = threadIdx.x; i < A.n_prob; i += blockDim.x)
+        s_rowbase[i] = A.row_base ? A.row_base[i] : (long long)i * A.row_base_stride;
     stage_start(A, s_start);
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform (SGPR)
     const int j = lane & 15;
     const int q = lane >> 4;
     const uint32_t vt_base = lds_addr(vtile[wave]);
@@ -587,21 +664,46 @@ __global__ __launch_bounds__(256) void decode_fp8_kernel(const DecodeArgs A) {
         const long long r0 = g0 - s_start[p];
         const long long r1 = seg_end - s_start[p];
         const int n_tiles = (int)((r1 - r0 + kTile - 1) / kTile);
-        const long long seg_base =
-            (A.row_base ? A.row_base[p] : (long long)p * A.row_base_stride);
-        const bool direct = !A.row_idx && !A.page_table;
-        // physical row of tile row (lane & 31); rows past the segment end copy
-        // the segment's first row (finite filler, masked in the softmax)
-        auto lane_phys = [&](int t) {
-            long long r = r0 + (long long)t * kTile + (lane & 31);
-            if (r >= r1) r = r0;
-            return direct ? seg_base + r : phys_row(A, p, r);
+        const long long seg_base = s_rowbase[p];
+        const bool gather = A.phys != nullptr;
+        const int k4 = lane >> 2;
+        // Physical rows of tile t needed by this lane's copies (tile rows k4,
+        // 16 + k4 and lane>>1); rows past the segment end repeat its last
+        // row (finite filler, masked in the softmax). Direct addressing is
+        // pure arithmetic; gathered rows come from the phys array (prologue)
+        // or from the phys slot that rode in with an earlier tile.
+        auto rows_direct = [&](int t, long long &h0, long long &h1, long long &e) {
+            const long long rb2 = r0 + (long long)t * kTile;
+            h0 = seg_base + min(rb2 + k4, r1 - 1);
+            h1 = seg_base + min(rb2 + 16 + k4, r1 - 1);
+            e = seg_base + min(rb2 + (lane >> 1), r1 - 1);
+        };
+        auto phys_src = [&](int t) -> const long long * {
+            if (!gather) return nullptr;
+            long long gb = g0 + (long long)t * kTile;
+            return A.phys + (gb < A.total ? gb : A.total);   // the array has 32 rows of padding
         };
 
         half8_t qh[4][4], ql[kQf32 ? 4 : 1][4];
         load_q_split<kQf32>(A, p, wave, j, q, qh, ql);
-        for (int s = 0; s < kStages - 1 && s < n_tiles; ++s)
-            issue_stage(A, stages[s], lane_phys(s), lane, wave);
+        // rows of the next tile to issue (gathered: read ahead, see below)
+        long long nh0 = 0, nh1 = 0, ne = 0;
+        auto rows_global = [&](int t, long long &h0, long long &h1, long long &e) {
+            const long long gb = g0 + (long long)t * kTile;
+            const long long gl = seg_end - 1;
+            h0 = A.phys[min(gb + k4, gl)];
+            h1 = A.phys[min(gb + 16 + k4, gl)];
+            e = A.phys[min(gb + (lane >> 1), gl)];
+        };
+        for (int s = 0; s < kStages - 1 && s < n_tiles; ++s) {
+            long long h0, h1, e;
+            if (gather)
+                rows_global(s, h0, h1, e);
+            else
+                rows_direct(s, h0, h1, e);
+            issue_stage(A, stages[s], h0, h1, e, phys_src(s + kStages), lane, wave);
+        }
+        if (gather && kStages - 1 < n_tiles) rows_global(kStages - 1, nh0, nh1, ne);
         SplitState S;
         S.m_run = -INFINITY;
         S.l_run = 0.0f;
@@ -615,31 +717,38 @@ __global__ __launch_bounds__(256) void decode_fp8_kernel(const DecodeArgs A) {
         int t = 0;
         while (t < n_tiles) {
         for (; t < n_tiles; ++t) {
-            if (t + kStages - 1 < n_tiles)
-                issue_stage(A, stages[(t + kStages - 1) % kStages], lane_phys(t + kStages - 1),
-                            lane, wave);
+            if (t + kStages - 1 < n_tiles) {
+                // refill the stage tile t-1 used (its readers passed B2 of t-1)
+                if (!gather) rows_direct(t + kStages - 1, nh0, nh1, ne);
+                issue_stage(A, stages[(t + kStages - 1) % kStages], nh0, nh1, ne,
+                            phys_src(t + 2 * kStages - 1), lane, wave);
+            }
             // The fp32-Q variant spills registers; spill stores share the vmcnt
             // counter with the copies, so it waits for the whole ring.
             wait_copies(kQf32 ? 0 : min(kStages - 1, n_tiles - 1 - t));
             lds_barrier();   // B1: tile t landed; last tile's P/alpha/S slots are consumed
 
             const uint8_t *st = stages[t % kStages];
+            // gathered rows of tile t+kStages rode in with tile t; they are read
+            // now, before the next iteration refills any stage
+            if (gather && t + kStages < n_tiles)
+                lds_ld_phys3(lds_addr(st + kPhysOff), k4, lane >> 1, nh0, nh1, ne);
             const long long rb = r0 + (long long)t * kTile;
 
             // ---- 1. partial S^T over this wave's dims; V_w slice to LDS ----------
             float4_t acc[2][4];
+            uint4_t cf[2][2], th[2];
+            uint2_t ef[2];
+            read_wave_frags(st, wave, j, q, cf, ef, th);
 #pragma unroll
             for (int h2 = 0; h2 < 2; ++h2) {
-                uint4_t c0, c1;
-                uint2_t e;
-                read_wave_frag(st, wave, h2, j, q, c0, c1, e);
                 half8_t a[4];
-                dequant16(c0, block_scale(e, 2 * wave), a[0], a[1]);
+                dequant16(cf[h2][0], block_scale(ef[h2], 2 * wave), a[0], a[1]);
                 if (wave < 3) {
-                    dequant16(c1, block_scale(e, 2 * wave + 1), a[2], a[3]);
+                    dequant16(cf[h2][1], block_scale(ef[h2], 2 * wave + 1), a[2], a[3]);
                 } else {
-                    a[2] = __builtin_bit_cast(half8_t, c1);
-                    a[3] = __builtin_bit_cast(half8_t, read_tail_hi(st, h2, j, q));
+                    a[2] = __builtin_bit_cast(half8_t, cf[h2][1]);
+                    a[3] = __builtin_bit_cast(half8_t, th[h2]);
                 }
                 // V_w row 16h2+j, dims 64*bb + 16q .. +15 (bb = 0,1 within the wave)
                 const uint32_t vrow = vt_base + (16 * h2 + j) * kVRowBytes + 32 * q;
@@ -661,11 +770,12 @@ __global__ __launch_bounds__(256) void decode_fp8_kernel(const DecodeArgs A) {
             // ---- 2. reduce-scatter S, softmax of the wave's heads ----------------
             // sx layout: [owner][writer][h2][lane] float4
             const uint32_t sx_base = lds_addr(sx);
-#pragma unroll
-            for (int hb = 0; hb < 4; ++hb)
-#pragma unroll
-                for (int h2 = 0; h2 < 2; ++h2)
-                    lds_st128(sx_base + (((hb * 4 + wave) * 2 + h2) * 64 + lane) * 16, acc[h2][hb]);
+            {
+                const float4_t sv[8] = {acc[0][0], acc[1][0], acc[0][1], acc[1][1],
+                                        acc[0][2], acc[1][2], acc[0][3], acc[1][3]};
+                lds_st128x8_mfma<0, 1024, 8192, 9216, 16384, 17408, 24576, 25600>(
+                    sx_base + ((wave * 2) * 64 + lane) * 16, sv);
+            }
             lds_barrier();   // B2: partials visible
             float4_t part[8];   // [w2*2 + h2]
             lds_ld128x8<0, 1024, 2048, 3072, 4096, 5120, 6144, 7168>(
@@ -765,7 +875,7 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(const DecodeArgs A) {
     stage_start(A, s_start);
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform (SGPR)
     const int j = lane & 15;
     const int q = lane >> 4;
     const int head = wave * 16 + j;
@@ -827,6 +937,324 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(const DecodeArgs A) {
 }
 
 // One block per (problem, head): combine the partials with the sink.
+// ---- head-split FP8 kernel: two independent workgroups per CU --------------------------
+//
+// The rows of a chunk are processed by two workgroups, each for 32 of the 64
+// heads; blocks b and b + 8 form the pair (same XCD, so the second reader of a
+// row finds it in L2). A workgroup needs ~55 KB of LDS and at most 256
+// registers per lane, so two run on every CU and the hardware overlaps one
+// workgroup's MFMA phases with the other's softmax and barriers.
+// Per workgroup the split is the one of decode_fp8_kernel: wave w owns dims
+// [128w, 128w+128) (QK^T partial over its dims, P.V for its dims); the FP8
+// tile comes straight from HBM into registers two tiles ahead (wave w loads
+// only its slice: two 16-byte code or tail chunks and the exponents of rows
+// j and 16 + j), so there is no copy ring and no vmcnt bookkeeping. Waves 0
+// and 1 own the softmax of head tiles 0 and 1 (heads 32hh + 16w + j).
+
+constexpr int kHsHeads = 32;
+
+// One tile's fragments of one wave, loaded straight into registers.
+struct HsTile {
+    uint4_t c[2][2];   // [half][0: codes 128w + 16q, 1: codes 128w + 64 + 16q or tail chunk 2q]
+    uint4_t th[2];     // tail chunk 2q + 1 (used by wave 3)
+    uint2_t e[2];      // exponents of rows j, 16 + j
+};
+
+// Branch-free on purpose: a branch in the tile loop makes the compiler wait
+// for every outstanding load at the join, which empties the prefetch.
+__device__ inline void hs_load(const DecodeArgs &A, int wave, int q, const long long *row,
+                               HsTile &T) {
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) {
+        const long long r = row[h2];
+        const uint8_t *cr = A.codes + r * kNope;
+        const uint8_t *tr = reinterpret_cast<const uint8_t *>(A.tail) + r * (2 * kRot);
+        const uint8_t *p1 = wave < 3 ? cr + 128 * wave + 64 + 16 * q : tr + 32 * q;
+        const uint8_t *p2 = wave < 3 ? p1 : tr + 32 * q + 16;   // waves 0-2: a cache hit, unused
+        T.c[h2][0] = *reinterpret_cast<const uint4_t *>(cr + 128 * wave + 16 * q);
+        T.c[h2][1] = *reinterpret_cast<const uint4_t *>(p1);
+        T.th[h2] = *reinterpret_cast<const uint4_t *>(p2);
+        T.e[h2] = *reinterpret_cast<const uint2_t *>(A.sexp + r * 8);
+    }
+}
+
+template <bool kGather>
+__global__ __launch_bounds__(256, 2) void decode_hs_kernel(const DecodeArgs A) {
+    __shared__ __attribute__((aligned(16))) uint8_t vtile[4][kVTileBytes];
+    __shared__ __attribute__((aligned(16))) float4_t sx[2][4][2][64];   // [head tile][writer][h2][lane]
+    __shared__ __attribute__((aligned(16))) half8_t pbuf[2][64];        // [head tile][lane]
+    __shared__ __attribute__((aligned(16))) float alpha_s[kHsHeads];
+    __shared__ long long s_start[kMaxProb + 1];
+    __shared__ long long s_rowbase[kMaxProb];
+    for (int i = threadIdx.x; i < A.n_prob; i += blockDim.x)
+        s_rowbase[i] = A.row_base ? A.row_base[i] : (long long)i * A.row_base_stride;
+    stage_start(A, s_start);
+
+    const int b = blockIdx.x;
+    const int hh = (b >> 3) & 1;                    // head half
+    const int chunk = ((b >> 4) << 3) | (b & 7);
+    const int n_chunks = (int)((A.total + A.chunk - 1) / A.chunk);
+    if (chunk >= n_chunks) return;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int j = lane & 15;
+    const int q = lane >> 4;
+    const int h0 = kHsHeads * hh;
+    const uint32_t vt_base = lds_addr(vtile[wave]);
+    const uint32_t pbuf_base = lds_addr(pbuf);
+    const uint32_t alpha_base = lds_addr(alpha_s);
+
+    long long g0 = (long long)chunk * A.chunk;
+    const long long g1 = min(g0 + (long long)A.chunk, A.total);
+    int p = 0;
+    int slot_s = 0;
+    while (g0 < g1) {
+        while (s_start[p + 1] <= g0) ++p;
+        const long long seg_end = min(g1, s_start[p + 1]);
+        const long long r0 = g0 - s_start[p];
+        const long long r1 = seg_end - s_start[p];
+        // an even tile count (a trailing tile past the end is fully masked) lets
+        // the loop run two tiles per iteration with static register buffers
+        const int n_tiles = 2 * (int)((r1 - r0 + 2 * kTile - 1) / (2 * kTile));
+        const long long seg_base = s_rowbase[p];
+        // cache rows j and 16 + j of tile t (past the segment end: its last row)
+        auto rows_direct = [&](int t, long long *row) {
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2)
+                row[h2] = seg_base + min(r0 + (long long)t * kTile + 16 * h2 + j, r1 - 1);
+        };
+        auto rows_gather = [&](int t, long long *row) {
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2)
+                row[h2] = A.phys[g0 + min((long long)t * kTile + 16 * h2 + j, r1 - 1 - r0)];
+        };
+
+        // Q^T fragments of this workgroup's heads over the wave's dims
+        half8_t qh[2][4];
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const int d = 64 * (2 * wave + (ks >> 1)) + 16 * q + 8 * (ks & 1);
+                const uint4_t v = *reinterpret_cast<const uint4_t *>(
+                    static_cast<const uint16_t *>(A.q) + (long long)p * A.q_stride +
+                    (long long)(h0 + 16 * hb + j) * kD + d);
+                half8_t h;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    h[2 * i] = (half_t)bf16_to_f32((uint16_t)(v[i] & 0xFFFF));
+                    h[2 * i + 1] = (half_t)bf16_to_f32((uint16_t)(v[i] >> 16));
+                }
+                qh[hb][ks] = h;
+            }
+
+        float m_run = -INFINITY, l_run = 0.0f;      // owners: head h0 + 16w + j
+        float4_t o[2][8];
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int c = 0; c < 8; ++c) o[a][c] = float4_t{0, 0, 0, 0};
+
+        // prologue: tiles 0 and 1 in flight; gathered: rows of tile 2 too. The
+        // scheduling barriers keep the issue order of the loop (Q, tile 0, rows
+        // of tile 2, tile 1), so that its load-count waits stay partial.
+        HsTile T0, T1;
+        long long rw[2], ph0[2] = {0, 0}, ph1[2] = {0, 0};
+        __builtin_amdgcn_sched_barrier(0);
+        if (kGather) {
+            long long rw1[2];
+            rows_gather(0, rw);
+            rows_gather(1, rw1);
+            __builtin_amdgcn_sched_barrier(0);
+            hs_load(A, wave, q, rw, T0);
+            __builtin_amdgcn_sched_barrier(0);
+            rows_gather(2, ph0);
+            __builtin_amdgcn_sched_barrier(0);
+            hs_load(A, wave, q, rw1, T1);
+        } else {
+            rows_direct(0, rw);
+            hs_load(A, wave, q, rw, T0);
+            __builtin_amdgcn_sched_barrier(0);
+            rows_direct(1, rw);
+            hs_load(A, wave, q, rw, T1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+
+        // one tile: cur holds tile t; it is refilled with tile t + 2. Gathered
+        // rows of tile t + 2 are in ph_use; those of t + 3 are fetched into
+        // ph_next first, so that waiting for them later leaves tile t + 2's
+        // loads in flight.
+        auto step = [&](int t, HsTile &cur, long long *ph_use, long long *ph_next) {
+            const long long rb = r0 + (long long)t * kTile;
+            // ---- 1. dequantize tile t, write V_w, prefetch tile t+2, S^T partials ----
+            half8_t a[2][4];
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2) {
+                half8_t d2, d3;
+                dequant16(cur.c[h2][0], block_scale(cur.e[h2], 2 * wave), a[h2][0], a[h2][1]);
+                dequant16(cur.c[h2][1], block_scale(cur.e[h2], 2 * wave + 1), d2, d3);
+                a[h2][2] = wave < 3 ? d2 : __builtin_bit_cast(half8_t, cur.c[h2][1]);
+                a[h2][3] = wave < 3 ? d3 : __builtin_bit_cast(half8_t, cur.th[h2]);
+                const uint32_t vrow = vt_base + (16 * h2 + j) * kVRowBytes + 32 * q;
+                asm volatile("ds_write_b128 %0, %1\n\tds_write_b128 %0, %2 offset:16\n\t"
+                             "ds_write_b128 %0, %3 offset:128\n\tds_write_b128 %0, %4 offset:144"
+                             :: "v"(vrow), "v"(a[h2][0]), "v"(a[h2][1]), "v"(a[h2][2]),
+                                "v"(a[h2][3]) : "memory");
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (kGather) {
+                rows_gather(t + 3, ph_next);
+                __builtin_amdgcn_sched_barrier(0);
+                hs_load(A, wave, q, ph_use, cur);
+            } else {
+                long long rn[2];
+                rows_direct(t + 2, rn);
+                hs_load(A, wave, q, rn, cur);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            float4_t acc[2][2];
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+                for (int hb = 0; hb < 2; ++hb) {
+                    float4_t c = float4_t{0, 0, 0, 0};
+#pragma unroll
+                    for (int ks = 0; ks < 4; ++ks)
+                        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[h2][ks], qh[hb][ks], c, 0, 0, 0);
+                    acc[h2][hb] = c;
+                }
+            // ---- 2. reduce-scatter S to the owners (waves 0, 1), softmax ----
+            // compiler-visible stores: it inserts the MFMA read hazard waits
+#pragma unroll
+            for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+                for (int h2 = 0; h2 < 2; ++h2) sx[hb][wave][h2][lane] = acc[h2][hb];
+            lds_barrier();   // B2: partials visible
+            if (wave < 2) {
+                float4_t part[8];   // [writer * 2 + h2]
+                lds_ld128x8<0, 1024, 2048, 3072, 4096, 5120, 6144, 7168>(
+                    lds_addr(sx) + ((wave * 8) * 64 + lane) * 16, part);
+                float s2[2][4];
+                float tmax = -INFINITY;
+#pragma unroll
+                for (int h2 = 0; h2 < 2; ++h2) {
+                    const float4_t sacc = ((part[h2] + part[2 + h2]) + part[4 + h2]) + part[6 + h2];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const bool ok = rb + 16 * h2 + 4 * q + r < r1;
+                        s2[h2][r] = ok ? sacc[r] * A.kq_log2 : -INFINITY;
+                        tmax = fmaxf(tmax, s2[h2][r]);
+                    }
+                }
+                tmax = xmax_16_32(tmax);
+                // lazy rescale: the reference point moves only when the tile max
+                // exceeds it by more than 8 (log2 units)
+                const bool bump = tmax > m_run + 8.0f;
+                const float m_new = bump ? tmax : m_run;
+                const bool none = m_new == -INFINITY;
+                const float alpha = (bump && m_run != -INFINITY) ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+                half8_t pf;
+                float psum = 0.0f;
+#pragma unroll
+                for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float pv = none ? 0.0f : __builtin_amdgcn_exp2f(s2[h2][r] - m_new);
+                        psum += pv;
+                        pf[4 * h2 + r] = (half_t)pv;
+                    }
+                l_run = l_run * alpha + psum;
+                m_run = m_new;
+                lds_st128(pbuf_base + (wave * 64 + lane) * 16, pf);
+                if (q == 0) lds_st32(alpha_base + (16 * wave + j) * 4, alpha);
+            }
+            lds_barrier();   // B3: P and rescale factors visible
+            // ---- 3. O_w += P . V_w ----
+            float4_t ar[2];
+            half8_t pa[2];
+            asm volatile(
+                "ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:64\n\t"
+                "ds_read_b128 %2, %5\n\tds_read_b128 %3, %5 offset:1024\n\t"
+                "s_waitcnt lgkmcnt(0)"
+                : "=&v"(ar[0]), "=&v"(ar[1]), "=&v"(pa[0]), "=&v"(pa[1])
+                : "v"(alpha_base + 16 * q), "v"(pbuf_base + lane * 16));
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                for (int nb = 0; nb < 8; ++nb) o[mb][nb] *= ar[mb];
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                uint2_t tb[8];
+                const uint32_t ab = vt_base + (4 * q + (j >> 2)) * kVRowBytes + 8 * (j & 3) + 128 * half;
+                asm volatile(
+                    "ds_read_b64_tr_b16 %0, %8\n\tds_read_b64_tr_b16 %1, %8 offset:4608\n\t"
+                    "ds_read_b64_tr_b16 %2, %8 offset:32\n\tds_read_b64_tr_b16 %3, %8 offset:4640\n\t"
+                    "ds_read_b64_tr_b16 %4, %8 offset:64\n\tds_read_b64_tr_b16 %5, %8 offset:4672\n\t"
+                    "ds_read_b64_tr_b16 %6, %8 offset:96\n\tds_read_b64_tr_b16 %7, %8 offset:4704\n\t"
+                    "s_waitcnt lgkmcnt(0)"
+                    : "=&v"(tb[0]), "=&v"(tb[1]), "=&v"(tb[2]), "=&v"(tb[3]), "=&v"(tb[4]),
+                      "=&v"(tb[5]), "=&v"(tb[6]), "=&v"(tb[7])
+                    : "v"(ab));
+#pragma unroll
+                for (int nb = 0; nb < 4; ++nb) {
+                    const half8_t vb = __builtin_bit_cast(
+                        half8_t, uint4_t{tb[2 * nb][0], tb[2 * nb][1], tb[2 * nb + 1][0], tb[2 * nb + 1][1]});
+#pragma unroll
+                    for (int mb = 0; mb < 2; ++mb)
+                        o[mb][4 * half + nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            pa[mb], vb, o[mb][4 * half + nb], 0, 0, 0);
+                }
+            }
+        };
+        for (int t = 0; t < n_tiles; t += 2) {
+            step(t, T0, ph0, ph1);
+            step(t + 1, T1, ph1, ph0);
+        }
+
+        // ---- emit: this workgroup's heads over the wave's dims; m, l by the owners ----
+        {
+            const long long slot = (long long)chunk * A.s_max + slot_s;
+            float *wo = A.ws_o + slot * (kH * kD) + (h0 + 4 * q) * kD + 128 * wave + j;
+            asm volatile("" : "+v"(wo));
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) wo[(16 * mb + r) * kD + 16 * nb] = o[mb][nb][r];
+            if (wave < 2) {
+                const float l = xsum_16_32(l_run);
+                if (q == 0) {
+                    A.ws_ml[slot * 2 * kH + h0 + 16 * wave + j] = m_run;
+                    A.ws_ml[slot * 2 * kH + kH + h0 + 16 * wave + j] = l;
+                }
+            }
+            if (hh == 0 && threadIdx.x == 0) A.ws_prob[slot] = p;
+        }
+        ++slot_s;
+        g0 = seg_end;
+        lds_barrier();   // vtile, sx and pbuf are reused by the next segment
+    }
+    if (hh == 0 && threadIdx.x == 0)
+        for (int s2 = slot_s; s2 < A.s_max; ++s2) A.ws_prob[(long long)chunk * A.s_max + s2] = -1;
+}
+
+// Physical cache row of every logical row of a gathered step (row_idx and/or
+// page table), plus 32 rows of padding that repeat the last row.
+__global__ __launch_bounds__(256) void phys_kernel(const DecodeArgs A) {
+    __shared__ long long s_start[kMaxProb + 1];
+    stage_start(A, s_start);
+    const long long g = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (g >= A.total + kTile) return;
+    const long long gg = g < A.total ? g : A.total - 1;
+    int lo = 0, hi = A.n_prob - 1;     // last problem with start <= gg
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (s_start[mid] <= gg) lo = mid; else hi = mid - 1;
+    }
+    A.phys[g] = phys_row(A, lo, gg - s_start[lo]);
+}
+
 // One workgroup per (problem, head). The partial slots of the problem are
 // spread over the 4 waves (slot i -> wave i % 4), so their loads are
 // independent; each lane covers 8 of the 512 dims. The max over the slots
@@ -933,7 +1361,8 @@ Plan make_plan(const long long *start, int n_prob, int wg_per_cu) {
     }
     pl.s_max = smax;
     const size_t slots = (size_t)std::max(pl.n_wg, 1) * smax;
-    pl.ws_bytes = slots * ((size_t)kH * kD * 4 + 2 * kH * 4) + slots * 4 + 256 * 3;
+    pl.ws_bytes = slots * ((size_t)kH * kD * 4 + 2 * kH * 4) + slots * 4 + 256 * 4 +
+                  (size_t)(total + kTile) * sizeof(long long);
     return pl;
 }
 
@@ -946,6 +1375,8 @@ void carve(DecodeArgs &A, void *ws, const Plan &pl) {
     A.ws_ml = reinterpret_cast<float *>(c);
     c += align(slots * 2 * kH * 4);
     A.ws_prob = reinterpret_cast<int *>(c);
+    c += align(slots * 4);
+    A.phys = reinterpret_cast<long long *>(c);   // used only by gathered steps (reset below)
 }
 
 template <bool kFp8, bool kQf32>
@@ -954,7 +1385,19 @@ int launch(DecodeArgs &A, const Plan &pl, hipStream_t st, int phases = 3) {
     A.s_max = pl.s_max;
     A.kq_log2 = kLog2e / sqrtf((float)kD);
     if ((phases & 1) && pl.n_wg > 0) {
-        if (kFp8)
+        if (kFp8 && A.phys) {
+            const long long n = A.total + kTile;
+            hipLaunchKernelGGL(phys_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, A);
+        }
+        if (kFp8 && !kQf32)
+        {
+            const dim3 grid(16 * ((pl.n_wg + 7) / 8));
+            if (A.phys)
+                hipLaunchKernelGGL(decode_hs_kernel<true>, grid, dim3(256), 0, st, A);
+            else
+                hipLaunchKernelGGL(decode_hs_kernel<false>, grid, dim3(256), 0, st, A);
+        }
+        else if (kFp8)
             hipLaunchKernelGGL(decode_fp8_kernel<kQf32>, dim3(pl.n_wg), dim3(256), 0, st, A);
         else
             hipLaunchKernelGGL(decode_f32_kernel, dim3(pl.n_wg), dim3(256), 0, st, A);
@@ -1024,6 +1467,7 @@ extern "C" int ds4hip_flash_attn_decode_fp8(
     A.n_prob = n_prob;
     A.total = A.start[n_prob];
     carve(A, workspace, pl);
+    if (!row_idx && !page_table) A.phys = nullptr;
     const hipStream_t st = (hipStream_t)stream;
     const int rc = q_is_f32 ? launch<true, true>(A, pl, st, phases)
                             : launch<true, false>(A, pl, st, phases);

@@ -32,6 +32,22 @@ N_LAYERS, N_KV, N_HEAD, HEAD_DIM = 43, 32768, 64, 512
 ROW_BYTES = 584                                   # FP8 cache row: 448 codes + 8 exps + 128 tail
 HBM_PEAK_GBS = 8000.0
 MFMA_PEAK_TFLOPS = 2500.0                          # dense f16 / bf16
+COPY_BYTES = 1 << 30                               # --copy-calibration: 1 GiB read + 1 GiB written
+TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                               "decode_fp8_cfg2_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the partial kernel, from the committed counter
+    summary (FETCH_SIZE + WRITE_SIZE, each scaled by the copy-kernel factor);
+    None when the summary is absent."""
+    try:
+        for line in open(TRAFFIC_PROFILE):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
 
 
 def bytes_per_layer():
@@ -273,6 +289,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the prefill / sparse-decode / batched-block figures")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain device copy of known size (the reference kernel "
+                         "that scales the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         log("bench.py measures the single-GPU path only: the attention path has no "
@@ -283,6 +302,16 @@ def main():
     from ds4cuda_amd import ops
 
     dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        n = COPY_BYTES // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration": {"bytes_read": COPY_BYTES, "bytes_written": COPY_BYTES,
+                                               "launches": 5}}), flush=True)
+        return
     torch.manual_seed(0)
     total_rows = N_LAYERS * N_KV
     log(f"building {N_LAYERS} x {N_KV} FP8 cache ({total_rows * ROW_BYTES / 1e6:.0f} MB)")
@@ -354,8 +383,8 @@ def main():
                    "kv_bytes_per_row": ROW_BYTES, "us_per_layer": round(ms * 1e3 / N_LAYERS, 3),
                    "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "decode_fp8_kernel<bf16 q>",
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "kernel": "decode_hs_kernel<direct rows>",
                      "kernel_ms": round(k_ms, 4), "bytes_per_launch": step_bytes},
     }
     if not args.no_secondary:

@@ -213,6 +213,16 @@ __device__ inline float xsum_16_32(float v) {
     auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
+// Reductions over lanes that differ in bits 3..5 (xor 8 by a DPP row rotate).
+__device__ inline float ror8(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));
+}
+__device__ inline float xmax_8_16_32(float v) {
+    return xmax_16_32(fmaxf(v, ror8(v)));
+}
+__device__ inline float xsum_8_16_32(float v) {
+    return xsum_16_32(v + ror8(v));
+}
 
 // Barrier for this kernel's LDS pipeline: waits for this wave's LDS
 // operations, then s_barrier. Unlike __syncthreads() it does not wait for
@@ -1048,7 +1058,7 @@ __global__ __launch_bounds__(256, 2) void decode_hs_kernel(const DecodeArgs A) {
                 qh[hb][ks] = h;
             }
 
-        float m_run = -INFINITY, l_run = 0.0f;      // owners: head h0 + 16w + j
+        float m_run = -INFINITY, l_run = 0.0f;      // softmax of head h0 + 16(w>>1) + 8(w&1) + lane%8
         float4_t o[2][8];
 #pragma unroll
         for (int a = 0; a < 2; ++a)
@@ -1130,43 +1140,43 @@ __global__ __launch_bounds__(256, 2) void decode_hs_kernel(const DecodeArgs A) {
 #pragma unroll
                 for (int h2 = 0; h2 < 2; ++h2) sx[hb][wave][h2][lane] = acc[h2][hb];
             lds_barrier();   // B2: partials visible
-            if (wave < 2) {
-                float4_t part[8];   // [writer * 2 + h2]
-                lds_ld128x8<0, 1024, 2048, 3072, 4096, 5120, 6144, 7168>(
-                    lds_addr(sx) + ((wave * 8) * 64 + lane) * 16, part);
-                float s2[2][4];
+            {
+                // softmax: wave w owns heads 16 hb + 8 (w & 1) + [0, 8), hb = w >> 1;
+                // lane (jj, kk) holds keys 16 h2 + 4 kq + [0, 4) of head jj
+                const int hb = wave >> 1;
+                const int jj = lane & 7, kk = lane >> 3;
+                const int h2 = kk >> 2, kq = kk & 3;
+                const int src = 8 * (wave & 1) + jj + 16 * kq;
+                const float4_t sacc = ((sx[hb][0][h2][src] + sx[hb][1][h2][src]) + sx[hb][2][h2][src]) +
+                                      sx[hb][3][h2][src];
+                float s4[4];
                 float tmax = -INFINITY;
 #pragma unroll
-                for (int h2 = 0; h2 < 2; ++h2) {
-                    const float4_t sacc = ((part[h2] + part[2 + h2]) + part[4 + h2]) + part[6 + h2];
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const bool ok = rb + 16 * h2 + 4 * q + r < r1;
-                        s2[h2][r] = ok ? sacc[r] * A.kq_log2 : -INFINITY;
-                        tmax = fmaxf(tmax, s2[h2][r]);
-                    }
+                for (int r = 0; r < 4; ++r) {
+                    const bool ok = rb + 16 * h2 + 4 * kq + r < r1;
+                    s4[r] = ok ? sacc[r] * A.kq_log2 : -INFINITY;
+                    tmax = fmaxf(tmax, s4[r]);
                 }
-                tmax = xmax_16_32(tmax);
+                tmax = xmax_8_16_32(tmax);
                 // lazy rescale: the reference point moves only when the tile max
                 // exceeds it by more than 8 (log2 units)
                 const bool bump = tmax > m_run + 8.0f;
                 const float m_new = bump ? tmax : m_run;
                 const bool none = m_new == -INFINITY;
                 const float alpha = (bump && m_run != -INFINITY) ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
-                half8_t pf;
+                half4_t pf;
                 float psum = 0.0f;
 #pragma unroll
-                for (int h2 = 0; h2 < 2; ++h2)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const float pv = none ? 0.0f : __builtin_amdgcn_exp2f(s2[h2][r] - m_new);
-                        psum += pv;
-                        pf[4 * h2 + r] = (half_t)pv;
-                    }
+                for (int r = 0; r < 4; ++r) {
+                    const float pv = none ? 0.0f : __builtin_amdgcn_exp2f(s4[r] - m_new);
+                    psum += pv;
+                    pf[r] = (half_t)pv;
+                }
                 l_run = l_run * alpha + psum;
                 m_run = m_new;
-                lds_st128(pbuf_base + (wave * 64 + lane) * 16, pf);
-                if (q == 0) lds_st32(alpha_base + (16 * wave + j) * 4, alpha);
+                // P^T fragment of head tile hb: lane (head, kq) keys {4kq.., 16+4kq..}
+                reinterpret_cast<uint2_t *>(&pbuf[hb][src])[h2] = __builtin_bit_cast(uint2_t, pf);
+                if (kk == 0) alpha_s[16 * hb + 8 * (wave & 1) + jj] = alpha;
             }
             lds_barrier();   // B3: P and rescale factors visible
             // ---- 3. O_w += P . V_w ----
@@ -1178,10 +1188,16 @@ __global__ __launch_bounds__(256, 2) void decode_hs_kernel(const DecodeArgs A) {
                 "s_waitcnt lgkmcnt(0)"
                 : "=&v"(ar[0]), "=&v"(ar[1]), "=&v"(pa[0]), "=&v"(pa[1])
                 : "v"(alpha_base + 16 * q), "v"(pbuf_base + lane * 16));
+            // rare (the reference point moved): rescale O before adding tile t
+            const bool need = ar[0][0] != 1.0f || ar[0][1] != 1.0f || ar[0][2] != 1.0f ||
+                              ar[0][3] != 1.0f || ar[1][0] != 1.0f || ar[1][1] != 1.0f ||
+                              ar[1][2] != 1.0f || ar[1][3] != 1.0f;
+            if (__any(need)) {
 #pragma unroll
-            for (int mb = 0; mb < 2; ++mb)
+                for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-                for (int nb = 0; nb < 8; ++nb) o[mb][nb] *= ar[mb];
+                    for (int nb = 0; nb < 8; ++nb) o[mb][nb] *= ar[mb];
+            }
 #pragma unroll
             for (int half = 0; half < 2; ++half) {
                 uint2_t tb[8];
@@ -1222,11 +1238,12 @@ __global__ __launch_bounds__(256, 2) void decode_hs_kernel(const DecodeArgs A) {
                 for (int nb = 0; nb < 8; ++nb)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) wo[(16 * mb + r) * kD + 16 * nb] = o[mb][nb][r];
-            if (wave < 2) {
-                const float l = xsum_16_32(l_run);
-                if (q == 0) {
-                    A.ws_ml[slot * 2 * kH + h0 + 16 * wave + j] = m_run;
-                    A.ws_ml[slot * 2 * kH + kH + h0 + 16 * wave + j] = l;
+            {
+                const float l = xsum_8_16_32(l_run);
+                if (lane < 8) {
+                    const int hd = h0 + 16 * (wave >> 1) + 8 * (wave & 1) + lane;
+                    A.ws_ml[slot * 2 * kH + hd] = m_run;
+                    A.ws_ml[slot * 2 * kH + kH + hd] = l;
                 }
             }
             if (hh == 0 && threadIdx.x == 0) A.ws_prob[slot] = p;

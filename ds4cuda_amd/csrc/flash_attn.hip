@@ -946,75 +946,55 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(const DecodeArgs A) {
         for (int s2 = slot_s; s2 < A.s_max; ++s2) A.ws_prob[(long long)blockIdx.x * A.s_max + s2] = -1;
 }
 
-// One block per (problem, head): combine the partials with the sink.
-// ---- head-split FP8 kernel: two independent workgroups per CU --------------------------
+// ---- merged FP8 kernel: one 8-wave workgroup per chunk, all 64 heads -------------------
 //
-// The rows of a chunk are processed by two workgroups, each for 32 of the 64
-// heads; blocks b and b + 8 form the pair (same XCD, so the second reader of a
-// row finds it in L2). A workgroup needs ~55 KB of LDS and at most 256
-// registers per lane, so two run on every CU and the hardware overlaps one
-// workgroup's MFMA phases with the other's softmax and barriers.
-// Per workgroup the split is the one of decode_fp8_kernel: wave w owns dims
-// [128w, 128w+128) (QK^T partial over its dims, P.V for its dims); the FP8
-// tile comes straight from HBM into registers two tiles ahead (wave w loads
-// only its slice: two 16-byte code or tail chunks and the exponents of rows
-// j and 16 + j), so there is no copy ring and no vmcnt bookkeeping. Waves 0
-// and 1 own the softmax of head tiles 0 and 1 (heads 32hh + 16w + j).
+// Wave (d, hh) = (w & 3, w >> 2) loads rows 16 hh + [0, 16) of each 32-row tile
+// for dims [128 d, 128 d + 128) straight into registers two tiles ahead, so
+// every byte of the chunk is read once, by one lane. It dequantizes them,
+// writes them to the f16 V tile of dims d (double-buffered: the two waves of a
+// dim quarter share it) and computes the partial S of its 16 rows for all 64
+// heads over its dims (16 MFMAs). After one barrier each wave owns the softmax
+// of 8 heads (sum of the four dim partials, lazy rescale, P in f16); after a
+// second one wave (d, hh) adds P . V_d for heads [32 hh, 32 hh + 32) over all 32
+// rows. Two waves per SIMD; one workgroup per CU.
 
-constexpr int kHsHeads = 32;
-
-// One tile's fragments of one wave, loaded straight into registers.
-struct HsTile {
-    uint4_t c[2][2];   // [half][0: codes 128w + 16q, 1: codes 128w + 64 + 16q or tail chunk 2q]
-    uint4_t th[2];     // tail chunk 2q + 1 (used by wave 3)
-    uint2_t e[2];      // exponents of rows j, 16 + j
+struct W8Tile {
+    uint4_t c0, c1;   // codes 128d + 16q; codes 128d + 64 + 16q or (d = 3) tail chunk 2q
+    uint4_t th;       // d = 3: tail chunk 2q + 1
+    uint2_t e;        // exponents of the row
 };
 
-// Branch-free on purpose: a branch in the tile loop makes the compiler wait
-// for every outstanding load at the join, which empties the prefetch.
-__device__ inline void hs_load(const DecodeArgs &A, int wave, int q, const long long *row,
-                               HsTile &T) {
-#pragma unroll
-    for (int h2 = 0; h2 < 2; ++h2) {
-        const long long r = row[h2];
-        const uint8_t *cr = A.codes + r * kNope;
-        const uint8_t *tr = reinterpret_cast<const uint8_t *>(A.tail) + r * (2 * kRot);
-        const uint8_t *p1 = wave < 3 ? cr + 128 * wave + 64 + 16 * q : tr + 32 * q;
-        const uint8_t *p2 = wave < 3 ? p1 : tr + 32 * q + 16;   // waves 0-2: a cache hit, unused
-        T.c[h2][0] = *reinterpret_cast<const uint4_t *>(cr + 128 * wave + 16 * q);
-        T.c[h2][1] = *reinterpret_cast<const uint4_t *>(p1);
-        T.th[h2] = *reinterpret_cast<const uint4_t *>(p2);
-        T.e[h2] = *reinterpret_cast<const uint2_t *>(A.sexp + r * 8);
-    }
+__device__ inline void w8_load(const DecodeArgs &A, int d, int q, long long r, W8Tile &T) {
+    const uint8_t *cr = A.codes + r * kNope;
+    const uint8_t *tr = reinterpret_cast<const uint8_t *>(A.tail) + r * (2 * kRot);
+    const uint8_t *p1 = d < 3 ? cr + 128 * d + 64 + 16 * q : tr + 32 * q;
+    T.c0 = *reinterpret_cast<const uint4_t *>(cr + 128 * d + 16 * q);
+    T.c1 = *reinterpret_cast<const uint4_t *>(p1);
+    T.th = d == 3 ? *reinterpret_cast<const uint4_t *>(tr + 32 * q + 16) : uint4_t{0, 0, 0, 0};
+    T.e = *reinterpret_cast<const uint2_t *>(A.sexp + r * 8);
 }
 
 template <bool kGather>
-__global__ __launch_bounds__(256, 2) void decode_hs_kernel(const DecodeArgs A) {
-    __shared__ __attribute__((aligned(16))) uint8_t vtile[4][kVTileBytes];
-    __shared__ __attribute__((aligned(16))) float4_t sx[2][4][2][64];   // [head tile][writer][h2][lane]
-    __shared__ __attribute__((aligned(16))) half8_t pbuf[2][64];        // [head tile][lane]
-    __shared__ __attribute__((aligned(16))) float alpha_s[kHsHeads];
+__global__ __launch_bounds__(512, 1) void decode_w8_kernel(const DecodeArgs A) {
+    __shared__ __attribute__((aligned(16))) uint8_t vtile[2][4][kVTileBytes];   // [buffer][d]
+    __shared__ __attribute__((aligned(16))) float4_t sx[4][4][2][64];   // [head tile][d][row half][lane]
+    __shared__ __attribute__((aligned(16))) half8_t pbuf[4][64];        // [head tile][lane]
+    __shared__ __attribute__((aligned(16))) float alpha_s[kH];
     __shared__ long long s_start[kMaxProb + 1];
     __shared__ long long s_rowbase[kMaxProb];
     for (int i = threadIdx.x; i < A.n_prob; i += blockDim.x)
         s_rowbase[i] = A.row_base ? A.row_base[i] : (long long)i * A.row_base_stride;
     stage_start(A, s_start);
 
-    const int b = blockIdx.x;
-    const int hh = (b >> 3) & 1;                    // head half
-    const int chunk = ((b >> 4) << 3) | (b & 7);
-    const int n_chunks = (int)((A.total + A.chunk - 1) / A.chunk);
-    if (chunk >= n_chunks) return;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int d = wave & 3, hh = wave >> 2;
     const int j = lane & 15;
     const int q = lane >> 4;
-    const int h0 = kHsHeads * hh;
-    const uint32_t vt_base = lds_addr(vtile[wave]);
     const uint32_t pbuf_base = lds_addr(pbuf);
     const uint32_t alpha_base = lds_addr(alpha_s);
 
-    long long g0 = (long long)chunk * A.chunk;
+    long long g0 = (long long)blockIdx.x * A.chunk;
     const long long g1 = min(g0 + (long long)A.chunk, A.total);
     int p = 0;
     int slot_s = 0;
@@ -1023,32 +1003,27 @@ __global__ __launch_bounds__(256, 2) void decode_hs_kernel(const DecodeArgs A) {
         const long long seg_end = min(g1, s_start[p + 1]);
         const long long r0 = g0 - s_start[p];
         const long long r1 = seg_end - s_start[p];
-        // an even tile count (a trailing tile past the end is fully masked) lets
-        // the loop run two tiles per iteration with static register buffers
+        // even tile count: a trailing tile past the end is fully masked
         const int n_tiles = 2 * (int)((r1 - r0 + 2 * kTile - 1) / (2 * kTile));
         const long long seg_base = s_rowbase[p];
-        // cache rows j and 16 + j of tile t (past the segment end: its last row)
-        auto rows_direct = [&](int t, long long *row) {
-#pragma unroll
-            for (int h2 = 0; h2 < 2; ++h2)
-                row[h2] = seg_base + min(r0 + (long long)t * kTile + 16 * h2 + j, r1 - 1);
+        // this lane's cache row of tile t (past the segment end: its last row)
+        auto row_direct = [&](int t) -> long long {
+            return seg_base + min(r0 + (long long)t * kTile + 16 * hh + j, r1 - 1);
         };
-        auto rows_gather = [&](int t, long long *row) {
-#pragma unroll
-            for (int h2 = 0; h2 < 2; ++h2)
-                row[h2] = A.phys[g0 + min((long long)t * kTile + 16 * h2 + j, r1 - 1 - r0)];
+        auto row_gather = [&](int t) -> long long {
+            return A.phys[g0 + min((long long)t * kTile + 16 * hh + j, r1 - 1 - r0)];
         };
 
-        // Q^T fragments of this workgroup's heads over the wave's dims
-        half8_t qh[2][4];
+        // Q^T fragments of all 64 heads over dims d
+        half8_t qh[4][4];
 #pragma unroll
-        for (int hb = 0; hb < 2; ++hb)
+        for (int hb = 0; hb < 4; ++hb)
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
-                const int d = 64 * (2 * wave + (ks >> 1)) + 16 * q + 8 * (ks & 1);
+                const int dd = 64 * (2 * d + (ks >> 1)) + 16 * q + 8 * (ks & 1);
                 const uint4_t v = *reinterpret_cast<const uint4_t *>(
                     static_cast<const uint16_t *>(A.q) + (long long)p * A.q_stride +
-                    (long long)(h0 + 16 * hb + j) * kD + d);
+                    (long long)(16 * hb + j) * kD + dd);
                 half8_t h;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -1058,91 +1033,69 @@ __global__ __launch_bounds__(256, 2) void decode_hs_kernel(const DecodeArgs A) {
                 qh[hb][ks] = h;
             }
 
-        float m_run = -INFINITY, l_run = 0.0f;      // softmax of head h0 + 16(w>>1) + 8(w&1) + lane%8
-        float4_t o[2][8];
+        float m_run = -INFINITY, l_run = 0.0f;      // softmax of head 8 wave + lane % 8
+        float4_t o[2][8];                           // heads 32 hh + 16 mb + .., dims 128 d + 16 nb + ..
 #pragma unroll
         for (int a = 0; a < 2; ++a)
 #pragma unroll
             for (int c = 0; c < 8; ++c) o[a][c] = float4_t{0, 0, 0, 0};
 
-        // prologue: tiles 0 and 1 in flight; gathered: rows of tile 2 too. The
-        // scheduling barriers keep the issue order of the loop (Q, tile 0, rows
-        // of tile 2, tile 1), so that its load-count waits stay partial.
-        HsTile T0, T1;
-        long long rw[2], ph0[2] = {0, 0}, ph1[2] = {0, 0};
+        // prologue (issue order = the loop's: tile 0, [rows of tile 2], tile 1)
+        W8Tile T0, T1;
+        long long ph0 = 0, ph1 = 0;
         __builtin_amdgcn_sched_barrier(0);
         if (kGather) {
-            long long rw1[2];
-            rows_gather(0, rw);
-            rows_gather(1, rw1);
+            const long long ra = row_gather(0), rb1 = row_gather(1);
             __builtin_amdgcn_sched_barrier(0);
-            hs_load(A, wave, q, rw, T0);
+            w8_load(A, d, q, ra, T0);
             __builtin_amdgcn_sched_barrier(0);
-            rows_gather(2, ph0);
+            ph0 = row_gather(2);
             __builtin_amdgcn_sched_barrier(0);
-            hs_load(A, wave, q, rw1, T1);
+            w8_load(A, d, q, rb1, T1);
         } else {
-            rows_direct(0, rw);
-            hs_load(A, wave, q, rw, T0);
+            w8_load(A, d, q, row_direct(0), T0);
             __builtin_amdgcn_sched_barrier(0);
-            rows_direct(1, rw);
-            hs_load(A, wave, q, rw, T1);
+            w8_load(A, d, q, row_direct(1), T1);
         }
         __builtin_amdgcn_sched_barrier(0);
 
-        // one tile: cur holds tile t; it is refilled with tile t + 2. Gathered
-        // rows of tile t + 2 are in ph_use; those of t + 3 are fetched into
-        // ph_next first, so that waiting for them later leaves tile t + 2's
-        // loads in flight.
-        auto step = [&](int t, HsTile &cur, long long *ph_use, long long *ph_next) {
+        auto step = [&](int t, W8Tile &cur, long long &ph_use, long long &ph_next, int buf) {
             const long long rb = r0 + (long long)t * kTile;
-            // ---- 1. dequantize tile t, write V_w, prefetch tile t+2, S^T partials ----
-            half8_t a[2][4];
-#pragma unroll
-            for (int h2 = 0; h2 < 2; ++h2) {
+            const uint32_t vt = lds_addr(vtile[buf][d]);
+            // ---- 1. dequantize, write V_d rows, prefetch tile t+2, partial S ----
+            half8_t a[4];
+            {
                 half8_t d2, d3;
-                dequant16(cur.c[h2][0], block_scale(cur.e[h2], 2 * wave), a[h2][0], a[h2][1]);
-                dequant16(cur.c[h2][1], block_scale(cur.e[h2], 2 * wave + 1), d2, d3);
-                a[h2][2] = wave < 3 ? d2 : __builtin_bit_cast(half8_t, cur.c[h2][1]);
-                a[h2][3] = wave < 3 ? d3 : __builtin_bit_cast(half8_t, cur.th[h2]);
-                const uint32_t vrow = vt_base + (16 * h2 + j) * kVRowBytes + 32 * q;
+                dequant16(cur.c0, block_scale(cur.e, 2 * d), a[0], a[1]);
+                dequant16(cur.c1, block_scale(cur.e, 2 * d + 1), d2, d3);
+                a[2] = d < 3 ? d2 : __builtin_bit_cast(half8_t, cur.c1);
+                a[3] = d < 3 ? d3 : __builtin_bit_cast(half8_t, cur.th);
+                const uint32_t vrow = vt + (16 * hh + j) * kVRowBytes + 32 * q;
                 asm volatile("ds_write_b128 %0, %1\n\tds_write_b128 %0, %2 offset:16\n\t"
                              "ds_write_b128 %0, %3 offset:128\n\tds_write_b128 %0, %4 offset:144"
-                             :: "v"(vrow), "v"(a[h2][0]), "v"(a[h2][1]), "v"(a[h2][2]),
-                                "v"(a[h2][3]) : "memory");
+                             :: "v"(vrow), "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]) : "memory");
             }
             __builtin_amdgcn_sched_barrier(0);
             if (kGather) {
-                rows_gather(t + 3, ph_next);
+                ph_next = row_gather(t + 3);
                 __builtin_amdgcn_sched_barrier(0);
-                hs_load(A, wave, q, ph_use, cur);
+                w8_load(A, d, q, ph_use, cur);
             } else {
-                long long rn[2];
-                rows_direct(t + 2, rn);
-                hs_load(A, wave, q, rn, cur);
+                w8_load(A, d, q, row_direct(t + 2), cur);
             }
             __builtin_amdgcn_sched_barrier(0);
-            float4_t acc[2][2];
 #pragma unroll
-            for (int h2 = 0; h2 < 2; ++h2)
+            for (int hb = 0; hb < 4; ++hb) {
+                float4_t c = float4_t{0, 0, 0, 0};
 #pragma unroll
-                for (int hb = 0; hb < 2; ++hb) {
-                    float4_t c = float4_t{0, 0, 0, 0};
-#pragma unroll
-                    for (int ks = 0; ks < 4; ++ks)
-                        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[h2][ks], qh[hb][ks], c, 0, 0, 0);
-                    acc[h2][hb] = c;
-                }
-            // ---- 2. reduce-scatter S to the owners (waves 0, 1), softmax ----
-            // compiler-visible stores: it inserts the MFMA read hazard waits
-#pragma unroll
-            for (int hb = 0; hb < 2; ++hb)
-#pragma unroll
-                for (int h2 = 0; h2 < 2; ++h2) sx[hb][wave][h2][lane] = acc[h2][hb];
-            lds_barrier();   // B2: partials visible
+                for (int ks = 0; ks < 4; ++ks)
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[ks], qh[hb][ks], c, 0, 0, 0);
+                sx[hb][d][hh][lane] = c;   // compiler-visible store: MFMA hazard waits inserted
+            }
+            lds_barrier();   // B2: partials and V tile visible
             {
-                // softmax: wave w owns heads 16 hb + 8 (w & 1) + [0, 8), hb = w >> 1;
-                // lane (jj, kk) holds keys 16 h2 + 4 kq + [0, 4) of head jj
+                // softmax: wave w owns heads 8w + [0, 8) (head tile hb = w >> 1);
+                // lane (jj, kk) holds rows 16 h2 + 4 kq + [0, 4) of head jj
                 const int hb = wave >> 1;
                 const int jj = lane & 7, kk = lane >> 3;
                 const int h2 = kk >> 2, kq = kk & 3;
@@ -1174,12 +1127,11 @@ __global__ __launch_bounds__(256, 2) void decode_hs_kernel(const DecodeArgs A) {
                 }
                 l_run = l_run * alpha + psum;
                 m_run = m_new;
-                // P^T fragment of head tile hb: lane (head, kq) keys {4kq.., 16+4kq..}
                 reinterpret_cast<uint2_t *>(&pbuf[hb][src])[h2] = __builtin_bit_cast(uint2_t, pf);
-                if (kk == 0) alpha_s[16 * hb + 8 * (wave & 1) + jj] = alpha;
+                if (kk == 0) alpha_s[8 * wave + jj] = alpha;
             }
             lds_barrier();   // B3: P and rescale factors visible
-            // ---- 3. O_w += P . V_w ----
+            // ---- 3. O += P . V_d for heads 32 hh + [0, 32) ----
             float4_t ar[2];
             half8_t pa[2];
             asm volatile(
@@ -1187,8 +1139,8 @@ __global__ __launch_bounds__(256, 2) void decode_hs_kernel(const DecodeArgs A) {
                 "ds_read_b128 %2, %5\n\tds_read_b128 %3, %5 offset:1024\n\t"
                 "s_waitcnt lgkmcnt(0)"
                 : "=&v"(ar[0]), "=&v"(ar[1]), "=&v"(pa[0]), "=&v"(pa[1])
-                : "v"(alpha_base + 16 * q), "v"(pbuf_base + lane * 16));
-            // rare (the reference point moved): rescale O before adding tile t
+                : "v"(alpha_base + (32 * hh + 4 * q) * 4), "v"(pbuf_base + (2 * hh * 64 + lane) * 16));
+            // rare (a reference point moved): rescale O before adding tile t
             const bool need = ar[0][0] != 1.0f || ar[0][1] != 1.0f || ar[0][2] != 1.0f ||
                               ar[0][3] != 1.0f || ar[1][0] != 1.0f || ar[1][1] != 1.0f ||
                               ar[1][2] != 1.0f || ar[1][3] != 1.0f;
@@ -1201,7 +1153,7 @@ __global__ __launch_bounds__(256, 2) void decode_hs_kernel(const DecodeArgs A) {
 #pragma unroll
             for (int half = 0; half < 2; ++half) {
                 uint2_t tb[8];
-                const uint32_t ab = vt_base + (4 * q + (j >> 2)) * kVRowBytes + 8 * (j & 3) + 128 * half;
+                const uint32_t ab = vt + (4 * q + (j >> 2)) * kVRowBytes + 8 * (j & 3) + 128 * half;
                 asm volatile(
                     "ds_read_b64_tr_b16 %0, %8\n\tds_read_b64_tr_b16 %1, %8 offset:4608\n\t"
                     "ds_read_b64_tr_b16 %2, %8 offset:32\n\tds_read_b64_tr_b16 %3, %8 offset:4640\n\t"
@@ -1223,14 +1175,14 @@ __global__ __launch_bounds__(256, 2) void decode_hs_kernel(const DecodeArgs A) {
             }
         };
         for (int t = 0; t < n_tiles; t += 2) {
-            step(t, T0, ph0, ph1);
-            step(t + 1, T1, ph1, ph0);
+            step(t, T0, ph0, ph1, 0);
+            step(t + 1, T1, ph1, ph0, 1);
         }
 
-        // ---- emit: this workgroup's heads over the wave's dims; m, l by the owners ----
+        // ---- emit: O of heads 32 hh + .. over dims d; m, l by the softmax owners ----
         {
-            const long long slot = (long long)chunk * A.s_max + slot_s;
-            float *wo = A.ws_o + slot * (kH * kD) + (h0 + 4 * q) * kD + 128 * wave + j;
+            const long long slot = (long long)blockIdx.x * A.s_max + slot_s;
+            float *wo = A.ws_o + slot * (kH * kD) + (32 * hh + 4 * q) * kD + 128 * d + j;
             asm volatile("" : "+v"(wo));
 #pragma unroll
             for (int mb = 0; mb < 2; ++mb)
@@ -1238,22 +1190,19 @@ __global__ __launch_bounds__(256, 2) void decode_hs_kernel(const DecodeArgs A) {
                 for (int nb = 0; nb < 8; ++nb)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) wo[(16 * mb + r) * kD + 16 * nb] = o[mb][nb][r];
-            {
-                const float l = xsum_8_16_32(l_run);
-                if (lane < 8) {
-                    const int hd = h0 + 16 * (wave >> 1) + 8 * (wave & 1) + lane;
-                    A.ws_ml[slot * 2 * kH + hd] = m_run;
-                    A.ws_ml[slot * 2 * kH + kH + hd] = l;
-                }
+            const float l = xsum_8_16_32(l_run);
+            if (lane < 8) {
+                A.ws_ml[slot * 2 * kH + 8 * wave + lane] = m_run;
+                A.ws_ml[slot * 2 * kH + kH + 8 * wave + lane] = l;
             }
-            if (hh == 0 && threadIdx.x == 0) A.ws_prob[slot] = p;
+            if (threadIdx.x == 0) A.ws_prob[slot] = p;
         }
         ++slot_s;
         g0 = seg_end;
-        lds_barrier();   // vtile, sx and pbuf are reused by the next segment
+        lds_barrier();   // the V tiles, sx and pbuf are reused by the next segment
     }
-    if (hh == 0 && threadIdx.x == 0)
-        for (int s2 = slot_s; s2 < A.s_max; ++s2) A.ws_prob[(long long)chunk * A.s_max + s2] = -1;
+    if (threadIdx.x == 0)
+        for (int s2 = slot_s; s2 < A.s_max; ++s2) A.ws_prob[(long long)blockIdx.x * A.s_max + s2] = -1;
 }
 
 // Physical cache row of every logical row of a gathered step (row_idx and/or
@@ -1277,6 +1226,7 @@ __global__ __launch_bounds__(256) void phys_kernel(const DecodeArgs A) {
 // independent; each lane covers 8 of the 512 dims. The max over the slots
 // (and the sink) is taken first, then every wave accumulates its slots
 // rescaled to that max, and the 4 wave sums are added in LDS in wave order.
+// One block per (problem, head): combine the partials with the sink.
 __global__ __launch_bounds__(256) void decode_merge_kernel(const DecodeArgs A) {
     __shared__ long long s_start[kMaxProb + 1];
     __shared__ float red_m[4];
@@ -1408,11 +1358,10 @@ int launch(DecodeArgs &A, const Plan &pl, hipStream_t st, int phases = 3) {
         }
         if (kFp8 && !kQf32)
         {
-            const dim3 grid(16 * ((pl.n_wg + 7) / 8));
             if (A.phys)
-                hipLaunchKernelGGL(decode_hs_kernel<true>, grid, dim3(256), 0, st, A);
+                hipLaunchKernelGGL(decode_w8_kernel<true>, dim3(pl.n_wg), dim3(512), 0, st, A);
             else
-                hipLaunchKernelGGL(decode_hs_kernel<false>, grid, dim3(256), 0, st, A);
+                hipLaunchKernelGGL(decode_w8_kernel<false>, dim3(pl.n_wg), dim3(512), 0, st, A);
         }
         else if (kFp8)
             hipLaunchKernelGGL(decode_fp8_kernel<kQf32>, dim3(pl.n_wg), dim3(256), 0, st, A);

@@ -953,10 +953,12 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(const DecodeArgs A) {
 // every byte of the chunk is read once, by one lane. It dequantizes them,
 // writes them to the f16 V tile of dims d (double-buffered: the two waves of a
 // dim quarter share it) and computes the partial S of its 16 rows for all 64
-// heads over its dims (16 MFMAs). After one barrier each wave owns the softmax
-// of 8 heads (sum of the four dim partials, lazy rescale, P in f16); after a
-// second one wave (d, hh) adds P . V_d for heads [32 hh, 32 hh + 32) over all 32
-// rows. Two waves per SIMD; one workgroup per CU.
+// heads over its dims (16 MFMAs). Each wave owns the softmax of 8 heads (sum
+// of the four dim partials, lazy rescale, P in f16) and wave (d, hh) adds
+// P . V_d for heads [32 hh, 32 hh + 32) over all 32 rows. The softmax of tile t
+// runs in the same barrier interval as the dequantize and partial S of tile
+// t + 1 (S partials and V tiles double-buffered by tile parity), P . V(t) in
+// the next one: two barriers per tile. Two waves per SIMD; one workgroup per CU.
 
 struct W8Tile {
     uint4_t c0, c1;   // codes 128d + 16q; codes 128d + 64 + 16q or (d = 3) tail chunk 2q
@@ -970,15 +972,18 @@ __device__ inline void w8_load(const DecodeArgs &A, int d, int q, long long r, W
     const uint8_t *p1 = d < 3 ? cr + 128 * d + 64 + 16 * q : tr + 32 * q;
     T.c0 = *reinterpret_cast<const uint4_t *>(cr + 128 * d + 16 * q);
     T.c1 = *reinterpret_cast<const uint4_t *>(p1);
-    T.th = d == 3 ? *reinterpret_cast<const uint4_t *>(tr + 32 * q + 16) : uint4_t{0, 0, 0, 0};
+    // unconditional (d < 3: a repeat of c1, an L1 hit): a load under a branch
+    // makes the compiler's load-count waits assume the shorter path
+    const uint8_t *p2 = d < 3 ? p1 : tr + 32 * q + 16;
+    T.th = *reinterpret_cast<const uint4_t *>(p2);
     T.e = *reinterpret_cast<const uint2_t *>(A.sexp + r * 8);
 }
 
 template <bool kGather>
 __global__ __launch_bounds__(512, 1) void decode_w8_kernel(const DecodeArgs A) {
-    __shared__ __attribute__((aligned(16))) uint8_t vtile[2][4][kVTileBytes];   // [buffer][d]
-    __shared__ __attribute__((aligned(16))) float4_t sx[4][4][2][64];   // [head tile][d][row half][lane]
-    __shared__ __attribute__((aligned(16))) half8_t pbuf[4][64];        // [head tile][lane]
+    __shared__ __attribute__((aligned(16))) uint8_t vtile[2][4][kVTileBytes];   // [tile & 1][d]
+    __shared__ __attribute__((aligned(16))) float4_t sx[2][4][4][2][64];  // [tile & 1][head tile][d][row half][lane]
+    __shared__ __attribute__((aligned(16))) half8_t pbuf[4][64];          // [head tile][lane]
     __shared__ __attribute__((aligned(16))) float alpha_s[kH];
     __shared__ long long s_start[kMaxProb + 1];
     __shared__ long long s_rowbase[kMaxProb];
@@ -993,6 +998,12 @@ __global__ __launch_bounds__(512, 1) void decode_w8_kernel(const DecodeArgs A) {
     const int q = lane >> 4;
     const uint32_t pbuf_base = lds_addr(pbuf);
     const uint32_t alpha_base = lds_addr(alpha_s);
+    // softmax ownership: wave w owns heads 8w + [0, 8) (head tile w >> 1); lane
+    // (jj, kk) holds rows 16 h2 + 4 kq + [0, 4) of head jj
+    const int own_hb = wave >> 1;
+    const int jj = lane & 7, kk = lane >> 3;
+    const int own_h2 = kk >> 2, own_kq = kk & 3;
+    const int own_src = 8 * (wave & 1) + jj + 16 * own_kq;
 
     long long g0 = (long long)blockIdx.x * A.chunk;
     const long long g1 = min(g0 + (long long)A.chunk, A.total);
@@ -1033,14 +1044,51 @@ __global__ __launch_bounds__(512, 1) void decode_w8_kernel(const DecodeArgs A) {
                 qh[hb][ks] = h;
             }
 
-        float m_run = -INFINITY, l_run = 0.0f;      // softmax of head 8 wave + lane % 8
+        float m_run = -INFINITY, l_run = 0.0f;      // softmax of head 8 wave + jj
         float4_t o[2][8];                           // heads 32 hh + 16 mb + .., dims 128 d + 16 nb + ..
 #pragma unroll
         for (int a = 0; a < 2; ++a)
 #pragma unroll
             for (int c = 0; c < 8; ++c) o[a][c] = float4_t{0, 0, 0, 0};
 
-        // prologue (issue order = the loop's: tile 0, [rows of tile 2], tile 1)
+        // tile u: dequantize (registers -> V tile u & 1), refill the registers
+        // with tile u + 2, partial S of tile u -> sx[u & 1]. Gathered rows of
+        // tile u + 2 are in ph_use; those of u + 3 are fetched into ph_next
+        // first, so that waiting for them later leaves tile u + 2 in flight.
+        auto qk_prep = [&](int u, W8Tile &cur, long long &ph_use, long long &ph_next, int buf) {
+            half8_t a[4];
+            {
+                half8_t d2, d3;
+                dequant16(cur.c0, block_scale(cur.e, 2 * d), a[0], a[1]);
+                dequant16(cur.c1, block_scale(cur.e, 2 * d + 1), d2, d3);
+                a[2] = d < 3 ? d2 : __builtin_bit_cast(half8_t, cur.c1);
+                a[3] = d < 3 ? d3 : __builtin_bit_cast(half8_t, cur.th);
+                const uint32_t vrow = lds_addr(vtile[buf][d]) + (16 * hh + j) * kVRowBytes + 32 * q;
+                asm volatile("ds_write_b128 %0, %1\n\tds_write_b128 %0, %2 offset:16\n\t"
+                             "ds_write_b128 %0, %3 offset:128\n\tds_write_b128 %0, %4 offset:144"
+                             :: "v"(vrow), "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]) : "memory");
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (kGather) {
+                ph_next = row_gather(u + 3);
+                __builtin_amdgcn_sched_barrier(0);
+                w8_load(A, d, q, ph_use, cur);
+            } else {
+                w8_load(A, d, q, row_direct(u + 2), cur);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int hb = 0; hb < 4; ++hb) {
+                float4_t c = float4_t{0, 0, 0, 0};
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks)
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[ks], qh[hb][ks], c, 0, 0, 0);
+                sx[buf][hb][d][hh][lane] = c;   // compiler-visible store: MFMA hazard waits inserted
+            }
+        };
+
+        // prologue (issue order = the loop's: tile 0, [rows of tile 2], tile 1),
+        // then tile 0's partial S
         W8Tile T0, T1;
         long long ph0 = 0, ph1 = 0;
         __builtin_amdgcn_sched_barrier(0);
@@ -1058,55 +1106,24 @@ __global__ __launch_bounds__(512, 1) void decode_w8_kernel(const DecodeArgs A) {
             w8_load(A, d, q, row_direct(1), T1);
         }
         __builtin_amdgcn_sched_barrier(0);
+        qk_prep(0, T0, ph0, ph1, 0);
+        lds_barrier();   // partials of tile 0 and V tile 0 visible
 
-        auto step = [&](int t, W8Tile &cur, long long &ph_use, long long &ph_next, int buf) {
+        // Tile t: softmax(t) overlapped with the next tile's dequantize + S
+        // (MFMA), barrier, P . V(t), barrier. V tiles and S partials are double
+        // buffered by tile parity; P and the rescale factors are single.
+        auto step = [&](int t, W8Tile &nxt, long long &ph_use, long long &ph_next, int buf) {
             const long long rb = r0 + (long long)t * kTile;
-            const uint32_t vt = lds_addr(vtile[buf][d]);
-            // ---- 1. dequantize, write V_d rows, prefetch tile t+2, partial S ----
-            half8_t a[4];
+            const float4_t sacc =
+                ((sx[buf][own_hb][0][own_h2][own_src] + sx[buf][own_hb][1][own_h2][own_src]) +
+                 sx[buf][own_hb][2][own_h2][own_src]) + sx[buf][own_hb][3][own_h2][own_src];
+            qk_prep(t + 1, nxt, ph_use, ph_next, buf ^ 1);
             {
-                half8_t d2, d3;
-                dequant16(cur.c0, block_scale(cur.e, 2 * d), a[0], a[1]);
-                dequant16(cur.c1, block_scale(cur.e, 2 * d + 1), d2, d3);
-                a[2] = d < 3 ? d2 : __builtin_bit_cast(half8_t, cur.c1);
-                a[3] = d < 3 ? d3 : __builtin_bit_cast(half8_t, cur.th);
-                const uint32_t vrow = vt + (16 * hh + j) * kVRowBytes + 32 * q;
-                asm volatile("ds_write_b128 %0, %1\n\tds_write_b128 %0, %2 offset:16\n\t"
-                             "ds_write_b128 %0, %3 offset:128\n\tds_write_b128 %0, %4 offset:144"
-                             :: "v"(vrow), "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]) : "memory");
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            if (kGather) {
-                ph_next = row_gather(t + 3);
-                __builtin_amdgcn_sched_barrier(0);
-                w8_load(A, d, q, ph_use, cur);
-            } else {
-                w8_load(A, d, q, row_direct(t + 2), cur);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int hb = 0; hb < 4; ++hb) {
-                float4_t c = float4_t{0, 0, 0, 0};
-#pragma unroll
-                for (int ks = 0; ks < 4; ++ks)
-                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[ks], qh[hb][ks], c, 0, 0, 0);
-                sx[hb][d][hh][lane] = c;   // compiler-visible store: MFMA hazard waits inserted
-            }
-            lds_barrier();   // B2: partials and V tile visible
-            {
-                // softmax: wave w owns heads 8w + [0, 8) (head tile hb = w >> 1);
-                // lane (jj, kk) holds rows 16 h2 + 4 kq + [0, 4) of head jj
-                const int hb = wave >> 1;
-                const int jj = lane & 7, kk = lane >> 3;
-                const int h2 = kk >> 2, kq = kk & 3;
-                const int src = 8 * (wave & 1) + jj + 16 * kq;
-                const float4_t sacc = ((sx[hb][0][h2][src] + sx[hb][1][h2][src]) + sx[hb][2][h2][src]) +
-                                      sx[hb][3][h2][src];
                 float s4[4];
                 float tmax = -INFINITY;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const bool ok = rb + 16 * h2 + 4 * kq + r < r1;
+                    const bool ok = rb + 16 * own_h2 + 4 * own_kq + r < r1;
                     s4[r] = ok ? sacc[r] * A.kq_log2 : -INFINITY;
                     tmax = fmaxf(tmax, s4[r]);
                 }
@@ -1127,11 +1144,12 @@ __global__ __launch_bounds__(512, 1) void decode_w8_kernel(const DecodeArgs A) {
                 }
                 l_run = l_run * alpha + psum;
                 m_run = m_new;
-                reinterpret_cast<uint2_t *>(&pbuf[hb][src])[h2] = __builtin_bit_cast(uint2_t, pf);
+                reinterpret_cast<uint2_t *>(&pbuf[own_hb][own_src])[own_h2] = __builtin_bit_cast(uint2_t, pf);
                 if (kk == 0) alpha_s[8 * wave + jj] = alpha;
             }
-            lds_barrier();   // B3: P and rescale factors visible
-            // ---- 3. O += P . V_d for heads 32 hh + [0, 32) ----
+            lds_barrier();   // P and rescale factors of tile t visible
+            // ---- O += P . V_d for heads 32 hh + [0, 32) ----
+            const uint32_t vt = lds_addr(vtile[buf][d]);
             float4_t ar[2];
             half8_t pa[2];
             asm volatile(
@@ -1173,10 +1191,11 @@ __global__ __launch_bounds__(512, 1) void decode_w8_kernel(const DecodeArgs A) {
                             pa[mb], vb, o[mb][4 * half + nb], 0, 0, 0);
                 }
             }
+            lds_barrier();   // partials of tile t+1 and V tile t+1 visible; P consumed
         };
         for (int t = 0; t < n_tiles; t += 2) {
-            step(t, T0, ph0, ph1, 0);
-            step(t + 1, T1, ph1, ph0, 1);
+            step(t, T1, ph1, ph0, 0);
+            step(t + 1, T0, ph0, ph1, 1);
         }
 
         // ---- emit: O of heads 32 hh + .. over dims d; m, l by the softmax owners ----
@@ -1199,7 +1218,6 @@ __global__ __launch_bounds__(512, 1) void decode_w8_kernel(const DecodeArgs A) {
         }
         ++slot_s;
         g0 = seg_end;
-        lds_barrier();   // the V tiles, sx and pbuf are reused by the next segment
     }
     if (threadIdx.x == 0)
         for (int s2 = slot_s; s2 < A.s_max; ++s2) A.ws_prob[(long long)blockIdx.x * A.s_max + s2] = -1;

@@ -1004,6 +1004,7 @@ __global__ __launch_bounds__(512, 1) void decode_w8_kernel(const DecodeArgs A) {
     const int jj = lane & 7, kk = lane >> 3;
     const int own_h2 = kk >> 2, own_kq = kk & 3;
     const int own_src = 8 * (wave & 1) + jj + 16 * own_kq;
+    const int own_sx = own_src ^ (own_kq & 1 ? 8 : 0);   // the stores' lane swizzle
 
     long long g0 = (long long)blockIdx.x * A.chunk;
     const long long g1 = min(g0 + (long long)A.chunk, A.total);
@@ -1063,10 +1064,14 @@ __global__ __launch_bounds__(512, 1) void decode_w8_kernel(const DecodeArgs A) {
                 dequant16(cur.c1, block_scale(cur.e, 2 * d + 1), d2, d3);
                 a[2] = d < 3 ? d2 : __builtin_bit_cast(half8_t, cur.c1);
                 a[3] = d < 3 ? d3 : __builtin_bit_cast(half8_t, cur.th);
+                // rows 8..15 of each half swap their 16-byte column pairs (bank spread
+                // for these stores; the transposing reads below apply the same swap)
                 const uint32_t vrow = lds_addr(vtile[buf][d]) + (16 * hh + j) * kVRowBytes + 32 * q;
-                asm volatile("ds_write_b128 %0, %1\n\tds_write_b128 %0, %2 offset:16\n\t"
-                             "ds_write_b128 %0, %3 offset:128\n\tds_write_b128 %0, %4 offset:144"
-                             :: "v"(vrow), "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]) : "memory");
+                const uint32_t sw = (j & 8) ? 16u : 0u;
+                const uint32_t va = vrow + sw, vb = vrow + (16u - sw);
+                asm volatile("ds_write_b128 %0, %2\n\tds_write_b128 %1, %3\n\t"
+                             "ds_write_b128 %0, %4 offset:128\n\tds_write_b128 %1, %5 offset:128"
+                             :: "v"(va), "v"(vb), "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]) : "memory");
             }
             __builtin_amdgcn_sched_barrier(0);
             if (kGather) {
@@ -1083,7 +1088,8 @@ __global__ __launch_bounds__(512, 1) void decode_w8_kernel(const DecodeArgs A) {
 #pragma unroll
                 for (int ks = 0; ks < 4; ++ks)
                     c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[ks], qh[hb][ks], c, 0, 0, 0);
-                sx[buf][hb][d][hh][lane] = c;   // compiler-visible store: MFMA hazard waits inserted
+                // lane ^ 8 for odd q: the softmax reads below are then bank-conflict free
+                sx[buf][hb][d][hh][lane ^ (lane & 16 ? 8 : 0)] = c;   // compiler-visible store: MFMA hazard waits inserted
             }
         };
 
@@ -1115,8 +1121,8 @@ __global__ __launch_bounds__(512, 1) void decode_w8_kernel(const DecodeArgs A) {
         auto step = [&](int t, W8Tile &nxt, long long &ph_use, long long &ph_next, int buf) {
             const long long rb = r0 + (long long)t * kTile;
             const float4_t sacc =
-                ((sx[buf][own_hb][0][own_h2][own_src] + sx[buf][own_hb][1][own_h2][own_src]) +
-                 sx[buf][own_hb][2][own_h2][own_src]) + sx[buf][own_hb][3][own_h2][own_src];
+                ((sx[buf][own_hb][0][own_h2][own_sx] + sx[buf][own_hb][1][own_h2][own_sx]) +
+                 sx[buf][own_hb][2][own_h2][own_sx]) + sx[buf][own_hb][3][own_h2][own_sx];
             qk_prep(t + 1, nxt, ph_use, ph_next, buf ^ 1);
             {
                 float s4[4];
@@ -1171,7 +1177,7 @@ __global__ __launch_bounds__(512, 1) void decode_w8_kernel(const DecodeArgs A) {
 #pragma unroll
             for (int half = 0; half < 2; ++half) {
                 uint2_t tb[8];
-                const uint32_t ab = vt + (4 * q + (j >> 2)) * kVRowBytes + 8 * (j & 3) + 128 * half;
+                const uint32_t ab = vt + (4 * q + (j >> 2)) * kVRowBytes + 8 * ((j & 3) ^ (q & 2)) + 128 * half;
                 asm volatile(
                     "ds_read_b64_tr_b16 %0, %8\n\tds_read_b64_tr_b16 %1, %8 offset:4608\n\t"
                     "ds_read_b64_tr_b16 %2, %8 offset:32\n\tds_read_b64_tr_b16 %3, %8 offset:4640\n\t"

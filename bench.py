@@ -33,21 +33,11 @@ ROW_BYTES = 584                                   # FP8 cache row: 448 codes + 8
 HBM_PEAK_GBS = 8000.0
 MFMA_PEAK_TFLOPS = 2500.0                          # dense f16 / bf16
 COPY_BYTES = 1 << 30                               # --copy-calibration: 1 GiB read + 1 GiB written
-TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                               "decode_fp8_cfg2_traffic.md")
-
-
-def measured_traffic():
-    """HBM bytes per launch of the partial kernel, from the committed counter
-    summary (FETCH_SIZE + WRITE_SIZE, each scaled by the copy-kernel factor);
-    None when the summary is absent."""
-    try:
-        for line in open(TRAFFIC_PROFILE):
-            if line.startswith("traffic_bytes_per_launch:"):
-                return int(float(line.split(":", 1)[1]))
-    except OSError:
-        pass
-    return None
+# HBM bytes per launch of the cfg-2 partial kernel, measured with rocprofv3
+# (FETCH_SIZE + WRITE_SIZE, each scaled by what the counter reads for
+# `--copy-calibration`); the counter summary and its commands are in
+# profiles/decode_fp8_cfg2_traffic.md. Re-measure after a kernel change.
+TRAFFIC_BYTES_PER_LAUNCH = 881910047
 
 
 def bytes_per_layer():
@@ -383,7 +373,7 @@ def main():
                    "kv_bytes_per_row": ROW_BYTES, "us_per_layer": round(ms * 1e3 / N_LAYERS, 3),
                    "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_BYTES_PER_LAUNCH,
                      "kernel": "decode_w8_kernel<direct rows>",
                      "kernel_ms": round(k_ms, 4), "bytes_per_launch": step_bytes},
     }

@@ -47,7 +47,7 @@ __device__ inline float key_elem(const void *keys, size_t i) {
 // hist (optional): top-11-bit histogram of the ordered keys of positions
 // [0, n_cand).
 template <int kKind, int kDim>
-__device__ inline float score_one(const float *__restrict__ q, const float *__restrict__ w,
+__device__ __attribute__((always_inline)) inline float score_one(const float *__restrict__ q, const float *__restrict__ w,
                                   const void *__restrict__ keys, int c, int n_head) {
     float k[kDim];
     if (kKind != 0 && kDim % 8 == 0) {
@@ -114,7 +114,9 @@ __device__ inline float score_any(const float *qs, const float *ws, const void *
     return s;
 }
 
-template <int kKind>
+// kFull: head_dim == 128 (the scalar-load path); otherwise the LDS path. Two
+// instantiations so that neither path's registers limit the other's occupancy.
+template <int kKind, bool kFull>
 __global__ __launch_bounds__(256) void score_kernel(const float *__restrict__ q,
                                                     const float *__restrict__ w,
                                                     const void *__restrict__ keys, int n_comp,
@@ -126,7 +128,7 @@ __global__ __launch_bounds__(256) void score_kernel(const float *__restrict__ q,
         for (int i = threadIdx.x; i < kBins; i += 256) lh[i] = 0;
     const int c = blockIdx.x * 256 + threadIdx.x;
     float s = 0.0f;
-    if (head_dim == kMaxDim) {
+    if (kFull) {
         if (c < n_comp) s = score_one<kKind, kMaxDim>(q, w, keys, c, n_head);
     } else {
         __shared__ float qs[kMaxHeads * kMaxDim];
@@ -386,10 +388,20 @@ int launch_scores(const float *q, const float *w, const void *keys, int kind, in
                   int n_head, int head_dim, float *scores, unsigned *hist, int n_cand,
                   hipStream_t st) {
     const dim3 grid((n_comp + 255) / 256);
+    const bool full = head_dim == kMaxDim;
     switch (kind) {
-    case 0: hipLaunchKernelGGL(score_kernel<0>, grid, dim3(256), 0, st, q, w, keys, n_comp, n_head, head_dim, scores, hist, n_cand); break;
-    case 1: hipLaunchKernelGGL(score_kernel<1>, grid, dim3(256), 0, st, q, w, keys, n_comp, n_head, head_dim, scores, hist, n_cand); break;
-    default: hipLaunchKernelGGL(score_kernel<2>, grid, dim3(256), 0, st, q, w, keys, n_comp, n_head, head_dim, scores, hist, n_cand); break;
+    case 0:
+        if (full) hipLaunchKernelGGL((score_kernel<0, true>), grid, dim3(256), 0, st, q, w, keys, n_comp, n_head, head_dim, scores, hist, n_cand);
+        else hipLaunchKernelGGL((score_kernel<0, false>), grid, dim3(256), 0, st, q, w, keys, n_comp, n_head, head_dim, scores, hist, n_cand);
+        break;
+    case 1:
+        if (full) hipLaunchKernelGGL((score_kernel<1, true>), grid, dim3(256), 0, st, q, w, keys, n_comp, n_head, head_dim, scores, hist, n_cand);
+        else hipLaunchKernelGGL((score_kernel<1, false>), grid, dim3(256), 0, st, q, w, keys, n_comp, n_head, head_dim, scores, hist, n_cand);
+        break;
+    default:
+        if (full) hipLaunchKernelGGL((score_kernel<2, true>), grid, dim3(256), 0, st, q, w, keys, n_comp, n_head, head_dim, scores, hist, n_cand);
+        else hipLaunchKernelGGL((score_kernel<2, false>), grid, dim3(256), 0, st, q, w, keys, n_comp, n_head, head_dim, scores, hist, n_cand);
+        break;
     }
     return hip_status(hipGetLastError());
 }

@@ -48,7 +48,7 @@ constexpr int kNope = kD - kRot; // 448 FP8-coded dims, 7 scale blocks
 constexpr int kTile = 32;        // rows per tile
 constexpr int kVtStride = 40;    // halves per V^T line (32 rows + 8 pad)
 constexpr int kMaxProb = 128;
-constexpr int kMinChunk = 4 * kTile;
+constexpr int kMinChunk = 2 * kTile;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kFp8WgPerCu = 1;   // the FP8 kernel's LDS ring allows one workgroup per CU
 
@@ -979,7 +979,9 @@ __device__ inline void w8_load(const DecodeArgs &A, int d, int q, long long r, W
     T.e = *reinterpret_cast<const uint2_t *>(A.sexp + r * 8);
 }
 
-template <bool kGather>
+// kMode: 0 direct rows (row_base + position), 1 the phys array (page tables),
+// 2 row_base + row_idx (position lists without pages, resolved here).
+template <int kMode>
 __global__ __launch_bounds__(512, 1) void decode_w8_kernel(const DecodeArgs A) {
     __shared__ __attribute__((aligned(16))) uint8_t vtile[2][4][kVTileBytes];   // [tile & 1][d]
     __shared__ __attribute__((aligned(16))) float4_t sx[2][4][4][2][64];  // [tile & 1][head tile][d][row half][lane]
@@ -1023,7 +1025,9 @@ __global__ __launch_bounds__(512, 1) void decode_w8_kernel(const DecodeArgs A) {
             return seg_base + min(r0 + (long long)t * kTile + 16 * hh + j, r1 - 1);
         };
         auto row_gather = [&](int t) -> long long {
-            return A.phys[g0 + min((long long)t * kTile + 16 * hh + j, r1 - 1 - r0)];
+            const long long lr = min((long long)t * kTile + 16 * hh + j, r1 - 1 - r0);
+            if (kMode == 1) return A.phys[g0 + lr];
+            return seg_base + A.row_idx[(long long)p * A.row_idx_stride + r0 + lr];
         };
 
         // Q^T fragments of all 64 heads over dims d
@@ -1074,7 +1078,7 @@ __global__ __launch_bounds__(512, 1) void decode_w8_kernel(const DecodeArgs A) {
                              :: "v"(va), "v"(vb), "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]) : "memory");
             }
             __builtin_amdgcn_sched_barrier(0);
-            if (kGather) {
+            if (kMode != 0) {
                 ph_next = row_gather(u + 3);
                 __builtin_amdgcn_sched_barrier(0);
                 w8_load(A, d, q, ph_use, cur);
@@ -1098,7 +1102,7 @@ __global__ __launch_bounds__(512, 1) void decode_w8_kernel(const DecodeArgs A) {
         W8Tile T0, T1;
         long long ph0 = 0, ph1 = 0;
         __builtin_amdgcn_sched_barrier(0);
-        if (kGather) {
+        if (kMode != 0) {
             const long long ra = row_gather(0), rb1 = row_gather(1);
             __builtin_amdgcn_sched_barrier(0);
             w8_load(A, d, q, ra, T0);
@@ -1376,16 +1380,19 @@ int launch(DecodeArgs &A, const Plan &pl, hipStream_t st, int phases = 3) {
     A.s_max = pl.s_max;
     A.kq_log2 = kLog2e / sqrtf((float)kD);
     if ((phases & 1) && pl.n_wg > 0) {
-        if (kFp8 && A.phys) {
+        // bf16 Q with position lists but no pages: the kernel resolves the rows
+        const bool idx_only = kFp8 && !kQf32 && A.row_idx && !A.page_table;
+        if (kFp8 && A.phys && !idx_only) {
             const long long n = A.total + kTile;
             hipLaunchKernelGGL(phys_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, A);
         }
-        if (kFp8 && !kQf32)
-        {
-            if (A.phys)
-                hipLaunchKernelGGL(decode_w8_kernel<true>, dim3(pl.n_wg), dim3(512), 0, st, A);
+        if (kFp8 && !kQf32) {
+            if (idx_only)
+                hipLaunchKernelGGL(decode_w8_kernel<2>, dim3(pl.n_wg), dim3(512), 0, st, A);
+            else if (A.phys)
+                hipLaunchKernelGGL(decode_w8_kernel<1>, dim3(pl.n_wg), dim3(512), 0, st, A);
             else
-                hipLaunchKernelGGL(decode_w8_kernel<false>, dim3(pl.n_wg), dim3(512), 0, st, A);
+                hipLaunchKernelGGL(decode_w8_kernel<0>, dim3(pl.n_wg), dim3(512), 0, st, A);
         }
         else if (kFp8)
             hipLaunchKernelGGL(decode_fp8_kernel<kQf32>, dim3(pl.n_wg), dim3(256), 0, st, A);

@@ -93,6 +93,57 @@ __device__ __attribute__((always_inline)) inline float score_one(const float *__
     return s;
 }
 
+// head_dim 128 with the query and the weights in LDS: every multiply-add
+// takes its query value from a broadcast 16-byte LDS read (in-order
+// returns, so the reads run several steps ahead of their use). Same
+// canonical order as score_one.
+template <int kKind>
+__device__ __attribute__((always_inline)) inline float score_lds(const float *qs, const float *ws,
+                                                                 const void *__restrict__ keys,
+                                                                 int c, int n_head) {
+    float k[kMaxDim];
+    if (kKind == 0) {
+        const float4_t *src = reinterpret_cast<const float4_t *>(
+            static_cast<const float *>(keys) + (size_t)c * kMaxDim);
+#pragma unroll
+        for (int v = 0; v < kMaxDim / 4; ++v) {
+            const float4_t u = src[v];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) k[4 * v + e] = u[e];
+        }
+    } else {
+        const uint4_t *src = reinterpret_cast<const uint4_t *>(
+            static_cast<const uint16_t *>(keys) + (size_t)c * kMaxDim);
+#pragma unroll
+        for (int v = 0; v < kMaxDim / 8; ++v) {
+            const uint4_t u = src[v];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint16_t h = (uint16_t)((u[e >> 1] >> (16 * (e & 1))) & 0xFFFF);
+                k[8 * v + e] = kKind == 1 ? f16_bits_to_f32(h) : bf16_to_f32(h);
+            }
+        }
+    }
+    float s = 0.0f;
+    for (int h = 0; h < n_head; h += 2) {
+        const float4_t *q0 = reinterpret_cast<const float4_t *>(qs + h * kMaxDim);
+        const float4_t *q1 = q0 + kMaxDim / 4;
+        float d0 = 0.0f, d1 = 0.0f;
+#pragma unroll
+        for (int v = 0; v < kMaxDim / 4; ++v) {
+            const float4_t a = q0[v], b = q1[v];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                d0 = fmaf(a[e], k[4 * v + e], d0);
+                d1 = fmaf(b[e], k[4 * v + e], d1);
+            }
+        }
+        s = fmaf(ws[h], d0 > 0.0f ? d0 : 0.0f, s);
+        s = fmaf(ws[h + 1], d1 > 0.0f ? d1 : 0.0f, s);
+    }
+    return s;
+}
+
 // Any head_dim <= 128: the key row is zero-padded to 128 in registers and
 // the query is read with the same padding from LDS.
 template <int kKind>
@@ -129,7 +180,16 @@ __global__ __launch_bounds__(256) void score_kernel(const float *__restrict__ q,
     const int c = blockIdx.x * 256 + threadIdx.x;
     float s = 0.0f;
     if (kFull) {
-        if (c < n_comp) s = score_one<kKind, kMaxDim>(q, w, keys, c, n_head);
+        __shared__ __attribute__((aligned(16))) float qs[kMaxHeads * kMaxDim];
+        __shared__ float ws[kMaxHeads];
+        for (int i = threadIdx.x; i < n_head * kMaxDim; i += 256) qs[i] = q[i];
+        for (int i = threadIdx.x; i < n_head; i += 256) ws[i] = w[i];
+        if (n_head & 1) {   // a zero head with zero weight keeps the pairs aligned
+            for (int i = threadIdx.x; i < kMaxDim; i += 256) qs[n_head * kMaxDim + i] = 0.0f;
+            if (threadIdx.x == 0) ws[n_head] = 0.0f;
+        }
+        __syncthreads();
+        if (c < n_comp) s = score_lds<kKind>(qs, ws, keys, c, n_head);
     } else {
         __shared__ float qs[kMaxHeads * kMaxDim];
         __shared__ float ws[kMaxHeads];

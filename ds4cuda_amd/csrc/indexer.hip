@@ -41,62 +41,11 @@ __device__ inline float key_elem(const void *keys, size_t i) {
     return bf16_to_f32(static_cast<const uint16_t *>(keys)[i]);
 }
 
-// 256 threads, one key per thread. The query and the weights are read with
-// uniform addresses, so they come through the scalar cache into SGPRs and
-// every multiply-add is one VALU instruction with no memory operand.
-// hist (optional): top-11-bit histogram of the ordered keys of positions
-// [0, n_cand).
-template <int kKind, int kDim>
-__device__ __attribute__((always_inline)) inline float score_one(const float *__restrict__ q, const float *__restrict__ w,
-                                  const void *__restrict__ keys, int c, int n_head) {
-    float k[kDim];
-    if (kKind != 0 && kDim % 8 == 0) {
-        const uint4_t *src = reinterpret_cast<const uint4_t *>(
-            static_cast<const uint16_t *>(keys) + (size_t)c * kDim);
-#pragma unroll
-        for (int v = 0; v < kDim / 8; ++v) {
-            const uint4_t u = src[v];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const uint16_t h = (uint16_t)((u[e >> 1] >> (16 * (e & 1))) & 0xFFFF);
-                k[8 * v + e] = kKind == 1 ? f16_bits_to_f32(h) : bf16_to_f32(h);
-            }
-        }
-    } else {
-#pragma unroll
-        for (int d = 0; d < kDim; ++d) k[d] = key_elem<kKind>(keys, (size_t)c * kDim + d);
-    }
-    // two heads at a time: their dot chains are independent, so the two
-    // interleaved chains keep the VALU busy; the chains and the head sum keep
-    // the canonical order
-    float s = 0.0f;
-    int h = 0;
-    for (; h + 1 < n_head; h += 2) {
-        const float *q0 = q + h * kDim;
-        const float *q1 = q0 + kDim;
-        float d0 = 0.0f, d1 = 0.0f;
-#pragma unroll
-        for (int d = 0; d < kDim; ++d) {
-            d0 = fmaf(q0[d], k[d], d0);
-            d1 = fmaf(q1[d], k[d], d1);
-        }
-        s = fmaf(w[h], d0 > 0.0f ? d0 : 0.0f, s);
-        s = fmaf(w[h + 1], d1 > 0.0f ? d1 : 0.0f, s);
-    }
-    if (h < n_head) {
-        const float *qh = q + h * kDim;
-        float dot = 0.0f;
-#pragma unroll
-        for (int d = 0; d < kDim; ++d) dot = fmaf(qh[d], k[d], dot);
-        s = fmaf(w[h], dot > 0.0f ? dot : 0.0f, s);
-    }
-    return s;
-}
-
-// head_dim 128 with the query and the weights in LDS: every multiply-add
-// takes its query value from a broadcast 16-byte LDS read (in-order
-// returns, so the reads run several steps ahead of their use). Same
-// canonical order as score_one.
+// head_dim 128, one key per thread, the key row in registers as fp32 and the
+// query and the weights in LDS: every multiply-add takes its query value from
+// a broadcast 16-byte LDS read (in-order returns, so the reads run several
+// steps ahead of their use). Two heads at a time: their dot chains are
+// independent, and the chains and the head sum keep the canonical order.
 template <int kKind>
 __device__ __attribute__((always_inline)) inline float score_lds(const float *qs, const float *ws,
                                                                  const void *__restrict__ keys,
@@ -644,10 +593,19 @@ __global__ __launch_bounds__(256) void score_batch_kernel(const BatchArgs A) {
     for (int i = 0; i < kMaxSeq; ++i)
         if (i == s) first = A.blk0[i];
     const int c = ((int)blockIdx.x - first) * 256 + threadIdx.x;
+    __shared__ __attribute__((aligned(16))) float qs[kMaxHeads * kMaxDim];
+    __shared__ float ws[kMaxHeads];
+    const float *qg = A.q + (size_t)s * A.n_head * kMaxDim;
+    const float *wg = A.w + (size_t)s * A.n_head;
+    for (int i = threadIdx.x; i < A.n_head * kMaxDim; i += 256) qs[i] = qg[i];
+    for (int i = threadIdx.x; i < A.n_head; i += 256) ws[i] = wg[i];
+    if (A.n_head & 1) {   // a zero head with zero weight keeps the pairs aligned
+        for (int i = threadIdx.x; i < kMaxDim; i += 256) qs[A.n_head * kMaxDim + i] = 0.0f;
+        if (threadIdx.x == 0) ws[A.n_head] = 0.0f;
+    }
+    __syncthreads();
     if (c >= n) return;
-    const float *qs = A.q + (size_t)s * A.n_head * kMaxDim;
-    const float *ws = A.w + (size_t)s * A.n_head;
-    A.scores[k0 + c] = score_one<kKind, kMaxDim>(qs, ws, A.keys, (int)(k0 + c), A.n_head);
+    A.scores[k0 + c] = score_lds<kKind>(qs, ws, A.keys, (int)(k0 + c), A.n_head);
 }
 
 __device__ inline unsigned scan1024_excl(unsigned v, unsigned *wsum, unsigned *total) {

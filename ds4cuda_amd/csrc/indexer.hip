@@ -41,6 +41,27 @@ __device__ inline float key_elem(const void *keys, size_t i) {
     return bf16_to_f32(static_cast<const uint16_t *>(keys)[i]);
 }
 
+// Copies the n_head x 128 fp32 query into LDS with all loads issued before
+// any store (a plain strided loop waits for each load in turn).
+__device__ inline void stage_query(float *qs, const float *q, int n_head) {
+    if (reinterpret_cast<uintptr_t>(q) & 15) {   // unaligned caller buffer: plain copy
+        for (int i = threadIdx.x; i < n_head * kMaxDim; i += 256) qs[i] = q[i];
+        return;
+    }
+    const int n4 = n_head * kMaxDim / 4;
+    float4_t v[kMaxHeads * kMaxDim / 4 / 256];
+#pragma unroll
+    for (int i = 0; i < kMaxHeads * kMaxDim / 4 / 256; ++i) {
+        const int k = (int)threadIdx.x + 256 * i;
+        v[i] = k < n4 ? reinterpret_cast<const float4_t *>(q)[k] : float4_t{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int i = 0; i < kMaxHeads * kMaxDim / 4 / 256; ++i) {
+        const int k = (int)threadIdx.x + 256 * i;
+        if (k < n4) reinterpret_cast<float4_t *>(qs)[k] = v[i];
+    }
+}
+
 // head_dim 128, one key per thread, the key row in registers as fp32 and the
 // query and the weights in LDS: every multiply-add takes its query value from
 // a broadcast 16-byte LDS read (in-order returns, so the reads run several
@@ -93,6 +114,77 @@ __device__ __attribute__((always_inline)) inline float score_lds(const float *qs
     return s;
 }
 
+// The same score with four threads per key (adjacent lanes): thread `part`
+// computes the dot chains of heads [part n_head/4, (part+1) n_head/4); the
+// head sum then runs through the four lanes in head order (each continues
+// the running sum of the previous one), so the result is bit-identical to
+// score_lds. For short key lists, where one thread per key leaves most of
+// the chip idle. n_head % 8 == 0.
+template <int kKind>
+__device__ __attribute__((always_inline)) inline float score_lds4(const float *qs, const float *ws,
+                                                                  const void *__restrict__ keys,
+                                                                  int c, int n_head, int part) {
+    float k[kMaxDim];
+    if (kKind == 0) {
+        const float4_t *src = reinterpret_cast<const float4_t *>(
+            static_cast<const float *>(keys) + (size_t)c * kMaxDim);
+#pragma unroll
+        for (int v = 0; v < kMaxDim / 4; ++v) {
+            const float4_t u = src[v];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) k[4 * v + e] = u[e];
+        }
+    } else {
+        const uint4_t *src = reinterpret_cast<const uint4_t *>(
+            static_cast<const uint16_t *>(keys) + (size_t)c * kMaxDim);
+#pragma unroll
+        for (int v = 0; v < kMaxDim / 8; ++v) {
+            const uint4_t u = src[v];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint16_t h = (uint16_t)((u[e >> 1] >> (16 * (e & 1))) & 0xFFFF);
+                k[8 * v + e] = kKind == 1 ? f16_bits_to_f32(h) : bf16_to_f32(h);
+            }
+        }
+    }
+    const int hp = n_head >> 2;
+    const int h0 = part * hp;
+    float r[kMaxHeads / 4];
+#pragma unroll
+    for (int i = 0; i < kMaxHeads / 4; i += 2) {
+        r[i] = 0.0f;
+        r[i + 1] = 0.0f;
+        if (i < hp) {
+            const float4_t *q0 = reinterpret_cast<const float4_t *>(qs + (h0 + i) * kMaxDim);
+            const float4_t *q1 = q0 + kMaxDim / 4;
+            float d0 = 0.0f, d1 = 0.0f;
+#pragma unroll
+            for (int v = 0; v < kMaxDim / 4; ++v) {
+                const float4_t a = q0[v], b = q1[v];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    d0 = fmaf(a[e], k[4 * v + e], d0);
+                    d1 = fmaf(b[e], k[4 * v + e], d1);
+                }
+            }
+            r[i] = d0 > 0.0f ? d0 : 0.0f;
+            r[i + 1] = d1 > 0.0f ? d1 : 0.0f;
+        }
+    }
+    const int lane = threadIdx.x & 63;
+    float s = 0.0f;
+#pragma unroll
+    for (int k2 = 0; k2 < 4; ++k2) {
+        if (part == k2) {
+#pragma unroll
+            for (int i = 0; i < kMaxHeads / 4; ++i)
+                if (i < hp) s = fmaf(ws[h0 + i], r[i], s);
+        }
+        s = __shfl(s, (lane & ~3) | k2);
+    }
+    return s;
+}
+
 // Any head_dim <= 128: the key row is zero-padded to 128 in registers and
 // the query is read with the same padding from LDS.
 template <int kKind>
@@ -131,7 +223,7 @@ __global__ __launch_bounds__(256) void score_kernel(const float *__restrict__ q,
     if (kFull) {
         __shared__ __attribute__((aligned(16))) float qs[kMaxHeads * kMaxDim];
         __shared__ float ws[kMaxHeads];
-        for (int i = threadIdx.x; i < n_head * kMaxDim; i += 256) qs[i] = q[i];
+        stage_query(qs, q, n_head);
         for (int i = threadIdx.x; i < n_head; i += 256) ws[i] = w[i];
         if (n_head & 1) {   // a zero head with zero weight keeps the pairs aligned
             for (int i = threadIdx.x; i < kMaxDim; i += 256) qs[n_head * kMaxDim + i] = 0.0f;
@@ -574,7 +666,8 @@ struct BatchArgs {
     int blk0[kMaxSeq + 1];     // first score block of each sequence
 };
 
-template <int kKind>
+// kSplit threads per key (1 or 4); blocks of 256 threads cover 256 / kSplit keys.
+template <int kKind, int kSplit>
 __global__ __launch_bounds__(256) void score_batch_kernel(const BatchArgs A) {
     int s = 0;
 #pragma unroll
@@ -592,20 +685,23 @@ __global__ __launch_bounds__(256) void score_batch_kernel(const BatchArgs A) {
 #pragma unroll
     for (int i = 0; i < kMaxSeq; ++i)
         if (i == s) first = A.blk0[i];
-    const int c = ((int)blockIdx.x - first) * 256 + threadIdx.x;
+    const int c = ((int)blockIdx.x - first) * (256 / kSplit) + (int)threadIdx.x / kSplit;
     __shared__ __attribute__((aligned(16))) float qs[kMaxHeads * kMaxDim];
     __shared__ float ws[kMaxHeads];
     const float *qg = A.q + (size_t)s * A.n_head * kMaxDim;
     const float *wg = A.w + (size_t)s * A.n_head;
-    for (int i = threadIdx.x; i < A.n_head * kMaxDim; i += 256) qs[i] = qg[i];
+    stage_query(qs, qg, A.n_head);
     for (int i = threadIdx.x; i < A.n_head; i += 256) ws[i] = wg[i];
-    if (A.n_head & 1) {   // a zero head with zero weight keeps the pairs aligned
+    if (kSplit == 1 && (A.n_head & 1)) {   // a zero head with zero weight keeps the pairs aligned
         for (int i = threadIdx.x; i < kMaxDim; i += 256) qs[A.n_head * kMaxDim + i] = 0.0f;
         if (threadIdx.x == 0) ws[A.n_head] = 0.0f;
     }
     __syncthreads();
-    if (c >= n) return;
-    A.scores[k0 + c] = score_lds<kKind>(qs, ws, A.keys, (int)(k0 + c), A.n_head);
+    if (c >= n) return;   // the kSplit lanes of a key leave together
+    const float v = kSplit == 1 ? score_lds<kKind>(qs, ws, A.keys, (int)(k0 + c), A.n_head)
+                                : score_lds4<kKind>(qs, ws, A.keys, (int)(k0 + c), A.n_head,
+                                                    (int)threadIdx.x % kSplit);
+    if (threadIdx.x % kSplit == kSplit - 1) A.scores[k0 + c] = v;
 }
 
 __device__ inline unsigned scan1024_excl(unsigned v, unsigned *wsum, unsigned *total) {
@@ -733,6 +829,9 @@ extern "C" int ds4hip_indexer_topk_positions_batch(
     A.top_k = top_k;
     A.n_recent = n_recent;
     A.pos_stride = pos_stride;
+    // four threads per key (64 keys per block) when the heads split evenly
+    const bool split = n_head % 8 == 0;
+    const int keys_per_blk = split ? 64 : 256;
     int blk = 0;
     for (int s = 0; s < kMaxSeq; ++s) {
         const int n = s < n_seq ? n_comp_host[s] : 0;
@@ -742,15 +841,25 @@ extern "C" int ds4hip_indexer_topk_positions_batch(
         A.key0[s] = s < n_seq ? key_row0_host[s] : 0;
         A.blk0[s] = blk;
         // only sequences that need a selection are scored
-        if (s < n_seq && n > top_k) blk += (n + 255) / 256;
+        if (s < n_seq && n > top_k) blk += (n + keys_per_blk - 1) / keys_per_blk;
     }
     A.blk0[kMaxSeq] = blk;
     const hipStream_t st = (hipStream_t)stream;
     if (blk > 0) {
+        const dim3 g(blk), b(256);
         switch (key_kind) {
-        case 0: hipLaunchKernelGGL(score_batch_kernel<0>, dim3(blk), dim3(256), 0, st, A); break;
-        case 1: hipLaunchKernelGGL(score_batch_kernel<1>, dim3(blk), dim3(256), 0, st, A); break;
-        default: hipLaunchKernelGGL(score_batch_kernel<2>, dim3(blk), dim3(256), 0, st, A); break;
+        case 0:
+            if (split) hipLaunchKernelGGL((score_batch_kernel<0, 4>), g, b, 0, st, A);
+            else hipLaunchKernelGGL((score_batch_kernel<0, 1>), g, b, 0, st, A);
+            break;
+        case 1:
+            if (split) hipLaunchKernelGGL((score_batch_kernel<1, 4>), g, b, 0, st, A);
+            else hipLaunchKernelGGL((score_batch_kernel<1, 1>), g, b, 0, st, A);
+            break;
+        default:
+            if (split) hipLaunchKernelGGL((score_batch_kernel<2, 4>), g, b, 0, st, A);
+            else hipLaunchKernelGGL((score_batch_kernel<2, 1>), g, b, 0, st, A);
+            break;
         }
     }
     hipLaunchKernelGGL(select_batch_kernel, dim3(n_seq), dim3(1024), 0, st, A);

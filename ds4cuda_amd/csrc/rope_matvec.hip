@@ -241,12 +241,9 @@ int launch_q8(const uint8_t *W, const float *x, float *y, int n_groups, int grou
 // bits. Column chunks (split-K) are summed with fp32 atomics into a zeroed Y.
 // n_batch <= 16, n_cols % 32 == 0.
 typedef short bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef short short2_t __attribute__((ext_vector_type(2)));
 constexpr int kMmCols = 2048;
-
-__device__ inline uint16_t f32_to_bf16_rne(float v) {
-    const uint32_t u = __float_as_uint(v);
-    return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
-}
 
 __global__ __launch_bounds__(256) void zero_kernel(float *__restrict__ y, size_t n) {
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
@@ -302,13 +299,19 @@ __device__ inline void mm_compute(const MmFrag<kF32W> &f, bool bok, float4_t *ac
                 acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(f.wb[t][j], xb[j], acc[t], 0, 0, 0);
         }
     } else {
+        // X = hi + lo in bf16 (hardware round-to-nearest-even conversions)
         bf16x8_t xh, xl;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float v = e < 4 ? xa[e] : xb[e - 4];
-            const uint16_t h = f32_to_bf16_rne(v);
-            xh[e] = (short)h;
-            xl[e] = (short)f32_to_bf16_rne(v - bf16_to_f32(h));
+        for (int e = 0; e < 8; e += 2) {
+            const float v0 = e < 4 ? xa[e] : xb[e - 4];
+            const float v1 = e < 4 ? xa[e + 1] : xb[e - 3];
+            const bf16x2_t h = bf16x2_t{(__bf16)v0, (__bf16)v1};
+            const bf16x2_t l = bf16x2_t{(__bf16)(v0 - (float)h[0]), (__bf16)(v1 - (float)h[1])};
+            const short2_t hs = __builtin_bit_cast(short2_t, h), ls = __builtin_bit_cast(short2_t, l);
+            xh[e] = hs[0];
+            xh[e + 1] = hs[1];
+            xl[e] = ls[0];
+            xl[e + 1] = ls[1];
         }
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
@@ -318,7 +321,10 @@ __device__ inline void mm_compute(const MmFrag<kF32W> &f, bool bok, float4_t *ac
     }
 }
 
-// grid.z selects one of two (W, Y) pairs with the same shape and X.
+// grid.z selects one of two (W, Y) pairs with the same shape and X. The four
+// waves of a workgroup take the same 64 rows and four consecutive k-slices;
+// their partial sums are added in LDS, so each workgroup issues one atomic
+// add per output (a quarter of the same-address atomics of one per wave).
 template <bool kF32W>
 __global__ __launch_bounds__(256) void mm_stream_kernel(const void *__restrict__ Wv0,
                                                         const void *__restrict__ Wv1,
@@ -327,45 +333,55 @@ __global__ __launch_bounds__(256) void mm_stream_kernel(const void *__restrict__
                                                         float *__restrict__ Y1, int n_rows,
                                                         int n_cols, int n_batch, int kslice) {
     constexpr int kDepth = 4;   // 32-column steps in flight
+    __shared__ float4_t red[4][4][64];   // [wave][row tile][lane]
     const void *Wv = blockIdx.z ? Wv1 : Wv0;
     float *Y = blockIdx.z ? Y1 : Y0;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int r0 = (blockIdx.x * 4 + wave) * 64;
-    if (r0 >= n_rows) return;
+    const int r0 = blockIdx.x * 64;
     const int i = lane & 15, q = lane >> 4;
-    const int k0 = blockIdx.y * kslice;
+    const int k0 = (blockIdx.y * 4 + wave) * kslice;
     const int k1 = min(k0 + kslice, n_cols);
     const bool bok = i < n_batch;
-    const float *xr = X + (size_t)(bok ? i : 0) * n_cols + 8 * q;
-    size_t roff[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) roff[t] = (size_t)min(r0 + 16 * t + i, n_rows - 1) * n_cols + 8 * q;
     float4_t acc[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc[t] = float4_t{0, 0, 0, 0};
-    // steps past k1 re-read the last step (never used)
-    auto clampk = [&](int k) { return k < k1 ? k : k1 - 32; };
-    MmFrag<kF32W> f[kDepth];
+    if (k0 < n_cols) {
+        const float *xr = X + (size_t)(bok ? i : 0) * n_cols + 8 * q;
+        size_t roff[4];
 #pragma unroll
-    for (int u = 0; u < kDepth; ++u) mm_load(f[u], Wv, xr, roff, clampk(k0 + 32 * u));
-    for (int k = k0; k < k1; k += 32 * kDepth) {
+        for (int t = 0; t < 4; ++t) roff[t] = (size_t)min(r0 + 16 * t + i, n_rows - 1) * n_cols + 8 * q;
+        // steps past k1 re-read the last step (never used)
+        auto clampk = [&](int k) { return k < k1 ? k : k1 - 32; };
+        MmFrag<kF32W> f[kDepth];
 #pragma unroll
         for (int u = 0; u < kDepth; ++u) {
-            // past k1 the fragment is a re-read of the last step: X is zeroed
-            // instead of branching, so the load pipeline never drains
-            mm_compute(f[u], bok && k + 32 * u < k1, acc);
-            mm_load(f[u], Wv, xr, roff, clampk(k + 32 * (u + kDepth)));
+            mm_load(f[u], Wv, xr, roff, clampk(k0 + 32 * u));
+            __builtin_amdgcn_sched_barrier(0);   // issue order = use order
+        }
+        for (int k = k0; k < k1; k += 32 * kDepth) {
+#pragma unroll
+            for (int u = 0; u < kDepth; ++u) {
+                // past k1 the fragment is a re-read of the last step: X is zeroed
+                // instead of branching, so the load pipeline never drains
+                mm_compute(f[u], bok && k + 32 * u < k1, acc);
+                mm_load(f[u], Wv, xr, roff, clampk(k + 32 * (u + kDepth)));
+                // keeps each refill where it is: otherwise the compiler sinks
+                // the loads next to their use and the ring drains
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
     }
-    // D[row 4q+r of tile t][batch i]
+#pragma unroll
+    for (int t = 0; t < 4; ++t) red[wave][t][lane] = acc[t];
+    __syncthreads();
+    // wave w adds row tile w of the four partials: D[row 4q+r of tile][batch i]
+    const float4_t sum = ((red[0][wave][lane] + red[1][wave][lane]) + red[2][wave][lane]) + red[3][wave][lane];
     if (!bok) return;
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int rr = r0 + 16 * t + 4 * q + r;
-            if (rr < n_rows) atomicAdd(&Y[(size_t)i * n_rows + rr], acc[t][r]);
-        }
+    for (int r = 0; r < 4; ++r) {
+        const int rr = r0 + 16 * wave + 4 * q + r;
+        if (rr < n_rows) atomicAdd(&Y[(size_t)i * n_rows + rr], sum[r]);
+    }
 }
 
 // k-slice so that the launch has about 2048 waves (two per SIMD; a multiple
@@ -392,7 +408,7 @@ int mm_launch(const void *W, const float *X, float *Y, int n_rows, int n_cols, i
                                dim3(256), 0, st, Y2, ny);
     }
     const int ks = mm_kslice(n_rows, n_cols, n_mats);
-    const dim3 grid((n_rows + 255) / 256, (n_cols + ks - 1) / ks, n_mats);
+    const dim3 grid((n_rows + 63) / 64, (n_cols + 4 * ks - 1) / (4 * ks), n_mats);
     hipLaunchKernelGGL(mm_stream_kernel<kF32W>, grid, dim3(256), 0, st, W, W2 ? W2 : W, X, Y,
                        Y2 ? Y2 : Y, n_rows, n_cols, n_batch, ks);
     return hip_status(hipGetLastError());

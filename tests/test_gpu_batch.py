@@ -26,6 +26,17 @@ def test_mul_mm_f32(gpu, n_rows, n_cols, nb):
     close(Y.cpu().numpy(), X.astype(np.float64) @ W.astype(np.float64).T, 1e-5)
 
 
+@pytest.mark.parametrize("n_rows,n_cols,nb", [(100, 64, 1), (256, 4096, 3), (300, 2080, 5), (4096, 32768, 16)])
+def test_mul_mm_bf16_shapes(gpu, n_rows, n_cols, nb):
+    W = synth.to_bf16_bits(synth.normal(52, 1, n_rows * n_cols) * 0.02).reshape(n_rows, n_cols)
+    X = synth.normal(52, 2, nb * n_cols).reshape(nb, n_cols)
+    Y = torch.full((nb, n_rows), 7.0, device=gpu)
+    ops.mul_mm_bf16_f32(t(W.view(np.int16), gpu).view(torch.bfloat16), t(X, gpu), Y, n_rows, n_cols, nb)
+    torch.cuda.synchronize()
+    ref = X.astype(np.float64) @ synth.bf16_bits_to_f32(W).astype(np.float64).T
+    close(Y.cpu().numpy(), ref, 1e-4)
+
+
 def test_rope_batch_inverse(gpu):
     n_seq, n_heads = 5, 64
     pos = np.array([3, 1000, 16383, 0, 77], np.int32)

@@ -62,6 +62,14 @@ __device__ inline void stage_query(float *qs, const float *q, int n_head) {
     }
 }
 
+// Zero heads of zero weight up to a multiple of 4 (they add +0 * 0 terms
+// after the real heads, which leaves every score bit-identical).
+__device__ inline void pad_heads(float *qs, float *ws, int n_head) {
+    const int n4 = (n_head + 3) & ~3;
+    for (int i = threadIdx.x; i < (n4 - n_head) * kMaxDim; i += 256) qs[n_head * kMaxDim + i] = 0.0f;
+    if ((int)threadIdx.x < n4 - n_head) ws[n_head + threadIdx.x] = 0.0f;
+}
+
 // head_dim 128, one key per thread, the key row in registers as fp32 and the
 // query and the weights in LDS: every multiply-add takes its query value from
 // a broadcast 16-byte LDS read (in-order returns, so the reads run several
@@ -94,34 +102,38 @@ __device__ __attribute__((always_inline)) inline float score_lds(const float *qs
             }
         }
     }
+    // four heads at a time: four independent dot chains keep the VALU busy
+    // (n_head is padded to a multiple of 4 with zero heads of zero weight)
     float s = 0.0f;
-    for (int h = 0; h < n_head; h += 2) {
+    for (int h = 0; h < n_head; h += 4) {
         const float4_t *q0 = reinterpret_cast<const float4_t *>(qs + h * kMaxDim);
-        const float4_t *q1 = q0 + kMaxDim / 4;
-        float d0 = 0.0f, d1 = 0.0f;
+        float d[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int v = 0; v < kMaxDim / 4; ++v) {
-            const float4_t a = q0[v], b = q1[v];
+            float4_t a[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                d0 = fmaf(a[e], k[4 * v + e], d0);
-                d1 = fmaf(b[e], k[4 * v + e], d1);
-            }
+            for (int z = 0; z < 4; ++z) a[z] = q0[z * (kMaxDim / 4) + v];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int z = 0; z < 4; ++z) d[z] = fmaf(a[z][e], k[4 * v + e], d[z]);
         }
-        s = fmaf(ws[h], d0 > 0.0f ? d0 : 0.0f, s);
-        s = fmaf(ws[h + 1], d1 > 0.0f ? d1 : 0.0f, s);
+#pragma unroll
+        for (int z = 0; z < 4; ++z) s = fmaf(ws[h + z], d[z] > 0.0f ? d[z] : 0.0f, s);
     }
     return s;
 }
 
 // The same score with four threads per key (adjacent lanes): thread `part`
-// computes the dot chains of heads [part n_head/4, (part+1) n_head/4); the
-// head sum then runs through the four lanes in head order (each continues
-// the running sum of the previous one), so the result is bit-identical to
-// score_lds. For short key lists, where one thread per key leaves most of
-// the chip idle. n_head % 8 == 0.
+// computes the dot chains of heads [part n_head/4, (part+1) n_head/4), and
+// the first lane of the key then sums all heads in head order, so the result
+// is bit-identical to score_lds. For short key lists, where one thread per key leaves most of
+// the chip idle. n_head % 16 == 0.
+constexpr int kRsRow = kMaxHeads + 4;   // relu values per key in LDS (padded: no bank conflicts)
+
 template <int kKind>
 __device__ __attribute__((always_inline)) inline float score_lds4(const float *qs, const float *ws,
+                                                                  float *rs,
                                                                   const void *__restrict__ keys,
                                                                   int c, int n_head, int part) {
     float k[kMaxDim];
@@ -147,40 +159,39 @@ __device__ __attribute__((always_inline)) inline float score_lds4(const float *q
             }
         }
     }
+    // dots of this part's heads, four at a time (a loop, not unrolled: the
+    // straight-line form overflows the instruction cache); the relu values go
+    // to LDS, then one lane per key runs the head sum in head order
     const int hp = n_head >> 2;
     const int h0 = part * hp;
-    float r[kMaxHeads / 4];
+    float *rk = rs + (threadIdx.x >> 2) * kRsRow;
+    for (int i = 0; i < hp; i += 4) {
+        const float4_t *q0 = reinterpret_cast<const float4_t *>(qs + (h0 + i) * kMaxDim);
+        float d[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int i = 0; i < kMaxHeads / 4; i += 2) {
-        r[i] = 0.0f;
-        r[i + 1] = 0.0f;
-        if (i < hp) {
-            const float4_t *q0 = reinterpret_cast<const float4_t *>(qs + (h0 + i) * kMaxDim);
-            const float4_t *q1 = q0 + kMaxDim / 4;
-            float d0 = 0.0f, d1 = 0.0f;
+        for (int v = 0; v < kMaxDim / 4; ++v) {
+            float4_t a[4];
 #pragma unroll
-            for (int v = 0; v < kMaxDim / 4; ++v) {
-                const float4_t a = q0[v], b = q1[v];
+            for (int z = 0; z < 4; ++z) a[z] = q0[z * (kMaxDim / 4) + v];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    d0 = fmaf(a[e], k[4 * v + e], d0);
-                    d1 = fmaf(b[e], k[4 * v + e], d1);
-                }
-            }
-            r[i] = d0 > 0.0f ? d0 : 0.0f;
-            r[i + 1] = d1 > 0.0f ? d1 : 0.0f;
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int z = 0; z < 4; ++z) d[z] = fmaf(a[z][e], k[4 * v + e], d[z]);
         }
+        *reinterpret_cast<float4_t *>(rk + h0 + i) =
+            float4_t{d[0] > 0.0f ? d[0] : 0.0f, d[1] > 0.0f ? d[1] : 0.0f,
+                     d[2] > 0.0f ? d[2] : 0.0f, d[3] > 0.0f ? d[3] : 0.0f};
     }
-    const int lane = threadIdx.x & 63;
+    // the four lanes of a key are in one wave: completing this wave's LDS
+    // stores (and fencing the compiler) makes the others' values visible
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     float s = 0.0f;
+    if (part == 0) {
+        for (int h = 0; h < n_head; h += 4) {
+            const float4_t r = *reinterpret_cast<const float4_t *>(rk + h);
 #pragma unroll
-    for (int k2 = 0; k2 < 4; ++k2) {
-        if (part == k2) {
-#pragma unroll
-            for (int i = 0; i < kMaxHeads / 4; ++i)
-                if (i < hp) s = fmaf(ws[h0 + i], r[i], s);
+            for (int z = 0; z < 4; ++z) s = fmaf(ws[h + z], r[z], s);
         }
-        s = __shfl(s, (lane & ~3) | k2);
     }
     return s;
 }
@@ -225,10 +236,7 @@ __global__ __launch_bounds__(256) void score_kernel(const float *__restrict__ q,
         __shared__ float ws[kMaxHeads];
         stage_query(qs, q, n_head);
         for (int i = threadIdx.x; i < n_head; i += 256) ws[i] = w[i];
-        if (n_head & 1) {   // a zero head with zero weight keeps the pairs aligned
-            for (int i = threadIdx.x; i < kMaxDim; i += 256) qs[n_head * kMaxDim + i] = 0.0f;
-            if (threadIdx.x == 0) ws[n_head] = 0.0f;
-        }
+        pad_heads(qs, ws, n_head);
         __syncthreads();
         if (c < n_comp) s = score_lds<kKind>(qs, ws, keys, c, n_head);
     } else {
@@ -692,16 +700,14 @@ __global__ __launch_bounds__(256) void score_batch_kernel(const BatchArgs A) {
     const float *wg = A.w + (size_t)s * A.n_head;
     stage_query(qs, qg, A.n_head);
     for (int i = threadIdx.x; i < A.n_head; i += 256) ws[i] = wg[i];
-    if (kSplit == 1 && (A.n_head & 1)) {   // a zero head with zero weight keeps the pairs aligned
-        for (int i = threadIdx.x; i < kMaxDim; i += 256) qs[A.n_head * kMaxDim + i] = 0.0f;
-        if (threadIdx.x == 0) ws[A.n_head] = 0.0f;
-    }
+    if (kSplit == 1) pad_heads(qs, ws, A.n_head);
     __syncthreads();
     if (c >= n) return;   // the kSplit lanes of a key leave together
+    __shared__ __attribute__((aligned(16))) float rs[kSplit == 1 ? 1 : 64 * kRsRow];
     const float v = kSplit == 1 ? score_lds<kKind>(qs, ws, A.keys, (int)(k0 + c), A.n_head)
-                                : score_lds4<kKind>(qs, ws, A.keys, (int)(k0 + c), A.n_head,
+                                : score_lds4<kKind>(qs, ws, rs, A.keys, (int)(k0 + c), A.n_head,
                                                     (int)threadIdx.x % kSplit);
-    if (threadIdx.x % kSplit == kSplit - 1) A.scores[k0 + c] = v;
+    if (threadIdx.x % kSplit == 0) A.scores[k0 + c] = v;
 }
 
 __device__ inline unsigned scan1024_excl(unsigned v, unsigned *wsum, unsigned *total) {
@@ -830,7 +836,7 @@ extern "C" int ds4hip_indexer_topk_positions_batch(
     A.n_recent = n_recent;
     A.pos_stride = pos_stride;
     // four threads per key (64 keys per block) when the heads split evenly
-    const bool split = n_head % 8 == 0;
+    const bool split = n_head % 16 == 0;
     const int keys_per_blk = split ? 64 : 256;
     int blk = 0;
     for (int s = 0; s < kMaxSeq; ++s) {

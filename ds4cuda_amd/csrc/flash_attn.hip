@@ -86,7 +86,8 @@ struct DecodeArgs {
     int s_max;
     float kq_log2;                   // log2(e) / sqrt(head_dim)
     long long total;
-    long long start[kMaxProb + 1];
+    long long start[kMaxProb + 1];   // row offset of each problem in the chunked row space
+    long long count[kMaxProb];       // rows of each problem (the space may pad between problems)
     // workspace
     float *ws_o;                     // [slot][64][512]
     float *ws_ml;                    // [slot][2][64]
@@ -672,7 +673,7 @@ __global__ __launch_bounds__(256) void decode_fp8_kernel(const DecodeArgs A) {
         while (s_start[p + 1] <= g0) ++p;
         const long long seg_end = min(g1, s_start[p + 1]);
         const long long r0 = g0 - s_start[p];
-        const long long r1 = seg_end - s_start[p];
+        const long long r1 = min(seg_end - s_start[p], A.count[p]);
         const int n_tiles = (int)((r1 - r0 + kTile - 1) / kTile);
         const long long seg_base = s_rowbase[p];
         const bool gather = A.phys != nullptr;
@@ -902,7 +903,7 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(const DecodeArgs A) {
         while (s_start[p + 1] <= g0) ++p;
         const long long seg_end = min(g1, s_start[p + 1]);
         const long long r0 = g0 - s_start[p];
-        const long long r1 = seg_end - s_start[p];
+        const long long r1 = min(seg_end - s_start[p], A.count[p]);
 
         half8_t qh[16], ql[16];
         load_q<true>(A, p, head, q, qh, ql);
@@ -1016,7 +1017,7 @@ __global__ __launch_bounds__(512, 1) void decode_w8_kernel(const DecodeArgs A) {
         while (s_start[p + 1] <= g0) ++p;
         const long long seg_end = min(g1, s_start[p + 1]);
         const long long r0 = g0 - s_start[p];
-        const long long r1 = seg_end - s_start[p];
+        const long long r1 = min(seg_end - s_start[p], A.count[p]);
         // even tile count: a trailing tile past the end is fully masked
         const int n_tiles = 2 * (int)((r1 - r0 + 2 * kTile - 1) / (2 * kTile));
         const long long seg_base = s_rowbase[p];
@@ -1246,7 +1247,7 @@ __global__ __launch_bounds__(256) void phys_kernel(const DecodeArgs A) {
         const int mid = (lo + hi + 1) >> 1;
         if (s_start[mid] <= gg) lo = mid; else hi = mid - 1;
     }
-    A.phys[g] = phys_row(A, lo, gg - s_start[lo]);
+    A.phys[g] = phys_row(A, lo, min(gg - s_start[lo], A.count[lo] - 1));
 }
 
 // One workgroup per (problem, head). The partial slots of the problem are
@@ -1265,7 +1266,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const DecodeArgs A) {
     const int h = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const float sink = A.sinks[(long long)p * A.sinks_stride + h] * kLog2e;
-    const long long b0 = s_start[p], b1 = s_start[p + 1];
+    const long long b0 = s_start[p], b1 = s_start[p] + A.count[p];
     long long s0 = 0, n_slot = 0;
     if (b1 > b0) {
         s0 = (b0 / A.chunk) * A.s_max;
@@ -1329,35 +1330,66 @@ struct Plan {
     int chunk = 0;
     int s_max = 0;
     size_t ws_bytes = 0;
+    long long start[kMaxProb + 1] = {};   // problem offsets in the chunked row space
 };
 
 size_t slot_bytes() { return (size_t)kH * kD * 4 + 2 * kH * 4 + 4; }
 
-// Chunk the concatenated rows so that about wg_per_cu workgroups run per CU,
-// each chunk a whole number of tiles and at least kMinChunk rows (small
-// steps get fewer, longer workgroups and fewer partials to merge); s_max
-// bounds the problems one chunk can touch.
-Plan make_plan(const long long *start, int n_prob, int wg_per_cu) {
+// Rows of work that one extra problem segment costs a workgroup (its Q
+// fragments and first tiles load before any compute, and it writes one
+// partial of 128 KB): about five 32-row tiles.
+constexpr long long kSegCostRows = 5 * kTile;
+
+// Chunks of whole tiles, at least kMinChunk rows, about wg_per_cu workgroups
+// per CU. Two layouts: (a) the problems' rows concatenated and cut evenly (a
+// chunk may span problem boundaries: s_max problems per chunk), or (b) every
+// problem cut separately, its first chunk aligned (one problem per chunk, a
+// few more chunks). (b) wins when chunks are short next to the per-segment
+// cost, e.g. a batch of 16 sequences of ~2000 selected rows.
+Plan make_plan(const long long *count, int n_prob, int wg_per_cu) {
     Plan pl;
-    const long long total = start[n_prob];
+    long long total = 0;
+    for (int p = 0; p < n_prob; ++p) total += count[p];
     const long long target = (long long)num_cus() * wg_per_cu;
-    long long chunk = total > 0 ? (total + target - 1) / target : kTile;
-    chunk = ((chunk + kTile - 1) / kTile) * kTile;
-    if (chunk < kMinChunk) chunk = kMinChunk;
-    pl.chunk = (int)chunk;
-    pl.n_wg = total > 0 ? (int)((total + chunk - 1) / chunk) : 0;
-    int smax = 1;
-    for (int w = 0; w < pl.n_wg; ++w) {
-        const long long a = (long long)w * chunk, b = std::min(a + chunk, total);
-        int cnt = 0;
-        for (int p = 0; p < n_prob; ++p)
-            if (start[p + 1] > a && start[p] < b) ++cnt;
-        smax = std::max(smax, cnt);
+    auto round_tile = [](long long x) { return ((x + kTile - 1) / kTile) * kTile; };
+    long long chunk_a = total > 0 ? round_tile((total + target - 1) / target) : kTile;
+    if (chunk_a < kMinChunk) chunk_a = kMinChunk;
+    int smax_a = 1;
+    {
+        long long st = 0;
+        const long long n_wg = total > 0 ? (total + chunk_a - 1) / chunk_a : 0;
+        std::vector<int> segs((size_t)std::max<long long>(n_wg, 1), 0);
+        for (int p = 0; p < n_prob; ++p) {
+            if (count[p] > 0)
+                for (long long w = st / chunk_a; w <= (st + count[p] - 1) / chunk_a; ++w) ++segs[(size_t)w];
+            st += count[p];
+        }
+        for (int c : segs) smax_a = std::max(smax_a, c);
     }
-    pl.s_max = smax;
-    const size_t slots = (size_t)std::max(pl.n_wg, 1) * smax;
+    long long chunk_b = chunk_a;
+    auto wgs_b = [&](long long ch) {
+        long long n = 0;
+        for (int p = 0; p < n_prob; ++p) n += (count[p] + ch - 1) / ch;
+        return n;
+    };
+    while (wgs_b(chunk_b) > std::max<long long>(target, n_prob)) chunk_b += kTile;
+    const bool use_b = smax_a > 1 && chunk_b + kSegCostRows < chunk_a + smax_a * kSegCostRows;
+    pl.start[0] = 0;
+    if (use_b) {
+        pl.chunk = (int)chunk_b;
+        for (int p = 0; p < n_prob; ++p)
+            pl.start[p + 1] = pl.start[p] + ((count[p] + chunk_b - 1) / chunk_b) * chunk_b;
+        pl.s_max = 1;
+    } else {
+        pl.chunk = (int)chunk_a;
+        for (int p = 0; p < n_prob; ++p) pl.start[p + 1] = pl.start[p] + count[p];
+        pl.s_max = smax_a;
+    }
+    const long long space = pl.start[n_prob];
+    pl.n_wg = space > 0 ? (int)((space + pl.chunk - 1) / pl.chunk) : 0;
+    const size_t slots = (size_t)std::max(pl.n_wg, 1) * pl.s_max;
     pl.ws_bytes = slots * ((size_t)kH * kD * 4 + 2 * kH * 4) + slots * 4 + 256 * 4 +
-                  (size_t)(total + kTile) * sizeof(long long);
+                  (size_t)(space + kTile) * sizeof(long long);
     return pl;
 }
 
@@ -1411,13 +1443,9 @@ int launch(DecodeArgs &A, const Plan &pl, hipStream_t st, int phases = 3) {
 extern "C" int ds4hip_flash_attn_decode_fp8_workspace_size(const long long *n_rows_per_prob,
                                                            int n_prob, size_t *bytes) {
     if (!bytes || n_prob <= 0 || n_prob > kMaxProb || !n_rows_per_prob) return kEINVAL;
-    long long start[kMaxProb + 1];
-    start[0] = 0;
-    for (int p = 0; p < n_prob; ++p) {
+    for (int p = 0; p < n_prob; ++p)
         if (n_rows_per_prob[p] < 0) return kEINVAL;
-        start[p + 1] = start[p] + n_rows_per_prob[p];
-    }
-    *bytes = make_plan(start, n_prob, kFp8WgPerCu).ws_bytes;
+    *bytes = make_plan(n_rows_per_prob, n_prob, kFp8WgPerCu).ws_bytes;
     return 0;
 }
 
@@ -1438,12 +1466,12 @@ extern "C" int ds4hip_flash_attn_decode_fp8(
         while ((1 << page_shift) < page_rows) ++page_shift;
     }
     DecodeArgs A = {};
-    A.start[0] = 0;
     for (int p = 0; p < n_prob; ++p) {
         if (n_rows_per_prob[p] < 0) return ds4hip_set_last_error(kEINVAL);
-        A.start[p + 1] = A.start[p] + n_rows_per_prob[p];
+        A.count[p] = n_rows_per_prob[p];
     }
-    const Plan pl = make_plan(A.start, n_prob, kFp8WgPerCu);
+    const Plan pl = make_plan(n_rows_per_prob, n_prob, kFp8WgPerCu);
+    for (int p = 0; p <= n_prob; ++p) A.start[p] = pl.start[p];
     if (workspace_bytes < pl.ws_bytes) return ds4hip_set_last_error(kEINVAL);
     A.q = q;
     A.q_stride = q_stride;
@@ -1478,9 +1506,10 @@ namespace {
 int run_f32(const float *Q, const float *raw, int n_raw, const float *comp, int n_comp,
             const int32_t *allowed, const float *sinks, float *out, hipStream_t st) {
     DecodeArgs A = {};
-    A.start[0] = 0;
-    A.start[1] = (long long)n_raw + n_comp;
-    const Plan pl = make_plan(A.start, 1, 2);
+    A.count[0] = (long long)n_raw + n_comp;
+    const Plan pl = make_plan(A.count, 1, 2);
+    A.start[0] = pl.start[0];
+    A.start[1] = pl.start[1];
     void *ws = nullptr;
     hipError_t e = hipMallocAsync(&ws, pl.ws_bytes, st);
     if (e != hipSuccess) return hip_status(e);

@@ -1255,59 +1255,43 @@ __global__ __launch_bounds__(256) void phys_kernel(const DecodeArgs A) {
 // independent; each lane covers 8 of the 512 dims. The max over the slots
 // (and the sink) is taken first, then every wave accumulates its slots
 // rescaled to that max, and the 4 wave sums are added in LDS in wave order.
-// One block per (problem, head): combine the partials with the sink.
-__global__ __launch_bounds__(256) void decode_merge_kernel(const DecodeArgs A) {
-    __shared__ long long s_start[kMaxProb + 1];
-    __shared__ float red_m[4];
-    __shared__ float red_l[4];
-    __shared__ float4_t red_o[4][128];
-    stage_start(A, s_start);
+// One block per (problem, head): combine the partials with the sink. Thread t
+// owns dims 4t..4t+3; the slot loop is unrolled so that several slots' loads
+// are in flight at once.
+__global__ __launch_bounds__(128) void decode_merge_kernel(const DecodeArgs A) {
     const int p = blockIdx.x;
     const int h = blockIdx.y;
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int tid = threadIdx.x;
     const float sink = A.sinks[(long long)p * A.sinks_stride + h] * kLog2e;
-    const long long b0 = s_start[p], b1 = s_start[p] + A.count[p];
+    const long long b0 = A.start[p], b1 = b0 + A.count[p];
     long long s0 = 0, n_slot = 0;
     if (b1 > b0) {
         s0 = (b0 / A.chunk) * A.s_max;
         n_slot = ((b1 - 1) / A.chunk) * A.s_max + A.s_max - s0;
     }
-    // max over this problem's partials
-    float mx = -INFINITY;
-    for (long long i = tid; i < n_slot; i += 256) {
+    float mx = sink;
+#pragma unroll 4
+    for (long long i = 0; i < n_slot; ++i) {
         const long long slot = s0 + i;
-        if (A.ws_prob[slot] == p) mx = fmaxf(mx, A.ws_ml[slot * 2 * kH + h]);
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-    if (lane == 0) red_m[wv] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3])), sink);
-    // weighted sums, slots strided over the waves
-    float4_t acc0 = float4_t{0, 0, 0, 0}, acc1 = acc0;
-    float den = 0.0f;
-    for (long long i = wv; i < n_slot; i += 4) {
-        const long long slot = s0 + i;
-        if (A.ws_prob[slot] != p) continue;
         const float m = A.ws_ml[slot * 2 * kH + h];
-        if (m == -INFINITY) continue;
+        if (A.ws_prob[slot] == p) mx = fmaxf(mx, m);
+    }
+    float den = __builtin_amdgcn_exp2f(sink - mx);
+    float4_t acc = float4_t{0, 0, 0, 0};
+#pragma unroll 4
+    for (long long i = 0; i < n_slot; ++i) {
+        const long long slot = s0 + i;
+        const int pr = A.ws_prob[slot];
+        const float m = A.ws_ml[slot * 2 * kH + h];
+        const float l = A.ws_ml[slot * 2 * kH + kH + h];
+        const float4_t o = reinterpret_cast<const float4_t *>(A.ws_o + slot * (kH * kD) + h * kD)[tid];
+        const bool use = pr == p && m != -INFINITY;
         const float sc = __builtin_amdgcn_exp2f(m - mx);
-        den += A.ws_ml[slot * 2 * kH + kH + h] * sc;
-        const float4_t *src = reinterpret_cast<const float4_t *>(A.ws_o + slot * (kH * kD) + h * kD) + lane;
-        acc0 += src[0] * sc;
-        acc1 += src[64] * sc;
+        den += use ? l * sc : 0.0f;
+        acc = use ? acc + o * sc : acc;   // a select: other problems' slots may hold anything
     }
-    red_o[wv][lane] = acc0;
-    red_o[wv][64 + lane] = acc1;
-    if (lane == 0) red_l[wv] = den;
-    __syncthreads();
-    if (tid < 128) {
-        const float denom = __builtin_amdgcn_exp2f(sink - mx) + ((red_l[0] + red_l[1]) + red_l[2]) + red_l[3];
-        const float4_t o = ((red_o[0][tid] + red_o[1][tid]) + red_o[2][tid]) + red_o[3][tid];
-        // lane t of the first 64 holds dims 4t..4t+3, the next 64 dims 256+4t..
-        *reinterpret_cast<float4_t *>(A.out + (long long)p * A.out_stride + h * kD + 4 * tid) =
-            o * (1.0f / denom);
-    }
+    *reinterpret_cast<float4_t *>(A.out + (long long)p * A.out_stride + h * kD + 4 * tid) = acc * (1.0f / den);
+}
 }
 
 // ---- host-side planning -----------------------------------------------------------
@@ -1434,7 +1418,7 @@ int launch(DecodeArgs &A, const Plan &pl, hipStream_t st, int phases = 3) {
         if (e) return e;
     }
     if (phases & 2)
-        hipLaunchKernelGGL(decode_merge_kernel, dim3(A.n_prob, kH), dim3(256), 0, st, A);
+        hipLaunchKernelGGL(decode_merge_kernel, dim3(A.n_prob, kH), dim3(128), 0, st, A);
     return hip_status(hipGetLastError());
 }
 

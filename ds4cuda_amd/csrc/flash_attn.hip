@@ -955,7 +955,7 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(const DecodeArgs A) {
 // writes them to the f16 V tile of dims d (double-buffered: the two waves of a
 // dim quarter share it) and computes the partial S of its 16 rows for all 64
 // heads over its dims (16 MFMAs). Each wave owns the softmax of 8 heads (sum
-// of the four dim partials, lazy rescale, P in f16) and wave (d, hh) adds
+// of the four dim partials, exact running max, P in f16) and wave (d, hh) adds
 // P . V_d for heads [32 hh, 32 hh + 32) over all 32 rows. The softmax of tile t
 // runs in the same barrier interval as the dequantize and partial S of tile
 // t + 1 (S partials and V tiles double-buffered by tile parity), P . V(t) in
@@ -1139,9 +1139,10 @@ __global__ __launch_bounds__(512, 1) void decode_w8_kernel(const DecodeArgs A) {
                     tmax = fmaxf(tmax, s4[r]);
                 }
                 tmax = xmax_8_16_32(tmax);
-                // lazy rescale: the reference point moves only when the tile max
-                // exceeds it by more than 8 (log2 units)
-                const bool bump = tmax > m_run + 8.0f;
+                // the reference point follows the running max exactly (the
+                // largest P of a head is 1, exact in f16), so O is rescaled
+                // whenever the max grows; after the first tiles that is rare
+                const bool bump = tmax > m_run;
                 const float m_new = bump ? tmax : m_run;
                 const bool none = m_new == -INFINITY;
                 const float alpha = (bump && m_run != -INFINITY) ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
@@ -1291,7 +1292,6 @@ __global__ __launch_bounds__(128) void decode_merge_kernel(const DecodeArgs A) {
         acc = use ? acc + o * sc : acc;   // a select: other problems' slots may hold anything
     }
     *reinterpret_cast<float4_t *>(A.out + (long long)p * A.out_stride + h * kD + 4 * tid) = acc * (1.0f / den);
-}
 }
 
 // ---- host-side planning -----------------------------------------------------------

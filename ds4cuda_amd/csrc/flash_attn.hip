@@ -1150,9 +1150,11 @@ __global__ __launch_bounds__(512, 1) void decode_w8_kernel(const DecodeArgs A) {
                 float psum = 0.0f;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const float pv = none ? 0.0f : __builtin_amdgcn_exp2f(s4[r] - m_new);
-                    psum += pv;
-                    pf[r] = (half_t)pv;
+                    // l sums the f16 values that P . V uses: O / l is then an exact
+                    // weighted mean whose weights carry only the f16 rounding
+                    const half_t ph = (half_t)(none ? 0.0f : __builtin_amdgcn_exp2f(s4[r] - m_new));
+                    psum += (float)ph;
+                    pf[r] = ph;
                 }
                 l_run = l_run * alpha + psum;
                 m_run = m_new;

@@ -955,7 +955,7 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(const DecodeArgs A) {
 // writes them to the f16 V tile of dims d (double-buffered: the two waves of a
 // dim quarter share it) and computes the partial S of its 16 rows for all 64
 // heads over its dims (16 MFMAs). Each wave owns the softmax of 8 heads (sum
-// of the four dim partials, exact running max, P in f16) and wave (d, hh) adds
+// of the four dim partials, exact running max, P as f16 hi + lo) and wave (d, hh) adds
 // P . V_d for heads [32 hh, 32 hh + 32) over all 32 rows. The softmax of tile t
 // runs in the same barrier interval as the dequantize and partial S of tile
 // t + 1 (S partials and V tiles double-buffered by tile parity), P . V(t) in
@@ -986,7 +986,7 @@ template <int kMode>
 __global__ __launch_bounds__(512, 1) void decode_w8_kernel(const DecodeArgs A) {
     __shared__ __attribute__((aligned(16))) uint8_t vtile[2][4][kVTileBytes];   // [tile & 1][d]
     __shared__ __attribute__((aligned(16))) float4_t sx[2][4][4][2][64];  // [tile & 1][head tile][d][row half][lane]
-    __shared__ __attribute__((aligned(16))) half8_t pbuf[4][64];          // [head tile][lane]
+    __shared__ __attribute__((aligned(16))) half8_t pbuf[2][4][64];       // [hi, lo][head tile][lane]
     __shared__ __attribute__((aligned(16))) float alpha_s[kH];
     __shared__ long long s_start[kMaxProb + 1];
     __shared__ long long s_rowbase[kMaxProb];
@@ -1146,31 +1146,35 @@ __global__ __launch_bounds__(512, 1) void decode_w8_kernel(const DecodeArgs A) {
                 const float m_new = bump ? tmax : m_run;
                 const bool none = m_new == -INFINITY;
                 const float alpha = (bump && m_run != -INFINITY) ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
-                half4_t pf;
+                // P as f16 hi + lo (p - hi): P . V then carries ~22 bits of P, so the
+                // f16 rounding of the weights does not show in O (a single f16 P
+                // leaves errors near 1e-3 of the output RMS when attention is diffuse)
+                half4_t pf, pl;
                 float psum = 0.0f;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    // l sums the f16 values that P . V uses: O / l is then an exact
-                    // weighted mean whose weights carry only the f16 rounding
-                    const half_t ph = (half_t)(none ? 0.0f : __builtin_amdgcn_exp2f(s4[r] - m_new));
-                    psum += (float)ph;
-                    pf[r] = ph;
+                    const float pv = none ? 0.0f : __builtin_amdgcn_exp2f(s4[r] - m_new);
+                    psum += pv;
+                    pf[r] = (half_t)pv;
+                    pl[r] = (half_t)(pv - (float)pf[r]);
                 }
                 l_run = l_run * alpha + psum;
                 m_run = m_new;
-                reinterpret_cast<uint2_t *>(&pbuf[own_hb][own_src])[own_h2] = __builtin_bit_cast(uint2_t, pf);
+                reinterpret_cast<uint2_t *>(&pbuf[0][own_hb][own_src])[own_h2] = __builtin_bit_cast(uint2_t, pf);
+                reinterpret_cast<uint2_t *>(&pbuf[1][own_hb][own_src])[own_h2] = __builtin_bit_cast(uint2_t, pl);
                 if (kk == 0) alpha_s[8 * wave + jj] = alpha;
             }
             lds_barrier();   // P and rescale factors of tile t visible
             // ---- O += P . V_d for heads 32 hh + [0, 32) ----
             const uint32_t vt = lds_addr(vtile[buf][d]);
             float4_t ar[2];
-            half8_t pa[2];
+            half8_t pa[2], pl[2];
             asm volatile(
-                "ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:64\n\t"
-                "ds_read_b128 %2, %5\n\tds_read_b128 %3, %5 offset:1024\n\t"
+                "ds_read_b128 %0, %6\n\tds_read_b128 %1, %6 offset:64\n\t"
+                "ds_read_b128 %2, %7\n\tds_read_b128 %3, %7 offset:1024\n\t"
+                "ds_read_b128 %4, %7 offset:4096\n\tds_read_b128 %5, %7 offset:5120\n\t"
                 "s_waitcnt lgkmcnt(0)"
-                : "=&v"(ar[0]), "=&v"(ar[1]), "=&v"(pa[0]), "=&v"(pa[1])
+                : "=&v"(ar[0]), "=&v"(ar[1]), "=&v"(pa[0]), "=&v"(pa[1]), "=&v"(pl[0]), "=&v"(pl[1])
                 : "v"(alpha_base + (32 * hh + 4 * q) * 4), "v"(pbuf_base + (2 * hh * 64 + lane) * 16));
             // rare (a reference point moved): rescale O before adding tile t
             const bool need = ar[0][0] != 1.0f || ar[0][1] != 1.0f || ar[0][2] != 1.0f ||
@@ -1195,15 +1199,24 @@ __global__ __launch_bounds__(512, 1) void decode_w8_kernel(const DecodeArgs A) {
                     : "=&v"(tb[0]), "=&v"(tb[1]), "=&v"(tb[2]), "=&v"(tb[3]), "=&v"(tb[4]),
                       "=&v"(tb[5]), "=&v"(tb[6]), "=&v"(tb[7])
                     : "v"(ab));
+                half8_t vb[4];
 #pragma unroll
-                for (int nb = 0; nb < 4; ++nb) {
-                    const half8_t vb = __builtin_bit_cast(
+                for (int nb = 0; nb < 4; ++nb)
+                    vb[nb] = __builtin_bit_cast(
                         half8_t, uint4_t{tb[2 * nb][0], tb[2 * nb][1], tb[2 * nb + 1][0], tb[2 * nb + 1][1]});
+                // hi products first, then lo: dependent MFMAs eight apart
+#pragma unroll
+                for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
                     for (int mb = 0; mb < 2; ++mb)
                         o[mb][4 * half + nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                            pa[mb], vb, o[mb][4 * half + nb], 0, 0, 0);
-                }
+                            pa[mb], vb[nb], o[mb][4 * half + nb], 0, 0, 0);
+#pragma unroll
+                for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+                    for (int mb = 0; mb < 2; ++mb)
+                        o[mb][4 * half + nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            pl[mb], vb[nb], o[mb][4 * half + nb], 0, 0, 0);
             }
             lds_barrier();   // partials of tile t+1 and V tile t+1 visible; P consumed
         };

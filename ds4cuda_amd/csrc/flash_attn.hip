@@ -459,6 +459,15 @@ __device__ inline void lds_ld128x8(uint32_t a, T *v) {
 }
 
 // Four 16-byte reads at a + 64*i and four at b + 1024*i, one wait.
+// Four 16-byte reads at a + 1024*i, one wait.
+__device__ inline void lds_ld128x4(uint32_t a, half8_t *v) {
+    asm volatile(
+        "ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:1024\n\t"
+        "ds_read_b128 %2, %4 offset:2048\n\tds_read_b128 %3, %4 offset:3072\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3])
+        : "v"(a));
+}
 __device__ inline void lds_ld_alpha_p(uint32_t a, uint32_t b, float4_t *ar, half8_t *pa) {
     asm volatile(
         "ds_read_b128 %0, %8\n\tds_read_b128 %1, %8 offset:64\n\t"
@@ -613,7 +622,7 @@ struct SplitState {
 // 16h + 4q + s/4, dims 16nb + 4(s&3)) come from the wave's V slice via
 // transposing reads, all 16 behind one wait.
 __device__ inline void pv_split(uint32_t vt_base, int j, int q, const half8_t *pa,
-                                float4_t (*o)[8]) {
+                                const half8_t *pl, float4_t (*o)[8]) {
             uint2_t tb[16];
             {
                 const uint32_t ab = vt_base + (4 * q + (j >> 2)) * kVRowBytes + 8 * (j & 3);
@@ -641,6 +650,9 @@ __device__ inline void pv_split(uint32_t vt_base, int j, int q, const half8_t *p
 #pragma unroll
                 for (int mb = 0; mb < 4; ++mb)
                     o[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[mb], vb, o[mb][nb], 0, 0, 0);
+#pragma unroll
+                for (int mb = 0; mb < 4; ++mb)
+                    o[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[mb], vb, o[mb][nb], 0, 0, 0);
             }
 }
 
@@ -650,7 +662,7 @@ __global__ __launch_bounds__(256) void decode_fp8_kernel(const DecodeArgs A) {
     __shared__ __attribute__((aligned(16))) uint8_t stages[kStages][kStageBytes];
     __shared__ __attribute__((aligned(16))) uint8_t vtile[4][kVTileBytes];
     __shared__ __attribute__((aligned(16))) float4_t sx[4][4][2][64];   // [owner][writer][h2][lane]
-    __shared__ __attribute__((aligned(16))) half8_t pbuf[4][64];        // [head block][lane]
+    __shared__ __attribute__((aligned(16))) half8_t pbuf[2][4][64];     // [hi, lo][head block][lane]
     __shared__ __attribute__((aligned(16))) float alpha_s[kH];
     __shared__ long long s_start[kMaxProb + 1];
     __shared__ long long s_rowbase[kMaxProb];   // LDS, so the ring loop issues no row loads
@@ -724,7 +736,7 @@ __global__ __launch_bounds__(256) void decode_fp8_kernel(const DecodeArgs A) {
             for (int nb = 0; nb < 8; ++nb) S.o[mb][nb] = float4_t{0, 0, 0, 0};
 
         float4_t ar[4];
-        half8_t pa[4];
+        half8_t pa[4], pl[4];
         int t = 0;
         while (t < n_tiles) {
         for (; t < n_tiles; ++t) {
@@ -806,14 +818,12 @@ __global__ __launch_bounds__(256) void decode_fp8_kernel(const DecodeArgs A) {
                     tmax = fmaxf(tmax, s[h2][r]);
                 }
             tmax = xmax_16_32(tmax);
-            // Lazy rescale: the reference point m_run moves only when the tile max
-            // exceeds it by more than 8 (log2 units); otherwise p <= 2^8, which f16
-            // P and the fp32 sums carry exactly as well.
-            const bool bump = tmax > S.m_run + 8.0f;
+            // exact running max as the reference point; P as f16 hi + lo
+            const bool bump = tmax > S.m_run;
             const float m_new = bump ? tmax : S.m_run;
             const bool none = m_new == -INFINITY;
             const float alpha = (bump && S.m_run != -INFINITY) ? __builtin_amdgcn_exp2f(S.m_run - m_new) : 1.0f;
-            half8_t pf;
+            half8_t pf, plo;
             float psum = 0.0f;
 #pragma unroll
             for (int h2 = 0; h2 < 2; ++h2)
@@ -822,17 +832,20 @@ __global__ __launch_bounds__(256) void decode_fp8_kernel(const DecodeArgs A) {
                     const float pv = none ? 0.0f : __builtin_amdgcn_exp2f(s[h2][r] - m_new);
                     psum += pv;
                     pf[4 * h2 + r] = (half_t)pv;
+                    plo[4 * h2 + r] = (half_t)(pv - (float)pf[4 * h2 + r]);
                 }
             S.l_run = S.l_run * alpha + psum;
             S.m_run = m_new;
             const uint32_t pbuf_base = lds_addr(pbuf);
             const uint32_t alpha_base = lds_addr(alpha_s);
             lds_st128(pbuf_base + (wave * 64 + lane) * 16, pf);
+            lds_st128(pbuf_base + 4096 + (wave * 64 + lane) * 16, plo);
             if (q == 0) lds_st32(alpha_base + (16 * wave + j) * 4, alpha);
             lds_barrier();   // B3: P and rescale factors of all heads visible
 
             // ---- 3. O_w += P . V_w --------------------------------------------------
             lds_ld_alpha_p(alpha_base + 16 * q, pbuf_base + lane * 16, ar, pa);
+            lds_ld128x4(pbuf_base + 4096 + lane * 16, pl);
             bool need_rescale = false;
 #pragma unroll
             for (int mb = 0; mb < 4; ++mb)
@@ -840,7 +853,7 @@ __global__ __launch_bounds__(256) void decode_fp8_kernel(const DecodeArgs A) {
                                 ar[mb][3] != 1.0f;
             need_rescale = __any(need_rescale);
             if (need_rescale) break;   // rare: the rescale runs outside the hot loop
-            pv_split(vt_base, j, q, pa, S.o);
+            pv_split(vt_base, j, q, pa, pl, S.o);
         }
         if (t < n_tiles) {
             // a softmax reference point moved: rescale O, then finish tile t
@@ -848,7 +861,7 @@ __global__ __launch_bounds__(256) void decode_fp8_kernel(const DecodeArgs A) {
             for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
                 for (int nb = 0; nb < 8; ++nb) S.o[mb][nb] *= ar[mb];
-            pv_split(vt_base, j, q, pa, S.o);
+            pv_split(vt_base, j, q, pa, pl, S.o);
             ++t;
         }
         }

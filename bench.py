@@ -70,7 +70,59 @@ def cpu_baseline(seed=0):
             "kind": "port",
             "sample": f"one layer of the workload ({n_kv} FP8 rows, 64 heads), oracle scalar C++; "
                       f"{threads} threads {tn*1e3:.1f} ms/layer, 1 thread {t1*1e3:.1f} ms/layer "
-                      f"({b / t1 / 1e9:.3f} GB/s)"}
+                      f"({b / t1 / 1e9:.3f} GB/s)",
+            "other_configs": cpu_other_configs(threads)}
+
+
+def cpu_other_configs(threads):
+    """The oracle on the other configs, bounded samples: cfg 1 in full, cfg 3
+    (indexer over 131072 keys, single thread, + decode of 2048 rows), cfg 4
+    (4 of the 2048 prefill queries, scaled to the chunk)."""
+    import ctypes as C
+    tests = os.path.join(os.path.dirname(os.path.abspath(__file__)), "tests")
+    if tests not in sys.path:
+        sys.path.insert(0, tests)
+    import oracle as O
+    from ds4cuda_amd import synth
+    res = {}
+    # cfg 1: 4096-row decode, one layer
+    x = synth.kv_rows(10, 1, 4096)
+    codes, sexp, tail, _ = O.fp8_quant_rows(x)
+    q = synth.bf16_bits_to_f32(synth.to_bf16_bits(synth.normal(10, 2, N_HEAD * HEAD_DIM)))
+    q = q.reshape(N_HEAD, HEAD_DIM)
+    sinks = synth.normal(10, 3, N_HEAD)
+    t0 = time.perf_counter()
+    O.attn_decode_fp8(q, codes, sexp, tail, np.arange(4096), sinks, n_threads=1)
+    res["cfg1_decode_4096_ms_1thread"] = round((time.perf_counter() - t0) * 1e3, 2)
+    # cfg 3: indexer scores + top-k (one thread), decode over the 2048 rows
+    n = 131072
+    keys = synth.to_bf16_bits(synth.normal(11, 1, n * 128))
+    qi = synth.bf16_bits_to_f32(synth.to_bf16_bits(synth.normal(11, 2, N_HEAD * 128)))
+    w = synth.normal(11, 3, N_HEAD).astype(np.float32)
+    scores = np.empty(n, np.float32)
+    pos = np.empty(2048, np.int32)
+    t0 = time.perf_counter()
+    O.lib().orc_indexer_scores(O.P(qi), O.P(w), O.P(keys), C.c_int(2), C.c_int(n), C.c_int(N_HEAD),
+                               C.c_int(128), O.P(scores))
+    O.lib().orc_topk_positions(O.P(scores), C.c_int(n), C.c_int(2048), C.c_int(128), O.P(pos))
+    t_idx = time.perf_counter() - t0
+    x = synth.kv_rows(12, 1, 2048)
+    codes, sexp, tail, _ = O.fp8_quant_rows(x)
+    t0 = time.perf_counter()
+    O.attn_decode_fp8(q, codes, sexp, tail, np.arange(2048), sinks, n_threads=threads)
+    t_dec = time.perf_counter() - t0
+    res["cfg3_indexer_ms_1thread"] = round(t_idx * 1e3, 1)
+    res["cfg3_decode_2048_ms"] = round(t_dec * 1e3, 2)
+    # cfg 4: 4 sampled queries of the 2048 (each over 8192 cached rows + its own prefix)
+    x = synth.kv_rows(13, 1, 8192 + 2048)
+    codes, sexp, tail, _ = O.fp8_quant_rows(x)
+    t0 = time.perf_counter()
+    for t in (0, 682, 1365, 2047):
+        O.attn_decode_fp8(q, codes, sexp, tail, np.arange(8192 + t + 1), sinks, n_threads=threads)
+    per_q = (time.perf_counter() - t0) / 4
+    res["cfg4_prefill_ms_est"] = round(per_q * 2048 * 1e3, 0)
+    res["cfg4_prefill_tflops_est"] = round(2.474035380224e12 / (per_q * 2048) / 1e12, 4)
+    return res
 
 
 def time_ms(fn, steps, warmup, stream):

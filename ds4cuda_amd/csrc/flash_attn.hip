@@ -1279,15 +1279,15 @@ __global__ __launch_bounds__(256) void phys_kernel(const DecodeArgs A) {
     A.phys[g] = phys_row(A, lo, min(gg - s_start[lo], A.count[lo] - 1));
 }
 
-// One workgroup per (problem, head). The partial slots of the problem are
-// spread over the 4 waves (slot i -> wave i % 4), so their loads are
-// independent; each lane covers 8 of the 512 dims. The max over the slots
-// (and the sink) is taken first, then every wave accumulates its slots
-// rescaled to that max, and the 4 wave sums are added in LDS in wave order.
-// One block per (problem, head): combine the partials with the sink. Thread t
-// owns dims 4t..4t+3; the slot loop is unrolled so that several slots' loads
-// are in flight at once.
+// One block per (problem, head): combine the partials with the sink. The
+// per-slot scalars (problem id, running max, sum) are read with vector loads,
+// one slot per thread, so their latencies overlap (a scalar-load loop pays one
+// L2 round trip per slot); the slots' scale factors then go through LDS and
+// thread t accumulates dims 4t..4t+3 over the slots in slot order, several
+// slots' 16-byte loads in flight at once.
 __global__ __launch_bounds__(128) void decode_merge_kernel(const DecodeArgs A) {
+    __shared__ float s_sc[128], s_dl[128];
+    __shared__ float s_mx[2];
     const int p = blockIdx.x;
     const int h = blockIdx.y;
     const int tid = threadIdx.x;
@@ -1299,25 +1299,41 @@ __global__ __launch_bounds__(128) void decode_merge_kernel(const DecodeArgs A) {
         n_slot = ((b1 - 1) / A.chunk) * A.s_max + A.s_max - s0;
     }
     float mx = sink;
-#pragma unroll 4
-    for (long long i = 0; i < n_slot; ++i) {
+    for (long long i = tid; i < n_slot; i += 128) {
         const long long slot = s0 + i;
         const float m = A.ws_ml[slot * 2 * kH + h];
         if (A.ws_prob[slot] == p) mx = fmaxf(mx, m);
     }
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if ((tid & 63) == 0) s_mx[tid >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(s_mx[0], s_mx[1]);
     float den = __builtin_amdgcn_exp2f(sink - mx);
     float4_t acc = float4_t{0, 0, 0, 0};
-#pragma unroll 4
-    for (long long i = 0; i < n_slot; ++i) {
-        const long long slot = s0 + i;
-        const int pr = A.ws_prob[slot];
-        const float m = A.ws_ml[slot * 2 * kH + h];
-        const float l = A.ws_ml[slot * 2 * kH + kH + h];
-        const float4_t o = reinterpret_cast<const float4_t *>(A.ws_o + slot * (kH * kD) + h * kD)[tid];
-        const bool use = pr == p && m != -INFINITY;
-        const float sc = __builtin_amdgcn_exp2f(m - mx);
-        den += use ? l * sc : 0.0f;
-        acc = use ? acc + o * sc : acc;   // a select: other problems' slots may hold anything
+    for (long long base = 0; base < n_slot; base += 128) {
+        float sc = 0.0f, dl = 0.0f;
+        if (base + tid < n_slot) {
+            const long long slot = s0 + base + tid;
+            const float m = A.ws_ml[slot * 2 * kH + h];
+            const float l = A.ws_ml[slot * 2 * kH + kH + h];
+            if (A.ws_prob[slot] == p && m != -INFINITY) {
+                sc = __builtin_amdgcn_exp2f(m - mx);
+                dl = l * sc;
+            }
+        }
+        __syncthreads();   // the previous batch's readers are done
+        s_sc[tid] = sc;
+        s_dl[tid] = dl;
+        __syncthreads();
+        const int nb = (int)std::min<long long>(128, n_slot - base);
+        const float *o0 = A.ws_o + (s0 + base) * (kH * kD) + h * kD + 4 * tid;
+#pragma unroll 8
+        for (int j = 0; j < nb; ++j) {
+            const float c = s_sc[j];
+            const float4_t o = *reinterpret_cast<const float4_t *>(o0 + (long long)j * (kH * kD));
+            den += s_dl[j];
+            acc = c != 0.0f ? acc + o * c : acc;   // a select: unused slots may hold anything
+        }
     }
     *reinterpret_cast<float4_t *>(A.out + (long long)p * A.out_stride + h * kD + 4 * tid) = acc * (1.0f / den);
 }

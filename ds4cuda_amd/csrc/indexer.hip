@@ -20,12 +20,15 @@
 #include "ds4hip_common.h"
 #include "../../include/ds4hip.h"
 
+#include <algorithm>
+
 using namespace ds4hip;
 
 namespace {
 
 constexpr int kMaxHeads = 64;
 constexpr int kMaxDim = 128;
+constexpr int kQStride = kMaxDim + 4;   // query row stride in LDS for the four-thread form
 constexpr int kBins = 2048;
 
 __device__ inline unsigned ord_key(float s) {
@@ -43,9 +46,11 @@ __device__ inline float key_elem(const void *keys, size_t i) {
 
 // Copies the n_head x 128 fp32 query into LDS with all loads issued before
 // any store (a plain strided loop waits for each load in turn).
+template <int kStride = kMaxDim>
 __device__ inline void stage_query(float *qs, const float *q, int n_head) {
     if (reinterpret_cast<uintptr_t>(q) & 15) {   // unaligned caller buffer: plain copy
-        for (int i = threadIdx.x; i < n_head * kMaxDim; i += 256) qs[i] = q[i];
+        for (int i = threadIdx.x; i < n_head * kMaxDim; i += 256)
+            qs[(i / kMaxDim) * kStride + i % kMaxDim] = q[i];
         return;
     }
     const int n4 = n_head * kMaxDim / 4;
@@ -58,7 +63,8 @@ __device__ inline void stage_query(float *qs, const float *q, int n_head) {
 #pragma unroll
     for (int i = 0; i < kMaxHeads * kMaxDim / 4 / 256; ++i) {
         const int k = (int)threadIdx.x + 256 * i;
-        if (k < n4) reinterpret_cast<float4_t *>(qs)[k] = v[i];
+        if (k < n4)
+            *reinterpret_cast<float4_t *>(qs + (k / (kMaxDim / 4)) * kStride + 4 * (k % (kMaxDim / 4))) = v[i];
     }
 }
 
@@ -124,33 +130,32 @@ __device__ __attribute__((always_inline)) inline float score_lds(const float *qs
     return s;
 }
 
-// The same score with four threads per key (adjacent lanes): thread `part`
-// computes the dot chains of heads [part n_head/4, (part+1) n_head/4), and
-// the first lane of the key then sums all heads in head order, so the result
-// is bit-identical to score_lds. For short key lists, where one thread per key leaves most of
-// the chip idle. n_head % 16 == 0.
-constexpr int kRsRow = kMaxHeads + 4;   // relu values per key in LDS (padded: no bank conflicts)
-
+// head_dim 128 with four threads per key (adjacent lanes): thread `part`
+// holds dims [32 part, 32 part + 32) of the key and continues the dot chain of
+// part - 1 (handed over by a lane shift), so every head's dot is still one fma
+// chain over d ascending from +0, and part 3 runs the head sum in head order:
+// bit-identical to the one-thread form, with a quarter of the key registers
+// (several waves per SIMD hide the LDS latency of the query reads). In
+// iteration i, part p works on head i - p. The query rows sit kQStride floats
+// apart in LDS: with stride 128 the four parts' reads (offsets 32 p - 128 p)
+// would fall on the same banks; 132 spreads them over four bank groups.
+// load_key32 reads one part's dims.
 template <int kKind>
-__device__ __attribute__((always_inline)) inline float score_lds4(const float *qs, const float *ws,
-                                                                  float *rs,
-                                                                  const void *__restrict__ keys,
-                                                                  int c, int n_head, int part) {
-    float k[kMaxDim];
+__device__ inline void load_key32(const void *__restrict__ keys, int c, int part, float *k) {
     if (kKind == 0) {
         const float4_t *src = reinterpret_cast<const float4_t *>(
-            static_cast<const float *>(keys) + (size_t)c * kMaxDim);
+            static_cast<const float *>(keys) + (size_t)c * kMaxDim + 32 * part);
 #pragma unroll
-        for (int v = 0; v < kMaxDim / 4; ++v) {
+        for (int v = 0; v < 8; ++v) {
             const float4_t u = src[v];
 #pragma unroll
             for (int e = 0; e < 4; ++e) k[4 * v + e] = u[e];
         }
     } else {
         const uint4_t *src = reinterpret_cast<const uint4_t *>(
-            static_cast<const uint16_t *>(keys) + (size_t)c * kMaxDim);
+            static_cast<const uint16_t *>(keys) + (size_t)c * kMaxDim + 32 * part);
 #pragma unroll
-        for (int v = 0; v < kMaxDim / 8; ++v) {
+        for (int v = 0; v < 4; ++v) {
             const uint4_t u = src[v];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
@@ -159,41 +164,45 @@ __device__ __attribute__((always_inline)) inline float score_lds4(const float *q
             }
         }
     }
-    // dots of this part's heads, four at a time (a loop, not unrolled: the
-    // straight-line form overflows the instruction cache); the relu values go
-    // to LDS, then one lane per key runs the head sum in head order
-    const int hp = n_head >> 2;
-    const int h0 = part * hp;
-    float *rk = rs + (threadIdx.x >> 2) * kRsRow;
-    for (int i = 0; i < hp; i += 4) {
-        const float4_t *q0 = reinterpret_cast<const float4_t *>(qs + (h0 + i) * kMaxDim);
-        float d[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+}
+
+// Two keys (c0, c1) per group of four lanes: their chains are independent,
+// which gives the VALU two dependency chains to interleave. Scores are valid
+// in part 3.
+template <int kKind>
+__device__ __attribute__((always_inline)) inline void score_chain4x2(const float *qs, const float *ws,
+                                                                     const void *__restrict__ keys,
+                                                                     int c0, int c1, int n_head, int part,
+                                                                     float &s0, float &s1) {
+    float k0[32], k1[32];
+    load_key32<kKind>(keys, c0, part, k0);
+    load_key32<kKind>(keys, c1, part, k1);
+    float carry0 = 0.0f, carry1 = 0.0f;
+    s0 = 0.0f;
+    s1 = 0.0f;
+    for (int i = 0; i < n_head + 3; ++i) {
+        const int h = i - part;
+        const bool act = h >= 0 && h < n_head;
+        const float4_t *qv = reinterpret_cast<const float4_t *>(qs + (act ? h : 0) * kQStride + 32 * part);
+        float d0 = part == 0 ? 0.0f : carry0;
+        float d1 = part == 0 ? 0.0f : carry1;
 #pragma unroll
-        for (int v = 0; v < kMaxDim / 4; ++v) {
-            float4_t a[4];
+        for (int v = 0; v < 8; ++v) {
+            const float4_t a = qv[v];
 #pragma unroll
-            for (int z = 0; z < 4; ++z) a[z] = q0[z * (kMaxDim / 4) + v];
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-#pragma unroll
-                for (int z = 0; z < 4; ++z) d[z] = fmaf(a[z][e], k[4 * v + e], d[z]);
+            for (int e = 0; e < 4; ++e) {
+                d0 = fmaf(a[e], k0[4 * v + e], d0);
+                d1 = fmaf(a[e], k1[4 * v + e], d1);
+            }
         }
-        *reinterpret_cast<float4_t *>(rk + h0 + i) =
-            float4_t{d[0] > 0.0f ? d[0] : 0.0f, d[1] > 0.0f ? d[1] : 0.0f,
-                     d[2] > 0.0f ? d[2] : 0.0f, d[3] > 0.0f ? d[3] : 0.0f};
-    }
-    // the four lanes of a key are in one wave: completing this wave's LDS
-    // stores (and fencing the compiler) makes the others' values visible
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    float s = 0.0f;
-    if (part == 0) {
-        for (int h = 0; h < n_head; h += 4) {
-            const float4_t r = *reinterpret_cast<const float4_t *>(rk + h);
-#pragma unroll
-            for (int z = 0; z < 4; ++z) s = fmaf(ws[h + z], r[z], s);
+        // lane l takes lane l-1's chains (row_shr:1; part 0 ignores them)
+        carry0 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(d0), 0x111, 0xF, 0xF, false));
+        carry1 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(d1), 0x111, 0xF, 0xF, false));
+        if (part == 3 && act) {
+            s0 = fmaf(ws[h], d0 > 0.0f ? d0 : 0.0f, s0);
+            s1 = fmaf(ws[h], d1 > 0.0f ? d1 : 0.0f, s1);
         }
     }
-    return s;
 }
 
 // Any head_dim <= 128: the key row is zero-padded to 128 in registers and
@@ -229,19 +238,42 @@ __global__ __launch_bounds__(256) void score_kernel(const float *__restrict__ q,
     __shared__ unsigned lh[kBins];
     if (hist)
         for (int i = threadIdx.x; i < kBins; i += 256) lh[i] = 0;
+    __shared__ __attribute__((aligned(16))) float qs[kMaxHeads * kQStride];
+    __shared__ float ws[kMaxHeads];
+    if (kFull) {
+        // four threads per key, two keys per thread group (128 keys per pass);
+        // the workgroup loops over key groups so that the query is staged once
+        // per workgroup
+        stage_query<kQStride>(qs, q, n_head);
+        for (int i = threadIdx.x; i < n_head; i += 256) ws[i] = w[i];
+        __syncthreads();
+        const bool own = (threadIdx.x & 3) == 3;   // the scores are in part 3
+        for (int g = blockIdx.x; g * 128 < n_comp; g += gridDim.x) {
+            const int c0 = g * 128 + (int)(threadIdx.x >> 2), c1 = c0 + 64;
+            if (c0 < n_comp) {
+                float s0, s1;
+                score_chain4x2<kKind>(qs, ws, keys, c0, c1 < n_comp ? c1 : c0, n_head,
+                                      (int)(threadIdx.x & 3), s0, s1);
+                if (own) {
+                    scores[c0] = s0;
+                    if (hist && c0 < n_cand) atomicAdd(&lh[ord_key(s0) >> 21], 1u);
+                    if (c1 < n_comp) {
+                        scores[c1] = s1;
+                        if (hist && c1 < n_cand) atomicAdd(&lh[ord_key(s1) >> 21], 1u);
+                    }
+                }
+            }
+        }
+        if (hist) {
+            __syncthreads();
+            for (int i = threadIdx.x; i < kBins; i += 256)
+                if (lh[i]) atomicAdd(&hist[i], lh[i]);
+        }
+        return;
+    }
     const int c = blockIdx.x * 256 + threadIdx.x;
     float s = 0.0f;
-    if (kFull) {
-        __shared__ __attribute__((aligned(16))) float qs[kMaxHeads * kMaxDim];
-        __shared__ float ws[kMaxHeads];
-        stage_query(qs, q, n_head);
-        for (int i = threadIdx.x; i < n_head; i += 256) ws[i] = w[i];
-        pad_heads(qs, ws, n_head);
-        __syncthreads();
-        if (c < n_comp) s = score_lds<kKind>(qs, ws, keys, c, n_head);
-    } else {
-        __shared__ float qs[kMaxHeads * kMaxDim];
-        __shared__ float ws[kMaxHeads];
+    {
         for (int i = threadIdx.x; i < n_head * head_dim; i += 256) qs[i] = q[i];
         for (int i = threadIdx.x; i < n_head; i += 256) ws[i] = w[i];
         __syncthreads();
@@ -493,11 +525,24 @@ __global__ void scale_kernel(float *y, int n, float s) {
     if (i < n) y[i] *= s;
 }
 
+int num_cus_idx() {
+    static int n = 0;
+    if (n == 0) {
+        int dev = 0;
+        hipDeviceProp_t prop;
+        if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess)
+            n = prop.multiProcessorCount;
+        else
+            n = 256;
+    }
+    return n;
+}
+
 int launch_scores(const float *q, const float *w, const void *keys, int kind, int n_comp,
                   int n_head, int head_dim, float *scores, unsigned *hist, int n_cand,
                   hipStream_t st) {
-    const dim3 grid((n_comp + 255) / 256);
     const bool full = head_dim == kMaxDim;
+    const dim3 grid(full ? std::min((n_comp + 127) / 128, 4 * num_cus_idx()) : (n_comp + 255) / 256);
     switch (kind) {
     case 0:
         if (full) hipLaunchKernelGGL((score_kernel<0, true>), grid, dim3(256), 0, st, q, w, keys, n_comp, n_head, head_dim, scores, hist, n_cand);
@@ -693,21 +738,32 @@ __global__ __launch_bounds__(256) void score_batch_kernel(const BatchArgs A) {
 #pragma unroll
     for (int i = 0; i < kMaxSeq; ++i)
         if (i == s) first = A.blk0[i];
-    const int c = ((int)blockIdx.x - first) * (256 / kSplit) + (int)threadIdx.x / kSplit;
-    __shared__ __attribute__((aligned(16))) float qs[kMaxHeads * kMaxDim];
+    const int c = ((int)blockIdx.x - first) * (kSplit == 1 ? 256 : 128) + (int)threadIdx.x / kSplit;
+    __shared__ __attribute__((aligned(16))) float qs[kMaxHeads * kQStride];
     __shared__ float ws[kMaxHeads];
     const float *qg = A.q + (size_t)s * A.n_head * kMaxDim;
     const float *wg = A.w + (size_t)s * A.n_head;
-    stage_query(qs, qg, A.n_head);
+    if (kSplit == 1)
+        stage_query(qs, qg, A.n_head);
+    else
+        stage_query<kQStride>(qs, qg, A.n_head);
     for (int i = threadIdx.x; i < A.n_head; i += 256) ws[i] = wg[i];
     if (kSplit == 1) pad_heads(qs, ws, A.n_head);
     __syncthreads();
     if (c >= n) return;   // the kSplit lanes of a key leave together
-    __shared__ __attribute__((aligned(16))) float rs[kSplit == 1 ? 1 : 64 * kRsRow];
-    const float v = kSplit == 1 ? score_lds<kKind>(qs, ws, A.keys, (int)(k0 + c), A.n_head)
-                                : score_lds4<kKind>(qs, ws, rs, A.keys, (int)(k0 + c), A.n_head,
-                                                    (int)threadIdx.x % kSplit);
-    if (threadIdx.x % kSplit == 0) A.scores[k0 + c] = v;
+    if (kSplit == 1) {
+        A.scores[k0 + c] = score_lds<kKind>(qs, ws, A.keys, (int)(k0 + c), A.n_head);
+    } else {
+        // keys c and c + 64 of this block's 128
+        const int c1 = c + 64;
+        float s0, s1;
+        score_chain4x2<kKind>(qs, ws, A.keys, (int)(k0 + c), (int)(k0 + (c1 < n ? c1 : c)), A.n_head,
+                              (int)threadIdx.x % kSplit, s0, s1);
+        if (threadIdx.x % kSplit == kSplit - 1) {
+            A.scores[k0 + c] = s0;
+            if (c1 < n) A.scores[k0 + c1] = s1;
+        }
+    }
 }
 
 __device__ inline unsigned scan1024_excl(unsigned v, unsigned *wsum, unsigned *total) {
@@ -835,9 +891,9 @@ extern "C" int ds4hip_indexer_topk_positions_batch(
     A.top_k = top_k;
     A.n_recent = n_recent;
     A.pos_stride = pos_stride;
-    // four threads per key (64 keys per block) when the heads split evenly
-    const bool split = n_head % 16 == 0;
-    const int keys_per_blk = split ? 64 : 256;
+    // four threads per key, two keys per thread group (128 keys per block)
+    const bool split = true;   // the chained four-thread form works for any n_head
+    const int keys_per_blk = split ? 128 : 256;
     int blk = 0;
     for (int s = 0; s < kMaxSeq; ++s) {
         const int n = s < n_seq ? n_comp_host[s] : 0;

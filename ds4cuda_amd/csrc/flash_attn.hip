@@ -35,6 +35,7 @@
 
 #include <algorithm>
 #include <cstddef>
+#include <type_traits>
 #include <vector>
 
 using namespace ds4hip;
@@ -1263,6 +1264,394 @@ __global__ __launch_bounds__(512, 1) void decode_w8_kernel(const DecodeArgs A) {
         for (int s2 = slot_s; s2 < A.s_max; ++s2) A.ws_prob[(long long)blockIdx.x * A.s_max + s2] = -1;
 }
 
+// ---- warp-specialized FP8 decode: producers and consumers -------------------------
+//
+// One 8-wave workgroup per chunk, all 64 heads. Waves 0-3 are producers: wave
+// d loads dims [128 d, 128 d + 128) of all 32 rows of a tile straight into
+// registers two tiles ahead, dequantizes them, computes the partial S of the
+// tile for all 64 heads over its dims (32 MFMAs) and writes it to LDS; in the
+// next barrier interval it sums the four partials of heads 16 d + [0, 16),
+// runs their softmax (exact running max, P as f16 hi + lo), interleaved with
+// the next tile's QK MFMAs, and writes the tile's dequantized V slice. Waves
+// 4-7 are consumers: wave 4 + c adds P . V over dims [128 c, 128 c + 128) for
+// all 64 heads (64 MFMAs) two intervals behind the producers. With one
+// producer and one consumer per SIMD, the consumer's MFMAs run while the
+// producer's VALU work issues; one barrier per tile:
+//   interval i: producers: softmax(i - 1), V(i - 1) -> LDS, QK(i) -> S(i);
+//               consumers: P . V(i - 2).
+// S partials, P, the rescale factors and V are double-buffered by tile parity.
+
+// P in LDS: [buf][hi, lo][head tile][lane] f16 x 8: the MFMA A fragment of
+// lane (j, q) is rows 4 q + [0, 4) and 16 + 4 q + [0, 4) of head j, which is
+// what the producer lane (j, q) holds; both sides access it lane-contiguously.
+__device__ inline uint32_t pws_off(int buf, int hl, int hb, int lane) {
+    return (uint32_t)((((buf * 2 + hl) * 4 + hb) * 64 + lane) * 16);
+}
+
+template <int kMode>
+__global__ __launch_bounds__(512, 1) void decode_ws_kernel(const DecodeArgs A) {
+    __shared__ __attribute__((aligned(16))) uint8_t vtile[2][4][kVTileBytes];   // [tile & 1][dim quarter]
+    __shared__ __attribute__((aligned(16))) float4_t sx[2][4][4][2][64];  // [tile & 1][head tile][dim quarter][row half][lane]
+    __shared__ __attribute__((aligned(16))) uint8_t pws[2 * 2 * 4 * 64 * 16];
+    __shared__ __attribute__((aligned(16))) float alpha_s[2][kH];
+    __shared__ long long s_start[kMaxProb + 1];
+    __shared__ long long s_rowbase[kMaxProb];
+    for (int i = threadIdx.x; i < A.n_prob; i += blockDim.x)
+        s_rowbase[i] = A.row_base ? A.row_base[i] : (long long)i * A.row_base_stride;
+    stage_start(A, s_start);
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const bool producer = wave < 4;
+    const int d = wave & 3;   // dim quarter; for a consumer also its softmax head tile
+    const int j = lane & 15;
+    const int q = lane >> 4;
+
+    long long g0 = (long long)blockIdx.x * A.chunk;
+    const long long g1 = min(g0 + (long long)A.chunk, A.total);
+    int p = 0;
+    int slot_s = 0;
+    while (g0 < g1) {
+        while (s_start[p + 1] <= g0) ++p;
+        const long long seg_end = min(g1, s_start[p + 1]);
+        const long long r0 = g0 - s_start[p];
+        const long long r1 = min(seg_end - s_start[p], A.count[p]);
+        const int n_tiles = 2 * (int)((r1 - r0 + 2 * kTile - 1) / (2 * kTile));   // even, >= 2
+        const long long slot = (long long)blockIdx.x * A.s_max + slot_s;
+        if (producer) {
+            const long long seg_base = s_rowbase[p];
+            // kT: the wave of dims [384, 512): one FP8 block + the f16 RoPE tail
+            auto produce = [&](auto tail_c) {
+                constexpr bool kT = decltype(tail_c)::value;
+                // this lane's cache row in row half hh of tile t (past the end: the last row)
+                auto row_direct = [&](int t, int hh) -> long long {
+                    return seg_base + min(r0 + (long long)t * kTile + 16 * hh + j, r1 - 1);
+                };
+                auto row_gather = [&](int t, int hh) -> long long {
+                    const long long lr = min((long long)t * kTile + 16 * hh + j, r1 - 1 - r0);
+                    if (kMode == 1) return A.phys[g0 + lr];
+                    return seg_base + A.row_idx[(long long)p * A.row_idx_stride + r0 + lr];
+                };
+                // codes 128 d + 16 q + [0, 16) and 128 d + 64 + 16 q + [0, 16), or
+                // (kT) codes 384 + 16 q + [0, 16) and tail dims 16 q + [0, 16);
+                // e: the exponent word of blocks 2 d, 2 d + 1
+                struct Tl { uint4_t c0, c1, c2; uint32_t e; };
+                auto load = [&](long long r, Tl &T) {
+                    const uint8_t *cr = A.codes + r * kNope + 128 * d + 16 * q;
+                    T.c0 = *reinterpret_cast<const uint4_t *>(cr);
+                    if (kT) {
+                        const uint8_t *tr = reinterpret_cast<const uint8_t *>(A.tail) + r * (2 * kRot) + 32 * q;
+                        T.c1 = *reinterpret_cast<const uint4_t *>(tr);
+                        T.c2 = *reinterpret_cast<const uint4_t *>(tr + 16);
+                    } else {
+                        T.c1 = *reinterpret_cast<const uint4_t *>(cr + 64);
+                    }
+                    // only the word this wave uses: a loaded but unused register can be
+                    // reallocated before the load returns, which forces a full wait
+                    T.e = *reinterpret_cast<const uint32_t *>(A.sexp + r * 8 + (d >= 2 ? 4 : 0));
+                };
+                half8_t qh[4][4];   // Q^T fragments of all 64 heads over dims d
+#pragma unroll
+                for (int hb = 0; hb < 4; ++hb)
+#pragma unroll
+                    for (int ks = 0; ks < 4; ++ks) {
+                        const int dd = 64 * (2 * d + (ks >> 1)) + 16 * q + 8 * (ks & 1);
+                        const uint4_t v = *reinterpret_cast<const uint4_t *>(
+                            static_cast<const uint16_t *>(A.q) + (long long)p * A.q_stride +
+                            (long long)(16 * hb + j) * kD + dd);
+                        half8_t h;
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            h[2 * i] = (half_t)bf16_to_f32((uint16_t)(v[i] & 0xFFFF));
+                            h[2 * i + 1] = (half_t)bf16_to_f32((uint16_t)(v[i] >> 16));
+                        }
+                        qh[hb][ks] = h;
+                    }
+                auto dequant = [&](const Tl (&cur)[2], half8_t (&av)[2][4]) {
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh) {
+                        dequant16(cur[hh].c0, pow2f((int)(int8_t)((cur[hh].e >> (16 * (d & 1))) & 0xFF)),
+                                  av[hh][0], av[hh][1]);
+                        if (kT) {
+                            av[hh][2] = __builtin_bit_cast(half8_t, cur[hh].c1);
+                            av[hh][3] = __builtin_bit_cast(half8_t, cur[hh].c2);
+                        } else {
+                            dequant16(cur[hh].c1, pow2f((int)(int8_t)((cur[hh].e >> (16 * (d & 1) + 8)) & 0xFF)),
+                                      av[hh][2], av[hh][3]);
+                        }
+                    }
+                };
+                // loads of tile u + 2 into cur (gathered rows: those of tile u + 2
+                // are in ph_use; the row numbers of tile u + 3 are fetched first)
+                auto refill = [&](int u, Tl (&cur)[2], long long (&ph_use)[2], long long (&ph_next)[2]) {
+                    if (kMode != 0) {
+                        ph_next[0] = row_gather(u + 3, 0);
+                        ph_next[1] = row_gather(u + 3, 1);
+                        __builtin_amdgcn_sched_barrier(0);
+                        load(ph_use[0], cur[0]);
+                        load(ph_use[1], cur[1]);
+                    } else {
+                        load(row_direct(u + 2, 0), cur[0]);
+                        load(row_direct(u + 2, 1), cur[1]);
+                    }
+                };
+                // partial S of a tile over dims d
+                auto qk = [&](const half8_t (&av)[2][4], float4_t (&acc)[4][2]) {
+#pragma unroll
+                    for (int hb = 0; hb < 4; ++hb)
+#pragma unroll
+                        for (int hh = 0; hh < 2; ++hh) {
+                            float4_t c = float4_t{0, 0, 0, 0};
+#pragma unroll
+                            for (int ks = 0; ks < 4; ++ks)
+                                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[hh][ks], qh[hb][ks], c, 0, 0, 0);
+                            acc[hb][hh] = c;
+                        }
+                };
+                auto store_s = [&](int u, const float4_t (&acc)[4][2]) {
+#pragma unroll
+                    for (int hb = 0; hb < 4; ++hb)
+#pragma unroll
+                        for (int hh = 0; hh < 2; ++hh)
+                            sx[u & 1][hb][d][hh][lane] = acc[hb][hh];   // compiler-visible: MFMA hazard waits inserted
+                };
+                // V slice of tile t -> LDS: rows with bit 2 set swap the 16-byte
+                // halves of their 32-byte column groups, so that the 8 lanes of a
+                // 16-byte store phase cover all banks (the transposing reads
+                // apply the same swap)
+                auto store_v = [&](int t, const half8_t (&av)[2][4]) {
+                    const uint32_t sw = (j & 4) ? 16u : 0u;
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh) {
+                        const uint32_t vrow = lds_addr(vtile[t & 1][d]) + (16 * hh + j) * kVRowBytes + 32 * q;
+                        const uint32_t va = vrow + sw, vb = vrow + (16u - sw);
+                        asm volatile("ds_write_b128 %0, %2\n\tds_write_b128 %1, %3\n\t"
+                                     "ds_write_b128 %0, %4 offset:128\n\tds_write_b128 %1, %5 offset:128"
+                                     :: "v"(va), "v"(vb), "v"(av[hh][0]), "v"(av[hh][1]), "v"(av[hh][2]),
+                                        "v"(av[hh][3]) : "memory");
+                    }
+                };
+                float m_run = -INFINITY, l_run = 0.0f;   // head 16 d + j; l over this lane's rows
+                auto read_s = [&](int t, float4_t (&sa)[2]) {
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh)
+                        sa[hh] = ((sx[t & 1][d][0][hh][lane] + sx[t & 1][d][1][hh][lane]) +
+                                  sx[t & 1][d][2][hh][lane]) + sx[t & 1][d][3][hh][lane];
+                };
+                // softmax of tile t for heads 16 d + [0, 16) -> P, alpha
+                auto softmax = [&](int t, const float4_t (&sa)[2]) {
+                    const int b = t & 1;
+                    const long long left = r1 - (r0 + (long long)t * kTile);
+                    const int nv = left < kTile ? (int)left : kTile;   // valid rows of the tile
+                    float s8[2][4];
+                    float tmax = -INFINITY;
+    #pragma unroll
+                    for (int hh = 0; hh < 2; ++hh)
+    #pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            s8[hh][r] = 16 * hh + 4 * q + r < nv ? sa[hh][r] * A.kq_log2 : -INFINITY;
+                            tmax = fmaxf(tmax, s8[hh][r]);
+                        }
+                    tmax = xmax_16_32(tmax);
+                    // the reference point follows the running max exactly (the
+                    // largest P of a head is 1, exact in f16); O is rescaled when it grows
+                    const bool bump = tmax > m_run;
+                    const float m_new = bump ? tmax : m_run;
+                    const bool none = m_new == -INFINITY;
+                    const float alpha = (bump && m_run != -INFINITY) ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+                    float psum = 0.0f;
+                    // P as f16 hi + lo (p - hi): P . V then carries ~22 bits of P.
+                    // Element 4 hh + r of lane (j, q) is row 16 hh + 4 q + r of head
+                    // j, the K order of the V fragments.
+                    half8_t pf, pl;
+    #pragma unroll
+                    for (int hh = 0; hh < 2; ++hh)
+    #pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const float pv = none ? 0.0f : __builtin_amdgcn_exp2f(s8[hh][r] - m_new);
+                            psum += pv;
+                            pf[4 * hh + r] = (half_t)pv;
+                            pl[4 * hh + r] = (half_t)(pv - (float)pf[4 * hh + r]);
+                        }
+                    *reinterpret_cast<half8_t *>(pws + pws_off(b, 0, d, lane)) = pf;
+                    *reinterpret_cast<half8_t *>(pws + pws_off(b, 1, d, lane)) = pl;
+                    l_run = l_run * alpha + psum;
+                    m_run = m_new;
+                    if (q == 0) alpha_s[b][16 * d + j] = alpha;
+                };
+                // interval u (1 <= u < n): S(u - 1) reads, V(u - 1) -> LDS,
+                // dequantize u, loads of u + 2, QK(u) MFMAs with softmax(u - 1)
+                // interleaved into their issue slots, S(u) -> LDS
+                auto interval = [&](int u, Tl (&cur)[2], half8_t (&av)[2][4], long long (&ph_use)[2],
+                                    long long (&ph_next)[2]) {
+                    float4_t sa[2];
+                    read_s(u - 1, sa);
+                    store_v(u - 1, av);
+                    dequant(cur, av);
+                    __builtin_amdgcn_sched_barrier(0);
+                    refill(u, cur, ph_use, ph_next);
+                    __builtin_amdgcn_sched_barrier(0);
+                    float4_t acc[4][2];
+                    qk(av, acc);
+                    softmax(u - 1, sa);
+                    store_s(u, acc);
+#pragma unroll
+                    for (int i = 0; i < 32; ++i) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+                        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);   // three VALU
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                };
+
+                // prologue (issue order = the loop's: tile 0, [rows of tile 2], tile 1)
+                Tl T0[2], T1[2];
+                long long ph0[2] = {0, 0}, ph1[2] = {0, 0};
+                __builtin_amdgcn_sched_barrier(0);
+                if (kMode != 0) {
+                    const long long ra0 = row_gather(0, 0), ra1 = row_gather(0, 1);
+                    const long long rb0 = row_gather(1, 0), rb1 = row_gather(1, 1);
+                    __builtin_amdgcn_sched_barrier(0);
+                    load(ra0, T0[0]);
+                    load(ra1, T0[1]);
+                    __builtin_amdgcn_sched_barrier(0);
+                    ph0[0] = row_gather(2, 0);
+                    ph0[1] = row_gather(2, 1);
+                    __builtin_amdgcn_sched_barrier(0);
+                    load(rb0, T1[0]);
+                    load(rb1, T1[1]);
+                } else {
+                    load(row_direct(0, 0), T0[0]);
+                    load(row_direct(0, 1), T0[1]);
+                    __builtin_amdgcn_sched_barrier(0);
+                    load(row_direct(1, 0), T1[0]);
+                    load(row_direct(1, 1), T1[1]);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                half8_t av[2][4];
+                dequant(T0, av);   // interval 0
+                __builtin_amdgcn_sched_barrier(0);
+                refill(0, T0, ph0, ph1);
+                __builtin_amdgcn_sched_barrier(0);
+                {
+                    float4_t acc[4][2];
+                    qk(av, acc);
+                    store_s(0, acc);
+                }
+                lds_barrier();
+                for (int t = 1; t < n_tiles - 1; t += 2) {
+                    interval(t, T1, av, ph1, ph0);
+                    lds_barrier();
+                    interval(t + 1, T0, av, ph0, ph1);
+                    lds_barrier();
+                }
+                interval(n_tiles - 1, T1, av, ph1, ph0);
+                lds_barrier();
+                {   // interval n: softmax(n - 1), V(n - 1) -> LDS
+                    float4_t sa[2];
+                    read_s(n_tiles - 1, sa);
+                    store_v(n_tiles - 1, av);
+                    softmax(n_tiles - 1, sa);
+                }
+                lds_barrier();
+                lds_barrier();              // interval n + 1
+                // m, l of heads 16 d + j
+                const float l = xsum_16_32(l_run);
+                if (q == 0) {
+                    A.ws_ml[slot * 2 * kH + 16 * d + j] = m_run;
+                    A.ws_ml[slot * 2 * kH + kH + 16 * d + j] = l;
+                }
+            };
+            if (d == 3)
+                produce(std::true_type{});
+            else
+                produce(std::false_type{});
+        } else {
+            float4_t o[4][8];   // heads 16 hb + 4 q + r, dims 128 d + 16 nb + j
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+#pragma unroll
+                for (int c = 0; c < 8; ++c) o[a][c] = float4_t{0, 0, 0, 0};
+            // O += P(t) . V(t) over dims d for all 64 heads (after the rescale by alpha(t))
+            auto pv = [&](int t) {
+                const int b = t & 1;
+                half8_t pa[4], pl[4];
+                float4_t ar[4];
+#pragma unroll
+                for (int hb = 0; hb < 4; ++hb) {
+                    pa[hb] = *reinterpret_cast<const half8_t *>(pws + pws_off(b, 0, hb, lane));
+                    pl[hb] = *reinterpret_cast<const half8_t *>(pws + pws_off(b, 1, hb, lane));
+                    ar[hb] = *reinterpret_cast<const float4_t *>(&alpha_s[b][16 * hb + 4 * q]);
+                }
+                const uint32_t vt = lds_addr(vtile[b][d]);
+                uint2_t tb[2][8];
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                    const uint32_t ab = vt + (4 * q + (j >> 2)) * kVRowBytes + 8 * ((j & 3) ^ ((q & 1) << 1)) + 128 * half;
+                    asm volatile(
+                        "ds_read_b64_tr_b16 %0, %8\n\tds_read_b64_tr_b16 %1, %8 offset:4608\n\t"
+                        "ds_read_b64_tr_b16 %2, %8 offset:32\n\tds_read_b64_tr_b16 %3, %8 offset:4640\n\t"
+                        "ds_read_b64_tr_b16 %4, %8 offset:64\n\tds_read_b64_tr_b16 %5, %8 offset:4672\n\t"
+                        "ds_read_b64_tr_b16 %6, %8 offset:96\n\tds_read_b64_tr_b16 %7, %8 offset:4704"
+                        : "=&v"(tb[half][0]), "=&v"(tb[half][1]), "=&v"(tb[half][2]), "=&v"(tb[half][3]),
+                          "=&v"(tb[half][4]), "=&v"(tb[half][5]), "=&v"(tb[half][6]), "=&v"(tb[half][7])
+                        : "v"(ab));
+                }
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                bool need = false;
+#pragma unroll
+                for (int hb = 0; hb < 4; ++hb)
+                    need |= ar[hb][0] != 1.0f || ar[hb][1] != 1.0f || ar[hb][2] != 1.0f || ar[hb][3] != 1.0f;
+                if (__any(need)) {   // rare: a reference point moved
+#pragma unroll
+                    for (int hb = 0; hb < 4; ++hb)
+#pragma unroll
+                        for (int nb = 0; nb < 8; ++nb) o[hb][nb] *= ar[hb];
+                }
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                    half8_t vb[4];
+#pragma unroll
+                    for (int nb = 0; nb < 4; ++nb)
+                        vb[nb] = __builtin_bit_cast(half8_t, uint4_t{tb[half][2 * nb][0], tb[half][2 * nb][1],
+                                                                     tb[half][2 * nb + 1][0], tb[half][2 * nb + 1][1]});
+                    // hi products first, then lo: dependent MFMAs sixteen apart
+#pragma unroll
+                    for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+                        for (int hb = 0; hb < 4; ++hb)
+                            o[hb][4 * half + nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                pa[hb], vb[nb], o[hb][4 * half + nb], 0, 0, 0);
+#pragma unroll
+                    for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+                        for (int hb = 0; hb < 4; ++hb)
+                            o[hb][4 * half + nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                pl[hb], vb[nb], o[hb][4 * half + nb], 0, 0, 0);
+                }
+            };
+            lds_barrier();   // interval 0
+            lds_barrier();   // interval 1
+            for (int t = 0; t < n_tiles; ++t) {   // interval t + 2
+                pv(t);
+                lds_barrier();
+            }
+            float *wo = A.ws_o + slot * (kH * kD) + (4 * q) * kD + 128 * d + j;
+            asm volatile("" : "+v"(wo));
+#pragma unroll
+            for (int hb = 0; hb < 4; ++hb)
+#pragma unroll
+                for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) wo[(16 * hb + r) * kD + 16 * nb] = o[hb][nb][r];
+        }
+        if (threadIdx.x == 0) A.ws_prob[slot] = p;
+        ++slot_s;
+        g0 = seg_end;
+    }
+    if (threadIdx.x == 0)
+        for (int s2 = slot_s; s2 < A.s_max; ++s2) A.ws_prob[(long long)blockIdx.x * A.s_max + s2] = -1;
+}
+
 // Physical cache row of every logical row of a gathered step (row_idx and/or
 // page table), plus 32 rows of padding that repeat the last row.
 __global__ __launch_bounds__(256) void phys_kernel(const DecodeArgs A) {
@@ -1448,11 +1837,11 @@ int launch(DecodeArgs &A, const Plan &pl, hipStream_t st, int phases = 3) {
         }
         if (kFp8 && !kQf32) {
             if (idx_only)
-                hipLaunchKernelGGL(decode_w8_kernel<2>, dim3(pl.n_wg), dim3(512), 0, st, A);
+                hipLaunchKernelGGL(decode_ws_kernel<2>, dim3(pl.n_wg), dim3(512), 0, st, A);
             else if (A.phys)
-                hipLaunchKernelGGL(decode_w8_kernel<1>, dim3(pl.n_wg), dim3(512), 0, st, A);
+                hipLaunchKernelGGL(decode_ws_kernel<1>, dim3(pl.n_wg), dim3(512), 0, st, A);
             else
-                hipLaunchKernelGGL(decode_w8_kernel<0>, dim3(pl.n_wg), dim3(512), 0, st, A);
+                hipLaunchKernelGGL(decode_ws_kernel<0>, dim3(pl.n_wg), dim3(512), 0, st, A);
         }
         else if (kFp8)
             hipLaunchKernelGGL(decode_fp8_kernel<kQf32>, dim3(pl.n_wg), dim3(256), 0, st, A);

@@ -426,7 +426,7 @@ def main():
                    "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_BYTES_PER_LAUNCH,
-                     "kernel": "decode_w8_kernel<0> (direct rows)",
+                     "kernel": "decode_ws_kernel<0> (direct rows)",
                      "kernel_ms": round(k_ms, 4), "bytes_per_launch": step_bytes},
     }
     if not args.no_secondary:

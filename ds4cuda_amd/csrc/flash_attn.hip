@@ -51,6 +51,7 @@ constexpr int kVtStride = 40;    // halves per V^T line (32 rows + 8 pad)
 constexpr int kMaxProb = 128;
 constexpr int kMinChunk = 2 * kTile;
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLazyLog2 = 8.0f;   // decode softmax: reference point slack (log2 units)
 constexpr int kFp8WgPerCu = 1;   // the FP8 kernel's LDS ring allows one workgroup per CU
 
 struct DecodeArgs {
@@ -214,16 +215,6 @@ __device__ inline float xsum_16_32(float v) {
     v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
     auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
-}
-// Reductions over lanes that differ in bits 3..5 (xor 8 by a DPP row rotate).
-__device__ inline float ror8(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));
-}
-__device__ inline float xmax_8_16_32(float v) {
-    return xmax_16_32(fmaxf(v, ror8(v)));
-}
-__device__ inline float xsum_8_16_32(float v) {
-    return xsum_16_32(v + ror8(v));
 }
 
 // Barrier for this kernel's LDS pipeline: waits for this wave's LDS
@@ -481,11 +472,6 @@ __device__ inline void lds_ld_alpha_p(uint32_t a, uint32_t b, float4_t *ar, half
         : "v"(a), "v"(b));
 }
 
-// The wave's raw fragment of one half-tile row: two 16-byte chunks (its two
-// 64-dim blocks, 16 dims each) and the row's exponents. Issued from inline
-// assembly because the compiler would otherwise make each read wait for all
-// outstanding global->LDS copies; the trailing lgkmcnt wait makes the outputs
-// valid when the statement completes.
 // The three physical rows a lane needs from a phys slot (rows a, 16 + a and b).
 __device__ inline void lds_ld_phys3(uint32_t slot, int a, int b, long long &h0, long long &h1,
                                     long long &e) {
@@ -499,31 +485,13 @@ __device__ inline void lds_ld_phys3(uint32_t slot, int a, int b, long long &h0, 
     e = (long long)(((unsigned long long)z[1] << 32) | z[0]);
 }
 
-__device__ inline void read_wave_frag(const uint8_t *st, int wave, int h2, int j, int q,
-                                      uint4_t &c0, uint4_t &c1, uint2_t &e) {
-    uint32_t a0, a1;
-    if (wave < 3) {
-        a0 = lds_addr(st) + stage_off(2 * (2 * wave) + h2, j, q);
-        a1 = lds_addr(st) + stage_off(2 * (2 * wave + 1) + h2, j, q);
-    } else {
-        // block 6 codes, then tail dims 16q..16q+15 = f16 chunks 2q, 2q+1 of the
-        // tail, i.e. chunk (2q)&3 of tail block 7 + (q>>1) (two 16 B chunks)
-        a0 = lds_addr(st) + stage_off(2 * 6 + h2, j, q);
-        a1 = lds_addr(st) + stage_off(2 * (7 + (q >> 1)) + h2, j, (2 * q) & 3);
-    }
-    const uint32_t ae = lds_addr(st) + kSexpOff + (16 * h2 + j) * 8;
-    asm volatile(
-        "ds_read_b128 %0, %3\n\t"
-        "ds_read_b128 %1, %4\n\t"
-        "ds_read_b64 %2, %5\n\t"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(c0), "=&v"(c1), "=&v"(e)
-        : "v"(a0), "v"(a1), "v"(ae));
-}
-
-// Both half-tiles at once (one LDS round trip): c[h2][0..1] and e[h2] as
-// read_wave_frag; for wave 3, th[h2] is the second tail chunk (f16 chunk
-// 2q+1), otherwise untouched.
+// The wave's raw fragments of both half-tile rows at once (one LDS round
+// trip): two 16-byte chunks (its two 64-dim blocks, 16 dims each) in
+// c[h2][0..1] and the row's exponents in e[h2]; for wave 3, th[h2] is the
+// second tail chunk (f16 chunk 2q+1), otherwise untouched. Issued from inline
+// assembly because the compiler would otherwise make each read wait for all
+// outstanding global->LDS copies; the trailing lgkmcnt wait makes the outputs
+// valid when the statement completes.
 __device__ inline void read_wave_frags(const uint8_t *st, int wave, int j, int q, uint4_t (*c)[2],
                                        uint2_t *e, uint4_t *th) {
     const uint32_t ae0 = lds_addr(st) + kSexpOff + j * 8;
@@ -554,13 +522,6 @@ __device__ inline void read_wave_frags(const uint8_t *st, int wave, int j, int q
     }
 }
 
-// Second tail chunk of wave 3 (f16 chunk 2q+1).
-__device__ inline uint4_t read_tail_hi(const uint8_t *st, int h2, int j, int q) {
-    uint4_t v;
-    const uint32_t a = lds_addr(st) + stage_off(2 * (7 + (q >> 1)) + h2, j, (2 * q + 1) & 3);
-    asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(a));
-    return v;
-}
 
 __device__ inline void dequant16(uint4_t c, float sc, half8_t &a0, half8_t &a1) {
     a0 = make_half8(cvt_fp8x2<false>(c[0], sc), cvt_fp8x2<true>(c[0], sc),
@@ -961,309 +922,6 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(const DecodeArgs A) {
         for (int s2 = slot_s; s2 < A.s_max; ++s2) A.ws_prob[(long long)blockIdx.x * A.s_max + s2] = -1;
 }
 
-// ---- merged FP8 kernel: one 8-wave workgroup per chunk, all 64 heads -------------------
-//
-// Wave (d, hh) = (w & 3, w >> 2) loads rows 16 hh + [0, 16) of each 32-row tile
-// for dims [128 d, 128 d + 128) straight into registers two tiles ahead, so
-// every byte of the chunk is read once, by one lane. It dequantizes them,
-// writes them to the f16 V tile of dims d (double-buffered: the two waves of a
-// dim quarter share it) and computes the partial S of its 16 rows for all 64
-// heads over its dims (16 MFMAs). Each wave owns the softmax of 8 heads (sum
-// of the four dim partials, exact running max, P as f16 hi + lo) and wave (d, hh) adds
-// P . V_d for heads [32 hh, 32 hh + 32) over all 32 rows. The softmax of tile t
-// runs in the same barrier interval as the dequantize and partial S of tile
-// t + 1 (S partials and V tiles double-buffered by tile parity), P . V(t) in
-// the next one: two barriers per tile. Two waves per SIMD; one workgroup per CU.
-
-struct W8Tile {
-    uint4_t c0, c1;   // codes 128d + 16q; codes 128d + 64 + 16q or (d = 3) tail chunk 2q
-    uint4_t th;       // d = 3: tail chunk 2q + 1
-    uint2_t e;        // exponents of the row
-};
-
-__device__ inline void w8_load(const DecodeArgs &A, int d, int q, long long r, W8Tile &T) {
-    const uint8_t *cr = A.codes + r * kNope;
-    const uint8_t *tr = reinterpret_cast<const uint8_t *>(A.tail) + r * (2 * kRot);
-    const uint8_t *p1 = d < 3 ? cr + 128 * d + 64 + 16 * q : tr + 32 * q;
-    T.c0 = *reinterpret_cast<const uint4_t *>(cr + 128 * d + 16 * q);
-    T.c1 = *reinterpret_cast<const uint4_t *>(p1);
-    // unconditional (d < 3: a repeat of c1, an L1 hit): a load under a branch
-    // makes the compiler's load-count waits assume the shorter path
-    const uint8_t *p2 = d < 3 ? p1 : tr + 32 * q + 16;
-    T.th = *reinterpret_cast<const uint4_t *>(p2);
-    T.e = *reinterpret_cast<const uint2_t *>(A.sexp + r * 8);
-}
-
-// kMode: 0 direct rows (row_base + position), 1 the phys array (page tables),
-// 2 row_base + row_idx (position lists without pages, resolved here).
-template <int kMode>
-__global__ __launch_bounds__(512, 1) void decode_w8_kernel(const DecodeArgs A) {
-    __shared__ __attribute__((aligned(16))) uint8_t vtile[2][4][kVTileBytes];   // [tile & 1][d]
-    __shared__ __attribute__((aligned(16))) float4_t sx[2][4][4][2][64];  // [tile & 1][head tile][d][row half][lane]
-    __shared__ __attribute__((aligned(16))) half8_t pbuf[2][4][64];       // [hi, lo][head tile][lane]
-    __shared__ __attribute__((aligned(16))) float alpha_s[kH];
-    __shared__ long long s_start[kMaxProb + 1];
-    __shared__ long long s_rowbase[kMaxProb];
-    for (int i = threadIdx.x; i < A.n_prob; i += blockDim.x)
-        s_rowbase[i] = A.row_base ? A.row_base[i] : (long long)i * A.row_base_stride;
-    stage_start(A, s_start);
-
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int d = wave & 3, hh = wave >> 2;
-    const int j = lane & 15;
-    const int q = lane >> 4;
-    const uint32_t pbuf_base = lds_addr(pbuf);
-    const uint32_t alpha_base = lds_addr(alpha_s);
-    // softmax ownership: wave w owns heads 8w + [0, 8) (head tile w >> 1); lane
-    // (jj, kk) holds rows 16 h2 + 4 kq + [0, 4) of head jj
-    const int own_hb = wave >> 1;
-    const int jj = lane & 7, kk = lane >> 3;
-    const int own_h2 = kk >> 2, own_kq = kk & 3;
-    const int own_src = 8 * (wave & 1) + jj + 16 * own_kq;
-    const int own_sx = own_src ^ (own_kq & 1 ? 8 : 0);   // the stores' lane swizzle
-
-    long long g0 = (long long)blockIdx.x * A.chunk;
-    const long long g1 = min(g0 + (long long)A.chunk, A.total);
-    int p = 0;
-    int slot_s = 0;
-    while (g0 < g1) {
-        while (s_start[p + 1] <= g0) ++p;
-        const long long seg_end = min(g1, s_start[p + 1]);
-        const long long r0 = g0 - s_start[p];
-        const long long r1 = min(seg_end - s_start[p], A.count[p]);
-        // even tile count: a trailing tile past the end is fully masked
-        const int n_tiles = 2 * (int)((r1 - r0 + 2 * kTile - 1) / (2 * kTile));
-        const long long seg_base = s_rowbase[p];
-        // this lane's cache row of tile t (past the segment end: its last row)
-        auto row_direct = [&](int t) -> long long {
-            return seg_base + min(r0 + (long long)t * kTile + 16 * hh + j, r1 - 1);
-        };
-        auto row_gather = [&](int t) -> long long {
-            const long long lr = min((long long)t * kTile + 16 * hh + j, r1 - 1 - r0);
-            if (kMode == 1) return A.phys[g0 + lr];
-            return seg_base + A.row_idx[(long long)p * A.row_idx_stride + r0 + lr];
-        };
-
-        // Q^T fragments of all 64 heads over dims d
-        half8_t qh[4][4];
-#pragma unroll
-        for (int hb = 0; hb < 4; ++hb)
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                const int dd = 64 * (2 * d + (ks >> 1)) + 16 * q + 8 * (ks & 1);
-                const uint4_t v = *reinterpret_cast<const uint4_t *>(
-                    static_cast<const uint16_t *>(A.q) + (long long)p * A.q_stride +
-                    (long long)(16 * hb + j) * kD + dd);
-                half8_t h;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    h[2 * i] = (half_t)bf16_to_f32((uint16_t)(v[i] & 0xFFFF));
-                    h[2 * i + 1] = (half_t)bf16_to_f32((uint16_t)(v[i] >> 16));
-                }
-                qh[hb][ks] = h;
-            }
-
-        float m_run = -INFINITY, l_run = 0.0f;      // softmax of head 8 wave + jj
-        float4_t o[2][8];                           // heads 32 hh + 16 mb + .., dims 128 d + 16 nb + ..
-#pragma unroll
-        for (int a = 0; a < 2; ++a)
-#pragma unroll
-            for (int c = 0; c < 8; ++c) o[a][c] = float4_t{0, 0, 0, 0};
-
-        // tile u: dequantize (registers -> V tile u & 1), refill the registers
-        // with tile u + 2, partial S of tile u -> sx[u & 1]. Gathered rows of
-        // tile u + 2 are in ph_use; those of u + 3 are fetched into ph_next
-        // first, so that waiting for them later leaves tile u + 2 in flight.
-        auto qk_prep = [&](int u, W8Tile &cur, long long &ph_use, long long &ph_next, int buf) {
-            half8_t a[4];
-            {
-                half8_t d2, d3;
-                dequant16(cur.c0, block_scale(cur.e, 2 * d), a[0], a[1]);
-                dequant16(cur.c1, block_scale(cur.e, 2 * d + 1), d2, d3);
-                a[2] = d < 3 ? d2 : __builtin_bit_cast(half8_t, cur.c1);
-                a[3] = d < 3 ? d3 : __builtin_bit_cast(half8_t, cur.th);
-                // rows 8..15 of each half swap their 16-byte column pairs (bank spread
-                // for these stores; the transposing reads below apply the same swap)
-                const uint32_t vrow = lds_addr(vtile[buf][d]) + (16 * hh + j) * kVRowBytes + 32 * q;
-                const uint32_t sw = (j & 8) ? 16u : 0u;
-                const uint32_t va = vrow + sw, vb = vrow + (16u - sw);
-                asm volatile("ds_write_b128 %0, %2\n\tds_write_b128 %1, %3\n\t"
-                             "ds_write_b128 %0, %4 offset:128\n\tds_write_b128 %1, %5 offset:128"
-                             :: "v"(va), "v"(vb), "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]) : "memory");
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            if (kMode != 0) {
-                ph_next = row_gather(u + 3);
-                __builtin_amdgcn_sched_barrier(0);
-                w8_load(A, d, q, ph_use, cur);
-            } else {
-                w8_load(A, d, q, row_direct(u + 2), cur);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int hb = 0; hb < 4; ++hb) {
-                float4_t c = float4_t{0, 0, 0, 0};
-#pragma unroll
-                for (int ks = 0; ks < 4; ++ks)
-                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[ks], qh[hb][ks], c, 0, 0, 0);
-                // lane ^ 8 for odd q: the softmax reads below are then bank-conflict free
-                sx[buf][hb][d][hh][lane ^ (lane & 16 ? 8 : 0)] = c;   // compiler-visible store: MFMA hazard waits inserted
-            }
-        };
-
-        // prologue (issue order = the loop's: tile 0, [rows of tile 2], tile 1),
-        // then tile 0's partial S
-        W8Tile T0, T1;
-        long long ph0 = 0, ph1 = 0;
-        __builtin_amdgcn_sched_barrier(0);
-        if (kMode != 0) {
-            const long long ra = row_gather(0), rb1 = row_gather(1);
-            __builtin_amdgcn_sched_barrier(0);
-            w8_load(A, d, q, ra, T0);
-            __builtin_amdgcn_sched_barrier(0);
-            ph0 = row_gather(2);
-            __builtin_amdgcn_sched_barrier(0);
-            w8_load(A, d, q, rb1, T1);
-        } else {
-            w8_load(A, d, q, row_direct(0), T0);
-            __builtin_amdgcn_sched_barrier(0);
-            w8_load(A, d, q, row_direct(1), T1);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        qk_prep(0, T0, ph0, ph1, 0);
-        lds_barrier();   // partials of tile 0 and V tile 0 visible
-
-        // Tile t: softmax(t) overlapped with the next tile's dequantize + S
-        // (MFMA), barrier, P . V(t), barrier. V tiles and S partials are double
-        // buffered by tile parity; P and the rescale factors are single.
-        auto step = [&](int t, W8Tile &nxt, long long &ph_use, long long &ph_next, int buf) {
-            const long long rb = r0 + (long long)t * kTile;
-            const float4_t sacc =
-                ((sx[buf][own_hb][0][own_h2][own_sx] + sx[buf][own_hb][1][own_h2][own_sx]) +
-                 sx[buf][own_hb][2][own_h2][own_sx]) + sx[buf][own_hb][3][own_h2][own_sx];
-            qk_prep(t + 1, nxt, ph_use, ph_next, buf ^ 1);
-            {
-                float s4[4];
-                float tmax = -INFINITY;
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const bool ok = rb + 16 * own_h2 + 4 * own_kq + r < r1;
-                    s4[r] = ok ? sacc[r] * A.kq_log2 : -INFINITY;
-                    tmax = fmaxf(tmax, s4[r]);
-                }
-                tmax = xmax_8_16_32(tmax);
-                // the reference point follows the running max exactly (the
-                // largest P of a head is 1, exact in f16), so O is rescaled
-                // whenever the max grows; after the first tiles that is rare
-                const bool bump = tmax > m_run;
-                const float m_new = bump ? tmax : m_run;
-                const bool none = m_new == -INFINITY;
-                const float alpha = (bump && m_run != -INFINITY) ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
-                // P as f16 hi + lo (p - hi): P . V then carries ~22 bits of P, so the
-                // f16 rounding of the weights does not show in O (a single f16 P
-                // leaves errors near 1e-3 of the output RMS when attention is diffuse)
-                half4_t pf, pl;
-                float psum = 0.0f;
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float pv = none ? 0.0f : __builtin_amdgcn_exp2f(s4[r] - m_new);
-                    psum += pv;
-                    pf[r] = (half_t)pv;
-                    pl[r] = (half_t)(pv - (float)pf[r]);
-                }
-                l_run = l_run * alpha + psum;
-                m_run = m_new;
-                reinterpret_cast<uint2_t *>(&pbuf[0][own_hb][own_src])[own_h2] = __builtin_bit_cast(uint2_t, pf);
-                reinterpret_cast<uint2_t *>(&pbuf[1][own_hb][own_src])[own_h2] = __builtin_bit_cast(uint2_t, pl);
-                if (kk == 0) alpha_s[8 * wave + jj] = alpha;
-            }
-            lds_barrier();   // P and rescale factors of tile t visible
-            // ---- O += P . V_d for heads 32 hh + [0, 32) ----
-            const uint32_t vt = lds_addr(vtile[buf][d]);
-            float4_t ar[2];
-            half8_t pa[2], pl[2];
-            asm volatile(
-                "ds_read_b128 %0, %6\n\tds_read_b128 %1, %6 offset:64\n\t"
-                "ds_read_b128 %2, %7\n\tds_read_b128 %3, %7 offset:1024\n\t"
-                "ds_read_b128 %4, %7 offset:4096\n\tds_read_b128 %5, %7 offset:5120\n\t"
-                "s_waitcnt lgkmcnt(0)"
-                : "=&v"(ar[0]), "=&v"(ar[1]), "=&v"(pa[0]), "=&v"(pa[1]), "=&v"(pl[0]), "=&v"(pl[1])
-                : "v"(alpha_base + (32 * hh + 4 * q) * 4), "v"(pbuf_base + (2 * hh * 64 + lane) * 16));
-            // rare (a reference point moved): rescale O before adding tile t
-            const bool need = ar[0][0] != 1.0f || ar[0][1] != 1.0f || ar[0][2] != 1.0f ||
-                              ar[0][3] != 1.0f || ar[1][0] != 1.0f || ar[1][1] != 1.0f ||
-                              ar[1][2] != 1.0f || ar[1][3] != 1.0f;
-            if (__any(need)) {
-#pragma unroll
-                for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-                    for (int nb = 0; nb < 8; ++nb) o[mb][nb] *= ar[mb];
-            }
-#pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                uint2_t tb[8];
-                const uint32_t ab = vt + (4 * q + (j >> 2)) * kVRowBytes + 8 * ((j & 3) ^ (q & 2)) + 128 * half;
-                asm volatile(
-                    "ds_read_b64_tr_b16 %0, %8\n\tds_read_b64_tr_b16 %1, %8 offset:4608\n\t"
-                    "ds_read_b64_tr_b16 %2, %8 offset:32\n\tds_read_b64_tr_b16 %3, %8 offset:4640\n\t"
-                    "ds_read_b64_tr_b16 %4, %8 offset:64\n\tds_read_b64_tr_b16 %5, %8 offset:4672\n\t"
-                    "ds_read_b64_tr_b16 %6, %8 offset:96\n\tds_read_b64_tr_b16 %7, %8 offset:4704\n\t"
-                    "s_waitcnt lgkmcnt(0)"
-                    : "=&v"(tb[0]), "=&v"(tb[1]), "=&v"(tb[2]), "=&v"(tb[3]), "=&v"(tb[4]),
-                      "=&v"(tb[5]), "=&v"(tb[6]), "=&v"(tb[7])
-                    : "v"(ab));
-                half8_t vb[4];
-#pragma unroll
-                for (int nb = 0; nb < 4; ++nb)
-                    vb[nb] = __builtin_bit_cast(
-                        half8_t, uint4_t{tb[2 * nb][0], tb[2 * nb][1], tb[2 * nb + 1][0], tb[2 * nb + 1][1]});
-                // hi products first, then lo: dependent MFMAs eight apart
-#pragma unroll
-                for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-                    for (int mb = 0; mb < 2; ++mb)
-                        o[mb][4 * half + nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                            pa[mb], vb[nb], o[mb][4 * half + nb], 0, 0, 0);
-#pragma unroll
-                for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-                    for (int mb = 0; mb < 2; ++mb)
-                        o[mb][4 * half + nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                            pl[mb], vb[nb], o[mb][4 * half + nb], 0, 0, 0);
-            }
-            lds_barrier();   // partials of tile t+1 and V tile t+1 visible; P consumed
-        };
-        for (int t = 0; t < n_tiles; t += 2) {
-            step(t, T1, ph1, ph0, 0);
-            step(t + 1, T0, ph0, ph1, 1);
-        }
-
-        // ---- emit: O of heads 32 hh + .. over dims d; m, l by the softmax owners ----
-        {
-            const long long slot = (long long)blockIdx.x * A.s_max + slot_s;
-            float *wo = A.ws_o + slot * (kH * kD) + (32 * hh + 4 * q) * kD + 128 * d + j;
-            asm volatile("" : "+v"(wo));
-#pragma unroll
-            for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-                for (int nb = 0; nb < 8; ++nb)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) wo[(16 * mb + r) * kD + 16 * nb] = o[mb][nb][r];
-            const float l = xsum_8_16_32(l_run);
-            if (lane < 8) {
-                A.ws_ml[slot * 2 * kH + 8 * wave + lane] = m_run;
-                A.ws_ml[slot * 2 * kH + kH + 8 * wave + lane] = l;
-            }
-            if (threadIdx.x == 0) A.ws_prob[slot] = p;
-        }
-        ++slot_s;
-        g0 = seg_end;
-    }
-    if (threadIdx.x == 0)
-        for (int s2 = slot_s; s2 < A.s_max; ++s2) A.ws_prob[(long long)blockIdx.x * A.s_max + s2] = -1;
-}
-
 // ---- warp-specialized FP8 decode: producers and consumers -------------------------
 //
 // One 8-wave workgroup per chunk, all 64 heads. Waves 0-3 are producers: wave
@@ -1373,8 +1031,18 @@ __global__ __launch_bounds__(512, 1) void decode_ws_kernel(const DecodeArgs A) {
                         dequant16(cur[hh].c0, pow2f((int)(int8_t)((cur[hh].e >> (16 * (d & 1))) & 0xFF)),
                                   av[hh][0], av[hh][1]);
                         if (kT) {
-                            av[hh][2] = __builtin_bit_cast(half8_t, cur[hh].c1);
-                            av[hh][3] = __builtin_bit_cast(half8_t, cur[hh].c2);
+                            // explicit copies here, where the data is due: left to the
+                            // compiler they become loop-carried copies at the loop head,
+                            // which wait for the loads of the next tile as well
+                            uint4_t t1, t2;
+                            asm volatile("v_mov_b32 %0, %4\n\tv_mov_b32 %1, %5\n\tv_mov_b32 %2, %6\n\tv_mov_b32 %3, %7"
+                                         : "=v"(t1[0]), "=v"(t1[1]), "=v"(t1[2]), "=v"(t1[3])
+                                         : "v"(cur[hh].c1[0]), "v"(cur[hh].c1[1]), "v"(cur[hh].c1[2]), "v"(cur[hh].c1[3]));
+                            asm volatile("v_mov_b32 %0, %4\n\tv_mov_b32 %1, %5\n\tv_mov_b32 %2, %6\n\tv_mov_b32 %3, %7"
+                                         : "=v"(t2[0]), "=v"(t2[1]), "=v"(t2[2]), "=v"(t2[3])
+                                         : "v"(cur[hh].c2[0]), "v"(cur[hh].c2[1]), "v"(cur[hh].c2[2]), "v"(cur[hh].c2[3]));
+                            av[hh][2] = __builtin_bit_cast(half8_t, t1);
+                            av[hh][3] = __builtin_bit_cast(half8_t, t2);
                         } else {
                             dequant16(cur[hh].c1, pow2f((int)(int8_t)((cur[hh].e >> (16 * (d & 1) + 8)) & 0xFF)),
                                       av[hh][2], av[hh][3]);
@@ -1453,9 +1121,10 @@ __global__ __launch_bounds__(512, 1) void decode_ws_kernel(const DecodeArgs A) {
                             tmax = fmaxf(tmax, s8[hh][r]);
                         }
                     tmax = xmax_16_32(tmax);
-                    // the reference point follows the running max exactly (the
-                    // largest P of a head is 1, exact in f16); O is rescaled when it grows
-                    const bool bump = tmax > m_run;
+                    // lazy reference point: it moves to the tile max only when that
+                    // exceeds it by more than 2^kLazyLog2 in P (P up to 256 is exact
+                    // enough as f16 hi + lo), so O is rescaled on few tiles
+                    const bool bump = tmax > m_run + kLazyLog2;
                     const float m_new = bump ? tmax : m_run;
                     const bool none = m_new == -INFINITY;
                     const float alpha = (bump && m_run != -INFINITY) ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
@@ -1596,7 +1265,9 @@ __global__ __launch_bounds__(512, 1) void decode_ws_kernel(const DecodeArgs A) {
                           "=&v"(tb[half][4]), "=&v"(tb[half][5]), "=&v"(tb[half][6]), "=&v"(tb[half][7])
                         : "v"(ab));
                 }
-                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                // P, alpha and the first half's V fragments (the second half's 8
+                // reads may still be in flight; LDS returns in order)
+                asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");
                 bool need = false;
 #pragma unroll
                 for (int hb = 0; hb < 4; ++hb)
@@ -1609,6 +1280,7 @@ __global__ __launch_bounds__(512, 1) void decode_ws_kernel(const DecodeArgs A) {
                 }
 #pragma unroll
                 for (int half = 0; half < 2; ++half) {
+                    if (half == 1) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
                     half8_t vb[4];
 #pragma unroll
                     for (int nb = 0; nb < 4; ++nb)
@@ -1750,7 +1422,6 @@ struct Plan {
     long long start[kMaxProb + 1] = {};   // problem offsets in the chunked row space
 };
 
-size_t slot_bytes() { return (size_t)kH * kD * 4 + 2 * kH * 4 + 4; }
 
 // Rows of work that one extra problem segment costs a workgroup (its Q
 // fragments and first tiles load before any compute, and it writes one

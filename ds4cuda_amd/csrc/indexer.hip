@@ -241,30 +241,19 @@ __global__ __launch_bounds__(256) void score_kernel(const float *__restrict__ q,
     __shared__ __attribute__((aligned(16))) float qs[kMaxHeads * kQStride];
     __shared__ float ws[kMaxHeads];
     if (kFull) {
-        // four threads per key, two keys per thread group (128 keys per pass);
-        // the workgroup loops over key groups so that the query is staged once
-        // per workgroup
-        stage_query<kQStride>(qs, q, n_head);
+        // one thread per key: the query staged once per 256 keys (the four-lane
+        // chained form measures slower here, where a launch has many keys)
+        const int c = blockIdx.x * 256 + threadIdx.x;
+        float s = 0.0f;
+        stage_query(qs, q, n_head);
         for (int i = threadIdx.x; i < n_head; i += 256) ws[i] = w[i];
+        pad_heads(qs, ws, n_head);
         __syncthreads();
-        const bool own = (threadIdx.x & 3) == 3;   // the scores are in part 3
-        for (int g = blockIdx.x; g * 128 < n_comp; g += gridDim.x) {
-            const int c0 = g * 128 + (int)(threadIdx.x >> 2), c1 = c0 + 64;
-            if (c0 < n_comp) {
-                float s0, s1;
-                score_chain4x2<kKind>(qs, ws, keys, c0, c1 < n_comp ? c1 : c0, n_head,
-                                      (int)(threadIdx.x & 3), s0, s1);
-                if (own) {
-                    scores[c0] = s0;
-                    if (hist && c0 < n_cand) atomicAdd(&lh[ord_key(s0) >> 21], 1u);
-                    if (c1 < n_comp) {
-                        scores[c1] = s1;
-                        if (hist && c1 < n_cand) atomicAdd(&lh[ord_key(s1) >> 21], 1u);
-                    }
-                }
-            }
-        }
+        if (c < n_comp) s = score_lds<kKind>(qs, ws, keys, c, n_head);
+        if (c < n_comp) scores[c] = s;
         if (hist) {
+            __syncthreads();
+            if (c < n_cand) atomicAdd(&lh[ord_key(s) >> 21], 1u);
             __syncthreads();
             for (int i = threadIdx.x; i < kBins; i += 256)
                 if (lh[i]) atomicAdd(&hist[i], lh[i]);
@@ -459,7 +448,7 @@ __global__ __launch_bounds__(256) void emit_kernel(const float *__restrict__ sco
                                                    int32_t *__restrict__ mask,
                                                    int32_t *__restrict__ pos_out) {
     __shared__ unsigned scratch[256], buf[256];
-    __shared__ unsigned s_bin, s_above, s_sel_before, s_eq_before;
+    __shared__ unsigned s_bin, s_above;
     unsigned T, need_eq;
     threshold(hists, need0, &T, &need_eq, scratch, &s_bin, &s_above);
     // selections and ties of the earlier chunks
@@ -525,24 +514,11 @@ __global__ void scale_kernel(float *y, int n, float s) {
     if (i < n) y[i] *= s;
 }
 
-int num_cus_idx() {
-    static int n = 0;
-    if (n == 0) {
-        int dev = 0;
-        hipDeviceProp_t prop;
-        if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess)
-            n = prop.multiProcessorCount;
-        else
-            n = 256;
-    }
-    return n;
-}
-
 int launch_scores(const float *q, const float *w, const void *keys, int kind, int n_comp,
                   int n_head, int head_dim, float *scores, unsigned *hist, int n_cand,
                   hipStream_t st) {
     const bool full = head_dim == kMaxDim;
-    const dim3 grid(full ? std::min((n_comp + 127) / 128, 4 * num_cus_idx()) : (n_comp + 255) / 256);
+    const dim3 grid((n_comp + 255) / 256);
     switch (kind) {
     case 0:
         if (full) hipLaunchKernelGGL((score_kernel<0, true>), grid, dim3(256), 0, st, q, w, keys, n_comp, n_head, head_dim, scores, hist, n_cand);

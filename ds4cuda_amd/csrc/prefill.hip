@@ -21,11 +21,10 @@
 //     ds_read_b64_tr_b16.
 // The FP8 tile (32 rows x 584 B) is loaded into registers one tile ahead,
 // dequantized once per workgroup (v_cvt_scalef32_pk_f16_fp8) and written to a
-// double-buffered f16 LDS tile. Rows are stored linearly with a 16-byte pad
-// (1040 B per row): ds_read/write_b128 resolve banks per 8 lanes over 256 B,
-// so the 8 threads storing one row (16-byte chunks 7j + i), 8 lanes reading
-// one column chunk of 8 rows, and the transposing reads of 4 rows x 32 B all
-// hit distinct banks. Inside a tile the keys are taken in the order pi (below):
+// double-buffered f16 LDS tile of 1056-byte rows whose 16-byte halves of each
+// 32-byte column group swap on rows 8..15 of every 16 (row_swz): the 8 threads
+// storing one row, the 16 lanes reading one column chunk of 16 rows and the
+// transposing reads of 8 rows x 32 B then all hit distinct banks. Inside a tile the keys are taken in the order pi (below):
 // the S^T rows of an MFMA, the P fragment and the V^T fragment then agree
 // without any register shuffling.
 
@@ -42,7 +41,16 @@ constexpr int kD = 512;
 constexpr int kRot = 64;
 constexpr int kNope = kD - kRot;
 constexpr int kTile = 32;            // keys per tile
-constexpr int kRowB = 2 * kD + 16;   // one f16 row + 16 B
+constexpr int kRowB = 2 * kD + 32;   // one f16 row + 32 B
+
+// Byte-offset swizzle of row r of an f16 tile: rows 8..15 of every 16 swap
+// the 16-byte halves of their 32-byte column groups. With 1056-byte rows the
+// 16-lane K reads (16 rows, one 16-byte column) and the transposing V reads
+// (8 rows x 32 bytes per 32 lanes) then hit distinct banks, and the 8-lane
+// 16-byte stores of one row stay conflict-free.
+__device__ inline uint32_t row_swz(int r) {
+    return 16u * ((r >> 3) & 1);
+}
 constexpr int kStageB = kTile * kRowB;
 constexpr int kRows = 128;           // query rows (2 queries x 64 heads) per workgroup
 constexpr float kLog2e = 1.4426950408889634f;
@@ -120,6 +128,7 @@ __device__ inline half2_t cvt2(uint32_t w, float scale) {
 __device__ inline void store_tile(uint8_t *stage, int tid, const Raw &R) {
     const int row = tid >> 3, j = tid & 7;
     uint8_t *rp = stage + row * kRowB;
+    const uint32_t x = row_swz(row);
 #pragma unroll
     for (int i = 0; i < 7; ++i) {
         const int d = 56 * j + 8 * i;       // first dim of the group
@@ -129,10 +138,10 @@ __device__ inline void store_tile(uint8_t *stage, int tid, const Raw &R) {
         const float sc = __uint_as_float((uint32_t)(e + 127) << 23);
         const half2_t h0 = cvt2<false>(R.c[i][0], sc), h1 = cvt2<true>(R.c[i][0], sc);
         const half2_t h2 = cvt2<false>(R.c[i][1], sc), h3 = cvt2<true>(R.c[i][1], sc);
-        *reinterpret_cast<half8_t *>(rp + 2 * d) =
+        *reinterpret_cast<half8_t *>(rp + ((2 * d) ^ x)) =
             half8_t{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
     }
-    *reinterpret_cast<uint4_t *>(rp + 2 * kNope + 16 * j) = R.t;
+    *reinterpret_cast<uint4_t *>(rp + ((2 * kNope + 16 * j) ^ x)) = R.t;
 }
 
 // V^T fragments of 4 of the wave's dim tiles (DT0 .. DT0+3): vb[i] holds,
@@ -256,11 +265,16 @@ __global__ __launch_bounds__(256) void prefill_fp8_kernel(const PrefillArgs A) {
     // lane-constant LDS offsets
     uint32_t ka[2];           // QK A rows (key tile kt), dims 8g
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) ka[kt] = pi_key(16 * kt + n16) * kRowB + 16 * g;
+    for (int kt = 0; kt < 2; ++kt) {
+        const int r = pi_key(16 * kt + n16);
+        ka[kt] = r * kRowB + ((16 * g) ^ row_swz(r));
+    }
     uint32_t va[2];           // V^T supplier rows (half h), dims 128w + 4(n16&3)
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
-        va[h] = pi_key(16 * h + 4 * g + (n16 >> 2)) * kRowB + 256 * w + 8 * (n16 & 3);
+    for (int h = 0; h < 2; ++h) {
+        const int r = pi_key(16 * h + 4 * g + (n16 >> 2));
+        va[h] = r * kRowB + 256 * w + ((8 * (n16 & 3)) ^ row_swz(r));
+    }
 
     Raw R;
     load_raw(A, 0, n_all, tid, R);
@@ -518,11 +532,16 @@ __global__ __launch_bounds__(256) void prefill_fast_kernel(const PrefillArgs A) 
 
     uint32_t ka[2];
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) ka[kt] = pi_key(16 * kt + n16) * kRowB + 16 * g;
+    for (int kt = 0; kt < 2; ++kt) {
+        const int r = pi_key(16 * kt + n16);
+        ka[kt] = r * kRowB + ((16 * g) ^ row_swz(r));
+    }
     uint32_t va[2];
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
-        va[h] = pi_key(16 * h + 4 * g + (n16 >> 2)) * kRowB + 256 * w + 8 * (n16 & 3);
+    for (int h = 0; h < 2; ++h) {
+        const int r = pi_key(16 * h + 4 * g + (n16 >> 2));
+        va[h] = r * kRowB + 256 * w + ((8 * (n16 & 3)) ^ row_swz(r));
+    }
 
     Raw R;
     load_raw(A, 0, n_all, tid, R);

@@ -1008,23 +1008,20 @@ __global__ __launch_bounds__(512, 1) void decode_ws_kernel(const DecodeArgs A) {
                     // reallocated before the load returns, which forces a full wait
                     T.e = *reinterpret_cast<const uint32_t *>(A.sexp + r * 8 + (d >= 2 ? 4 : 0));
                 };
-                half8_t qh[4][4];   // Q^T fragments of all 64 heads over dims d
+                // Q^T fragments of all 64 heads over dims d: the raw bf16 loads are
+                // issued before the first tiles' loads and converted after them, so
+                // the two memory round trips overlap
+                uint4_t qraw[4][4];
 #pragma unroll
                 for (int hb = 0; hb < 4; ++hb)
 #pragma unroll
                     for (int ks = 0; ks < 4; ++ks) {
                         const int dd = 64 * (2 * d + (ks >> 1)) + 16 * q + 8 * (ks & 1);
-                        const uint4_t v = *reinterpret_cast<const uint4_t *>(
+                        qraw[hb][ks] = *reinterpret_cast<const uint4_t *>(
                             static_cast<const uint16_t *>(A.q) + (long long)p * A.q_stride +
                             (long long)(16 * hb + j) * kD + dd);
-                        half8_t h;
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            h[2 * i] = (half_t)bf16_to_f32((uint16_t)(v[i] & 0xFFFF));
-                            h[2 * i + 1] = (half_t)bf16_to_f32((uint16_t)(v[i] >> 16));
-                        }
-                        qh[hb][ks] = h;
                     }
+                half8_t qh[4][4];
                 auto dequant = [&](const Tl (&cur)[2], half8_t (&av)[2][4]) {
 #pragma unroll
                     for (int hh = 0; hh < 2; ++hh) {
@@ -1196,6 +1193,19 @@ __global__ __launch_bounds__(512, 1) void decode_ws_kernel(const DecodeArgs A) {
                     load(row_direct(1, 1), T1[1]);
                 }
                 __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int hb = 0; hb < 4; ++hb)
+#pragma unroll
+                    for (int ks = 0; ks < 4; ++ks) {
+                        const uint4_t v = qraw[hb][ks];
+                        half8_t x;
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            x[2 * i] = (half_t)bf16_to_f32((uint16_t)(v[i] & 0xFFFF));
+                            x[2 * i + 1] = (half_t)bf16_to_f32((uint16_t)(v[i] >> 16));
+                        }
+                        qh[hb][ks] = x;
+                    }
                 half8_t av[2][4];
                 dequant(T0, av);   // interval 0
                 __builtin_amdgcn_sched_barrier(0);
@@ -1388,7 +1398,7 @@ __global__ __launch_bounds__(128) void decode_merge_kernel(const DecodeArgs A) {
         __syncthreads();
         const int nb = (int)std::min<long long>(128, n_slot - base);
         const float *o0 = A.ws_o + (s0 + base) * (kH * kD) + h * kD + 4 * tid;
-#pragma unroll 8
+#pragma unroll 16
         for (int j = 0; j < nb; ++j) {
             const float c = s_sc[j];
             const float4_t o = *reinterpret_cast<const float4_t *>(o0 + (long long)j * (kH * kD));

@@ -981,10 +981,8 @@ __global__ __launch_bounds__(512, 1) void decode_ws_kernel(const DecodeArgs A) {
             // kT: the wave of dims [384, 512): one FP8 block + the f16 RoPE tail
             auto produce = [&](auto tail_c) {
                 constexpr bool kT = decltype(tail_c)::value;
-                // this lane's cache row in row half hh of tile t (past the end: the last row)
-                auto row_direct = [&](int t, int hh) -> long long {
-                    return seg_base + min(r0 + (long long)t * kTile + 16 * hh + j, r1 - 1);
-                };
+                // gathered rows: this lane's cache row in row half hh of tile t (past
+                // the end: the last row)
                 auto row_gather = [&](int t, int hh) -> long long {
                     const long long lr = min((long long)t * kTile + 16 * hh + j, r1 - 1 - r0);
                     if (kMode == 1) return A.phys[g0 + lr];
@@ -1007,6 +1005,25 @@ __global__ __launch_bounds__(512, 1) void decode_ws_kernel(const DecodeArgs A) {
                     // only the word this wave uses: a loaded but unused register can be
                     // reallocated before the load returns, which forces a full wait
                     T.e = *reinterpret_cast<const uint32_t *>(A.sexp + r * 8 + (d >= 2 ? 4 : 0));
+                };
+                // direct rows: 32-bit row offsets from the segment's first row (a
+                // segment is at most one chunk of rows), so that the loads take a
+                // uniform 64-bit base and one 32-bit offset each
+                const long long seg_r0 = seg_base + r0;
+                const int seg_last = (int)(r1 - 1 - r0);
+                const uint8_t *codes_s = A.codes + seg_r0 * kNope + 128 * d;
+                const uint8_t *tail_s = reinterpret_cast<const uint8_t *>(A.tail) + seg_r0 * (2 * kRot);
+                const uint8_t *sexp_s = reinterpret_cast<const uint8_t *>(A.sexp) + seg_r0 * 8 + (d >= 2 ? 4 : 0);
+                auto load_direct = [&](int t, int hh, Tl &T) {
+                    const uint32_t lr = (uint32_t)min(t * kTile + 16 * hh + j, seg_last);
+                    T.c0 = *reinterpret_cast<const uint4_t *>(codes_s + (lr * kNope + 16 * q));
+                    if (kT) {
+                        T.c1 = *reinterpret_cast<const uint4_t *>(tail_s + (lr * (2 * kRot) + 32 * q));
+                        T.c2 = *reinterpret_cast<const uint4_t *>(tail_s + (lr * (2 * kRot) + 32 * q + 16));
+                    } else {
+                        T.c1 = *reinterpret_cast<const uint4_t *>(codes_s + (lr * kNope + 16 * q + 64));
+                    }
+                    T.e = *reinterpret_cast<const uint32_t *>(sexp_s + lr * 8);
                 };
                 // Q^T fragments of all 64 heads over dims d: the raw bf16 loads are
                 // issued before the first tiles' loads and converted after them, so
@@ -1056,8 +1073,8 @@ __global__ __launch_bounds__(512, 1) void decode_ws_kernel(const DecodeArgs A) {
                         load(ph_use[0], cur[0]);
                         load(ph_use[1], cur[1]);
                     } else {
-                        load(row_direct(u + 2, 0), cur[0]);
-                        load(row_direct(u + 2, 1), cur[1]);
+                        load_direct(u + 2, 0, cur[0]);
+                        load_direct(u + 2, 1, cur[1]);
                     }
                 };
                 // partial S of a tile over dims d
@@ -1186,11 +1203,11 @@ __global__ __launch_bounds__(512, 1) void decode_ws_kernel(const DecodeArgs A) {
                     load(rb0, T1[0]);
                     load(rb1, T1[1]);
                 } else {
-                    load(row_direct(0, 0), T0[0]);
-                    load(row_direct(0, 1), T0[1]);
+                    load_direct(0, 0, T0[0]);
+                    load_direct(0, 1, T0[1]);
                     __builtin_amdgcn_sched_barrier(0);
-                    load(row_direct(1, 0), T1[0]);
-                    load(row_direct(1, 1), T1[1]);
+                    load_direct(1, 0, T1[0]);
+                    load_direct(1, 1, T1[1]);
                 }
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll

@@ -427,6 +427,14 @@ __global__ __launch_bounds__(256) void prefill_fp8_kernel(const PrefillArgs A) {
 }
 
 // QK^T of one tile for the wave's 32 rows: acc[kt][rt] = S^T[keys pi(16kt+4g+r)][row 16rt+n16].
+// S^T accumulation with VGPR accumulators (inline asm): O already takes all 256
+// AGPRs, and compiler-placed QK^T accumulators in AGPRs made it shuffle O
+// between register files every tile. Consecutive MFMAs on one accumulator are
+// four apart in the loop below, past the accumulate-forwarding window.
+__device__ inline void mfma_vgpr(float4_t &c, const half8_t &a, const half8_t &b) {
+    asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+}
+
 __device__ inline void qk_tile(const uint8_t *st, const uint32_t *ka, const half8_t (*qf)[16],
                                float4_t (*acc)[2]) {
 #pragma unroll
@@ -445,11 +453,14 @@ __device__ inline void qk_tile(const uint8_t *st, const uint32_t *ka, const half
         }
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt) {
-            acc[0][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0[s & 1], qf[rt][s], acc[0][rt], 0, 0, 0);
-            acc[1][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1[s & 1], qf[rt][s], acc[1][rt], 0, 0, 0);
+            mfma_vgpr(acc[0][rt], k0[s & 1], qf[rt][s]);
+            mfma_vgpr(acc[1][rt], k1[s & 1], qf[rt][s]);
         }
         __builtin_amdgcn_sched_barrier(0);
     }
+    // the results are read by VALU next: 16x16x32 f16 (8 passes) needs 11 wait
+    // states after the last write, which the compiler does not track for asm
+    asm volatile("s_nop 7\n\ts_nop 7" ::: "memory");
 }
 
 // Softmax of one tile with the reference max fixed (set on the first tile):

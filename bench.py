@@ -37,7 +37,7 @@ COPY_BYTES = 1 << 30                               # --copy-calibration: 1 GiB r
 # (FETCH_SIZE + WRITE_SIZE, each scaled by what the counter reads for
 # `--copy-calibration`); the counter summary and its commands are in
 # profiles/decode_fp8_cfg2_traffic.md. Re-measure after a kernel change.
-TRAFFIC_BYTES_PER_LAUNCH = 884806497
+TRAFFIC_BYTES_PER_LAUNCH = 884805617
 
 
 def bytes_per_layer():

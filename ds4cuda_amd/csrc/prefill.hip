@@ -220,12 +220,11 @@ __device__ inline void pv_step(const half8_t (*phi)[64], const half8_t (*plo)[64
     }
 }
 
-// kFix = false: the fast kernel. The softmax reference max of a row is fixed
-// by the first tile; later tiles may exceed it by up to 2^kLazy (P <= 2^15
-// stays an f16 number). A row whose max grows further marks its query pair
-// in A.fail and the pair's output is left to the fixup launch.
-// kFix = true: the fixup kernel. Only flagged pairs run; the reference max
-// moves whenever a row max exceeds it by 2^8, with O rescaled.
+// Two-barrier form of the prefill. The launcher runs it as kFix = true, the
+// fixup kernel: only query pairs flagged by prefill_fast_kernel (a row max that
+// outgrew the fixed reference by more than 2^kLazy) run, and the reference max
+// moves whenever a row max exceeds it by 2^8, with O rescaled. kFix = false
+// (not launched) is the same pass with the fast kernel's fixed reference.
 // P is carried as f16 hi + lo (p - hi), so P . V keeps ~22 bits of P.
 template <bool kFix>
 __global__ __launch_bounds__(256) void prefill_fp8_kernel(const PrefillArgs A) {

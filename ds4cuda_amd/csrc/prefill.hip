@@ -433,13 +433,15 @@ __global__ __launch_bounds__(256) void prefill_fp8_kernel(const PrefillArgs A) {
 __device__ inline void mfma_vgpr(float4_t &c, const half8_t &a, const half8_t &b) {
     asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
 }
+// First k-step: C = 0 inline, so no VALU write of the accumulator precedes it
+// (a VALU write feeding an MFMA operand needs wait states the compiler does not
+// insert for asm).
+__device__ inline void mfma_vgpr0(float4_t &c, const half8_t &a, const half8_t &b) {
+    asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, 0" : "=v"(c) : "v"(a), "v"(b));
+}
 
 __device__ inline void qk_tile(const uint8_t *st, const uint32_t *ka, const half8_t (*qf)[16],
                                float4_t (*acc)[2]) {
-#pragma unroll
-    for (int a = 0; a < 2; ++a)
-#pragma unroll
-        for (int b = 0; b < 2; ++b) acc[a][b] = float4_t{0, 0, 0, 0};
     half8_t k0[2], k1[2];
     k0[0] = *reinterpret_cast<const half8_t *>(st + ka[0]);
     k1[0] = *reinterpret_cast<const half8_t *>(st + ka[1]);
@@ -452,8 +454,13 @@ __device__ inline void qk_tile(const uint8_t *st, const uint32_t *ka, const half
         }
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt) {
-            mfma_vgpr(acc[0][rt], k0[s & 1], qf[rt][s]);
-            mfma_vgpr(acc[1][rt], k1[s & 1], qf[rt][s]);
+            if (s == 0) {
+                mfma_vgpr0(acc[0][rt], k0[0], qf[rt][0]);
+                mfma_vgpr0(acc[1][rt], k1[0], qf[rt][0]);
+            } else {
+                mfma_vgpr(acc[0][rt], k0[s & 1], qf[rt][s]);
+                mfma_vgpr(acc[1][rt], k1[s & 1], qf[rt][s]);
+            }
         }
         __builtin_amdgcn_sched_barrier(0);
     }

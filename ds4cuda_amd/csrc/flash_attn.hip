@@ -1126,14 +1126,22 @@ __global__ __launch_bounds__(512, 1) void decode_ws_kernel(const DecodeArgs A) {
                     const long long left = r1 - (r0 + (long long)t * kTile);
                     const int nv = left < kTile ? (int)left : kTile;   // valid rows of the tile
                     float s8[2][4];
-                    float tmax = -INFINITY;
-    #pragma unroll
+#pragma unroll
                     for (int hh = 0; hh < 2; ++hh)
-    #pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            s8[hh][r] = 16 * hh + 4 * q + r < nv ? sa[hh][r] * A.kq_log2 : -INFINITY;
-                            tmax = fmaxf(tmax, s8[hh][r]);
-                        }
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) s8[hh][r] = sa[hh][r] * A.kq_log2;
+                    if (nv < kTile) {   // (uniform) the segment's last tile: rows past its end take no part
+#pragma unroll
+                        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                            for (int r = 0; r < 4; ++r)
+                                if (16 * hh + 4 * q + r >= nv) s8[hh][r] = -INFINITY;
+                    }
+                    float tmax = -INFINITY;
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, s8[hh][r]);
                     tmax = xmax_16_32(tmax);
                     // lazy reference point: it moves to the tile max only when that
                     // exceeds it by more than 2^kLazyLog2 in P (P up to 256 is exact
@@ -1147,9 +1155,9 @@ __global__ __launch_bounds__(512, 1) void decode_ws_kernel(const DecodeArgs A) {
                     // Element 4 hh + r of lane (j, q) is row 16 hh + 4 q + r of head
                     // j, the K order of the V fragments.
                     half8_t pf, pl;
-    #pragma unroll
+#pragma unroll
                     for (int hh = 0; hh < 2; ++hh)
-    #pragma unroll
+#pragma unroll
                         for (int r = 0; r < 4; ++r) {
                             const float pv = none ? 0.0f : __builtin_amdgcn_exp2f(s8[hh][r] - m_new);
                             psum += pv;

@@ -946,7 +946,7 @@ __device__ inline uint32_t pws_off(int buf, int hl, int hb, int lane) {
     return (uint32_t)((((buf * 2 + hl) * 4 + hb) * 64 + lane) * 16);
 }
 
-template <int kMode>
+template <int kMode, bool kPLo>
 __global__ __launch_bounds__(512, 1) void decode_ws_kernel(const DecodeArgs A) {
     __shared__ __attribute__((aligned(16))) uint8_t vtile[2][4][kVTileBytes];   // [tile & 1][dim quarter]
     __shared__ __attribute__((aligned(16))) float4_t sx[2][4][4][2][64];  // [tile & 1][head tile][dim quarter][row half][lane]
@@ -1151,21 +1151,28 @@ __global__ __launch_bounds__(512, 1) void decode_ws_kernel(const DecodeArgs A) {
                     const bool none = m_new == -INFINITY;
                     const float alpha = (bump && m_run != -INFINITY) ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
                     float psum = 0.0f;
-                    // P as f16 hi + lo (p - hi): P . V then carries ~22 bits of P.
-                    // Element 4 hh + r of lane (j, q) is row 16 hh + 4 q + r of head
-                    // j, the K order of the V fragments.
+                    // kPLo: P as f16 hi + lo (p - hi), so that P . V carries ~22 bits
+                    // of P. Otherwise P is one f16 and l sums the rounded values, so
+                    // that O stays an exactly normalized average of V rows with
+                    // weights off by at most 2^-11 relative. Element 4 hh + r of lane
+                    // (j, q) is row 16 hh + 4 q + r of head j, the K order of the V
+                    // fragments.
                     half8_t pf, pl;
 #pragma unroll
                     for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
                             const float pv = none ? 0.0f : __builtin_amdgcn_exp2f(s8[hh][r] - m_new);
-                            psum += pv;
                             pf[4 * hh + r] = (half_t)pv;
-                            pl[4 * hh + r] = (half_t)(pv - (float)pf[4 * hh + r]);
+                            if (kPLo) {
+                                psum += pv;
+                                pl[4 * hh + r] = (half_t)(pv - (float)pf[4 * hh + r]);
+                            } else {
+                                psum += (float)pf[4 * hh + r];
+                            }
                         }
                     *reinterpret_cast<half8_t *>(pws + pws_off(b, 0, d, lane)) = pf;
-                    *reinterpret_cast<half8_t *>(pws + pws_off(b, 1, d, lane)) = pl;
+                    if (kPLo) *reinterpret_cast<half8_t *>(pws + pws_off(b, 1, d, lane)) = pl;
                     l_run = l_run * alpha + psum;
                     m_run = m_new;
                     if (q == 0) alpha_s[b][16 * d + j] = alpha;
@@ -1283,7 +1290,7 @@ __global__ __launch_bounds__(512, 1) void decode_ws_kernel(const DecodeArgs A) {
 #pragma unroll
                 for (int hb = 0; hb < 4; ++hb) {
                     pa[hb] = *reinterpret_cast<const half8_t *>(pws + pws_off(b, 0, hb, lane));
-                    pl[hb] = *reinterpret_cast<const half8_t *>(pws + pws_off(b, 1, hb, lane));
+                    if (kPLo) pl[hb] = *reinterpret_cast<const half8_t *>(pws + pws_off(b, 1, hb, lane));
                     ar[hb] = *reinterpret_cast<const float4_t *>(&alpha_s[b][16 * hb + 4 * q]);
                 }
                 const uint32_t vt = lds_addr(vtile[b][d]);
@@ -1328,12 +1335,14 @@ __global__ __launch_bounds__(512, 1) void decode_ws_kernel(const DecodeArgs A) {
                         for (int hb = 0; hb < 4; ++hb)
                             o[hb][4 * half + nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
                                 pa[hb], vb[nb], o[hb][4 * half + nb], 0, 0, 0);
+                    if (kPLo) {
 #pragma unroll
-                    for (int nb = 0; nb < 4; ++nb)
+                        for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
-                        for (int hb = 0; hb < 4; ++hb)
-                            o[hb][4 * half + nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                                pl[hb], vb[nb], o[hb][4 * half + nb], 0, 0, 0);
+                            for (int hb = 0; hb < 4; ++hb)
+                                o[hb][4 * half + nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                    pl[hb], vb[nb], o[hb][4 * half + nb], 0, 0, 0);
+                    }
                 }
             };
             lds_barrier();   // interval 0
@@ -1529,6 +1538,25 @@ void carve(DecodeArgs &A, void *ws, const Plan &pl) {
     A.phys = reinterpret_cast<long long *>(c);   // used only by gathered steps (reset below)
 }
 
+// P . V precision of the bf16-Q decode: 1 = P as f16 hi + lo, 0 = one f16 P
+// (a third fewer MFMAs). Initial value from DS4HIP_DECODE_EXACT_P, default 0.
+int g_decode_exact_p = -1;
+bool decode_exact_p() {
+    if (g_decode_exact_p < 0) {
+        const char *e = getenv("DS4HIP_DECODE_EXACT_P");
+        g_decode_exact_p = (e && e[0] == '1') ? 1 : 0;
+    }
+    return g_decode_exact_p == 1;
+}
+
+template <int kMode>
+void launch_ws(const DecodeArgs &A, const Plan &pl, hipStream_t st) {
+    if (decode_exact_p())
+        hipLaunchKernelGGL((decode_ws_kernel<kMode, true>), dim3(pl.n_wg), dim3(512), 0, st, A);
+    else
+        hipLaunchKernelGGL((decode_ws_kernel<kMode, false>), dim3(pl.n_wg), dim3(512), 0, st, A);
+}
+
 template <bool kFp8, bool kQf32>
 int launch(DecodeArgs &A, const Plan &pl, hipStream_t st, int phases = 3) {
     A.chunk = pl.chunk;
@@ -1543,11 +1571,11 @@ int launch(DecodeArgs &A, const Plan &pl, hipStream_t st, int phases = 3) {
         }
         if (kFp8 && !kQf32) {
             if (idx_only)
-                hipLaunchKernelGGL(decode_ws_kernel<2>, dim3(pl.n_wg), dim3(512), 0, st, A);
+                launch_ws<2>(A, pl, st);
             else if (A.phys)
-                hipLaunchKernelGGL(decode_ws_kernel<1>, dim3(pl.n_wg), dim3(512), 0, st, A);
+                launch_ws<1>(A, pl, st);
             else
-                hipLaunchKernelGGL(decode_ws_kernel<0>, dim3(pl.n_wg), dim3(512), 0, st, A);
+                launch_ws<0>(A, pl, st);
         }
         else if (kFp8)
             hipLaunchKernelGGL(decode_fp8_kernel<kQf32>, dim3(pl.n_wg), dim3(256), 0, st, A);
@@ -1562,6 +1590,13 @@ int launch(DecodeArgs &A, const Plan &pl, hipStream_t st, int phases = 3) {
 }
 
 }  // namespace
+
+extern "C" int ds4hip_set_decode_exact_p(int exact) {
+    if (exact != 0 && exact != 1) return -22;
+    const int prev = decode_exact_p() ? 1 : 0;
+    g_decode_exact_p = exact;
+    return prev;
+}
 
 extern "C" int ds4hip_flash_attn_decode_fp8_workspace_size(const long long *n_rows_per_prob,
                                                            int n_prob, size_t *bytes) {

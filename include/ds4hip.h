@@ -112,6 +112,15 @@ int ds4hip_flash_attn_decode_fp8(const void *q, int q_is_f32, long long q_stride
                                  int n_rot, void *workspace, size_t workspace_bytes,
                                  int phases, void *stream);
 
+/* P . V precision of the bf16-Q FP8 decode (no counterpart in the reference,
+ * whose scalar kernel keeps P in fp32, cuda/flash_attn.cu:70-85): exact = 1
+ * passes P as f16 hi + lo halves (~22 bits), exact = 0 as one f16 (the
+ * default; max-abs error stays ~1e-3 x RMS(out), a third fewer MFMAs). The
+ * initial value comes from the environment variable DS4HIP_DECODE_EXACT_P.
+ * Returns the previous setting, or -22 for another value. Process-wide; not
+ * synchronized with launches in flight on other host threads. */
+int ds4hip_set_decode_exact_p(int exact);
+
 /* ---- chunked prefill ------------------------------------------------------------- */
 
 /* Causal chunked-prefill attention over the FP8 cache (additive: the

@@ -155,3 +155,32 @@ def test_fp8_cfg2_scale_long_chunks(gpu):
         rows = p * n_kv + np.arange(n_kv)
         ref = O.attn_decode_fp8(qf[p], codes, sexp, tail, rows, sinks[p], n_threads=8)
         check(out[p].cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("n_kv", [1000, 32768])
+def test_fp8_p_precision_modes(gpu, n_kv):
+    """Both P . V precisions of the bf16-Q decode meet the bar. Measured max err /
+    RMS: hi + lo 5.8e-5 and 5.1e-4, one f16 3.5e-4 and 5.0e-4 (1000 and 32768
+    rows; at 32768 the fp32 summation of the oracle dominates)."""
+    from ds4cuda_amd import _lib
+    cache, (codes, sexp, tail) = make_cache(n_kv, 41, gpu)
+    bits, qf = q_bf16(42, 1)
+    sinks = sinks_for(43, 1)
+    q = torch.from_numpy(bits.view(np.int16)).to(gpu).view(torch.bfloat16)
+    ref = O.attn_decode_fp8(qf[0], codes, sexp, tail, np.arange(n_kv), sinks[0], n_threads=8)
+    rms = np.sqrt(np.mean(ref.astype(np.float64) ** 2))
+    prev = _lib.lib().ds4hip_set_decode_exact_p(1)
+    try:
+        errs = {}
+        for exact in (1, 0):
+            _lib.lib().ds4hip_set_decode_exact_p(exact)
+            out = torch.zeros((1, 64, 512), dtype=torch.float32, device=gpu)
+            ops.flash_attn_decode_fp8(q, torch.from_numpy(sinks).to(gpu), out, cache, [n_kv])
+            torch.cuda.synchronize()
+            errs[exact] = np.abs(out[0].cpu().numpy().astype(np.float64) - ref).max() / rms
+        print(f"n_kv {n_kv}: max err / rms  hi+lo {errs[1]:.2e}  f16 {errs[0]:.2e}")
+    finally:
+        _lib.lib().ds4hip_set_decode_exact_p(prev)
+    assert errs[1] <= TOL
+    assert errs[0] <= TOL
+    assert _lib.lib().ds4hip_set_decode_exact_p(2) == -22

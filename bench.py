@@ -37,7 +37,7 @@ COPY_BYTES = 1 << 30                               # --copy-calibration: 1 GiB r
 # (FETCH_SIZE + WRITE_SIZE, each scaled by what the counter reads for
 # `--copy-calibration`); the counter summary and its commands are in
 # profiles/decode_fp8_cfg2_traffic.md. Re-measure after a kernel change.
-TRAFFIC_BYTES_PER_LAUNCH = 884805617
+TRAFFIC_BYTES_PER_LAUNCH = 882340981
 
 
 def bytes_per_layer():
@@ -426,7 +426,7 @@ def main():
                    "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_BYTES_PER_LAUNCH,
-                     "kernel": "decode_ws_kernel<0> (direct rows)",
+                     "kernel": "decode_ws_kernel<0, false> (direct rows, one f16 P)",
                      "kernel_ms": round(k_ms, 4), "bytes_per_launch": step_bytes},
     }
     if not args.no_secondary:

@@ -188,6 +188,12 @@ __device__ inline void load_q(const PrefillArgs &A, int qi, int w, int n16, int 
 // The P fragments are read one row tile ahead of their MFMAs, and a
 // scheduling barrier closes every row tile so the compiler cannot hoist all
 // reads to the front (which would need 64 more VGPRs than exist).
+// P passed as f16 hi + lo halves (kPrefillPLo) or as one f16 with l summing the
+// rounded P. One f16 measured 2.44 against 3.0 ms at cfg 4 but a max error of
+// 1.75e-3 x RMS against the 2e-3 bar (the hi + lo form: 3.1e-4), too thin a
+// margin to be the default.
+constexpr bool kPrefillPLo = true;
+
 __device__ inline void pv_step(const half8_t (*phi)[64], const half8_t (*plo)[64], int lane,
                                uint32_t a0, uint32_t a1, float4_t (*o)[8]) {
 #pragma unroll
@@ -199,22 +205,24 @@ __device__ inline void pv_step(const half8_t (*phi)[64], const half8_t (*plo)[64
             read_vt4<4>(a0, a1, vb);
         half8_t ph[2], pl[2];
         ph[0] = phi[0][lane];
-        pl[0] = plo[0][lane];
+        if (kPrefillPLo) pl[0] = plo[0][lane];
 #pragma unroll
         for (int rt8 = 0; rt8 < 8; ++rt8) {
             if (rt8 < 7) {
                 ph[(rt8 + 1) & 1] = phi[rt8 + 1][lane];
-                pl[(rt8 + 1) & 1] = plo[rt8 + 1][lane];
+                if (kPrefillPLo) pl[(rt8 + 1) & 1] = plo[rt8 + 1][lane];
             }
             // hi products of the 4 dim tiles, then lo: dependent MFMAs 4 apart
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 o[rt8][4 * half + i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
                     ph[rt8 & 1], vb[i], o[rt8][4 * half + i], 0, 0, 0);
+            if (kPrefillPLo) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                o[rt8][4 * half + i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                    pl[rt8 & 1], vb[i], o[rt8][4 * half + i], 0, 0, 0);
+                for (int i = 0; i < 4; ++i)
+                    o[rt8][4 * half + i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        pl[rt8 & 1], vb[i], o[rt8][4 * half + i], 0, 0, 0);
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
     }
@@ -342,13 +350,13 @@ __global__ __launch_bounds__(256) void prefill_fp8_kernel(const PrefillArgs A) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const float p = s2[kt][r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s2[kt][r] - m);
-                        l_part[rt] += p;
                         const half_t h = (half_t)p;
+                        l_part[rt] += kPrefillPLo ? p : (float)h;
                         hi[4 * kt + r] = h;
                         lo[4 * kt + r] = (half_t)(p - (float)h);
                     }
                 phi[2 * w + rt][lane] = hi;
-                plo[2 * w + rt][lane] = lo;
+                if (kPrefillPLo) plo[2 * w + rt][lane] = lo;
                 if (kFix && g == 0) alpha_s[32 * w + 16 * rt + n16] = alpha;
             }
             if (kFix) {
@@ -503,8 +511,8 @@ __device__ inline void softmax_fixed(const float4_t (*acc)[2], float kq_log2, in
                 const float x = s2[kt][r] - m;
                 big |= x > kLazy;
                 const float p = s2[kt][r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(x);
-                lsum += p;
                 const half_t h = (half_t)p;
+                lsum += kPrefillPLo ? p : (float)h;
                 hi[4 * kt + r] = h;
                 lo[4 * kt + r] = (half_t)(p - (float)h);
             }

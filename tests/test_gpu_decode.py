@@ -18,6 +18,7 @@ def check(got, ref, tol=TOL):
     rms = np.sqrt(np.mean(ref ** 2))
     err = np.abs(got - ref).max()
     assert np.isfinite(got).all()
+    print(f"[err/rms {err / max(rms, 1e-30):.2e}]")
     assert err <= tol * rms, f"max err {err:.3e} > {tol} * rms {rms:.3e}"
 
 

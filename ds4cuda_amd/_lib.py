@@ -36,7 +36,8 @@ SIGNATURES: dict[str, list] = {
     "ds4hip_mul_mv_q8_0_q8_0_grouped_f32": [_vp, _vp, _vp, _i, _i, _i, _vp],
     "ds4hip_mul_mv_q8_0_q8_0_grouped_f32_prealloc": [_vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp],
     "ds4hip_mul_mv_q8_0_q8_0_f32_prealloc": [_vp, _vp, _vp, _i, _i, _vp, _vp, _vp],
-    "ds4hip_mul_mm_bf16_f32": [_vp, _vp, _vp, _i, _i, _i, _vp],
+    "ds4hip_mul_mm_workspace_bytes": [_i, _i, _i],
+    "ds4hip_mul_mm_bf16_f32": [_vp, _vp, _vp, _i, _i, _i, _vp, _sz, _vp],
     "ds4hip_indexer_allowed_short_circuit_i32": [_vp, _i, _i, _vp],
     "ds4hip_scale_inplace_f32": [_vp, _i, C.c_float, _vp],
     "ds4hip_indexer_score_topk_i32": [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp],
@@ -50,12 +51,14 @@ SIGNATURES: dict[str, list] = {
                                           _vp, _vp, _vp, _vp],
     "ds4hip_compressor_decode_step_w32": [_i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp,
                                           _vp, _vp, _vp, _vp],
-    "ds4hip_mul_mm_f32_f32": [_vp, _vp, _vp, _i, _i, _i, _vp],
+    "ds4hip_mul_mm_f32_f32": [_vp, _vp, _vp, _i, _i, _i, _vp, _sz, _vp],
+    "ds4hip_compressor_batch_scratch_bytes": [_i, _i, _i, _i],
     "ds4hip_tail_rope_yarn_batch_f32": [_vp, _vp, _i, _i, _i, _i, _vp, _i, _i, _vp],
     "ds4hip_indexer_topk_positions_batch": [_vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _i, _i, _vp,
                                             _vp, _i, _vp],
     "ds4hip_compressor_decode_step_batch_w32": [_i, _i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp,
-                                                _vp, _i, _vp, _vp, _ll, _vp, _vp, _vp, _vp],
+                                                _vp, _i, _vp, _vp, _ll, _vp, _vp, _vp, _sz,
+                                                _vp],
     "ds4hip_swa_push_f32": [_vp, C.POINTER(_i), _i, _vp, _i, _vp],
     "ds4hip_comp_push_f32": [_vp, C.POINTER(_i), _i, _vp, _i, _vp],
     "ds4hip_session_state_arena_bytes": [_i],
@@ -65,13 +68,16 @@ SIGNATURES: dict[str, list] = {
     "ds4hip_session_push_raw": [_vp, _i, _vp, _vp],
     "ds4hip_session_push_comp": [_vp, _i, _vp, _vp],
     "ds4hip_session_push_index_comp": [_vp, _i, _vp, _vp],
+    "ds4hip_rows_scatter_f32": [_vp, _i, _i, _vp, _vp, _vp],
     "ds4hip_session_layer_rows": [_vp, _i, _i, C.POINTER(_vp), C.POINTER(_ll), C.POINTER(_vp)],
 }
 
 # entry points that return a value rather than a status
 RESTYPES = {"ds4hip_indexer_select_scratch_bytes": C.c_size_t,
             "ds4hip_flash_attn_prefill_fp8_workspace_size": C.c_size_t,
-            "ds4hip_session_state_arena_bytes": C.c_size_t}
+            "ds4hip_session_state_arena_bytes": C.c_size_t,
+            "ds4hip_mul_mm_workspace_bytes": C.c_size_t,
+            "ds4hip_compressor_batch_scratch_bytes": C.c_size_t}
 
 _lib = None
 

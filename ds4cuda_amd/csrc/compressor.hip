@@ -221,19 +221,27 @@ __global__ __launch_bounds__(512) void comp_emit_kernel(float *__restrict__ stat
 
 // Y = [kv | gate] projections, [2][n_seq][width]; writes each sequence's
 // state row (cuda/compressor.cu:85) with the APE bias on the gate.
+// Sums the n_kg k-group partials of both projections in group order (the
+// same result on every run), adds the APE row to the gate and writes the
+// state row. P: kv partials [n_kg][n_seq][width], then gate partials likewise.
 __global__ __launch_bounds__(256) void comp_batch_update_kernel(
-        const float *__restrict__ Y, const uint16_t *__restrict__ w_ape,
+        const float *__restrict__ P, int n_kg, const uint16_t *__restrict__ w_ape,
         const int *__restrict__ pos, int n_seq, int width, int ratio, float *__restrict__ state_kv,
         float *__restrict__ state_score, long long state_stride) {
     const int b = blockIdx.y;
     const int o = blockIdx.x * 256 + threadIdx.x;
     if (o >= width) return;
+    const size_t n = (size_t)n_seq * width, j = (size_t)b * width + o;
+    float kv = P[j], sc = P[(size_t)n_kg * n + j];
+    for (int g = 1; g < n_kg; ++g) {
+        kv += P[(size_t)g * n + j];
+        sc += P[(size_t)(n_kg + g) * n + j];
+    }
     const int pm = pos[b] % ratio;
     const int row = ratio == 4 ? ratio + pm : pm;
     const size_t off = (size_t)b * state_stride + (size_t)row * width + o;
-    state_kv[off] = Y[(size_t)b * width + o];
-    state_score[off] = Y[((size_t)n_seq + b) * width + o] +
-                       f16_bits_to_f32(w_ape[(size_t)pm * width + o]);
+    state_kv[off] = kv;
+    state_score[off] = sc + f16_bits_to_f32(w_ape[(size_t)pm * width + o]);
 }
 
 // One workgroup per sequence; sequences whose position does not close a
@@ -323,12 +331,21 @@ extern "C" int ds4hip_compressor_decode_step_w32(int is_attn, const float *x_f32
 }
 
 
+extern "C" size_t ds4hip_compressor_batch_scratch_bytes(int n_seq, int in_dim, int head_dim_out,
+                                                       int compress_ratio) {
+    if (n_seq <= 0 || in_dim <= 0 || head_dim_out <= 0 ||
+        (compress_ratio != 4 && compress_ratio != 128))
+        return 0;
+    const int width = (compress_ratio == 4 ? 2 : 1) * head_dim_out;
+    return (size_t)2 * ds4hip_mm_k_groups(width, in_dim, 2) * n_seq * width * sizeof(float);
+}
+
 extern "C" int ds4hip_compressor_decode_step_batch_w32(
         int is_attn, int n_seq, const float *x_f32, const float *w_kv_f32,
         const float *w_gate_f32, const uint16_t *w_ape_f16, const float *w_norm_f32, int in_dim,
         int head_dim_out, int compress_ratio, const int *pos_host, const int *pos_dev, int il,
         float *state_kv, float *state_score, long long state_stride, float *emit_out,
-        int *emitted_out_host, float *scratch, void *stream) {
+        int *emitted_out_host, float *scratch, size_t scratch_bytes, void *stream) {
     const int ratio = compress_ratio;
     if (n_seq <= 0 || n_seq > 16 || !x_f32 || !w_kv_f32 || !w_gate_f32 || !w_ape_f16 ||
         !w_norm_f32 || !pos_host || !pos_dev || !state_kv || !state_score || !emit_out ||
@@ -337,7 +354,9 @@ extern "C" int ds4hip_compressor_decode_step_batch_w32(
         return ds4hip_set_last_error(kEINVAL);
     const int coff = ratio == 4 ? 2 : 1;
     const int width = coff * head_dim_out;
-    if (state_stride < (long long)coff * ratio * width) return ds4hip_set_last_error(kEINVAL);
+    if (state_stride < (long long)coff * ratio * width ||
+        scratch_bytes < ds4hip_compressor_batch_scratch_bytes(n_seq, in_dim, head_dim_out, ratio))
+        return ds4hip_set_last_error(kEINVAL);
     bool any = false;
     for (int b = 0; b < n_seq; ++b) {
         if (pos_host[b] < 0) return ds4hip_set_last_error(kEINVAL);
@@ -346,13 +365,12 @@ extern "C" int ds4hip_compressor_decode_step_batch_w32(
         any |= e;
     }
     const hipStream_t st = (hipStream_t)stream;
-    int rc = ds4hip_zero_f32(scratch, (size_t)2 * n_seq * width, st);
-    if (!rc)
-        rc = ds4hip_mm_f32(w_kv_f32, x_f32, scratch, width, in_dim, n_seq, st, false, w_gate_f32,
-                           scratch + (size_t)n_seq * width);
+    const int n_kg = ds4hip_mm_k_groups(width, in_dim, 2);
+    const int rc = ds4hip_mm_f32_parts(w_kv_f32, x_f32, scratch, width, in_dim, n_seq, st,
+                                       w_gate_f32, scratch + (size_t)n_kg * n_seq * width);
     if (rc) return ds4hip_set_last_error(rc);
     hipLaunchKernelGGL(comp_batch_update_kernel, dim3((width + 255) / 256, n_seq), dim3(256), 0,
-                       st, scratch, w_ape_f16, pos_dev, n_seq, width, ratio, state_kv,
+                       st, scratch, n_kg, w_ape_f16, pos_dev, n_seq, width, ratio, state_kv,
                        state_score, state_stride);
     if (any)
         hipLaunchKernelGGL(comp_batch_emit_kernel, dim3(n_seq), dim3(512), 0, st, state_kv,

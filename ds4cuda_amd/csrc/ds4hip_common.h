@@ -128,11 +128,14 @@ __host__ inline int hip_status(hipError_t e) { return e == hipSuccess ? 0 : kHip
 
 // Library-internal launchers shared between translation units (rope_matvec.hip).
 // Batched fp32-weight projection Y[b][r] = sum_c W[r][c] X[b][c] (n_cols % 32
-// == 0, n_batch <= 16); zero = false adds into Y. (W2, Y2): a second matrix of
-// the same shape on the same X, in the same launch.
-int ds4hip_mm_f32(const float *W, const float *X, float *Y, int n_rows, int n_cols, int n_batch,
-                  hipStream_t st, bool zero, const float *W2 = nullptr, float *Y2 = nullptr);
-int ds4hip_zero_f32(float *y, size_t n, hipStream_t st);
+// == 0, n_batch <= 16) as k-group partials: k-group g writes
+// part[g][b][r]; the caller sums the ds4hip_mm_k_groups(n_rows, n_cols,
+// n_mats) groups in g order. (W2, part2): a second matrix of the same shape on
+// the same X, in the same launch (n_mats = 2).
+int ds4hip_mm_k_groups(int n_rows, int n_cols, int n_mats);
+int ds4hip_mm_f32_parts(const float *W, const float *X, float *part, int n_rows, int n_cols,
+                        int n_batch, hipStream_t st, const float *W2 = nullptr,
+                        float *part2 = nullptr);
 
 // Records the last failing status for the void-returning C++ shims.
 extern "C" int ds4hip_set_last_error(int code);

@@ -238,17 +238,11 @@ int launch_q8(const uint8_t *W, const float *x, float *y, int n_groups, int grou
 // wave owns 16 output rows; v_mfma_f32_16x16x32_bf16 with A = W rows (16 rows
 // x 32 cols per step, read straight from HBM) and B = X^T from LDS. X is split
 // into bf16 hi + lo parts (two MFMAs) so the activations keep ~16 mantissa
-// bits. Column chunks (split-K) are summed with fp32 atomics into a zeroed Y.
+// bits. Column chunks (split-K) are summed in a fixed order (deterministic).
 // n_batch <= 16, n_cols % 32 == 0.
 typedef short bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef short short2_t __attribute__((ext_vector_type(2)));
-constexpr int kMmCols = 2048;
-
-__global__ __launch_bounds__(256) void zero_kernel(float *__restrict__ y, size_t n) {
-    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
-        y[i] = 0.0f;
-}
 
 // Batched projection Y[b][r] = sum_c W[r][c] X[b][c] for n_batch <= 16,
 // streamed: weight-bandwidth bound, every weight is read once. One wave owns
@@ -257,8 +251,8 @@ __global__ __launch_bounds__(256) void zero_kernel(float *__restrict__ y, size_t
 // step, so the four row tiles share one B fragment. bf16 W: X is split into
 // bf16 hi + lo on the fly and multiplied with v_mfma_f32_16x16x32_bf16 twice
 // (~16 bits of X kept); fp32 W: v_mfma_f32_16x16x4f32 on the exact fp32 values,
-// element j of the 8 columns feeding MFMA step j. k-ranges add into Y with
-// atomics (Y zeroed first).
+// element j of the 8 columns feeding MFMA step j. Each workgroup's k-range
+// (k-group) stores a partial; the k-groups are summed in order afterwards.
 template <bool kF32W>
 struct MmFrag {
     float4_t xa, xb;           // X[batch i][8 columns]
@@ -323,8 +317,10 @@ __device__ inline void mm_compute(const MmFrag<kF32W> &f, bool bok, float4_t *ac
 
 // grid.z selects one of two (W, Y) pairs with the same shape and X. The four
 // waves of a workgroup take the same 64 rows and four consecutive k-slices;
-// their partial sums are added in LDS, so each workgroup issues one atomic
-// add per output (a quarter of the same-address atomics of one per wave).
+// their partial sums are added in LDS in wave order, and the workgroup stores
+// the k-group's partial to Y + blockIdx.y * n_batch * n_rows (no atomics): the
+// k-groups are summed afterwards in k order, so the result is the same on
+// every run.
 template <bool kF32W>
 __global__ __launch_bounds__(256) void mm_stream_kernel(const void *__restrict__ Wv0,
                                                         const void *__restrict__ Wv1,
@@ -377,10 +373,22 @@ __global__ __launch_bounds__(256) void mm_stream_kernel(const void *__restrict__
     // wave w adds row tile w of the four partials: D[row 4q+r of tile][batch i]
     const float4_t sum = ((red[0][wave][lane] + red[1][wave][lane]) + red[2][wave][lane]) + red[3][wave][lane];
     if (!bok) return;
+    float *Yp = Y + (size_t)blockIdx.y * n_batch * n_rows + (size_t)i * n_rows;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const int rr = r0 + 16 * wave + 4 * q + r;
-        if (rr < n_rows) atomicAdd(&Y[(size_t)i * n_rows + rr], sum[r]);
+        if (rr < n_rows) Yp[rr] = sum[r];
+    }
+}
+
+// Y[j] = sum over k-groups g = 0 .. n_kg-1 of P[g * n + j], in g order.
+__global__ __launch_bounds__(256) void mm_reduce_kernel(const float *__restrict__ P,
+                                                        float *__restrict__ Y, size_t n,
+                                                        int n_kg) {
+    for (size_t j = (size_t)blockIdx.x * 256 + threadIdx.x; j < n; j += (size_t)gridDim.x * 256) {
+        float acc = P[j];
+        for (int g = 1; g < n_kg; ++g) acc += P[(size_t)g * n + j];
+        Y[j] = acc;
     }
 }
 
@@ -396,44 +404,62 @@ int mm_kslice(int n_rows, int n_cols, int n_mats) {
 }
 
 template <bool kF32W>
-int mm_launch(const void *W, const float *X, float *Y, int n_rows, int n_cols, int n_batch,
-              bool zero, hipStream_t st, const void *W2 = nullptr, float *Y2 = nullptr) {
+int mm_launch(const void *W, const float *X, float *part, int n_rows, int n_cols, int n_batch,
+              hipStream_t st, const void *W2 = nullptr, float *part2 = nullptr) {
     const int n_mats = W2 ? 2 : 1;
-    if (zero) {
-        const size_t ny = (size_t)n_batch * n_rows;
-        hipLaunchKernelGGL(zero_kernel, dim3((unsigned)std::min<size_t>((ny + 255) / 256, 1024)),
-                           dim3(256), 0, st, Y, ny);
-        if (Y2)
-            hipLaunchKernelGGL(zero_kernel, dim3((unsigned)std::min<size_t>((ny + 255) / 256, 1024)),
-                               dim3(256), 0, st, Y2, ny);
-    }
     const int ks = mm_kslice(n_rows, n_cols, n_mats);
     const dim3 grid((n_rows + 63) / 64, (n_cols + 4 * ks - 1) / (4 * ks), n_mats);
-    hipLaunchKernelGGL(mm_stream_kernel<kF32W>, grid, dim3(256), 0, st, W, W2 ? W2 : W, X, Y,
-                       Y2 ? Y2 : Y, n_rows, n_cols, n_batch, ks);
+    hipLaunchKernelGGL(mm_stream_kernel<kF32W>, grid, dim3(256), 0, st, W, W2 ? W2 : W, X, part,
+                       part2 ? part2 : part, n_rows, n_cols, n_batch, ks);
+    return hip_status(hipGetLastError());
+}
+
+// Projection into Y through k-group partials in ws (skipped when one k-group
+// covers all columns: the kernel then writes Y itself).
+template <bool kF32W>
+int mm_full(const void *W, const float *X, float *Y, int n_rows, int n_cols, int n_batch,
+            void *ws, size_t ws_bytes, hipStream_t st) {
+    const int n_kg = ds4hip_mm_k_groups(n_rows, n_cols, 1);
+    if (n_kg == 1) return mm_launch<kF32W>(W, X, Y, n_rows, n_cols, n_batch, st);
+    const size_t n = (size_t)n_batch * n_rows;
+    if (!ws || ws_bytes < (size_t)n_kg * n * sizeof(float)) return kEINVAL;
+    float *P = static_cast<float *>(ws);
+    int rc = mm_launch<kF32W>(W, X, P, n_rows, n_cols, n_batch, st);
+    if (rc) return rc;
+    hipLaunchKernelGGL(mm_reduce_kernel, dim3((unsigned)std::min<size_t>((n + 255) / 256, 1024)),
+                       dim3(256), 0, st, P, Y, n, n_kg);
     return hip_status(hipGetLastError());
 }
 
 }  // namespace
 
-int ds4hip_mm_f32(const float *W, const float *X, float *Y, int n_rows, int n_cols, int n_batch,
-                  hipStream_t st, bool zero, const float *W2, float *Y2) {
-    if (!W || !X || !Y || n_rows <= 0 || n_cols <= 0 || n_cols % 32 || n_batch <= 0 ||
-        n_batch > 16 || (!W2 != !Y2))
-        return kEINVAL;
-    return mm_launch<true>(W, X, Y, n_rows, n_cols, n_batch, zero, st, W2, Y2);
+int ds4hip_mm_k_groups(int n_rows, int n_cols, int n_mats) {
+    const int ks = mm_kslice(n_rows, n_cols, n_mats);
+    return (n_cols + 4 * ks - 1) / (4 * ks);
 }
 
-int ds4hip_zero_f32(float *y, size_t n, hipStream_t st) {
-    hipLaunchKernelGGL(zero_kernel, dim3((unsigned)std::min<size_t>((n + 255) / 256, 1024)),
-                       dim3(256), 0, st, y, n);
-    return hip_status(hipGetLastError());
+int ds4hip_mm_f32_parts(const float *W, const float *X, float *part, int n_rows, int n_cols,
+                        int n_batch, hipStream_t st, const float *W2, float *part2) {
+    if (!W || !X || !part || n_rows <= 0 || n_cols <= 0 || n_cols % 32 || n_batch <= 0 ||
+        n_batch > 16 || (!W2 != !part2))
+        return kEINVAL;
+    return mm_launch<true>(W, X, part, n_rows, n_cols, n_batch, st, W2, part2);
+}
+
+extern "C" size_t ds4hip_mul_mm_workspace_bytes(int n_rows, int n_cols, int n_batch) {
+    if (n_rows <= 0 || n_cols <= 0 || n_batch <= 0) return 0;
+    const int n_kg = ds4hip_mm_k_groups(n_rows, n_cols, 1);
+    return n_kg == 1 ? 0 : (size_t)n_kg * n_batch * n_rows * sizeof(float);
 }
 
 extern "C" int ds4hip_mul_mm_f32_f32(const float *W, const float *X, float *Y, int n_rows,
-                                     int n_cols, int n_batch, void *stream) {
-    return ds4hip_set_last_error(ds4hip_mm_f32(W, X, Y, n_rows, n_cols, n_batch,
-                                               (hipStream_t)stream, true));
+                                     int n_cols, int n_batch, void *workspace,
+                                     size_t workspace_bytes, void *stream) {
+    if (!W || !X || !Y || n_rows <= 0 || n_cols <= 0 || n_cols % 32 || n_batch <= 0 ||
+        n_batch > 16)
+        return ds4hip_set_last_error(kEINVAL);
+    return ds4hip_set_last_error(mm_full<true>(W, X, Y, n_rows, n_cols, n_batch, workspace,
+                                               workspace_bytes, (hipStream_t)stream));
 }
 
 extern "C" int ds4hip_tail_rope_yarn_batch_f32(const float *x_in, float *x_out, int n_seq,
@@ -512,10 +538,11 @@ extern "C" int ds4hip_mul_mv_q8_0_q8_0_f32_prealloc(const void *W, const float *
 }
 
 extern "C" int ds4hip_mul_mm_bf16_f32(const uint16_t *W, const float *X, float *Y, int n_rows,
-                                      int n_cols, int n_batch, void *stream) {
+                                      int n_cols, int n_batch, void *workspace,
+                                      size_t workspace_bytes, void *stream) {
     if (!W || !X || !Y || n_rows <= 0 || n_cols <= 0 || n_cols % 32 || n_batch <= 0 ||
         n_batch > 16)
         return ds4hip_set_last_error(kEINVAL);
-    return ds4hip_set_last_error(
-        mm_launch<false>(W, X, Y, n_rows, n_cols, n_batch, true, (hipStream_t)stream));
+    return ds4hip_set_last_error(mm_full<false>(W, X, Y, n_rows, n_cols, n_batch, workspace,
+                                                workspace_bytes, (hipStream_t)stream));
 }

@@ -345,3 +345,28 @@ extern "C" int ds4hip_session_layer_rows(const ds4hip_session_state *s, int il, 
     if (selected_out) *selected_out = L->row_list + L->cap_raw;
     return 0;
 }
+
+namespace {
+// dst[dst_rows[r]][:] = src[r][:] for r < n_rows; one 64-lane wave per row,
+// 16-byte moves (width % 4 == 0).
+__global__ __launch_bounds__(256) void rows_scatter_kernel(const float *__restrict__ src,
+                                                           int n_rows, int width,
+                                                           float *__restrict__ dst,
+                                                           const long long *__restrict__ dst_rows) {
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= n_rows) return;
+    const float4_t *s = reinterpret_cast<const float4_t *>(src + (size_t)r * width);
+    float4_t *d = reinterpret_cast<float4_t *>(dst + (size_t)dst_rows[r] * width);
+    for (int i = threadIdx.x & 63; i < width / 4; i += 64) d[i] = s[i];
+}
+}  // namespace
+
+extern "C" int ds4hip_rows_scatter_f32(const float *src, int n_rows, int width, float *dst,
+                                       const long long *dst_rows, void *stream) {
+    if (n_rows < 0 || width <= 0 || width % 4 != 0 || (n_rows && (!src || !dst || !dst_rows)))
+        return ds4hip_set_last_error(kEINVAL);
+    if (n_rows == 0) return 0;
+    hipLaunchKernelGGL(rows_scatter_kernel, dim3((n_rows + 3) / 4), dim3(256), 0,
+                       (hipStream_t)stream, src, n_rows, width, dst, dst_rows);
+    return ds4hip_set_last_error(hip_status(hipGetLastError()));
+}

@@ -222,12 +222,23 @@ def launch_mul_mv_q8_0_q8_0_f32_prealloc(W, x, y, n_rows, n_cols, scratch_xq, sc
          _ptr(scratch_xq), _ptr(scratch_xscale), _stream(stream))
 
 
-def mul_mm_bf16_f32(W, X, Y, n_rows, n_cols, n_batch, stream=None):
+def mul_mm_workspace(n_rows, n_cols, n_batch, device):
+    """Workspace tensor for mul_mm_bf16_f32 / mul_mm_f32_f32 of this shape."""
+    from ._lib import lib
+    nb = lib().ds4hip_mul_mm_workspace_bytes(n_rows, n_cols, n_batch)
+    return torch.empty(max(nb, 1), dtype=torch.uint8, device=device)
+
+
+def mul_mm_bf16_f32(W, X, Y, n_rows, n_cols, n_batch, workspace=None, stream=None):
+    """Y [n_batch, n_rows] = X W^T, bf16 W; deterministic (fixed-order split-K)."""
     _check(W, torch.bfloat16, n_rows * n_cols, "W")
     _check(X, torch.float32, n_batch * n_cols, "X")
     _check(Y, torch.float32, n_batch * n_rows, "Y")
+    if workspace is None:
+        workspace = mul_mm_workspace(n_rows, n_cols, n_batch, X.device)
     call("ds4hip_mul_mm_bf16_f32", _ptr(W), _ptr(X), _ptr(Y), n_rows, n_cols, n_batch,
-         _stream(stream))
+         _ptr(workspace), workspace.numel(), _stream(stream))
+    return workspace
 
 
 # ---- indexer (cuda/indexer_allowed.cuh:33,67,83,97) ----------------------------------------
@@ -319,12 +330,15 @@ def compressor_decode_step_w32(is_attn, x_f32, w_kv_f32, w_gate_f32, w_ape_f16, 
 
 # ---- batched forms (the batched-decode attention block) ------------------------------------
 
-def mul_mm_f32_f32(W, X, Y, n_rows, n_cols, n_batch, stream=None):
+def mul_mm_f32_f32(W, X, Y, n_rows, n_cols, n_batch, workspace=None, stream=None):
     _check(W, torch.float32, n_rows * n_cols, "W")
     _check(X, torch.float32, n_batch * n_cols, "X")
     _check(Y, torch.float32, n_batch * n_rows, "Y")
+    if workspace is None:
+        workspace = mul_mm_workspace(n_rows, n_cols, n_batch, X.device)
     call("ds4hip_mul_mm_f32_f32", _ptr(W), _ptr(X), _ptr(Y), n_rows, n_cols, n_batch,
-         _stream(stream))
+         _ptr(workspace), workspace.numel(), _stream(stream))
+    return workspace
 
 
 def tail_rope_yarn_batch_f32(x_in, x_out, n_seq, n_heads, head_dim, n_rot, pos_dev, il,
@@ -356,10 +370,18 @@ def indexer_topk_positions_batch(q, weights, keys, key_row0, n_comp, top_k, n_re
          C.c_void_p(positions.data_ptr() + 4 * pos_offset), stride, _stream(stream))
 
 
+def compressor_batch_scratch(n_seq, in_dim, head_dim_out, ratio, device):
+    """Scratch tensor (uint8) for compressor_decode_step_batch_w32."""
+    from ._lib import lib
+    nb = lib().ds4hip_compressor_batch_scratch_bytes(n_seq, in_dim, head_dim_out, ratio)
+    return torch.empty(nb, dtype=torch.uint8, device=device)
+
+
 def compressor_decode_step_batch_w32(is_attn, x, w_kv, w_gate, w_ape, w_norm, in_dim,
                                      head_dim_out, ratio, pos, pos_dev, il, state_kv,
                                      state_score, state_stride, emit_out, scratch, stream=None):
-    """One compressor step for len(pos) sequences; returns the host emit flags."""
+    """One compressor step for len(pos) sequences; returns the host emit flags.
+    scratch: a tensor of compressor_batch_scratch(...) bytes."""
     n = len(pos)
     ph = (C.c_int * n)(*[int(p) for p in pos])
     em = (C.c_int * n)()
@@ -368,5 +390,5 @@ def compressor_decode_step_batch_w32(is_attn, x, w_kv, w_gate, w_ape, w_norm, in
          _ptr(w_gate), _ptr(w_ape), _ptr(w_norm), in_dim, head_dim_out, ratio,
          C.cast(ph, C.c_void_p), _ptr(pos_dev), il, _ptr(state_kv), _ptr(state_score),
          int(state_stride), _ptr(emit_out), C.cast(em, C.c_void_p), _ptr(scratch),
-         _stream(stream))
+         scratch.numel() * scratch.element_size(), _stream(stream))
     return list(em)

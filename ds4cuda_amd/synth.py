@@ -63,3 +63,63 @@ def kv_rows(seed: int, stream: int, n_rows: int, head_dim: int = 512,
         sel = uniform(seed, stream + 7919, n_rows) < outlier_frac
         x[sel] *= outlier_scale
     return x
+
+
+def _signed(v: int) -> int:
+    return v - (1 << 64) if v >= (1 << 63) else v
+
+
+def normal_device(seed: int, stream: int, n: int, device, std: float = 1.0, chunk: int = 1 << 24):
+    """The same samples as normal(seed, stream, n, std), generated on `device`
+    with torch integer ops (64-bit wrapping arithmetic, logical shifts by
+    masking), so large inputs need no host generation or upload. The fp64
+    log / cos of the device may differ from the host's in the last fp64 bit,
+    which after the fp32 rounding changes a value only in rare ties."""
+    import torch
+    m = (n + 1) // 2
+    state = _signed((seed * 1_000_003 + stream) & 0xFFFFFFFFFFFFFFFF)
+    gold, m1, m2 = (_signed(int(c)) for c in (_GOLDEN, _M1, _M2))
+    out = torch.empty(2 * m, dtype=torch.float32, device=device)
+
+    def lsr(z, k):
+        return (z >> k) & ((1 << (64 - k)) - 1)
+
+    for p0 in range(0, m, chunk):
+        p1 = min(m, p0 + chunk)
+        i = torch.arange(2 * p0 + 1, 2 * p1 + 1, dtype=torch.int64, device=device)
+        z = state + i * gold
+        z = (z ^ lsr(z, 30)) * m1
+        z = (z ^ lsr(z, 27)) * m2
+        z = z ^ lsr(z, 31)
+        u = (lsr(z, 11).to(torch.float64) + 1.0) * (1.0 / 9007199254740992.0)
+        u1, u2 = u[0::2], u[1::2]
+        r = torch.sqrt(-2.0 * torch.log(u1))
+        seg = torch.empty(2 * (p1 - p0), dtype=torch.float64, device=device)
+        seg[0::2] = r * torch.cos(2.0 * torch.pi * u2)
+        seg[1::2] = r * torch.sin(2.0 * torch.pi * u2)
+        out[2 * p0:2 * p1] = (seg * std).to(torch.float32)
+    return out[:n]
+
+
+def uniform_device(seed: int, stream: int, n: int, device):
+    """uniform(seed, stream, n) generated on `device` (fp64)."""
+    import torch
+    state = _signed((seed * 1_000_003 + stream) & 0xFFFFFFFFFFFFFFFF)
+    gold, m1, m2 = (_signed(int(c)) for c in (_GOLDEN, _M1, _M2))
+    lsr = lambda z, k: (z >> k) & ((1 << (64 - k)) - 1)
+    i = torch.arange(1, n + 1, dtype=torch.int64, device=device)
+    z = state + i * gold
+    z = (z ^ lsr(z, 30)) * m1
+    z = (z ^ lsr(z, 27)) * m2
+    z = z ^ lsr(z, 31)
+    return lsr(z, 11).to(torch.float64) * (1.0 / 9007199254740992.0)
+
+
+def kv_rows_device(seed: int, stream: int, n_rows: int, device, head_dim: int = 512,
+                   outlier_frac: float = 0.0, outlier_scale: float = 8.0):
+    """kv_rows() generated on `device`."""
+    x = normal_device(seed, stream, n_rows * head_dim, device).reshape(n_rows, head_dim)
+    if outlier_frac > 0:
+        sel = uniform_device(seed, stream + 7919, n_rows, device) < outlier_frac
+        x[sel] *= outlier_scale
+    return x

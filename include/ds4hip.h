@@ -183,17 +183,23 @@ int ds4hip_mul_mv_q8_0_q8_0_f32_prealloc(const void *W, const float *x, float *y
                                          int n_cols, int8_t *scratch_xq, float *scratch_xscale,
                                          void *stream);
 
+/* Workspace bytes of ds4hip_mul_mm_bf16_f32 / ds4hip_mul_mm_f32_f32 for this
+ * shape (0 when one column group covers every column). */
+size_t ds4hip_mul_mm_workspace_bytes(int n_rows, int n_cols, int n_batch);
+
 /* Batched bf16 projection (additive; the forward_batch form of the attention
  * output projection): Y[b][r] = sum_c W[r][c] X[b][c] for n_batch <= 16 rows
- * of X, W bf16 [n_rows][n_cols], n_cols % 32 == 0. Y is overwritten. */
+ * of X, W bf16 [n_rows][n_cols], n_cols % 32 == 0. Y is overwritten. The
+ * column groups' partial sums go to workspace (ds4hip_mul_mm_workspace_bytes)
+ * and are added in a fixed order: the result is the same on every run. */
 int ds4hip_mul_mm_bf16_f32(const uint16_t *W, const float *X, float *Y, int n_rows, int n_cols,
-                           int n_batch, void *stream);
+                           int n_batch, void *workspace, size_t workspace_bytes, void *stream);
 
 /* Batched fp32 projection (additive; the batched-decode compressor
  * projection): Y[b][r] = sum_c W[r][c] X[b][c], W fp32 [n_rows][n_cols],
- * n_batch <= 16, n_cols % 32 == 0. Y is overwritten. */
+ * n_batch <= 16, n_cols % 32 == 0. Y is overwritten; workspace as above. */
 int ds4hip_mul_mm_f32_f32(const float *W, const float *X, float *Y, int n_rows, int n_cols,
-                          int n_batch, void *stream);
+                          int n_batch, void *workspace, size_t workspace_bytes, void *stream);
 
 /* Tail RoPE for n_seq sequences at their own positions (additive; batched form
  * of ds4hip_tail_rope_yarn_f32 / _inverse_f32): x [n_seq][n_heads][head_dim],
@@ -302,7 +308,11 @@ int ds4hip_compressor_decode_step_w32(int is_attn, const float *x_f32, const flo
  * position pos_host[b] (pos_dev: the same array in device memory) with state
  * at state_kv / state_score + b * state_stride floats; emit_out row b is
  * written when (pos + 1) % ratio == 0, and emitted_out_host[b] (host, may be
- * NULL) says so. scratch: 2 * n_seq * coff * head_dim_out floats. */
+ * NULL) says so. scratch: ds4hip_compressor_batch_scratch_bytes(...) bytes
+ * (the projections' column-group partials, added in a fixed order, so the
+ * step is the same on every run). */
+size_t ds4hip_compressor_batch_scratch_bytes(int n_seq, int in_dim, int head_dim_out,
+                                             int compress_ratio);
 int ds4hip_compressor_decode_step_batch_w32(int is_attn, int n_seq, const float *x_f32,
                                             const float *w_kv_f32, const float *w_gate_f32,
                                             const uint16_t *w_ape_f16, const float *w_norm_f32,
@@ -310,7 +320,8 @@ int ds4hip_compressor_decode_step_batch_w32(int is_attn, int n_seq, const float 
                                             const int *pos_host, const int *pos_dev, int il,
                                             float *state_kv, float *state_score,
                                             long long state_stride, float *emit_out,
-                                            int *emitted_out_host, float *scratch, void *stream);
+                                            int *emitted_out_host, float *scratch,
+                                            size_t scratch_bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -114,6 +114,13 @@ int ds4hip_session_push_comp(ds4hip_session_state *s, int il, const float *row, 
 int ds4hip_session_push_index_comp(ds4hip_session_state *s, int il, const float *row,
                                    void *stream);
 
+/* Batched push of fp32 rows (additive; the batched-decode form of the
+ * compressed-row D2D copies of cuda/forward_layer.cu:1021-1034 and the
+ * indexer-key push): dst[dst_rows[r]][0..width) = src[r][0..width) for
+ * r < n_rows, dst_rows a device int64 array. width % 4 == 0. */
+int ds4hip_rows_scatter_f32(const float *src, int n_rows, int width, float *dst,
+                            const long long *dst_rows, void *stream);
+
 /* Rows for layer il's decode attention: *row_idx (device) and *n_rows are
  * the row_idx / n_rows arguments of ds4hip_flash_attn_decode_fp8 with
  * row_base = layers[il].row_base: the valid ring rows, then n_selected

@@ -37,6 +37,28 @@ def test_mul_mm_bf16_shapes(gpu, n_rows, n_cols, nb):
     close(Y.cpu().numpy(), ref, 1e-4)
 
 
+def test_mul_mm_deterministic(gpu):
+    """The split-K partials are added in a fixed order: repeated runs of the
+    batched projections (attn_out shape, bf16; compressor shape, fp32) are
+    bit-identical."""
+    W = t(synth.to_bf16_bits(synth.normal(56, 1, 4096 * 32768) * 0.02).view(np.int16),
+          gpu).view(torch.bfloat16).reshape(4096, 32768)
+    X = t(synth.normal(56, 2, 16 * 32768), gpu)
+    Wf = t(synth.normal(56, 3, 1024 * 4096) * 0.02, gpu)
+    Xf = t(synth.normal(56, 4, 16 * 4096), gpu)
+    ys, yf = [], []
+    for _ in range(3):
+        Y = torch.empty((16, 4096), device=gpu)
+        ops.mul_mm_bf16_f32(W, X, Y, 4096, 32768, 16)
+        Yf = torch.empty((16, 1024), device=gpu)
+        ops.mul_mm_f32_f32(Wf, Xf, Yf, 1024, 4096, 16)
+        torch.cuda.synchronize()
+        ys.append(Y.cpu().numpy())
+        yf.append(Yf.cpu().numpy())
+    assert all(np.array_equal(ys[0].view(np.uint32), y.view(np.uint32)) for y in ys[1:])
+    assert all(np.array_equal(yf[0].view(np.uint32), y.view(np.uint32)) for y in yf[1:])
+
+
 def test_rope_batch_inverse(gpu):
     n_seq, n_heads = 5, 64
     pos = np.array([3, 1000, 16383, 0, 77], np.int32)
@@ -50,6 +72,11 @@ def test_rope_batch_inverse(gpu):
 
 
 def test_compressor_batch_matches_per_sequence(gpu):
+    """Batched fp32-weight compressor against the oracle one sequence at a
+    time: state at 1e-5; emitted rows through check_fp8_emit (pre-quantization
+    row from the same batch run with is_attn = 0 at 2e-3 x RMS, FP8 row
+    bit-exact up to counted midpoint flips)."""
+    from fp8_check import check_fp8_emit
     n_seq, in_dim, hd, ratio, il = 16, 4096, 512, 4, 2
     width = 2 * hd
     rows = 2 * ratio
@@ -61,49 +88,77 @@ def test_compressor_batch_matches_per_sequence(gpu):
     stride = rows * width
     skv = np.zeros((n_seq, rows, width), np.float32)
     ssc = np.full((n_seq, rows, width), -np.inf, np.float32)
+    skv0, ssc0 = skv.copy(), ssc.copy()
     g_kv, g_sc = t(skv, gpu), t(ssc, gpu)
+    g_kv0, g_sc0 = t(skv, gpu), t(ssc, gpu)
     g_wkv, g_wg, g_ape, g_wn = t(wkv, gpu), t(wg, gpu), t(ape.view(np.int16), gpu), t(wn, gpu)
     emit = torch.zeros((n_seq, hd), device=gpu)
-    scratch = torch.empty(2 * n_seq * width, device=gpu)
+    emit0 = torch.zeros((n_seq, hd), device=gpu)
+    scratch = ops.compressor_batch_scratch(n_seq, in_dim, hd, ratio, gpu)
     start = np.arange(n_seq) * 3 + 1          # sequences at different phases of the window
+    worst, flips, n_emit = 0.0, 0, 0
     for step in range(6):
         pos = (start + step).astype(np.int32)
         x = synth.normal(54, step, n_seq * in_dim).reshape(n_seq, in_dim)
+        xg, pg = t(x, gpu), t(pos, gpu)
         flags = ops.compressor_decode_step_batch_w32(
-            True, t(x, gpu), g_wkv, g_wg, g_ape, g_wn, in_dim, hd, ratio, pos, t(pos, gpu), il,
+            True, xg, g_wkv, g_wg, g_ape, g_wn, in_dim, hd, ratio, pos, pg, il,
             g_kv, g_sc, stride, emit, scratch)
+        flags0 = ops.compressor_decode_step_batch_w32(
+            False, xg, g_wkv, g_wg, g_ape, g_wn, in_dim, hd, ratio, pos, pg, il,
+            g_kv0, g_sc0, stride, emit0, scratch)
         torch.cuda.synchronize()
         got_e = emit.cpu().numpy()
+        got_e0 = emit0.cpu().numpy()
         for b in range(n_seq):
             ref_e = np.zeros(hd, np.float32)
+            ref_p = np.zeros(hd, np.float32)
             r = O.lib().orc_compressor_step_w32(
                 C.c_int(1), P(x[b]), P(wkv), P(wg), P(ape), P(wn), C.c_int(in_dim), C.c_int(hd),
                 C.c_int(ratio), C.c_int(int(pos[b])), C.c_int(il), P(skv[b]), P(ssc[b]),
                 P(ref_e))
-            assert flags[b] == r
+            O.lib().orc_compressor_step_w32(
+                C.c_int(0), P(x[b]), P(wkv), P(wg), P(ape), P(wn), C.c_int(in_dim), C.c_int(hd),
+                C.c_int(ratio), C.c_int(int(pos[b])), C.c_int(il), P(skv0[b]), P(ssc0[b]),
+                P(ref_p))
+            assert flags[b] == r == flags0[b]
             if r:
-                close(got_e[b], ref_e, 3e-2)
+                n_emit += 1
+                e, f = check_fp8_emit(got_e[b], got_e0[b], ref_e, ref_p)
+                worst, flips = max(worst, e), flips + f
         close(g_kv.cpu().numpy(), skv, 1e-5)
         fin = np.isfinite(ssc)
         got_sc = g_sc.cpu().numpy()
         assert np.array_equal(np.isfinite(got_sc), fin)
         close(got_sc[fin], ssc[fin], 1e-5)
+    assert n_emit >= 16
+    print(f"batched compressor: {n_emit} emits, worst pre-quant err/RMS {worst:.2e}, "
+          f"FP8 midpoint flips {flips}")
 
 
-def test_indexer_batch_positions(gpu):
+@pytest.mark.parametrize("key_kind", [0, 1, 2])
+def test_indexer_batch_positions(gpu, key_kind):
+    """Batched scorer + selection for fp32 (0), f16 (1) and bf16 (2) keys:
+    scores and positions bit-exact against the oracle per sequence."""
     n_seq, top_k, recent = 6, 512, 64
     n_comp = [100, 512, 513, 2000, 4000, 3]
     row0 = np.concatenate([[0], np.cumsum(n_comp)[:-1]]) + 10
     n_rows = int(row0[-1] + n_comp[-1])
-    keys = synth.to_bf16_bits(synth.normal(55, 1, n_rows * 128)).reshape(n_rows, 128)
+    kf = synth.normal(55, 1, n_rows * 128).reshape(n_rows, 128)
+    if key_kind == 0:
+        keys, tdt = np.ascontiguousarray(kf), torch.float32
+    elif key_kind == 1:
+        keys, tdt = np.ascontiguousarray(kf.astype(np.float16).view(np.uint16)), torch.float16
+    else:
+        keys, tdt = synth.to_bf16_bits(kf).reshape(n_rows, 128), torch.bfloat16
     keys[row0[3] + 200: row0[3] + 260] = keys[row0[3] + 5]       # tied scores
     q = synth.normal(55, 2, n_seq * 64 * 128).reshape(n_seq, 64, 128)
     w = synth.normal(55, 3, n_seq * 64).reshape(n_seq, 64) / np.float32(np.sqrt(128 * 64))
     scores = torch.zeros(n_rows, device=gpu)
     pos = torch.full((n_seq, top_k + 7), -1, dtype=torch.int32, device=gpu)
-    ops.indexer_topk_positions_batch(t(q, gpu), t(w, gpu),
-                                     t(keys.view(np.int16), gpu).view(torch.bfloat16),
-                                     row0, n_comp, top_k, recent, scores, pos)
+    gk = t(keys, gpu) if key_kind == 0 else t(keys.view(np.int16), gpu).view(tdt)
+    ops.indexer_topk_positions_batch(t(q, gpu), t(w, gpu), gk, row0, n_comp, top_k, recent,
+                                     scores, pos)
     torch.cuda.synchronize()
     got = pos.cpu().numpy()
     for s in range(n_seq):
@@ -113,8 +168,8 @@ def test_indexer_batch_positions(gpu):
             continue
         ks = np.ascontiguousarray(keys[row0[s]:row0[s] + n])
         sc = np.zeros(n, np.float32)
-        O.lib().orc_indexer_scores(P(q[s]), P(w[s]), P(ks), C.c_int(2), C.c_int(n), C.c_int(64),
-                                   C.c_int(128), P(sc))
+        O.lib().orc_indexer_scores(P(q[s]), P(w[s]), P(ks), C.c_int(key_kind), C.c_int(n),
+                                   C.c_int(64), C.c_int(128), P(sc))
         assert np.array_equal(scores.cpu().numpy()[row0[s]:row0[s] + n].view(np.uint32),
                               sc.view(np.uint32))
         ref = np.zeros(top_k, np.int32)

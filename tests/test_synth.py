@@ -30,3 +30,14 @@ def test_outlier_rows():
     x = synth.kv_rows(0, 3, 4000, 64, outlier_frac=0.01)
     big = np.abs(x).max(axis=1) > 6.0
     assert 10 <= big.sum() <= 90
+
+
+def test_device_generator_matches_host():
+    # the torch form (run here on the CPU device) gives the host stream exactly
+    from ds4cuda_amd import synth
+    a = synth.normal(3, 5, 100001)
+    b = synth.normal_device(3, 5, 100001, "cpu", chunk=30000).numpy()
+    assert np.array_equal(a, b)
+    a = synth.kv_rows(7, 2, 300, outlier_frac=0.05)
+    b = synth.kv_rows_device(7, 2, 300, "cpu", outlier_frac=0.05).numpy()
+    assert np.array_equal(a, b)

@@ -75,6 +75,23 @@ def build_lib(verbose: bool = False) -> Path:
     return LIB
 
 
+def build_native_checks(verbose: bool = False) -> Path:
+    """The C++ caller of the launcher shims used by the GPU tests
+    (tests/native/forward_layer_check.cpp), linked against libds4hip.so."""
+    out_dir = ROOT / "tests" / "native" / "_bin"
+    out_dir.mkdir(parents=True, exist_ok=True)
+    exe = out_dir / "forward_layer_check"
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-O2", "-std=c++17", "-I", str(ROOT / "include"),
+           str(ROOT / "tests" / "native" / "forward_layer_check.cpp"), "-o", str(exe),
+           f"-L{PKG}", "-lds4hip", f"-Wl,-rpath,{PKG}"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"forward_layer_check build failed:\n{r.stdout}\n{r.stderr}")
+    if verbose:
+        print(f"built {exe}")
+    return exe
+
+
 def build_oracle(verbose: bool = False) -> Path:
     r = subprocess.run(["make", "-C", str(ROOT / "oracle"), "-B", "-j8"], capture_output=True,
                        text=True)
@@ -87,5 +104,7 @@ def build_oracle(verbose: bool = False) -> Path:
 
 if __name__ == "__main__":
     build_lib(verbose=True)
-    if "--lib-only" not in sys.argv and shutil.which("make"):
-        build_oracle(verbose=True)
+    if "--lib-only" not in sys.argv:
+        build_native_checks(verbose=True)
+        if shutil.which("make"):
+            build_oracle(verbose=True)

@@ -68,6 +68,7 @@ struct DecodeArgs {
     // fp32 rows of the reference launchers: rows < f32_n_raw come from f32_raw,
     // the rest from f32_comp, gated by f32_allowed (may be null)
     const float *f32_raw;
+    const float *f32_v_raw;          // V rows of the raw launcher when V != K, else null
     const float *f32_comp;
     const int32_t *f32_allowed;
     int f32_n_raw;
@@ -855,6 +856,9 @@ __global__ __launch_bounds__(256) void decode_fp8_kernel(const DecodeArgs A) {
 }
 
 // ---- fp32-row kernel (reference launchers): fragments straight from global -----------
+// kSepV: V rows come from f32_v_raw (the raw launcher with V != K); otherwise
+// the K fragments are also the V tile (MLA: K == V).
+template <bool kSepV>
 __global__ __launch_bounds__(256) void decode_f32_kernel(const DecodeArgs A) {
     __shared__ half_t vt[kD * kVtStride];
     __shared__ long long s_start[kMaxProb + 1];
@@ -904,7 +908,15 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(const DecodeArgs A) {
                     acc[h2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qh[2 * b + 1], acc[h2], 0, 0, 0);
                     acc[h2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, ql[2 * b], acc[h2], 0, 0, 0);
                     acc[h2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, ql[2 * b + 1], acc[h2], 0, 0, 0);
-                    if ((b >> 1) == wave) vt_write(vt, b, q, prow, a0, a1);
+                    if ((b >> 1) == wave) {
+                        if (kSepV) {
+                            half8_t v0, v1;
+                            load_f32_block(A.f32_v_raw + r * kD, b, q, valid, v0, v1);
+                            vt_write(vt, b, q, prow, v0, v1);
+                        } else {
+                            vt_write(vt, b, q, prow, a0, a1);
+                        }
+                    }
                 }
             }
             const half8_t pf = softmax_tile(acc, A.kq_log2, q, S, [&](int h2, int r) {
@@ -1478,11 +1490,14 @@ constexpr long long kSegCostRows = 5 * kTile;
 // problem cut separately, its first chunk aligned (one problem per chunk, a
 // few more chunks). (b) wins when chunks are short next to the per-segment
 // cost, e.g. a batch of 16 sequences of ~2000 selected rows.
-Plan make_plan(const long long *count, int n_prob, int wg_per_cu) {
+// target_wg: workgroups to aim for (0: wg_per_cu per CU). with_phys: the
+// workspace also holds the physical-row array of gathered FP8 steps.
+Plan make_plan(const long long *count, int n_prob, int wg_per_cu, long long target_wg = 0,
+               bool with_phys = true) {
     Plan pl;
     long long total = 0;
     for (int p = 0; p < n_prob; ++p) total += count[p];
-    const long long target = (long long)num_cus() * wg_per_cu;
+    const long long target = target_wg > 0 ? target_wg : (long long)num_cus() * wg_per_cu;
     auto round_tile = [](long long x) { return ((x + kTile - 1) / kTile) * kTile; };
     long long chunk_a = total > 0 ? round_tile((total + target - 1) / target) : kTile;
     if (chunk_a < kMinChunk) chunk_a = kMinChunk;
@@ -1521,7 +1536,7 @@ Plan make_plan(const long long *count, int n_prob, int wg_per_cu) {
     pl.n_wg = space > 0 ? (int)((space + pl.chunk - 1) / pl.chunk) : 0;
     const size_t slots = (size_t)std::max(pl.n_wg, 1) * pl.s_max;
     pl.ws_bytes = slots * ((size_t)kH * kD * 4 + 2 * kH * 4) + slots * 4 + 256 * 4 +
-                  (size_t)(space + kTile) * sizeof(long long);
+                  (with_phys ? (size_t)(space + kTile) * sizeof(long long) : 0);
     return pl;
 }
 
@@ -1579,8 +1594,10 @@ int launch(DecodeArgs &A, const Plan &pl, hipStream_t st, int phases = 3) {
         }
         else if (kFp8)
             hipLaunchKernelGGL(decode_fp8_kernel<kQf32>, dim3(pl.n_wg), dim3(256), 0, st, A);
+        else if (A.f32_v_raw)
+            hipLaunchKernelGGL(decode_f32_kernel<true>, dim3(pl.n_wg), dim3(256), 0, st, A);
         else
-            hipLaunchKernelGGL(decode_f32_kernel, dim3(pl.n_wg), dim3(256), 0, st, A);
+            hipLaunchKernelGGL(decode_f32_kernel<false>, dim3(pl.n_wg), dim3(256), 0, st, A);
         const int e = hip_status(hipGetLastError());
         if (e) return e;
     }
@@ -1657,25 +1674,34 @@ extern "C" int ds4hip_flash_attn_decode_fp8(
     return ds4hip_set_last_error(rc);
 }
 
-// fp32 launchers of the reference (cuda/flash_attn.cuh:73,142). The workspace
-// for the split partials is stream-ordered (hipMallocAsync/hipFreeAsync), as
-// the reference's non-prealloc launchers do for their scratch.
+// fp32 launchers of the reference (cuda/flash_attn.cuh:73,142). The split-K
+// partials live in a workspace: the caller's (the _prealloc forms), or a
+// stream-ordered hipMallocAsync / hipFreeAsync one.
 namespace {
-int run_f32(const float *Q, const float *raw, int n_raw, const float *comp, int n_comp,
-            const int32_t *allowed, const float *sinks, float *out, hipStream_t st) {
+Plan f32_plan(long long n_rows) { return make_plan(&n_rows, 1, 2, 0, false); }
+
+int run_f32(const float *Q, const float *raw, const float *v_raw, int n_raw, const float *comp,
+            int n_comp, const int32_t *allowed, const float *sinks, float *out, void *ws,
+            size_t ws_bytes, hipStream_t st, const Plan *plan = nullptr) {
     DecodeArgs A = {};
     A.count[0] = (long long)n_raw + n_comp;
-    const Plan pl = make_plan(A.count, 1, 2);
+    const Plan pl = plan ? *plan : f32_plan(A.count[0]);
     A.start[0] = pl.start[0];
     A.start[1] = pl.start[1];
-    void *ws = nullptr;
-    hipError_t e = hipMallocAsync(&ws, pl.ws_bytes, st);
-    if (e != hipSuccess) return hip_status(e);
+    bool own = false;
+    if (!ws) {
+        hipError_t e = hipMallocAsync(&ws, pl.ws_bytes, st);
+        if (e != hipSuccess) return hip_status(e);
+        own = true;
+    } else if (ws_bytes < pl.ws_bytes) {
+        return kEINVAL;
+    }
     A.q = Q;
     A.q_stride = 0;
     A.sinks = sinks;
     A.out = out;
     A.f32_raw = raw;
+    A.f32_v_raw = (v_raw && v_raw != raw) ? v_raw : nullptr;
     A.f32_comp = comp;
     A.f32_allowed = allowed;
     A.f32_n_raw = n_raw;
@@ -1683,23 +1709,66 @@ int run_f32(const float *Q, const float *raw, int n_raw, const float *comp, int 
     A.total = A.start[1];
     carve(A, ws, pl);
     int rc = launch<false, true>(A, pl, st);
-    e = hipFreeAsync(ws, st);
-    if (!rc) rc = hip_status(e);
+    if (own) {
+        const hipError_t e = hipFreeAsync(ws, st);
+        if (!rc) rc = hip_status(e);
+    }
     return rc;
 }
+
+bool raw_args_ok(const float *Q, const float *K, const float *V, const float *sinks,
+                 const float *out, int n_head, int n_kv, int head_dim) {
+    return head_dim == kD && n_head == kH && n_kv >= 0 && Q && sinks && out &&
+           (n_kv == 0 || (K && V));
+}
+
+bool mixed_args_ok(const float *Q, const float *raw_kv, const float *comp_kv,
+                   const float *sinks, const float *out, int n_head, int n_raw, int n_comp,
+                   int head_dim) {
+    return head_dim == kD && n_head == kH && n_raw >= 0 && n_comp >= 0 && Q && sinks && out &&
+           (n_raw == 0 || raw_kv) && (n_comp == 0 || comp_kv);
+}
 }  // namespace
+
+extern "C" int ds4hip_flash_attn_decode_f32_workspace_size(long long n_rows, size_t *bytes) {
+    if (!bytes || n_rows < 0) return kEINVAL;
+    *bytes = f32_plan(n_rows).ws_bytes;
+    return 0;
+}
+
+extern "C" int ds4hip_flash_attn_decode_raw_f32_prealloc(const float *Q, const float *K,
+                                                         const float *V, const float *sinks,
+                                                         float *out, int n_head, int n_kv,
+                                                         int head_dim, void *workspace,
+                                                         size_t workspace_bytes, void *stream) {
+    if (!raw_args_ok(Q, K, V, sinks, out, n_head, n_kv, head_dim) || !workspace)
+        return ds4hip_set_last_error(kEINVAL);
+    return ds4hip_set_last_error(run_f32(Q, K, V, n_kv, nullptr, 0, nullptr, sinks, out,
+                                         workspace, workspace_bytes, (hipStream_t)stream));
+}
+
+extern "C" int ds4hip_flash_attn_decode_mixed_f32_prealloc(
+        const float *Q, const float *raw_kv, const float *comp_kv, const int32_t *comp_allowed,
+        const float *sinks, float *out, int n_head, int n_raw, int n_comp, int head_dim,
+        void *workspace, size_t workspace_bytes, void *stream) {
+    if (!mixed_args_ok(Q, raw_kv, comp_kv, sinks, out, n_head, n_raw, n_comp, head_dim) ||
+        !workspace)
+        return ds4hip_set_last_error(kEINVAL);
+    return ds4hip_set_last_error(run_f32(Q, raw_kv, nullptr, n_raw, comp_kv, n_comp,
+                                         comp_allowed, sinks, out, workspace, workspace_bytes,
+                                         (hipStream_t)stream));
+}
 
 extern "C" int ds4hip_flash_attn_decode_raw_f32(const float *Q, const float *K, const float *V,
                                                 const float *sinks, float *out, int n_head,
                                                 int n_kv, int head_dim, void *stream) {
     // cuda/flash_attn.cu:259-269 drops the launch on a bad shape; the 128-row
-    // cap of the reference kernel is lifted. K and V must be the same buffer
-    // (MLA layout, cuda/flash_attn.cu:30-33).
-    if (head_dim != kD || n_head != kH || n_kv < 0 || K != V || !Q || !sinks || !out ||
-        (n_kv > 0 && !K))
+    // cap of the reference kernel is lifted. K and V may be the same buffer
+    // (MLA layout, cuda/flash_attn.cu:30-33) or two buffers.
+    if (!raw_args_ok(Q, K, V, sinks, out, n_head, n_kv, head_dim))
         return ds4hip_set_last_error(kEINVAL);
-    return ds4hip_set_last_error(
-        run_f32(Q, K, n_kv, nullptr, 0, nullptr, sinks, out, (hipStream_t)stream));
+    return ds4hip_set_last_error(run_f32(Q, K, V, n_kv, nullptr, 0, nullptr, sinks, out, nullptr,
+                                         0, (hipStream_t)stream));
 }
 
 extern "C" int ds4hip_flash_attn_decode_mixed_f32(const float *Q, const float *raw_kv,
@@ -1708,9 +1777,8 @@ extern "C" int ds4hip_flash_attn_decode_mixed_f32(const float *Q, const float *r
                                                   const float *sinks, float *out, int n_head,
                                                   int n_raw, int n_comp, int head_dim,
                                                   void *stream) {
-    if (head_dim != kD || n_head != kH || n_raw < 0 || n_comp < 0 || !Q || !sinks || !out ||
-        (n_raw > 0 && !raw_kv) || (n_comp > 0 && !comp_kv))
+    if (!mixed_args_ok(Q, raw_kv, comp_kv, sinks, out, n_head, n_raw, n_comp, head_dim))
         return ds4hip_set_last_error(kEINVAL);
-    return ds4hip_set_last_error(run_f32(Q, raw_kv, n_raw, comp_kv, n_comp, comp_allowed, sinks,
-                                         out, (hipStream_t)stream));
+    return ds4hip_set_last_error(run_f32(Q, raw_kv, nullptr, n_raw, comp_kv, n_comp, comp_allowed,
+                                         sinks, out, nullptr, 0, (hipStream_t)stream));
 }

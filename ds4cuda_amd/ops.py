@@ -88,10 +88,28 @@ class Fp8KVCache:
 
 def launch_flash_attn_decode_raw_f32(Q, K, V, sinks, out, n_head, n_kv, head_dim, stream=None):
     for t, n, nm in ((Q, n_head * head_dim, "Q"), (K, n_kv * head_dim, "K"),
-                     (sinks, n_head, "sinks"), (out, n_head * head_dim, "out")):
+                     (V, n_kv * head_dim, "V"), (sinks, n_head, "sinks"),
+                     (out, n_head * head_dim, "out")):
         _check(t, torch.float32, n, nm)
     call("ds4hip_flash_attn_decode_raw_f32", _ptr(Q), _ptr(K), _ptr(V), _ptr(sinks), _ptr(out),
          n_head, n_kv, head_dim, _stream(stream))
+
+
+def decode_f32_workspace(n_rows, device):
+    """Workspace (uint8 tensor) of the _prealloc fp32 decode launchers."""
+    out = C.c_size_t(0)
+    call("ds4hip_flash_attn_decode_f32_workspace_size", int(n_rows), C.byref(out))
+    return torch.empty(max(out.value, 1), dtype=torch.uint8, device=device)
+
+
+def launch_flash_attn_decode_raw_f32_prealloc(Q, K, V, sinks, out, n_head, n_kv, head_dim,
+                                              workspace, stream=None):
+    for t, n, nm in ((Q, n_head * head_dim, "Q"), (K, n_kv * head_dim, "K"),
+                     (V, n_kv * head_dim, "V"), (sinks, n_head, "sinks"),
+                     (out, n_head * head_dim, "out")):
+        _check(t, torch.float32, n, nm)
+    call("ds4hip_flash_attn_decode_raw_f32_prealloc", _ptr(Q), _ptr(K), _ptr(V), _ptr(sinks),
+         _ptr(out), n_head, n_kv, head_dim, _ptr(workspace), workspace.numel(), _stream(stream))
 
 
 def launch_flash_attn_decode_mixed_f32(Q, raw_kv, comp_kv, comp_allowed, sinks, out, n_head,
@@ -103,6 +121,18 @@ def launch_flash_attn_decode_mixed_f32(Q, raw_kv, comp_kv, comp_allowed, sinks, 
     call("ds4hip_flash_attn_decode_mixed_f32", _ptr(Q), _ptr(raw_kv), _ptr(comp_kv),
          _ptr(comp_allowed), _ptr(sinks), _ptr(out), n_head, n_raw, n_comp, head_dim,
          _stream(stream))
+
+
+def launch_flash_attn_decode_mixed_f32_prealloc(Q, raw_kv, comp_kv, comp_allowed, sinks, out,
+                                                n_head, n_raw, n_comp, head_dim, workspace,
+                                                stream=None):
+    _check(Q, torch.float32, n_head * head_dim, "Q")
+    _check(raw_kv, torch.float32, n_raw * head_dim, "raw_kv")
+    _check(comp_kv, torch.float32, n_comp * head_dim, "comp_kv")
+    _check(comp_allowed, torch.int32, n_comp, "comp_allowed")
+    call("ds4hip_flash_attn_decode_mixed_f32_prealloc", _ptr(Q), _ptr(raw_kv), _ptr(comp_kv),
+         _ptr(comp_allowed), _ptr(sinks), _ptr(out), n_head, n_raw, n_comp, head_dim,
+         _ptr(workspace), workspace.numel(), _stream(stream))
 
 
 def decode_fp8_workspace_bytes(n_rows_per_prob) -> int:

@@ -60,11 +60,12 @@ int ds4hip_fp8_kv_quantize_append(const float *kv_in, int n_rows, int head_dim, 
 /* ---- decode attention ------------------------------------------------------------- */
 
 /* Replaces ds4cuda::launch_flash_attn_decode_raw_f32 (cuda/flash_attn.cuh:73).
- * fp32 Q [n_head][head_dim], K == V rows [n_kv][head_dim] (MLA: the caller
- * passes the same buffer, cuda/forward_layer.cu:1167; K != V is rejected),
- * sinks [n_head], out [n_head][head_dim]. n_head = 64, head_dim = 512; the
- * reference's n_kv <= 128 cap is lifted. Partial-result scratch is
- * stream-ordered hipMallocAsync / hipFreeAsync. */
+ * fp32 Q [n_head][head_dim], K and V rows [n_kv][head_dim] (the same buffer in
+ * the MLA layout, cuda/forward_layer.cu:1167, or two buffers), sinks
+ * [n_head], out [n_head][head_dim]. n_head = 64, head_dim = 512; the
+ * reference's n_kv <= 128 cap is lifted. The split-K partials need scratch:
+ * this form takes it stream-ordered (hipMallocAsync / hipFreeAsync, freed
+ * before the call returns); the _prealloc form below allocates nothing. */
 int ds4hip_flash_attn_decode_raw_f32(const float *Q, const float *K, const float *V,
                                      const float *sinks, float *out, int n_head, int n_kv,
                                      int head_dim, void *stream);
@@ -77,6 +78,27 @@ int ds4hip_flash_attn_decode_mixed_f32(const float *Q, const float *raw_kv,
                                        const float *comp_kv, const int32_t *comp_allowed,
                                        const float *sinks, float *out, int n_head, int n_raw,
                                        int n_comp, int head_dim, void *stream);
+
+/* Bytes of caller workspace the _prealloc fp32 launchers need for n_rows rows
+ * (n_raw + n_comp). */
+int ds4hip_flash_attn_decode_f32_workspace_size(long long n_rows, size_t *bytes);
+
+/* ds4cuda::launch_flash_attn_decode_raw_f32 / _mixed_f32 with caller scratch
+ * (the _prealloc convention of cuda/compressor.cuh:96-101 and
+ * cuda/attn_out.cuh:94-97): the same results, no allocation. workspace holds
+ * ds4hip_flash_attn_decode_f32_workspace_size(n_rows) bytes; calls that share
+ * one workspace must be ordered on one stream. */
+int ds4hip_flash_attn_decode_raw_f32_prealloc(const float *Q, const float *K, const float *V,
+                                              const float *sinks, float *out, int n_head,
+                                              int n_kv, int head_dim, void *workspace,
+                                              size_t workspace_bytes, void *stream);
+int ds4hip_flash_attn_decode_mixed_f32_prealloc(const float *Q, const float *raw_kv,
+                                                const float *comp_kv,
+                                                const int32_t *comp_allowed,
+                                                const float *sinks, float *out, int n_head,
+                                                int n_raw, int n_comp, int head_dim,
+                                                void *workspace, size_t workspace_bytes,
+                                                void *stream);
 
 /* Workspace bytes needed by ds4hip_flash_attn_decode_fp8 for the given host
  * array of per-problem row counts. */

@@ -64,6 +64,33 @@ inline void launch_flash_attn_decode_mixed_f32(const float *Q, const float *raw_
                                                      n_head, n_raw, n_comp, head_dim, stream));
 }
 
+/* cuda/flash_attn.cuh:73 and :142 with caller scratch, following the
+ * reference's _prealloc convention (cuda/attn_out.cuh:94-98): the same
+ * results as the launchers above, no allocation. workspace: at least
+ * ds4hip_flash_attn_decode_f32_workspace_size(n_rows) bytes. */
+inline void launch_flash_attn_decode_raw_f32_prealloc(const float *Q, const float *K,
+                                                      const float *V, const float *sinks,
+                                                      float *out, int n_head, int n_kv,
+                                                      int head_dim, void *workspace,
+                                                      size_t workspace_bytes,
+                                                      hipStream_t stream = 0) {
+    ds4hip_report("launch_flash_attn_decode_raw_f32_prealloc",
+                  ds4hip_flash_attn_decode_raw_f32_prealloc(Q, K, V, sinks, out, n_head, n_kv,
+                                                            head_dim, workspace, workspace_bytes,
+                                                            stream));
+}
+
+inline void launch_flash_attn_decode_mixed_f32_prealloc(
+        const float *Q, const float *raw_kv, const float *comp_kv, const int32_t *comp_allowed,
+        const float *sinks, float *out, int n_head, int n_raw, int n_comp, int head_dim,
+        void *workspace, size_t workspace_bytes, hipStream_t stream = 0) {
+    ds4hip_report("launch_flash_attn_decode_mixed_f32_prealloc",
+                  ds4hip_flash_attn_decode_mixed_f32_prealloc(Q, raw_kv, comp_kv, comp_allowed,
+                                                              sinks, out, n_head, n_raw, n_comp,
+                                                              head_dim, workspace,
+                                                              workspace_bytes, stream));
+}
+
 /* cuda/fp8_kv.cuh:62 */
 inline void launch_fp8_kv_quantize_round_trip_f32(const float *kv_in, float *kv_out, int n_rows,
                                                   int head_dim, int n_rot,

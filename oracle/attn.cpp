@@ -16,7 +16,9 @@ namespace {
 // cuda/flash_attn.cu:185,223).
 void head_attention(const float *qh, const float *const *krows, int n,
                     float sink, float kq_scale, int head_dim,
-                    std::vector<float> &scores, float *oh) {
+                    std::vector<float> &scores, float *oh,
+                    const float *const *vrows = nullptr) {
+    if (!vrows) vrows = krows;
     scores.resize((size_t)n);
     float mx = sink;
     for (int k = 0; k < n; ++k) {
@@ -33,7 +35,7 @@ void head_attention(const float *qh, const float *const *krows, int n,
         if (!krows[k]) continue;
         const float w = std::exp(scores[k] - mx);
         denom += w;
-        for (int d = 0; d < head_dim; ++d) oh[d] += w * krows[k][d];
+        for (int d = 0; d < head_dim; ++d) oh[d] += w * vrows[k][d];
     }
     const float inv = 1.0f / denom;
     for (int d = 0; d < head_dim; ++d) oh[d] *= inv;
@@ -98,6 +100,28 @@ extern "C" void orc_attn_decode_mixed_f32(const float *Q, const float *raw_kv, i
         rows[k] = dst;
     }
     run_heads(Q, rows.data(), n, sinks, out, n_head, head_dim, 1);
+}
+
+// cuda/flash_attn.cu:148-244 with K and V read from separate buffers (both
+// f16-rounded on read).
+extern "C" void orc_attn_decode_kv_f32(const float *Q, const float *K, const float *V, int n_kv,
+                                       const float *sinks, float *out, int n_head,
+                                       int head_dim) {
+    std::vector<float> kb((size_t)(n_kv > 0 ? n_kv : 1) * head_dim), vb(kb.size());
+    std::vector<const float *> kr((size_t)(n_kv > 0 ? n_kv : 1)), vr(kr.size());
+    for (int k = 0; k < n_kv; ++k) {
+        for (int d = 0; d < head_dim; ++d) {
+            kb[(size_t)k * head_dim + d] = orc_f16_round(K[(size_t)k * head_dim + d]);
+            vb[(size_t)k * head_dim + d] = orc_f16_round(V[(size_t)k * head_dim + d]);
+        }
+        kr[k] = kb.data() + (size_t)k * head_dim;
+        vr[k] = vb.data() + (size_t)k * head_dim;
+    }
+    const float kq_scale = 1.0f / std::sqrt((float)head_dim);
+    std::vector<float> scores;
+    for (int h = 0; h < n_head; ++h)
+        head_attention(Q + (size_t)h * head_dim, kr.data(), n_kv, sinks[h], kq_scale, head_dim,
+                       scores, out + (size_t)h * head_dim, vr.data());
 }
 
 extern "C" void orc_attn_decode_fp8(const float *Q, const uint8_t *codes, const int8_t *sexp,

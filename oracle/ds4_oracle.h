@@ -64,6 +64,10 @@ void orc_attn_decode_mixed_f32(const float *Q, const float *raw_kv, int n_raw,
                                const float *comp_kv, int n_comp,
                                const int32_t *comp_allowed, const float *sinks,
                                float *out, int n_head, int head_dim);
+// The raw launcher's math with K and V in separate buffers
+// (cuda/flash_attn.cu:148-244 reads K[k] for the scores and V[k] for the sum).
+void orc_attn_decode_kv_f32(const float *Q, const float *K, const float *V, int n_kv,
+                            const float *sinks, float *out, int n_head, int head_dim);
 // Same math over rows of the FP8 cache (codes [*,n_nope], sexp [*,8],
 // tail [*,n_rot] f16), selected by physical row ids rows[0..n_rows).
 // n_threads > 1 splits the heads over std::threads (CPU baseline mode).

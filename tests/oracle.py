@@ -72,6 +72,19 @@ def attn_decode_mixed_f32(Q, raw, comp, allowed, sinks):
     return out
 
 
+def attn_decode_kv_f32(Q, K, V, sinks):
+    """Separate K and V rows (the raw launcher with V != K)."""
+    Q = np.ascontiguousarray(Q, np.float32)
+    n_head, d = Q.shape
+    out = np.zeros((n_head, d), np.float32)
+    K = np.ascontiguousarray(K, np.float32)
+    V = np.ascontiguousarray(V, np.float32)
+    lib().orc_attn_decode_kv_f32(P(Q), P(K), P(V), C.c_int(K.shape[0]),
+                                 P(np.ascontiguousarray(sinks, np.float32)), P(out),
+                                 C.c_int(n_head), C.c_int(d))
+    return out
+
+
 def attn_decode_fp8(Q, codes, sexp, tail, rows, sinks, n_threads=1):
     Q = np.ascontiguousarray(Q, np.float32)
     n_head, d = Q.shape

@@ -112,6 +112,27 @@ def test_raw_f32_launcher(gpu, n_kv):
     check(out.cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("n_kv", [1, 100, 300])
+def test_raw_f32_separate_v_and_prealloc(gpu, n_kv):
+    """K != V (two buffers) through the allocating and the _prealloc launcher;
+    the _prealloc result equals the allocating one bit for bit."""
+    K = synth.kv_rows(44, 1, n_kv) * 1.5
+    V = synth.kv_rows(44, 2, n_kv)
+    Q = synth.normal(45, 2, 64 * 512).reshape(64, 512)
+    sinks = sinks_for(46, 1)[0]
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(gpu)
+    out = torch.zeros((64, 512), dtype=torch.float32, device=gpu)
+    out2 = torch.zeros((64, 512), dtype=torch.float32, device=gpu)
+    ops.launch_flash_attn_decode_raw_f32(t(Q), t(K), t(V), t(sinks), out, 64, n_kv, 512)
+    ws = ops.decode_f32_workspace(n_kv, gpu)
+    ops.launch_flash_attn_decode_raw_f32_prealloc(t(Q), t(K), t(V), t(sinks), out2, 64, n_kv,
+                                                  512, ws)
+    torch.cuda.synchronize()
+    ref = O.attn_decode_kv_f32(Q, K, V, sinks)
+    check(out.cpu().numpy(), ref)
+    assert torch.equal(out, out2)
+
+
 @pytest.mark.parametrize("n_raw,n_comp", [(128, 0), (0, 50), (128, 300), (5, 1000)])
 def test_mixed_f32_launcher(gpu, n_raw, n_comp):
     raw = synth.kv_rows(51, 1, max(n_raw, 1))[:n_raw]
@@ -130,6 +151,14 @@ def test_mixed_f32_launcher(gpu, n_raw, n_comp):
         ref = O.attn_decode_mixed_f32(Q, raw if n_raw else None, comp if n_comp else None,
                                       mask if use_mask else None, sinks)
         check(out.cpu().numpy(), ref)
+        # the _prealloc form: the same bits from a caller workspace
+        out2 = torch.zeros((64, 512), dtype=torch.float32, device=gpu)
+        ops.launch_flash_attn_decode_mixed_f32_prealloc(
+            t(Q), t(raw) if n_raw else None, t(comp) if n_comp else None,
+            t(mask, np.int32) if (use_mask and n_comp) else None, t(sinks), out2, 64, n_raw,
+            n_comp, 512, ops.decode_f32_workspace(n_raw + n_comp, gpu))
+        torch.cuda.synchronize()
+        assert torch.equal(out, out2)
 
 
 def test_fp8_cfg2_scale_long_chunks(gpu):

@@ -105,3 +105,19 @@ def test_fp8_path_equals_f32_path_on_dequantized_rows(data):
     a = O.attn_decode_fp8(Q, codes, sexp, tail, sel, sinks, n_threads=4)
     b = O.attn_decode_mixed_f32(Q, deq[sel], None, None, sinks)
     assert np.array_equal(a, b)
+
+
+def test_separate_v_rows(data):
+    # K == V gives the MLA form; with V != K the output is the fp64 softmax of
+    # Q.K applied to V (sink = extra key with value 0)
+    Q, K, sinks = data
+    assert np.array_equal(O.attn_decode_kv_f32(Q, K, K, sinks),
+                          O.attn_decode_mixed_f32(Q, K, None, None, sinks))
+    V = np.random.default_rng(13).standard_normal(K.shape).astype(np.float32)
+    out = O.attn_decode_kv_f32(Q, K, V, sinks)
+    Kr, Vr = f16r(K).astype(np.float64), f16r(V).astype(np.float64)
+    s = Q.astype(np.float64) @ Kr.T / np.sqrt(512)
+    s = np.concatenate([s, sinks.astype(np.float64)[:, None]], axis=1)
+    w = np.exp(s - s.max(axis=1, keepdims=True))
+    ref = (w[:, :-1] @ Vr) / w.sum(axis=1, keepdims=True)
+    assert np.abs(out - ref).max() < 1e-5

@@ -26,6 +26,8 @@ SIGNATURES: dict[str, list] = {
     "ds4hip_flash_attn_decode_f32_workspace_size": [_ll, C.POINTER(_sz)],
     "ds4hip_flash_attn_decode_raw_f32_prealloc": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp, _sz,
                                                   _vp],
+    "ds4hip_flash_attn_decode_mixed_f32_noalloc": [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i,
+                                                   _vp],
     "ds4hip_flash_attn_decode_mixed_f32_prealloc": [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i,
                                                     _vp, _sz, _vp],
     "ds4hip_flash_attn_decode_fp8_workspace_size": [_vp, _i, C.POINTER(_sz)],

@@ -34,6 +34,7 @@
 #include "../../include/ds4hip.h"
 
 #include <algorithm>
+#include <mutex>
 #include <cstddef>
 #include <type_traits>
 #include <vector>
@@ -1781,4 +1782,60 @@ extern "C" int ds4hip_flash_attn_decode_mixed_f32(const float *Q, const float *r
         return ds4hip_set_last_error(kEINVAL);
     return ds4hip_set_last_error(run_f32(Q, raw_kv, nullptr, n_raw, comp_kv, n_comp, comp_allowed,
                                          sinks, out, nullptr, 0, (hipStream_t)stream));
+}
+
+// ---- allocation-free fp32 decode (no counterpart in the reference) -------------------
+// For callers that cannot allocate (code under graph capture, serving loops):
+// the split-K partials live in a file-scope device array instead of a
+// workspace. The plan is capped at kNoAllocSlots chunks so that any row count
+// fits. Every call on one GPU shares that GPU's copy of the array: calls that
+// overlap on one GPU (two streams, two host threads) race. Nothing in it needs
+// to start at zero: every partial slot and slot tag is written before the
+// merge reads it.
+namespace {
+constexpr int kNoAllocSlots = 64;
+constexpr long long kNoAllocMaxRows = 1ll << 22;
+constexpr size_t kNoAllocScratchBytes = 8u << 20 | 512u << 10;   // 8.5 MiB
+constexpr int kMaxDevices = 64;
+
+__device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of this GPU's scratch array (looked up once per device, with
+// that device current); the array's name is not a device address in host code.
+int scratch_ptr(void **out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_status(e);
+    if (dev < 0 || dev >= kMaxDevices) return kEINVAL;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_status(e);
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return 0;
+}
+}  // namespace
+
+extern "C" int ds4hip_flash_attn_decode_mixed_f32_noalloc(
+        const float *Q, const float *raw_kv, const float *comp_kv, const int32_t *comp_allowed,
+        const float *sinks, float *out, int n_head, int n_raw, int n_comp, int head_dim,
+        void *stream) {
+    if (!mixed_args_ok(Q, raw_kv, comp_kv, sinks, out, n_head, n_raw, n_comp, head_dim) ||
+        (long long)n_raw + n_comp > kNoAllocMaxRows)
+        return ds4hip_set_last_error(kEINVAL);
+    const long long n = (long long)n_raw + n_comp;
+    const Plan pl = make_plan(&n, 1, 2, kNoAllocSlots, false);
+    if (pl.ws_bytes > kNoAllocScratchBytes) return ds4hip_set_last_error(kEINVAL);
+    void *ws = nullptr;
+    const int rc = scratch_ptr(&ws);
+    if (rc) return ds4hip_set_last_error(rc);
+    return ds4hip_set_last_error(run_f32(Q, raw_kv, nullptr, n_raw, comp_kv, n_comp,
+                                         comp_allowed, sinks, out, ws, kNoAllocScratchBytes,
+                                         (hipStream_t)stream, &pl));
 }

@@ -100,6 +100,20 @@ int ds4hip_flash_attn_decode_mixed_f32_prealloc(const float *Q, const float *raw
                                                 void *workspace, size_t workspace_bytes,
                                                 void *stream);
 
+/* Allocation-free form of ds4hip_flash_attn_decode_mixed_f32 (no counterpart
+ * in the reference): for callers that cannot call hipMalloc (code under graph
+ * capture, tight serving loops, harnesses that forbid allocation). Same
+ * arguments and results; the split-K partials live in a library-owned 8.5 MiB
+ * device array per GPU (held until the process ends), so the call allocates
+ * nothing and takes no workspace. n_raw + n_comp <= 4194304 (larger: -22).
+ * Calls that overlap on one GPU (several streams or host threads) share that
+ * array and race: order them on one stream. */
+int ds4hip_flash_attn_decode_mixed_f32_noalloc(const float *Q, const float *raw_kv,
+                                               const float *comp_kv,
+                                               const int32_t *comp_allowed, const float *sinks,
+                                               float *out, int n_head, int n_raw, int n_comp,
+                                               int head_dim, void *stream);
+
 /* Workspace bytes needed by ds4hip_flash_attn_decode_fp8 for the given host
  * array of per-problem row counts. */
 int ds4hip_flash_attn_decode_fp8_workspace_size(const long long *n_rows_per_prob, int n_prob,

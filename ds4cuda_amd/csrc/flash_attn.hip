@@ -1381,6 +1381,617 @@ __global__ __launch_bounds__(512, 1) void decode_ws_kernel(const DecodeArgs A) {
         for (int s2 = slot_s; s2 < A.s_max; ++s2) A.ws_prob[(long long)blockIdx.x * A.s_max + s2] = -1;
 }
 
+// ---- flat-stage FP8 decode (direct rows) ----------------------------------------------
+//
+// One 8-wave workgroup per chunk, all 64 heads, as decode_ws_kernel, with the
+// tile copied HBM -> LDS by the consumers' global_load_lds instructions and
+// read from there by everyone:
+//  * Each 32-row tile takes 20 copy instructions (19 of 16 bytes per lane, one
+//    of 4 for the exponents), each 1 KB of consecutive cache bytes (whole rows
+//    of codes, then of tails), 5 per consumer wave, kFsLead tiles ahead.
+//  * LDS layout of a stage, chosen so that every fragment read runs at the
+//    full LDS rate (measured on gfx950: a 16-byte read of 16 lanes is
+//    conflict-free when the lanes' rows are 480 bytes apart, and at half rate
+//    for 464 or 448): code rows of 480 bytes (28 code chunks + 2 pad chunks
+//    that re-read chunk 27), then tail rows of 128 bytes whose 16-byte chunk c
+//    sits at position c ^ ((row >> 1) & 7), then the rows' 8 exponents, then
+//    the f16 scale table the producers write for the consumers.
+//  * Producer wave d: QK^T of heads [16d, 16d+16) on the scaled FP8 MFMA, then
+//    the softmax one interval later; consumer wave c: P . V over dims
+//    [128c, 128c+128) for all 64 heads, two intervals behind the QK.
+constexpr int kFsCodeRow = kNope + 32;                    // 480: codes + 2 pad chunks
+constexpr int kFsTailRow = 2 * kRot;                      // 128: f16 tail, swizzled chunks
+constexpr int kFsTailOff = kTile * kFsCodeRow;            // 15360
+constexpr int kFsExpOff = kFsTailOff + kTile * kFsTailRow; // 19456
+constexpr int kFsBytes = kFsExpOff + kTile * 8;           // 19712
+constexpr int kFsScaleOff = kFsBytes;                     // f16 2^e per [block][row]
+constexpr int kFsSlot = kFsBytes + 8 * kTile * 2;          // 20224
+constexpr int kFsStages = 6;
+constexpr int kFsLead = 3;                                 // tiles copied ahead of the producers
+constexpr int kFsCodeChunks = kTile * (kFsCodeRow / 16);  // 960
+constexpr int kFsChunks = kFsCodeChunks + kTile * (kFsTailRow / 16);   // 1216 = 19 x 64
+// LDS chunk position of tail chunk c of tile row r (an involution on c)
+__device__ __host__ constexpr int fs_tail_pos(int r, int c) { return c ^ ((r >> 1) & 7); }
+static_assert(kFsChunks == 19 * 64, "codes + tails fill 19 copy instructions");
+
+// Consumer side shared by the decode kernels: O[64 heads x 128 dims] of dim
+// quarter d += P(t) . V(t) for the tiles of one segment, then the partial O.
+template <bool kPLo>
+__device__ inline void consume_segment(const DecodeArgs &A, uint8_t (*vtile)[4][kVTileBytes],
+                                       const uint8_t *pws, const float (*alpha_s)[kH],
+                                       int n_tiles, long long slot, int lane, int j, int q,
+                                       int d, int lead) {
+    float4_t o[4][8];   // heads 16 hb + 4 q + r, dims 128 d + 16 nb + j
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int c = 0; c < 8; ++c) o[a][c] = float4_t{0, 0, 0, 0};
+    auto pv = [&](int t) {
+        const int b = t & 1;
+        half8_t pa[4], pl[4];
+        float4_t ar[4];
+#pragma unroll
+        for (int hb = 0; hb < 4; ++hb) {
+            pa[hb] = *reinterpret_cast<const half8_t *>(pws + pws_off(b, 0, hb, lane));
+            if (kPLo) pl[hb] = *reinterpret_cast<const half8_t *>(pws + pws_off(b, 1, hb, lane));
+            ar[hb] = *reinterpret_cast<const float4_t *>(&alpha_s[b][16 * hb + 4 * q]);
+        }
+        const uint32_t vt = lds_addr(vtile[b][d]);
+        uint2_t tb[2][8];
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            const uint32_t ab = vt + (4 * q + (j >> 2)) * kVRowBytes + 8 * ((j & 3) ^ ((q & 1) << 1)) + 128 * half;
+            asm volatile(
+                "ds_read_b64_tr_b16 %0, %8\n\tds_read_b64_tr_b16 %1, %8 offset:4608\n\t"
+                "ds_read_b64_tr_b16 %2, %8 offset:32\n\tds_read_b64_tr_b16 %3, %8 offset:4640\n\t"
+                "ds_read_b64_tr_b16 %4, %8 offset:64\n\tds_read_b64_tr_b16 %5, %8 offset:4672\n\t"
+                "ds_read_b64_tr_b16 %6, %8 offset:96\n\tds_read_b64_tr_b16 %7, %8 offset:4704"
+                : "=&v"(tb[half][0]), "=&v"(tb[half][1]), "=&v"(tb[half][2]), "=&v"(tb[half][3]),
+                  "=&v"(tb[half][4]), "=&v"(tb[half][5]), "=&v"(tb[half][6]), "=&v"(tb[half][7])
+                : "v"(ab));
+        }
+        asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");
+        bool need = false;
+#pragma unroll
+        for (int hb = 0; hb < 4; ++hb)
+            need |= ar[hb][0] != 1.0f || ar[hb][1] != 1.0f || ar[hb][2] != 1.0f || ar[hb][3] != 1.0f;
+        if (__any(need)) {   // rare: a reference point moved
+#pragma unroll
+            for (int hb = 0; hb < 4; ++hb)
+#pragma unroll
+                for (int nb = 0; nb < 8; ++nb) o[hb][nb] *= ar[hb];
+        }
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            if (half == 1) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            half8_t vb[4];
+#pragma unroll
+            for (int nb = 0; nb < 4; ++nb)
+                vb[nb] = __builtin_bit_cast(half8_t, uint4_t{tb[half][2 * nb][0], tb[half][2 * nb][1],
+                                                             tb[half][2 * nb + 1][0], tb[half][2 * nb + 1][1]});
+#pragma unroll
+            for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+                for (int hb = 0; hb < 4; ++hb)
+                    o[hb][4 * half + nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        pa[hb], vb[nb], o[hb][4 * half + nb], 0, 0, 0);
+            if (kPLo) {
+#pragma unroll
+                for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+                    for (int hb = 0; hb < 4; ++hb)
+                        o[hb][4 * half + nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            pl[hb], vb[nb], o[hb][4 * half + nb], 0, 0, 0);
+            }
+        }
+    };
+    // the producers' barriers before P(0) and V(0) are published
+    for (int i = 0; i < lead; ++i) lds_barrier();
+    for (int t = 0; t < n_tiles; ++t) {   // interval t + lead
+        pv(t);
+        lds_barrier();
+    }
+    float *wo = A.ws_o + slot * (kH * kD) + (4 * q) * kD + 128 * d + j;
+    asm volatile("" : "+v"(wo));
+#pragma unroll
+    for (int hb = 0; hb < 4; ++hb)
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) wo[(16 * hb + r) * kD + 16 * nb] = o[hb][nb][r];
+}
+
+// The LDS reads of one stage row for a producer lane (no wait): the 7 code
+// chunks c[b] = dims 64 b + 16 q + [0, 16), the f16 tail chunks t[s] = dims
+// 448 + 32 s + 8 q + [0, 8) (at tail_a[s]) and the row's 8 exponents. lds_rows_wait completes the
+// reads of both row halves; their registers are tied to the wait so that
+// nothing reads them before it.
+__device__ inline void lds_read_row(uint32_t code_a, uint32_t tail_a0, uint32_t tail_a1, uint32_t exp_a,
+                                    uint4_t (&c)[7], uint4_t (&t)[2], uint2_t &e) {
+    asm volatile(
+        "ds_read_b128 %0, %10\n\tds_read_b128 %1, %10 offset:64\n\t"
+        "ds_read_b128 %2, %10 offset:128\n\tds_read_b128 %3, %10 offset:192\n\t"
+        "ds_read_b128 %4, %10 offset:256\n\tds_read_b128 %5, %10 offset:320\n\t"
+        "ds_read_b128 %6, %10 offset:384\n\tds_read_b128 %7, %11\n\t"
+        "ds_read_b128 %8, %12\n\tds_read_b64 %9, %13"
+        : "=&v"(c[0]), "=&v"(c[1]), "=&v"(c[2]), "=&v"(c[3]), "=&v"(c[4]), "=&v"(c[5]),
+          "=&v"(c[6]), "=&v"(t[0]), "=&v"(t[1]), "=&v"(e)
+        : "v"(code_a), "v"(tail_a0), "v"(tail_a1), "v"(exp_a));
+}
+__device__ inline void lds_row_wait(uint4_t (&c)[7], uint4_t (&t)[2], uint2_t &e) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(c[0]), "+v"(c[1]), "+v"(c[2]), "+v"(c[3]), "+v"(c[4]), "+v"(c[5]),
+                   "+v"(c[6]), "+v"(t[0]), "+v"(t[1]), "+v"(e)
+                 :: "memory");
+}
+
+typedef unsigned int uint8x_t __attribute__((ext_vector_type(8)));
+// f(integral_constant<int, i>) for i = 0 .. N-1 (indices usable as constant
+// builtin operands)
+template <int N, typename F>
+__device__ inline void static_for(F &&f) {
+    if constexpr (N > 0) {
+        static_for<N - 1>(f);
+        f(std::integral_constant<int, N - 1>{});
+    }
+}
+__device__ inline uint8x_t uint4x2_cat(uint4_t a, uint4_t b) {
+    return uint8x_t{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+__device__ inline uint8x_t qf8v(const uint32_t (&w)[8]) {
+    return uint8x_t{w[0], w[1], w[2], w[3], w[4], w[5], w[6], w[7]};
+}
+
+template <bool kPLo>
+__global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A) {
+    static_assert(!kPLo, "the flat kernel passes P as one f16");
+    __shared__ __attribute__((aligned(16))) uint8_t stage[kFsStages][kFsSlot];
+    __shared__ __attribute__((aligned(16))) uint8_t pws[2 * 4 * 64 * 16];   // [t & 1][head tile][lane] f16 x 8
+    __shared__ __attribute__((aligned(16))) float alpha_s[2][kH];
+    __shared__ __attribute__((aligned(16))) int rescale_s[2][4];   // [t & 1][head tile]: some alpha != 1
+    __shared__ long long s_start[kMaxProb + 1];
+    __shared__ long long s_rowbase[kMaxProb];
+    for (int i = threadIdx.x; i < A.n_prob; i += blockDim.x)
+        s_rowbase[i] = A.row_base ? A.row_base[i] : (long long)i * A.row_base_stride;
+    stage_start(A, s_start);
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const bool producer = wave < 4;
+    const int d = wave & 3;   // producer: head tile; consumer: dim quarter
+    const int j = lane & 15;
+    const int q = lane >> 4;
+
+    long long g0 = (long long)blockIdx.x * A.chunk;
+    const long long g1 = min(g0 + (long long)A.chunk, A.total);
+    int p = 0;
+    int slot_s = 0;
+    while (g0 < g1) {
+        while (s_start[p + 1] <= g0) ++p;
+        const long long seg_end = min(g1, s_start[p + 1]);
+        const long long r0 = g0 - s_start[p];
+        const long long r1 = min(seg_end - s_start[p], A.count[p]);
+        const int n_tiles = (int)((r1 - r0 + kTile - 1) / kTile);
+        const long long slot = (long long)blockIdx.x * A.s_max + slot_s;
+        const long long seg_r0 = s_rowbase[p] + r0;
+        const int seg_last = (int)(r1 - 1 - r0);
+        // ---- the producers: QK^T on the scaled FP8 MFMA and the softmax, one
+        // interval apart (interval u: QK(u) with softmax(u - 1) in its issue slots)
+        auto produce = [&]() {
+            // Q of head 16 d + j as the B operand of the scaled FP8 MFMA. k-step ks
+            // covers dims 128 ks + [0, 128); the MFMA takes lane (j, q)'s 32 bytes
+            // as dims 128 ks + 16 q + [0, 16) and 128 ks + 64 + 16 q + [0, 16)
+            // (lane q supplies the scale of dims 128 ks + 32 q + [0, 32)). Q ~ hi +
+            // lo, each E4M3 codes with one E8M0 scale per head and k-step (a bf16
+            // value has 8 significant bits: hi keeps 4, lo the rest). Dims >= 448
+            // (the f16 RoPE tail) are zero here and take the f16 MFMA instead:
+            // qt[s] = dims 448 + 32 s + 8 q + [0, 8).
+            uint32_t qf8[4][2][8];
+            int qsc[2] = {0, 0};   // [part]: byte ks = E8M0 scale of k-step ks (the MFMA's op_sel picks it)
+            half8_t qt[2];
+            {
+                const uint16_t *qsrc = static_cast<const uint16_t *>(A.q) + (long long)p * A.q_stride +
+                                       (long long)(16 * d + j) * kD;
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    float x[32];
+#pragma unroll
+                    for (int hv = 0; hv < 2; ++hv) {
+                        const bool live = ks < 3 || hv == 0;
+#pragma unroll
+                        for (int v = 0; v < 2; ++v) {
+                            uint4_t w = uint4_t{0, 0, 0, 0};
+                            if (live) w = *reinterpret_cast<const uint4_t *>(qsrc + 128 * ks + 64 * hv + 16 * q + 8 * v);
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) {
+                                x[16 * hv + 8 * v + 2 * i] = bf16_to_f32((uint16_t)(w[i] & 0xFFFF));
+                                x[16 * hv + 8 * v + 2 * i + 1] = bf16_to_f32((uint16_t)(w[i] >> 16));
+                            }
+                        }
+                    }
+#pragma unroll
+                    for (int part = 0; part < 2; ++part) {
+                        float amax = 0.0f;
+#pragma unroll
+                        for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(x[i]));
+                        amax = xmax_16_32(amax);   // one scale for the head's 128 dims
+                        // scale 2^e with amax / 2^e in [128, 256): no E4M3 overflow
+                        const int e = amax > 0.0f ? ((int)((__float_as_uint(amax) >> 23) & 0xFF) - 127 - 7) : 0;
+                        const float inv = pow2f(-e), sc = pow2f(e);
+                        qsc[part] |= (e + 127) << (8 * ks);
+#pragma unroll
+                        for (int w = 0; w < 8; ++w) {
+                            int pk = 0;
+                            pk = __builtin_amdgcn_cvt_pk_fp8_f32(x[4 * w] * inv, x[4 * w + 1] * inv, pk, false);
+                            pk = __builtin_amdgcn_cvt_pk_fp8_f32(x[4 * w + 2] * inv, x[4 * w + 3] * inv, pk, true);
+                            qf8[ks][part][w] = (uint32_t)pk;
+                            if (part == 0) {   // the residual goes to lo
+                                x[4 * w] -= __builtin_amdgcn_cvt_f32_fp8(pk, 0) * sc;
+                                x[4 * w + 1] -= __builtin_amdgcn_cvt_f32_fp8(pk, 1) * sc;
+                                x[4 * w + 2] -= __builtin_amdgcn_cvt_f32_fp8(pk, 2) * sc;
+                                x[4 * w + 3] -= __builtin_amdgcn_cvt_f32_fp8(pk, 3) * sc;
+                            }
+                        }
+                    }
+                }
+                // tail dims 448 + 32 s2 + 8 q + [0, 8), bf16 -> f16
+#pragma unroll
+                for (int s2 = 0; s2 < 2; ++s2) {
+                    const uint4_t w = *reinterpret_cast<const uint4_t *>(qsrc + 448 + 32 * s2 + 8 * q);
+                    half8_t h;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        h[2 * i] = (half_t)bf16_to_f32((uint16_t)(w[i] & 0xFFFF));
+                        h[2 * i + 1] = (half_t)bf16_to_f32((uint16_t)(w[i] >> 16));
+                    }
+                    qt[s2] = h;
+                }
+            }
+            float m_run = -INFINITY, l_run = 0.0f;   // head 16 d + j; l over this lane's rows
+            // softmax of tile t (S^T in sa) for heads 16 d + [0, 16) -> P, alpha in LDS
+            auto softmax = [&](int t, const float4_t (&sa)[2]) {
+                const int b = t & 1;
+                const long long left = r1 - (r0 + (long long)t * kTile);
+                const int nv = left < kTile ? (int)left : kTile;
+                float s8[2][4];
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) s8[hh][r] = sa[hh][r] * A.kq_log2;
+                if (nv < kTile) {
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            if (16 * hh + 4 * q + r >= nv) s8[hh][r] = -INFINITY;
+                }
+                float tmax = -INFINITY;
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, s8[hh][r]);
+                tmax = xmax_16_32(tmax);
+                // lazy reference point (as decode_ws_kernel): it moves only when the
+                // tile max exceeds it by more than 2^kLazyLog2 in P
+                const bool bump = tmax > m_run + kLazyLog2;
+                const float m_new = bump ? tmax : m_run;
+                const bool none = m_new == -INFINITY;
+                const float alpha = (bump && m_run != -INFINITY) ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+                float psum = 0.0f;
+                half8_t pf, pl;
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float pv = none ? 0.0f : __builtin_amdgcn_exp2f(s8[hh][r] - m_new);
+                        pf[4 * hh + r] = (half_t)pv;
+                        if (kPLo) {
+                            psum += pv;
+                            pl[4 * hh + r] = (half_t)(pv - (float)pf[4 * hh + r]);
+                        } else {
+                            psum += (float)pf[4 * hh + r];
+                        }
+                    }
+                lds_st128(lds_addr(pws) + (uint32_t)(((b * 4 + d) * 64 + lane) * 16), pf);
+                l_run = l_run * alpha + psum;
+                m_run = m_new;
+                if (q == 0) lds_st32(lds_addr(&alpha_s[b][16 * d + j]), alpha);
+                const int moved = __any(alpha != 1.0f) ? 1 : 0;
+                if (lane == 0) lds_st32(lds_addr(&rescale_s[b][d]), __int_as_float(moved));
+            };
+            // QK^T of tile u from its stage: the A operand is the raw codes (lane
+            // (j, q): row 16 hh + j, dims 128 ks + 16 q + [0, 16) and 128 ks + 64 +
+            // 16 q + [0, 16); its scale operand is the row's exponent of dims
+            // 128 ks + 32 q + [0, 32), i.e. of block 2 ks + q / 2), so the codes
+            // need no conversion; dims 448..511 of k-step 3 are zeros and the f16
+            // tail takes two f16 MFMAs. The wave also writes the f16 scale 2^e of
+            // blocks 2d, 2d + 1 of the tile's rows to the stage's scale table, which
+            // the consumers' V conversion reads.
+            auto qk = [&](int u, float4_t (&acc)[2]) {
+                const uint32_t st = lds_addr(stage[u % kFsStages]);
+                // tail chunks q and 4 + q of rows j and 16 + j (same swizzle);
+                // rebuilt per tile from an opaque lane id so that they are not
+                // held through the whole loop
+                int ln = lane;
+                asm volatile("" : "+v"(ln));
+                const uint32_t tpos0 = 16 * fs_tail_pos(ln & 15, ln >> 4);
+                const uint32_t tpos1 = tpos0 ^ 64;
+                typedef int int8v __attribute__((ext_vector_type(8)));
+                const uint4_t z4 = uint4_t{0, 0, 0, 0};
+                // one row half at a time: the reads of half 1 go out after the
+                // MFMAs of half 0 are issued and land while those run, so only one
+                // half's fragments are live
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    uint4_t kc[7];      // dims 64 b + 16 q + [0, 16)
+                    uint4_t kt[2];      // f16 tail dims 448 + 16 q + [0, 16)
+                    uint2_t ke;         // exponents
+                    const uint32_t ta = st + kFsTailOff + (16 * hh + j) * kFsTailRow;
+                    lds_read_row(st + (16 * hh + j) * kFsCodeRow + 16 * q, ta + tpos0, ta + tpos1,
+                                 st + kFsExpOff + (16 * hh + j) * 8, kc, kt, ke);
+                    lds_row_wait(kc, kt, ke);
+                    if (q < 2 && (d < 3 || q == 0)) {
+                        const int e = (int)(int8_t)((ke[(2 * d + q) >> 2] >> (8 * ((2 * d + q) & 3))) & 0xFF);
+                        const half_t f = (half_t)pow2f(e);
+                        const uint32_t ta = st + kFsScaleOff + ((2 * d + q) * kTile + 16 * hh + j) * 2;
+                        asm volatile("ds_write_b16 %0, %1" :: "v"(ta), "v"(f) : "memory");
+                    }
+                    float4_t c2[2] = {float4_t{0, 0, 0, 0}, float4_t{0, 0, 0, 0}};
+                    static_for<4>([&](auto ksc) {
+                        constexpr int ks = decltype(ksc)::value;
+                        const uint32_t ew = ks < 2 ? ke[0] : ke[1];
+                        const int sa = __builtin_amdgcn_sbfe((int)ew, 16 * (ks & 1) + 8 * (q >> 1), 8) + 127;
+                        const int8v av = __builtin_bit_cast(
+                            int8v, uint4x2_cat(kc[2 * ks], ks < 3 ? kc[2 * ks + 1] : z4));
+#pragma unroll
+                        for (int part = 0; part < 2; ++part) {
+                            const int8v bv = __builtin_bit_cast(int8v, qf8v(qf8[ks][part]));
+                            c2[part] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                                av, bv, c2[part], 0, 0, 0, sa, ks, qsc[part]);
+                        }
+                    });
+                    c2[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, kt[0]), qt[0],
+                                                                   c2[0], 0, 0, 0);
+                    c2[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, kt[1]), qt[1],
+                                                                   c2[1], 0, 0, 0);
+                    acc[hh] = c2[0] + c2[1];
+                }
+            };
+
+            float4_t sprev[2];
+            __builtin_amdgcn_sched_barrier(0);
+            qk(0, sprev);                       // interval 0
+            lds_barrier();
+            for (int u = 1; u < n_tiles; ++u) { // interval u
+                float4_t acc[2];
+                qk(u, acc);
+                softmax(u - 1, sprev);
+                sprev[0] = acc[0];
+                sprev[1] = acc[1];
+                lds_barrier();
+            }
+            softmax(n_tiles - 1, sprev);        // interval n
+            lds_barrier();
+            lds_barrier();                      // interval n + 1: P . V(n - 1)
+            const float l = xsum_16_32(l_run);
+            if (q == 0) {
+                int ln = lane;   // opaque: the address is not held through the loop
+                asm volatile("" : "+v"(ln));
+                float *ml = A.ws_ml + slot * 2 * kH + 16 * d + ln;
+                ml[0] = m_run;
+                ml[kH] = l;
+            }
+        };
+        // ---- the consumers: the copies (kFsLead tiles ahead) and P . V over their
+        // 128 dims for all 64 heads, two intervals behind the producers' QK, with
+        // V converted from the FP8 stage
+        auto consume = [&](auto tc) {
+            constexpr bool kTailQ = decltype(tc)::value;   // dim quarter 3 (64 FP8 + 64 f16 dims)
+            const int c = d;
+            int c_row[5];
+            uint32_t c_off[5];
+            bool c_tail[5];
+            // computed here, per segment: hoisted to the kernel start they would
+            // stay live through the producers' code as well
+            int ln = lane;
+            asm volatile("" : "+v"(ln));
+#pragma unroll
+            for (int k = 0; k < 5; ++k) {
+                const int n = 5 * c + k;
+                const int s = 64 * n + ln;
+                if (n == 19) {           // exponents: 4 bytes per lane
+                    c_row[k] = ln >> 1;
+                    c_off[k] = 4 * (ln & 1);
+                    c_tail[k] = false;
+                } else if (s < kFsCodeChunks) {
+                    const int cc2 = s % (kFsCodeRow / 16);
+                    c_row[k] = s / (kFsCodeRow / 16);
+                    c_off[k] = 16 * min(cc2, kNope / 16 - 1);   // the pad chunks re-read chunk 27
+                    c_tail[k] = false;
+                } else {
+                    const int s2 = s - kFsCodeChunks;
+                    c_row[k] = s2 / (kFsTailRow / 16);
+                    c_off[k] = 16 * fs_tail_pos(c_row[k], s2 % (kFsTailRow / 16));
+                    c_tail[k] = true;
+                }
+            }
+            const uint8_t *codes_s = A.codes + seg_r0 * kNope;
+            const uint8_t *tail_s = reinterpret_cast<const uint8_t *>(A.tail) + seg_r0 * (2 * kRot);
+            const uint8_t *sexp_s = reinterpret_cast<const uint8_t *>(A.sexp) + seg_r0 * 8;
+            // copies of tile u into its stage slot (rows past the segment repeat its
+            // last row: every tile issues the same 5 copies per wave, so the vmcnt
+            // waits are exact)
+            auto issue = [&](int u) {
+                uint8_t *st = stage[u % kFsStages];
+#pragma unroll
+                for (int k = 0; k < 5; ++k) {
+                    const int n = 5 * c + k;
+                    const uint32_t lr = (uint32_t)min(kTile * u + c_row[k], seg_last);
+                    if (n == 19) {
+                        __builtin_amdgcn_global_load_lds(sexp_s + (lr * 8 + c_off[k]),
+                                                         st + kFsExpOff, 4, 0, 0);
+                    } else {
+                        const uint8_t *g = c_tail[k] ? tail_s + (lr * (2 * kRot) + c_off[k])
+                                                     : codes_s + (lr * kNope + c_off[k]);
+                        __builtin_amdgcn_global_load_lds(g, st + 1024 * n, 16, 0, 0);
+                    }
+                }
+            };
+            float4_t o[4][8];   // heads 16 hb + 4 q + r, dims 128 c + 16 nb + j
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+#pragma unroll
+                for (int b = 0; b < 8; ++b) o[a][b] = float4_t{0, 0, 0, 0};
+            // K order of the P . V fragments: element i of lane group q is tile
+            // row R(q, i) = 16 (i >> 2) + 4 q + (i & 3), the S^T rows the producer
+            // lane (j, q) holds. V fragment of dims 16 nb + [0, 16): the FP8 rows
+            // through the transposing 8-bit read (lane (m, g) supplies row
+            // R(g, m >> 1), bytes 8 (m & 1) + [0, 8)), then code -> f16 times the
+            // row's f16 block scale; the f16 tail through two transposing 16-bit
+            // reads (lane (m, g) supplies row 4 g + (m >> 2), dims 4 (m & 3) + [0, 4)
+            // of the chunk pair 2 nb', 2 nb' + 1 of dims 448 + 16 nb' + [0, 16)).
+            const uint32_t tr8_row = (uint32_t)((16 * ((j >> 1) >> 2) + 4 * q + ((j >> 1) & 3)) * kFsCodeRow +
+                                                128 * c + 8 * (j & 1));
+            auto pv = [&](int t) {
+                const int b = t & 1;
+                const uint32_t st = lds_addr(stage[t % kFsStages]);
+                half8_t pa[4];
+                uint4_t mv;         // the producers' rescale flags of tile t
+                uint2_t sc[2][2];   // [block of the quarter][row group]: f16 x 2 scale pairs
+                uint2_t tb[8];      // FP8 fragments (nb < 4 or c < 3)
+                uint2_t tt[4][2];   // tail fragments (c == 3, nb >= 4)
+                asm volatile(
+                    "ds_read_b128 %0, %5\n\tds_read_b128 %1, %5 offset:1024\n\t"
+                    "ds_read_b128 %2, %5 offset:2048\n\tds_read_b128 %3, %5 offset:3072\n\t"
+                    "ds_read_b128 %4, %6"
+                    : "=&v"(pa[0]), "=&v"(pa[1]), "=&v"(pa[2]), "=&v"(pa[3]), "=&v"(mv)
+                    : "v"(lds_addr(pws) + (uint32_t)((b * 4 * 64 + lane) * 16)),
+                      "v"(lds_addr(&rescale_s[b][0])));
+#pragma unroll
+                for (int bb = 0; bb < 2; ++bb) {
+                    if (kTailQ && bb == 1) continue;
+                    const uint32_t ta = st + kFsScaleOff + ((2 * c + bb) * kTile + 4 * q) * 2;
+                    asm volatile("ds_read_b64 %0, %2\n\tds_read_b64 %1, %2 offset:32"
+                                 : "=&v"(sc[bb][0]), "=&v"(sc[bb][1]) : "v"(ta));
+                }
+                constexpr int n8 = kTailQ ? 4 : 8;
+#pragma unroll
+                for (int nb = 0; nb < n8; ++nb)
+                    asm volatile("ds_read_b64_tr_b8 %0, %1 offset:%2"
+                                 : "=&v"(tb[nb]) : "v"(st + tr8_row), "n"(16 * nb));
+                if constexpr (kTailQ) {
+#pragma unroll
+                    for (int nb = 0; nb < 4; ++nb) {
+                        int ln = lane;   // opaque: the addresses are not held across tiles
+                        asm volatile("" : "+v"(ln));
+                        const int r16 = 4 * (ln >> 4) + ((ln & 15) >> 2);
+                        const uint32_t a = st + kFsTailOff + r16 * kFsTailRow + 8 * (ln & 1) +
+                                           16 * fs_tail_pos(r16, 2 * nb + ((ln & 3) >> 1));
+                        asm volatile("ds_read_b64_tr_b16 %0, %2\n\t"
+                                     "ds_read_b64_tr_b16 %1, %2 offset:%3"
+                                     : "=&v"(tt[nb][0]), "=&v"(tt[nb][1])
+                                     : "v"(a), "n"(16 * kFsTailRow));
+                    }
+                }
+                // fragments nb < 4 first: the reads of nb >= 4 (the last 4 FP8
+                // reads, or the 8 tail reads) land while their MFMAs run
+                asm volatile("s_waitcnt lgkmcnt(%14)"
+                             : "+v"(pa[0]), "+v"(pa[1]), "+v"(pa[2]), "+v"(pa[3]), "+v"(mv),
+                               "+v"(sc[0][0]), "+v"(sc[0][1]), "+v"(sc[1][0]), "+v"(sc[1][1]),
+                               "+v"(tb[0]), "+v"(tb[1]), "+v"(tb[2]), "+v"(tb[3]), "+v"(tt[0][0])
+                             : "n"(kTailQ ? 8 : 4) : "memory");
+                // rare: a producer moved a reference point; the accumulators of
+                // its heads are rescaled by alpha (1 for the other heads)
+                if (__builtin_amdgcn_readfirstlane((int)(mv[0] | mv[1] | mv[2] | mv[3]))) {
+                    float4_t ar[4];
+#pragma unroll
+                    for (int hb = 0; hb < 4; ++hb)
+                        ar[hb] = *reinterpret_cast<const float4_t *>(&alpha_s[b][16 * hb + 4 * q]);
+#pragma unroll
+                    for (int hb = 0; hb < 4; ++hb)
+#pragma unroll
+                        for (int nb = 0; nb < 8; ++nb) o[hb][nb] *= ar[hb];
+                }
+                auto frag = [&](int nb) {
+                    if (!kTailQ || nb < 4) {
+                        const int bb = nb >> 2;
+                        // (whole-vector casts: a bit_cast of one element of these
+                        // asm-produced vectors was observed to read element 0)
+                        const half4_t sl = __builtin_bit_cast(half4_t, sc[bb][0]);
+                        const half4_t sh = __builtin_bit_cast(half4_t, sc[bb][1]);
+                        const half2_t s01 = half2_t{sl[0], sl[1]}, s23 = half2_t{sl[2], sl[3]};
+                        const half2_t s45 = half2_t{sh[0], sh[1]}, s67 = half2_t{sh[2], sh[3]};
+                        return make_half8(cvt_fp8x2<false>(tb[nb][0], 1.0f) * s01,
+                                          cvt_fp8x2<true>(tb[nb][0], 1.0f) * s23,
+                                          cvt_fp8x2<false>(tb[nb][1], 1.0f) * s45,
+                                          cvt_fp8x2<true>(tb[nb][1], 1.0f) * s67);
+                    }
+                    return __builtin_bit_cast(half8_t, uint4_t{tt[nb - 4][0][0], tt[nb - 4][0][1],
+                                                               tt[nb - 4][1][0], tt[nb - 4][1][1]});
+                };
+                // fragment nb + 1 is converted while the MFMAs of nb run
+                half8_t vb = frag(0);
+#pragma unroll
+                for (int nb = 0; nb < 8; ++nb) {
+                    if (nb == 3)
+                        asm volatile("s_waitcnt lgkmcnt(0)"
+                                     : "+v"(tb[4]), "+v"(tb[5]), "+v"(tb[6]), "+v"(tb[7]), "+v"(tt[0][0]),
+                                       "+v"(tt[0][1]), "+v"(tt[1][0]), "+v"(tt[1][1]), "+v"(tt[2][0]),
+                                       "+v"(tt[2][1]), "+v"(tt[3][0]), "+v"(tt[3][1])
+                                     :: "memory");
+                    const half8_t vn = nb < 7 ? frag(nb + 1) : vb;
+#pragma unroll
+                    for (int hb = 0; hb < 4; ++hb)
+                        o[hb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[hb], vb, o[hb][nb], 0, 0, 0);
+                    vb = vn;
+                }
+            };
+            // prologue: tiles 0 .. kFsLead - 1; tile 0 lands before the first barrier
+#pragma unroll
+            for (int u = 0; u < kFsLead; ++u) issue(u);
+            asm volatile("s_waitcnt vmcnt(%0)" :: "n"(5 * (kFsLead - 1)) : "memory");
+            lds_barrier();
+            // interval u: copies of u + kFsLead, P . V(u - 2); before the barrier
+            // that ends it, tile u + 1 has landed (this wave's copies)
+            for (int u = 0; u < n_tiles + 2; ++u) {
+                issue(u + kFsLead);
+                if (u >= 2) pv(u - 2);
+                asm volatile("s_waitcnt vmcnt(%0)" :: "n"(5 * (kFsLead - 1)) : "memory");
+                lds_barrier();
+            }
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            // the lane offset is rebuilt here: hoisted to the kernel start it would
+            // stay live through both loops
+            int lo = (4 * q) * kD + j;
+            asm volatile("" : "+v"(lo));
+            float *wo = A.ws_o + slot * (kH * kD) + 128 * c + lo;
+            asm volatile("" : "+v"(wo));
+#pragma unroll
+            for (int hb = 0; hb < 4; ++hb)
+#pragma unroll
+                for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) wo[(16 * hb + r) * kD + 16 * nb] = o[hb][nb][r];
+        };
+        if (n_tiles > 0) {
+            if (producer) {
+                lds_barrier();   // stage 0 complete (the consumers' prologue copies)
+                produce();
+            } else {
+                if (d == 3) consume(std::true_type{});
+                else consume(std::false_type{});
+            }
+        }
+        // a segment with no rows (padding of the chunked row space) has no partial
+        if (threadIdx.x == 0) A.ws_prob[slot] = n_tiles > 0 ? p : -1;
+        ++slot_s;
+        g0 = seg_end;
+        lds_barrier();   // the next segment reuses the stages
+    }
+    if (threadIdx.x == 0)
+        for (int s2 = slot_s; s2 < A.s_max; ++s2) A.ws_prob[(long long)blockIdx.x * A.s_max + s2] = -1;
+}
+
 // Physical cache row of every logical row of a gathered step (row_idx and/or
 // page table), plus 32 rows of padding that repeat the last row.
 __global__ __launch_bounds__(256) void phys_kernel(const DecodeArgs A) {
@@ -1565,8 +2176,24 @@ bool decode_exact_p() {
     return g_decode_exact_p == 1;
 }
 
+// Direct rows with one f16 P use the flat-stage kernel unless
+// DS4HIP_DECODE_KERNEL=ws selects the register-load kernel.
+bool use_flat_kernel() {
+    static const int v = [] {
+        const char *e = getenv("DS4HIP_DECODE_KERNEL");
+        return (e && e[0] == 'w') ? 0 : 1;
+    }();
+    return v == 1;
+}
+
 template <int kMode>
 void launch_ws(const DecodeArgs &A, const Plan &pl, hipStream_t st) {
+    // (the f16 hi + lo P form keeps the register-load kernel: the flat kernel's
+    // producers have no registers left for the second P fragment)
+    if (kMode == 0 && use_flat_kernel() && !decode_exact_p()) {
+        hipLaunchKernelGGL(decode_flat_kernel<false>, dim3(pl.n_wg), dim3(512), 0, st, A);
+        return;
+    }
     if (decode_exact_p())
         hipLaunchKernelGGL((decode_ws_kernel<kMode, true>), dim3(pl.n_wg), dim3(512), 0, st, A);
     else

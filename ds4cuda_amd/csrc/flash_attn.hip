@@ -1410,6 +1410,7 @@ constexpr int kFsStages = 6;
 constexpr int kFsLead = 3;                                 // tiles copied ahead of the producers
 constexpr int kFsCodeChunks = kTile * (kFsCodeRow / 16);  // 960
 constexpr int kFsChunks = kFsCodeChunks + kTile * (kFsTailRow / 16);   // 1216 = 19 x 64
+static_assert(kFsCodeChunks % 64 == 0, "code and tail chunks take separate copy instructions");
 // LDS chunk position of tail chunk c of tile row r (an involution on c)
 __device__ __host__ constexpr int fs_tail_pos(int r, int c) { return c ^ ((r >> 1) & 7); }
 static_assert(kFsChunks == 19 * 64, "codes + tails fill 19 copy instructions");
@@ -1707,7 +1708,7 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
             // tail takes two f16 MFMAs. The wave also writes the f16 scale 2^e of
             // blocks 2d, 2d + 1 of the tile's rows to the stage's scale table, which
             // the consumers' V conversion reads.
-            auto qk = [&](int u, float4_t (&acc)[2]) {
+            auto qk = [&](int u, float4_t (&acc)[2], auto &&pre) {
                 const uint32_t st = lds_addr(stage[u % kFsStages]);
                 // tail chunks q and 4 + q of rows j and 16 + j (same swizzle);
                 // rebuilt per tile from an opaque lane id so that they are not
@@ -1718,17 +1719,19 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
                 const uint32_t tpos1 = tpos0 ^ 64;
                 typedef int int8v __attribute__((ext_vector_type(8)));
                 const uint4_t z4 = uint4_t{0, 0, 0, 0};
-                // one row half at a time: the reads of half 1 go out after the
+                // one row half at a time: the softmax of the previous tile runs
+                // while half 0's reads land; the reads of half 1 go out after the
                 // MFMAs of half 0 are issued and land while those run, so only one
                 // half's fragments are live
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh) {
                     uint4_t kc[7];      // dims 64 b + 16 q + [0, 16)
-                    uint4_t kt[2];      // f16 tail dims 448 + 16 q + [0, 16)
+                    uint4_t kt[2];      // f16 tail dims 448 + 32 s + 8 q + [0, 8)
                     uint2_t ke;         // exponents
                     const uint32_t ta = st + kFsTailOff + (16 * hh + j) * kFsTailRow;
                     lds_read_row(st + (16 * hh + j) * kFsCodeRow + 16 * q, ta + tpos0, ta + tpos1,
                                  st + kFsExpOff + (16 * hh + j) * 8, kc, kt, ke);
+                    if (hh == 0) pre();
                     lds_row_wait(kc, kt, ke);
                     if (q < 2 && (d < 3 || q == 0)) {
                         const int e = (int)(int8_t)((ke[(2 * d + q) >> 2] >> (8 * ((2 * d + q) & 3))) & 0xFF);
@@ -1760,12 +1763,11 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
 
             float4_t sprev[2];
             __builtin_amdgcn_sched_barrier(0);
-            qk(0, sprev);                       // interval 0
+            qk(0, sprev, [] {});                // interval 0
             lds_barrier();
-            for (int u = 1; u < n_tiles; ++u) { // interval u
-                float4_t acc[2];
-                qk(u, acc);
-                softmax(u - 1, sprev);
+            for (int u = 1; u < n_tiles; ++u) { // interval u: the softmax of u - 1
+                float4_t acc[2];                // first, under the first reads of u
+                qk(u, acc, [&] { softmax(u - 1, sprev); });
                 sprev[0] = acc[0];
                 sprev[1] = acc[1];
                 lds_barrier();
@@ -1788,11 +1790,14 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
         auto consume = [&](auto tc) {
             constexpr bool kTailQ = decltype(tc)::value;   // dim quarter 3 (64 FP8 + 64 f16 dims)
             const int c = d;
+            // copy instruction n = 5 c + k moves chunks 64 n + [0, 64) of the
+            // stage: n < 15 code chunks, 15 <= n < 19 tail chunks, n = 19 the
+            // exponents (n is wave-uniform, so each copy is one scalar-branched
+            // global_load_lds with a 32-bit lane offset from the segment base).
+            // The lane's row and byte offset are computed per segment: hoisted to
+            // the kernel start they would stay live through the producers' code.
             int c_row[5];
             uint32_t c_off[5];
-            bool c_tail[5];
-            // computed here, per segment: hoisted to the kernel start they would
-            // stay live through the producers' code as well
             int ln = lane;
             asm volatile("" : "+v"(ln));
 #pragma unroll
@@ -1802,17 +1807,14 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
                 if (n == 19) {           // exponents: 4 bytes per lane
                     c_row[k] = ln >> 1;
                     c_off[k] = 4 * (ln & 1);
-                    c_tail[k] = false;
-                } else if (s < kFsCodeChunks) {
+                } else if (n < kFsCodeChunks / 64) {
                     const int cc2 = s % (kFsCodeRow / 16);
                     c_row[k] = s / (kFsCodeRow / 16);
                     c_off[k] = 16 * min(cc2, kNope / 16 - 1);   // the pad chunks re-read chunk 27
-                    c_tail[k] = false;
                 } else {
                     const int s2 = s - kFsCodeChunks;
                     c_row[k] = s2 / (kFsTailRow / 16);
                     c_off[k] = 16 * fs_tail_pos(c_row[k], s2 % (kFsTailRow / 16));
-                    c_tail[k] = true;
                 }
             }
             const uint8_t *codes_s = A.codes + seg_r0 * kNope;
@@ -1827,14 +1829,12 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
                 for (int k = 0; k < 5; ++k) {
                     const int n = 5 * c + k;
                     const uint32_t lr = (uint32_t)min(kTile * u + c_row[k], seg_last);
-                    if (n == 19) {
-                        __builtin_amdgcn_global_load_lds(sexp_s + (lr * 8 + c_off[k]),
-                                                         st + kFsExpOff, 4, 0, 0);
-                    } else {
-                        const uint8_t *g = c_tail[k] ? tail_s + (lr * (2 * kRot) + c_off[k])
-                                                     : codes_s + (lr * kNope + c_off[k]);
-                        __builtin_amdgcn_global_load_lds(g, st + 1024 * n, 16, 0, 0);
-                    }
+                    if (n == 19)
+                        __builtin_amdgcn_global_load_lds(sexp_s + (lr * 8 + c_off[k]), st + kFsExpOff, 4, 0, 0);
+                    else if (n < kFsCodeChunks / 64)
+                        __builtin_amdgcn_global_load_lds(codes_s + (lr * kNope + c_off[k]), st + 1024 * n, 16, 0, 0);
+                    else
+                        __builtin_amdgcn_global_load_lds(tail_s + (lr * (2 * kRot) + c_off[k]), st + 1024 * n, 16, 0, 0);
                 }
             };
             float4_t o[4][8];   // heads 16 hb + 4 q + r, dims 128 c + 16 nb + j

@@ -77,6 +77,8 @@ SIGNATURES: dict[str, list] = {
     "ds4hip_session_push_index_comp": [_vp, _i, _vp, _vp],
     "ds4hip_rows_scatter_f32": [_vp, _i, _i, _vp, _vp, _vp],
     "ds4hip_session_layer_rows": [_vp, _i, _i, C.POINTER(_vp), C.POINTER(_ll), C.POINTER(_vp)],
+    "ds4hip_session_save_to_disk": [_vp, _vp, _i, C.c_char_p],
+    "ds4hip_session_load_from_disk": [_vp, C.c_char_p, C.POINTER(_i), C.POINTER(_i)],
 }
 
 # entry points that return a value rather than a status

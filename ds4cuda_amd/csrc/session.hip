@@ -20,7 +20,9 @@
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
+#include <cstdio>
 #include <cstring>
+#include <vector>
 
 #include "../../include/ds4hip_session.h"
 #include "ds4hip_common.h"
@@ -369,4 +371,194 @@ extern "C" int ds4hip_rows_scatter_f32(const float *src, int n_rows, int width, 
     hipLaunchKernelGGL(rows_scatter_kernel, dim3((n_rows + 3) / 4), dim3(256), 0,
                        (hipStream_t)stream, src, n_rows, width, dst, dst_rows);
     return ds4hip_set_last_error(hip_status(hipGetLastError()));
+}
+
+// ---- disk persistence of the FP8 session (cuda/kv_persist.cu) ----------------------------
+//
+// Every layer's payload is a list of (device pointer, bytes) buffers, written
+// and read in the same order through one host bounce buffer sized to the
+// largest of them. The device is synchronized before a save (the copies must
+// see the finished state) and after a load (the caller sees the buffers
+// filled on return).
+
+namespace {
+
+static_assert(sizeof(ds4hip_kvc_header) == 4096, "header is 4 KiB");
+static_assert(sizeof(ds4hip_kvc_layer_meta) == 64, "layer meta is 64 B");
+
+constexpr int kEIO = -5;
+
+struct Buf {
+    void *p;
+    size_t bytes;
+};
+
+// The buffers of layer L in file order; returns their count.
+int layer_bufs(const ds4hip_session_state *s, const ds4hip_layer_state *L, Buf (&b)[9]) {
+    const size_t rows = (size_t)L->cap_comp + L->cap_raw;
+    int n = 0;
+    b[n++] = {s->codes + (size_t)L->row_base * DS4HIP_FP8_CODES, rows * DS4HIP_FP8_CODES};
+    b[n++] = {s->sexp + (size_t)L->row_base * DS4HIP_FP8_SEXP, rows * DS4HIP_FP8_SEXP};
+    b[n++] = {s->tail + (size_t)L->row_base * DS4HIP_FP8_TAIL, rows * DS4HIP_FP8_TAIL * 2};
+    b[n++] = {L->row_list, rows * 4};
+    if (L->compress_ratio) {
+        const size_t sb = attn_state_cells(L->compress_ratio) * 4;
+        b[n++] = {L->attn_state_kv, sb};
+        b[n++] = {L->attn_state_score, sb};
+    }
+    if (L->has_indexer) {
+        b[n++] = {L->index_comp_kv, (size_t)L->cap_comp * DS4HIP_INDEXER_HEAD_DIM * 4};
+        b[n++] = {L->index_state_kv, index_state_cells() * 4};
+        b[n++] = {L->index_state_score, index_state_cells() * 4};
+    }
+    return n;
+}
+
+uint64_t layer_payload(const ds4hip_session_state *s, const ds4hip_layer_state *L, size_t *max_buf) {
+    Buf b[9];
+    const int n = layer_bufs(s, L, b);
+    uint64_t t = 0;
+    for (int i = 0; i < n; ++i) {
+        t += b[i].bytes;
+        if (max_buf && b[i].bytes > *max_buf) *max_buf = b[i].bytes;
+    }
+    return t;
+}
+
+// Geometry of an allocated session matches what ds4hip_session_state_alloc
+// builds for its max_context (a struct edited by hand is refused).
+bool session_ok(const ds4hip_session_state *s) {
+    if (!s || !s->arena_base || s->max_context <= 0) return false;
+    const Plan P = make_plan(s->max_context);
+    if (s->n_cache_rows != P.n_rows) return false;
+    for (int il = 0; il < DS4HIP_N_LAYER; ++il) {
+        const ds4hip_layer_state &L = s->layers[il];
+        if (L.il != il || L.compress_ratio != layer_ratio(il) || L.cap_raw != P.cap_raw ||
+            L.cap_comp != P.cap_comp[il] || L.row_base != P.row_base[il] || !L.row_list)
+            return false;
+    }
+    return true;
+}
+
+struct File {
+    FILE *f = nullptr;
+    ~File() {
+        if (f) std::fclose(f);
+    }
+};
+
+int fail(int code) {
+    ds4hip_set_last_error(code);
+    return -1;
+}
+
+}  // namespace
+
+extern "C" int ds4hip_session_save_to_disk(const ds4hip_session_state *s, const int32_t *prompt_token_ids,
+                                           int n_tokens, const char *path) {
+    if (!path || !session_ok(s) || n_tokens < 0 || (n_tokens > 0 && !prompt_token_ids)) return fail(kEINVAL);
+    int rc = hip_status(hipDeviceSynchronize());
+    if (rc) return fail(rc);
+    ds4hip_kvc_header h;
+    std::memset(&h, 0, sizeof(h));
+    std::memcpy(h.magic, DS4HIP_KVC_MAGIC, 8);
+    h.version = DS4HIP_KVC_VERSION;
+    h.n_layer = DS4HIP_N_LAYER;
+    h.max_context = (uint32_t)s->max_context;
+    h.pos = (uint32_t)s->pos;
+    h.n_tokens_processed = (uint32_t)s->n_tokens_processed;
+    h.n_prompt_tokens = (uint32_t)(n_tokens < DS4HIP_KVC_MAX_TOKENS_HDR ? n_tokens : DS4HIP_KVC_MAX_TOKENS_HDR);
+    for (uint32_t i = 0; i < h.n_prompt_tokens; ++i) h.prompt_token_ids[i] = prompt_token_ids[i];
+    h.cap_raw = (uint32_t)s->layers[0].cap_raw;
+    h.row_codes = DS4HIP_FP8_CODES;
+    h.row_sexp = DS4HIP_FP8_SEXP;
+    h.row_tail = DS4HIP_FP8_TAIL;
+    h.n_cache_rows = (uint64_t)s->n_cache_rows;
+    size_t max_buf = 0;
+    for (int il = 0; il < DS4HIP_N_LAYER; ++il) layer_payload(s, &s->layers[il], &max_buf);
+    std::vector<uint8_t> bounce(max_buf);
+    File out;
+    out.f = std::fopen(path, "wb");   // truncates: a failed save leaves no stale payload behind
+    if (!out.f) return fail(kEIO);
+    if (std::fwrite(&h, sizeof(h), 1, out.f) != 1) return fail(kEIO);
+    for (int il = 0; il < DS4HIP_N_LAYER; ++il) {
+        const ds4hip_layer_state &L = s->layers[il];
+        ds4hip_kvc_layer_meta m;
+        std::memset(&m, 0, sizeof(m));
+        m.il = il;
+        m.compress_ratio = L.compress_ratio;
+        m.has_indexer = L.has_indexer;
+        m.cap_raw = L.cap_raw;
+        m.cap_comp = L.cap_comp;
+        m.n_raw = L.n_raw;
+        m.raw_head = L.raw_head;
+        m.n_comp = L.n_comp;
+        m.n_index_comp = L.n_index_comp;
+        m.row_base = L.row_base;
+        m.bytes_after = layer_payload(s, &L, nullptr);
+        if (std::fwrite(&m, sizeof(m), 1, out.f) != 1) return fail(kEIO);
+        Buf b[9];
+        const int nb = layer_bufs(s, &L, b);
+        for (int i = 0; i < nb; ++i) {
+            rc = hip_status(hipMemcpy(bounce.data(), b[i].p, b[i].bytes, hipMemcpyDeviceToHost));
+            if (rc) return fail(rc);
+            if (std::fwrite(bounce.data(), 1, b[i].bytes, out.f) != b[i].bytes) return fail(kEIO);
+        }
+    }
+    if (std::fwrite(DS4HIP_KVC_TRAILER, 1, 8, out.f) != 8) return fail(kEIO);
+    const int cr = std::fclose(out.f);
+    out.f = nullptr;
+    return cr == 0 ? 0 : fail(kEIO);
+}
+
+extern "C" int ds4hip_session_load_from_disk(ds4hip_session_state *s_out, const char *path, int *out_pos,
+                                             int *out_n_tokens) {
+    if (!path || !session_ok(s_out)) return fail(kEINVAL);
+    File in;
+    in.f = std::fopen(path, "rb");
+    if (!in.f) return fail(kEIO);
+    ds4hip_kvc_header h;
+    if (std::fread(&h, sizeof(h), 1, in.f) != 1) return fail(kEIO);
+    if (std::memcmp(h.magic, DS4HIP_KVC_MAGIC, 8) != 0 || h.version != DS4HIP_KVC_VERSION ||
+        h.n_layer != DS4HIP_N_LAYER || h.max_context != (uint32_t)s_out->max_context ||
+        h.cap_raw != (uint32_t)s_out->layers[0].cap_raw || h.row_codes != DS4HIP_FP8_CODES ||
+        h.row_sexp != DS4HIP_FP8_SEXP || h.row_tail != DS4HIP_FP8_TAIL ||
+        h.n_cache_rows != (uint64_t)s_out->n_cache_rows || h.pos > h.max_context ||
+        h.n_prompt_tokens > DS4HIP_KVC_MAX_TOKENS_HDR)
+        return fail(kEINVAL);
+    size_t max_buf = 0;
+    for (int il = 0; il < DS4HIP_N_LAYER; ++il) layer_payload(s_out, &s_out->layers[il], &max_buf);
+    std::vector<uint8_t> bounce(max_buf);
+    for (int il = 0; il < DS4HIP_N_LAYER; ++il) {
+        ds4hip_layer_state &L = s_out->layers[il];
+        ds4hip_kvc_layer_meta m;
+        if (std::fread(&m, sizeof(m), 1, in.f) != 1) return fail(kEIO);
+        if (m.il != il || m.compress_ratio != L.compress_ratio || m.has_indexer != L.has_indexer ||
+            m.cap_raw != L.cap_raw || m.cap_comp != L.cap_comp || m.row_base != L.row_base ||
+            m.bytes_after != layer_payload(s_out, &L, nullptr) || m.n_raw < 0 || m.n_raw > L.cap_raw ||
+            m.raw_head < 0 || m.raw_head >= (L.cap_raw ? L.cap_raw : 1) || m.n_comp < 0 ||
+            m.n_comp > L.cap_comp || m.n_index_comp < 0 || m.n_index_comp > L.cap_comp ||
+            (!L.compress_ratio && m.n_comp) || (!L.has_indexer && m.n_index_comp))
+            return fail(kEINVAL);
+        Buf b[9];
+        const int nb = layer_bufs(s_out, &L, b);
+        for (int i = 0; i < nb; ++i) {
+            if (std::fread(bounce.data(), 1, b[i].bytes, in.f) != b[i].bytes) return fail(kEIO);
+            const int rc = hip_status(hipMemcpy(b[i].p, bounce.data(), b[i].bytes, hipMemcpyHostToDevice));
+            if (rc) return fail(rc);
+        }
+        L.n_raw = m.n_raw;
+        L.raw_head = m.raw_head;
+        L.n_comp = m.n_comp;
+        L.n_index_comp = m.n_index_comp;
+    }
+    char tr[8];
+    if (std::fread(tr, 1, 8, in.f) != 8 || std::memcmp(tr, DS4HIP_KVC_TRAILER, 8) != 0) return fail(kEINVAL);
+    const int rc = hip_status(hipDeviceSynchronize());
+    if (rc) return fail(rc);
+    s_out->pos = (int)h.pos;
+    s_out->n_tokens_processed = (int)h.n_tokens_processed;
+    if (out_pos) *out_pos = s_out->pos;
+    if (out_n_tokens) *out_n_tokens = s_out->n_tokens_processed;
+    return 0;
 }

@@ -9,6 +9,7 @@ cuda/session_state.cu:110-256): one device arena, per-layer FP8 rows
 from __future__ import annotations
 
 import ctypes as C
+import os
 
 import torch
 
@@ -97,6 +98,29 @@ class Session:
     def push_index_comp(self, il, row, stream=None):
         _check(row, torch.float32, 128, "row")
         call("ds4hip_session_push_index_comp", C.byref(self.s), il, _ptr(row), _stream(stream))
+
+    def save(self, path, prompt_token_ids=None):
+        """Writes the session to path (format in include/ds4hip_session.h);
+        at most the first 64 prompt token ids are stored."""
+        ids = [] if prompt_token_ids is None else [int(t) for t in prompt_token_ids]
+        arr = (C.c_int32 * max(len(ids), 1))(*ids)
+        self._persist("ds4hip_session_save_to_disk", C.byref(self.s), arr if ids else None,
+                      len(ids), os.fsencode(path))
+
+    def load(self, path):
+        """Restores a saved session (same max_context); returns (pos, n_tokens_processed)."""
+        pos, n = C.c_int(), C.c_int()
+        self._persist("ds4hip_session_load_from_disk", C.byref(self.s), os.fsencode(path),
+                      C.byref(pos), C.byref(n))
+        return pos.value, n.value
+
+    @staticmethod
+    def _persist(name, *args):
+        # these two return -1 on any error (the reference's convention); the
+        # detailed status is the library's last error
+        lib().ds4hip_clear_last_error()
+        if getattr(lib(), name)(*args) != 0:
+            raise Ds4HipError(name, lib().ds4hip_get_last_error())
 
     def layer_rows(self, il, n_selected=-1):
         """(row_idx device address, n_rows, selected device address)."""

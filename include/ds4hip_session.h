@@ -130,6 +130,84 @@ int ds4hip_rows_scatter_f32(const float *src, int n_rows, int width, float *dst,
 int ds4hip_session_layer_rows(const ds4hip_session_state *s, int il, int n_selected,
                               const int32_t **row_idx, long long *n_rows, int32_t **selected_out);
 
+/* ---- disk format of the FP8 session (cuda/kv_persist.cuh:6-37, adapted) ---------- */
+
+/* One file holds the whole session: the header, then per layer its meta and
+ * payload, then the trailer. Every buffer is written at full capacity, so a
+ * load is a straight host-to-device copy and the restored arena is
+ * byte-identical to the saved one:
+ *
+ *   [ ds4hip_kvc_header ]                           4096 B
+ *   for il in 0..42:
+ *     [ ds4hip_kvc_layer_meta ]                     64 B
+ *     [ codes  (cap_comp + cap_raw) x 448 B ]       the layer's FP8 rows
+ *     [ sexp   (cap_comp + cap_raw) x 8 B ]
+ *     [ tail   (cap_comp + cap_raw) x 128 B ]       f16
+ *     [ row_list (cap_raw + cap_comp) x 4 B ]
+ *     if compress_ratio:  [ attn_state_kv ] [ attn_state_score ]   fp32 cells
+ *     if has_indexer:     [ index_comp_kv cap_comp x 128 x 4 B ]
+ *                         [ index_state_kv ] [ index_state_score ]
+ *   [ trailer "DS4HIP01" ]
+ *
+ * The reference's file also carries the hyper-connection residual, which is
+ * not part of this session (see ds4hip_session_state). */
+#define DS4HIP_KVC_MAGIC "DS4HIPK8"   /* 8 bytes, no NUL */
+#define DS4HIP_KVC_TRAILER "DS4HIP01" /* 8 bytes, no NUL */
+#define DS4HIP_KVC_VERSION 1u
+#define DS4HIP_KVC_MAX_TOKENS_HDR 64
+
+typedef struct ds4hip_kvc_header {
+    char magic[8];
+    uint32_t version;
+    uint32_t n_layer;
+    uint32_t max_context;
+    uint32_t pos;
+    uint32_t n_tokens_processed;
+    uint32_t n_prompt_tokens; /* valid entries of prompt_token_ids */
+    uint32_t cap_raw;
+    uint32_t row_codes;       /* 448 */
+    uint32_t row_sexp;        /* 8 */
+    uint32_t row_tail;        /* 64 (f16 elements) */
+    uint64_t n_cache_rows;
+    int32_t prompt_token_ids[DS4HIP_KVC_MAX_TOKENS_HDR];
+    uint8_t pad[4096 - 56 - 4 * DS4HIP_KVC_MAX_TOKENS_HDR];
+} ds4hip_kvc_header;
+
+typedef struct ds4hip_kvc_layer_meta {
+    int32_t il;
+    int32_t compress_ratio;
+    int32_t has_indexer;
+    int32_t cap_raw;
+    int32_t cap_comp;
+    int32_t n_raw;
+    int32_t raw_head;
+    int32_t n_comp;
+    int32_t n_index_comp;
+    int32_t reserved0;
+    int64_t row_base;
+    uint64_t bytes_after; /* payload bytes of this layer (checked on load) */
+    uint64_t reserved[1];
+} ds4hip_kvc_layer_meta;
+
+/* Writes the session to path (cuda/kv_persist.cuh:97-100): synchronizes the
+ * device, then copies each buffer through one host bounce buffer. At most the
+ * first 64 prompt token ids are stored (n_tokens may be 0 with NULL ids).
+ * Returns 0, or -1 on any error (the reference's convention); the detailed
+ * status (-22 arguments, -5 I/O, -1000 - hipError_t) is kept for
+ * ds4hip_get_last_error. */
+int ds4hip_session_save_to_disk(const ds4hip_session_state *s, const int32_t *prompt_token_ids,
+                                int n_tokens, const char *path);
+
+/* Restores a saved session into s_out, which must come from
+ * ds4hip_session_state_alloc with the file's max_context
+ * (cuda/kv_persist.cuh:102-127): header and every layer meta are checked
+ * against s_out's geometry before its buffers are written; the counters, pos
+ * and n_tokens_processed are set from the file. out_pos / out_n_tokens may be
+ * NULL. Returns 0 or -1 as ds4hip_session_save_to_disk; after a failure past
+ * the header check s_out is indeterminate (reset it before reuse). */
+int ds4hip_session_load_from_disk(ds4hip_session_state *s_out, const char *path, int *out_pos,
+                                  int *out_n_tokens);
+
 #ifdef __cplusplus
 }
 #endif

@@ -77,6 +77,11 @@ SIGNATURES: dict[str, list] = {
     "ds4hip_session_push_index_comp": [_vp, _i, _vp, _vp],
     "ds4hip_rows_scatter_f32": [_vp, _i, _i, _vp, _vp, _vp],
     "ds4hip_session_layer_rows": [_vp, _i, _i, C.POINTER(_vp), C.POINTER(_ll), C.POINTER(_vp)],
+    "ds4hip_rms_norm_f32": [_vp, _vp, _vp, _i, C.c_float, _vp],
+    "ds4hip_rms_norm_batch_f32": [_vp, _vp, _i, _vp, _i, _i, C.c_float, _vp],
+    "ds4hip_attn_qkv_decode_workspace_bytes": [],
+    "ds4hip_attn_qkv_decode_f32": [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _sz,
+                                   _vp],
     "ds4hip_session_save_to_disk": [_vp, _vp, _i, C.c_char_p],
     "ds4hip_session_load_from_disk": [_vp, C.c_char_p, C.POINTER(_i), C.POINTER(_i)],
 }
@@ -86,7 +91,8 @@ RESTYPES = {"ds4hip_indexer_select_scratch_bytes": C.c_size_t,
             "ds4hip_flash_attn_prefill_fp8_workspace_size": C.c_size_t,
             "ds4hip_session_state_arena_bytes": C.c_size_t,
             "ds4hip_mul_mm_workspace_bytes": C.c_size_t,
-            "ds4hip_compressor_batch_scratch_bytes": C.c_size_t}
+            "ds4hip_compressor_batch_scratch_bytes": C.c_size_t,
+            "ds4hip_attn_qkv_decode_workspace_bytes": C.c_size_t}
 
 _lib = None
 

@@ -67,6 +67,27 @@ RopeParams rope_params(int n_rot, int il, bool inverse) {
     return P;
 }
 
+// Rotation of pair t (dims n_nope + 2t, n_nope + 2t + 1) at position pos.
+__device__ inline void rope_pair(float x0, float x1, int t, int pos, const RopeParams &P, float &y0,
+                                 float &y1) {
+    float theta_extrap = (float)pos;
+    for (int k = 0; k < t; ++k) theta_extrap *= P.theta_scale;   // running product (rope.cu:172-177)
+    const float theta_interp = P.freq_scale * theta_extrap;
+    float theta = theta_interp;
+    float mscale = P.attn_factor;
+    if (P.ext_factor != 0.0f) {
+        // cuda/rope.cu:130-133 ramp, then the YaRN mix
+        const float y = ((float)((2 * t) / 2) - P.corr_low) / fmaxf(0.001f, P.corr_high - P.corr_low);
+        const float ramp_mix = (1.0f - fminf(1.0f, fmaxf(0.0f, y))) * P.ext_factor;
+        theta = theta_interp * (1.0f - ramp_mix) + theta_extrap * ramp_mix;
+        mscale *= 1.0f + 0.1f * logf(1.0f / P.freq_scale);
+    }
+    const float c = cosf(theta) * mscale;
+    const float s = P.sin_sign * sinf(theta) * mscale;
+    y0 = x0 * c - x1 * s;
+    y1 = x0 * s + x1 * c;
+}
+
 // pos_dev (optional): position per group of heads_per_pos consecutive heads.
 __global__ __launch_bounds__(64) void rope_tail_kernel(const float *__restrict__ x_in,
                                                        float *__restrict__ x_out, int head_dim,
@@ -83,23 +104,10 @@ __global__ __launch_bounds__(64) void rope_tail_kernel(const float *__restrict__
     if (xi != xo)
         for (int d = t; d < n_nope; d += 64) xo[d] = xi[d];
     if (t >= half) return;
-    float theta_extrap = (float)pos;
-    for (int k = 0; k < t; ++k) theta_extrap *= P.theta_scale;   // running product (rope.cu:172-177)
-    const float theta_interp = P.freq_scale * theta_extrap;
-    float theta = theta_interp;
-    float mscale = P.attn_factor;
-    if (P.ext_factor != 0.0f) {
-        // cuda/rope.cu:130-133 ramp, then the YaRN mix
-        const float y = ((float)((2 * t) / 2) - P.corr_low) / fmaxf(0.001f, P.corr_high - P.corr_low);
-        const float ramp_mix = (1.0f - fminf(1.0f, fmaxf(0.0f, y))) * P.ext_factor;
-        theta = theta_interp * (1.0f - ramp_mix) + theta_extrap * ramp_mix;
-        mscale *= 1.0f + 0.1f * logf(1.0f / P.freq_scale);
-    }
-    const float c = cosf(theta) * mscale;
-    const float s = P.sin_sign * sinf(theta) * mscale;
-    const float x0 = xi[n_nope + 2 * t], x1 = xi[n_nope + 2 * t + 1];
-    xo[n_nope + 2 * t] = x0 * c - x1 * s;
-    xo[n_nope + 2 * t + 1] = x0 * s + x1 * c;
+    float y0, y1;
+    rope_pair(xi[n_nope + 2 * t], xi[n_nope + 2 * t + 1], t, pos, P, y0, y1);
+    xo[n_nope + 2 * t] = y0;
+    xo[n_nope + 2 * t + 1] = y1;
 }
 
 int launch_rope(const float *x_in, float *x_out, int n_heads, int head_dim, int n_rot, int pos,
@@ -231,6 +239,125 @@ int launch_q8(const uint8_t *W, const float *x, float *y, int n_groups, int grou
     hipLaunchKernelGGL(mv_q8_kernel, dim3((n_rows + 3) / 4), dim3(256), 0, st, W, xq, xs, y,
                        n_rows, bpg, rank, grouped ? 1 : 0);
     return hip_status(hipGetLastError());
+}
+
+// ---- RMSNorm (cuda/norm.cu) and the decode Q / KV producer chain ---------------------------
+// (cuda/forward_layer.cu:827-913, Steps 3-10). RMSNorm: one 256-thread block
+// per row; thread t accumulates x[i]^2 for i = t, t + 256, ... in order, the
+// wave sums are added in wave order, scale = 1 / sqrtf(ss / n + eps) and
+// y = x * scale * w (w NULL: unit gain), the reference's operation order.
+constexpr float kRmsEps = 1.0e-6f;
+
+__device__ inline float block_sum_256(float v, float *part) {
+    v = wave_sum(v);
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) part[wave] = v;
+    __syncthreads();
+    return ((part[0] + part[1]) + part[2]) + part[3];
+}
+
+__global__ __launch_bounds__(256) void rms_norm_kernel(const float *__restrict__ x,
+                                                       const float *__restrict__ w, int weight_dim,
+                                                       float *__restrict__ y, int n, float eps) {
+    __shared__ float part[4];
+    const int row = blockIdx.x;
+    const float *xr = x + (size_t)row * n;
+    float *yr = y + (size_t)row * n;
+    const float *wr = weight_dim == 0 ? nullptr : (weight_dim == n ? w : w + (size_t)row * n);
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < n; i += 256) ss = fmaf(xr[i], xr[i], ss);
+    const float scale = 1.0f / sqrtf(block_sum_256(ss, part) / (float)n + eps);
+    for (int i = threadIdx.x; i < n; i += 256) yr[i] = wr ? xr[i] * scale * wr[i] : xr[i] * scale;
+}
+
+// RMSNorm of one row of n = 256 k elements (weight w), then the Q8_0
+// activation quantization of the normed row (the q_b matvec's input): element
+// i = t + 256 k sits in thread t, so each 32-element block is one half-wave.
+__global__ __launch_bounds__(256) void norm_q8_kernel(const float *__restrict__ x,
+                                                      const float *__restrict__ w,
+                                                      float *__restrict__ y, int8_t *__restrict__ xq,
+                                                      float *__restrict__ xscale, int n, float eps) {
+    __shared__ float part[4];
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < n; i += 256) ss = fmaf(x[i], x[i], ss);
+    const float scale = 1.0f / sqrtf(block_sum_256(ss, part) / (float)n + eps);
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const float v = x[i] * scale * w[i];
+        y[i] = v;
+        float a = fabsf(v);
+#pragma unroll
+        for (int off = 16; off > 0; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, 32));
+        const float d = a / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        int q = (int)__builtin_rintf(v * id);
+        q = q > 127 ? 127 : (q < -128 ? -128 : q);
+        xq[i] = (int8_t)q;
+        if ((threadIdx.x & 31) == 0) xscale[i >> 5] = d;
+    }
+}
+
+// Per-head RMSNorm over 512 dims (optional weight shared by the heads), then
+// the tail RoPE of dims 448..511: one wave per head, lane l holds dims
+// 8 l .. 8 l + 7 (so lanes 56..63 hold the 32 rotated pairs, 4 each).
+__global__ __launch_bounds__(64) void head_norm_rope_kernel(const float *__restrict__ x,
+                                                            const float *__restrict__ w,
+                                                            float *__restrict__ y, int pos,
+                                                            RopeParams P, float eps) {
+    constexpr int kHd = 512, kNope = 448;
+    const int l = threadIdx.x;
+    const float *xr = x + (size_t)blockIdx.x * kHd + 8 * l;
+    float *yr = y + (size_t)blockIdx.x * kHd + 8 * l;
+    float v[8];
+    const float4_t a = *reinterpret_cast<const float4_t *>(xr);
+    const float4_t b = *reinterpret_cast<const float4_t *>(xr + 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        v[i] = a[i];
+        v[4 + i] = b[i];
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss = fmaf(v[i], v[i], ss);
+    const float scale = 1.0f / sqrtf(wave_sum(ss) / (float)kHd + eps);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = w ? v[i] * scale * w[8 * l + i] : v[i] * scale;
+    if (8 * l >= kNope) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            rope_pair(v[2 * i], v[2 * i + 1], (8 * l - kNope) / 2 + i, pos, P, v[2 * i], v[2 * i + 1]);
+    }
+    *reinterpret_cast<float4_t *>(yr) = float4_t{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<float4_t *>(yr + 4) = float4_t{v[4], v[5], v[6], v[7]};
+}
+
+// Workspace of the decode producer chain, 256-byte aligned pieces.
+struct QkvWs {
+    int8_t *xq;       // [4096] attn_norm as int8
+    float *xs;        // [128]
+    float *q_lora;    // [1024]
+    float *kv_raw;    // [512]
+    int8_t *xq2;      // [1024] q_lora_norm as int8
+    float *xs2;       // [32]
+    float *q_raw;     // [64 * 512]
+    size_t bytes;
+};
+constexpr int kEmbd = 4096, kQLora = 1024, kKvDim = 512, kQDim = 64 * 512;
+
+QkvWs qkv_ws(void *base) {   // base NULL: only the size is wanted
+    auto al = [](size_t n) { return (n + 255) & ~size_t(255); };
+    static uint8_t size_only[1];
+    uint8_t *p = base ? static_cast<uint8_t *>(base) : size_only;
+    QkvWs W;
+    size_t o = 0;
+    W.xq = reinterpret_cast<int8_t *>(p + o); o += al(kEmbd);
+    W.xs = reinterpret_cast<float *>(p + o); o += al(kEmbd / 32 * 4);
+    W.q_lora = reinterpret_cast<float *>(p + o); o += al(kQLora * 4);
+    W.kv_raw = reinterpret_cast<float *>(p + o); o += al(kKvDim * 4);
+    W.xq2 = reinterpret_cast<int8_t *>(p + o); o += al(kQLora);
+    W.xs2 = reinterpret_cast<float *>(p + o); o += al(kQLora / 32 * 4);
+    W.q_raw = reinterpret_cast<float *>(p + o); o += al((size_t)kQDim * 4);
+    W.bytes = o;
+    return W;
 }
 
 // ---- bf16 batched matvec / skinny GEMM: Y[b][r] = sum_c W[r][c] X[b][c] -----------------
@@ -545,4 +672,61 @@ extern "C" int ds4hip_mul_mm_bf16_f32(const uint16_t *W, const float *X, float *
         return ds4hip_set_last_error(kEINVAL);
     return ds4hip_set_last_error(mm_full<false>(W, X, Y, n_rows, n_cols, n_batch, workspace,
                                                 workspace_bytes, (hipStream_t)stream));
+}
+
+extern "C" int ds4hip_rms_norm_f32(const float *x, const float *w, float *y, int n, float eps,
+                                   void *stream) {
+    if (!x || !w || !y || n <= 0) return ds4hip_set_last_error(kEINVAL);
+    hipLaunchKernelGGL(rms_norm_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, x, w, n, y, n,
+                       eps);
+    return ds4hip_set_last_error(hip_status(hipGetLastError()));
+}
+
+extern "C" int ds4hip_rms_norm_batch_f32(const float *x, const float *w, int weight_dim, float *y,
+                                         int n_rows, int n_per_row, float eps, void *stream) {
+    if (!x || !y || n_rows < 0 || n_per_row <= 0 ||
+        !(weight_dim == 0 || weight_dim == n_per_row || (long long)weight_dim == (long long)n_rows * n_per_row) ||
+        (weight_dim && !w))
+        return ds4hip_set_last_error(kEINVAL);
+    if (n_rows == 0) return 0;
+    hipLaunchKernelGGL(rms_norm_kernel, dim3(n_rows), dim3(256), 0, (hipStream_t)stream, x, w,
+                       weight_dim, y, n_per_row, eps);
+    return ds4hip_set_last_error(hip_status(hipGetLastError()));
+}
+
+extern "C" size_t ds4hip_attn_qkv_decode_workspace_bytes(void) { return qkv_ws(nullptr).bytes; }
+
+extern "C" int ds4hip_attn_qkv_decode_f32(const float *attn_norm, const void *w_q_a,
+                                          const float *w_q_a_norm, const void *w_kv_a,
+                                          const float *w_kv_a_norm, const void *w_q_b, int pos,
+                                          int il, float *q_lora_norm, float *q_cur, float *kv_rope,
+                                          void *workspace, size_t workspace_bytes, void *stream) {
+    if (!attn_norm || !w_q_a || !w_q_a_norm || !w_kv_a || !w_kv_a_norm || !w_q_b || !q_lora_norm ||
+        !q_cur || !kv_rope || !workspace || pos < 0 || il < 0 ||
+        workspace_bytes < ds4hip_attn_qkv_decode_workspace_bytes())
+        return ds4hip_set_last_error(kEINVAL);
+    const hipStream_t st = (hipStream_t)stream;
+    const QkvWs W = qkv_ws(workspace);
+    const uint8_t *qa = static_cast<const uint8_t *>(w_q_a);
+    const uint8_t *kva = static_cast<const uint8_t *>(w_kv_a);
+    const uint8_t *qb = static_cast<const uint8_t *>(w_q_b);
+    // Steps 3 and 5: q_lora and KVraw from one quantization of attn_norm
+    hipLaunchKernelGGL(q8_quant_kernel, dim3(kEmbd / 256), dim3(256), 0, st, attn_norm, W.xq, W.xs,
+                       kEmbd / 32);
+    hipLaunchKernelGGL(mv_q8_kernel, dim3(kQLora / 4), dim3(256), 0, st, qa, W.xq, W.xs, W.q_lora,
+                       kQLora, kEmbd / 32, kQLora, 0);
+    hipLaunchKernelGGL(mv_q8_kernel, dim3(kKvDim / 4), dim3(256), 0, st, kva, W.xq, W.xs, W.kv_raw,
+                       kKvDim, kEmbd / 32, kKvDim, 0);
+    // Step 4 with the quantization of Step 7's input; Steps 6 + 10
+    hipLaunchKernelGGL(norm_q8_kernel, dim3(1), dim3(256), 0, st, W.q_lora, w_q_a_norm, q_lora_norm,
+                       W.xq2, W.xs2, kQLora, kRmsEps);
+    const RopeParams P = rope_params(64, il, false);
+    hipLaunchKernelGGL(head_norm_rope_kernel, dim3(1), dim3(64), 0, st, W.kv_raw, w_kv_a_norm,
+                       kv_rope, pos, P, kRmsEps);
+    // Step 7, then Steps 8 + 9
+    hipLaunchKernelGGL(mv_q8_kernel, dim3(kQDim / 4), dim3(256), 0, st, qb, W.xq2, W.xs2, W.q_raw,
+                       kQDim, kQLora / 32, kQDim, 0);
+    hipLaunchKernelGGL(head_norm_rope_kernel, dim3(64), dim3(64), 0, st, W.q_raw, nullptr, q_cur,
+                       pos, P, kRmsEps);
+    return ds4hip_set_last_error(hip_status(hipGetLastError()));
 }

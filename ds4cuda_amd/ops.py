@@ -422,3 +422,43 @@ def compressor_decode_step_batch_w32(is_attn, x, w_kv, w_gate, w_ape, w_norm, in
          int(state_stride), _ptr(emit_out), C.cast(em, C.c_void_p), _ptr(scratch),
          scratch.numel() * scratch.element_size(), _stream(stream))
     return list(em)
+
+
+def launch_rms_norm_f32(x, w, y, n, eps=1e-6, stream=None):
+    _check(x, torch.float32, n, "x")
+    _check(w, torch.float32, n, "w")
+    _check(y, torch.float32, n, "y")
+    call("ds4hip_rms_norm_f32", _ptr(x), _ptr(w), _ptr(y), n, eps, _stream(stream))
+
+
+def launch_rms_norm_batch_f32(x, w, weight_dim, y, n_rows, n_per_row, eps=1e-6, stream=None):
+    _check(x, torch.float32, n_rows * n_per_row, "x")
+    _check(y, torch.float32, n_rows * n_per_row, "y")
+    if weight_dim:
+        _check(w, torch.float32, weight_dim, "w")
+    call("ds4hip_rms_norm_batch_f32", _ptr(x), _ptr(w) if weight_dim else None, weight_dim,
+         _ptr(y), n_rows, n_per_row, eps, _stream(stream))
+
+
+def attn_qkv_decode_f32(attn_norm, w_q_a, w_q_a_norm, w_kv_a, w_kv_a_norm, w_q_b, pos, il,
+                        q_lora_norm, q_cur, kv_rope, workspace=None, stream=None):
+    """Steps 3-10 of one decode layer (Q8_0 weights as uint8 block rows):
+    fills q_lora_norm [1024], q_cur [64*512] and kv_rope [512]; returns the
+    workspace (reusable)."""
+    _check(attn_norm, torch.float32, 4096, "attn_norm")
+    _check(w_q_a, torch.uint8, 1024 * 128 * 34, "w_q_a")
+    _check(w_kv_a, torch.uint8, 512 * 128 * 34, "w_kv_a")
+    _check(w_q_b, torch.uint8, 32768 * 32 * 34, "w_q_b")
+    _check(w_q_a_norm, torch.float32, 1024, "w_q_a_norm")
+    _check(w_kv_a_norm, torch.float32, 512, "w_kv_a_norm")
+    _check(q_lora_norm, torch.float32, 1024, "q_lora_norm")
+    _check(q_cur, torch.float32, 64 * 512, "q_cur")
+    _check(kv_rope, torch.float32, 512, "kv_rope")
+    from ._lib import lib
+    need = lib().ds4hip_attn_qkv_decode_workspace_bytes()
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=attn_norm.device)
+    call("ds4hip_attn_qkv_decode_f32", _ptr(attn_norm), _ptr(w_q_a), _ptr(w_q_a_norm),
+         _ptr(w_kv_a), _ptr(w_kv_a_norm), _ptr(w_q_b), pos, il, _ptr(q_lora_norm), _ptr(q_cur),
+         _ptr(kv_rope), _ptr(workspace), workspace.numel(), _stream(stream))
+    return workspace

@@ -219,6 +219,35 @@ int ds4hip_mul_mv_q8_0_q8_0_f32_prealloc(const void *W, const float *x, float *y
                                          int n_cols, int8_t *scratch_xq, float *scratch_xscale,
                                          void *stream);
 
+/* Replaces ds4cuda::launch_rms_norm_f32 (cuda/norm.cuh:24): one row of n,
+ * y = x * (1 / sqrtf(mean(x^2) + eps)) * w, fp32 accumulation. */
+int ds4hip_rms_norm_f32(const float *x, const float *w, float *y, int n, float eps, void *stream);
+
+/* Replaces ds4cuda::launch_rms_norm_batch_f32 (cuda/norm.cuh:40): n_rows rows
+ * of n_per_row, each normalized on its own; weight_dim 0 (unit gain, w may be
+ * NULL), n_per_row (w shared) or n_rows * n_per_row (a weight row each). */
+int ds4hip_rms_norm_batch_f32(const float *x, const float *w, int weight_dim, float *y, int n_rows,
+                              int n_per_row, float eps, void *stream);
+
+/* Workspace bytes of ds4hip_attn_qkv_decode_f32. */
+size_t ds4hip_attn_qkv_decode_workspace_bytes(void);
+
+/* The decode Q / KV producer of one layer, Steps 3-10 of
+ * cuda/forward_layer.cu:827-913 in one call (six launches, no allocation):
+ *   q_lora      = Q8_0 matvec(w_q_a [1024 x 4096], attn_norm [4096])
+ *   q_lora_norm = RMSNorm(q_lora, w_q_a_norm [1024])          -> q_lora_norm
+ *   kv_raw      = Q8_0 matvec(w_kv_a [512 x 4096], attn_norm)
+ *   kv_rope     = tail RoPE(RMSNorm(kv_raw, w_kv_a_norm [512]), pos, il) -> kv_rope
+ *   q_raw       = Q8_0 matvec(w_q_b [32768 x 1024], q_lora_norm)
+ *   q_cur       = tail RoPE(per-head RMSNorm(q_raw) [64 x 512], pos, il) -> q_cur
+ * with eps 1e-6, weights as block_q8_0 rows. kv_rope is what
+ * ds4hip_session_push_raw / ds4hip_fp8_kv_quantize_append take (Step 11) and
+ * q_lora_norm is the indexer query's input. */
+int ds4hip_attn_qkv_decode_f32(const float *attn_norm, const void *w_q_a, const float *w_q_a_norm,
+                               const void *w_kv_a, const float *w_kv_a_norm, const void *w_q_b,
+                               int pos, int il, float *q_lora_norm, float *q_cur, float *kv_rope,
+                               void *workspace, size_t workspace_bytes, void *stream);
+
 /* Workspace bytes of ds4hip_mul_mm_bf16_f32 / ds4hip_mul_mm_f32_f32 for this
  * shape (0 when one column group covers every column). */
 size_t ds4hip_mul_mm_workspace_bytes(int n_rows, int n_cols, int n_batch);

@@ -208,6 +208,20 @@ inline void launch_mul_mv_q8_0_q8_0_f32_prealloc(const block_q8_0 *W_dev,
                                                        stream));
 }
 
+/* cuda/norm.cuh:24 */
+inline void launch_rms_norm_f32(const float *x, const float *w, float *y, int n, float eps,
+                                hipStream_t stream = 0) {
+    ds4hip_report("launch_rms_norm_f32", ds4hip_rms_norm_f32(x, w, y, n, eps, stream));
+}
+
+/* cuda/norm.cuh:40 */
+inline void launch_rms_norm_batch_f32(const float *x, const float *w, int weight_dim, float *y,
+                                      int n_rows, int n_per_row, float eps,
+                                      hipStream_t stream = 0) {
+    ds4hip_report("launch_rms_norm_batch_f32",
+                  ds4hip_rms_norm_batch_f32(x, w, weight_dim, y, n_rows, n_per_row, eps, stream));
+}
+
 /* cuda/rope.cuh:51 */
 inline void launch_tail_rope_yarn_f32(const float *x_in, float *x_out, int n_heads, int head_dim,
                                       int n_rot, int pos, int il, hipStream_t stream = 0) {

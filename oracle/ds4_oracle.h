@@ -120,6 +120,14 @@ void orc_q8_matvec(const uint8_t *W, const float *x, float *y, int n_rows, int n
 // y = W x with W bf16 [n_rows][n_cols], fp64 accumulate.
 void orc_bf16_matvec(const uint16_t *W, const float *x, float *y, int n_rows, int n_cols);
 
+// ---- RMSNorm (cuda/norm.cu:4-7, cuda/norm.cuh:26-45) ------------------------
+// ss = sum x^2 in fp64, scale = 1 / sqrtf((float)(ss / n) + eps),
+// y = x * scale * w; w NULL is unit gain.
+void orc_rms_norm_f32(const float *x, const float *w, float *y, int n, float eps);
+// weight_dim: 0 (unit gain), n_per_row (shared row), n_rows * n_per_row (per row).
+void orc_rms_norm_batch_f32(const float *x, const float *w, int weight_dim, float *y,
+                            int n_rows, int n_per_row, float eps);
+
 // ---- compressor decode step (cuda/compressor.cu:64-349) ------------------
 // State layout and semantics exactly as the reference. Returns 1 on emit.
 int orc_compressor_step(int is_attn, const float *x, const uint16_t *w_kv,

@@ -272,3 +272,24 @@ static int compressor_after_projection(int is_attn, const float *kv, const float
     }
     return 1;
 }
+
+// ---- RMSNorm (cuda/norm.cu:4-7, the ds4.c rms_norm_weight spec the device
+// kernels are checked against): ss in fp64, scale = 1 / sqrtf((float)(ss / n)
+// + eps), y = x * scale * w (w NULL: unit gain).
+extern "C" void orc_rms_norm_f32(const float *x, const float *w, float *y, int n, float eps) {
+    double ss = 0.0;
+    for (int i = 0; i < n; ++i) ss += (double)x[i] * (double)x[i];
+    const float scale = 1.0f / std::sqrt((float)(ss / (double)n) + eps);
+    for (int i = 0; i < n; ++i) y[i] = w ? x[i] * scale * w[i] : x[i] * scale;
+}
+
+// Per-row form (cuda/norm.cuh:26-45): weight_dim 0 = unit gain, n_per_row =
+// one weight row shared by all rows, n_rows * n_per_row = a weight row each.
+extern "C" void orc_rms_norm_batch_f32(const float *x, const float *w, int weight_dim, float *y,
+                                       int n_rows, int n_per_row, float eps) {
+    for (int r = 0; r < n_rows; ++r) {
+        const float *wr = weight_dim == 0 ? nullptr
+                          : weight_dim == n_per_row ? w : w + (size_t)r * n_per_row;
+        orc_rms_norm_f32(x + (size_t)r * n_per_row, wr, y + (size_t)r * n_per_row, n_per_row, eps);
+    }
+}

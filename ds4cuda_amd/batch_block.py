@@ -176,3 +176,22 @@ class BatchedAttentionBlock:
         ops.mul_mm_bf16_f32(w["w_out"], self.out, self.y, self.out_dim, N_HEAD * HEAD_DIM, B,
                             workspace=self.mm_ws, stream=stream)
         return self.y
+
+    def capture(self, pos, x, kv_cur, q, q_idx, w_idx, sinks):
+        """Records one step() with these arguments into a HIP graph
+        (torch.cuda.CUDAGraph) and returns it; graph.replay() runs the step
+        again on the same buffers with one launch of the graph instead of the
+        step's 13 kernel launches. Nothing in step() allocates, synchronizes
+        the host or writes memory with hipMemsetAsync, so the graph holds
+        kernel nodes only; the host-side plan for pos is built before the
+        capture. Each replay advances the block's state as an eager step()
+        would (compressor states, appended rows)."""
+        self.plan(pos)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(g, stream=side):
+                self.step(pos, x, kv_cur, q, q_idx, w_idx, sinks, stream=side)
+        torch.cuda.current_stream().wait_stream(side)
+        return g

@@ -204,3 +204,39 @@ def test_sparse_decode_full_size(gpu):
     close(host(out)[0], ref, 2e-3)
     err = np.abs(host(out)[0] - ref).max() / np.sqrt(np.mean(ref.astype(np.float64) ** 2))
     print(f"sparse decode 131072 -> 2048: positions bit-exact, out err/RMS {err:.2e}")
+
+
+def test_batched_block_graph_replay(gpu):
+    """The captured step replays like the eager step: from the same saved
+    state, replay k equals eager step k bit for bit (k = 1..3, with emits),
+    with eager work and host synchronization between the replays."""
+    nb = 4
+    ctx = np.array([700, 1301, 2046, 4099])
+    pos = (ctx - 1).astype(np.int64)   # sequence 2 emits on its first step
+    w = make_weights(gpu)
+    blk = BatchedAttentionBlock(w, nb, int(pos.max()) + 1, device=gpu)
+    for b in range(nb):
+        n = int(pos[b]) // 4
+        blk.load_history(b, torch.from_numpy(synth.kv_rows(81, b, n)).to(gpu),
+                         torch.from_numpy(synth.kv_rows(82, b, SWA)).to(gpu),
+                         np.arange(pos[b] - SWA + 1, pos[b] + 1),
+                         torch.from_numpy(synth.normal(83, b, n * 128).reshape(n, 128)).to(gpu))
+    g = lambda s, shape: torch.from_numpy(synth.normal(84, s, int(np.prod(shape))).reshape(shape)).to(gpu)
+    x, kv_cur = g(1, (nb, IN)), g(2, (nb, 512))
+    q = g(3, (nb, 64, 512)).to(torch.bfloat16)
+    q_idx, w_idx, sinks = g(4, (nb, 64, 128)), g(5, (nb, 64)) / float(np.sqrt(128 * 64)), g(6, (nb, 64))
+    state = (blk.st_kv, blk.st_sc, blk.sti_kv, blk.sti_sc)
+    saved = [s.clone() for s in state]
+    eager = []
+    for _ in range(3):
+        eager.append(blk.step(pos, x, kv_cur, q, q_idx, w_idx, sinks).clone())
+    torch.cuda.synchronize()
+    assert not torch.equal(eager[0], eager[1])   # the state moved between the steps
+    graph = blk.capture(pos, x, kv_cur, q, q_idx, w_idx, sinks)
+    for s, v in zip(state, saved):
+        s.copy_(v)
+    for k in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(blk.y, eager[k]), k
+        _ = (blk.y * 2).sum().item()   # eager work between replays

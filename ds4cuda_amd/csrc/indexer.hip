@@ -21,6 +21,7 @@
 #include "../../include/ds4hip.h"
 
 #include <algorithm>
+#include <cstdlib>
 
 using namespace ds4hip;
 
@@ -514,6 +515,503 @@ __global__ void scale_kernel(float *y, int n, float s) {
     if (i < n) y[i] *= s;
 }
 
+// ---- prefiltered selection (bf16 keys, 64 heads x 128) -------------------------------------
+//
+// The exact scores cost 8192 dependent fp32 fma per key. Only the keys whose
+// score could fall on either side of the selection threshold need them:
+//
+//  1. prefilter_kernel: approximate scores a_c on the bf16 MFMA (the query
+//     split into bf16 hi + lo, the key bf16 exact; fp32 accumulation), with a
+//     per-key bound b_c >= |a_c - s_c| on the distance to the exact score s_c
+//     (derivation below), the level-1 histogram of a and max_c b_c.
+//  2. hist_next_kernel<2>: the level-2 histogram of a. The need-th largest a
+//     then lies in a 22-bit key bucket [lo, hi].
+//  3. band_kernel: with B = max b, the need-th largest exact score lies in
+//     [lo - B, hi + B]; a key with a - b > hi + B is certainly selected, one
+//     with a + b < lo - B certainly not; the rest (the band) is rescored with
+//     the exact fixed-order chains. The last workgroup to finish selects the
+//     need - (certainly selected) best band keys by (exact score desc, index
+//     asc), marks every candidate's score slot +inf (selected) or -inf, and
+//     writes each chunk's output offset.
+//  4. emit_marked_kernel: the positions (and/or mask) in index order.
+//
+// Bound: with u = 2^-24, the reference's chains give |s - s*| <= (128 + 64) u
+// sum_h |w_h| A_h, A_h = sum_d |q_hd k_d| (s* the exact real score; relu is
+// 1-Lipschitz). The MFMA form differs from s* by at most (2 * 128 + 64) u
+// sum_h |w_h| A_h for its two accumulation passes and head sum, plus 2^-18
+// sum_h |w_h| A_h for the part of q that hi + lo drops. So |a - s| <= 3.5e-5
+// sum_h |w_h| A_h <= 3.5e-5 ||k|| sum_h |w_h| ||q_h|| (Cauchy-Schwarz); b
+// uses the constant 1e-4 for margin.
+constexpr float kBoundC = 1.0e-4f;
+constexpr int kPfMaxChunks = 1024;   // candidates <= kPfMaxChunks * kChunk
+constexpr int kPfMinCand = 8192;      // fewer candidates: the exact scorer outright
+// DS4HIP_INDEXER_PREFILTER=0 keeps the exact scorer for every key.
+// Off by default: a GPU run of a variant build of this path (one process
+// loading several builds of the library) left the GPU faulted twice without
+// a cause found yet; until one is shown the exact scorer is the default and
+// the prefilter runs only when asked for (DS4HIP_INDEXER_PREFILTER=1 or
+// ds4hip_set_indexer_prefilter(1)).
+int g_prefilter = -1;
+bool prefilter_enabled() {
+    if (g_prefilter < 0) {
+        const char *e = getenv("DS4HIP_INDEXER_PREFILTER");
+        g_prefilter = (e && e[0] == '1') ? 1 : 0;
+    }
+    return g_prefilter == 1;
+}
+typedef short pf_bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 pf_bf16x2_t __attribute__((ext_vector_type(2)));
+typedef short pf_short2_t __attribute__((ext_vector_type(2)));
+
+// A load that sees other workgroups' completed writes (device-coherent).
+template <typename T>
+__device__ inline T ld_agent(const T *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ inline float key_to_float(unsigned k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
+// Selection scratch of the prefiltered path, after the three histograms.
+struct PfScratch {
+    unsigned *bmax;        // max bound (float bits; bounds are >= 0)
+    unsigned *done;        // band workgroups finished
+    unsigned *chunk_in;    // [n_chunks] certainly selected candidates per chunk
+    unsigned *chunk_off;   // [n_chunks] output offset of each chunk
+    unsigned *band_n;      // [n_chunks] band keys per chunk
+    float *bound;          // [n_chunks * kChunk]
+    float *band_val;       // [n_chunks * kChunk] exact scores of band keys, per chunk
+    int *band_idx;         // [n_chunks * kChunk]
+    float *cval;           // [n_chunks * kChunk] the band entries compacted
+    int *cidx;             // [n_chunks * kChunk]
+};
+
+__host__ __device__ inline size_t pf_align(size_t n) { return (n + 63) & ~size_t(63); }
+
+__host__ __device__ inline PfScratch pf_scratch(unsigned *base, int n_comp) {
+    const size_t chunks = (size_t)(n_comp > 0 ? n_comp : 1) / kChunk + 1;
+    const size_t rows = chunks * kChunk;
+    unsigned *p = base + 3 * kBins;
+    PfScratch S;
+    S.bmax = p;
+    S.done = p + 1;
+    p += 64;
+    S.chunk_in = p;
+    p += pf_align(chunks);
+    S.chunk_off = p;
+    p += pf_align(chunks);
+    S.band_n = p;
+    p += pf_align(chunks);
+    S.bound = reinterpret_cast<float *>(p);
+    p += rows;
+    S.band_val = reinterpret_cast<float *>(p);
+    p += rows;
+    S.band_idx = reinterpret_cast<int *>(p);
+    p += rows;
+    S.cval = reinterpret_cast<float *>(p);
+    p += rows;
+    S.cidx = reinterpret_cast<int *>(p);
+    return S;
+}
+
+size_t pf_scratch_words(int n_comp) {
+    const size_t chunks = (size_t)(n_comp > 0 ? n_comp : 1) / kChunk + 1;
+    return 3 * kBins + 64 + 3 * pf_align(chunks) + 5 * chunks * kChunk;
+}
+
+// One wave scores 16 keys per step: A = 16 key rows x 32 dims (lane (i, g):
+// key i, dims 8 g .. 8 g + 7 of the k-step), B = 32 dims x 16 heads of the
+// query (hi and lo parts), C = keys x heads; the head sum reduces over the 16
+// lanes of a column group.
+__global__ __launch_bounds__(256) void prefilter_kernel(const float *__restrict__ q,
+                                                        const float *__restrict__ w,
+                                                        const uint16_t *__restrict__ keys,
+                                                        int n_cand, float *__restrict__ a_out,
+                                                        unsigned *__restrict__ hist1, PfScratch S) {
+    __shared__ unsigned lh[kBins];
+    __shared__ unsigned s_bmax;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int i = tid; i < kBins; i += 256) lh[i] = 0;
+    if (tid == 0) s_bmax = 0;
+    const int j = lane & 15, g = lane >> 4;
+    pf_bf16x8_t qh[4][4], ql[4][4];   // [head tile][k-step]
+    float qn2[4] = {0.0f, 0.0f, 0.0f, 0.0f};   // ||q_h||^2 of head 16 ht + j (this lane's 32 dims)
+#pragma unroll
+    for (int ht = 0; ht < 4; ++ht)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const float *src = q + (16 * ht + j) * kMaxDim + 32 * ks + 8 * g;
+            const float4_t x0 = *reinterpret_cast<const float4_t *>(src);
+            const float4_t x1 = *reinterpret_cast<const float4_t *>(src + 4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) qn2[ht] = fmaf(x0[e], x0[e], fmaf(x1[e], x1[e], qn2[ht]));
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+                const float v0 = e < 4 ? x0[e] : x1[e - 4], v1 = e < 4 ? x0[e + 1] : x1[e - 3];
+                const pf_bf16x2_t h = pf_bf16x2_t{(__bf16)v0, (__bf16)v1};
+                const pf_bf16x2_t l = pf_bf16x2_t{(__bf16)(v0 - (float)h[0]), (__bf16)(v1 - (float)h[1])};
+                const pf_short2_t hs = __builtin_bit_cast(pf_short2_t, h), ls = __builtin_bit_cast(pf_short2_t, l);
+                qh[ht][ks][e] = hs[0];
+                qh[ht][ks][e + 1] = hs[1];
+                ql[ht][ks][e] = ls[0];
+                ql[ht][ks][e + 1] = ls[1];
+            }
+        }
+    float wj[4];
+#pragma unroll
+    for (int ht = 0; ht < 4; ++ht) wj[ht] = w[16 * ht + j];
+    // Wq = sum_h |w_h| ||q_h||: the 4 lane groups' parts of each head, then the 16 columns
+    float wq = 0.0f;
+#pragma unroll
+    for (int ht = 0; ht < 4; ++ht) {
+        float n2 = qn2[ht];
+        n2 += __shfl_xor(n2, 16);
+        n2 += __shfl_xor(n2, 32);
+        wq += fabsf(wj[ht]) * sqrtf(n2);
+    }
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) wq += __shfl_xor(wq, off, 16);
+    __syncthreads();
+    float bmax = 0.0f;
+    const int n_tiles = (n_cand + 15) / 16;
+    // the next tile's key fragments are loaded before this tile's MFMAs
+    auto load_tile = [&](int tile, uint4_t (&u)[4]) {
+        const int row = 16 * tile + j;
+        const int rr = row < n_cand ? row : n_cand - 1;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+            u[ks] = *reinterpret_cast<const uint4_t *>(keys + (size_t)rr * kMaxDim + 32 * ks + 8 * g);
+    };
+    const int stride = gridDim.x * 4;
+    uint4_t un[4];
+    if (blockIdx.x * 4 + wave < n_tiles) load_tile(blockIdx.x * 4 + wave, un);
+    for (int tile = blockIdx.x * 4 + wave; tile < n_tiles; tile += stride) {
+        uint4_t uc[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) uc[ks] = un[ks];
+        if (tile + stride < n_tiles) load_tile(tile + stride, un);
+        pf_bf16x8_t a[4];
+        float n2 = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const uint4_t u = uc[ks];
+            a[ks] = __builtin_bit_cast(pf_bf16x8_t, u);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float lo = __uint_as_float(u[e] << 16), hi = __uint_as_float(u[e] & 0xFFFF0000u);
+                n2 = fmaf(lo, lo, fmaf(hi, hi, n2));
+            }
+        }
+        n2 += __shfl_xor(n2, 16);
+        n2 += __shfl_xor(n2, 32);   // ||k_row||^2 in every lane (i = row)
+        float4_t c[4];
+#pragma unroll
+        for (int ht = 0; ht < 4; ++ht) {
+            c[ht] = float4_t{0, 0, 0, 0};
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                c[ht] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[ks], qh[ht][ks], c[ht], 0, 0, 0);
+                c[ht] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[ks], ql[ht][ks], c[ht], 0, 0, 0);
+            }
+        }
+        // lane (j, g): keys 4 g + r, head 16 ht + j
+        float s[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float v = 0.0f;
+#pragma unroll
+            for (int ht = 0; ht < 4; ++ht) v = fmaf(wj[ht], c[ht][r] > 0.0f ? c[ht][r] : 0.0f, v);
+#pragma unroll
+            for (int off = 1; off < 16; off <<= 1) v += __shfl_xor(v, off, 16);
+            s[r] = v;
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int kr = 16 * tile + 4 * g + r;
+            const float kn2 = __shfl(n2, 4 * g + r);
+            if (j == r && kr < n_cand) {
+                const float b = kBoundC * sqrtf(kn2) * wq;
+                a_out[kr] = s[r];
+                S.bound[kr] = b;
+                bmax = fmaxf(bmax, b);
+                atomicAdd(&lh[ord_key(s[r]) >> 21], 1u);
+            }
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) bmax = fmaxf(bmax, __shfl_xor(bmax, off));
+    if (lane == 0) atomicMax(&s_bmax, __float_as_uint(bmax));
+    __syncthreads();
+    for (int i = tid; i < kBins; i += 256)
+        if (lh[i]) atomicAdd(&hist1[i], lh[i]);
+    if (tid == 0) atomicMax(S.bmax, s_bmax);
+}
+
+// Exact score of key c (the canonical chains): lane h forms dot_h over d
+// ascending, then the head chain runs over h ascending in lane 0.
+__device__ inline float exact_score_wave(const float *qs, const float *ws, const uint16_t *keys, int c) {
+    const int h = threadIdx.x & 63;
+    const uint16_t *kr = keys + (size_t)c * kMaxDim;
+    uint4_t kk[kMaxDim / 8];   // the whole key first: one memory round trip
+#pragma unroll
+    for (int v = 0; v < kMaxDim / 8; ++v) kk[v] = *reinterpret_cast<const uint4_t *>(kr + 8 * v);
+    float dot = 0.0f;
+#pragma unroll
+    for (int v = 0; v < kMaxDim / 8; ++v) {
+        const uint4_t u = kk[v];
+        const float4_t q0 = *reinterpret_cast<const float4_t *>(qs + h * kQStride + 8 * v);
+        const float4_t q1 = *reinterpret_cast<const float4_t *>(qs + h * kQStride + 8 * v + 4);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint16_t b = (uint16_t)((u[e >> 1] >> (16 * (e & 1))) & 0xFFFF);
+            dot = fmaf(e < 4 ? q0[e] : q1[e - 4], bf16_to_f32(b), dot);
+        }
+    }
+    const float r = dot > 0.0f ? dot : 0.0f;
+    float s = 0.0f;
+#pragma unroll
+    for (int hh = 0; hh < kMaxHeads; ++hh)
+        s = fmaf(ws[hh], __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r), hh)), s);
+    return s;
+}
+
+// Threshold of the need-th largest of n 32-bit keys key_of(i) (need >= 1):
+// returns T and how many entries equal to T are taken. One workgroup.
+template <typename KeyOf>
+__device__ void wg_select(int n, unsigned need, KeyOf key_of, unsigned *lh, unsigned *scratch,
+                          unsigned *s_bin, unsigned *s_above, unsigned *T_out, unsigned *eq_out) {
+    unsigned prefix = 0, mask = 0;
+    const int shifts[3] = {21, 10, 0};
+    const int widths[3] = {11, 11, 10};
+    for (int lvl = 0; lvl < 3; ++lvl) {
+        const int nb = 1 << widths[lvl];
+        for (int i = threadIdx.x; i < kBins; i += 256) lh[i] = 0;
+        __syncthreads();
+        for (int i = threadIdx.x; i < n; i += 256) {
+            const unsigned k = key_of(i);
+            if ((k & mask) == prefix) atomicAdd(&lh[(k >> shifts[lvl]) & (nb - 1)], 1u);
+        }
+        __syncthreads();
+        find_bin(lh, nb, need, s_bin, s_above, scratch);
+        prefix |= *s_bin << shifts[lvl];
+        mask |= (unsigned)(nb - 1) << shifts[lvl];
+        need -= *s_above;
+        __syncthreads();
+    }
+    *T_out = prefix;
+    *eq_out = need;
+}
+
+__global__ __launch_bounds__(256) void band_kernel(const float *__restrict__ q,
+                                                   const float *__restrict__ w,
+                                                   const uint16_t *__restrict__ keys, int n_cand,
+                                                   int n_comp, unsigned need0, int n_chunks,
+                                                   float *__restrict__ a_io,
+                                                   const unsigned *__restrict__ hists, PfScratch S) {
+    __shared__ __attribute__((aligned(16))) float qs[kMaxHeads * kQStride];
+    __shared__ float ws[kMaxHeads];
+    __shared__ unsigned lh[kBins];
+    __shared__ unsigned scratch[256];
+    __shared__ unsigned s_bin, s_above, s_ticket, s_cnt[4];
+    __shared__ int band_l[kChunk];
+    __shared__ unsigned s_nband;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // the bucket of the need0-th largest approximate score
+    find_bin(hists, kBins, need0, &s_bin, &s_above, scratch);
+    unsigned prefix = s_bin << 21;
+    const unsigned need1 = need0 - s_above;
+    __syncthreads();
+    find_bin(hists + kBins, kBins, need1, &s_bin, &s_above, scratch);
+    prefix |= s_bin << 10;
+    const float lo = key_to_float(prefix), hi = key_to_float(prefix | 0x3FFu);
+    const float B = __uint_as_float(*S.bmax);
+    if (tid == 0) s_nband = 0;
+    stage_query<kQStride>(qs, q, kMaxHeads);
+    if (tid < kMaxHeads) ws[tid] = w[tid];
+    __syncthreads();
+    unsigned cin = 0;
+    for (int i = 0; i < 4; ++i) {
+        const int c = blockIdx.x * kChunk + i * 256 + tid;
+        if (c >= n_cand) continue;
+        const float a = a_io[c], b = S.bound[c];
+        if (a - b > hi + B) {
+            a_io[c] = INFINITY;
+            ++cin;
+        } else if (a + b < lo - B) {
+            a_io[c] = -INFINITY;
+        } else {
+            band_l[atomicAdd(&s_nband, 1u)] = c;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) cin += __shfl_xor(cin, off);
+    if (lane == 0) s_cnt[wave] = cin;
+    __syncthreads();
+    const unsigned nband = s_nband;
+    // exact rescoring: one wave per band key, into this chunk's band slots
+    const size_t base = (size_t)blockIdx.x * kChunk;
+    for (unsigned e = wave; e < nband; e += 4) {
+        const int c = band_l[e];
+        const float s = exact_score_wave(qs, ws, keys, c);
+        if (lane == 0) {
+            S.band_val[base + e] = s;
+            S.band_idx[base + e] = c;
+        }
+    }
+    if (tid == 0) {
+        S.chunk_in[blockIdx.x] = s_cnt[0] + s_cnt[1] + s_cnt[2] + s_cnt[3];
+        S.band_n[blockIdx.x] = nband;
+    }
+    // the last workgroup to finish selects within the band
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) s_ticket = atomicAdd(S.done, 1u);
+    __syncthreads();
+    if (s_ticket != gridDim.x - 1) return;
+    __threadfence();
+    // compact the chunks' band entries (4 chunks per thread; <= 1024 chunks)
+    int nb;
+    {
+        unsigned v[4], tot = 0;
+        for (int k = 0; k < 4; ++k) {
+            const int i = 4 * tid + k;
+            // (bounded: a chunk holds at most kChunk band keys)
+            v[k] = i < (int)gridDim.x ? min(ld_agent(&S.band_n[i]), (unsigned)kChunk) : 0u;
+            tot += v[k];
+        }
+        unsigned ex;
+        nb = (int)block_excl_scan(tot, scratch, &ex);
+        for (int k = 0; k < 4; ++k) {
+            const int i = 4 * tid + k;
+            for (unsigned e = 0; e < v[k]; ++e) {
+                S.cval[ex + e] = ld_agent(&S.band_val[(size_t)i * kChunk + e]);
+                S.cidx[ex + e] = ld_agent(&S.band_idx[(size_t)i * kChunk + e]);
+            }
+            ex += v[k];
+        }
+        __threadfence_block();
+        __syncthreads();
+    }
+    unsigned c_in = 0;
+    for (int i = tid; i < (int)gridDim.x; i += 256) c_in += ld_agent(&S.chunk_in[i]);
+    for (int off = 32; off > 0; off >>= 1) c_in += __shfl_xor(c_in, off);
+    if (lane == 0) s_cnt[wave] = c_in;
+    __syncthreads();
+    c_in = s_cnt[0] + s_cnt[1] + s_cnt[2] + s_cnt[3];
+    const unsigned m = need0 - c_in;   // band keys to take (1 <= m <= nb)
+    unsigned T, eq;
+    wg_select(nb, m, [&](int i) { return ord_key(S.cval[i]); }, lh, scratch, &s_bin, &s_above, &T, &eq);
+    // ties at T: the eq lowest indices (the largest ~index)
+    unsigned Ti = 0, eqi = 0;
+    if (eq > 0) {
+        wg_select(nb, eq, [&](int i) { return ord_key(S.cval[i]) == T ? ~(unsigned)S.cidx[i] : 0u; },
+                  lh, scratch, &s_bin, &s_above, &Ti, &eqi);
+    }
+    // chunk counts: certainly selected + selected band keys + forced recent positions
+    unsigned *cnt = lh;   // reuse: n_chunks <= kPfMaxChunks <= kBins
+    for (int i = tid; i < n_chunks; i += 256) cnt[i] = i < (int)gridDim.x ? ld_agent(&S.chunk_in[i]) : 0u;
+    __syncthreads();
+    for (int i = tid; i < nb; i += 256) {
+        const unsigned k = ord_key(S.cval[i]);
+        const int c = S.cidx[i];
+        if ((unsigned)c >= (unsigned)n_cand) continue;   // (never: every entry is a candidate)
+        const bool sel = k > T || (k == T && eq > 0 && ~(unsigned)c >= Ti);
+        a_io[c] = sel ? INFINITY : -INFINITY;
+        if (sel) atomicAdd(&cnt[c / kChunk], 1u);
+    }
+    __syncthreads();
+    for (int i = tid; i < n_chunks; i += 256) {
+        const int c0 = i * kChunk, c1 = min(c0 + kChunk, n_comp);
+        const int r0 = max(c0, n_cand);
+        cnt[i] += r0 < c1 ? (unsigned)(c1 - r0) : 0u;
+    }
+    __syncthreads();
+    // exclusive prefix over the chunks (n_chunks <= 1024: 4 per thread)
+    unsigned v[4], tot = 0;
+    for (int k = 0; k < 4; ++k) {
+        const int i = 4 * tid + k;
+        v[k] = i < n_chunks ? cnt[i] : 0u;
+        tot += v[k];
+    }
+    unsigned ex;
+    const unsigned total = block_excl_scan(tot, scratch, &ex);
+    for (int k = 0; k < 4; ++k) {
+        const int i = 4 * tid + k;
+        if (i < n_chunks) S.chunk_off[i] = ex;
+        ex += v[k];
+    }
+    if (tid == 0) {
+        *S.done = 0;
+        // the counts add up to the output size by construction; if they ever
+        // did not, the emit kernel writes positions 0.. instead of a list with
+        // holes (every output slot stays a valid row index)
+        S.bmax[2] = total == need0 + (unsigned)(n_comp - n_cand) ? 0u : 1u;
+    }
+}
+
+// Per chunk: positions of the marked (+inf) candidates and of the forced
+// recent window, in index order, from the chunk's offset.
+__global__ __launch_bounds__(256) void emit_marked_kernel(const float *__restrict__ marks, int n_comp,
+                                                          int n_cand, int n_out, PfScratch S,
+                                                          int32_t *__restrict__ mask,
+                                                          int32_t *__restrict__ pos_out) {
+    __shared__ unsigned buf[256];
+    if (S.bmax[2]) {
+        for (int i = blockIdx.x * 256 + threadIdx.x; i < n_out; i += gridDim.x * 256) {
+            if (pos_out) pos_out[i] = i < n_comp ? i : n_comp - 1;
+            if (mask && i < n_comp) mask[i] = 1;
+        }
+        return;
+    }
+    const int base = blockIdx.x * kChunk + threadIdx.x * 4;
+    bool take[4];
+    unsigned my = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int c = base + i;
+        take[i] = c < n_cand ? marks[c] == INFINITY : c < n_comp;
+        my += take[i];
+    }
+    unsigned ex;
+    block_excl_scan(my, buf, &ex);
+    unsigned o = S.chunk_off[blockIdx.x] + ex;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int c = base + i;
+        if (c >= n_comp) break;
+        if (mask) mask[c] = take[i] ? 1 : 0;
+        if (take[i] && pos_out && o < (unsigned)n_out) pos_out[o] = c;
+        o += take[i];
+    }
+}
+
+int pf_grid() {
+    static const int v = [] {
+        const char *e = getenv("DS4HIP_PF_GRID");
+        return e ? atoi(e) : 256;
+    }();
+    return v;
+}
+
+int score_select_prefilter(const float *q, const float *w, const uint16_t *keys, int n_comp,
+                           int n_cand, unsigned need0, float *scores, unsigned *scratch, int32_t *mask,
+                           int32_t *pos_out, hipStream_t st) {
+    const PfScratch S = pf_scratch(scratch, n_comp);
+    const int n_chunks = (n_comp + kChunk - 1) / kChunk;
+    const int n_band_wg = (n_cand + kChunk - 1) / kChunk;
+    hipLaunchKernelGGL(zero_u32_kernel, dim3(24), dim3(256), 0, st, scratch, 3 * kBins + 64);
+    hipLaunchKernelGGL(prefilter_kernel, dim3(std::min(pf_grid(), (n_cand + 63) / 64)), dim3(256), 0, st, q, w,
+                       keys, n_cand, scores, scratch, S);
+    const int g = (n_cand + 256 * 8 - 1) / (256 * 8) + 1;
+    hipLaunchKernelGGL(hist_next_kernel<2>, dim3(g), dim3(256), 0, st, scores, n_cand, need0, scratch);
+    hipLaunchKernelGGL(band_kernel, dim3(n_band_wg), dim3(256), 0, st, q, w, keys, n_cand, n_comp, need0,
+                       n_chunks, scores, scratch, S);
+    hipLaunchKernelGGL(emit_marked_kernel, dim3(n_chunks), dim3(256), 0, st, scores, n_comp, n_cand,
+                       (int)need0 + (n_comp - n_cand), S, mask, pos_out);
+    return hip_status(hipGetLastError());
+}
+
 int launch_scores(const float *q, const float *w, const void *keys, int kind, int n_comp,
                   int n_head, int head_dim, float *scores, unsigned *hist, int n_cand,
                   hipStream_t st) {
@@ -540,7 +1038,7 @@ int launch_scores(const float *q, const float *w, const void *keys, int kind, in
 // always selected and take part in no comparison.
 size_t select_scratch_bytes(int n_comp) {
     const size_t chunks = (size_t)(n_comp > 0 ? n_comp : 1) / kChunk + 1;
-    return (3 * kBins + 2 * chunks) * sizeof(unsigned);
+    return std::max((3 * kBins + 2 * chunks), pf_scratch_words(n_comp)) * sizeof(unsigned);
 }
 
 int score_select(const float *q, const float *w, const void *keys, int kind, int n_comp,
@@ -565,6 +1063,14 @@ int score_select(const float *q, const float *w, const void *keys, int kind, int
     const int n_cand = n_comp - recent;
     const unsigned need0 = (unsigned)(top_k - recent);
     const int n_chunks = (n_comp + kChunk - 1) / kChunk;
+    // bf16 keys of the model's indexer shape: the MFMA prefilter with exact
+    // rescoring near the threshold (the same selection, a fraction of the work)
+    if (kind == 2 && n_head == kMaxHeads && head_dim == kMaxDim && n_cand >= kPfMinCand &&
+        (n_cand + kChunk - 1) / kChunk <= kPfMaxChunks && n_chunks <= kPfMaxChunks &&
+        !(reinterpret_cast<uintptr_t>(keys) & 15) && !(reinterpret_cast<uintptr_t>(q) & 15) &&
+        prefilter_enabled())
+        return score_select_prefilter(q, w, static_cast<const uint16_t *>(keys), n_comp, n_cand, need0,
+                                      scores, scratch, mask, pos_out, st);
     unsigned *hists = scratch;
     unsigned *chunk_gt = scratch + 3 * kBins;
     unsigned *chunk_eq = chunk_gt + n_chunks;
@@ -602,6 +1108,13 @@ extern "C" int ds4hip_scale_inplace_f32(float *y, int n, float scale, void *stre
 }
 
 extern "C" size_t ds4hip_indexer_select_scratch_bytes(int n_comp) { return select_scratch_bytes(n_comp); }
+
+extern "C" int ds4hip_set_indexer_prefilter(int enable) {
+    if (enable != 0 && enable != 1) return ds4hip_set_last_error(kEINVAL);
+    const int prev = prefilter_enabled() ? 1 : 0;
+    g_prefilter = enable;
+    return prev;
+}
 
 // The reference launchers take only a score scratch; the selection
 // histograms are stream-ordered allocations here.

@@ -1,0 +1,79 @@
+"""The indexer's MFMA prefilter (ds4hip_indexer_topk_positions over bf16
+keys, 64 heads x 128): the selected positions are those of the exact
+fixed-order scores (the oracle's orc_indexer_scores + orc_topk_positions) in
+cases built to stress the band around the threshold: every key equal (the
+band is every candidate, all ties), duplicated keys straddling the
+threshold, keys over a wide dynamic range, sizes that are not multiples of
+the tiles, and the smallest candidate count the prefilter takes. The exact
+path (prefilter off) must agree as well."""
+import ctypes as C
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from oracle import P
+from ds4cuda_amd import lib, ops, synth
+from test_gpu_ops import t
+
+
+def reference(qf, w, kb, top_k, recent):
+    n = kb.shape[0]
+    sc = np.zeros(n, np.float32)
+    O.lib().orc_indexer_scores(P(qf), P(w), P(np.ascontiguousarray(kb)), C.c_int(2), C.c_int(n),
+                               C.c_int(64), C.c_int(128), P(sc))
+    ref = np.zeros(min(top_k, n), np.int32)
+    O.lib().orc_topk_positions(P(sc), C.c_int(n), C.c_int(top_k), C.c_int(recent), P(ref))
+    return ref
+
+
+def run(gpu, qf, w, kb, top_k, recent, mode):
+    prev = lib().ds4hip_set_indexer_prefilter(mode)
+    try:
+        kt = t(np.ascontiguousarray(kb).view(np.int16), gpu).view(torch.bfloat16)
+        pos, _, _ = ops.indexer_topk_positions(t(qf, gpu), t(w, gpu), kt, top_k, recent)
+        torch.cuda.synchronize()
+        return pos.cpu().numpy()
+    finally:
+        lib().ds4hip_set_indexer_prefilter(prev)
+
+
+def inputs(seed, n):
+    qf = synth.bf16_bits_to_f32(synth.to_bf16_bits(synth.normal(seed, 1, 64 * 128))).reshape(64, 128)
+    w = synth.normal(seed, 2, 64) / np.float32(np.sqrt(128 * 64))
+    kb = synth.to_bf16_bits(synth.normal(seed, 3, n * 128)).reshape(n, 128)
+    return qf, w, kb
+
+
+CASES = {
+    "all_equal": (8192 + 300, 512, 64),
+    "dup_straddle": (20000, 2048, 128),
+    "wide_range": (33333, 1024, 0),
+    "ragged": (8192 + 64 + 17, 2000, 64),
+    "min_cand": (8192 + 128, 2048, 128),
+}
+
+
+@pytest.mark.gpu
+@pytest.mark.skip(reason="prefilter path disabled: a GPU fault seen in a run that exercised it "
+                         "is not explained yet (the exact path is the default)")
+@pytest.mark.parametrize("case", list(CASES))
+def test_prefilter_matches_exact_selection(gpu, case):
+    n, top_k, recent = CASES[case]
+    qf, w, kb = inputs(90 + len(case), n)
+    if case == "all_equal":
+        kb[:] = kb[3]
+    elif case == "dup_straddle":
+        ref0 = reference(qf, w, kb, top_k, recent)
+        edge = int(ref0[top_k - recent - 1])   # the weakest selected candidate
+        kb[7000:7300] = kb[edge]               # 300 copies of it: ties across the threshold
+    elif case == "wide_range":
+        scale = np.where(np.arange(n) % 3 == 0, 64.0, 1.0 / 32.0).astype(np.float32)
+        kb = synth.to_bf16_bits(synth.bf16_bits_to_f32(kb) * scale[:, None])
+    ref = reference(qf, w, kb, top_k, recent)
+    for mode in (1, 0):
+        got = run(gpu, qf, w, kb, top_k, recent, mode)
+        assert np.array_equal(got, ref), (case, mode)
+    if case == "all_equal":   # ties: the lowest indices, then the recent window
+        assert np.array_equal(ref, np.concatenate([np.arange(top_k - recent), np.arange(n - recent, n)]))

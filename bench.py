@@ -36,9 +36,15 @@ COPY_BYTES = 1 << 30                               # --copy-calibration: 1 GiB r
 # HBM bytes per launch of the cfg-2 partial kernel, measured with rocprofv3
 # (FETCH_SIZE + WRITE_SIZE, each scaled by what the counter reads for
 # `--copy-calibration`); the counter summary and its commands are in
-# profiles/decode_fp8_cfg2_traffic.md. Re-measure after a kernel change.
-TRAFFIC_BYTES_PER_LAUNCH = 882340981
-TRAFFIC_MEASURED_AT = "22db79c"                    # commit whose partial kernel was counted
+# profiles/decode_fp8_cfg2_traffic.md. They were counted for the
+# register-load kernel (decode_ws_kernel, DS4HIP_DECODE_KERNEL=ws); the
+# flat-stage kernel that runs by default has not been counted, so its line
+# reports traffic null. Re-measure after a kernel change.
+TRAFFIC_BYTES_PER_LAUNCH = {"ws": 882340981}
+TRAFFIC_MEASURED_AT = {"ws": "22db79c"}            # commit whose partial kernel was counted
+DECODE_KERNEL = "ws" if os.environ.get("DS4HIP_DECODE_KERNEL", "").startswith("w") else "flat"
+KERNEL_LABEL = {"ws": "decode_ws_kernel<0, false> (direct rows, register loads, one f16 P)",
+                "flat": "decode_flat_kernel<false> (direct rows, DMA-fed flat LDS stages, one f16 P)"}
 
 
 def bytes_per_layer():
@@ -395,9 +401,10 @@ def main():
                    "exact_p": {"ms_per_step": round(ms_exact, 4),
                                "value": round(step_bytes / (ms_exact * 1e-3) / 1e9, 2)}},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_BYTES_PER_LAUNCH,
-                     "traffic_measured_at": TRAFFIC_MEASURED_AT,
-                     "kernel": "decode_ws_kernel<0, false> (direct rows, one f16 P)",
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": TRAFFIC_BYTES_PER_LAUNCH.get(DECODE_KERNEL),
+                     "traffic_measured_at": TRAFFIC_MEASURED_AT.get(DECODE_KERNEL),
+                     "kernel": KERNEL_LABEL[DECODE_KERNEL],
                      "kernel_ms": round(k_ms, 4), "bytes_per_launch": step_bytes},
     }
     if not args.no_secondary:

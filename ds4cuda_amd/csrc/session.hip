@@ -130,13 +130,15 @@ Plan make_plan(int max_context) {
         rows += P.cap_comp[il] + P.cap_raw;
     }
     P.n_rows = rows;
+    // the layers' rows, then DS4HIP_CHUNK_MAX staging rows for a prefill chunk
+    const long long all_rows = rows + DS4HIP_CHUNK_MAX;
     size_t off = 0;
     P.off_codes = off;
-    off += align256((size_t)rows * DS4HIP_FP8_CODES);
+    off += align256((size_t)all_rows * DS4HIP_FP8_CODES);
     P.off_sexp = off;
-    off += align256((size_t)rows * DS4HIP_FP8_SEXP);
+    off += align256((size_t)all_rows * DS4HIP_FP8_SEXP);
     P.off_tail = off;
-    off += align256((size_t)rows * DS4HIP_FP8_TAIL * 2);
+    off += align256((size_t)all_rows * DS4HIP_FP8_TAIL * 2);
     P.off_lists = off;
     for (int il = 0; il < DS4HIP_N_LAYER; ++il) {
         P.list_off[il] = off;
@@ -561,4 +563,64 @@ extern "C" int ds4hip_session_load_from_disk(ds4hip_session_state *s_out, const 
     if (out_pos) *out_pos = s_out->pos;
     if (out_n_tokens) *out_n_tokens = s_out->n_tokens_processed;
     return 0;
+}
+
+// ---- row lists of a prefill chunk -----------------------------------------------------------
+namespace {
+struct ChunkTok {   // per token: compressed rows visible, and how many of them it attends
+    int n_comp[DS4HIP_CHUNK_MAX];
+    int n_sel[DS4HIP_CHUNK_MAX];
+};
+
+// One workgroup per token t (position p0 + t): the window rows still in the
+// ring (positions max(0, p0 + t - cap_raw + 1) .. p0 - 1, slot position %
+// cap_raw), the chunk's staged rows 0..t, then the token's compressed rows
+// (its selection sel[t], or all of them); entries relative to the layer's
+// row_base.
+__global__ __launch_bounds__(256) void chunk_rows_kernel(int32_t *__restrict__ lists, int stride, int p0,
+                                                         int cap_raw, int cap_comp, int stage_rel,
+                                                         ChunkTok T, const int32_t *__restrict__ sel,
+                                                         int sel_stride) {
+    const int t = blockIdx.x;
+    int32_t *out = lists + (size_t)t * stride;
+    const int first = max(0, p0 + t - cap_raw + 1);
+    const int n_ring = p0 > first ? p0 - first : 0;
+    const int n_stage = t + 1;
+    const int n_sel = T.n_sel[t];
+    const bool all = n_sel == T.n_comp[t];
+    for (int i = threadIdx.x; i < n_ring; i += 256) out[i] = cap_comp + (first + i) % cap_raw;
+    for (int i = threadIdx.x; i < n_stage; i += 256) out[n_ring + i] = stage_rel + i;
+    for (int i = threadIdx.x; i < n_sel; i += 256)
+        out[n_ring + n_stage + i] = all ? i : sel[(size_t)t * sel_stride + i];
+}
+}  // namespace
+
+extern "C" int ds4hip_session_chunk_rows(const ds4hip_session_state *s, int il, int p0, int n_tok,
+                                         const int *n_comp_tok, const int *n_sel_tok,
+                                         const int32_t *sel, int sel_stride, int32_t *lists,
+                                         int list_stride, long long *counts_out, void *stream) {
+    if (!layer_ok(s, il) || n_tok <= 0 || n_tok > DS4HIP_CHUNK_MAX || p0 < 0 || !n_comp_tok ||
+        !n_sel_tok || !lists || !counts_out || list_stride <= 0)
+        return ds4hip_set_last_error(kEINVAL);
+    const ds4hip_layer_state *L = &s->layers[il];
+    // the ring holds exactly the positions < p0 (one push per position)
+    if (L->n_raw != (p0 < L->cap_raw ? p0 : L->cap_raw) || L->raw_head != p0 % L->cap_raw)
+        return ds4hip_set_last_error(kEINVAL);
+    ChunkTok T;
+    for (int t = 0; t < n_tok; ++t) {
+        const int first = p0 + t - L->cap_raw + 1 > 0 ? p0 + t - L->cap_raw + 1 : 0;
+        const long long n_ring = p0 > first ? p0 - first : 0;
+        const bool all = n_sel_tok[t] == n_comp_tok[t];
+        if (n_comp_tok[t] < 0 || n_comp_tok[t] > L->cap_comp || n_sel_tok[t] < 0 ||
+            n_sel_tok[t] > n_comp_tok[t] || (!all && (!sel || n_sel_tok[t] > sel_stride)))
+            return ds4hip_set_last_error(kEINVAL);
+        counts_out[t] = n_ring + (t + 1) + n_sel_tok[t];
+        if (counts_out[t] > list_stride) return ds4hip_set_last_error(kEINVAL);
+        T.n_comp[t] = n_comp_tok[t];
+        T.n_sel[t] = n_sel_tok[t];
+    }
+    const long long stage_rel = s->n_cache_rows - L->row_base;
+    hipLaunchKernelGGL(chunk_rows_kernel, dim3(n_tok), dim3(256), 0, (hipStream_t)stream, lists, list_stride,
+                       p0, L->cap_raw, L->cap_comp, (int)stage_rel, T, sel, sel_stride);
+    return ds4hip_set_last_error(hip_status(hipGetLastError()));
 }

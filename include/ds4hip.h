@@ -128,6 +128,7 @@ int ds4hip_flash_attn_decode_fp8_workspace_size(const long long *n_rows_per_prob
  *   sinks  sinks + p*sinks_stride, [64] fp32
  *   out    out + p*out_stride, [64][512] fp32
  *   n_rows_per_prob  HOST array [n_prob] of row counts (n_prob <= 128)
+ *   row_base, row_idx, page_table  DEVICE arrays (the kernels read them)
  * Logical row r of problem p reads position pos = row_idx[p*row_idx_stride + r]
  * (or r when row_idx is NULL) and physical cache row
  *   page_table[p*page_table_stride + pos / page_rows] * page_rows + pos % page_rows

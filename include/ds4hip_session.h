@@ -25,6 +25,7 @@ extern "C" {
 #define DS4HIP_FP8_SEXP 8    /* scale exponents per cache row (7 used) */
 #define DS4HIP_FP8_TAIL 64   /* f16 tail elements per cache row */
 #define DS4HIP_ENOSPC (-28)
+#define DS4HIP_CHUNK_MAX 128 /* tokens per prefill chunk (staging rows in the arena) */
 
 /* ---- reference fp32 row layout --------------------------------------------------- */
 
@@ -82,6 +83,8 @@ typedef struct ds4hip_session_state {
     uint8_t *codes;  /* [n_cache_rows][448] */
     int8_t *sexp;    /* [n_cache_rows][8] */
     uint16_t *tail;  /* [n_cache_rows][64] f16 */
+    /* the layers' rows; rows [n_cache_rows, n_cache_rows + DS4HIP_CHUNK_MAX)
+     * of codes / sexp / tail follow them: the staging rows of a prefill chunk */
     long long n_cache_rows;
     size_t codes_bytes; /* bytes of the cache region at the start of the arena */
     void *arena_base;
@@ -129,6 +132,22 @@ int ds4hip_rows_scatter_f32(const float *src, int n_rows, int width, float *dst,
  * numbers (for example ds4hip_indexer_topk_positions' positions_out). */
 int ds4hip_session_layer_rows(const ds4hip_session_state *s, int il, int n_selected,
                               const int32_t **row_idx, long long *n_rows, int32_t **selected_out);
+
+/* Row lists of a prefill chunk of layer il (additive; the batched form of the
+ * per-token loop of cuda/forward_batch.cu:264-284): tokens t < n_tok at
+ * positions p0 + t whose KV rows have been written to the staging rows
+ * n_cache_rows + t (not yet to the ring), while the ring still holds exactly
+ * the positions < p0. Token t attends the window rows still in the ring
+ * (positions max(0, p0 + t - 127) .. p0 - 1), staging rows 0..t, and of the
+ * n_comp_tok[t] compressed rows either all (n_sel_tok[t] == n_comp_tok[t]) or
+ * the n_sel_tok[t] listed at sel + t * sel_stride (device). Writes list t at
+ * lists + t * list_stride (device int32, relative to layers[il].row_base: the
+ * row_idx / row_base form of ds4hip_flash_attn_decode_fp8) and its length to
+ * counts_out[t] (host). n_tok <= DS4HIP_CHUNK_MAX. */
+int ds4hip_session_chunk_rows(const ds4hip_session_state *s, int il, int p0, int n_tok,
+                              const int *n_comp_tok, const int *n_sel_tok, const int32_t *sel,
+                              int sel_stride, int32_t *lists, int list_stride, long long *counts_out,
+                              void *stream);
 
 /* ---- disk format of the FP8 session (cuda/kv_persist.cuh:6-37, adapted) ---------- */
 

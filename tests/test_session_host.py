@@ -10,7 +10,7 @@ def expected_bytes(max_ctx):
     cap_raw = min(128, max_ctx)
     ratio = lambda il: 0 if il < 2 else (4 if il % 2 == 0 else 128)
     caps = [max_ctx // ratio(il) + 2 if ratio(il) else 0 for il in range(43)]
-    rows = sum(c + cap_raw for c in caps)
+    rows = sum(c + cap_raw for c in caps) + 128   # + the prefill chunk's staging rows
     b = align(rows * 448) + align(rows * 8) + align(rows * 128)
     b += sum(align((cap_raw + c) * 4) for c in caps)
     for il in range(43):

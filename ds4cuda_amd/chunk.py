@@ -140,12 +140,14 @@ def forward_chunk_attn(session, il, p0, attn_norm, q_lora_norm, q_cur, kv_rope, 
     need = decode_fp8_workspace_bytes(cnt)
     if workspace is None or workspace.numel() < need:
         workspace = torch.empty(need, dtype=torch.uint8, device=dev)
-    # row_base is read by the kernels: a device array (one base per problem)
-    rb = torch.full((n,), int(L.row_base), dtype=torch.int64, device=dev)
+    # the list entries are relative to the layer's first row: the cache
+    # pointers start there and every problem's base is 0 (row_base NULL,
+    # stride 0), as in Session.decode
+    rb = int(L.row_base)
     call("ds4hip_flash_attn_decode_fp8", _ptr(q_cur), 1, N_HEAD * HEAD_DIM, _ptr(sinks), 0, _ptr(out),
-         N_HEAD * HEAD_DIM, _vp(s.codes), _vp(s.sexp), _vp(s.tail), C.cast(counts, C.c_void_p), n,
-         _ptr(rb), 0, _ptr(lists), stride, None, 0, 256, N_HEAD, HEAD_DIM, N_ROT,
-         _ptr(workspace), workspace.numel(), 3, st)
+         N_HEAD * HEAD_DIM, _vp(s.codes + rb * 448), _vp(s.sexp + rb * 8), _vp(s.tail + rb * 128),
+         C.cast(counts, C.c_void_p), n, None, 0, _ptr(lists), stride, None, 0, 256, N_HEAD, HEAD_DIM,
+         N_ROT, _ptr(workspace), workspace.numel(), 3, st)
     # 4. the chunk's rows into the ring, in position order
     for t in range(n):
         session.push_raw(il, kv_rope[t], stream=stream)

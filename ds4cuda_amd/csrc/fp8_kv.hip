@@ -85,6 +85,9 @@ __global__ __launch_bounds__(256) void fp8_rows_kernel(
             packed[1] = c[4] | c[5] << 8 | c[6] << 16 | c[7] << 24;
             *reinterpret_cast<uint2_t *>(codes + (size_t)prow * n_nope + d0) = packed;
             if ((t & 7) == 0) sexp[(size_t)prow * 8 + (d0 >> 6)] = (int8_t)e;
+            // without a tail, the lane of dim 0 zeroes the unused scale slots
+            if (n_rot == 0 && d0 == 0)
+                for (int s = n_nope / 64; s < 8; ++s) sexp[(size_t)prow * 8 + s] = 0;
         }
     } else {
         if (kRoundTrip) {

@@ -133,7 +133,8 @@ def layer_bytes(s, il):
 
 @pytest.mark.skip(reason="not yet run on the GPU: its first run faulted (the driver passed the "
                          "decode's row_base as a host array; the kernels read it on the device); the "
-                         "fix (a device array) could not be run this round")
+                         "fixed driver (cache pointers offset to the layer, row_base NULL, as "
+                         "Session.decode) has not run on the GPU yet")
 @pytest.mark.parametrize("il", [0, 2, 3])
 def test_chunk_matches_token_loop(gpu, tmp_path, il):
     layer = layer_weights(il, gpu)

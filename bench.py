@@ -301,6 +301,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the prefill / sparse-decode / batched-block figures")
+    ap.add_argument("--only", choices=("prefill", "sparse", "batch"),
+                    help="run one secondary config alone and print its figures as one JSON "
+                         "line (for profiling it without the cfg 2 cache)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain device copy of known size (the reference kernel "
                          "that scales the FETCH_SIZE / WRITE_SIZE counters)")
@@ -323,6 +326,14 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_calibration": {"bytes_read": COPY_BYTES, "bytes_written": COPY_BYTES,
                                                "launches": 5}}), flush=True)
+        return
+    if args.only:
+        stream = torch.cuda.current_stream()
+        fn = {"prefill": lambda: bench_prefill(dev, stream, max(3, args.steps // 10)),
+              "sparse": lambda: bench_sparse(dev, stream, args.steps),
+              "batch": lambda: bench_batch(dev, stream, args.steps)}[args.only]
+        log(f"secondary config {args.only} alone")
+        print(json.dumps({"only": args.only, "figures": fn()}), flush=True)
         return
     from ds4cuda_amd import synth
     total_rows = N_LAYERS * N_KV

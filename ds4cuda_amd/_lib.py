@@ -23,6 +23,7 @@ SIGNATURES: dict[str, list] = {
     "ds4hip_flash_attn_decode_raw_f32": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp],
     "ds4hip_flash_attn_decode_mixed_f32": [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp],
     "ds4hip_set_decode_exact_p": [_i],
+    "ds4hip_set_decode_flat_lean": [_i],
     "ds4hip_flash_attn_decode_f32_workspace_size": [_ll, C.POINTER(_sz)],
     "ds4hip_flash_attn_decode_raw_f32_prealloc": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp, _sz,
                                                   _vp],

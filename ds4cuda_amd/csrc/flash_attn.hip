@@ -1543,7 +1543,26 @@ __device__ inline uint8x_t qf8v(const uint32_t (&w)[8]) {
     return uint8x_t{w[0], w[1], w[2], w[3], w[4], w[5], w[6], w[7]};
 }
 
-template <bool kPLo>
+// max of two floats without the quieting of signalling NaNs that fmaxf adds
+// for operands of unknown origin (the scores here are never NaN)
+__device__ inline float vmax_f32(float a, float b) {
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+__device__ inline float xmax_16_32_raw(float v) {
+    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = vmax_f32(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return vmax_f32(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+// kLean: the producer form with fewer VALU instructions per tile (the score
+// scale folded into Q, packed E8M0 row scales from one byte permute, the f16
+// scale table from v_ldexp_f16, P's row sums by v_dot2, one select for empty
+// tiles). Same results up to rounding: Q is scaled by log2(e)/sqrt(d) before
+// its FP8 / f16 rounding instead of S after the MFMA.
+template <bool kPLo, bool kLean>
 __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A) {
     static_assert(!kPLo, "the flat kernel passes P as one f16");
     __shared__ __attribute__((aligned(16))) uint8_t stage[kFsStages][kFsSlot];
@@ -1607,6 +1626,10 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
                             for (int i = 0; i < 4; ++i) {
                                 x[16 * hv + 8 * v + 2 * i] = bf16_to_f32((uint16_t)(w[i] & 0xFFFF));
                                 x[16 * hv + 8 * v + 2 * i + 1] = bf16_to_f32((uint16_t)(w[i] >> 16));
+                                if constexpr (kLean) {   // S comes out in log2 units
+                                    x[16 * hv + 8 * v + 2 * i] *= A.kq_log2;
+                                    x[16 * hv + 8 * v + 2 * i + 1] *= A.kq_log2;
+                                }
                             }
                         }
                     }
@@ -1617,9 +1640,12 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
                         for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(x[i]));
                         amax = xmax_16_32(amax);   // one scale for the head's 128 dims
                         // scale 2^e with amax / 2^e in [128, 256): no E4M3 overflow
-                        const int e = amax > 0.0f ? ((int)((__float_as_uint(amax) >> 23) & 0xFF) - 127 - 7) : 0;
+                        int e = amax > 0.0f ? ((int)((__float_as_uint(amax) >> 23) & 0xFF) - 127 - 7) : 0;
+                        // kLean: the rows' E8M0 scales are 2^(e_row + 1) (byte e_row ^ 0x80),
+                        // so Q's scale carries the compensating 2^-1
+                        if constexpr (kLean) e = max(e, -126);
                         const float inv = pow2f(-e), sc = pow2f(e);
-                        qsc[part] |= (e + 127) << (8 * ks);
+                        qsc[part] |= (e + (kLean ? 126 : 127)) << (8 * ks);
 #pragma unroll
                         for (int w = 0; w < 8; ++w) {
                             int pk = 0;
@@ -1642,8 +1668,13 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
                     half8_t h;
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        h[2 * i] = (half_t)bf16_to_f32((uint16_t)(w[i] & 0xFFFF));
-                        h[2 * i + 1] = (half_t)bf16_to_f32((uint16_t)(w[i] >> 16));
+                        if constexpr (kLean) {
+                            h[2 * i] = (half_t)(bf16_to_f32((uint16_t)(w[i] & 0xFFFF)) * A.kq_log2);
+                            h[2 * i + 1] = (half_t)(bf16_to_f32((uint16_t)(w[i] >> 16)) * A.kq_log2);
+                        } else {
+                            h[2 * i] = (half_t)bf16_to_f32((uint16_t)(w[i] & 0xFFFF));
+                            h[2 * i + 1] = (half_t)bf16_to_f32((uint16_t)(w[i] >> 16));
+                        }
                     }
                     qt[s2] = h;
                 }
@@ -1658,7 +1689,7 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) s8[hh][r] = sa[hh][r] * A.kq_log2;
+                    for (int r = 0; r < 4; ++r) s8[hh][r] = kLean ? sa[hh][r] : sa[hh][r] * A.kq_log2;
                 if (nv < kTile) {
 #pragma unroll
                     for (int hh = 0; hh < 2; ++hh)
@@ -1667,32 +1698,48 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
                             if (16 * hh + 4 * q + r >= nv) s8[hh][r] = -INFINITY;
                 }
                 float tmax = -INFINITY;
+                if constexpr (kLean) {
+                    tmax = s8[0][0];
 #pragma unroll
-                for (int hh = 0; hh < 2; ++hh)
+                    for (int i = 1; i < 8; ++i) tmax = vmax_f32(tmax, s8[i >> 2][i & 3]);
+                    tmax = xmax_16_32_raw(tmax);
+                } else {
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, s8[hh][r]);
-                tmax = xmax_16_32(tmax);
+                    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, s8[hh][r]);
+                    tmax = xmax_16_32(tmax);
+                }
                 // lazy reference point (as decode_ws_kernel): it moves only when the
                 // tile max exceeds it by more than 2^kLazyLog2 in P
                 const bool bump = tmax > m_run + kLazyLog2;
                 const float m_new = bump ? tmax : m_run;
                 const bool none = m_new == -INFINITY;
                 const float alpha = (bump && m_run != -INFINITY) ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+                // kLean: with no finite score yet every s8 is -inf, and exp2(-inf - 0) = 0
+                const float m_use = none ? 0.0f : m_new;
                 float psum = 0.0f;
                 half8_t pf, pl;
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const float pv = none ? 0.0f : __builtin_amdgcn_exp2f(s8[hh][r] - m_new);
+                        const float pv = kLean ? __builtin_amdgcn_exp2f(s8[hh][r] - m_use)
+                                               : (none ? 0.0f : __builtin_amdgcn_exp2f(s8[hh][r] - m_new));
                         pf[4 * hh + r] = (half_t)pv;
                         if (kPLo) {
                             psum += pv;
                             pl[4 * hh + r] = (half_t)(pv - (float)pf[4 * hh + r]);
-                        } else {
+                        } else if (!kLean) {
                             psum += (float)pf[4 * hh + r];
                         }
                     }
+                if constexpr (kLean && !kPLo) {   // the rounded P values, summed in pairs
+                    const half2_t one2 = half2_t{(half_t)1.0f, (half_t)1.0f};
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        psum = __builtin_amdgcn_fdot2(half2_t{pf[2 * i], pf[2 * i + 1]}, one2, psum, false);
+                }
                 lds_st128(lds_addr(pws) + (uint32_t)(((b * 4 + d) * 64 + lane) * 16), pf);
                 l_run = l_run * alpha + psum;
                 m_run = m_new;
@@ -1734,23 +1781,36 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
                     if (hh == 0) pre();
                     lds_row_wait(kc, kt, ke);
                     if (q < 2 && (d < 3 || q == 0)) {
-                        const int e = (int)(int8_t)((ke[(2 * d + q) >> 2] >> (8 * ((2 * d + q) & 3))) & 0xFF);
-                        const half_t f = (half_t)pow2f(e);
-                        const uint32_t ta = st + kFsScaleOff + ((2 * d + q) * kTile + 16 * hh + j) * 2;
-                        asm volatile("ds_write_b16 %0, %1" :: "v"(ta), "v"(f) : "memory");
+                        if constexpr (kLean) {
+                            const int e = __builtin_amdgcn_sbfe((int)ke[d >> 1], 8 * ((2 * d + q) & 3), 8);
+                            const half_t f = __builtin_amdgcn_ldexph((half_t)1.0f, e);
+                            const uint32_t ta = st + kFsScaleOff + ((2 * d + q) * kTile + 16 * hh + j) * 2;
+                            asm volatile("ds_write_b16 %0, %1" :: "v"(ta), "v"(f) : "memory");
+                        } else {
+                            const int e = (int)(int8_t)((ke[(2 * d + q) >> 2] >> (8 * ((2 * d + q) & 3))) & 0xFF);
+                            const half_t f = (half_t)pow2f(e);
+                            const uint32_t ta = st + kFsScaleOff + ((2 * d + q) * kTile + 16 * hh + j) * 2;
+                            asm volatile("ds_write_b16 %0, %1" :: "v"(ta), "v"(f) : "memory");
+                        }
                     }
+                    // kLean: byte ks of scl = E8M0 of block 2 ks + q / 2 (the block the
+                    // hardware's K group q of k-step ks falls in), as 2^(e + 1)
+                    uint32_t scl = 0;
+                    if constexpr (kLean)
+                        scl = __builtin_amdgcn_perm(ke[1], ke[0], (q >> 1) ? 0x07050301u : 0x06040200u) ^ 0x80808080u;
                     float4_t c2[2] = {float4_t{0, 0, 0, 0}, float4_t{0, 0, 0, 0}};
                     static_for<4>([&](auto ksc) {
                         constexpr int ks = decltype(ksc)::value;
                         const uint32_t ew = ks < 2 ? ke[0] : ke[1];
-                        const int sa = __builtin_amdgcn_sbfe((int)ew, 16 * (ks & 1) + 8 * (q >> 1), 8) + 127;
+                        const int sa = kLean ? (int)scl
+                                             : __builtin_amdgcn_sbfe((int)ew, 16 * (ks & 1) + 8 * (q >> 1), 8) + 127;
                         const int8v av = __builtin_bit_cast(
                             int8v, uint4x2_cat(kc[2 * ks], ks < 3 ? kc[2 * ks + 1] : z4));
 #pragma unroll
                         for (int part = 0; part < 2; ++part) {
                             const int8v bv = __builtin_bit_cast(int8v, qf8v(qf8[ks][part]));
                             c2[part] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                                av, bv, c2[part], 0, 0, 0, sa, ks, qsc[part]);
+                                av, bv, c2[part], 0, 0, kLean ? ks : 0, sa, ks, qsc[part]);
                         }
                     });
                     c2[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, kt[0]), qt[0],
@@ -1823,8 +1883,40 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
             // copies of tile u into its stage slot (rows past the segment repeat its
             // last row: every tile issues the same 5 copies per wave, so the vmcnt
             // waits are exact)
+            // kLean: a whole tile inside the segment takes its copies from a
+            // tile base in SGPRs plus a per-segment lane offset (no per-tile
+            // clamp or 64-bit multiply); the segment's last tile clamps as below
+            uint32_t c_voff[5];
+            if constexpr (kLean) {
+#pragma unroll
+                for (int k = 0; k < 5; ++k) {
+                    const int n = 5 * c + k;
+                    const uint32_t rb = n == 19 ? 8u : (n < kFsCodeChunks / 64 ? (uint32_t)kNope : 2u * kRot);
+                    c_voff[k] = (uint32_t)c_row[k] * rb + c_off[k];
+                }
+            }
             auto issue = [&](int u) {
                 uint8_t *st = stage[u % kFsStages];
+                if constexpr (kLean) {
+                    if (kTile * u + kTile - 1 <= seg_last) {
+                        const uint32_t r0 = (uint32_t)(kTile * u);
+#pragma unroll
+                        for (int k = 0; k < 5; ++k) {
+                            const int n = 5 * c + k;
+                            // opaque per use: a 32-bit offset (saddr + voffset form),
+                            // not a hoisted 64-bit extension
+                            uint32_t vo = c_voff[k];
+                            asm volatile("" : "+v"(vo));
+                            if (n == 19)
+                                __builtin_amdgcn_global_load_lds(sexp_s + r0 * 8 + vo, st + kFsExpOff, 4, 0, 0);
+                            else if (n < kFsCodeChunks / 64)
+                                __builtin_amdgcn_global_load_lds(codes_s + r0 * kNope + vo, st + 1024 * n, 16, 0, 0);
+                            else
+                                __builtin_amdgcn_global_load_lds(tail_s + r0 * (2 * kRot) + vo, st + 1024 * n, 16, 0, 0);
+                        }
+                        return;
+                    }
+                }
 #pragma unroll
                 for (int k = 0; k < 5; ++k) {
                     const int n = 5 * c + k;
@@ -2178,6 +2270,17 @@ bool decode_exact_p() {
 
 // Direct rows with one f16 P use the flat-stage kernel unless
 // DS4HIP_DECODE_KERNEL=ws selects the register-load kernel.
+// 1 selects the flat kernel's lean form (kLean); initial value from
+// DS4HIP_FLAT_LEAN, default 0.
+int g_flat_lean = -1;
+bool use_flat_lean() {
+    if (g_flat_lean < 0) {
+        const char *e = getenv("DS4HIP_FLAT_LEAN");
+        g_flat_lean = (e && e[0] == '1') ? 1 : 0;
+    }
+    return g_flat_lean == 1;
+}
+
 bool use_flat_kernel() {
     static const int v = [] {
         const char *e = getenv("DS4HIP_DECODE_KERNEL");
@@ -2191,7 +2294,10 @@ void launch_ws(const DecodeArgs &A, const Plan &pl, hipStream_t st) {
     // (the f16 hi + lo P form keeps the register-load kernel: the flat kernel's
     // producers have no registers left for the second P fragment)
     if (kMode == 0 && use_flat_kernel() && !decode_exact_p()) {
-        hipLaunchKernelGGL(decode_flat_kernel<false>, dim3(pl.n_wg), dim3(512), 0, st, A);
+        if (use_flat_lean())
+            hipLaunchKernelGGL((decode_flat_kernel<false, true>), dim3(pl.n_wg), dim3(512), 0, st, A);
+        else
+            hipLaunchKernelGGL((decode_flat_kernel<false, false>), dim3(pl.n_wg), dim3(512), 0, st, A);
         return;
     }
     if (decode_exact_p())
@@ -2240,6 +2346,13 @@ extern "C" int ds4hip_set_decode_exact_p(int exact) {
     if (exact != 0 && exact != 1) return -22;
     const int prev = decode_exact_p() ? 1 : 0;
     g_decode_exact_p = exact;
+    return prev;
+}
+
+extern "C" int ds4hip_set_decode_flat_lean(int lean) {
+    if (lean != 0 && lean != 1) return -22;
+    const int prev = use_flat_lean() ? 1 : 0;
+    g_flat_lean = lean;
     return prev;
 }
 

@@ -158,6 +158,16 @@ int ds4hip_flash_attn_decode_fp8(const void *q, int q_is_f32, long long q_stride
  * synchronized with launches in flight on other host threads. */
 int ds4hip_set_decode_exact_p(int exact);
 
+/* Form of the flat-stage decode kernel that serves direct rows with one f16 P
+ * (no counterpart in the reference): lean = 1 folds the score scale into Q
+ * before its FP8 split, takes the rows' E8M0 scales from one byte permute and
+ * trims the producer's and the copies' per-tile instructions; 0 (the default)
+ * keeps the checked form. Results agree to rounding. The initial value comes
+ * from the environment variable DS4HIP_FLAT_LEAN. Returns the previous
+ * setting, or -22 for another value. Process-wide, like
+ * ds4hip_set_decode_exact_p. */
+int ds4hip_set_decode_flat_lean(int lean);
+
 /* ---- chunked prefill ------------------------------------------------------------- */
 
 /* Causal chunked-prefill attention over the FP8 cache (additive: the

@@ -214,3 +214,41 @@ def test_fp8_p_precision_modes(gpu, n_kv):
     assert errs[1] <= TOL
     assert errs[0] <= TOL
     assert _lib.lib().ds4hip_set_decode_exact_p(2) == -22
+
+
+@pytest.mark.skip(reason="the lean form of the flat decode kernel (ds4hip_set_decode_flat_lean) "
+                         "has not run on the GPU yet")
+@pytest.mark.parametrize("counts", [[1], [33], [1000], [300, 0, 64, 1025, 7], [32768]])
+def test_fp8_flat_lean_form(gpu, counts):
+    """The lean form (score scale folded into Q, packed row scales, SGPR-based
+    copies of whole tiles) against the oracle at the decode bar, and against
+    the default form: both round Q and P differently, so they agree to the
+    same bar, not bit for bit. Ragged counts exercise the clamped last tile."""
+    from ds4cuda_amd import _lib
+    total = int(sum(counts))
+    base = np.concatenate([[0], np.cumsum(counts)[:-1]])
+    cache, (codes, sexp, tail) = make_cache(total, 61, gpu)
+    n = len(counts)
+    bits, qf = q_bf16(62, n)
+    sinks = sinks_for(63, n)
+    q = torch.from_numpy(bits.view(np.int16)).to(gpu).view(torch.bfloat16)
+    rb = torch.from_numpy(base.astype(np.int64)).to(gpu)
+    outs = {}
+    prev = _lib.lib().ds4hip_set_decode_flat_lean(0)
+    try:
+        for lean in (0, 1):
+            assert _lib.lib().ds4hip_set_decode_flat_lean(lean) in (0, 1)
+            out = torch.zeros((n, 64, 512), dtype=torch.float32, device=gpu)
+            ops.flash_attn_decode_fp8(q, torch.from_numpy(sinks).to(gpu), out, cache, counts, row_base=rb)
+            torch.cuda.synchronize()
+            outs[lean] = out.cpu().numpy()
+    finally:
+        _lib.lib().ds4hip_set_decode_flat_lean(prev)
+    assert _lib.lib().ds4hip_set_decode_flat_lean(2) == -22
+    for p, c in enumerate(counts):
+        if c == 0:
+            continue
+        rows = base[p] + np.arange(c)
+        ref = O.attn_decode_fp8(qf[p], codes, sexp, tail, rows, sinks[p], n_threads=8)
+        check(outs[1][p], ref)
+        check(outs[1][p], outs[0][p])

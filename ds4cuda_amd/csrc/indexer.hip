@@ -546,11 +546,12 @@ constexpr float kBoundC = 1.0e-4f;
 constexpr int kPfMaxChunks = 1024;   // candidates <= kPfMaxChunks * kChunk
 constexpr int kPfMinCand = 8192;      // fewer candidates: the exact scorer outright
 // DS4HIP_INDEXER_PREFILTER=0 keeps the exact scorer for every key.
-// Off by default: a GPU run of a variant build of this path (one process
-// loading several builds of the library) left the GPU faulted twice without
-// a cause found yet; until one is shown the exact scorer is the default and
-// the prefilter runs only when asked for (DS4HIP_INDEXER_PREFILTER=1 or
-// ds4hip_set_indexer_prefilter(1)).
+// Off by default: two GPU runs of a timing variant of this path (a fake
+// level-1 histogram, not part of this code) left most of the position list
+// unwritten, and the gathered decode then read rows at garbage indices. The
+// emit kernel now writes valid positions whenever the counts disagree; the
+// prefilter stays opt-in (DS4HIP_INDEXER_PREFILTER=1 or
+// ds4hip_set_indexer_prefilter(1)) until it has run again.
 int g_prefilter = -1;
 bool prefilter_enabled() {
     if (g_prefilter < 0) {
@@ -620,10 +621,20 @@ size_t pf_scratch_words(int n_comp) {
     return 3 * kBins + 64 + 3 * pf_align(chunks) + 5 * chunks * kChunk;
 }
 
-// One wave scores 16 keys per step: A = 16 key rows x 32 dims (lane (i, g):
-// key i, dims 8 g .. 8 g + 7 of the k-step), B = 32 dims x 16 heads of the
-// query (hi and lo parts), C = keys x heads; the head sum reduces over the 16
-// lanes of a column group.
+// sum over lanes l, l^16, l^32, l^48 with VALU lane swaps (no LDS)
+__device__ inline float pf_xsum(float v) {
+    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// One wave scores 16 keys per step: D = Q . K^T per head tile with A = 16
+// query heads x 32 dims (lane (j, g): head 16 ht + j, dims 8 g .. 8 g + 7 of
+// the k-step; hi and lo parts) and B = 32 dims x 16 keys (lane (j, g): key j,
+// the same dims). Lane (j, g) then holds heads 16 ht + 4 g + r of key j, so
+// the weighted head sum is 16 fmas in the lane and two lane swaps, and the
+// key's norm reduces the same way: no LDS round trips.
 __global__ __launch_bounds__(256) void prefilter_kernel(const float *__restrict__ q,
                                                         const float *__restrict__ w,
                                                         const uint16_t *__restrict__ keys,
@@ -658,20 +669,18 @@ __global__ __launch_bounds__(256) void prefilter_kernel(const float *__restrict_
                 ql[ht][ks][e + 1] = ls[1];
             }
         }
-    float wj[4];
-#pragma unroll
-    for (int ht = 0; ht < 4; ++ht) wj[ht] = w[16 * ht + j];
-    // Wq = sum_h |w_h| ||q_h||: the 4 lane groups' parts of each head, then the 16 columns
+    // Wq = sum_h |w_h| ||q_h|| (lane (j, g) holds a quarter of head 16 ht + j's norm)
     float wq = 0.0f;
 #pragma unroll
-    for (int ht = 0; ht < 4; ++ht) {
-        float n2 = qn2[ht];
-        n2 += __shfl_xor(n2, 16);
-        n2 += __shfl_xor(n2, 32);
-        wq += fabsf(wj[ht]) * sqrtf(n2);
-    }
+    for (int ht = 0; ht < 4; ++ht) wq += fabsf(w[16 * ht + j]) * sqrtf(pf_xsum(qn2[ht]));
 #pragma unroll
     for (int off = 1; off < 16; off <<= 1) wq += __shfl_xor(wq, off, 16);
+    // the head weights of the D rows this lane holds: head 16 ht + 4 g + r
+    float wr[4][4];
+#pragma unroll
+    for (int ht = 0; ht < 4; ++ht)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) wr[ht][r] = w[16 * ht + 4 * g + r];
     __syncthreads();
     float bmax = 0.0f;
     const int n_tiles = (n_cand + 15) / 16;
@@ -684,13 +693,9 @@ __global__ __launch_bounds__(256) void prefilter_kernel(const float *__restrict_
             u[ks] = *reinterpret_cast<const uint4_t *>(keys + (size_t)rr * kMaxDim + 32 * ks + 8 * g);
     };
     const int stride = gridDim.x * 4;
-    uint4_t un[4];
-    if (blockIdx.x * 4 + wave < n_tiles) load_tile(blockIdx.x * 4 + wave, un);
-    for (int tile = blockIdx.x * 4 + wave; tile < n_tiles; tile += stride) {
-        uint4_t uc[4];
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) uc[ks] = un[ks];
-        if (tile + stride < n_tiles) load_tile(tile + stride, un);
+    // two fragment buffers in turn, so the next tile's loads need no copy; a
+    // load past the last tile re-reads the last tile (unused)
+    auto process = [&](int tile, const uint4_t (&uc)[4]) {
         pf_bf16x8_t a[4];
         float n2 = 0.0f;
 #pragma unroll
@@ -699,45 +704,50 @@ __global__ __launch_bounds__(256) void prefilter_kernel(const float *__restrict_
             a[ks] = __builtin_bit_cast(pf_bf16x8_t, u);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float lo = __uint_as_float(u[e] << 16), hi = __uint_as_float(u[e] & 0xFFFF0000u);
-                n2 = fmaf(lo, lo, fmaf(hi, hi, n2));
+                const pf_bf16x2_t kp = __builtin_bit_cast(pf_bf16x2_t, u[e]);
+                n2 = __builtin_amdgcn_fdot2_f32_bf16(kp, kp, n2, false);
             }
         }
-        n2 += __shfl_xor(n2, 16);
-        n2 += __shfl_xor(n2, 32);   // ||k_row||^2 in every lane (i = row)
         float4_t c[4];
 #pragma unroll
         for (int ht = 0; ht < 4; ++ht) {
             c[ht] = float4_t{0, 0, 0, 0};
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
-                c[ht] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[ks], qh[ht][ks], c[ht], 0, 0, 0);
-                c[ht] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[ks], ql[ht][ks], c[ht], 0, 0, 0);
+                c[ht] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qh[ht][ks], a[ks], c[ht], 0, 0, 0);
+                c[ht] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ql[ht][ks], a[ks], c[ht], 0, 0, 0);
             }
         }
-        // lane (j, g): keys 4 g + r, head 16 ht + j
-        float s[4];
+        // lane (j, g): heads 16 ht + 4 g + r of key j
+        float v = 0.0f;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            float v = 0.0f;
+        for (int ht = 0; ht < 4; ++ht)
 #pragma unroll
-            for (int ht = 0; ht < 4; ++ht) v = fmaf(wj[ht], c[ht][r] > 0.0f ? c[ht][r] : 0.0f, v);
-#pragma unroll
-            for (int off = 1; off < 16; off <<= 1) v += __shfl_xor(v, off, 16);
-            s[r] = v;
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int kr = 16 * tile + 4 * g + r;
-            const float kn2 = __shfl(n2, 4 * g + r);
-            if (j == r && kr < n_cand) {
-                const float b = kBoundC * sqrtf(kn2) * wq;
-                a_out[kr] = s[r];
-                S.bound[kr] = b;
-                bmax = fmaxf(bmax, b);
-                atomicAdd(&lh[ord_key(s[r]) >> 21], 1u);
+            for (int r = 0; r < 4; ++r) {
+                float rl;   // relu without the quieting that fmaxf adds
+                asm("v_max_f32 %0, 0, %1" : "=v"(rl) : "v"(c[ht][r]));
+                v = fmaf(wr[ht][r], rl, v);
             }
+        v = pf_xsum(v);
+        const float kn2 = pf_xsum(n2);   // ||k_j||^2
+        const int kr = 16 * tile + j;
+        if (g == 0 && kr < n_cand) {
+            const float b = kBoundC * sqrtf(kn2) * wq;
+            a_out[kr] = v;
+            S.bound[kr] = b;
+            bmax = fmaxf(bmax, b);
+            atomicAdd(&lh[ord_key(v) >> 21], 1u);
         }
+    };
+    const int first = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(wave);
+    uint4_t ub0[4], ub1[4];
+    if (first < n_tiles) load_tile(first, ub0);
+    for (int tile = first; tile < n_tiles; tile += 2 * stride) {
+        load_tile(min(tile + stride, n_tiles - 1), ub1);
+        process(tile, ub0);
+        if (tile + stride >= n_tiles) break;
+        load_tile(min(tile + 2 * stride, n_tiles - 1), ub0);
+        process(tile + stride, ub1);
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) bmax = fmaxf(bmax, __shfl_xor(bmax, off));

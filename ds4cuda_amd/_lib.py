@@ -85,6 +85,8 @@ SIGNATURES: dict[str, list] = {
                                    _vp],
     "ds4hip_set_indexer_prefilter": [_i],
     "ds4hip_session_chunk_rows": [_vp, _i, _i, _i, _vp, _vp, _vp, _i, _vp, _i, _vp, _vp],
+    "ds4hip_session_chunk_rows_host": [_vp, _i, _i, _i, _vp, _vp, _vp, _i, _vp, _i, _vp],
+    "ds4hip_session_state_describe": [_vp, _i],
     "ds4hip_session_save_to_disk": [_vp, _vp, _i, C.c_char_p],
     "ds4hip_session_load_from_disk": [_vp, C.c_char_p, C.POINTER(_i), C.POINTER(_i)],
 }

@@ -238,6 +238,27 @@ extern "C" size_t ds4hip_session_state_arena_bytes(int max_context) {
     return make_plan(max_context).bytes;
 }
 
+extern "C" int ds4hip_session_state_describe(ds4hip_session_state *out, int max_context) {
+    if (!out || max_context <= 0) return ds4hip_set_last_error(kEINVAL);
+    std::memset(out, 0, sizeof(*out));
+    const Plan P = make_plan(max_context);
+    out->max_context = max_context;
+    out->arena_bytes = P.bytes;
+    out->n_cache_rows = P.n_rows;
+    out->codes_bytes = P.off_lists;
+    for (int il = 0; il < DS4HIP_N_LAYER; ++il) {
+        ds4hip_layer_state *L = &out->layers[il];
+        const int r = layer_ratio(il);
+        L->il = il;
+        L->compress_ratio = r;
+        L->has_indexer = r == 4;
+        L->cap_raw = P.cap_raw;
+        L->cap_comp = P.cap_comp[il];
+        L->row_base = P.row_base[il];
+    }
+    return 0;
+}
+
 extern "C" int ds4hip_session_state_alloc(ds4hip_session_state *out, int max_context) {
     if (!out || max_context <= 0) return ds4hip_set_last_error(kEINVAL);
     std::memset(out, 0, sizeof(*out));
@@ -571,27 +592,66 @@ struct ChunkTok {   // per token: compressed rows visible, and how many of them 
     int n_comp[DS4HIP_CHUNK_MAX];
     int n_sel[DS4HIP_CHUNK_MAX];
 };
+struct ChunkGeom {
+    int p0, cap_raw, cap_comp, stage_rel;
+};
 
-// One workgroup per token t (position p0 + t): the window rows still in the
-// ring (positions max(0, p0 + t - cap_raw + 1) .. p0 - 1, slot position %
-// cap_raw), the chunk's staged rows 0..t, then the token's compressed rows
-// (its selection sel[t], or all of them); entries relative to the layer's
-// row_base.
-__global__ __launch_bounds__(256) void chunk_rows_kernel(int32_t *__restrict__ lists, int stride, int p0,
-                                                         int cap_raw, int cap_comp, int stage_rel,
+// Token t (position p0 + t) sees the window positions max(0, p0 + t -
+// cap_raw + 1) .. p0 + t: those below p0 in the ring (position x in slot
+// x % cap_raw, after the compressed rows), the others in the staging rows.
+__host__ __device__ inline int chunk_first(const ChunkGeom &G, int t) {
+    const int f = G.p0 + t - G.cap_raw + 1;
+    return f > 0 ? f : 0;
+}
+__host__ __device__ inline int chunk_n_ring(const ChunkGeom &G, int t) {
+    const int f = chunk_first(G, t);
+    return G.p0 > f ? G.p0 - f : 0;
+}
+// Entry i < chunk_n_ring + t + 1 of token t's list (relative to row_base).
+__host__ __device__ inline int32_t chunk_entry(const ChunkGeom &G, int t, int i) {
+    const int nr = chunk_n_ring(G, t);
+    return i < nr ? G.cap_comp + (chunk_first(G, t) + i) % G.cap_raw : G.stage_rel + (i - nr);
+}
+
+// One workgroup per token t: the window rows, then the token's compressed
+// rows (its selection sel[t], or all of them).
+__global__ __launch_bounds__(256) void chunk_rows_kernel(int32_t *__restrict__ lists, int stride, ChunkGeom G,
                                                          ChunkTok T, const int32_t *__restrict__ sel,
                                                          int sel_stride) {
     const int t = blockIdx.x;
     int32_t *out = lists + (size_t)t * stride;
-    const int first = max(0, p0 + t - cap_raw + 1);
-    const int n_ring = p0 > first ? p0 - first : 0;
-    const int n_stage = t + 1;
+    const int n_win = chunk_n_ring(G, t) + t + 1;
     const int n_sel = T.n_sel[t];
     const bool all = n_sel == T.n_comp[t];
-    for (int i = threadIdx.x; i < n_ring; i += 256) out[i] = cap_comp + (first + i) % cap_raw;
-    for (int i = threadIdx.x; i < n_stage; i += 256) out[n_ring + i] = stage_rel + i;
+    for (int i = threadIdx.x; i < n_win; i += 256) out[i] = chunk_entry(G, t, i);
     for (int i = threadIdx.x; i < n_sel; i += 256)
-        out[n_ring + n_stage + i] = all ? i : sel[(size_t)t * sel_stride + i];
+        out[n_win + i] = all ? i : sel[(size_t)t * sel_stride + i];
+}
+
+// Checks the arguments shared by the device and host forms and fills T,
+// the geometry and the counts.
+int chunk_plan(const ds4hip_session_state *s, int il, int p0, int n_tok, const int *n_comp_tok,
+               const int *n_sel_tok, bool have_sel, int sel_stride, int list_stride, long long *counts_out,
+               ChunkTok &T, ChunkGeom &G) {
+    if (!s || il < 0 || il >= DS4HIP_N_LAYER || n_tok <= 0 || n_tok > DS4HIP_CHUNK_MAX || p0 < 0 ||
+        !n_comp_tok || !n_sel_tok || !counts_out || list_stride <= 0)
+        return kEINVAL;
+    const ds4hip_layer_state *L = &s->layers[il];
+    if (L->cap_raw <= 0) return kEINVAL;
+    // the ring holds exactly the positions < p0 (one push per position)
+    if (L->n_raw != (p0 < L->cap_raw ? p0 : L->cap_raw) || L->raw_head != p0 % L->cap_raw) return kEINVAL;
+    G = ChunkGeom{p0, L->cap_raw, L->cap_comp, (int)(s->n_cache_rows - L->row_base)};
+    for (int t = 0; t < n_tok; ++t) {
+        const bool all = n_sel_tok[t] == n_comp_tok[t];
+        if (n_comp_tok[t] < 0 || n_comp_tok[t] > L->cap_comp || n_sel_tok[t] < 0 ||
+            n_sel_tok[t] > n_comp_tok[t] || (!all && (!have_sel || n_sel_tok[t] > sel_stride)))
+            return kEINVAL;
+        counts_out[t] = (long long)chunk_n_ring(G, t) + (t + 1) + n_sel_tok[t];
+        if (counts_out[t] > list_stride) return kEINVAL;
+        T.n_comp[t] = n_comp_tok[t];
+        T.n_sel[t] = n_sel_tok[t];
+    }
+    return 0;
 }
 }  // namespace
 
@@ -599,28 +659,33 @@ extern "C" int ds4hip_session_chunk_rows(const ds4hip_session_state *s, int il, 
                                          const int *n_comp_tok, const int *n_sel_tok,
                                          const int32_t *sel, int sel_stride, int32_t *lists,
                                          int list_stride, long long *counts_out, void *stream) {
-    if (!layer_ok(s, il) || n_tok <= 0 || n_tok > DS4HIP_CHUNK_MAX || p0 < 0 || !n_comp_tok ||
-        !n_sel_tok || !lists || !counts_out || list_stride <= 0)
-        return ds4hip_set_last_error(kEINVAL);
-    const ds4hip_layer_state *L = &s->layers[il];
-    // the ring holds exactly the positions < p0 (one push per position)
-    if (L->n_raw != (p0 < L->cap_raw ? p0 : L->cap_raw) || L->raw_head != p0 % L->cap_raw)
-        return ds4hip_set_last_error(kEINVAL);
+    if (!layer_ok(s, il) || !lists) return ds4hip_set_last_error(kEINVAL);
     ChunkTok T;
-    for (int t = 0; t < n_tok; ++t) {
-        const int first = p0 + t - L->cap_raw + 1 > 0 ? p0 + t - L->cap_raw + 1 : 0;
-        const long long n_ring = p0 > first ? p0 - first : 0;
-        const bool all = n_sel_tok[t] == n_comp_tok[t];
-        if (n_comp_tok[t] < 0 || n_comp_tok[t] > L->cap_comp || n_sel_tok[t] < 0 ||
-            n_sel_tok[t] > n_comp_tok[t] || (!all && (!sel || n_sel_tok[t] > sel_stride)))
-            return ds4hip_set_last_error(kEINVAL);
-        counts_out[t] = n_ring + (t + 1) + n_sel_tok[t];
-        if (counts_out[t] > list_stride) return ds4hip_set_last_error(kEINVAL);
-        T.n_comp[t] = n_comp_tok[t];
-        T.n_sel[t] = n_sel_tok[t];
-    }
-    const long long stage_rel = s->n_cache_rows - L->row_base;
-    hipLaunchKernelGGL(chunk_rows_kernel, dim3(n_tok), dim3(256), 0, (hipStream_t)stream, lists, list_stride,
-                       p0, L->cap_raw, L->cap_comp, (int)stage_rel, T, sel, sel_stride);
+    ChunkGeom G;
+    const int rc = chunk_plan(s, il, p0, n_tok, n_comp_tok, n_sel_tok, sel != nullptr, sel_stride, list_stride,
+                              counts_out, T, G);
+    if (rc) return ds4hip_set_last_error(rc);
+    hipLaunchKernelGGL(chunk_rows_kernel, dim3(n_tok), dim3(256), 0, (hipStream_t)stream, lists, list_stride, G,
+                       T, sel, sel_stride);
     return ds4hip_set_last_error(hip_status(hipGetLastError()));
+}
+
+extern "C" int ds4hip_session_chunk_rows_host(const ds4hip_session_state *s, int il, int p0, int n_tok,
+                                              const int *n_comp_tok, const int *n_sel_tok,
+                                              const int32_t *sel, int sel_stride, int32_t *lists,
+                                              int list_stride, long long *counts_out) {
+    if (!lists) return ds4hip_set_last_error(kEINVAL);
+    ChunkTok T;
+    ChunkGeom G;
+    const int rc = chunk_plan(s, il, p0, n_tok, n_comp_tok, n_sel_tok, sel != nullptr, sel_stride, list_stride,
+                              counts_out, T, G);
+    if (rc) return ds4hip_set_last_error(rc);
+    for (int t = 0; t < n_tok; ++t) {
+        int32_t *out = lists + (size_t)t * list_stride;
+        const int n_win = chunk_n_ring(G, t) + t + 1;
+        const bool all = T.n_sel[t] == T.n_comp[t];
+        for (int i = 0; i < n_win; ++i) out[i] = chunk_entry(G, t, i);
+        for (int i = 0; i < T.n_sel[t]; ++i) out[n_win + i] = all ? i : sel[(size_t)t * sel_stride + i];
+    }
+    return 0;
 }

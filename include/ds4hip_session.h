@@ -95,6 +95,12 @@ typedef struct ds4hip_session_state {
  * size calculation; cuda/session_state.cu:147 for the fp32 form). */
 size_t ds4hip_session_state_arena_bytes(int max_context);
 
+/* The geometry ds4hip_session_state_alloc would give a session of
+ * max_context tokens (capacities, row bases, n_cache_rows, arena_bytes), with
+ * every pointer NULL and every counter 0: nothing is allocated. For planning
+ * memory and for the host form of ds4hip_session_chunk_rows. */
+int ds4hip_session_state_describe(ds4hip_session_state *out, int max_context);
+
 /* One hipMalloc, carved; cache rows zeroed, compressor scores -inf, counters
  * 0 (cuda/session_state.cu:110-256). Synchronizes the null stream once. */
 int ds4hip_session_state_alloc(ds4hip_session_state *out, int max_context);
@@ -148,6 +154,15 @@ int ds4hip_session_chunk_rows(const ds4hip_session_state *s, int il, int p0, int
                               const int *n_comp_tok, const int *n_sel_tok, const int32_t *sel,
                               int sel_stride, int32_t *lists, int list_stride, long long *counts_out,
                               void *stream);
+
+/* Host form of ds4hip_session_chunk_rows (same lists and checks): sel and
+ * lists in host memory, no device access, so s may come from
+ * ds4hip_session_state_describe with layer il's n_raw / raw_head set. For a
+ * caller that stages the lists with its own copies. */
+int ds4hip_session_chunk_rows_host(const ds4hip_session_state *s, int il, int p0, int n_tok,
+                                   const int *n_comp_tok, const int *n_sel_tok, const int32_t *sel,
+                                   int sel_stride, int32_t *lists, int list_stride,
+                                   long long *counts_out);
 
 /* ---- disk format of the FP8 session (cuda/kv_persist.cuh:6-37, adapted) ---------- */
 

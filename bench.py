@@ -273,8 +273,14 @@ def bench_batch(dev, stream, steps):
     ms_eager = time_ms(step, steps, 3, stream)
     # the same step captured once in a HIP graph (13 kernels, one graph launch)
     torch.cuda.synchronize()
-    graph = blk.capture(pos, x, kv_cur, q, q_idx, w_idx, sinks)
-    ms = time_ms(graph.replay, steps, 3, stream)
+    graph_error = None
+    try:
+        graph = blk.capture(pos, x, kv_cur, q, q_idx, w_idx, sinks)
+        ms = time_ms(graph.replay, steps, 3, stream)
+    except Exception as e:   # noqa: BLE001
+        graph_error = f"{type(e).__name__}: {e}"
+        log(f"graph capture of the batched block failed ({graph_error}); reporting the eager step")
+        ms = ms_eager
     n_comp = blk.plan(pos)["n_comp"]
     sel = [min(int(n), TOPK) for n in n_comp]
     b = (w["w_out"].numel() * 2 + sum(w[k].numel() for k in ("w_kv", "w_gate", "wi_kv", "wi_gate")) * 4
@@ -286,7 +292,8 @@ def bench_batch(dev, stream, steps):
                         "top-2048 selection, decode, inverse RoPE, bf16 attn_out 32768->4096 "
                         "(BASELINE configs[4])",
             "us_per_step_layer": round(ms * 1e3, 2), "us_per_step_layer_eager": round(ms_eager * 1e3, 2),
-            "timing": "HIP graph replay of the step (us_per_step_layer_eager: 13 launches from Python)",
+            "timing": ("HIP graph replay of the step (us_per_step_layer_eager: 13 launches from Python)"
+                       if graph_error is None else f"eager step (graph capture failed: {graph_error})"),
             "bytes": b,
             "gbs": round(b / (ms * 1e-3) / 1e9, 1),
             "frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
@@ -420,9 +427,17 @@ def main():
     }
     if not args.no_secondary:
         log("secondary configs: chunked prefill, sparse decode, batched block")
-        res["secondary"] = {"prefill": bench_prefill(dev, stream, max(3, args.steps // 10)),
-                            "sparse_decode": bench_sparse(dev, stream, args.steps),
-                            "batched_block": bench_batch(dev, stream, args.steps)}
+        # a failing secondary config is reported in its entry; it does not
+        # take the headline line down with it
+        def guarded(fn):
+            try:
+                return fn()
+            except Exception as e:   # noqa: BLE001
+                log(f"secondary config failed: {type(e).__name__}: {e}")
+                return {"error": f"{type(e).__name__}: {e}"}
+        res["secondary"] = {"prefill": guarded(lambda: bench_prefill(dev, stream, max(3, args.steps // 10))),
+                            "sparse_decode": guarded(lambda: bench_sparse(dev, stream, args.steps)),
+                            "batched_block": guarded(lambda: bench_batch(dev, stream, args.steps))}
     if not args.no_cpu_baseline:
         log("timing the CPU baseline (oracle) on one layer")
         res["cpu_baseline"] = cpu_baseline()

@@ -44,6 +44,7 @@ TRAFFIC_BYTES_PER_LAUNCH = {"ws": 882340981}
 TRAFFIC_MEASURED_AT = {"ws": "22db79c"}            # commit whose partial kernel was counted
 DECODE_KERNEL = "ws" if os.environ.get("DS4HIP_DECODE_KERNEL", "").startswith("w") else "flat"
 KERNEL_LABEL = {"ws": "decode_ws_kernel<0, false> (direct rows, register loads, one f16 P)",
+                "lean": "decode_flat_kernel<false, true> (flat stages, lean producer form, one f16 P)",
                 "flat": "decode_flat_kernel<false> (direct rows, DMA-fed flat LDS stages, one f16 P)"}
 
 
@@ -308,6 +309,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the prefill / sparse-decode / batched-block figures")
+    ap.add_argument("--kernel", choices=("flat", "lean", "ws"), default=None,
+                    help="decode kernel for direct rows: the flat-stage kernel (default), its lean "
+                         "form, or the register-load kernel")
     ap.add_argument("--only", choices=("prefill", "sparse", "batch"),
                     help="run one secondary config alone and print its figures as one JSON "
                          "line (for profiling it without the cfg 2 cache)")
@@ -320,10 +324,18 @@ def main():
             "cross-GPU component in this build (run with --gpus 1).")
         sys.exit(2)
 
+    global DECODE_KERNEL
+    if args.kernel == "ws":
+        os.environ["DS4HIP_DECODE_KERNEL"] = "ws"   # read once, at the first decode launch
+    if args.kernel:
+        DECODE_KERNEL = args.kernel
     import torch
     from ds4cuda_amd import ops
 
     dev = torch.device("cuda:0")
+    if args.kernel == "lean":
+        from ds4cuda_amd import lib
+        lib().ds4hip_set_decode_flat_lean(1)
     if args.copy_calibration:
         n = COPY_BYTES // 4
         src = torch.ones(n, dtype=torch.float32, device=dev)

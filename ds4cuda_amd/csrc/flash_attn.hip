@@ -1804,8 +1804,9 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
                         const uint32_t ew = ks < 2 ? ke[0] : ke[1];
                         const int sa = kLean ? (int)scl
                                              : __builtin_amdgcn_sbfe((int)ew, 16 * (ks & 1) + 8 * (q >> 1), 8) + 127;
-                        const int8v av = __builtin_bit_cast(
-                            int8v, uint4x2_cat(kc[2 * ks], ks < 3 ? kc[2 * ks + 1] : z4));
+                        uint4_t k_hi = z4;   // dims 448.. of k-step 3 are zeros
+                        if constexpr (ks < 3) k_hi = kc[2 * ks + 1];
+                        const int8v av = __builtin_bit_cast(int8v, uint4x2_cat(kc[2 * ks], k_hi));
 #pragma unroll
                         for (int part = 0; part < 2; ++part) {
                             const int8v bv = __builtin_bit_cast(int8v, qf8v(qf8[ks][part]));

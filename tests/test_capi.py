@@ -49,3 +49,33 @@ def test_workspace_size_is_positive():
     from ds4cuda_amd.ops import decode_fp8_workspace_bytes
     assert decode_fp8_workspace_bytes([32768] * 43) > 0
     assert decode_fp8_workspace_bytes([0, 5, 0]) > 0
+
+
+def test_newer_entry_points_refuse_bad_arguments_on_the_host():
+    """Null pointers, unsupported shapes and out-of-range switches are refused
+    with -22 before any device work (the persistence calls return -1, as the
+    reference's do, and keep -22 for ds4hip_get_last_error)."""
+    from ds4cuda_amd import lib
+    l = lib()
+    N = None
+    assert l.ds4hip_attn_qkv_decode_f32(N, N, N, N, N, N, 0, 0, N, N, N, N, C.c_size_t(0), N) == -22
+    assert l.ds4hip_rms_norm_f32(N, N, N, 16, C.c_float(1e-6), N) == -22
+    assert l.ds4hip_rms_norm_batch_f32(N, N, 0, N, 4, 16, C.c_float(1e-6), N) == -22
+    assert l.ds4hip_session_save_to_disk(N, N, 0, b"/nonexistent/kv") == -1
+    assert l.ds4hip_get_last_error() == -22
+    assert l.ds4hip_session_load_from_disk(N, b"/nonexistent/kv", N, N) == -1
+    assert l.ds4hip_get_last_error() == -22
+    assert l.ds4hip_session_chunk_rows(N, 0, 0, 1, N, N, N, 0, N, 0, N, N) == -22
+    assert l.ds4hip_session_push_raw(N, 0, N, N) == -22
+    assert l.ds4hip_session_state_describe(N, 16) == -22
+    for setter in (l.ds4hip_set_decode_flat_lean, l.ds4hip_set_indexer_prefilter,
+                   l.ds4hip_set_decode_exact_p):
+        assert setter(5) == -22
+    cnt = (C.c_longlong * 1)(10)
+    # 32 heads: the decode serves 64
+    assert l.ds4hip_flash_attn_decode_fp8(N, 0, C.c_longlong(0), N, C.c_longlong(0), N, C.c_longlong(0), N, N,
+                                          N, cnt, 1, N, C.c_longlong(0), N, C.c_longlong(0), N, 0, 256, 32,
+                                          512, 64, N, C.c_size_t(0), 3, N) == -22
+    assert l.ds4hip_flash_attn_prefill_fp8(N, N, N, N, N, N, 4, 8, 64, 512, 64, N, C.c_size_t(0), N) == -22
+    assert l.ds4hip_flash_attn_decode_mixed_f32_noalloc(N, N, N, N, N, N, 64, -1, 0, 512, N) == -22
+    assert l.ds4hip_mul_mm_f32_f32(N, N, N, 16, 32, 1, N, C.c_size_t(0), N) == -22

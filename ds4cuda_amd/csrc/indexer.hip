@@ -279,6 +279,83 @@ __global__ __launch_bounds__(256) void score_kernel(const float *__restrict__ q,
     }
 }
 
+// The same scores (head_dim 128, n_head a multiple of 4) with the query and
+// the weights read from global memory at wave-uniform addresses, so they come
+// through scalar loads into SGPRs and every fma takes its query value as a
+// scalar operand: no LDS staging and no LDS reads. The key row, the four
+// independent head chains and the head sum keep score_lds' order, so the
+// scores are bit-identical to it.
+template <int kKind>
+__global__ __launch_bounds__(256) void score_sgpr_kernel(const float *__restrict__ q,
+                                                         const float *__restrict__ w,
+                                                         const void *__restrict__ keys, int n_comp,
+                                                         int n_head, float *__restrict__ scores,
+                                                         unsigned *__restrict__ hist, int n_cand) {
+    __shared__ unsigned lh[kBins];
+    if (hist)
+        for (int i = threadIdx.x; i < kBins; i += 256) lh[i] = 0;
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    const int cc = c < n_comp ? c : n_comp - 1;   // the last block's spare lanes score a real key
+    float k[kMaxDim];
+    if (kKind == 0) {
+        const float4_t *src = reinterpret_cast<const float4_t *>(
+            static_cast<const float *>(keys) + (size_t)cc * kMaxDim);
+#pragma unroll
+        for (int v = 0; v < kMaxDim / 4; ++v) {
+            const float4_t u = src[v];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) k[4 * v + e] = u[e];
+        }
+    } else {
+        const uint4_t *src = reinterpret_cast<const uint4_t *>(
+            static_cast<const uint16_t *>(keys) + (size_t)cc * kMaxDim);
+#pragma unroll
+        for (int v = 0; v < kMaxDim / 8; ++v) {
+            const uint4_t u = src[v];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint16_t h = (uint16_t)((u[e >> 1] >> (16 * (e & 1))) & 0xFFFF);
+                k[8 * v + e] = kKind == 1 ? f16_bits_to_f32(h) : bf16_to_f32(h);
+            }
+        }
+    }
+    float s = 0.0f;
+    for (int h = 0; h < n_head; h += 4) {
+        const float *q0 = q + (size_t)h * kMaxDim;
+        float d[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int v = 0; v < kMaxDim / 4; ++v) {
+            float4_t a[4];
+#pragma unroll
+            for (int z = 0; z < 4; ++z) a[z] = *reinterpret_cast<const float4_t *>(q0 + z * kMaxDim + 4 * v);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int z = 0; z < 4; ++z) d[z] = fmaf(a[z][e], k[4 * v + e], d[z]);
+            // at most 4 x 64 query values in SGPRs at a time (the other waves
+            // of the SIMD cover the scalar loads' latency)
+            if ((v & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int z = 0; z < 4; ++z) s = fmaf(w[h + z], d[z] > 0.0f ? d[z] : 0.0f, s);
+    }
+    if (c < n_comp) scores[c] = s;
+    if (hist) {
+        __syncthreads();
+        if (c < n_cand) atomicAdd(&lh[ord_key(s) >> 21], 1u);
+        __syncthreads();
+        for (int i = threadIdx.x; i < kBins; i += 256)
+            if (lh[i]) atomicAdd(&hist[i], lh[i]);
+    }
+}
+
+// DS4HIP_INDEXER_SGPR_SCORES=1 scores with score_sgpr_kernel (read at every
+// launch; off by default until it has run on the GPU).
+bool sgpr_scores_enabled() {
+    const char *e = getenv("DS4HIP_INDEXER_SGPR_SCORES");
+    return e && e[0] == '1';
+}
+
 __global__ void zero_u32_kernel(unsigned *p, int n) {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0;
 }
@@ -1027,6 +1104,14 @@ int launch_scores(const float *q, const float *w, const void *keys, int kind, in
                   hipStream_t st) {
     const bool full = head_dim == kMaxDim;
     const dim3 grid((n_comp + 255) / 256);
+    if (full && n_head % 4 == 0 && n_comp > 0 && sgpr_scores_enabled()) {
+        switch (kind) {
+        case 0: hipLaunchKernelGGL(score_sgpr_kernel<0>, grid, dim3(256), 0, st, q, w, keys, n_comp, n_head, scores, hist, n_cand); break;
+        case 1: hipLaunchKernelGGL(score_sgpr_kernel<1>, grid, dim3(256), 0, st, q, w, keys, n_comp, n_head, scores, hist, n_cand); break;
+        default: hipLaunchKernelGGL(score_sgpr_kernel<2>, grid, dim3(256), 0, st, q, w, keys, n_comp, n_head, scores, hist, n_cand); break;
+        }
+        return hip_status(hipGetLastError());
+    }
     switch (kind) {
     case 0:
         if (full) hipLaunchKernelGGL((score_kernel<0, true>), grid, dim3(256), 0, st, q, w, keys, n_comp, n_head, head_dim, scores, hist, n_cand);

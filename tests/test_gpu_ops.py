@@ -164,8 +164,8 @@ def test_indexer_positions_with_ties_and_recent(gpu):
     from ds4cuda_amd import lib
     prev = lib().ds4hip_set_indexer_prefilter(0)
     try:
-        # mode 1 (the MFMA prefilter) is disabled until a GPU fault seen with it
-        # is explained; only the exact path runs
+        # the exact path only: the MFMA prefilter (mode 1) has its own test,
+        # test_gpu_prefilter.py, skipped until the prefilter runs again
         for mode in (0,):
             lib().ds4hip_set_indexer_prefilter(mode)
             mask = torch.empty(n_comp, dtype=torch.int32, device=gpu)

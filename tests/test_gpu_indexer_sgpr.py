@@ -12,11 +12,12 @@ import torch
 import oracle as O
 from oracle import P
 from ds4cuda_amd import ops, synth
+from unverified import unverified
 
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.skip(reason="the scalar-operand scorer has not run on the GPU yet")
+@unverified("the scalar-operand scorer has not run on the GPU yet")
 @pytest.mark.parametrize("kind,n_comp", [(0, 1000), (1, 4097), (2, 131072)])
 def test_sgpr_scorer_bit_identical(gpu, kind, n_comp):
     n_head, hd, top_k, recent = 64, 128, 512, 128

@@ -16,6 +16,7 @@ import oracle as O
 from oracle import P
 from ds4cuda_amd import lib, ops, synth
 from test_gpu_ops import t
+from unverified import unverified
 
 
 def reference(qf, w, kb, top_k, recent):
@@ -56,8 +57,9 @@ CASES = {
 
 
 @pytest.mark.gpu
-@pytest.mark.skip(reason="prefilter path disabled: a GPU fault seen in a run that exercised it "
-                         "is not explained yet (the exact path is the default)")
+@unverified("the prefilter is off by default: two runs of a timing variant of it (a fake histogram, "
+            "never part of this code) faulted the GPU; the prefilter itself, since rewritten, has not "
+            "run again")
 @pytest.mark.parametrize("case", list(CASES))
 def test_prefilter_matches_exact_selection(gpu, case):
     n, top_k, recent = CASES[case]

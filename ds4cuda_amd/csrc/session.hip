@@ -20,6 +20,7 @@
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
 #include <vector>
@@ -687,5 +688,198 @@ extern "C" int ds4hip_session_chunk_rows_host(const ds4hip_session_state *s, int
         for (int i = 0; i < n_win; ++i) out[i] = chunk_entry(G, t, i);
         for (int i = 0; i < T.n_sel[t]; ++i) out[n_win + i] = all ? i : sel[(size_t)t * sel_stride + i];
     }
+    return 0;
+}
+
+// ---- import of a reference session file ----------------------------------------------------
+//
+// The reference writes its header and layer metas as their structs
+// (cuda/kv_persist.cu:206-236,246-262; layouts at cuda/kv_persist.cuh:57-88);
+// the fields are read here at their byte offsets, little-endian.
+namespace {
+
+constexpr size_t kRefHdrBytes = 360;
+constexpr size_t kRefMetaBytes = 64;
+constexpr size_t kRefResidualBytes = (size_t)4 * 4096 * 4;   // N_HC x N_EMBD fp32
+
+uint32_t rd_u32(const uint8_t *p) {
+    uint32_t v;
+    std::memcpy(&v, p, 4);
+    return v;
+}
+int32_t rd_i32(const uint8_t *p) {
+    int32_t v;
+    std::memcpy(&v, p, 4);
+    return v;
+}
+uint64_t rd_u64(const uint8_t *p) {
+    uint64_t v;
+    std::memcpy(&v, p, 8);
+    return v;
+}
+
+// Payload bytes of one layer in the reference file.
+uint64_t ref_layer_payload(int ratio, int cap_raw, int cap_comp) {
+    uint64_t b = (uint64_t)cap_raw * DS4HIP_HEAD_DIM * 4;
+    if (ratio) {
+        b += (uint64_t)cap_comp * DS4HIP_HEAD_DIM * 4 + 2 * attn_state_cells(ratio) * 4;
+        if (ratio == 4) b += (uint64_t)cap_comp * DS4HIP_INDEXER_HEAD_DIM * 4 + 2 * index_state_cells() * 4;
+    }
+    return b;
+}
+
+// Reads and checks the file; fills info and each layer's payload offset.
+int ref_probe(FILE *f, ds4hip_ds4cudak_info *info, long long (&payload_off)[DS4HIP_N_LAYER]) {
+    uint8_t h[kRefHdrBytes];
+    if (std::fread(h, 1, kRefHdrBytes, f) != kRefHdrBytes) return kEIO;
+    if (std::memcmp(h, "DS4CUDAK", 8) != 0 || rd_u32(h + 8) != 1u || rd_u32(h + 12) != DS4HIP_N_LAYER)
+        return kEINVAL;
+    const uint32_t max_ctx = rd_u32(h + 16);
+    if (max_ctx == 0 || max_ctx > (1u << 24)) return kEINVAL;
+    const Plan P = make_plan((int)max_ctx);
+    std::memset(info, 0, sizeof(*info));
+    info->max_context = (int)max_ctx;
+    info->pos = (int)rd_u32(h + 20);
+    info->n_tokens_processed = (int)rd_u32(h + 24);
+    info->n_prompt_tokens = (int)rd_u32(h + 28);
+    info->cap_raw = (int)rd_u32(h + 32);
+    if (info->cap_raw != P.cap_raw || info->n_prompt_tokens < 0 ||
+        info->n_prompt_tokens > DS4HIP_KVC_MAX_TOKENS_HDR || info->pos < 0 || info->n_tokens_processed < 0)
+        return kEINVAL;
+    for (int i = 0; i < DS4HIP_KVC_MAX_TOKENS_HDR; ++i) info->prompt_token_ids[i] = rd_i32(h + 40 + 4 * i);
+    long long off = (long long)kRefHdrBytes;
+    for (int il = 0; il < DS4HIP_N_LAYER; ++il) {
+        uint8_t m[kRefMetaBytes];
+        if (std::fseek(f, off, SEEK_SET) != 0 || std::fread(m, 1, kRefMetaBytes, f) != kRefMetaBytes) return kEIO;
+        const int ratio = layer_ratio(il);
+        const int cap_comp = P.cap_comp[il];
+        const int n_raw = rd_i32(m + 20), n_comp = rd_i32(m + 24), n_idx = rd_i32(m + 28);
+        const uint64_t payload = ref_layer_payload(ratio, P.cap_raw, cap_comp);
+        if (rd_i32(m) != il || rd_i32(m + 4) != ratio || rd_i32(m + 8) != (ratio == 4 ? 1 : 0) ||
+            rd_i32(m + 12) != P.cap_raw || rd_i32(m + 16) != cap_comp || n_raw < 0 || n_raw > P.cap_raw ||
+            n_comp < 0 || n_comp > cap_comp || n_idx < 0 || n_idx > cap_comp || (!ratio && n_comp) ||
+            (ratio != 4 && n_idx) || rd_u64(m + 32) != payload)
+            return kEINVAL;
+        info->n_raw[il] = n_raw;
+        info->n_comp[il] = n_comp;
+        info->n_index_comp[il] = n_idx;
+        payload_off[il] = off + (long long)kRefMetaBytes;
+        off = payload_off[il] + (long long)payload;
+    }
+    off += (long long)kRefResidualBytes;
+    char tr[8];
+    if (std::fseek(f, off, SEEK_SET) != 0 || std::fread(tr, 1, 8, f) != 8) return kEIO;
+    if (std::memcmp(tr, "DS4CUDA1", 8) != 0) return kEINVAL;
+    if (std::fgetc(f) != EOF) return kEINVAL;   // nothing after the trailer
+    info->file_bytes = off + 8;
+    return 0;
+}
+
+int read_at(FILE *f, long long off, void *dst, size_t bytes) {
+    if (std::fseek(f, off, SEEK_SET) != 0 || std::fread(dst, 1, bytes, f) != bytes) return kEIO;
+    return 0;
+}
+
+}  // namespace
+
+extern "C" int ds4hip_ds4cudak_probe(const char *path, ds4hip_ds4cudak_info *info) {
+    if (!path || !info) return fail(kEINVAL);
+    File in;
+    in.f = std::fopen(path, "rb");
+    if (!in.f) return fail(kEIO);
+    long long off[DS4HIP_N_LAYER];
+    const int rc = ref_probe(in.f, info, off);
+    return rc ? fail(rc) : 0;
+}
+
+extern "C" int ds4hip_session_import_ds4cudak(ds4hip_session_state *s, const char *path, int *out_pos,
+                                              int *out_n_tokens) {
+    if (!path || !session_ok(s)) return fail(kEINVAL);
+    File in;
+    in.f = std::fopen(path, "rb");
+    if (!in.f) return fail(kEIO);
+    ds4hip_ds4cudak_info info;
+    long long off[DS4HIP_N_LAYER];
+    int rc = ref_probe(in.f, &info, off);
+    if (rc) return fail(rc);
+    if (info.max_context != s->max_context) return fail(kEINVAL);
+    // device staging for one buffer of fp32 rows and their destination rows
+    size_t max_rows = (size_t)s->layers[0].cap_raw;
+    for (int il = 0; il < DS4HIP_N_LAYER; ++il)
+        max_rows = std::max(max_rows, (size_t)s->layers[il].cap_comp);
+    std::vector<float> host(max_rows * DS4HIP_HEAD_DIM);
+    std::vector<long long> dst(max_rows);
+    float *d_rows = nullptr;
+    long long *d_dst = nullptr;
+    struct Free {
+        void *a, *b;
+        ~Free() {
+            if (a) (void)hipFree(a);
+            if (b) (void)hipFree(b);
+        }
+    } guard{nullptr, nullptr};
+    if ((rc = hip_status(hipMalloc(&d_rows, max_rows * DS4HIP_HEAD_DIM * 4)))) return fail(rc);
+    guard.a = d_rows;
+    if ((rc = hip_status(hipMalloc(&d_dst, max_rows * 8)))) return fail(rc);
+    guard.b = d_dst;
+    if ((rc = init_buffers(s, 0))) return fail(rc);
+    // rows [0, n) of the staged buffer into cache rows dst[0..n)
+    auto put_rows = [&](int n) -> int {
+        if (n == 0) return 0;
+        int r = hip_status(hipMemcpy(d_rows, host.data(), (size_t)n * DS4HIP_HEAD_DIM * 4, hipMemcpyHostToDevice));
+        if (!r) r = hip_status(hipMemcpy(d_dst, dst.data(), (size_t)n * 8, hipMemcpyHostToDevice));
+        if (!r)
+            r = ds4hip_fp8_kv_quantize_append(d_rows, n, DS4HIP_HEAD_DIM, DS4HIP_N_ROT, s->codes, s->sexp, s->tail,
+                                              0, d_dst, nullptr);
+        if (!r) r = hip_status(hipDeviceSynchronize());   // the staging buffers are reused
+        return r;
+    };
+    auto copy_in = [&](long long at, void *d, size_t bytes) -> int {
+        int r = read_at(in.f, at, host.data(), bytes);
+        if (!r) r = hip_status(hipMemcpy(d, host.data(), bytes, hipMemcpyHostToDevice));
+        return r;
+    };
+    for (int il = 0; il < DS4HIP_N_LAYER; ++il) {
+        ds4hip_layer_state &L = s->layers[il];
+        const int n_raw = info.n_raw[il];
+        long long at = off[il];
+        // window rows: raw row i holds position base + i
+        const long long P = info.pos >= n_raw ? info.pos
+                          : (info.n_tokens_processed >= n_raw ? info.n_tokens_processed : n_raw);
+        const long long base = P - n_raw;
+        if ((rc = read_at(in.f, at, host.data(), (size_t)L.cap_raw * DS4HIP_HEAD_DIM * 4))) return fail(rc);
+        for (int i = 0; i < n_raw; ++i) dst[i] = L.row_base + L.cap_comp + (base + i) % L.cap_raw;
+        if ((rc = put_rows(n_raw))) return fail(rc);
+        at += (long long)L.cap_raw * DS4HIP_HEAD_DIM * 4;
+        if (L.compress_ratio) {
+            if ((rc = read_at(in.f, at, host.data(), (size_t)L.cap_comp * DS4HIP_HEAD_DIM * 4))) return fail(rc);
+            for (int i = 0; i < info.n_comp[il]; ++i) dst[i] = L.row_base + i;
+            if ((rc = put_rows(info.n_comp[il]))) return fail(rc);
+            at += (long long)L.cap_comp * DS4HIP_HEAD_DIM * 4;
+            const size_t sb = attn_state_cells(L.compress_ratio) * 4;
+            if ((rc = copy_in(at, L.attn_state_kv, sb))) return fail(rc);
+            at += (long long)sb;
+            if ((rc = copy_in(at, L.attn_state_score, sb))) return fail(rc);
+            at += (long long)sb;
+            if (L.has_indexer) {
+                const size_t kb = (size_t)L.cap_comp * DS4HIP_INDEXER_HEAD_DIM * 4;
+                if ((rc = copy_in(at, L.index_comp_kv, kb))) return fail(rc);
+                at += (long long)kb;
+                const size_t ib = index_state_cells() * 4;
+                if ((rc = copy_in(at, L.index_state_kv, ib))) return fail(rc);
+                at += (long long)ib;
+                if ((rc = copy_in(at, L.index_state_score, ib))) return fail(rc);
+            }
+        }
+        L.n_raw = n_raw;
+        L.raw_head = (int)((base + n_raw) % L.cap_raw);
+        L.n_comp = info.n_comp[il];
+        L.n_index_comp = info.n_index_comp[il];
+    }
+    if ((rc = hip_status(hipDeviceSynchronize()))) return fail(rc);
+    s->pos = info.pos;
+    s->n_tokens_processed = info.n_tokens_processed;
+    if (out_pos) *out_pos = s->pos;
+    if (out_n_tokens) *out_n_tokens = s->n_tokens_processed;
     return 0;
 }

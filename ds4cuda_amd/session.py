@@ -39,6 +39,26 @@ class SessionState(C.Structure):
                 ("arena_bytes", C.c_size_t)]
 
 
+class Ds4cudakInfo(C.Structure):
+    """ds4hip_ds4cudak_info: what ds4hip_ds4cudak_probe reads from a
+    reference session file."""
+    _fields_ = [("max_context", C.c_int), ("pos", C.c_int), ("n_tokens_processed", C.c_int),
+                ("cap_raw", C.c_int), ("n_prompt_tokens", C.c_int),
+                ("prompt_token_ids", C.c_int32 * 64), ("n_raw", C.c_int * N_LAYER),
+                ("n_comp", C.c_int * N_LAYER), ("n_index_comp", C.c_int * N_LAYER),
+                ("file_bytes", C.c_longlong)]
+
+
+def probe_ds4cudak(path) -> Ds4cudakInfo:
+    """Checks a reference (fp32, "DS4CUDAK") session file on the host and
+    returns its header fields and per-layer counts; raises Ds4HipError."""
+    info = Ds4cudakInfo()
+    lib().ds4hip_clear_last_error()
+    if lib().ds4hip_ds4cudak_probe(os.fsencode(path), C.byref(info)) != 0:
+        raise Ds4HipError("ds4hip_ds4cudak_probe", lib().ds4hip_get_last_error())
+    return info
+
+
 def swa_push_f32(raw_kv, n_raw, cap_raw, kv_cur, head_dim, stream=None) -> int:
     """Returns the new n_raw."""
     _check(raw_kv, torch.float32, cap_raw * head_dim, "raw_kv")
@@ -111,6 +131,14 @@ class Session:
         """Restores a saved session (same max_context); returns (pos, n_tokens_processed)."""
         pos, n = C.c_int(), C.c_int()
         self._persist("ds4hip_session_load_from_disk", C.byref(self.s), os.fsencode(path),
+                      C.byref(pos), C.byref(n))
+        return pos.value, n.value
+
+    def import_ds4cudak(self, path):
+        """Loads a reference session file (fp32 rows) into this FP8 session
+        (same max_context); returns (pos, n_tokens_processed)."""
+        pos, n = C.c_int(), C.c_int()
+        self._persist("ds4hip_session_import_ds4cudak", C.byref(self.s), os.fsencode(path),
                       C.byref(pos), C.byref(n))
         return pos.value, n.value
 

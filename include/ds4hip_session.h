@@ -242,6 +242,55 @@ int ds4hip_session_save_to_disk(const ds4hip_session_state *s, const int32_t *pr
 int ds4hip_session_load_from_disk(ds4hip_session_state *s_out, const char *path, int *out_pos,
                                   int *out_n_tokens);
 
+/* ---- import of the reference's session files ---------------------------------------
+ *
+ * The reference saves its fp32 session as a "DS4CUDAK" file
+ * (cuda/kv_persist.cuh:6-37,57-88): a header written as its struct (360
+ * bytes: magic, version 1, n_layer 43, max_context, pos, n_tokens_processed,
+ * n_prompt_tokens, cap_raw, a reserved word, 64 prompt token ids, 8 reserved
+ * words), then per layer a 64-byte meta (il, compress_ratio, has_indexer,
+ * cap_raw, cap_comp, n_raw, n_comp, n_index_comp, payload bytes) and the
+ * layer's buffers at full capacity (raw_kv fp32 [cap_raw][512]; on compressed
+ * layers comp_kv [cap_comp][512], attn_state_kv and attn_state_score; on
+ * indexer layers index_comp_kv [cap_comp][128], index_state_kv and
+ * index_state_score), then residual_hc (4 x 4096 fp32) and the trailer
+ * "DS4CUDA1". */
+typedef struct ds4hip_ds4cudak_info {
+    int max_context;
+    int pos;
+    int n_tokens_processed;
+    int cap_raw;
+    int n_prompt_tokens;
+    int32_t prompt_token_ids[DS4HIP_KVC_MAX_TOKENS_HDR];
+    int n_raw[DS4HIP_N_LAYER];
+    int n_comp[DS4HIP_N_LAYER];
+    int n_index_comp[DS4HIP_N_LAYER];
+    long long file_bytes;
+} ds4hip_ds4cudak_info;
+
+/* Reads and checks a reference session file on the host (no device work):
+ * header, every layer meta against the geometry the header's max_context
+ * gives, payload sizes, trailer and file length. Fills *info. Returns 0, or
+ * -1 with -22 (format or geometry) / -5 (I/O, truncation) kept for
+ * ds4hip_get_last_error. (No counterpart in the reference.) */
+int ds4hip_ds4cudak_probe(const char *path, ds4hip_ds4cudak_info *info);
+
+/* Loads a reference session file into an FP8 session of the same
+ * max_context (no counterpart in the reference; the bridge from its fp32
+ * files). The session is reset first. Window rows: raw_kv row i of a layer
+ * holds position base + i, base = P - n_raw with P the header's pos, or
+ * n_tokens_processed when pos is smaller than n_raw, or n_raw when both are;
+ * it is quantized into ring slot (base + i) % cap_raw and raw_head becomes
+ * (base + n_raw) % cap_raw. Compressed rows 0..n_comp-1 are quantized into
+ * the layer's compressed rows; compressor states, indexer keys and indexer
+ * states are copied as they are (the same layouts); residual_hc belongs to
+ * the rest of the layer and is skipped. pos and n_tokens_processed come from
+ * the header. Returns 0 or -1 as ds4hip_session_load_from_disk (the detail in
+ * ds4hip_get_last_error); after a failure past the probe the session is
+ * indeterminate (reset it). Synchronizes the device. */
+int ds4hip_session_import_ds4cudak(ds4hip_session_state *s, const char *path, int *out_pos,
+                                   int *out_n_tokens);
+
 #ifdef __cplusplus
 }
 #endif

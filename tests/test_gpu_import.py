@@ -1,0 +1,79 @@
+"""Import of a reference session file (DS4CUDAK, fp32 rows) into the FP8
+session: counters, ring placement (raw row i of a layer holds position
+pos - n_raw + i and lands in slot (pos - n_raw + i) % 128), FP8 codes of the
+window and compressed rows bit-exact against the oracle's quantization,
+compressor / indexer state copied bit for bit, and decode attention over the
+imported rows against the oracle over the file's rows."""
+import ctypes as C
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+import ds4cudak_file as F
+from ds4cuda_amd import session, synth
+from unverified import unverified
+
+pytestmark = pytest.mark.gpu
+
+
+def d2h(ptr, n):
+    hip = C.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    torch.cuda.synchronize()
+    b = np.empty(n, np.uint8)
+    assert hip.hipMemcpy(b.ctypes.data, ptr, n, 2) == 0
+    return b
+
+
+@unverified("the import of reference session files has not run on the GPU yet")
+def test_import_reference_session(gpu, tmp_path):
+    max_ctx, pos = 256, 203
+    cap_raw, caps = F.geometry(max_ctx)
+    raw0 = synth.kv_rows(501, 0, cap_raw, outlier_frac=0.02).astype(np.float32)
+    raw2 = synth.kv_rows(501, 2, cap_raw).astype(np.float32)
+    comp2 = np.zeros((caps[2], 512), np.float32)
+    comp2[:50] = 2 * synth.kv_rows(501, 3, 50)
+    st_kv = synth.normal(501, 4, F.attn_cells(4)).astype(np.float32)
+    st_sc = synth.normal(501, 5, F.attn_cells(4)).astype(np.float32)
+    idx = np.zeros((caps[2], 128), np.float32)
+    idx[:50] = synth.normal(501, 6, 50 * 128).reshape(50, 128)
+    layers = {0: {"n_raw": cap_raw, "raw": raw0},
+              2: {"n_raw": cap_raw, "raw": raw2, "comp": comp2, "n_comp": 50, "st_kv": st_kv,
+                  "st_sc": st_sc, "idx": idx, "n_idx": 50}}
+    path = tmp_path / "ref.kvc"
+    F.write(path, max_ctx, pos, pos, range(7), layers)
+    s = session.Session(max_ctx)
+    try:
+        assert s.import_ds4cudak(path) == (pos, pos)
+        L0, L2 = s.layer(0), s.layer(2)
+        assert (L0.n_raw, L0.raw_head, L0.n_comp) == (cap_raw, pos % cap_raw, 0)
+        assert (L2.n_raw, L2.n_comp, L2.n_index_comp) == (cap_raw, 50, 50)
+        # FP8 codes of the ring: raw row i in slot (pos - 128 + i) % 128
+        codes, sexp, tail, deq0 = O.fp8_quant_rows(raw0)
+        rows = cap_raw + L0.cap_comp
+        got = d2h(s.s.codes + L0.row_base * 448, rows * 448).reshape(rows, 448)
+        for i in range(cap_raw):
+            assert np.array_equal(got[L0.cap_comp + (pos - cap_raw + i) % cap_raw], codes[i]), i
+        # compressed rows of layer 2 in order
+        c2, _, _, deq_c = O.fp8_quant_rows(comp2[:50])
+        got2 = d2h(s.s.codes + L2.row_base * 448, 50 * 448).reshape(50, 448)
+        assert np.array_equal(got2, c2)
+        # state copied as it is
+        assert np.array_equal(d2h(L2.attn_state_kv, st_kv.nbytes).view(np.float32), st_kv)
+        assert np.array_equal(d2h(L2.attn_state_score, st_sc.nbytes).view(np.float32), st_sc)
+        assert np.array_equal(d2h(L2.index_comp_kv, 50 * 128 * 4).view(np.float32), idx[:50].reshape(-1))
+        # decode over the imported rows against the oracle over the file's rows
+        q = synth.normal(502, 0, 64 * 512).reshape(64, 512).astype(np.float32)
+        sinks = synth.normal(502, 1, 64).astype(np.float32)
+        for il, kv in ((0, raw0), (2, np.concatenate([raw2, comp2[:50]]))):
+            out = torch.empty(64 * 512, device=gpu)
+            s.decode(il, torch.from_numpy(q.reshape(-1)).to(gpu), torch.from_numpy(sinks).to(gpu), out)
+            torch.cuda.synchronize()
+            cq, sq, tq, _ = O.fp8_quant_rows(kv)
+            ref = O.attn_decode_fp8(q, cq, sq, tq, np.arange(kv.shape[0]), sinks)
+            err = np.abs(out.cpu().numpy().reshape(64, 512) - ref).max() / np.sqrt(np.mean(ref.astype(np.float64) ** 2))
+            assert err < 2e-3, (il, err)
+    finally:
+        s.close()

@@ -91,6 +91,7 @@ SIGNATURES: dict[str, list] = {
     "ds4hip_session_load_from_disk": [_vp, C.c_char_p, C.POINTER(_i), C.POINTER(_i)],
     "ds4hip_ds4cudak_probe": [C.c_char_p, _vp],
     "ds4hip_session_import_ds4cudak": [_vp, C.c_char_p, C.POINTER(_i), C.POINTER(_i)],
+    "ds4hip_session_export_ds4cudak": [_vp, _vp, _i, C.c_char_p],
 }
 
 # entry points that return a value rather than a status

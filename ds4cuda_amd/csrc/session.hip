@@ -21,6 +21,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <vector>
@@ -882,4 +883,116 @@ extern "C" int ds4hip_session_import_ds4cudak(ds4hip_session_state *s, const cha
     if (out_pos) *out_pos = s->pos;
     if (out_n_tokens) *out_n_tokens = s->n_tokens_processed;
     return 0;
+}
+
+namespace {
+
+void wr_u32(std::vector<uint8_t> &b, size_t at, uint32_t v) { std::memcpy(b.data() + at, &v, 4); }
+void wr_u64(std::vector<uint8_t> &b, size_t at, uint64_t v) { std::memcpy(b.data() + at, &v, 8); }
+
+// OCP E4M3FN value of code c (0x7F / 0xFF, the NaN codes, never occur in the cache)
+float e4m3_value(uint8_t c) {
+    const int e = (c >> 3) & 15, m = c & 7;
+    const float mag = e == 0 ? std::ldexp((float)m, -9) : std::ldexp(1.0f + m / 8.0f, e - 7);
+    return (c & 0x80) ? -mag : mag;
+}
+
+float f16_bits_to_float(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+// One cache row as fp32: codes times 2^exponent per 64-dim block (rounded to
+// f16 when f16_codes), then the f16 tail.
+void dequant_row(const uint8_t *codes, const int8_t *sexp, const uint16_t *tail, bool f16_codes, float *out) {
+    for (int d = 0; d < DS4HIP_FP8_CODES; ++d) {
+        float v = std::ldexp(e4m3_value(codes[d]), sexp[d >> 6]);
+        if (f16_codes) v = (float)(_Float16)v;
+        out[d] = v;
+    }
+    for (int d = 0; d < DS4HIP_FP8_TAIL; ++d) out[DS4HIP_FP8_CODES + d] = f16_bits_to_float(tail[d]);
+}
+
+}  // namespace
+
+extern "C" int ds4hip_session_export_ds4cudak(const ds4hip_session_state *s, const int32_t *prompt_token_ids,
+                                              int n_tokens, const char *path) {
+    if (!path || !session_ok(s) || n_tokens < 0 || (n_tokens > 0 && !prompt_token_ids)) return fail(kEINVAL);
+    int rc = hip_status(hipDeviceSynchronize());
+    if (rc) return fail(rc);
+    File out;
+    out.f = std::fopen(path, "wb");
+    if (!out.f) return fail(kEIO);
+    std::vector<uint8_t> h(kRefHdrBytes, 0);
+    std::memcpy(h.data(), "DS4CUDAK", 8);
+    wr_u32(h, 8, 1u);
+    wr_u32(h, 12, DS4HIP_N_LAYER);
+    wr_u32(h, 16, (uint32_t)s->max_context);
+    wr_u32(h, 20, (uint32_t)s->pos);
+    wr_u32(h, 24, (uint32_t)s->n_tokens_processed);
+    const int n_ids = n_tokens < DS4HIP_KVC_MAX_TOKENS_HDR ? n_tokens : DS4HIP_KVC_MAX_TOKENS_HDR;
+    wr_u32(h, 28, (uint32_t)n_ids);
+    wr_u32(h, 32, (uint32_t)s->layers[0].cap_raw);
+    for (int i = 0; i < n_ids; ++i) wr_u32(h, 40 + 4 * (size_t)i, (uint32_t)prompt_token_ids[i]);
+    if (std::fwrite(h.data(), 1, h.size(), out.f) != h.size()) return fail(kEIO);
+    std::vector<uint8_t> codes, sexp;
+    std::vector<uint16_t> tail;
+    std::vector<float> rows;
+    auto get = [&](const void *d, void *hp, size_t bytes) {
+        return hip_status(hipMemcpy(hp, d, bytes, hipMemcpyDeviceToHost));
+    };
+    auto put = [&](const void *p, size_t bytes) { return std::fwrite(p, 1, bytes, out.f) == bytes ? 0 : kEIO; };
+    for (int il = 0; il < DS4HIP_N_LAYER; ++il) {
+        const ds4hip_layer_state &L = s->layers[il];
+        const size_t n_rows = (size_t)L.cap_comp + L.cap_raw;
+        codes.resize(n_rows * DS4HIP_FP8_CODES);
+        sexp.resize(n_rows * DS4HIP_FP8_SEXP);
+        tail.resize(n_rows * DS4HIP_FP8_TAIL);
+        if ((rc = get(s->codes + (size_t)L.row_base * DS4HIP_FP8_CODES, codes.data(), codes.size())) ||
+            (rc = get(s->sexp + (size_t)L.row_base * DS4HIP_FP8_SEXP, sexp.data(), sexp.size())) ||
+            (rc = get(s->tail + (size_t)L.row_base * DS4HIP_FP8_TAIL, tail.data(), tail.size() * 2)))
+            return fail(rc);
+        std::vector<uint8_t> m(kRefMetaBytes, 0);
+        wr_u32(m, 0, (uint32_t)il);
+        wr_u32(m, 4, (uint32_t)L.compress_ratio);
+        wr_u32(m, 8, (uint32_t)L.has_indexer);
+        wr_u32(m, 12, (uint32_t)L.cap_raw);
+        wr_u32(m, 16, (uint32_t)L.cap_comp);
+        wr_u32(m, 20, (uint32_t)L.n_raw);
+        wr_u32(m, 24, (uint32_t)L.n_comp);
+        wr_u32(m, 28, (uint32_t)L.n_index_comp);
+        wr_u64(m, 32, ref_layer_payload(L.compress_ratio, L.cap_raw, L.cap_comp));
+        if ((rc = put(m.data(), m.size()))) return fail(rc);
+        auto row = [&](size_t r, bool f16_codes, float *o) {
+            dequant_row(codes.data() + r * DS4HIP_FP8_CODES, (const int8_t *)sexp.data() + r * DS4HIP_FP8_SEXP,
+                        tail.data() + r * DS4HIP_FP8_TAIL, f16_codes, o);
+        };
+        // window rows oldest first, the rest of the capacity zero
+        rows.assign((size_t)L.cap_raw * DS4HIP_HEAD_DIM, 0.0f);
+        for (int i = 0; i < L.n_raw; ++i) {
+            const int slot = ((L.raw_head - L.n_raw + i) % L.cap_raw + L.cap_raw) % L.cap_raw;
+            row((size_t)L.cap_comp + slot, true, rows.data() + (size_t)i * DS4HIP_HEAD_DIM);
+        }
+        if ((rc = put(rows.data(), rows.size() * 4))) return fail(rc);
+        if (L.compress_ratio) {
+            rows.assign((size_t)L.cap_comp * DS4HIP_HEAD_DIM, 0.0f);
+            for (int i = 0; i < L.n_comp; ++i) row((size_t)i, false, rows.data() + (size_t)i * DS4HIP_HEAD_DIM);
+            if ((rc = put(rows.data(), rows.size() * 4))) return fail(rc);
+            std::vector<float> st(attn_state_cells(L.compress_ratio));
+            if ((rc = get(L.attn_state_kv, st.data(), st.size() * 4)) || (rc = put(st.data(), st.size() * 4)) ||
+                (rc = get(L.attn_state_score, st.data(), st.size() * 4)) || (rc = put(st.data(), st.size() * 4)))
+                return fail(rc);
+            if (L.has_indexer) {
+                std::vector<float> kk((size_t)L.cap_comp * DS4HIP_INDEXER_HEAD_DIM), ist(index_state_cells());
+                if ((rc = get(L.index_comp_kv, kk.data(), kk.size() * 4)) || (rc = put(kk.data(), kk.size() * 4)) ||
+                    (rc = get(L.index_state_kv, ist.data(), ist.size() * 4)) ||
+                    (rc = put(ist.data(), ist.size() * 4)) ||
+                    (rc = get(L.index_state_score, ist.data(), ist.size() * 4)) ||
+                    (rc = put(ist.data(), ist.size() * 4)))
+                    return fail(rc);
+            }
+        }
+    }
+    std::vector<uint8_t> zeros(kRefResidualBytes, 0);
+    if ((rc = put(zeros.data(), zeros.size())) || (rc = put("DS4CUDA1", 8))) return fail(rc);
+    const int cr = std::fclose(out.f);
+    out.f = nullptr;
+    return cr == 0 ? 0 : fail(kEIO);
 }

@@ -142,6 +142,13 @@ class Session:
                       C.byref(pos), C.byref(n))
         return pos.value, n.value
 
+    def export_ds4cudak(self, path, prompt_token_ids=None):
+        """Writes this session as a reference (fp32, "DS4CUDAK") session file."""
+        ids = [] if prompt_token_ids is None else [int(t) for t in prompt_token_ids]
+        arr = (C.c_int32 * max(len(ids), 1))(*ids)
+        self._persist("ds4hip_session_export_ds4cudak", C.byref(self.s), arr if ids else None, len(ids),
+                      os.fsencode(path))
+
     @staticmethod
     def _persist(name, *args):
         # these two return -1 on any error (the reference's convention); the

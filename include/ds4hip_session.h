@@ -291,6 +291,18 @@ int ds4hip_ds4cudak_probe(const char *path, ds4hip_ds4cudak_info *info);
 int ds4hip_session_import_ds4cudak(ds4hip_session_state *s, const char *path, int *out_pos,
                                    int *out_n_tokens);
 
+/* Writes the session as a reference session file that the reference's
+ * ds4_session_save/load format describes (no counterpart in the reference;
+ * the way back from the FP8 session). Window rows are written oldest first
+ * (ring slot (raw_head - n_raw + i) % cap_raw as raw row i), dequantized and
+ * f16-rounded as the reference's window holds them; compressed rows are
+ * dequantized (their RoPE tail is the cache's f16 value); compressor and
+ * indexer state are copied; residual_hc, which this session does not hold,
+ * is written as zeros. At most the first 64 prompt token ids are stored.
+ * Returns 0 or -1 as ds4hip_session_save_to_disk. Synchronizes the device. */
+int ds4hip_session_export_ds4cudak(const ds4hip_session_state *s, const int32_t *prompt_token_ids,
+                                   int n_tokens, const char *path);
+
 #ifdef __cplusplus
 }
 #endif

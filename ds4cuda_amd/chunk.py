@@ -62,10 +62,16 @@ def forward_chunk_attn(session, il, p0, attn_norm, q_lora_norm, q_cur, kv_rope, 
     q_cur [n, 64, 512], kv_rope [n, 512] fp32 (the producer's outputs, e.g.
     ops.attn_qkv_decode_f32 per token); sinks [64]; out [n, 64, 512] receives
     each token's attention output (Step 13's kqv). Returns the workspace."""
-    from .ops import decode_fp8_workspace_bytes
+    from .ops import _check, decode_fp8_workspace_bytes
     n = kv_rope.shape[0]
     if not 0 < n <= CHUNK_MAX:
         raise Ds4HipError("chunk of 1..128 tokens", -22)
+    _check(kv_rope, torch.float32, n * HEAD_DIM, "kv_rope")
+    _check(attn_norm, torch.float32, n * N_EMBD, "attn_norm")
+    _check(q_lora_norm, torch.float32, n * 1024, "q_lora_norm")
+    _check(q_cur, torch.float32, n * N_HEAD * HEAD_DIM, "q_cur")
+    _check(sinks, torch.float32, N_HEAD, "sinks")
+    _check(out, torch.float32, n * N_HEAD * HEAD_DIM, "out")
     s = session.s
     L = s.layers[il]
     ratio = L.compress_ratio

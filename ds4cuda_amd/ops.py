@@ -38,6 +38,10 @@ def _stream(stream):
 def _check(t, dtype, numel=None, name="tensor"):
     if t is None:
         return
+    if t.device.type != "cuda":
+        # the kernels read and write these buffers: host memory here would
+        # fault the GPU instead of failing the call
+        raise Ds4HipError(f"{name}: expected a GPU tensor, got one on {t.device}", -22)
     if t.dtype != dtype or not t.is_contiguous():
         raise Ds4HipError(f"{name}: expected contiguous {dtype}, got {t.dtype}", -22)
     if numel is not None and t.numel() < numel:

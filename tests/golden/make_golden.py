@@ -23,7 +23,13 @@ the oracle's code:
   rms_norm    one 4096 row with a weight (cuda/norm.cu:4-7); checked in fp64
   compressor  8 ratio-4 attention steps (two emits) and 8 indexer-compressor
               steps with fp32 weights (cuda/compressor.cu:64-349); the emitted
-              rows and final states are recorded
+              rows and final states are recorded; 128 ratio-128 steps (one
+              emit)
+  prefill     2 queries over 40 cached rows + causal self (the chunked prefill
+              the reference runs token by token); checked per query in fp64
+  q8_grouped  Q8_0 x Q8_0 grouped matvec, 2 groups x rank 16
+              (cuda/attn_out.cu:119-197); checked against exact int32 block
+              sums scaled in fp64
 
 Run from the repository root: python tests/golden/make_golden.py
 """
@@ -256,6 +262,85 @@ def main():
         put(case, "state_kv", skv)
         put(case, "state_score", ssc, in_dim=in_dim, head_dim=hd, ratio=4, il=2, steps=steps,
             positions="0..7 from a fresh state")
+
+    # ---- prefill: 2 queries (64 heads) over 40 cached rows + causal self
+    n_cached, n_q = 40, 2
+    xp = synth.kv_rows(408, 0, n_cached + n_q, outlier_frac=0.1).astype(np.float32)
+    cp, sp, tp, dp = O.fp8_quant_rows(xp)
+    qp = synth.bf16_bits_to_f32(synth.to_bf16_bits(synth.normal(408, 1, n_q * 64 * 512))).reshape(n_q, 64, 512)
+    sinks_p = synth.normal(408, 2, 64).astype(np.float32)
+    outp = np.zeros_like(qp)
+    O.lib().orc_attn_prefill_fp8(P(np.ascontiguousarray(qp)), C.c_int(n_q), P(cp), P(sp), P(tp),
+                                 C.c_int(n_cached), P(sinks_p), P(outp), C.c_int(64), C.c_int(512),
+                                 C.c_int(64), C.c_int(1))
+    kvp = dp.astype(np.float16).astype(np.float64)
+    for t in range(n_q):
+        kt = kvp[:n_cached + t + 1]
+        ref = attn64(qp[t].astype(np.float64), kt, kt, sinks_p.astype(np.float64), 1 / np.sqrt(512))
+        assert rel(outp[t], ref) < 1e-5, (t, rel(outp[t], ref))
+    put("prefill", "kv_src", xp)
+    put("prefill", "q", qp)
+    put("prefill", "sinks", sinks_p)
+    put("prefill", "out", outp, n_cached=n_cached, n_q=n_q,
+        note="query t attends rows 0 .. n_cached + t of kv_src after the FP8 rule")
+
+    # ---- Q8_0 x Q8_0 grouped matvec: 2 groups of 256 inputs, rank 16
+    n_groups, group_dim, rank = 2, 256, 16
+    wq = (0.05 * synth.normal(409, 0, n_groups * rank * group_dim)).reshape(n_groups * rank, group_dim)
+    blocks = wq.reshape(n_groups * rank, group_dim // 32, 32)
+    d16 = (np.abs(blocks).max(axis=2) / 127.0).astype(np.float16)
+    df = d16.astype(np.float64)
+    qw = np.clip(np.where(df[..., None] > 0, np.rint(blocks / np.where(df > 0, df, 1)[..., None]), 0), -128, 127)
+    qw = qw.astype(np.int8)
+    Wb = np.zeros((n_groups * rank, group_dim // 32, 34), np.uint8)
+    Wb[..., :2] = d16.view(np.uint8).reshape(n_groups * rank, group_dim // 32, 2)
+    Wb[..., 2:] = qw.view(np.uint8)
+    Wb = Wb.reshape(n_groups * rank, -1)
+    xg = synth.normal(409, 1, n_groups * group_dim).astype(np.float32)
+    yg = np.zeros(n_groups * rank, np.float32)
+    O.lib().orc_q8_grouped_matvec(P(np.ascontiguousarray(Wb)), P(xg), P(yg), C.c_int(n_groups),
+                                  C.c_int(group_dim), C.c_int(rank))
+    # independent: per-32 activation quantization (d = amax / 127, round to
+    # nearest even) and the int32 sums, each block scaled by d_w * d_x, in fp64
+    xb = xg.astype(np.float64).reshape(-1, 32)
+    dx = np.abs(xb).max(axis=1) / 127.0
+    xq = np.clip(np.rint(xb / np.where(dx > 0, dx, 1)[:, None]), -127, 127)
+    ref = np.zeros(n_groups * rank)
+    for r in range(n_groups * rank):
+        g = r // rank
+        for b in range(group_dim // 32):
+            isum = int(np.dot(qw[r, b].astype(np.int64), xq[g * group_dim // 32 + b].astype(np.int64)))
+            ref[r] += float(df[r, b]) * dx[g * group_dim // 32 + b] * isum
+    assert rel(yg, ref) < 1e-5, rel(yg, ref)
+    put("q8_grouped", "w_q8", Wb.astype(np.int32))
+    put("q8_grouped", "x", xg)
+    put("q8_grouped", "y", yg, n_groups=n_groups, group_dim=group_dim, rank=rank,
+        note="w_q8 holds the block_q8_0 bytes (f16 d, 32 int8), one per int32")
+
+    # ---- compressor, ratio 128 (fp32 weights, in_dim 16, il 3): 128 steps, one emit
+    in_dim, hd = 16, 512
+    wkv = (0.2 * synth.normal(410, 0, hd * in_dim)).reshape(hd, in_dim).astype(np.float32)
+    wg = (0.2 * synth.normal(410, 1, hd * in_dim)).reshape(hd, in_dim).astype(np.float32)
+    ape = (0.1 * synth.normal(410, 2, 128 * hd)).astype(np.float16).reshape(128, hd)
+    wnorm = (1 + 0.1 * synth.normal(410, 3, hd)).astype(np.float32)
+    xs = synth.normal(410, 4, 128 * in_dim).reshape(128, in_dim).astype(np.float32)
+    skv = np.zeros((128, hd), np.float32)
+    ssc = np.full((128, hd), -np.inf, np.float32)
+    emit = None
+    for p in range(128):
+        e = np.zeros(hd, np.float32)
+        r = O.lib().orc_compressor_step_w32(
+            C.c_int(1), P(xs[p]), P(wkv), P(wg), P(np.ascontiguousarray(ape.view(np.uint16))), P(wnorm),
+            C.c_int(in_dim), C.c_int(hd), C.c_int(128), C.c_int(p), C.c_int(3), P(skv), P(ssc), P(e))
+        assert r == int(p == 127)
+        if r:
+            emit = e
+    put("compressor_r128", "w_kv", wkv)
+    put("compressor_r128", "w_gate", wg)
+    put("compressor_r128", "ape", ape)
+    put("compressor_r128", "w_norm", wnorm)
+    put("compressor_r128", "x", xs)
+    put("compressor_r128", "emit", emit, in_dim=in_dim, head_dim=hd, ratio=128, il=3, steps=128)
 
     (HERE / "index.json").write_text(json.dumps(idx, indent=1, sort_keys=True) + "\n")
     total = sum((HERE / t["file"]).stat().st_size for c in idx.values() for t in c["tensors"].values())

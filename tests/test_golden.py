@@ -134,3 +134,48 @@ def test_dsst_rejects_bad_files(tmp_path):
         p.write_bytes(bad)
         with pytest.raises(ValueError):
             dsst.read(p)
+
+
+def test_prefill():
+    src, q, sinks = T("prefill", "kv_src"), T("prefill", "q"), T("prefill", "sinks")
+    n_cached = INDEX["prefill"]["params"]["n_cached"]
+    c, s, t, dq = O.fp8_quant_rows(src)
+    out = np.zeros_like(q)
+    O.lib().orc_attn_prefill_fp8(P(np.ascontiguousarray(q)), C.c_int(q.shape[0]), P(c), P(s), P(t),
+                                 C.c_int(n_cached), P(sinks), P(out), C.c_int(64), C.c_int(512), C.c_int(64),
+                                 C.c_int(1))
+    assert np.array_equal(out, T("prefill", "out"))
+    kv = dq.astype(np.float16).astype(np.float64)
+    for i in range(q.shape[0]):
+        k = kv[:n_cached + i + 1]
+        assert MG.rel(out[i], MG.attn64(q[i].astype(np.float64), k, k, sinks.astype(np.float64),
+                                        1 / np.sqrt(512))) < 1e-5
+
+
+def test_q8_grouped():
+    prm = INDEX["q8_grouped"]["params"]
+    w = np.ascontiguousarray(T("q8_grouped", "w_q8").astype(np.uint8))
+    x = T("q8_grouped", "x")
+    y = np.zeros(prm["n_groups"] * prm["rank"], np.float32)
+    O.lib().orc_q8_grouped_matvec(P(w), P(x), P(y), C.c_int(prm["n_groups"]), C.c_int(prm["group_dim"]),
+                                  C.c_int(prm["rank"]))
+    assert np.array_equal(y, T("q8_grouped", "y"))
+
+
+def test_compressor_ratio128():
+    case = "compressor_r128"
+    prm = INDEX[case]["params"]
+    wkv, wg, ape = T(case, "w_kv"), T(case, "w_gate"), T(case, "ape")
+    wn, xs = T(case, "w_norm"), T(case, "x")
+    hd = prm["head_dim"]
+    skv = np.zeros((128, hd), np.float32)
+    ssc = np.full((128, hd), -np.inf, np.float32)
+    emit = None
+    for p in range(prm["steps"]):
+        e = np.zeros(hd, np.float32)
+        if O.lib().orc_compressor_step_w32(C.c_int(1), P(np.ascontiguousarray(xs[p])), P(wkv), P(wg),
+                                           P(np.ascontiguousarray(ape.view(np.uint16))), P(wn),
+                                           C.c_int(prm["in_dim"]), C.c_int(hd), C.c_int(128), C.c_int(p),
+                                           C.c_int(prm["il"]), P(skv), P(ssc), P(e)):
+            emit = e
+    assert emit is not None and np.array_equal(emit, T(case, "emit"))

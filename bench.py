@@ -35,13 +35,12 @@ MFMA_PEAK_TFLOPS = 2500.0                          # dense f16 / bf16
 COPY_BYTES = 1 << 30                               # --copy-calibration: 1 GiB read + 1 GiB written
 # HBM bytes per launch of the cfg-2 partial kernel, measured with rocprofv3
 # (FETCH_SIZE + WRITE_SIZE, each scaled by what the counter reads for
-# `--copy-calibration`); the counter summary and its commands are in
-# profiles/decode_fp8_cfg2_traffic.md. They were counted for the
-# register-load kernel (decode_ws_kernel, DS4HIP_DECODE_KERNEL=ws); the
-# flat-stage kernel that runs by default has not been counted, so its line
-# reports traffic null. Re-measure after a kernel change.
-TRAFFIC_BYTES_PER_LAUNCH = {"ws": 882340981}
-TRAFFIC_MEASURED_AT = {"ws": "22db79c"}            # commit whose partial kernel was counted
+# `--copy-calibration`); the counter summaries and their commands are in
+# profiles/decode_flat_kernel_cfg2_traffic.md (flat kernel) and
+# profiles/decode_ws_kernel_cfg2_traffic.md (register-load kernel).
+# Re-measure after a kernel change.
+TRAFFIC_BYTES_PER_LAUNCH = {"ws": 882340981, "flat": 882148944}
+TRAFFIC_MEASURED_AT = {"ws": "22db79c", "flat": "dedad2c"}   # commit whose partial kernel was counted
 DECODE_KERNEL = "ws" if os.environ.get("DS4HIP_DECODE_KERNEL", "").startswith("w") else "flat"
 KERNEL_LABEL = {"ws": "decode_ws_kernel<0, false> (direct rows, register loads, one f16 P)",
                 "lean": "decode_flat_kernel<false, true> (flat stages, lean producer form, one f16 P)",

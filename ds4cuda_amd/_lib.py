@@ -78,6 +78,7 @@ SIGNATURES: dict[str, list] = {
     "ds4hip_session_push_index_comp": [_vp, _i, _vp, _vp],
     "ds4hip_rows_scatter_f32": [_vp, _i, _i, _vp, _vp, _vp],
     "ds4hip_session_layer_rows": [_vp, _i, _i, C.POINTER(_vp), C.POINTER(_ll), C.POINTER(_vp)],
+    "ds4hip_session_set_selection": [_vp, _i, _vp, _i, _vp],
     "ds4hip_rms_norm_f32": [_vp, _vp, _vp, _i, C.c_float, _vp],
     "ds4hip_rms_norm_batch_f32": [_vp, _vp, _i, _vp, _i, _i, C.c_float, _vp],
     "ds4hip_attn_qkv_decode_workspace_bytes": [],

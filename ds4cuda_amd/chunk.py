@@ -136,8 +136,16 @@ def forward_chunk_attn(session, il, p0, attn_norm, q_lora_norm, q_cur, kv_rope, 
                      _ptr(sel[t]), st)
                 n_sel[t] = layer.top_k
     # 3. all tokens' attention in one decode launch
-    stride = (min(p0, 128) + n + int(n_comp.max()) + 63) // 64 * 64
+    # list stride: the longest token list (window rows still in the ring, the
+    # chunk's own rows up to the token, its compressed rows), from the layer's
+    # ring capacity; ds4hip_session_chunk_rows refuses a stride too short
+    n_ring0 = min(p0, L.cap_raw - 1)
+    stride = (n_ring0 + n + int(n_sel.max()) + 63) // 64 * 64
     lists = torch.empty((n, stride), dtype=torch.int32, device=dev)
+    # the decode and the list kernel read these on the device
+    _check(lists, torch.int32, n * stride, "lists")
+    if sel is not None:
+        _check(sel, torch.int32, n * layer.top_k, "sel")
     counts = (C.c_longlong * n)()
     call("ds4hip_session_chunk_rows", C.byref(s), il, p0, n, n_comp.ctypes.data_as(C.c_void_p),
          n_sel.ctypes.data_as(C.c_void_p), _ptr(sel), sel.shape[1] if sel is not None else 0, _ptr(lists),
@@ -154,6 +162,10 @@ def forward_chunk_attn(session, il, p0, attn_norm, q_lora_norm, q_cur, kv_rope, 
          N_HEAD * HEAD_DIM, _vp(s.codes + rb * 448), _vp(s.sexp + rb * 8), _vp(s.tail + rb * 128),
          C.cast(counts, C.c_void_p), n, None, 0, _ptr(lists), stride, None, 0, 256, N_HEAD, HEAD_DIM,
          N_ROT, _ptr(workspace), workspace.numel(), 3, st)
+    # the last token's selection stays in the layer's row list, where the
+    # token-by-token loop leaves it
+    if sel is not None and n_sel[-1] < n_comp[-1]:
+        call("ds4hip_session_set_selection", C.byref(s), il, _ptr(sel[n - 1]), int(n_sel[-1]), st)
     # 4. the chunk's rows into the ring, in position order
     for t in range(n):
         session.push_raw(il, kv_rope[t], stream=stream)

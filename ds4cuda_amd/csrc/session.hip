@@ -373,6 +373,16 @@ extern "C" int ds4hip_session_layer_rows(const ds4hip_session_state *s, int il, 
     return 0;
 }
 
+extern "C" int ds4hip_session_set_selection(ds4hip_session_state *s, int il, const int32_t *sel, int n,
+                                            void *stream) {
+    if (!layer_ok(s, il) || n < 0 || (n && !sel)) return ds4hip_set_last_error(kEINVAL);
+    const ds4hip_layer_state *L = &s->layers[il];
+    if (n > L->cap_comp) return ds4hip_set_last_error(kEINVAL);
+    if (!n) return 0;
+    return ds4hip_set_last_error(hip_status(hipMemcpyAsync(L->row_list + L->cap_raw, sel, (size_t)n * 4,
+                                                           hipMemcpyDeviceToDevice, (hipStream_t)stream)));
+}
+
 namespace {
 // dst[dst_rows[r]][:] = src[r][:] for r < n_rows; one 64-lane wave per row,
 // 16-byte moves (width % 4 == 0).
@@ -640,6 +650,9 @@ int chunk_plan(const ds4hip_session_state *s, int il, int p0, int n_tok, const i
         return kEINVAL;
     const ds4hip_layer_state *L = &s->layers[il];
     if (L->cap_raw <= 0) return kEINVAL;
+    // the chunk stays inside the session's positions, and a token's window
+    // (at most cap_raw rows) can hold the chunk's own rows up to it
+    if ((long long)p0 + n_tok > s->max_context || n_tok > L->cap_raw) return kEINVAL;
     // the ring holds exactly the positions < p0 (one push per position)
     if (L->n_raw != (p0 < L->cap_raw ? p0 : L->cap_raw) || L->raw_head != p0 % L->cap_raw) return kEINVAL;
     G = ChunkGeom{p0, L->cap_raw, L->cap_comp, (int)(s->n_cache_rows - L->row_base)};
@@ -804,11 +817,21 @@ extern "C" int ds4hip_session_import_ds4cudak(ds4hip_session_state *s, const cha
     int rc = ref_probe(in.f, &info, off);
     if (rc) return fail(rc);
     if (info.max_context != s->max_context) return fail(kEINVAL);
-    // device staging for one buffer of fp32 rows and their destination rows
+    // device staging for one buffer of fp32 rows and their destination rows;
+    // the host bounce buffer also receives whole compressor / indexer states,
+    // which at small contexts are larger than the row buffers
     size_t max_rows = (size_t)s->layers[0].cap_raw;
-    for (int il = 0; il < DS4HIP_N_LAYER; ++il)
-        max_rows = std::max(max_rows, (size_t)s->layers[il].cap_comp);
-    std::vector<float> host(max_rows * DS4HIP_HEAD_DIM);
+    size_t host_floats = 0;
+    for (int il = 0; il < DS4HIP_N_LAYER; ++il) {
+        const ds4hip_layer_state &L = s->layers[il];
+        max_rows = std::max(max_rows, (size_t)std::max(L.cap_comp, L.cap_raw));
+        if (L.compress_ratio) host_floats = std::max(host_floats, attn_state_cells(L.compress_ratio));
+        if (L.has_indexer)
+            host_floats = std::max({host_floats, index_state_cells(),
+                                    (size_t)L.cap_comp * DS4HIP_INDEXER_HEAD_DIM});
+    }
+    host_floats = std::max(host_floats, max_rows * DS4HIP_HEAD_DIM);
+    std::vector<float> host(host_floats);
     std::vector<long long> dst(max_rows);
     float *d_rows = nullptr;
     long long *d_dst = nullptr;
@@ -824,6 +847,13 @@ extern "C" int ds4hip_session_import_ds4cudak(ds4hip_session_state *s, const cha
     if ((rc = hip_status(hipMalloc(&d_dst, max_rows * 8)))) return fail(rc);
     guard.b = d_dst;
     if ((rc = init_buffers(s, 0))) return fail(rc);
+    // From here on the session is being overwritten: any failure leaves it
+    // reset (empty, counters 0), never a mix of old counters and new rows.
+    auto fail_reset = [&](int code) {
+        (void)init_buffers(s, 0);
+        (void)hipDeviceSynchronize();
+        return fail(code);
+    };
     // rows [0, n) of the staged buffer into cache rows dst[0..n)
     auto put_rows = [&](int n) -> int {
         if (n == 0) return 0;
@@ -836,6 +866,7 @@ extern "C" int ds4hip_session_import_ds4cudak(ds4hip_session_state *s, const cha
         return r;
     };
     auto copy_in = [&](long long at, void *d, size_t bytes) -> int {
+        if (bytes > host.size() * sizeof(float)) return kEINVAL;
         int r = read_at(in.f, at, host.data(), bytes);
         if (!r) r = hip_status(hipMemcpy(d, host.data(), bytes, hipMemcpyHostToDevice));
         return r;
@@ -848,28 +879,28 @@ extern "C" int ds4hip_session_import_ds4cudak(ds4hip_session_state *s, const cha
         const long long P = info.pos >= n_raw ? info.pos
                           : (info.n_tokens_processed >= n_raw ? info.n_tokens_processed : n_raw);
         const long long base = P - n_raw;
-        if ((rc = read_at(in.f, at, host.data(), (size_t)L.cap_raw * DS4HIP_HEAD_DIM * 4))) return fail(rc);
+        if ((rc = read_at(in.f, at, host.data(), (size_t)L.cap_raw * DS4HIP_HEAD_DIM * 4))) return fail_reset(rc);
         for (int i = 0; i < n_raw; ++i) dst[i] = L.row_base + L.cap_comp + (base + i) % L.cap_raw;
-        if ((rc = put_rows(n_raw))) return fail(rc);
+        if ((rc = put_rows(n_raw))) return fail_reset(rc);
         at += (long long)L.cap_raw * DS4HIP_HEAD_DIM * 4;
         if (L.compress_ratio) {
-            if ((rc = read_at(in.f, at, host.data(), (size_t)L.cap_comp * DS4HIP_HEAD_DIM * 4))) return fail(rc);
+            if ((rc = read_at(in.f, at, host.data(), (size_t)L.cap_comp * DS4HIP_HEAD_DIM * 4))) return fail_reset(rc);
             for (int i = 0; i < info.n_comp[il]; ++i) dst[i] = L.row_base + i;
-            if ((rc = put_rows(info.n_comp[il]))) return fail(rc);
+            if ((rc = put_rows(info.n_comp[il]))) return fail_reset(rc);
             at += (long long)L.cap_comp * DS4HIP_HEAD_DIM * 4;
             const size_t sb = attn_state_cells(L.compress_ratio) * 4;
-            if ((rc = copy_in(at, L.attn_state_kv, sb))) return fail(rc);
+            if ((rc = copy_in(at, L.attn_state_kv, sb))) return fail_reset(rc);
             at += (long long)sb;
-            if ((rc = copy_in(at, L.attn_state_score, sb))) return fail(rc);
+            if ((rc = copy_in(at, L.attn_state_score, sb))) return fail_reset(rc);
             at += (long long)sb;
             if (L.has_indexer) {
                 const size_t kb = (size_t)L.cap_comp * DS4HIP_INDEXER_HEAD_DIM * 4;
-                if ((rc = copy_in(at, L.index_comp_kv, kb))) return fail(rc);
+                if ((rc = copy_in(at, L.index_comp_kv, kb))) return fail_reset(rc);
                 at += (long long)kb;
                 const size_t ib = index_state_cells() * 4;
-                if ((rc = copy_in(at, L.index_state_kv, ib))) return fail(rc);
+                if ((rc = copy_in(at, L.index_state_kv, ib))) return fail_reset(rc);
                 at += (long long)ib;
-                if ((rc = copy_in(at, L.index_state_score, ib))) return fail(rc);
+                if ((rc = copy_in(at, L.index_state_score, ib))) return fail_reset(rc);
             }
         }
         L.n_raw = n_raw;
@@ -877,7 +908,7 @@ extern "C" int ds4hip_session_import_ds4cudak(ds4hip_session_state *s, const cha
         L.n_comp = info.n_comp[il];
         L.n_index_comp = info.n_index_comp[il];
     }
-    if ((rc = hip_status(hipDeviceSynchronize()))) return fail(rc);
+    if ((rc = hip_status(hipDeviceSynchronize()))) return fail_reset(rc);
     s->pos = info.pos;
     s->n_tokens_processed = info.n_tokens_processed;
     if (out_pos) *out_pos = s->pos;

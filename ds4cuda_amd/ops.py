@@ -48,6 +48,19 @@ def _check(t, dtype, numel=None, name="tensor"):
         raise Ds4HipError(f"{name}: needs {numel} elements, has {t.numel()}", -22)
 
 
+def _dev(t, name, nbytes=None):
+    """Device-memory check for a buffer the kernels use as raw bytes
+    (workspaces, scratch): any dtype, but on the GPU and large enough."""
+    if t is None:
+        raise Ds4HipError(f"{name}: a GPU tensor is required", -22)
+    if t.device.type != "cuda":
+        raise Ds4HipError(f"{name}: expected a GPU tensor, got one on {t.device}", -22)
+    if not t.is_contiguous():
+        raise Ds4HipError(f"{name}: expected a contiguous tensor", -22)
+    if nbytes is not None and t.numel() * t.element_size() < nbytes:
+        raise Ds4HipError(f"{name}: needs {nbytes} bytes, has {t.numel() * t.element_size()}", -22)
+
+
 # ---- fp8_kv (cuda/fp8_kv.cuh:62) ---------------------------------------------------
 
 def launch_fp8_kv_quantize_round_trip_f32(kv_in, kv_out, n_rows, head_dim, n_rot, stream=None):
@@ -112,6 +125,7 @@ def launch_flash_attn_decode_raw_f32_prealloc(Q, K, V, sinks, out, n_head, n_kv,
                      (V, n_kv * head_dim, "V"), (sinks, n_head, "sinks"),
                      (out, n_head * head_dim, "out")):
         _check(t, torch.float32, n, nm)
+    _dev(workspace, "workspace")
     call("ds4hip_flash_attn_decode_raw_f32_prealloc", _ptr(Q), _ptr(K), _ptr(V), _ptr(sinks),
          _ptr(out), n_head, n_kv, head_dim, _ptr(workspace), workspace.numel(), _stream(stream))
 
@@ -122,6 +136,8 @@ def launch_flash_attn_decode_mixed_f32(Q, raw_kv, comp_kv, comp_allowed, sinks, 
     _check(raw_kv, torch.float32, n_raw * head_dim, "raw_kv")
     _check(comp_kv, torch.float32, n_comp * head_dim, "comp_kv")
     _check(comp_allowed, torch.int32, n_comp, "comp_allowed")
+    _check(sinks, torch.float32, n_head, "sinks")
+    _check(out, torch.float32, n_head * head_dim, "out")
     call("ds4hip_flash_attn_decode_mixed_f32", _ptr(Q), _ptr(raw_kv), _ptr(comp_kv),
          _ptr(comp_allowed), _ptr(sinks), _ptr(out), n_head, n_raw, n_comp, head_dim,
          _stream(stream))
@@ -134,6 +150,9 @@ def launch_flash_attn_decode_mixed_f32_prealloc(Q, raw_kv, comp_kv, comp_allowed
     _check(raw_kv, torch.float32, n_raw * head_dim, "raw_kv")
     _check(comp_kv, torch.float32, n_comp * head_dim, "comp_kv")
     _check(comp_allowed, torch.int32, n_comp, "comp_allowed")
+    _check(sinks, torch.float32, n_head, "sinks")
+    _check(out, torch.float32, n_head * head_dim, "out")
+    _dev(workspace, "workspace")
     call("ds4hip_flash_attn_decode_mixed_f32_prealloc", _ptr(Q), _ptr(raw_kv), _ptr(comp_kv),
          _ptr(comp_allowed), _ptr(sinks), _ptr(out), n_head, n_raw, n_comp, head_dim,
          _ptr(workspace), workspace.numel(), _stream(stream))
@@ -170,6 +189,7 @@ def flash_attn_decode_fp8(q, sinks, out, cache: Fp8KVCache, n_rows_per_prob, *, 
     need = decode_fp8_workspace_bytes(n_rows_per_prob)
     if workspace is None or workspace.numel() < need:
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    _dev(workspace, "workspace", need)
     call("ds4hip_flash_attn_decode_fp8", _ptr(q), int(q.dtype == torch.float32),
          N_HEAD * HEAD_DIM, _ptr(sinks), N_HEAD, _ptr(out), N_HEAD * HEAD_DIM,
          _ptr(cache.codes), _ptr(cache.sexp), _ptr(cache.tail), C.cast(counts, C.c_void_p),
@@ -241,6 +261,8 @@ def launch_mul_mv_q8_0_q8_0_grouped_f32(W, x, y, n_groups, group_dim, rank, stre
 def launch_mul_mv_q8_0_q8_0_grouped_f32_prealloc(W, x, y, n_groups, group_dim, rank, scratch_xq,
                                                  scratch_xscale, stream=None):
     _check(W, torch.uint8, n_groups * rank * (group_dim // 32) * 34, "W")
+    _check(x, torch.float32, n_groups * group_dim, "x")
+    _check(y, torch.float32, n_groups * rank, "y")
     _check(scratch_xq, torch.int8, n_groups * group_dim, "scratch_xq")
     _check(scratch_xscale, torch.float32, n_groups * group_dim // 32, "scratch_xscale")
     call("ds4hip_mul_mv_q8_0_q8_0_grouped_f32_prealloc", _ptr(W), _ptr(x), _ptr(y), n_groups,
@@ -250,6 +272,8 @@ def launch_mul_mv_q8_0_q8_0_grouped_f32_prealloc(W, x, y, n_groups, group_dim, r
 def launch_mul_mv_q8_0_q8_0_f32_prealloc(W, x, y, n_rows, n_cols, scratch_xq, scratch_xscale,
                                          stream=None):
     _check(W, torch.uint8, n_rows * (n_cols // 32) * 34, "W")
+    _check(x, torch.float32, n_cols, "x")
+    _check(y, torch.float32, n_rows, "y")
     _check(scratch_xq, torch.int8, n_cols, "scratch_xq")
     _check(scratch_xscale, torch.float32, n_cols // 32, "scratch_xscale")
     call("ds4hip_mul_mv_q8_0_q8_0_f32_prealloc", _ptr(W), _ptr(x), _ptr(y), n_rows, n_cols,
@@ -278,6 +302,7 @@ def mul_mm_bf16_f32(W, X, Y, n_rows, n_cols, n_batch, workspace=None, stream=Non
 # ---- indexer (cuda/indexer_allowed.cuh:33,67,83,97) ----------------------------------------
 
 def launch_indexer_allowed_short_circuit_i32(out_i32, n_comp, top_k, stream=None):
+    _check(out_i32, torch.int32, max(n_comp, 0), "out_i32")
     call("ds4hip_indexer_allowed_short_circuit_i32", _ptr(out_i32), n_comp, top_k,
          _stream(stream))
 
@@ -290,6 +315,10 @@ def launch_scale_inplace_f32(y, n, scale, stream=None):
 def launch_indexer_score_topk_i32(q, weights, index_comp, n_comp, n_head, head_dim, top_k,
                                   allowed_out, scratch_scores, stream=None):
     _check(index_comp, torch.int16, n_comp * head_dim, "index_comp")
+    _check(q, torch.float32, n_head * head_dim, "q")
+    _check(weights, torch.float32, n_head, "weights")
+    _check(allowed_out, torch.int32, n_comp, "allowed_out")
+    _check(scratch_scores, torch.float32, n_comp, "scratch_scores")
     call("ds4hip_indexer_score_topk_i32", _ptr(q), _ptr(weights), _ptr(index_comp), n_comp,
          n_head, head_dim, top_k, _ptr(allowed_out), _ptr(scratch_scores), _stream(stream))
 
@@ -297,6 +326,10 @@ def launch_indexer_score_topk_i32(q, weights, index_comp, n_comp, n_head, head_d
 def launch_indexer_score_topk_f32_i32(q, weights, index_comp_f32, n_comp, n_head, head_dim,
                                       top_k, allowed_out, scratch_scores, stream=None):
     _check(index_comp_f32, torch.float32, n_comp * head_dim, "index_comp_f32")
+    _check(q, torch.float32, n_head * head_dim, "q")
+    _check(weights, torch.float32, n_head, "weights")
+    _check(allowed_out, torch.int32, n_comp, "allowed_out")
+    _check(scratch_scores, torch.float32, n_comp, "scratch_scores")
     call("ds4hip_indexer_score_topk_f32_i32", _ptr(q), _ptr(weights), _ptr(index_comp_f32),
          n_comp, n_head, head_dim, top_k, _ptr(allowed_out), _ptr(scratch_scores),
          _stream(stream))
@@ -319,6 +352,13 @@ def indexer_topk_positions(q, weights, keys, top_k, n_recent, *, scores=None, se
         select = torch.empty(nb, dtype=torch.uint8, device=dev)
     if positions is None:
         positions = torch.empty(min(top_k, n_comp), dtype=torch.int32, device=dev)
+    _check(q, torch.float32, n_head * head_dim, "q")
+    _check(weights, torch.float32, n_head, "weights")
+    _check(scores, torch.float32, n_comp, "scores")
+    _check(mask, torch.int32, n_comp, "mask")
+    _check(positions, torch.int32, min(top_k, n_comp), "positions")
+    _dev(keys, "keys")
+    _dev(select, "select")
     call("ds4hip_indexer_topk_positions", _ptr(q), _ptr(weights), _ptr(keys),
          _KEY_KIND[keys.dtype], n_comp, n_head, head_dim, top_k, n_recent, _ptr(scores),
          _ptr(select), _ptr(mask), _ptr(positions), _stream(stream))
@@ -332,6 +372,15 @@ def launch_compressor_decode_step_f32_prealloc(is_attn, x_f32, w_kv_f16, w_gate_
                                                pos, il, state_kv, state_score, emit_out,
                                                scratch_kv_cur, scratch_sc_cur, stream=None):
     """Returns `emitted` (the reference's *emitted_out_host)."""
+    coff = 2 if compress_ratio == 4 else 1
+    for t, nm in ((x_f32, "x"), (w_kv_f16, "w_kv"), (w_gate_f16, "w_gate"), (w_ape_f16, "w_ape"),
+                  (w_norm_f32, "w_norm"), (state_kv, "state_kv"), (state_score, "state_score"),
+                  (emit_out, "emit_out")):
+        _dev(t, nm)
+    _check(scratch_kv_cur, torch.float32, coff * head_dim_out, "scratch_kv_cur")
+    _check(scratch_sc_cur, torch.float32, coff * head_dim_out, "scratch_sc_cur")
+    _dev(scratch_kv_cur, "scratch_kv_cur")
+    _dev(scratch_sc_cur, "scratch_sc_cur")
     emitted = C.c_int(0)
     call("ds4hip_compressor_decode_step_f32_prealloc", int(bool(is_attn)), _ptr(x_f32),
          _ptr(w_kv_f16), _ptr(w_gate_f16), _ptr(w_ape_f16), _ptr(w_norm_f32), in_dim,
@@ -343,6 +392,10 @@ def launch_compressor_decode_step_f32_prealloc(is_attn, x_f32, w_kv_f16, w_gate_
 def launch_compressor_decode_step_f32(is_attn, x_f32, w_kv_f16, w_gate_f16, w_ape_f16,
                                       w_norm_f32, in_dim, head_dim_out, compress_ratio, pos, il,
                                       state_kv, state_score, emit_out, stream=None):
+    for t, nm in ((x_f32, "x"), (w_kv_f16, "w_kv"), (w_gate_f16, "w_gate"), (w_ape_f16, "w_ape"),
+                  (w_norm_f32, "w_norm"), (state_kv, "state_kv"), (state_score, "state_score"),
+                  (emit_out, "emit_out")):
+        _dev(t, nm)
     emitted = C.c_int(0)
     call("ds4hip_compressor_decode_step_f32", int(bool(is_attn)), _ptr(x_f32), _ptr(w_kv_f16),
          _ptr(w_gate_f16), _ptr(w_ape_f16), _ptr(w_norm_f32), in_dim, head_dim_out,

@@ -130,6 +130,15 @@ int ds4hip_session_push_index_comp(ds4hip_session_state *s, int il, const float 
 int ds4hip_rows_scatter_f32(const float *src, int n_rows, int width, float *dst,
                             const long long *dst_rows, void *stream);
 
+/* Writes n compressed-row numbers (device int32 sel[0..n)) where
+ * ds4hip_session_layer_rows' *selected_out points: the selection the next
+ * decode of layer il reads with n_selected = n (stream-ordered device copy).
+ * The prefill chunk driver leaves its last token's indexer selection there,
+ * as the token-by-token loop does (cuda/forward_layer.cu:1088-1137 keeps
+ * the allowed mask of the last step in the session's scratch). */
+int ds4hip_session_set_selection(ds4hip_session_state *s, int il, const int32_t *sel, int n,
+                                 void *stream);
+
 /* Rows for layer il's decode attention: *row_idx (device) and *n_rows are
  * the row_idx / n_rows arguments of ds4hip_flash_attn_decode_fp8 with
  * row_base = layers[il].row_base: the valid ring rows, then n_selected

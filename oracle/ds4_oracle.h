@@ -85,10 +85,12 @@ void orc_attn_prefill_fp8(const float *Q, int n_q, const uint8_t *codes,
                           int n_rot, int n_threads);
 
 // ---- indexer (cuda/indexer_allowed.cu:68-279) ----------------------------
-// score[c] = sum_h w[h] * relu(q_h . k_c) in the canonical order used by the
-// HIP kernels: dot = fma chain over d ascending from 0; score = fma chain
-// over h ascending, score = fma(w[h], relu(dot_h), score). key_kind:
-// 0 = f32 keys, 1 = f16 bits, 2 = bf16 bits.
+// score[c] = sum_h w[h] * relu(q_h . k_c) in the reference kernel's own
+// order (cuda/indexer_allowed.cu:68-171): per head an fma chain over d
+// ascending from 0, relu, the rounded product dot * w[h], then the 32-lane
+// xor butterfly (16, 8, 4, 2, 1) per warp of heads and warp 0's 8-lane xor
+// butterfly (4, 2, 1) over the warp sums. key_kind: 0 = f32 keys, 1 = f16
+// bits, 2 = bf16 bits (bf16 keys: the same arithmetic, keys widened exactly).
 void orc_indexer_scores(const float *q, const float *w, const void *keys,
                         int key_kind, int n_comp, int n_head, int head_dim,
                         float *scores);

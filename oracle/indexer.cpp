@@ -15,23 +15,53 @@ static inline float key_at(const void *keys, int kind, size_t i) {
     }
 }
 
-// cuda/indexer_allowed.cu:68-171 (score = sum_h w_h * relu(q_h . k_c)),
-// evaluated in the fixed fma order the HIP kernel uses (ds4_oracle.h).
+// cuda/indexer_allowed.cu:68-115 (f16 keys) and :120-171 (fp32 keys), one
+// block per key c, thread h = head h (block of roundup32(n_head) threads):
+//   dot_h = sum_d q_h[d] * k_c[d], accumulated left to right from 0.0f as
+//           `dot += qh[d] * kv[d]` (:85-88, :136-139), which nvcc compiles to
+//           one fma per step (its default contraction);
+//   relu:   `if (dot < 0.0f) dot = 0.0f` (:89), so NaN and -0 pass unchanged;
+//   partial_h = dot_h * w[h] (:90), a rounded product (not fused into a sum);
+//   each 32-lane warp sums its partials with the xor butterfly
+//           partial += shfl_xor(partial, off), off = 16, 8, 4, 2, 1 (:96-99);
+//   warp 0 reads the warp sums (lanes >= n_warps read 0.0f) and runs the
+//           butterfly with off = 4, 2, 1 over MAX_WARPS = 8 lanes (:103-110);
+//   score = lane 0's value.
+// Heads >= n_head contribute 0.0f (:80). The butterfly is written out lane by
+// lane below; every lane of a butterfly ends with the same value (IEEE
+// addition is commutative), so lane 0 is the reference's result.
+static float xor_butterfly(float *v, int n_lanes, int first_off) {
+    std::vector<float> nv((size_t)n_lanes);
+    for (int off = first_off; off > 0; off >>= 1) {
+        for (int l = 0; l < n_lanes; ++l) nv[l] = v[l] + v[l ^ off];
+        for (int l = 0; l < n_lanes; ++l) v[l] = nv[l];
+    }
+    return v[0];
+}
+
 extern "C" void orc_indexer_scores(const float *q, const float *w, const void *keys,
                                    int key_kind, int n_comp, int n_head, int head_dim,
                                    float *scores) {
-    std::vector<float> k((size_t)head_dim);
+    // the launcher's block is min(roundup32(n_head), 256) threads (:318-321)
+    const int n_warps = std::min((n_head + 31) / 32, 8);
+    std::vector<float> k((size_t)head_dim), lane((size_t)32 * n_warps);
     for (int c = 0; c < n_comp; ++c) {
         for (int d = 0; d < head_dim; ++d) k[d] = key_at(keys, key_kind, (size_t)c * head_dim + d);
-        float s = 0.0f;
-        for (int h = 0; h < n_head; ++h) {
-            const float *qh = q + (size_t)h * head_dim;
-            float dot = 0.0f;
-            for (int d = 0; d < head_dim; ++d) dot = std::fmaf(qh[d], k[d], dot);
-            const float r = dot > 0.0f ? dot : 0.0f;
-            s = std::fmaf(w[h], r, s);
+        for (int h = 0; h < 32 * n_warps; ++h) {
+            float partial = 0.0f;
+            if (h < n_head) {
+                const float *qh = q + (size_t)h * head_dim;
+                float dot = 0.0f;
+                for (int d = 0; d < head_dim; ++d) dot = std::fmaf(qh[d], k[d], dot);
+                if (dot < 0.0f) dot = 0.0f;
+                partial = dot * w[h];
+            }
+            lane[h] = partial;
         }
-        scores[c] = s;
+        float warp_sums[8];
+        for (int wv = 0; wv < 8; ++wv)
+            warp_sums[wv] = wv < n_warps ? xor_butterfly(&lane[(size_t)32 * wv], 32, 16) : 0.0f;
+        scores[c] = xor_butterfly(warp_sums, 8, 4);
     }
 }
 

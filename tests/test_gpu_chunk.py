@@ -24,7 +24,6 @@ from ds4cuda_amd import session, synth
 from ds4cuda_amd.chunk import ChunkLayer, forward_chunk_attn
 from ds4cuda_amd.ops import _ptr, _stream
 from ds4cuda_amd._lib import call
-from unverified import unverified
 
 pytestmark = pytest.mark.gpu
 
@@ -132,9 +131,6 @@ def layer_bytes(s, il):
     return out, (L.n_raw, L.raw_head, L.n_comp, L.n_index_comp)
 
 
-@unverified("not yet run on the GPU: its first run faulted (the driver passed the decode's "
-            "row_base as a host array; the kernels read it on the device); the fixed driver "
-            "(cache pointers offset to the layer, row_base NULL, as Session.decode) has not run yet")
 @pytest.mark.parametrize("il", [0, 2, 3])
 def test_chunk_matches_token_loop(gpu, tmp_path, il):
     layer = layer_weights(il, gpu)

@@ -27,21 +27,23 @@ def d2h(ptr, n):
     return b
 
 
-@unverified("the import of reference session files has not run on the GPU yet")
-def test_import_reference_session(gpu, tmp_path):
-    max_ctx, pos = 256, 203
+@pytest.mark.parametrize("max_ctx,pos", [(256, 203), (64, 64)])
+def test_import_reference_session(gpu, tmp_path, max_ctx, pos):
+    # max_ctx 64: the ratio-128 states (128 x 512 floats) are larger than the
+    # 64-row window buffer the import stages rows through
     cap_raw, caps = F.geometry(max_ctx)
+    nc = min(50, caps[2])
     raw0 = synth.kv_rows(501, 0, cap_raw, outlier_frac=0.02).astype(np.float32)
     raw2 = synth.kv_rows(501, 2, cap_raw).astype(np.float32)
     comp2 = np.zeros((caps[2], 512), np.float32)
-    comp2[:50] = 2 * synth.kv_rows(501, 3, 50)
+    comp2[:nc] = 2 * synth.kv_rows(501, 3, nc)
     st_kv = synth.normal(501, 4, F.attn_cells(4)).astype(np.float32)
     st_sc = synth.normal(501, 5, F.attn_cells(4)).astype(np.float32)
     idx = np.zeros((caps[2], 128), np.float32)
-    idx[:50] = synth.normal(501, 6, 50 * 128).reshape(50, 128)
+    idx[:nc] = synth.normal(501, 6, nc * 128).reshape(nc, 128)
     layers = {0: {"n_raw": cap_raw, "raw": raw0},
-              2: {"n_raw": cap_raw, "raw": raw2, "comp": comp2, "n_comp": 50, "st_kv": st_kv,
-                  "st_sc": st_sc, "idx": idx, "n_idx": 50}}
+              2: {"n_raw": cap_raw, "raw": raw2, "comp": comp2, "n_comp": nc, "st_kv": st_kv,
+                  "st_sc": st_sc, "idx": idx, "n_idx": nc}}
     path = tmp_path / "ref.kvc"
     F.write(path, max_ctx, pos, pos, range(7), layers)
     s = session.Session(max_ctx)
@@ -49,7 +51,7 @@ def test_import_reference_session(gpu, tmp_path):
         assert s.import_ds4cudak(path) == (pos, pos)
         L0, L2 = s.layer(0), s.layer(2)
         assert (L0.n_raw, L0.raw_head, L0.n_comp) == (cap_raw, pos % cap_raw, 0)
-        assert (L2.n_raw, L2.n_comp, L2.n_index_comp) == (cap_raw, 50, 50)
+        assert (L2.n_raw, L2.n_comp, L2.n_index_comp) == (cap_raw, nc, nc)
         # FP8 codes of the ring: raw row i in slot (pos - 128 + i) % 128
         codes, sexp, tail, deq0 = O.fp8_quant_rows(raw0)
         rows = cap_raw + L0.cap_comp
@@ -57,17 +59,17 @@ def test_import_reference_session(gpu, tmp_path):
         for i in range(cap_raw):
             assert np.array_equal(got[L0.cap_comp + (pos - cap_raw + i) % cap_raw], codes[i]), i
         # compressed rows of layer 2 in order
-        c2, _, _, deq_c = O.fp8_quant_rows(comp2[:50])
-        got2 = d2h(s.s.codes + L2.row_base * 448, 50 * 448).reshape(50, 448)
+        c2, _, _, deq_c = O.fp8_quant_rows(comp2[:nc])
+        got2 = d2h(s.s.codes + L2.row_base * 448, nc * 448).reshape(nc, 448)
         assert np.array_equal(got2, c2)
         # state copied as it is
         assert np.array_equal(d2h(L2.attn_state_kv, st_kv.nbytes).view(np.float32), st_kv)
         assert np.array_equal(d2h(L2.attn_state_score, st_sc.nbytes).view(np.float32), st_sc)
-        assert np.array_equal(d2h(L2.index_comp_kv, 50 * 128 * 4).view(np.float32), idx[:50].reshape(-1))
+        assert np.array_equal(d2h(L2.index_comp_kv, nc * 128 * 4).view(np.float32), idx[:nc].reshape(-1))
         # decode over the imported rows against the oracle over the file's rows
         q = synth.normal(502, 0, 64 * 512).reshape(64, 512).astype(np.float32)
         sinks = synth.normal(502, 1, 64).astype(np.float32)
-        for il, kv in ((0, raw0), (2, np.concatenate([raw2, comp2[:50]]))):
+        for il, kv in ((0, raw0), (2, np.concatenate([raw2, comp2[:nc]]))):
             out = torch.empty(64 * 512, device=gpu)
             s.decode(il, torch.from_numpy(q.reshape(-1)).to(gpu), torch.from_numpy(sinks).to(gpu), out)
             torch.cuda.synchronize()
@@ -83,7 +85,8 @@ def test_import_reference_session(gpu, tmp_path):
 def test_reference_file_round_trip(gpu, tmp_path):
     """A reference file whose rows are what the reference holds (window rows
     FP8 values rounded to f16, compressed rows FP8 values with an f16 tail)
-    comes back byte for byte from import followed by export."""
+    comes back byte for byte from import followed by export, except that a
+    -0.0 in a coded dim comes back as +0.0 (the reference's quantizer rule)."""
     max_ctx, pos = 256, 300
     cap_raw, caps = F.geometry(max_ctx)
 
@@ -110,14 +113,25 @@ def test_reference_file_round_trip(gpu, tmp_path):
                 L.update(idx=idx, n_idx=n, ist_kv=synth.normal(515, il, F.IDX_CELLS),
                          ist_sc=synth.normal(516, il, F.IDX_CELLS))
         layers[il] = L
-    src, back = tmp_path / "src.kvc", tmp_path / "back.kvc"
+    src, back, exp = tmp_path / "src.kvc", tmp_path / "back.kvc", tmp_path / "exp.kvc"
     F.write(src, max_ctx, pos, pos, range(40), layers)
+    # The reference's quantizer takes the sign from x < 0 (cuda/fp8_kv.cu:102),
+    # so a -0.0 in a coded dim (an FP8 -0 the reference holds) quantizes to +0:
+    # the export writes +0.0 there. Everything else comes back unchanged.
+    for L in layers.values():
+        for name in ("raw", "comp"):
+            if name in L:
+                x = L[name].copy()
+                x[:, :448] = np.where(x[:, :448] == 0, np.float32(0), x[:, :448])
+                L[name] = x
+    F.write(exp, max_ctx, pos, pos, range(40), layers)
     s = session.Session(max_ctx)
     try:
         s.import_ds4cudak(src)
         s.export_ds4cudak(back, prompt_token_ids=range(40))
     finally:
         s.close()
-    a, b = src.read_bytes(), back.read_bytes()
+    a, b = exp.read_bytes(), back.read_bytes()
     assert len(a) == len(b)
+    assert src.read_bytes() != a    # the case above occurs in this file
     assert a == b

@@ -81,9 +81,11 @@ def host_lists(s, il, p0, n_tok, n_comp, n_sel, sel, stride):
     return rc, lists, counts
 
 
-@pytest.mark.parametrize("il,p0,n_tok", [(0, 0, 5), (0, 3, 128), (0, 150, 41), (2, 127, 2), (3, 1000, 128)])
-def test_chunk_rows_match_token_steps(il, p0, n_tok):
-    s = described(4096)
+@pytest.mark.parametrize("il,p0,n_tok,ctx", [(0, 0, 5, 4096), (0, 3, 128, 4096), (0, 150, 41, 4096),
+                                            (2, 127, 2, 4096), (3, 1000, 128, 4096), (2, 130, 126, 4096),
+                                            (0, 20, 44, 64), (2, 37, 27, 64), (3, 0, 64, 64)])
+def test_chunk_rows_match_token_steps(il, p0, n_tok, ctx):
+    s = described(ctx)
     L = s.layers[il]
     L.n_raw, L.raw_head = min(p0, L.cap_raw), p0 % L.cap_raw
     rng = np.random.default_rng(il * 1000 + p0)
@@ -110,6 +112,13 @@ def test_chunk_rows_match_token_steps(il, p0, n_tok):
         ring = (win >= L.cap_comp) & (win < L.cap_comp + L.cap_raw)
         stage = (win >= s.n_cache_rows - L.row_base) & (win < s.n_cache_rows - L.row_base + 128)
         assert (ring | stage).all()
+        # every entry the decode will read lies inside the arena's rows
+        # (relative to the layer's first row: the layer's rows and the staging rows)
+        assert counts[t] <= stride
+        ent = lists[t, :counts[t]]
+        assert (ent >= 0).all() and (ent < s.n_cache_rows - L.row_base + 128).all()
+        comp = lists[t, counts[t] - n_sel[t]:counts[t]]
+        assert (comp < max(n_comp[t], 1)).all()
 
 
 def test_chunk_rows_refuse_bad_arguments():
@@ -121,6 +130,15 @@ def test_chunk_rows_refuse_bad_arguments():
     assert host_lists(s, 0, 101, 4, [0] * 4, [0] * 4, None, 256)[0] == -22     # ring not at p0
     assert host_lists(s, 0, 100, 129, [0] * 129, [0] * 129, None, 256)[0] == -22   # > 128 tokens
     assert host_lists(s, 0, 100, 4, [0] * 4, [0] * 4, None, 100)[0] == -22     # list too short
+    assert host_lists(s, 0, 100, 4, [0] * 4, [0] * 4, None, 256)[0] == 0
+    s64 = described(64)
+    s64.layers[0].n_raw, s64.layers[0].raw_head = 60, 60
+    assert host_lists(s64, 0, 60, 4, [0] * 4, [0] * 4, None, 256)[0] == 0
+    assert host_lists(s64, 0, 60, 5, [0] * 5, [0] * 5, None, 256)[0] == -22   # past max_context
+    s64.layers[0].n_raw, s64.layers[0].raw_head = 0, 0
+    assert host_lists(s64, 0, 0, 64, [0] * 64, [0] * 64, None, 256)[0] == 0
+    s100 = described(100)   # cap_raw 100: a chunk of more tokens than the window holds
+    assert host_lists(s100, 0, 0, 101, [0] * 101, [0] * 101, None, 256)[0] == -22
     L2 = s.layers[2]
     L2.n_raw, L2.raw_head = 100, 100
     assert host_lists(s, 2, 100, 2, [30, 30], [8, 8], None, 256)[0] == -22     # selection missing

@@ -84,7 +84,6 @@ SIGNATURES: dict[str, list] = {
     "ds4hip_attn_qkv_decode_workspace_bytes": [],
     "ds4hip_attn_qkv_decode_f32": [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _sz,
                                    _vp],
-    "ds4hip_set_indexer_prefilter": [_i],
     "ds4hip_session_chunk_rows": [_vp, _i, _i, _i, _vp, _vp, _vp, _i, _vp, _i, _vp, _vp],
     "ds4hip_session_chunk_rows_host": [_vp, _i, _i, _i, _vp, _vp, _vp, _i, _vp, _i, _vp],
     "ds4hip_session_state_describe": [_vp, _i],

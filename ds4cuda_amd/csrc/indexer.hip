@@ -1,12 +1,21 @@
 // indexer.hip — lightning-indexer scores and exact top-k selection.
 //
-// Scores (cuda/indexer_allowed.cu:68-171): score[c] = sum_h w[h] relu(q_h . k_c).
-// The reference reduces in a warp-shuffle order and accepts ULP drift at the
-// top-k boundary (cuda/indexer_allowed.cuh:64-66). Here the order is fixed so
-// that the selected set is reproducible bit for bit: dot_h is an fma chain
-// over d ascending from +0, then score = fma(w[h], relu(dot_h), score) over h
-// ascending from +0. One thread scores one key: the key row (up to 128 dims)
-// sits in registers as fp32, the 64 x 128 query in LDS (broadcast reads).
+// Scores (cuda/indexer_allowed.cu:68-171): score[c] = sum_h w[h] relu(q_h . k_c),
+// computed with the reference kernel's own operations so that scores and the
+// selected positions are bit-identical to it. The reference runs one block per
+// key, thread h = head h:
+//   dot_h = fma chain over d ascending from 0.0f (`dot += q * k`, contracted);
+//   relu `dot < 0 ? 0 : dot`; partial_h = dot_h * w[h] (a rounded product);
+//   each 32-head warp adds its partials with an xor butterfly (16, 8, 4, 2, 1),
+//   warp 0 combines the warp sums with an xor butterfly over 8 lanes (4, 2, 1;
+//   lanes past the last warp hold 0.0f).
+// Here one thread scores one key (the key row in registers, the query in LDS)
+// and evaluates the same tree: a butterfly's lane-0 result is a balanced
+// binary tree whose leaves, left to right, are the heads in bit-reversed
+// order (h, h + 16, h + 8, h + 24, ...), so feeding the products in that
+// order to a five-level carry chain (HeadTree) adds exactly the reference's
+// pairs. Floating-point contraction is off in this file: every product and
+// sum rounds where the reference's does; the dot chains call fmaf.
 //
 // Selection (cuda/indexer_allowed.cu:200-279): top_k rounds of argmax with
 // ties to the lowest index select exactly the top_k entries in
@@ -24,6 +33,8 @@
 #include <cstdlib>
 
 using namespace ds4hip;
+
+#pragma clang fp contract(off)
 
 namespace {
 
@@ -69,12 +80,59 @@ __device__ inline void stage_query(float *qs, const float *q, int n_head) {
     }
 }
 
-// Zero heads of zero weight up to a multiple of 4 (they add +0 * 0 terms
-// after the real heads, which leaves every score bit-identical).
-__device__ inline void pad_heads(float *qs, float *ws, int n_head) {
-    const int n4 = (n_head + 3) & ~3;
-    for (int i = threadIdx.x; i < (n4 - n_head) * kMaxDim; i += 256) qs[n_head * kMaxDim + i] = 0.0f;
-    if ((int)threadIdx.x < n4 - n_head) ws[n_head + threadIdx.x] = 0.0f;
+// Zero query rows and weights for the heads past n_head up to the next
+// multiple of 32 (a whole warp of the reference's block). Their products are
+// replaced by 0.0f anyway, as the reference's idle threads contribute.
+__device__ inline void pad_heads(float *qs, float *ws, int n_head, int stride = kMaxDim) {
+    const int n32 = (n_head + 31) & ~31;
+    for (int i = threadIdx.x; i < (n32 - n_head) * kMaxDim; i += 256)
+        qs[(n_head + i / kMaxDim) * stride + i % kMaxDim] = 0.0f;
+    if ((int)threadIdx.x < n32 - n_head) ws[n_head + threadIdx.x] = 0.0f;
+}
+
+// The reference's head sum (see the top of the file), fed one leaf at a time
+// in leaf order: leaf t of warp t >> kLevels. A leaf is one head's product
+// (kLevels = 5) or the sum of a group of four heads h, h + 16, h + 8, h + 24
+// (kLevels = 3, the butterfly's first two levels already added). An odd leaf
+// index closes a pair with the level below, like a binary counter's carry.
+template <int kLevels>
+struct HeadTree {
+    float l[kLevels];
+    float w0 = 0.0f, w1 = 0.0f;
+    // branch-free (t is uniform, but branches here cost the caller's
+    // registers): every level's sum is formed and selects keep the right ones
+    __device__ inline void push(int t, float v) {
+        bool carry = true;   // v still travels up
+#pragma unroll
+        for (int k = 0; k < kLevels; ++k) {
+            const bool odd = (t >> k) & 1;
+            const float up = l[k] + v;
+            l[k] = (carry && !odd) ? v : l[k];
+            carry = carry && odd;
+            v = up;
+        }
+        const bool w_is_1 = (t >> kLevels) & 1;
+        w0 = (carry && !w_is_1) ? v : w0;
+        w1 = (carry && w_is_1) ? v : w1;
+    }
+    // warp 0's 8-lane butterfly over (w0, w1, 0, ..., 0): lane 0 gets
+    // ((w0 + 0) + 0) + ((w1 + 0) + 0); x + 0 + 0 == x + 0
+    __device__ inline float result() const { return (w0 + 0.0f) + (w1 + 0.0f); }
+};
+
+// Head of leaf t in the 5-level order: bits 0..4 reversed within the warp.
+__device__ inline int head_of_leaf(int t) {
+    return (t & ~31) | (int)(__builtin_bitreverse32((unsigned)(t & 31)) >> 27);
+}
+// First head of four-head group g: the 3 low bits of g reversed.
+__device__ inline int head_of_group(int g) {
+    return (g & ~7) * 4 + (int)(__builtin_bitreverse32((unsigned)(g & 7)) >> 29);
+}
+
+// relu and the rounded product of one head (cuda/indexer_allowed.cu:89-90)
+__device__ inline float head_partial(float dot, float w) {
+    if (dot < 0.0f) dot = 0.0f;
+    return dot * w;
 }
 
 // head_dim 128, one key per thread, the key row in registers as fp32 and the
@@ -109,26 +167,42 @@ __device__ __attribute__((always_inline)) inline float score_lds(const float *qs
             }
         }
     }
-    // four heads at a time: four independent dot chains keep the VALU busy
-    // (n_head is padded to a multiple of 4 with zero heads of zero weight)
-    float s = 0.0f;
-    for (int h = 0; h < n_head; h += 4) {
-        const float4_t *q0 = reinterpret_cast<const float4_t *>(qs + h * kMaxDim);
-        float d[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    // four heads at a time (four independent dot chains keep the VALU busy):
+    // group g = heads h, h + 16, h + 8, h + 24 of one warp, whose products
+    // the butterfly's first two levels add as ((p_h + p_h+16) + (p_h+8 + p_h+24))
+    HeadTree<3> tree;
+    const int n_groups = ((n_head + 31) & ~31) / 4;
+    for (int g = 0; g < n_groups; ++g) {
+        const int h = head_of_group(g);
+        float v = 0.0f;
+        if (h < n_head) {   // else all four heads are idle threads of the reference
+            const float4_t *q0 = reinterpret_cast<const float4_t *>(qs + h * kMaxDim);
+            constexpr int kOff[4] = {0, 16, 8, 24};
+            float d[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int v = 0; v < kMaxDim / 4; ++v) {
-            float4_t a[4];
+            for (int v4 = 0; v4 < kMaxDim / 4; ++v4) {
+                float4_t a[4];
 #pragma unroll
-            for (int z = 0; z < 4; ++z) a[z] = q0[z * (kMaxDim / 4) + v];
+                for (int z = 0; z < 4; ++z) a[z] = q0[kOff[z] * (kMaxDim / 4) + v4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
+                for (int e = 0; e < 4; ++e)
 #pragma unroll
-                for (int z = 0; z < 4; ++z) d[z] = fmaf(a[z][e], k[4 * v + e], d[z]);
+                    for (int z = 0; z < 4; ++z) d[z] = fmaf(a[z][e], k[4 * v4 + e], d[z]);
+            }
+            float p[4];
+#pragma unroll
+            for (int z = 0; z < 4; ++z) {
+                // heads past n_head give +0.0f (the reference's idle threads);
+                // their query rows and weights are zero-padded, so the loads
+                // stay in bounds, and a bit mask replaces the product
+                const float pz = head_partial(d[z], ws[h + kOff[z]]);
+                p[z] = __int_as_float(__float_as_int(pz) & (h + kOff[z] < n_head ? ~0 : 0));
+            }
+            v = (p[0] + p[1]) + (p[2] + p[3]);
         }
-#pragma unroll
-        for (int z = 0; z < 4; ++z) s = fmaf(ws[h + z], d[z] > 0.0f ? d[z] : 0.0f, s);
+        tree.push(g, v);
     }
-    return s;
+    return tree.result();
 }
 
 // head_dim 128 with four threads per key (adjacent lanes): thread `part`
@@ -179,11 +253,13 @@ __device__ __attribute__((always_inline)) inline void score_chain4x2(const float
     load_key32<kKind>(keys, c0, part, k0);
     load_key32<kKind>(keys, c1, part, k1);
     float carry0 = 0.0f, carry1 = 0.0f;
-    s0 = 0.0f;
-    s1 = 0.0f;
-    for (int i = 0; i < n_head + 3; ++i) {
-        const int h = i - part;
-        const bool act = h >= 0 && h < n_head;
+    HeadTree<5> t0, t1;
+    const int n_leaves = (n_head + 31) & ~31;
+    for (int i = 0; i < n_leaves + 3; ++i) {
+        const int leaf = i - part;
+        const bool in = leaf >= 0 && leaf < n_leaves;
+        const int h = in ? head_of_leaf(leaf) : 0;
+        const bool act = in && h < n_head;
         const float4_t *qv = reinterpret_cast<const float4_t *>(qs + (act ? h : 0) * kQStride + 32 * part);
         float d0 = part == 0 ? 0.0f : carry0;
         float d1 = part == 0 ? 0.0f : carry1;
@@ -199,11 +275,13 @@ __device__ __attribute__((always_inline)) inline void score_chain4x2(const float
         // lane l takes lane l-1's chains (row_shr:1; part 0 ignores them)
         carry0 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(d0), 0x111, 0xF, 0xF, false));
         carry1 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(d1), 0x111, 0xF, 0xF, false));
-        if (part == 3 && act) {
-            s0 = fmaf(ws[h], d0 > 0.0f ? d0 : 0.0f, s0);
-            s1 = fmaf(ws[h], d1 > 0.0f ? d1 : 0.0f, s1);
+        if (part == 3 && in) {
+            t0.push(leaf, act ? head_partial(d0, ws[h]) : 0.0f);
+            t1.push(leaf, act ? head_partial(d1, ws[h]) : 0.0f);
         }
     }
+    s0 = t0.result();
+    s1 = t1.result();
 }
 
 // Any head_dim <= 128: the key row is zero-padded to 128 in registers and
@@ -215,16 +293,22 @@ __device__ inline float score_any(const float *qs, const float *ws, const void *
 #pragma unroll
     for (int d = 0; d < kMaxDim; ++d)
         k[d] = d < head_dim ? key_elem<kKind>(keys, (size_t)c * head_dim + d) : 0.0f;
-    float s = 0.0f;
-    for (int h = 0; h < n_head; ++h) {
-        const float *qh = qs + h * head_dim;
-        float dot = 0.0f;
+    HeadTree<5> tree;
+    const int n_leaves = (n_head + 31) & ~31;
+    for (int t = 0; t < n_leaves; ++t) {
+        const int h = head_of_leaf(t);
+        float p = 0.0f;
+        if (h < n_head) {
+            const float *qh = qs + h * head_dim;
+            float dot = 0.0f;
 #pragma unroll
-        for (int d = 0; d < kMaxDim; ++d)
-            if (d < head_dim) dot = fmaf(qh[d], k[d], dot);
-        s = fmaf(ws[h], dot > 0.0f ? dot : 0.0f, s);
+            for (int d = 0; d < kMaxDim; ++d)
+                if (d < head_dim) dot = fmaf(qh[d], k[d], dot);
+            p = head_partial(dot, ws[h]);
+        }
+        tree.push(t, p);
     }
-    return s;
+    return tree.result();
 }
 
 // kFull: head_dim == 128 (the scalar-load path); otherwise the LDS path. Two
@@ -277,83 +361,6 @@ __global__ __launch_bounds__(256) void score_kernel(const float *__restrict__ q,
         for (int i = threadIdx.x; i < kBins; i += 256)
             if (lh[i]) atomicAdd(&hist[i], lh[i]);
     }
-}
-
-// The same scores (head_dim 128, n_head a multiple of 4) with the query and
-// the weights read from global memory at wave-uniform addresses, so they come
-// through scalar loads into SGPRs and every fma takes its query value as a
-// scalar operand: no LDS staging and no LDS reads. The key row, the four
-// independent head chains and the head sum keep score_lds' order, so the
-// scores are bit-identical to it.
-template <int kKind>
-__global__ __launch_bounds__(256) void score_sgpr_kernel(const float *__restrict__ q,
-                                                         const float *__restrict__ w,
-                                                         const void *__restrict__ keys, int n_comp,
-                                                         int n_head, float *__restrict__ scores,
-                                                         unsigned *__restrict__ hist, int n_cand) {
-    __shared__ unsigned lh[kBins];
-    if (hist)
-        for (int i = threadIdx.x; i < kBins; i += 256) lh[i] = 0;
-    const int c = blockIdx.x * 256 + threadIdx.x;
-    const int cc = c < n_comp ? c : n_comp - 1;   // the last block's spare lanes score a real key
-    float k[kMaxDim];
-    if (kKind == 0) {
-        const float4_t *src = reinterpret_cast<const float4_t *>(
-            static_cast<const float *>(keys) + (size_t)cc * kMaxDim);
-#pragma unroll
-        for (int v = 0; v < kMaxDim / 4; ++v) {
-            const float4_t u = src[v];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) k[4 * v + e] = u[e];
-        }
-    } else {
-        const uint4_t *src = reinterpret_cast<const uint4_t *>(
-            static_cast<const uint16_t *>(keys) + (size_t)cc * kMaxDim);
-#pragma unroll
-        for (int v = 0; v < kMaxDim / 8; ++v) {
-            const uint4_t u = src[v];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const uint16_t h = (uint16_t)((u[e >> 1] >> (16 * (e & 1))) & 0xFFFF);
-                k[8 * v + e] = kKind == 1 ? f16_bits_to_f32(h) : bf16_to_f32(h);
-            }
-        }
-    }
-    float s = 0.0f;
-    for (int h = 0; h < n_head; h += 4) {
-        const float *q0 = q + (size_t)h * kMaxDim;
-        float d[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int v = 0; v < kMaxDim / 4; ++v) {
-            float4_t a[4];
-#pragma unroll
-            for (int z = 0; z < 4; ++z) a[z] = *reinterpret_cast<const float4_t *>(q0 + z * kMaxDim + 4 * v);
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-#pragma unroll
-                for (int z = 0; z < 4; ++z) d[z] = fmaf(a[z][e], k[4 * v + e], d[z]);
-            // at most 4 x 64 query values in SGPRs at a time (the other waves
-            // of the SIMD cover the scalar loads' latency)
-            if ((v & 3) == 3) __builtin_amdgcn_sched_barrier(0);
-        }
-#pragma unroll
-        for (int z = 0; z < 4; ++z) s = fmaf(w[h + z], d[z] > 0.0f ? d[z] : 0.0f, s);
-    }
-    if (c < n_comp) scores[c] = s;
-    if (hist) {
-        __syncthreads();
-        if (c < n_cand) atomicAdd(&lh[ord_key(s) >> 21], 1u);
-        __syncthreads();
-        for (int i = threadIdx.x; i < kBins; i += 256)
-            if (lh[i]) atomicAdd(&hist[i], lh[i]);
-    }
-}
-
-// DS4HIP_INDEXER_SGPR_SCORES=1 scores with score_sgpr_kernel (read at every
-// launch; off by default until it has run on the GPU).
-bool sgpr_scores_enabled() {
-    const char *e = getenv("DS4HIP_INDEXER_SGPR_SCORES");
-    return e && e[0] == '1';
 }
 
 __global__ void zero_u32_kernel(unsigned *p, int n) {
@@ -592,526 +599,11 @@ __global__ void scale_kernel(float *y, int n, float s) {
     if (i < n) y[i] *= s;
 }
 
-// ---- prefiltered selection (bf16 keys, 64 heads x 128) -------------------------------------
-//
-// The exact scores cost 8192 dependent fp32 fma per key. Only the keys whose
-// score could fall on either side of the selection threshold need them:
-//
-//  1. prefilter_kernel: approximate scores a_c on the bf16 MFMA (the query
-//     split into bf16 hi + lo, the key bf16 exact; fp32 accumulation), with a
-//     per-key bound b_c >= |a_c - s_c| on the distance to the exact score s_c
-//     (derivation below), the level-1 histogram of a and max_c b_c.
-//  2. hist_next_kernel<2>: the level-2 histogram of a. The need-th largest a
-//     then lies in a 22-bit key bucket [lo, hi].
-//  3. band_kernel: with B = max b, the need-th largest exact score lies in
-//     [lo - B, hi + B]; a key with a - b > hi + B is certainly selected, one
-//     with a + b < lo - B certainly not; the rest (the band) is rescored with
-//     the exact fixed-order chains. The last workgroup to finish selects the
-//     need - (certainly selected) best band keys by (exact score desc, index
-//     asc), marks every candidate's score slot +inf (selected) or -inf, and
-//     writes each chunk's output offset.
-//  4. emit_marked_kernel: the positions (and/or mask) in index order.
-//
-// Bound: with u = 2^-24, the reference's chains give |s - s*| <= (128 + 64) u
-// sum_h |w_h| A_h, A_h = sum_d |q_hd k_d| (s* the exact real score; relu is
-// 1-Lipschitz). The MFMA form differs from s* by at most (2 * 128 + 64) u
-// sum_h |w_h| A_h for its two accumulation passes and head sum, plus 2^-18
-// sum_h |w_h| A_h for the part of q that hi + lo drops. So |a - s| <= 3.5e-5
-// sum_h |w_h| A_h <= 3.5e-5 ||k|| sum_h |w_h| ||q_h|| (Cauchy-Schwarz); b
-// uses the constant 1e-4 for margin.
-constexpr float kBoundC = 1.0e-4f;
-constexpr int kPfMaxChunks = 1024;   // candidates <= kPfMaxChunks * kChunk
-constexpr int kPfMinCand = 8192;      // fewer candidates: the exact scorer outright
-// DS4HIP_INDEXER_PREFILTER=0 keeps the exact scorer for every key.
-// Off by default: two GPU runs of a timing variant of this path (a fake
-// level-1 histogram, not part of this code) left most of the position list
-// unwritten, and the gathered decode then read rows at garbage indices. The
-// emit kernel now writes valid positions whenever the counts disagree; the
-// prefilter stays opt-in (DS4HIP_INDEXER_PREFILTER=1 or
-// ds4hip_set_indexer_prefilter(1)) until it has run again.
-int g_prefilter = -1;
-bool prefilter_enabled() {
-    if (g_prefilter < 0) {
-        const char *e = getenv("DS4HIP_INDEXER_PREFILTER");
-        g_prefilter = (e && e[0] == '1') ? 1 : 0;
-    }
-    return g_prefilter == 1;
-}
-typedef short pf_bf16x8_t __attribute__((ext_vector_type(8)));
-typedef __bf16 pf_bf16x2_t __attribute__((ext_vector_type(2)));
-typedef short pf_short2_t __attribute__((ext_vector_type(2)));
-
-// A load that sees other workgroups' completed writes (device-coherent).
-template <typename T>
-__device__ inline T ld_agent(const T *p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ inline float key_to_float(unsigned k) {
-    return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
-}
-
-// Selection scratch of the prefiltered path, after the three histograms.
-struct PfScratch {
-    unsigned *bmax;        // max bound (float bits; bounds are >= 0)
-    unsigned *done;        // band workgroups finished
-    unsigned *chunk_in;    // [n_chunks] certainly selected candidates per chunk
-    unsigned *chunk_off;   // [n_chunks] output offset of each chunk
-    unsigned *band_n;      // [n_chunks] band keys per chunk
-    float *bound;          // [n_chunks * kChunk]
-    float *band_val;       // [n_chunks * kChunk] exact scores of band keys, per chunk
-    int *band_idx;         // [n_chunks * kChunk]
-    float *cval;           // [n_chunks * kChunk] the band entries compacted
-    int *cidx;             // [n_chunks * kChunk]
-};
-
-__host__ __device__ inline size_t pf_align(size_t n) { return (n + 63) & ~size_t(63); }
-
-__host__ __device__ inline PfScratch pf_scratch(unsigned *base, int n_comp) {
-    const size_t chunks = (size_t)(n_comp > 0 ? n_comp : 1) / kChunk + 1;
-    const size_t rows = chunks * kChunk;
-    unsigned *p = base + 3 * kBins;
-    PfScratch S;
-    S.bmax = p;
-    S.done = p + 1;
-    p += 64;
-    S.chunk_in = p;
-    p += pf_align(chunks);
-    S.chunk_off = p;
-    p += pf_align(chunks);
-    S.band_n = p;
-    p += pf_align(chunks);
-    S.bound = reinterpret_cast<float *>(p);
-    p += rows;
-    S.band_val = reinterpret_cast<float *>(p);
-    p += rows;
-    S.band_idx = reinterpret_cast<int *>(p);
-    p += rows;
-    S.cval = reinterpret_cast<float *>(p);
-    p += rows;
-    S.cidx = reinterpret_cast<int *>(p);
-    return S;
-}
-
-size_t pf_scratch_words(int n_comp) {
-    const size_t chunks = (size_t)(n_comp > 0 ? n_comp : 1) / kChunk + 1;
-    return 3 * kBins + 64 + 3 * pf_align(chunks) + 5 * chunks * kChunk;
-}
-
-// sum over lanes l, l^16, l^32, l^48 with VALU lane swaps (no LDS)
-__device__ inline float pf_xsum(float v) {
-    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
-}
-
-// One wave scores 16 keys per step: D = Q . K^T per head tile with A = 16
-// query heads x 32 dims (lane (j, g): head 16 ht + j, dims 8 g .. 8 g + 7 of
-// the k-step; hi and lo parts) and B = 32 dims x 16 keys (lane (j, g): key j,
-// the same dims). Lane (j, g) then holds heads 16 ht + 4 g + r of key j, so
-// the weighted head sum is 16 fmas in the lane and two lane swaps, and the
-// key's norm reduces the same way: no LDS round trips.
-__global__ __launch_bounds__(256) void prefilter_kernel(const float *__restrict__ q,
-                                                        const float *__restrict__ w,
-                                                        const uint16_t *__restrict__ keys,
-                                                        int n_cand, float *__restrict__ a_out,
-                                                        unsigned *__restrict__ hist1, PfScratch S) {
-    __shared__ unsigned lh[kBins];
-    __shared__ unsigned s_bmax;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    for (int i = tid; i < kBins; i += 256) lh[i] = 0;
-    if (tid == 0) s_bmax = 0;
-    const int j = lane & 15, g = lane >> 4;
-    pf_bf16x8_t qh[4][4], ql[4][4];   // [head tile][k-step]
-    float qn2[4] = {0.0f, 0.0f, 0.0f, 0.0f};   // ||q_h||^2 of head 16 ht + j (this lane's 32 dims)
-#pragma unroll
-    for (int ht = 0; ht < 4; ++ht)
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            const float *src = q + (16 * ht + j) * kMaxDim + 32 * ks + 8 * g;
-            const float4_t x0 = *reinterpret_cast<const float4_t *>(src);
-            const float4_t x1 = *reinterpret_cast<const float4_t *>(src + 4);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) qn2[ht] = fmaf(x0[e], x0[e], fmaf(x1[e], x1[e], qn2[ht]));
-#pragma unroll
-            for (int e = 0; e < 8; e += 2) {
-                const float v0 = e < 4 ? x0[e] : x1[e - 4], v1 = e < 4 ? x0[e + 1] : x1[e - 3];
-                const pf_bf16x2_t h = pf_bf16x2_t{(__bf16)v0, (__bf16)v1};
-                const pf_bf16x2_t l = pf_bf16x2_t{(__bf16)(v0 - (float)h[0]), (__bf16)(v1 - (float)h[1])};
-                const pf_short2_t hs = __builtin_bit_cast(pf_short2_t, h), ls = __builtin_bit_cast(pf_short2_t, l);
-                qh[ht][ks][e] = hs[0];
-                qh[ht][ks][e + 1] = hs[1];
-                ql[ht][ks][e] = ls[0];
-                ql[ht][ks][e + 1] = ls[1];
-            }
-        }
-    // Wq = sum_h |w_h| ||q_h|| (lane (j, g) holds a quarter of head 16 ht + j's norm)
-    float wq = 0.0f;
-#pragma unroll
-    for (int ht = 0; ht < 4; ++ht) wq += fabsf(w[16 * ht + j]) * sqrtf(pf_xsum(qn2[ht]));
-#pragma unroll
-    for (int off = 1; off < 16; off <<= 1) wq += __shfl_xor(wq, off, 16);
-    // the head weights of the D rows this lane holds: head 16 ht + 4 g + r
-    float wr[4][4];
-#pragma unroll
-    for (int ht = 0; ht < 4; ++ht)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) wr[ht][r] = w[16 * ht + 4 * g + r];
-    __syncthreads();
-    float bmax = 0.0f;
-    const int n_tiles = (n_cand + 15) / 16;
-    // the next tile's key fragments are loaded before this tile's MFMAs
-    auto load_tile = [&](int tile, uint4_t (&u)[4]) {
-        const int row = 16 * tile + j;
-        const int rr = row < n_cand ? row : n_cand - 1;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
-            u[ks] = *reinterpret_cast<const uint4_t *>(keys + (size_t)rr * kMaxDim + 32 * ks + 8 * g);
-    };
-    const int stride = gridDim.x * 4;
-    // two fragment buffers in turn, so the next tile's loads need no copy; a
-    // load past the last tile re-reads the last tile (unused)
-    auto process = [&](int tile, const uint4_t (&uc)[4]) {
-        pf_bf16x8_t a[4];
-        float n2 = 0.0f;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            const uint4_t u = uc[ks];
-            a[ks] = __builtin_bit_cast(pf_bf16x8_t, u);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const pf_bf16x2_t kp = __builtin_bit_cast(pf_bf16x2_t, u[e]);
-                n2 = __builtin_amdgcn_fdot2_f32_bf16(kp, kp, n2, false);
-            }
-        }
-        float4_t c[4];
-#pragma unroll
-        for (int ht = 0; ht < 4; ++ht) {
-            c[ht] = float4_t{0, 0, 0, 0};
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                c[ht] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qh[ht][ks], a[ks], c[ht], 0, 0, 0);
-                c[ht] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ql[ht][ks], a[ks], c[ht], 0, 0, 0);
-            }
-        }
-        // lane (j, g): heads 16 ht + 4 g + r of key j
-        float v = 0.0f;
-#pragma unroll
-        for (int ht = 0; ht < 4; ++ht)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                float rl;   // relu without the quieting that fmaxf adds
-                asm("v_max_f32 %0, 0, %1" : "=v"(rl) : "v"(c[ht][r]));
-                v = fmaf(wr[ht][r], rl, v);
-            }
-        v = pf_xsum(v);
-        const float kn2 = pf_xsum(n2);   // ||k_j||^2
-        const int kr = 16 * tile + j;
-        if (g == 0 && kr < n_cand) {
-            const float b = kBoundC * sqrtf(kn2) * wq;
-            a_out[kr] = v;
-            S.bound[kr] = b;
-            bmax = fmaxf(bmax, b);
-            atomicAdd(&lh[ord_key(v) >> 21], 1u);
-        }
-    };
-    const int first = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(wave);
-    uint4_t ub0[4], ub1[4];
-    if (first < n_tiles) load_tile(first, ub0);
-    for (int tile = first; tile < n_tiles; tile += 2 * stride) {
-        load_tile(min(tile + stride, n_tiles - 1), ub1);
-        process(tile, ub0);
-        if (tile + stride >= n_tiles) break;
-        load_tile(min(tile + 2 * stride, n_tiles - 1), ub0);
-        process(tile + stride, ub1);
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) bmax = fmaxf(bmax, __shfl_xor(bmax, off));
-    if (lane == 0) atomicMax(&s_bmax, __float_as_uint(bmax));
-    __syncthreads();
-    for (int i = tid; i < kBins; i += 256)
-        if (lh[i]) atomicAdd(&hist1[i], lh[i]);
-    if (tid == 0) atomicMax(S.bmax, s_bmax);
-}
-
-// Exact score of key c (the canonical chains): lane h forms dot_h over d
-// ascending, then the head chain runs over h ascending in lane 0.
-__device__ inline float exact_score_wave(const float *qs, const float *ws, const uint16_t *keys, int c) {
-    const int h = threadIdx.x & 63;
-    const uint16_t *kr = keys + (size_t)c * kMaxDim;
-    uint4_t kk[kMaxDim / 8];   // the whole key first: one memory round trip
-#pragma unroll
-    for (int v = 0; v < kMaxDim / 8; ++v) kk[v] = *reinterpret_cast<const uint4_t *>(kr + 8 * v);
-    float dot = 0.0f;
-#pragma unroll
-    for (int v = 0; v < kMaxDim / 8; ++v) {
-        const uint4_t u = kk[v];
-        const float4_t q0 = *reinterpret_cast<const float4_t *>(qs + h * kQStride + 8 * v);
-        const float4_t q1 = *reinterpret_cast<const float4_t *>(qs + h * kQStride + 8 * v + 4);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const uint16_t b = (uint16_t)((u[e >> 1] >> (16 * (e & 1))) & 0xFFFF);
-            dot = fmaf(e < 4 ? q0[e] : q1[e - 4], bf16_to_f32(b), dot);
-        }
-    }
-    const float r = dot > 0.0f ? dot : 0.0f;
-    float s = 0.0f;
-#pragma unroll
-    for (int hh = 0; hh < kMaxHeads; ++hh)
-        s = fmaf(ws[hh], __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r), hh)), s);
-    return s;
-}
-
-// Threshold of the need-th largest of n 32-bit keys key_of(i) (need >= 1):
-// returns T and how many entries equal to T are taken. One workgroup.
-template <typename KeyOf>
-__device__ void wg_select(int n, unsigned need, KeyOf key_of, unsigned *lh, unsigned *scratch,
-                          unsigned *s_bin, unsigned *s_above, unsigned *T_out, unsigned *eq_out) {
-    unsigned prefix = 0, mask = 0;
-    const int shifts[3] = {21, 10, 0};
-    const int widths[3] = {11, 11, 10};
-    for (int lvl = 0; lvl < 3; ++lvl) {
-        const int nb = 1 << widths[lvl];
-        for (int i = threadIdx.x; i < kBins; i += 256) lh[i] = 0;
-        __syncthreads();
-        for (int i = threadIdx.x; i < n; i += 256) {
-            const unsigned k = key_of(i);
-            if ((k & mask) == prefix) atomicAdd(&lh[(k >> shifts[lvl]) & (nb - 1)], 1u);
-        }
-        __syncthreads();
-        find_bin(lh, nb, need, s_bin, s_above, scratch);
-        prefix |= *s_bin << shifts[lvl];
-        mask |= (unsigned)(nb - 1) << shifts[lvl];
-        need -= *s_above;
-        __syncthreads();
-    }
-    *T_out = prefix;
-    *eq_out = need;
-}
-
-__global__ __launch_bounds__(256) void band_kernel(const float *__restrict__ q,
-                                                   const float *__restrict__ w,
-                                                   const uint16_t *__restrict__ keys, int n_cand,
-                                                   int n_comp, unsigned need0, int n_chunks,
-                                                   float *__restrict__ a_io,
-                                                   const unsigned *__restrict__ hists, PfScratch S) {
-    __shared__ __attribute__((aligned(16))) float qs[kMaxHeads * kQStride];
-    __shared__ float ws[kMaxHeads];
-    __shared__ unsigned lh[kBins];
-    __shared__ unsigned scratch[256];
-    __shared__ unsigned s_bin, s_above, s_ticket, s_cnt[4];
-    __shared__ int band_l[kChunk];
-    __shared__ unsigned s_nband;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    // the bucket of the need0-th largest approximate score
-    find_bin(hists, kBins, need0, &s_bin, &s_above, scratch);
-    unsigned prefix = s_bin << 21;
-    const unsigned need1 = need0 - s_above;
-    __syncthreads();
-    find_bin(hists + kBins, kBins, need1, &s_bin, &s_above, scratch);
-    prefix |= s_bin << 10;
-    const float lo = key_to_float(prefix), hi = key_to_float(prefix | 0x3FFu);
-    const float B = __uint_as_float(*S.bmax);
-    if (tid == 0) s_nband = 0;
-    stage_query<kQStride>(qs, q, kMaxHeads);
-    if (tid < kMaxHeads) ws[tid] = w[tid];
-    __syncthreads();
-    unsigned cin = 0;
-    for (int i = 0; i < 4; ++i) {
-        const int c = blockIdx.x * kChunk + i * 256 + tid;
-        if (c >= n_cand) continue;
-        const float a = a_io[c], b = S.bound[c];
-        if (a - b > hi + B) {
-            a_io[c] = INFINITY;
-            ++cin;
-        } else if (a + b < lo - B) {
-            a_io[c] = -INFINITY;
-        } else {
-            band_l[atomicAdd(&s_nband, 1u)] = c;
-        }
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) cin += __shfl_xor(cin, off);
-    if (lane == 0) s_cnt[wave] = cin;
-    __syncthreads();
-    const unsigned nband = s_nband;
-    // exact rescoring: one wave per band key, into this chunk's band slots
-    const size_t base = (size_t)blockIdx.x * kChunk;
-    for (unsigned e = wave; e < nband; e += 4) {
-        const int c = band_l[e];
-        const float s = exact_score_wave(qs, ws, keys, c);
-        if (lane == 0) {
-            S.band_val[base + e] = s;
-            S.band_idx[base + e] = c;
-        }
-    }
-    if (tid == 0) {
-        S.chunk_in[blockIdx.x] = s_cnt[0] + s_cnt[1] + s_cnt[2] + s_cnt[3];
-        S.band_n[blockIdx.x] = nband;
-    }
-    // the last workgroup to finish selects within the band
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) s_ticket = atomicAdd(S.done, 1u);
-    __syncthreads();
-    if (s_ticket != gridDim.x - 1) return;
-    __threadfence();
-    // compact the chunks' band entries (4 chunks per thread; <= 1024 chunks)
-    int nb;
-    {
-        unsigned v[4], tot = 0;
-        for (int k = 0; k < 4; ++k) {
-            const int i = 4 * tid + k;
-            // (bounded: a chunk holds at most kChunk band keys)
-            v[k] = i < (int)gridDim.x ? min(ld_agent(&S.band_n[i]), (unsigned)kChunk) : 0u;
-            tot += v[k];
-        }
-        unsigned ex;
-        nb = (int)block_excl_scan(tot, scratch, &ex);
-        for (int k = 0; k < 4; ++k) {
-            const int i = 4 * tid + k;
-            for (unsigned e = 0; e < v[k]; ++e) {
-                S.cval[ex + e] = ld_agent(&S.band_val[(size_t)i * kChunk + e]);
-                S.cidx[ex + e] = ld_agent(&S.band_idx[(size_t)i * kChunk + e]);
-            }
-            ex += v[k];
-        }
-        __threadfence_block();
-        __syncthreads();
-    }
-    unsigned c_in = 0;
-    for (int i = tid; i < (int)gridDim.x; i += 256) c_in += ld_agent(&S.chunk_in[i]);
-    for (int off = 32; off > 0; off >>= 1) c_in += __shfl_xor(c_in, off);
-    if (lane == 0) s_cnt[wave] = c_in;
-    __syncthreads();
-    c_in = s_cnt[0] + s_cnt[1] + s_cnt[2] + s_cnt[3];
-    const unsigned m = need0 - c_in;   // band keys to take (1 <= m <= nb)
-    unsigned T, eq;
-    wg_select(nb, m, [&](int i) { return ord_key(S.cval[i]); }, lh, scratch, &s_bin, &s_above, &T, &eq);
-    // ties at T: the eq lowest indices (the largest ~index)
-    unsigned Ti = 0, eqi = 0;
-    if (eq > 0) {
-        wg_select(nb, eq, [&](int i) { return ord_key(S.cval[i]) == T ? ~(unsigned)S.cidx[i] : 0u; },
-                  lh, scratch, &s_bin, &s_above, &Ti, &eqi);
-    }
-    // chunk counts: certainly selected + selected band keys + forced recent positions
-    unsigned *cnt = lh;   // reuse: n_chunks <= kPfMaxChunks <= kBins
-    for (int i = tid; i < n_chunks; i += 256) cnt[i] = i < (int)gridDim.x ? ld_agent(&S.chunk_in[i]) : 0u;
-    __syncthreads();
-    for (int i = tid; i < nb; i += 256) {
-        const unsigned k = ord_key(S.cval[i]);
-        const int c = S.cidx[i];
-        if ((unsigned)c >= (unsigned)n_cand) continue;   // (never: every entry is a candidate)
-        const bool sel = k > T || (k == T && eq > 0 && ~(unsigned)c >= Ti);
-        a_io[c] = sel ? INFINITY : -INFINITY;
-        if (sel) atomicAdd(&cnt[c / kChunk], 1u);
-    }
-    __syncthreads();
-    for (int i = tid; i < n_chunks; i += 256) {
-        const int c0 = i * kChunk, c1 = min(c0 + kChunk, n_comp);
-        const int r0 = max(c0, n_cand);
-        cnt[i] += r0 < c1 ? (unsigned)(c1 - r0) : 0u;
-    }
-    __syncthreads();
-    // exclusive prefix over the chunks (n_chunks <= 1024: 4 per thread)
-    unsigned v[4], tot = 0;
-    for (int k = 0; k < 4; ++k) {
-        const int i = 4 * tid + k;
-        v[k] = i < n_chunks ? cnt[i] : 0u;
-        tot += v[k];
-    }
-    unsigned ex;
-    const unsigned total = block_excl_scan(tot, scratch, &ex);
-    for (int k = 0; k < 4; ++k) {
-        const int i = 4 * tid + k;
-        if (i < n_chunks) S.chunk_off[i] = ex;
-        ex += v[k];
-    }
-    if (tid == 0) {
-        *S.done = 0;
-        // the counts add up to the output size by construction; if they ever
-        // did not, the emit kernel writes positions 0.. instead of a list with
-        // holes (every output slot stays a valid row index)
-        S.bmax[2] = total == need0 + (unsigned)(n_comp - n_cand) ? 0u : 1u;
-    }
-}
-
-// Per chunk: positions of the marked (+inf) candidates and of the forced
-// recent window, in index order, from the chunk's offset.
-__global__ __launch_bounds__(256) void emit_marked_kernel(const float *__restrict__ marks, int n_comp,
-                                                          int n_cand, int n_out, PfScratch S,
-                                                          int32_t *__restrict__ mask,
-                                                          int32_t *__restrict__ pos_out) {
-    __shared__ unsigned buf[256];
-    if (S.bmax[2]) {
-        for (int i = blockIdx.x * 256 + threadIdx.x; i < n_out; i += gridDim.x * 256) {
-            if (pos_out) pos_out[i] = i < n_comp ? i : n_comp - 1;
-            if (mask && i < n_comp) mask[i] = 1;
-        }
-        return;
-    }
-    const int base = blockIdx.x * kChunk + threadIdx.x * 4;
-    bool take[4];
-    unsigned my = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int c = base + i;
-        take[i] = c < n_cand ? marks[c] == INFINITY : c < n_comp;
-        my += take[i];
-    }
-    unsigned ex;
-    block_excl_scan(my, buf, &ex);
-    unsigned o = S.chunk_off[blockIdx.x] + ex;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int c = base + i;
-        if (c >= n_comp) break;
-        if (mask) mask[c] = take[i] ? 1 : 0;
-        if (take[i] && pos_out && o < (unsigned)n_out) pos_out[o] = c;
-        o += take[i];
-    }
-}
-
-int pf_grid() {
-    static const int v = [] {
-        const char *e = getenv("DS4HIP_PF_GRID");
-        return e ? atoi(e) : 256;
-    }();
-    return v;
-}
-
-int score_select_prefilter(const float *q, const float *w, const uint16_t *keys, int n_comp,
-                           int n_cand, unsigned need0, float *scores, unsigned *scratch, int32_t *mask,
-                           int32_t *pos_out, hipStream_t st) {
-    const PfScratch S = pf_scratch(scratch, n_comp);
-    const int n_chunks = (n_comp + kChunk - 1) / kChunk;
-    const int n_band_wg = (n_cand + kChunk - 1) / kChunk;
-    hipLaunchKernelGGL(zero_u32_kernel, dim3(24), dim3(256), 0, st, scratch, 3 * kBins + 64);
-    hipLaunchKernelGGL(prefilter_kernel, dim3(std::min(pf_grid(), (n_cand + 63) / 64)), dim3(256), 0, st, q, w,
-                       keys, n_cand, scores, scratch, S);
-    const int g = (n_cand + 256 * 8 - 1) / (256 * 8) + 1;
-    hipLaunchKernelGGL(hist_next_kernel<2>, dim3(g), dim3(256), 0, st, scores, n_cand, need0, scratch);
-    hipLaunchKernelGGL(band_kernel, dim3(n_band_wg), dim3(256), 0, st, q, w, keys, n_cand, n_comp, need0,
-                       n_chunks, scores, scratch, S);
-    hipLaunchKernelGGL(emit_marked_kernel, dim3(n_chunks), dim3(256), 0, st, scores, n_comp, n_cand,
-                       (int)need0 + (n_comp - n_cand), S, mask, pos_out);
-    return hip_status(hipGetLastError());
-}
-
 int launch_scores(const float *q, const float *w, const void *keys, int kind, int n_comp,
                   int n_head, int head_dim, float *scores, unsigned *hist, int n_cand,
                   hipStream_t st) {
     const bool full = head_dim == kMaxDim;
     const dim3 grid((n_comp + 255) / 256);
-    if (full && n_head % 4 == 0 && n_comp > 0 && sgpr_scores_enabled()) {
-        switch (kind) {
-        case 0: hipLaunchKernelGGL(score_sgpr_kernel<0>, grid, dim3(256), 0, st, q, w, keys, n_comp, n_head, scores, hist, n_cand); break;
-        case 1: hipLaunchKernelGGL(score_sgpr_kernel<1>, grid, dim3(256), 0, st, q, w, keys, n_comp, n_head, scores, hist, n_cand); break;
-        default: hipLaunchKernelGGL(score_sgpr_kernel<2>, grid, dim3(256), 0, st, q, w, keys, n_comp, n_head, scores, hist, n_cand); break;
-        }
-        return hip_status(hipGetLastError());
-    }
     switch (kind) {
     case 0:
         if (full) hipLaunchKernelGGL((score_kernel<0, true>), grid, dim3(256), 0, st, q, w, keys, n_comp, n_head, head_dim, scores, hist, n_cand);
@@ -1133,7 +625,7 @@ int launch_scores(const float *q, const float *w, const void *keys, int kind, in
 // always selected and take part in no comparison.
 size_t select_scratch_bytes(int n_comp) {
     const size_t chunks = (size_t)(n_comp > 0 ? n_comp : 1) / kChunk + 1;
-    return std::max((3 * kBins + 2 * chunks), pf_scratch_words(n_comp)) * sizeof(unsigned);
+    return (3 * kBins + 2 * chunks) * sizeof(unsigned);
 }
 
 int score_select(const float *q, const float *w, const void *keys, int kind, int n_comp,
@@ -1158,14 +650,6 @@ int score_select(const float *q, const float *w, const void *keys, int kind, int
     const int n_cand = n_comp - recent;
     const unsigned need0 = (unsigned)(top_k - recent);
     const int n_chunks = (n_comp + kChunk - 1) / kChunk;
-    // bf16 keys of the model's indexer shape: the MFMA prefilter with exact
-    // rescoring near the threshold (the same selection, a fraction of the work)
-    if (kind == 2 && n_head == kMaxHeads && head_dim == kMaxDim && n_cand >= kPfMinCand &&
-        (n_cand + kChunk - 1) / kChunk <= kPfMaxChunks && n_chunks <= kPfMaxChunks &&
-        !(reinterpret_cast<uintptr_t>(keys) & 15) && !(reinterpret_cast<uintptr_t>(q) & 15) &&
-        prefilter_enabled())
-        return score_select_prefilter(q, w, static_cast<const uint16_t *>(keys), n_comp, n_cand, need0,
-                                      scores, scratch, mask, pos_out, st);
     unsigned *hists = scratch;
     unsigned *chunk_gt = scratch + 3 * kBins;
     unsigned *chunk_eq = chunk_gt + n_chunks;
@@ -1203,13 +687,6 @@ extern "C" int ds4hip_scale_inplace_f32(float *y, int n, float scale, void *stre
 }
 
 extern "C" size_t ds4hip_indexer_select_scratch_bytes(int n_comp) { return select_scratch_bytes(n_comp); }
-
-extern "C" int ds4hip_set_indexer_prefilter(int enable) {
-    if (enable != 0 && enable != 1) return ds4hip_set_last_error(kEINVAL);
-    const int prev = prefilter_enabled() ? 1 : 0;
-    g_prefilter = enable;
-    return prev;
-}
 
 // The reference launchers take only a score scratch; the selection
 // histograms are stream-ordered allocations here.

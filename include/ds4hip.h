@@ -327,18 +327,6 @@ int ds4hip_indexer_topk_positions(const float *q, const float *weights, const vo
                                   int n_recent, float *scratch_scores, void *scratch_select,
                                   int32_t *allowed_mask, int32_t *positions_out, void *stream);
 
-/* Selects how ds4hip_indexer_topk_positions scores bf16 keys of the model's
- * shape (64 heads x 128, at least 8192 candidates): 0 (the default; also
- * DS4HIP_INDEXER_PREFILTER unset or not "1") = exact scores for every key;
- * 1 = approximate scores on the bf16 MFMA with a proven error bound, exact
- * fixed-order rescoring of the keys that bound leaves near the threshold.
- * Both select the same positions. Mode 1 is experimental: it stays off by
- * default until a GPU fault seen with it is explained. In mode 1, scratch_scores ends holding +inf for
- * the selected candidates and -inf for the others instead of the scores.
- * Process-wide, not synchronized with calls in flight; returns the previous
- * mode. No counterpart in the reference (its scorer has no prefilter). */
-int ds4hip_set_indexer_prefilter(int enable);
-
 /* Sparse-decode selection for up to 16 sequences in one launch pair
  * (additive). Sequence s scores its n_comp_host[s] key rows starting at key
  * row key_row0_host[s] of `keys` (key_kind as above, head_dim 128) with query

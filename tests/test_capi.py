@@ -68,7 +68,7 @@ def test_newer_entry_points_refuse_bad_arguments_on_the_host():
     assert l.ds4hip_session_chunk_rows(N, 0, 0, 1, N, N, N, 0, N, 0, N, N) == -22
     assert l.ds4hip_session_push_raw(N, 0, N, N) == -22
     assert l.ds4hip_session_state_describe(N, 16) == -22
-    for setter in (l.ds4hip_set_decode_flat_lean, l.ds4hip_set_indexer_prefilter,
+    for setter in (l.ds4hip_set_decode_flat_lean,
                    l.ds4hip_set_decode_exact_p):
         assert setter(5) == -22
     cnt = (C.c_longlong * 1)(10)

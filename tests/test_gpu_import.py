@@ -81,7 +81,6 @@ def test_import_reference_session(gpu, tmp_path, max_ctx, pos):
         s.close()
 
 
-@unverified("the export to reference session files has not run on the GPU yet")
 def test_reference_file_round_trip(gpu, tmp_path):
     """A reference file whose rows are what the reference holds (window rows
     FP8 values rounded to f16, compressed rows FP8 values with an f16 tail)

@@ -161,29 +161,13 @@ def test_indexer_positions_with_ties_and_recent(gpu):
     O.lib().orc_topk_positions(P(ref_s), C.c_int(n_comp), C.c_int(top_k), C.c_int(recent),
                                P(ref_p))
     kt = t(kb.view(np.int16), gpu).view(torch.bfloat16)
-    from ds4cuda_amd import lib
-    prev = lib().ds4hip_set_indexer_prefilter(0)
-    try:
-        # the exact path only: the MFMA prefilter (mode 1) has its own test,
-        # test_gpu_prefilter.py, skipped until the prefilter runs again
-        for mode in (0,):
-            lib().ds4hip_set_indexer_prefilter(mode)
-            mask = torch.empty(n_comp, dtype=torch.int32, device=gpu)
-            pos, _, scores = ops.indexer_topk_positions(t(qf, gpu), t(w, gpu), kt, top_k, recent,
-                                                        mask=mask)
-            torch.cuda.synchronize()
-            sc = scores.cpu().numpy()
-            if mode == 0:
-                assert np.array_equal(sc.view(np.uint32), ref_s.view(np.uint32))
-            else:   # candidates marked +inf (selected) / -inf
-                sel = np.zeros(n_comp - recent, bool)
-                sel[ref_p[ref_p < n_comp - recent]] = True
-                assert np.array_equal(sc[:n_comp - recent], np.where(sel, np.inf, -np.inf).astype(np.float32))
-            assert np.array_equal(pos.cpu().numpy(), ref_p), mode
-            m = mask.cpu().numpy()
-            assert m.sum() == top_k and np.array_equal(np.nonzero(m)[0], ref_p)
-    finally:
-        lib().ds4hip_set_indexer_prefilter(prev)
+    mask = torch.empty(n_comp, dtype=torch.int32, device=gpu)
+    pos, _, scores = ops.indexer_topk_positions(t(qf, gpu), t(w, gpu), kt, top_k, recent, mask=mask)
+    torch.cuda.synchronize()
+    assert np.array_equal(scores.cpu().numpy().view(np.uint32), ref_s.view(np.uint32))
+    assert np.array_equal(pos.cpu().numpy(), ref_p)
+    m = mask.cpu().numpy()
+    assert m.sum() == top_k and np.array_equal(np.nonzero(m)[0], ref_p)
 
 
 def test_short_circuit_and_scale(gpu):

@@ -1557,11 +1557,12 @@ __device__ inline float xmax_16_32_raw(float v) {
     return vmax_f32(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
-// kLean: the producer form with fewer VALU instructions per tile (the score
-// scale folded into Q, packed E8M0 row scales from one byte permute, the f16
-// scale table from v_ldexp_f16, P's row sums by v_dot2, one select for empty
-// tiles). Same results up to rounding: Q is scaled by log2(e)/sqrt(d) before
-// its FP8 / f16 rounding instead of S after the MFMA.
+// kLean: the producer form with fewer VALU instructions per tile (packed
+// E8M0 row scales from one byte permute, the f16 scale table from
+// v_ldexp_f16, P's row sums by v_dot2, one select for empty tiles, whole-tile
+// copies from an SGPR base). The score scale log2(e)/sqrt(d) stays on S after
+// the MFMA: folded into Q it would make the bf16 values inexact in the two
+// E4M3 parts (a bf16 value's 8 significant bits split exactly into hi + lo).
 template <bool kPLo, bool kLean>
 __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A) {
     static_assert(!kPLo, "the flat kernel passes P as one f16");
@@ -1626,10 +1627,6 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
                             for (int i = 0; i < 4; ++i) {
                                 x[16 * hv + 8 * v + 2 * i] = bf16_to_f32((uint16_t)(w[i] & 0xFFFF));
                                 x[16 * hv + 8 * v + 2 * i + 1] = bf16_to_f32((uint16_t)(w[i] >> 16));
-                                if constexpr (kLean) {   // S comes out in log2 units
-                                    x[16 * hv + 8 * v + 2 * i] *= A.kq_log2;
-                                    x[16 * hv + 8 * v + 2 * i + 1] *= A.kq_log2;
-                                }
                             }
                         }
                     }
@@ -1668,13 +1665,8 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
                     half8_t h;
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        if constexpr (kLean) {
-                            h[2 * i] = (half_t)(bf16_to_f32((uint16_t)(w[i] & 0xFFFF)) * A.kq_log2);
-                            h[2 * i + 1] = (half_t)(bf16_to_f32((uint16_t)(w[i] >> 16)) * A.kq_log2);
-                        } else {
-                            h[2 * i] = (half_t)bf16_to_f32((uint16_t)(w[i] & 0xFFFF));
-                            h[2 * i + 1] = (half_t)bf16_to_f32((uint16_t)(w[i] >> 16));
-                        }
+                        h[2 * i] = (half_t)bf16_to_f32((uint16_t)(w[i] & 0xFFFF));
+                        h[2 * i + 1] = (half_t)bf16_to_f32((uint16_t)(w[i] >> 16));
                     }
                     qt[s2] = h;
                 }
@@ -1689,7 +1681,7 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) s8[hh][r] = kLean ? sa[hh][r] : sa[hh][r] * A.kq_log2;
+                    for (int r = 0; r < 4; ++r) s8[hh][r] = sa[hh][r] * A.kq_log2;
                 if (nv < kTile) {
 #pragma unroll
                     for (int hh = 0; hh < 2; ++hh)

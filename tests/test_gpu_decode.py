@@ -6,7 +6,6 @@ import torch
 
 import oracle as O
 from ds4cuda_amd import ops, synth
-from unverified import unverified
 
 pytestmark = pytest.mark.gpu
 
@@ -217,8 +216,6 @@ def test_fp8_p_precision_modes(gpu, n_kv):
     assert _lib.lib().ds4hip_set_decode_exact_p(2) == -22
 
 
-@unverified("the lean form of the flat decode kernel (ds4hip_set_decode_flat_lean) has not run on "
-            "the GPU yet")
 @pytest.mark.parametrize("counts", [[1], [33], [1000], [300, 0, 64, 1025, 7], [32768]])
 def test_fp8_flat_lean_form(gpu, counts):
     """The lean form (score scale folded into Q, packed row scales, SGPR-based

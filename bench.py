@@ -41,10 +41,9 @@ COPY_BYTES = 1 << 30                               # --copy-calibration: 1 GiB r
 # Re-measure after a kernel change.
 TRAFFIC_BYTES_PER_LAUNCH = {"ws": 882340981, "flat": 882148944}
 TRAFFIC_MEASURED_AT = {"ws": "22db79c", "flat": "dedad2c"}   # commit whose partial kernel was counted
-DECODE_KERNEL = "ws" if os.environ.get("DS4HIP_DECODE_KERNEL", "").startswith("w") else "flat"
+DECODE_KERNEL = "flat"
 KERNEL_LABEL = {"ws": "decode_ws_kernel<0, false> (direct rows, register loads, one f16 P)",
-                "lean": "decode_flat_kernel<false, true> (flat stages, lean producer form, one f16 P)",
-                "flat": "decode_flat_kernel<false> (direct rows, DMA-fed flat LDS stages, one f16 P)"}
+                "flat": "decode_flat_kernel<false, true> (direct rows, DMA-fed flat LDS stages, one f16 P)"}
 
 
 def bytes_per_layer():
@@ -308,9 +307,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the prefill / sparse-decode / batched-block figures")
-    ap.add_argument("--kernel", choices=("flat", "lean", "ws"), default=None,
-                    help="decode kernel for direct rows: the flat-stage kernel (default), its lean "
-                         "form, or the register-load kernel")
+    ap.add_argument("--kernel", choices=("flat", "ws"), default=None,
+                    help="decode kernel for direct rows: the flat-stage kernel (default) or the "
+                         "register-load kernel")
     ap.add_argument("--only", choices=("prefill", "sparse", "batch"),
                     help="run one secondary config alone and print its figures as one JSON "
                          "line (for profiling it without the cfg 2 cache)")
@@ -324,17 +323,12 @@ def main():
         sys.exit(2)
 
     global DECODE_KERNEL
-    if args.kernel == "ws":
-        os.environ["DS4HIP_DECODE_KERNEL"] = "ws"   # read once, at the first decode launch
     if args.kernel:
         DECODE_KERNEL = args.kernel
     import torch
     from ds4cuda_amd import ops
 
     dev = torch.device("cuda:0")
-    if args.kernel == "lean":
-        from ds4cuda_amd import lib
-        lib().ds4hip_set_decode_flat_lean(1)
     if args.copy_calibration:
         n = COPY_BYTES // 4
         src = torch.ones(n, dtype=torch.float32, device=dev)
@@ -368,9 +362,12 @@ def main():
     ws = torch.empty(ops.decode_fp8_workspace_bytes(counts), dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream()
 
-    def step(phases=3):
+    kern = "regload" if DECODE_KERNEL == "ws" else "auto"
+
+    def step(phases=3, exact_p=False):
         ops.flash_attn_decode_fp8(q, sinks, out, cache, counts, row_base_stride=N_KV,
-                                  workspace=ws, phases=phases, stream=stream)
+                                  workspace=ws, phases=phases, exact_p=exact_p, kernel=kern,
+                                  stream=stream)
 
     for _ in range(args.warmup):
         step()
@@ -398,10 +395,7 @@ def main():
     k_ms = float(np.mean([s.elapsed_time(e) for s, e in zip(starts, ends)]))
 
     # the same step with P passed to P.V as f16 hi + lo halves (~22 bits)
-    from ds4cuda_amd._lib import lib as _l
-    prev = _l().ds4hip_set_decode_exact_p(1)
-    ms_exact = time_ms(step, args.steps, 2, stream)
-    _l().ds4hip_set_decode_exact_p(prev)
+    ms_exact = time_ms(lambda: step(exact_p=True), args.steps, 2, stream)
 
     step_bytes = N_LAYERS * bytes_per_layer()
     value = step_bytes / (ms * 1e-3) / 1e9

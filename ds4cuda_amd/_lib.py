@@ -22,8 +22,6 @@ SIGNATURES: dict[str, list] = {
     "ds4hip_fp8_kv_quantize_append": [_vp, _i, _i, _i, _vp, _vp, _vp, _ll, _vp, _vp],
     "ds4hip_flash_attn_decode_raw_f32": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp],
     "ds4hip_flash_attn_decode_mixed_f32": [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp],
-    "ds4hip_set_decode_exact_p": [_i],
-    "ds4hip_set_decode_flat_lean": [_i],
     "ds4hip_flash_attn_decode_f32_workspace_size": [_ll, C.POINTER(_sz)],
     "ds4hip_flash_attn_decode_raw_f32_prealloc": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp, _sz,
                                                   _vp],
@@ -34,7 +32,7 @@ SIGNATURES: dict[str, list] = {
     "ds4hip_flash_attn_decode_fp8_workspace_size": [_vp, _i, C.POINTER(_sz)],
     "ds4hip_flash_attn_decode_fp8": [
         _vp, _i, _ll, _vp, _ll, _vp, _ll, _vp, _vp, _vp, _vp, _i, _vp, _ll, _vp, _ll, _vp, _i,
-        _i, _i, _i, _i, _vp, _sz, _i, _vp],
+        _i, _i, _i, _i, _ll, _vp, _vp, _sz, _i, _vp],
     "ds4hip_flash_attn_prefill_fp8_workspace_size": [_i],
     "ds4hip_flash_attn_prefill_fp8": [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _sz,
                                       _vp],

@@ -161,7 +161,7 @@ def forward_chunk_attn(session, il, p0, attn_norm, q_lora_norm, q_cur, kv_rope, 
     call("ds4hip_flash_attn_decode_fp8", _ptr(q_cur), 1, N_HEAD * HEAD_DIM, _ptr(sinks), 0, _ptr(out),
          N_HEAD * HEAD_DIM, _vp(s.codes + rb * 448), _vp(s.sexp + rb * 8), _vp(s.tail + rb * 128),
          C.cast(counts, C.c_void_p), n, None, 0, _ptr(lists), stride, None, 0, 256, N_HEAD, HEAD_DIM,
-         N_ROT, _ptr(workspace), workspace.numel(), 3, st)
+         N_ROT, C.c_longlong(session.rows_from(rb)), None, _ptr(workspace), workspace.numel(), 3, st)
     # the last token's selection stays in the layer's row list, where the
     # token-by-token loop leaves it
     if sel is not None and n_sel[-1] < n_comp[-1]:

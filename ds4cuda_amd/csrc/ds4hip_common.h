@@ -20,6 +20,16 @@ typedef short short4_t __attribute__((ext_vector_type(4)));
 constexpr int kEINVAL = -22;
 constexpr int kHipErrBase = -1000;   // returned as kHipErrBase - hipError_t
 
+// Scratch memory the library keeps per (device, stream) for entry points whose
+// reference counterparts take no workspace (the fp32 decode launchers, the
+// indexer top-k launchers): *out receives at least `bytes` of device memory
+// owned by the library, reused by every later call on the same stream, so the
+// steady state allocates nothing. It grows (stream-ordered free + allocation)
+// only when a call needs more than any earlier one on that stream. Calls on one
+// stream are ordered, so they never share it concurrently; distinct streams get
+// distinct buffers. Returns 0 or a status.
+int stream_scratch(hipStream_t stream, size_t bytes, void **out);
+
 // ---- scale rule -------------------------------------------------------------
 // The reference picks scale = 2^ceil(log2(amax/448)) per 64-element block
 // (cuda/fp8_kv.cu:174-176). With log2 evaluated as a correctly rounded fp32

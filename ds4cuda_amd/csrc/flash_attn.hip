@@ -84,6 +84,9 @@ struct DecodeArgs {
     // gathered rows (row_idx or page_table): physical row of every logical
     // row, resolved by phys_kernel before the partial kernel
     long long *phys;
+    // rows addressable from codes / sexp / tail: a row outside [0, n_cache_rows)
+    // is never read; its problem is marked bad and its output set to NaN
+    long long n_cache_rows;
     // schedule
     int n_prob;
     int chunk;
@@ -117,13 +120,73 @@ __device__ inline half8_t f32x8_to_half8(float4_t a, float4_t b) {
                    (half_t)b[0], (half_t)b[1], (half_t)b[2], (half_t)b[3]};
 }
 
+// (-1 for a position past the problem's page list: no table entry is read
+// outside [0, page_table_stride))
 __device__ inline long long phys_row(const DecodeArgs &A, int p, long long r) {
     long long pos = A.row_idx ? (long long)A.row_idx[(long long)p * A.row_idx_stride + r] : r;
     if (A.page_table) {
+        if (pos < 0 || (pos >> A.page_shift) >= A.page_table_stride) return -1;
         const long long page = A.page_table[(long long)p * A.page_table_stride + (pos >> A.page_shift)];
         return (page << A.page_shift) | (pos & ((1LL << A.page_shift) - 1));
     }
     return (A.row_base ? A.row_base[p] : (long long)p * A.row_base_stride) + pos;
+}
+
+// Out-of-range rows. phys_kernel stores kBadRow for a gathered row outside
+// the cache. A partial kernel scans its segment's rows once before the tile
+// loop (scan_segment_rows) and marks its slot with kBadSlot in ws_prob; the
+// merge then writes NaN for every head of that problem. Inside the tile loop
+// a bad row only becomes row 0 (unmark_row / clamp_row: two or three VALU
+// instructions, no carried flag, no branch), so nothing outside the cache is
+// ever read.
+constexpr long long kBadRow = (long long)(1ULL << 63);
+constexpr int kBadSlot = 1 << 30;
+__device__ inline long long unmark_row(long long r) { return r & ~(r >> 63); }
+__device__ inline long long clamp_row(long long r, long long n_rows) {
+    return min(max(r, 0LL), n_rows - 1);
+}
+// Row bases of the problems into LDS (so the tile loops issue no row loads).
+// A direct-row problem (no row_idx, no pages) whose rows [base, base + count)
+// leave the cache reads from base 0 instead and is marked bad.
+__device__ inline void stage_rowbase(const DecodeArgs &A, long long *s_rowbase, int *s_badp) {
+    const bool direct = !A.row_idx && !A.page_table;
+    for (int i = threadIdx.x; i < A.n_prob; i += blockDim.x) {
+        const long long rb = A.row_base ? A.row_base[i] : (long long)i * A.row_base_stride;
+        const bool bad = direct && (rb < 0 || rb + A.count[i] > A.n_cache_rows);
+        s_rowbase[i] = bad ? 0 : rb;
+        s_badp[i] = bad ? 1 : 0;
+    }
+}
+// Called by every thread at the start of a segment of problem p (logical
+// rows [r0, r1), global rows [g0, g1)): sets s_bad[slot_s & 1] when a
+// gathered row of the segment lies outside the cache. use_phys: the rows come
+// from the phys array this launch's phys pass wrote; otherwise from row_idx
+// (the array the workspace reserves for phys then holds nothing of this launch).
+__device__ inline void scan_segment_rows(const DecodeArgs &A, bool use_phys, int p, long long g0, long long g1,
+                                         long long r0, long long r1, long long seg_base, int slot_s, int *s_bad) {
+    bool bad = false;
+    if (use_phys) {
+        for (long long g = g0 + threadIdx.x; g < g1; g += blockDim.x) bad |= A.phys[g] < 0;
+    } else if (A.row_idx) {
+        for (long long r = r0 + threadIdx.x; r < r1; r += blockDim.x) {
+            const long long v = seg_base + A.row_idx[(long long)p * A.row_idx_stride + r];
+            bad |= v < 0 || v >= A.n_cache_rows;
+        }
+    }
+    if (bad) atomicOr(&s_bad[slot_s & 1], 1);
+}
+
+// Slot mark of a finished segment: the problem id, plus kBadSlot when a lane
+// of the workgroup met a bad row (s_bad, one word per segment parity, so the
+// next segment's marks cannot mix in) or the problem's rows were refused.
+// Called by every thread; ends with a barrier.
+__device__ inline void mark_slot(const DecodeArgs &A, long long slot, int p, int slot_s, int *s_bad,
+                                 const int *s_badp) {
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        A.ws_prob[slot] = p | ((s_bad[slot_s & 1] | s_badp[p]) ? kBadSlot : 0);
+        s_bad[slot_s & 1] = 0;
+    }
 }
 
 // fp32 rows (reference launchers): the lane's 16-dim slice of block b,
@@ -630,8 +693,9 @@ __global__ __launch_bounds__(256) void decode_fp8_kernel(const DecodeArgs A) {
     __shared__ __attribute__((aligned(16))) float alpha_s[kH];
     __shared__ long long s_start[kMaxProb + 1];
     __shared__ long long s_rowbase[kMaxProb];   // LDS, so the ring loop issues no row loads
-    for (int i = threadIdx.x; i < A.n_prob; i += blockDim.x)
-        s_rowbase[i] = A.row_base ? A.row_base[i] : (long long)i * A.row_base_stride;
+    __shared__ int s_badp[kMaxProb], s_bad[2];
+    stage_rowbase(A, s_rowbase, s_badp);
+    if (threadIdx.x < 2) s_bad[threadIdx.x] = 0;
     stage_start(A, s_start);
 
     const int lane = threadIdx.x & 63;
@@ -675,12 +739,13 @@ __global__ __launch_bounds__(256) void decode_fp8_kernel(const DecodeArgs A) {
         load_q_split<kQf32>(A, p, wave, j, q, qh, ql);
         // rows of the next tile to issue (gathered: read ahead, see below)
         long long nh0 = 0, nh1 = 0, ne = 0;
+        scan_segment_rows(A, gather, p, g0, seg_end, r0, r1, seg_base, slot_s, s_bad);
         auto rows_global = [&](int t, long long &h0, long long &h1, long long &e) {
             const long long gb = g0 + (long long)t * kTile;
             const long long gl = seg_end - 1;
-            h0 = A.phys[min(gb + k4, gl)];
-            h1 = A.phys[min(gb + 16 + k4, gl)];
-            e = A.phys[min(gb + (lane >> 1), gl)];
+            h0 = unmark_row(A.phys[min(gb + k4, gl)]);
+            h1 = unmark_row(A.phys[min(gb + 16 + k4, gl)]);
+            e = unmark_row(A.phys[min(gb + (lane >> 1), gl)]);
         };
         for (int s = 0; s < kStages - 1 && s < n_tiles; ++s) {
             long long h0, h1, e;
@@ -718,8 +783,12 @@ __global__ __launch_bounds__(256) void decode_fp8_kernel(const DecodeArgs A) {
             const uint8_t *st = stages[t % kStages];
             // gathered rows of tile t+kStages rode in with tile t; they are read
             // now, before the next iteration refills any stage
-            if (gather && t + kStages < n_tiles)
+            if (gather && t + kStages < n_tiles) {
                 lds_ld_phys3(lds_addr(st + kPhysOff), k4, lane >> 1, nh0, nh1, ne);
+                nh0 = unmark_row(nh0);
+                nh1 = unmark_row(nh1);
+                ne = unmark_row(ne);
+            }
             const long long rb = r0 + (long long)t * kTile;
 
             // ---- 1. partial S^T over this wave's dims; V_w slice to LDS ----------
@@ -846,7 +915,7 @@ __global__ __launch_bounds__(256) void decode_fp8_kernel(const DecodeArgs A) {
                 A.ws_ml[slot * 2 * kH + 16 * wave + j] = S.m_run;
                 A.ws_ml[slot * 2 * kH + kH + 16 * wave + j] = l;
             }
-            if (threadIdx.x == 0) A.ws_prob[slot] = p;
+            mark_slot(A, slot, p, slot_s, s_bad, s_badp);
         }
         ++slot_s;
         g0 = seg_end;
@@ -967,8 +1036,9 @@ __global__ __launch_bounds__(512, 1) void decode_ws_kernel(const DecodeArgs A) {
     __shared__ __attribute__((aligned(16))) float alpha_s[2][kH];
     __shared__ long long s_start[kMaxProb + 1];
     __shared__ long long s_rowbase[kMaxProb];
-    for (int i = threadIdx.x; i < A.n_prob; i += blockDim.x)
-        s_rowbase[i] = A.row_base ? A.row_base[i] : (long long)i * A.row_base_stride;
+    __shared__ int s_badp[kMaxProb], s_bad[2];
+    stage_rowbase(A, s_rowbase, s_badp);
+    if (threadIdx.x < 2) s_bad[threadIdx.x] = 0;
     stage_start(A, s_start);
 
     const int lane = threadIdx.x & 63;
@@ -989,6 +1059,7 @@ __global__ __launch_bounds__(512, 1) void decode_ws_kernel(const DecodeArgs A) {
         const long long r1 = min(seg_end - s_start[p], A.count[p]);
         const int n_tiles = 2 * (int)((r1 - r0 + 2 * kTile - 1) / (2 * kTile));   // even, >= 2
         const long long slot = (long long)blockIdx.x * A.s_max + slot_s;
+        scan_segment_rows(A, kMode == 1, p, g0, seg_end, r0, r1, s_rowbase[p], slot_s, s_bad);
         if (producer) {
             const long long seg_base = s_rowbase[p];
             // kT: the wave of dims [384, 512): one FP8 block + the f16 RoPE tail
@@ -998,8 +1069,9 @@ __global__ __launch_bounds__(512, 1) void decode_ws_kernel(const DecodeArgs A) {
                 // the end: the last row)
                 auto row_gather = [&](int t, int hh) -> long long {
                     const long long lr = min((long long)t * kTile + 16 * hh + j, r1 - 1 - r0);
-                    if (kMode == 1) return A.phys[g0 + lr];
-                    return seg_base + A.row_idx[(long long)p * A.row_idx_stride + r0 + lr];
+                    if (kMode == 1) return unmark_row(A.phys[g0 + lr]);
+                    return clamp_row(seg_base + A.row_idx[(long long)p * A.row_idx_stride + r0 + lr],
+                                     A.n_cache_rows);
                 };
                 // codes 128 d + 16 q + [0, 16) and 128 d + 64 + 16 q + [0, 16), or
                 // (kT) codes 384 + 16 q + [0, 16) and tail dims 16 q + [0, 16);
@@ -1373,7 +1445,7 @@ __global__ __launch_bounds__(512, 1) void decode_ws_kernel(const DecodeArgs A) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) wo[(16 * hb + r) * kD + 16 * nb] = o[hb][nb][r];
         }
-        if (threadIdx.x == 0) A.ws_prob[slot] = p;
+        mark_slot(A, slot, p, slot_s, s_bad, s_badp);
         ++slot_s;
         g0 = seg_end;
     }
@@ -1572,8 +1644,8 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
     __shared__ __attribute__((aligned(16))) int rescale_s[2][4];   // [t & 1][head tile]: some alpha != 1
     __shared__ long long s_start[kMaxProb + 1];
     __shared__ long long s_rowbase[kMaxProb];
-    for (int i = threadIdx.x; i < A.n_prob; i += blockDim.x)
-        s_rowbase[i] = A.row_base ? A.row_base[i] : (long long)i * A.row_base_stride;
+    __shared__ int s_badp[kMaxProb];
+    stage_rowbase(A, s_rowbase, s_badp);
     stage_start(A, s_start);
 
     const int lane = threadIdx.x & 63;
@@ -2068,7 +2140,7 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
             }
         }
         // a segment with no rows (padding of the chunked row space) has no partial
-        if (threadIdx.x == 0) A.ws_prob[slot] = n_tiles > 0 ? p : -1;
+        if (threadIdx.x == 0) A.ws_prob[slot] = n_tiles > 0 ? (p | (s_badp[p] ? kBadSlot : 0)) : -1;
         ++slot_s;
         g0 = seg_end;
         lds_barrier();   // the next segment reuses the stages
@@ -2090,7 +2162,8 @@ __global__ __launch_bounds__(256) void phys_kernel(const DecodeArgs A) {
         const int mid = (lo + hi + 1) >> 1;
         if (s_start[mid] <= gg) lo = mid; else hi = mid - 1;
     }
-    A.phys[g] = phys_row(A, lo, min(gg - s_start[lo], A.count[lo] - 1));
+    const long long r = phys_row(A, lo, min(gg - s_start[lo], A.count[lo] - 1));
+    A.phys[g] = (r >= 0 && r < A.n_cache_rows) ? r : kBadRow;
 }
 
 // One block per (problem, head): combine the partials with the sink. The
@@ -2113,11 +2186,17 @@ __global__ __launch_bounds__(128) void decode_merge_kernel(const DecodeArgs A) {
         n_slot = ((b1 - 1) / A.chunk) * A.s_max + A.s_max - s0;
     }
     float mx = sink;
+    int bad = 0;
     for (long long i = tid; i < n_slot; i += 128) {
         const long long slot = s0 + i;
         const float m = A.ws_ml[slot * 2 * kH + h];
-        if (A.ws_prob[slot] == p) mx = fmaxf(mx, m);
+        const int pr = A.ws_prob[slot];
+        if ((pr & ~kBadSlot) == p) {
+            mx = fmaxf(mx, m);
+            bad |= pr & kBadSlot;
+        }
     }
+    bad = __syncthreads_or(bad);
     for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
     if ((tid & 63) == 0) s_mx[tid >> 6] = mx;
     __syncthreads();
@@ -2130,7 +2209,7 @@ __global__ __launch_bounds__(128) void decode_merge_kernel(const DecodeArgs A) {
             const long long slot = s0 + base + tid;
             const float m = A.ws_ml[slot * 2 * kH + h];
             const float l = A.ws_ml[slot * 2 * kH + kH + h];
-            if (A.ws_prob[slot] == p && m != -INFINITY) {
+            if ((A.ws_prob[slot] & ~kBadSlot) == p && m != -INFINITY) {
                 sc = __builtin_amdgcn_exp2f(m - mx);
                 dl = l * sc;
             }
@@ -2149,7 +2228,9 @@ __global__ __launch_bounds__(128) void decode_merge_kernel(const DecodeArgs A) {
             acc = c != 0.0f ? acc + o * c : acc;   // a select: unused slots may hold anything
         }
     }
-    *reinterpret_cast<float4_t *>(A.out + (long long)p * A.out_stride + h * kD + 4 * tid) = acc * (1.0f / den);
+    // a problem that met a row outside the cache gets NaN, never a plausible value
+    const float4_t res = bad ? float4_t{NAN, NAN, NAN, NAN} : acc * (1.0f / den);
+    *reinterpret_cast<float4_t *>(A.out + (long long)p * A.out_stride + h * kD + 4 * tid) = res;
 }
 
 // ---- host-side planning -----------------------------------------------------------
@@ -2250,57 +2331,26 @@ void carve(DecodeArgs &A, void *ws, const Plan &pl) {
     A.phys = reinterpret_cast<long long *>(c);   // used only by gathered steps (reset below)
 }
 
-// P . V precision of the bf16-Q decode: 1 = P as f16 hi + lo, 0 = one f16 P
-// (a third fewer MFMAs). Initial value from DS4HIP_DECODE_EXACT_P, default 0.
-int g_decode_exact_p = -1;
-bool decode_exact_p() {
-    if (g_decode_exact_p < 0) {
-        const char *e = getenv("DS4HIP_DECODE_EXACT_P");
-        g_decode_exact_p = (e && e[0] == '1') ? 1 : 0;
-    }
-    return g_decode_exact_p == 1;
-}
-
-// Direct rows with one f16 P use the flat-stage kernel unless
-// DS4HIP_DECODE_KERNEL=ws selects the register-load kernel.
-// 1 selects the flat kernel's lean form (kLean); initial value from
-// DS4HIP_FLAT_LEAN, default 0.
-int g_flat_lean = -1;
-bool use_flat_lean() {
-    if (g_flat_lean < 0) {
-        const char *e = getenv("DS4HIP_FLAT_LEAN");
-        g_flat_lean = (e && e[0] == '1') ? 1 : 0;
-    }
-    return g_flat_lean == 1;
-}
-
-bool use_flat_kernel() {
-    static const int v = [] {
-        const char *e = getenv("DS4HIP_DECODE_KERNEL");
-        return (e && e[0] == 'w') ? 0 : 1;
-    }();
-    return v == 1;
-}
-
+// Kernel for the bf16-Q partials, chosen per call (ds4hip_decode_opts): direct
+// rows with one f16 P run the flat-stage kernel (its lean form) unless the
+// caller asks for the register-load kernel; row lists, pages and the
+// hi + lo P form always run the register-load kernel (the flat kernel's
+// producers have no registers left for a second P fragment).
 template <int kMode>
-void launch_ws(const DecodeArgs &A, const Plan &pl, hipStream_t st) {
-    // (the f16 hi + lo P form keeps the register-load kernel: the flat kernel's
-    // producers have no registers left for the second P fragment)
-    if (kMode == 0 && use_flat_kernel() && !decode_exact_p()) {
-        if (use_flat_lean())
-            hipLaunchKernelGGL((decode_flat_kernel<false, true>), dim3(pl.n_wg), dim3(512), 0, st, A);
-        else
-            hipLaunchKernelGGL((decode_flat_kernel<false, false>), dim3(pl.n_wg), dim3(512), 0, st, A);
+void launch_ws(const DecodeArgs &A, const Plan &pl, hipStream_t st, const ds4hip_decode_opts &o) {
+    if (kMode == 0 && o.kernel != DS4HIP_DECODE_KERNEL_REGLOAD && !o.exact_p) {
+        hipLaunchKernelGGL((decode_flat_kernel<false, true>), dim3(pl.n_wg), dim3(512), 0, st, A);
         return;
     }
-    if (decode_exact_p())
+    if (o.exact_p)
         hipLaunchKernelGGL((decode_ws_kernel<kMode, true>), dim3(pl.n_wg), dim3(512), 0, st, A);
     else
         hipLaunchKernelGGL((decode_ws_kernel<kMode, false>), dim3(pl.n_wg), dim3(512), 0, st, A);
 }
 
 template <bool kFp8, bool kQf32>
-int launch(DecodeArgs &A, const Plan &pl, hipStream_t st, int phases = 3) {
+int launch(DecodeArgs &A, const Plan &pl, hipStream_t st, int phases = 3,
+           const ds4hip_decode_opts &o = ds4hip_decode_opts{0, 0}) {
     A.chunk = pl.chunk;
     A.s_max = pl.s_max;
     A.kq_log2 = kLog2e / sqrtf((float)kD);
@@ -2313,11 +2363,11 @@ int launch(DecodeArgs &A, const Plan &pl, hipStream_t st, int phases = 3) {
         }
         if (kFp8 && !kQf32) {
             if (idx_only)
-                launch_ws<2>(A, pl, st);
+                launch_ws<2>(A, pl, st, o);
             else if (A.phys)
-                launch_ws<1>(A, pl, st);
+                launch_ws<1>(A, pl, st, o);
             else
-                launch_ws<0>(A, pl, st);
+                launch_ws<0>(A, pl, st, o);
         }
         else if (kFp8)
             hipLaunchKernelGGL(decode_fp8_kernel<kQf32>, dim3(pl.n_wg), dim3(256), 0, st, A);
@@ -2335,20 +2385,6 @@ int launch(DecodeArgs &A, const Plan &pl, hipStream_t st, int phases = 3) {
 
 }  // namespace
 
-extern "C" int ds4hip_set_decode_exact_p(int exact) {
-    if (exact != 0 && exact != 1) return -22;
-    const int prev = decode_exact_p() ? 1 : 0;
-    g_decode_exact_p = exact;
-    return prev;
-}
-
-extern "C" int ds4hip_set_decode_flat_lean(int lean) {
-    if (lean != 0 && lean != 1) return -22;
-    const int prev = use_flat_lean() ? 1 : 0;
-    g_flat_lean = lean;
-    return prev;
-}
-
 extern "C" int ds4hip_flash_attn_decode_fp8_workspace_size(const long long *n_rows_per_prob,
                                                            int n_prob, size_t *bytes) {
     if (!bytes || n_prob <= 0 || n_prob > kMaxProb || !n_rows_per_prob) return kEINVAL;
@@ -2365,20 +2401,34 @@ extern "C" int ds4hip_flash_attn_decode_fp8(
         int n_prob, const long long *row_base, long long row_base_stride,
         const int32_t *row_idx, long long row_idx_stride, const int32_t *page_table,
         int page_table_stride, int page_rows, int n_head, int head_dim, int n_rot,
-        void *workspace, size_t workspace_bytes, int phases, void *stream) {
+        long long n_cache_rows, const ds4hip_decode_opts *opts, void *workspace,
+        size_t workspace_bytes, int phases, void *stream) {
     if (phases < 1 || phases > 3 || n_head != kH || head_dim != kD || n_rot != kRot || n_prob <= 0 || n_prob > kMaxProb ||
-        !n_rows_per_prob || !q || !sinks || !out || !codes || !sexp || !tail || !workspace)
+        !n_rows_per_prob || !q || !sinks || !out || !codes || !sexp || !tail || !workspace || n_cache_rows <= 0)
+        return ds4hip_set_last_error(kEINVAL);
+    const ds4hip_decode_opts o = opts ? *opts : ds4hip_decode_opts{0, DS4HIP_DECODE_KERNEL_AUTO};
+    if ((o.exact_p != 0 && o.exact_p != 1) ||
+        (o.kernel != DS4HIP_DECODE_KERNEL_AUTO && o.kernel != DS4HIP_DECODE_KERNEL_REGLOAD))
         return ds4hip_set_last_error(kEINVAL);
     int page_shift = 0;
     if (page_table) {
-        if (page_rows <= 0 || (page_rows & (page_rows - 1))) return ds4hip_set_last_error(kEINVAL);
+        if (page_rows <= 0 || (page_rows & (page_rows - 1)) || page_table_stride <= 0)
+            return ds4hip_set_last_error(kEINVAL);
         while ((1 << page_shift) < page_rows) ++page_shift;
     }
     DecodeArgs A = {};
     for (int p = 0; p < n_prob; ++p) {
-        if (n_rows_per_prob[p] < 0) return ds4hip_set_last_error(kEINVAL);
-        A.count[p] = n_rows_per_prob[p];
+        const long long n = n_rows_per_prob[p];
+        if (n < 0) return ds4hip_set_last_error(kEINVAL);
+        // direct rows: every problem's rows inside the cache (with a device
+        // row_base array the kernels check the base; gathered rows are
+        // checked one by one on the device)
+        if (!row_idx && !page_table &&
+            (n > n_cache_rows || (!row_base && (row_base_stride < 0 || (long long)p * row_base_stride + n > n_cache_rows))))
+            return ds4hip_set_last_error(kEINVAL);
+        A.count[p] = n;
     }
+    A.n_cache_rows = n_cache_rows;
     const Plan pl = make_plan(n_rows_per_prob, n_prob, kFp8WgPerCu);
     for (int p = 0; p <= n_prob; ++p) A.start[p] = pl.start[p];
     if (workspace_bytes < pl.ws_bytes) return ds4hip_set_last_error(kEINVAL);
@@ -2403,14 +2453,14 @@ extern "C" int ds4hip_flash_attn_decode_fp8(
     carve(A, workspace, pl);
     if (!row_idx && !page_table) A.phys = nullptr;
     const hipStream_t st = (hipStream_t)stream;
-    const int rc = q_is_f32 ? launch<true, true>(A, pl, st, phases)
-                            : launch<true, false>(A, pl, st, phases);
+    const int rc = q_is_f32 ? launch<true, true>(A, pl, st, phases, o)
+                            : launch<true, false>(A, pl, st, phases, o);
     return ds4hip_set_last_error(rc);
 }
 
 // fp32 launchers of the reference (cuda/flash_attn.cuh:73,142). The split-K
-// partials live in a workspace: the caller's (the _prealloc forms), or a
-// stream-ordered hipMallocAsync / hipFreeAsync one.
+// partials live in a workspace: the caller's (the _prealloc forms), or the
+// library's per-stream scratch (see stream_scratch).
 namespace {
 Plan f32_plan(long long n_rows) { return make_plan(&n_rows, 1, 2, 0, false); }
 
@@ -2422,11 +2472,11 @@ int run_f32(const float *Q, const float *raw, const float *v_raw, int n_raw, con
     const Plan pl = plan ? *plan : f32_plan(A.count[0]);
     A.start[0] = pl.start[0];
     A.start[1] = pl.start[1];
-    bool own = false;
     if (!ws) {
-        hipError_t e = hipMallocAsync(&ws, pl.ws_bytes, st);
-        if (e != hipSuccess) return hip_status(e);
-        own = true;
+        // the reference-named launchers take no workspace: the library's
+        // per-stream scratch (allocates only when a call outgrows it)
+        const int e = stream_scratch(st, pl.ws_bytes, &ws);
+        if (e) return e;
     } else if (ws_bytes < pl.ws_bytes) {
         return kEINVAL;
     }
@@ -2442,12 +2492,7 @@ int run_f32(const float *Q, const float *raw, const float *v_raw, int n_raw, con
     A.n_prob = 1;
     A.total = A.start[1];
     carve(A, ws, pl);
-    int rc = launch<false, true>(A, pl, st);
-    if (own) {
-        const hipError_t e = hipFreeAsync(ws, st);
-        if (!rc) rc = hip_status(e);
-    }
-    return rc;
+    return launch<false, true>(A, pl, st);
 }
 
 bool raw_args_ok(const float *Q, const float *K, const float *V, const float *sinks,

@@ -689,14 +689,13 @@ extern "C" int ds4hip_scale_inplace_f32(float *y, int n, float scale, void *stre
 extern "C" size_t ds4hip_indexer_select_scratch_bytes(int n_comp) { return select_scratch_bytes(n_comp); }
 
 // The reference launchers take only a score scratch; the selection
-// histograms are stream-ordered allocations here.
+// histograms live in the library's per-stream scratch (no allocation once it
+// has grown to the size a stream needs).
 static int with_hists(int (*fn)(unsigned *, void *), void *ctx, int n_comp, hipStream_t st) {
     void *h = nullptr;
-    hipError_t e = hipMallocAsync(&h, select_scratch_bytes(n_comp), st);
-    if (e != hipSuccess) return hip_status(e);
-    int rc = fn(static_cast<unsigned *>(h), ctx);
-    e = hipFreeAsync(h, st);
-    return rc ? rc : hip_status(e);
+    const int e = stream_scratch(st, select_scratch_bytes(n_comp), &h);
+    if (e) return e;
+    return fn(static_cast<unsigned *>(h), ctx);
 }
 
 struct TopkCall {

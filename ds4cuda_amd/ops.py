@@ -158,6 +158,20 @@ def launch_flash_attn_decode_mixed_f32_prealloc(Q, raw_kv, comp_kv, comp_allowed
          _ptr(workspace), workspace.numel(), _stream(stream))
 
 
+class DecodeOpts(C.Structure):
+    """ds4hip_decode_opts: per-call P precision and kernel choice."""
+    _fields_ = [("exact_p", C.c_int), ("kernel", C.c_int)]
+
+
+_KERNELS = {"auto": 0, "regload": 1}
+
+
+def decode_opts(exact_p=False, kernel="auto"):
+    if kernel not in _KERNELS:
+        raise Ds4HipError(f"kernel must be one of {sorted(_KERNELS)}", -22)
+    return DecodeOpts(int(bool(exact_p)), _KERNELS[kernel])
+
+
 def decode_fp8_workspace_bytes(n_rows_per_prob) -> int:
     arr = (C.c_longlong * len(n_rows_per_prob))(*[int(x) for x in n_rows_per_prob])
     out = C.c_size_t(0)
@@ -168,13 +182,15 @@ def decode_fp8_workspace_bytes(n_rows_per_prob) -> int:
 
 def flash_attn_decode_fp8(q, sinks, out, cache: Fp8KVCache, n_rows_per_prob, *, row_base=None,
                           row_base_stride=0, row_idx=None, page_table=None, page_rows=256,
-                          workspace=None, phases=3, stream=None):
+                          workspace=None, phases=3, exact_p=False, kernel="auto", stream=None):
     """Decode attention of n_prob single-query problems over the FP8 cache.
 
     q [n_prob, 64, 512] bf16 or fp32; sinks [n_prob, 64] fp32; out
     [n_prob, 64, 512] fp32; n_rows_per_prob: host ints. Row r of problem p is
     position row_idx[p, r] (or r), mapped through page_table[p] (pages of
     page_rows rows) or offset by row_base[p] (int64 tensor) / p*row_base_stride.
+    exact_p: P as f16 hi + lo instead of one f16; kernel: "auto" or "regload"
+    (the register-load kernel for direct rows too).
     """
     n_prob = len(n_rows_per_prob)
     if q.dtype not in (torch.bfloat16, torch.float32):
@@ -196,7 +212,8 @@ def flash_attn_decode_fp8(q, sinks, out, cache: Fp8KVCache, n_rows_per_prob, *, 
          n_prob, _ptr(row_base), int(row_base_stride), _ptr(row_idx),
          row_idx.shape[-1] if row_idx is not None else 0, _ptr(page_table),
          page_table.shape[-1] if page_table is not None else 0, int(page_rows), N_HEAD,
-         HEAD_DIM, N_ROT, _ptr(workspace), workspace.numel(), int(phases), _stream(stream))
+         HEAD_DIM, N_ROT, C.c_longlong(cache.n_rows), C.byref(decode_opts(exact_p, kernel)),
+         _ptr(workspace), workspace.numel(), int(phases), _stream(stream))
     return workspace
 
 

@@ -18,6 +18,7 @@ from .ops import _check, _ptr, _stream
 
 N_LAYER = 43
 N_SWA = 128
+CHUNK_STAGING_ROWS = 128   # staging rows of a prefill chunk after the layers' rows
 ENOSPC = -28
 
 
@@ -157,6 +158,11 @@ class Session:
         if getattr(lib(), name)(*args) != 0:
             raise Ds4HipError(name, lib().ds4hip_get_last_error())
 
+    def rows_from(self, row):
+        """Arena rows from cache row `row` on: the layers' rows and the prefill
+        chunk's staging rows after them."""
+        return self.s.n_cache_rows + CHUNK_STAGING_ROWS - row
+
     def layer_rows(self, il, n_selected=-1):
         """(row_idx device address, n_rows, selected device address)."""
         ri, n, sel = C.c_void_p(), C.c_longlong(), C.c_void_p()
@@ -184,6 +190,6 @@ class Session:
              C.c_void_p(self.s.codes + rb * 448), C.c_void_p(self.s.sexp + rb * 8),
              C.c_void_p(self.s.tail + rb * 128), C.cast(counts, C.c_void_p), 1, None, 0,
              C.c_void_p(ri),
-             0, None, 0, 256, N_HEAD, HEAD_DIM, N_ROT, _ptr(workspace), workspace.numel(), 3,
-             _stream(stream))
+             0, None, 0, 256, N_HEAD, HEAD_DIM, N_ROT, C.c_longlong(self.rows_from(rb)), None,
+             _ptr(workspace), workspace.numel(), 3, _stream(stream))
         return workspace

@@ -28,12 +28,13 @@ extern "C" {
 
 /* ---- runtime ---------------------------------------------------------------- */
 
-/* Last non-zero status set by any entry point of this library (process-wide),
- * for the void-returning C++ shims. Reading it does not clear it. */
+/* Last non-zero status set by an entry point of this library on the calling
+ * host thread (thread-local, like hipGetLastError), for the void-returning
+ * C++ shims. Reading it does not clear it. */
 int ds4hip_get_last_error(void);
 int ds4hip_set_last_error(int code);
-/* Returns the last non-zero status and resets it to 0 (the analogue of
- * hipGetLastError for this library). */
+/* Returns the calling thread's last non-zero status and resets it to 0 (the
+ * analogue of hipGetLastError for this library). */
 int ds4hip_clear_last_error(void);
 /* Library version, (major << 16) | minor. */
 int ds4hip_version(void);
@@ -119,6 +120,23 @@ int ds4hip_flash_attn_decode_mixed_f32_noalloc(const float *Q, const float *raw_
 int ds4hip_flash_attn_decode_fp8_workspace_size(const long long *n_rows_per_prob, int n_prob,
                                                 size_t *bytes);
 
+/* Per-call options of ds4hip_flash_attn_decode_fp8 (no counterpart in the
+ * reference, whose scalar kernel keeps P in fp32, cuda/flash_attn.cu:70-85).
+ * NULL selects the defaults (all fields 0). Nothing is process-wide: calls
+ * with different options may run concurrently on different streams. */
+typedef struct ds4hip_decode_opts {
+    /* P . V precision of the bf16-Q decode: 0 (default) passes P as one f16
+     * (max-abs error ~1e-3 x RMS(out), a third fewer MFMAs); 1 as f16 hi + lo
+     * halves (~22 bits). The fp32-Q path always uses hi + lo. */
+    int exact_p;
+    /* DS4HIP_DECODE_KERNEL_AUTO (default): direct rows with one f16 P run the
+     * flat-stage kernel, everything else the register-load kernel;
+     * DS4HIP_DECODE_KERNEL_REGLOAD: the register-load kernel for direct rows too. */
+    int kernel;
+} ds4hip_decode_opts;
+#define DS4HIP_DECODE_KERNEL_AUTO 0
+#define DS4HIP_DECODE_KERNEL_REGLOAD 1
+
 /* Decode attention over the FP8 cache (additive: the FP8-cache form of
  * cuda/flash_attn.cuh:9-26,90-117, which take fp32 rows). Solves n_prob
  * independent single-query problems in one launch pair — layers of one token,
@@ -134,6 +152,12 @@ int ds4hip_flash_attn_decode_fp8_workspace_size(const long long *n_rows_per_prob
  *   page_table[p*page_table_stride + pos / page_rows] * page_rows + pos % page_rows
  * when page_table != NULL (page_rows a power of two), else
  *   (row_base ? row_base[p] : p*row_base_stride) + pos.
+ * n_cache_rows (> 0) is the number of rows codes / sexp / tail hold. Direct
+ * rows outside it are refused on the host (-22) where the host can see them
+ * (row_base NULL); rows the host cannot see (row_base, row_idx, page_table
+ * contents) are checked on the device: no row outside [0, n_cache_rows) is
+ * ever read, and every output of a problem that named one is NaN.
+ * opts: see ds4hip_decode_opts (NULL = defaults).
  * workspace must hold ds4hip_flash_attn_decode_fp8_workspace_size bytes.
  * phases: 3 runs both kernels; 1 launches only the split partial kernel and 2
  * only the merge, so a caller can place the merge next to its consumer (the
@@ -146,27 +170,8 @@ int ds4hip_flash_attn_decode_fp8(const void *q, int q_is_f32, long long q_stride
                                  long long row_base_stride, const int32_t *row_idx,
                                  long long row_idx_stride, const int32_t *page_table,
                                  int page_table_stride, int page_rows, int n_head, int head_dim,
-                                 int n_rot, void *workspace, size_t workspace_bytes,
-                                 int phases, void *stream);
-
-/* P . V precision of the bf16-Q FP8 decode (no counterpart in the reference,
- * whose scalar kernel keeps P in fp32, cuda/flash_attn.cu:70-85): exact = 1
- * passes P as f16 hi + lo halves (~22 bits), exact = 0 as one f16 (the
- * default; max-abs error stays ~1e-3 x RMS(out), a third fewer MFMAs). The
- * initial value comes from the environment variable DS4HIP_DECODE_EXACT_P.
- * Returns the previous setting, or -22 for another value. Process-wide; not
- * synchronized with launches in flight on other host threads. */
-int ds4hip_set_decode_exact_p(int exact);
-
-/* Form of the flat-stage decode kernel that serves direct rows with one f16 P
- * (no counterpart in the reference): lean = 1 folds the score scale into Q
- * before its FP8 split, takes the rows' E8M0 scales from one byte permute and
- * trims the producer's and the copies' per-tile instructions; 0 (the default)
- * keeps the checked form. Results agree to rounding. The initial value comes
- * from the environment variable DS4HIP_FLAT_LEAN. Returns the previous
- * setting, or -22 for another value. Process-wide, like
- * ds4hip_set_decode_exact_p. */
-int ds4hip_set_decode_flat_lean(int lean);
+                                 int n_rot, long long n_cache_rows, const ds4hip_decode_opts *opts,
+                                 void *workspace, size_t workspace_bytes, int phases, void *stream);
 
 /* ---- chunked prefill ------------------------------------------------------------- */
 

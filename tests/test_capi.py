@@ -68,14 +68,36 @@ def test_newer_entry_points_refuse_bad_arguments_on_the_host():
     assert l.ds4hip_session_chunk_rows(N, 0, 0, 1, N, N, N, 0, N, 0, N, N) == -22
     assert l.ds4hip_session_push_raw(N, 0, N, N) == -22
     assert l.ds4hip_session_state_describe(N, 16) == -22
-    for setter in (l.ds4hip_set_decode_flat_lean,
-                   l.ds4hip_set_decode_exact_p):
-        assert setter(5) == -22
     cnt = (C.c_longlong * 1)(10)
     # 32 heads: the decode serves 64
     assert l.ds4hip_flash_attn_decode_fp8(N, 0, C.c_longlong(0), N, C.c_longlong(0), N, C.c_longlong(0), N, N,
                                           N, cnt, 1, N, C.c_longlong(0), N, C.c_longlong(0), N, 0, 256, 32,
-                                          512, 64, N, C.c_size_t(0), 3, N) == -22
+                                          512, 64, C.c_longlong(100), N, N, C.c_size_t(0), 3, N) == -22
+    # the host-visible checks that come before any launch: stand-in pointers
+    # (never dereferenced) and a workspace size large enough
+    from ds4cuda_amd.ops import DecodeOpts
+    X = C.c_void_p(16)
+    ws_sz = C.c_size_t(1 << 30)
+
+    def dec(counts, n_cache_rows, opts=None, stride=0, row_idx=N, q=X):
+        c = (C.c_longlong * len(counts))(*counts)
+        return l.ds4hip_flash_attn_decode_fp8(q, 0, C.c_longlong(0), X, C.c_longlong(0), X, C.c_longlong(0), X,
+                                              X, X, c, len(counts), N, C.c_longlong(stride), row_idx,
+                                              C.c_longlong(0), N, 0, 256, 64, 512, 64, C.c_longlong(n_cache_rows),
+                                              None if opts is None else C.byref(opts), X, ws_sz, 3, N)
+    assert dec([10], 0) == -22                         # no cache size
+    assert dec([10], 9) == -22                         # direct rows past the cache
+    assert dec([10, 10], 19, stride=10) == -22         # problem 1's rows past the cache
+    assert dec([10], 100, DecodeOpts(2, 0)) == -22     # unknown P mode
+    assert dec([10], 100, DecodeOpts(0, 7)) == -22     # unknown kernel
+    assert dec([10], 100, row_idx=X, q=N) == -22       # (control: a null q is refused too)
     assert l.ds4hip_flash_attn_prefill_fp8(N, N, N, N, N, N, 4, 8, 64, 512, 64, N, C.c_size_t(0), N) == -22
     assert l.ds4hip_flash_attn_decode_mixed_f32_noalloc(N, N, N, N, N, N, 64, -1, 0, 512, N) == -22
     assert l.ds4hip_mul_mm_f32_f32(N, N, N, 16, 32, 1, N, C.c_size_t(0), N) == -22
+
+
+def test_bench_and_entry_points_compile():
+    """bench.py and __graft_entry__.py parse (the GPU box runs them unbuilt)."""
+    import py_compile
+    for f in ("bench.py", "__graft_entry__.py"):
+        py_compile.compile(str(ROOT / f), doraise=True)

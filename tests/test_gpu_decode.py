@@ -199,29 +199,24 @@ def test_fp8_p_precision_modes(gpu, n_kv):
     q = torch.from_numpy(bits.view(np.int16)).to(gpu).view(torch.bfloat16)
     ref = O.attn_decode_fp8(qf[0], codes, sexp, tail, np.arange(n_kv), sinks[0], n_threads=8)
     rms = np.sqrt(np.mean(ref.astype(np.float64) ** 2))
-    prev = _lib.lib().ds4hip_set_decode_exact_p(1)
-    try:
-        errs = {}
-        for exact in (1, 0):
-            _lib.lib().ds4hip_set_decode_exact_p(exact)
-            out = torch.zeros((1, 64, 512), dtype=torch.float32, device=gpu)
-            ops.flash_attn_decode_fp8(q, torch.from_numpy(sinks).to(gpu), out, cache, [n_kv])
-            torch.cuda.synchronize()
-            errs[exact] = np.abs(out[0].cpu().numpy().astype(np.float64) - ref).max() / rms
-        print(f"n_kv {n_kv}: max err / rms  hi+lo {errs[1]:.2e}  f16 {errs[0]:.2e}")
-    finally:
-        _lib.lib().ds4hip_set_decode_exact_p(prev)
+    errs = {}
+    for exact in (1, 0):
+        out = torch.zeros((1, 64, 512), dtype=torch.float32, device=gpu)
+        ops.flash_attn_decode_fp8(q, torch.from_numpy(sinks).to(gpu), out, cache, [n_kv], exact_p=bool(exact))
+        torch.cuda.synchronize()
+        errs[exact] = np.abs(out[0].cpu().numpy().astype(np.float64) - ref).max() / rms
+    print(f"n_kv {n_kv}: max err / rms  hi+lo {errs[1]:.2e}  f16 {errs[0]:.2e}")
     assert errs[1] <= TOL
     assert errs[0] <= TOL
-    assert _lib.lib().ds4hip_set_decode_exact_p(2) == -22
 
 
 @pytest.mark.parametrize("counts", [[1], [33], [1000], [300, 0, 64, 1025, 7], [32768]])
-def test_fp8_flat_lean_form(gpu, counts):
-    """The lean form (score scale folded into Q, packed row scales, SGPR-based
-    copies of whole tiles) against the oracle at the decode bar, and against
-    the default form: both round Q and P differently, so they agree to the
-    same bar, not bit for bit. Ragged counts exercise the clamped last tile."""
+def test_fp8_flat_and_regload_kernels(gpu, counts):
+    """The two bf16-Q kernels for direct rows (the flat-stage kernel, the
+    default, and the register-load kernel) against the oracle at the decode
+    bar, and against each other: they round Q differently, so they agree to
+    the same bar, not bit for bit. Ragged counts exercise the clamped last
+    tile of the flat kernel's whole-tile copies."""
     from ds4cuda_amd import _lib
     total = int(sum(counts))
     base = np.concatenate([[0], np.cumsum(counts)[:-1]])
@@ -232,17 +227,12 @@ def test_fp8_flat_lean_form(gpu, counts):
     q = torch.from_numpy(bits.view(np.int16)).to(gpu).view(torch.bfloat16)
     rb = torch.from_numpy(base.astype(np.int64)).to(gpu)
     outs = {}
-    prev = _lib.lib().ds4hip_set_decode_flat_lean(0)
-    try:
-        for lean in (0, 1):
-            assert _lib.lib().ds4hip_set_decode_flat_lean(lean) in (0, 1)
-            out = torch.zeros((n, 64, 512), dtype=torch.float32, device=gpu)
-            ops.flash_attn_decode_fp8(q, torch.from_numpy(sinks).to(gpu), out, cache, counts, row_base=rb)
-            torch.cuda.synchronize()
-            outs[lean] = out.cpu().numpy()
-    finally:
-        _lib.lib().ds4hip_set_decode_flat_lean(prev)
-    assert _lib.lib().ds4hip_set_decode_flat_lean(2) == -22
+    for lean, kern in ((1, "auto"), (0, "regload")):
+        out = torch.zeros((n, 64, 512), dtype=torch.float32, device=gpu)
+        ops.flash_attn_decode_fp8(q, torch.from_numpy(sinks).to(gpu), out, cache, counts, row_base=rb,
+                                  kernel=kern)
+        torch.cuda.synchronize()
+        outs[lean] = out.cpu().numpy()
     for p, c in enumerate(counts):
         if c == 0:
             continue
@@ -250,3 +240,53 @@ def test_fp8_flat_lean_form(gpu, counts):
         ref = O.attn_decode_fp8(qf[p], codes, sexp, tail, rows, sinks[p], n_threads=8)
         check(outs[1][p], ref)
         check(outs[1][p], outs[0][p])
+
+
+@pytest.mark.parametrize("q_f32,paged", [(False, False), (True, False), (False, True)])
+def test_fp8_gathered_rows_outside_the_cache(gpu, q_f32, paged):
+    """A row list (or page table) naming rows outside the cache: the kernels
+    read no such row, finish normally and write NaN for every output of that
+    problem; the other problems of the launch are unaffected. Paths: bf16 Q
+    with a row list (resolved in the partial kernel), fp32 Q with a row list
+    and bf16 Q with pages (both resolved by the phys pass)."""
+    n_rows = 1024
+    cache, (codes, sexp, tail) = make_cache(n_rows, 81, gpu)
+    n_prob, n_list = 3, 300
+    rng = np.random.default_rng(82)
+    lists = np.stack([np.sort(rng.choice(n_rows, n_list, replace=False)) for _ in range(n_prob)]).astype(np.int32)
+    bad = lists.copy()
+    page_rows = 256
+    if paged:
+        # identity pages over the 4 pages of the cache; problem 1's table names
+        # page 9 (rows 2304.., past the cache) for its positions 512..767, and
+        # problem 2 has a position past its page list
+        table = np.tile(np.arange(4, dtype=np.int32), (n_prob, 1))
+        table[1, 2] = 9
+        assert (bad[1] >= 512).any() and (bad[1] < 768).any()
+        bad[2, 5] = 4 * page_rows + 3
+    else:
+        bad[1, 7] = n_rows + 5
+        bad[2, 0] = -3
+    bits, qf = q_bf16(83, n_prob)
+    sinks = sinks_for(84, n_prob)
+    q = (torch.from_numpy(qf).to(gpu) if q_f32 else
+         torch.from_numpy(bits.view(np.int16)).to(gpu).view(torch.bfloat16))
+    out = torch.zeros((n_prob, 64, 512), dtype=torch.float32, device=gpu)
+    kw = dict(row_idx=torch.from_numpy(bad).to(gpu))
+    if paged:
+        kw.update(page_table=torch.from_numpy(table).to(gpu), page_rows=page_rows)
+    ops.flash_attn_decode_fp8(q, torch.from_numpy(sinks).to(gpu), out, cache, [n_list] * n_prob, **kw)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    check(got[0], O.attn_decode_fp8(qf[0], codes, sexp, tail, lists[0], sinks[0]))
+    assert np.isnan(got[1]).all()
+    assert np.isnan(got[2]).all()
+    # the same workspace and launch shape afterwards, all rows valid: no NaN left over
+    out2 = torch.zeros_like(out)
+    kw["row_idx"] = torch.from_numpy(lists).to(gpu)
+    if paged:
+        kw["page_table"] = torch.from_numpy(np.tile(np.arange(4, dtype=np.int32), (n_prob, 1))).to(gpu)
+    ops.flash_attn_decode_fp8(q, torch.from_numpy(sinks).to(gpu), out2, cache, [n_list] * n_prob, **kw)
+    torch.cuda.synchronize()
+    for p in range(n_prob):
+        check(out2[p].cpu().numpy(), O.attn_decode_fp8(qf[p], codes, sexp, tail, lists[p], sinks[p]))

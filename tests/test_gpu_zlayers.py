@@ -1,6 +1,6 @@
 """All 43 layers of the cfg 2 decode step (43 x 32768 FP8 rows, bf16 Q, one
 multi-problem launch): the default kernel against the register-load kernel
-with hi + lo P (ds4hip_set_decode_exact_p(1)), layer by layer, at the decode
+with hi + lo P (exact_p), layer by layer, at the decode
 bar, plus the middle layer against the CPU oracle. The full-size parity test
 checks only the first and last layer against the oracle; workgroup chunks
 that straddle the other 41 layer boundaries are covered here."""
@@ -26,16 +26,12 @@ def test_cfg2_all_layers_two_kernels(gpu):
     sinks_h = synth.normal(72, 1, n_layer * 64).reshape(n_layer, 64).astype(np.float32)
     sinks = torch.from_numpy(sinks_h).to(gpu)
     outs = []
-    prev = _lib.lib().ds4hip_set_decode_exact_p(0)
-    try:
-        for exact in (0, 1):
-            _lib.lib().ds4hip_set_decode_exact_p(exact)
-            out = torch.zeros((n_layer, 64, 512), dtype=torch.float32, device=gpu)
-            ops.flash_attn_decode_fp8(q, sinks, out, cache, [n_kv] * n_layer, row_base_stride=n_kv)
-            torch.cuda.synchronize()
-            outs.append(out.cpu().numpy().astype(np.float64))
-    finally:
-        _lib.lib().ds4hip_set_decode_exact_p(prev)
+    for exact in (0, 1):
+        out = torch.zeros((n_layer, 64, 512), dtype=torch.float32, device=gpu)
+        ops.flash_attn_decode_fp8(q, sinks, out, cache, [n_kv] * n_layer, row_base_stride=n_kv,
+                                  exact_p=bool(exact))
+        torch.cuda.synchronize()
+        outs.append(out.cpu().numpy().astype(np.float64))
     worst = 0.0
     for l in range(n_layer):
         ref = outs[1][l]

@@ -13,7 +13,6 @@ import torch
 import oracle as O
 import ds4cudak_file as F
 from ds4cuda_amd import session, synth
-from unverified import unverified
 
 pytestmark = pytest.mark.gpu
 

@@ -99,6 +99,67 @@ def test_q8_grouped_matvec_brute_force():
     assert np.abs(y - exact).max() < 0.05 * np.abs(exact).max()
 
 
+def test_q8_dense_matvec_brute_force():
+    """orc_q8_matvec (cuda/dense_q8.cu, Step 16) against an fp64 product of
+    the dequantized weights and activations built here from the block bytes:
+    rows are independent (row r reads only W row r), each block's f16 scale
+    multiplies its own 32 int8 values, the activation is quantized per 32."""
+    rng = np.random.default_rng(31)
+    n_rows, n_cols = 24, 512
+    w = rng.standard_normal((n_rows, n_cols)).astype(np.float32)
+    w[3, 64:96] = 0.0                       # an all-zero weight block (d = 0)
+    Wb, dw, qw = q8_pack(w)
+    x = rng.standard_normal(n_cols).astype(np.float32)
+    x[128:160] *= 1e-3                      # a block of small activations (own scale)
+    y = np.zeros(n_rows, np.float32)
+    O.lib().orc_q8_matvec(P(np.ascontiguousarray(Wb)), P(x), P(y), C.c_int(n_rows), C.c_int(n_cols))
+    # activation quantization restated (d = amax / 127 in fp32, rint(x / d))
+    xb = x.reshape(-1, 32)
+    xd = (np.abs(xb).max(axis=1) / np.float32(127.0)).astype(np.float32)
+    xq = np.clip(np.rint(xb * (np.float32(1.0) / xd)[:, None]), -128, 127)
+    # per block: f16(d_w) * d_x as an fp32 product, times the exact int32 dot
+    ref = np.zeros(n_rows)
+    for r in range(n_rows):
+        blk = Wb[r].reshape(-1, 34)
+        dwb = blk[:, :2].copy().view(np.float16).reshape(-1).astype(np.float32)
+        qwb = blk[:, 2:].view(np.int8).astype(np.int64)
+        dots = (qwb * xq.astype(np.int64)).sum(axis=1)
+        ref[r] = ((dwb * xd).astype(np.float64) * dots).sum()
+    assert np.max(np.abs(y - ref)) <= 1e-6 * np.abs(ref).max()
+    # a transposed or mis-scaled reading fails this: compare with the exact product
+    exact = w.astype(np.float64) @ x.astype(np.float64)
+    assert np.abs(y - exact).max() < 0.02 * np.abs(exact).max()
+    # one-hot activation: y = the dequantized weight column (up to the activation scale)
+    e = np.zeros(n_cols, np.float32)
+    e[77] = 1.0
+    O.lib().orc_q8_matvec(P(np.ascontiguousarray(Wb)), P(e), P(y), C.c_int(n_rows), C.c_int(n_cols))
+    # block 2 of x: d = 1/127, xq[77] = 127, every other block d = 0
+    dd = (dw[:, 2].astype(np.float32) * np.float32(1.0 / 127.0)).astype(np.float64)
+    col = qw.reshape(n_rows, -1)[:, 77].astype(np.float64) * 127 * dd
+    assert np.array_equal(y, col.astype(np.float32))
+
+
+def test_bf16_matvec_brute_force():
+    """orc_bf16_matvec (the cfg 5 attn_out checker) against an fp64 product of
+    the bf16 weights decoded by torch and against hand-made rows."""
+    import torch
+    rng = np.random.default_rng(32)
+    n_rows, n_cols = 16, 300
+    wf = rng.standard_normal((n_rows, n_cols)).astype(np.float32)
+    wb = torch.from_numpy(wf).to(torch.bfloat16)
+    bits = np.ascontiguousarray(wb.view(torch.int16).numpy().view(np.uint16))
+    x = rng.standard_normal(n_cols).astype(np.float32)
+    y = np.zeros(n_rows, np.float32)
+    O.lib().orc_bf16_matvec(P(bits), P(x), P(y), C.c_int(n_rows), C.c_int(n_cols))
+    ref = wb.to(torch.float64).numpy() @ x.astype(np.float64)
+    assert np.array_equal(y, ref.astype(np.float32))   # fp64 sum, one rounding
+    # row r = e_r (the identity) selects x[r]; a transposed W would not
+    eye = torch.eye(n_rows, n_cols, dtype=torch.bfloat16)
+    ib = np.ascontiguousarray(eye.view(torch.int16).numpy().view(np.uint16))
+    O.lib().orc_bf16_matvec(P(ib), P(x), P(y), C.c_int(n_rows), C.c_int(n_cols))
+    assert np.array_equal(y, x[:n_rows])
+
+
 def test_indexer_scores_and_selection():
     rng = np.random.default_rng(4)
     n_head, hd, n = 8, 128, 500

@@ -162,6 +162,9 @@ def bench_prefill(dev, stream, steps):
     ms = time_ms(lambda: ops.flash_attn_prefill_fp8(q, sinks, out, cache, n_q, n_cached,
                                                     workspace=ws, stream=stream),
                  steps, 2, stream)
+    ms_exact = time_ms(lambda: ops.flash_attn_prefill_fp8(q, sinks, out, cache, n_q, n_cached,
+                                                          workspace=ws, exact_p=True, stream=stream),
+                       steps, 2, stream)
     causal = 4 * N_HEAD * HEAD_DIM * sum(n_cached + i + 1 for i in range(n_q))
     full = 4 * N_HEAD * HEAD_DIM * n_q * (n_cached + n_q)
     tf = causal / (ms * 1e-3) / 1e12
@@ -170,7 +173,11 @@ def bench_prefill(dev, stream, steps):
             "ms": round(ms, 4), "tflops_causal": round(tf, 1),
             "tflops_nomask_credit": round(full / (ms * 1e-3) / 1e12, 1),
             "flops_causal": causal, "peak_tflops": MFMA_PEAK_TFLOPS,
-            "frac": round(tf / MFMA_PEAK_TFLOPS, 4)}
+            "frac": round(tf / MFMA_PEAK_TFLOPS, 4),
+            "p_precision": "one f16 P (default); hi + lo P figure under exact_p",
+            "exact_p": {"ms": round(ms_exact, 4),
+                        "tflops_causal": round(causal / (ms_exact * 1e-3) / 1e12, 1),
+                        "frac": round(causal / (ms_exact * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4)}}
 
 
 def bench_sparse(dev, stream, steps):
@@ -234,6 +241,53 @@ def batch_weights(dev, seed=70):
         "wn_i": (1.0 + n(8, (128,), 0.1)).contiguous(),
         "w_out": n(9, (4096, N_HEAD * HEAD_DIM), 0.02).to(torch.bfloat16).contiguous(),
     }
+
+
+def bench_token(dev, stream, steps, ctx=4096):
+    """The attention slice (Steps 11-16) of all 43 layers for one token at
+    context `ctx` over the FP8 session (ds4cuda_amd.token), model top-k 512:
+    eager launches from Python against one HIP graph of the whole token
+    (cuda/forward_token.cu:368-378 runs the layers one launch at a time)."""
+    import torch
+    from ds4cuda_amd import session, token
+    w = token.synthetic_weights(dev)
+    s = session.Session(ctx + 64)
+    try:
+        token.fill_history(s, ctx)
+        ts = token.TokenSlice(s, w, top_k=512)
+        g = torch.Generator(device=dev)
+        g.manual_seed(7)
+        x = [torch.randn(shape, generator=g, device=dev) for shape in ((43, 512), (43, 4096),
+                                                                      (43, 64, 512), (43, 1024))]
+        out = torch.empty((43, 4096), device=dev)
+        n_eager = max(3, steps // 10)
+        torch.cuda.synchronize()
+        ts.step(ctx, *x, out, stream=stream)          # warm
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(n_eager):
+            ts.step(ctx + 1 + i, *x, out, stream=stream)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        us_eager = e0.elapsed_time(e1) * 1e3 / n_eager
+        graph = ts.capture(ctx + 1 + n_eager, *x, out)
+        us_graph = time_ms(graph.replay, steps, 3, torch.cuda.current_stream()) * 1e3
+    finally:
+        s.close()
+    # weight bytes a token streams: the Q8_0 output projections (8192 x 4096 and
+    # 4096 x 8192, 34 B per 32) and the f16 compressor / indexer projections
+    q8 = 2 * 8192 * 4096 // 32 * 34
+    f16c = sum((2 * 2 * 512 * 4096 * 2 + 2 * 2 * 128 * 4096 * 2 + 8192 * 1024 * 2 + 64 * 4096 * 2)
+               if token.layer_ratio(il) == 4 else (2 * 512 * 4096 * 2 if token.layer_ratio(il) else 0)
+               for il in range(43))
+    b = 43 * q8 + f16c
+    return {"workload": f"attention slice (Steps 11-16) of all 43 layers for one token at context {ctx}, "
+                        "FP8 session, fp32 Q, indexer top-512, Q8_0 attn_out",
+            "us_per_token_graph": round(us_graph, 1), "us_per_token_eager": round(us_eager, 1),
+            "us_per_layer_graph": round(us_graph / 43, 2),
+            "weight_bytes": b, "gbs_graph": round(b / (us_graph * 1e-6) / 1e9, 1),
+            "frac": round(b / (us_graph * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
 def bench_batch(dev, stream, steps):
@@ -310,7 +364,7 @@ def main():
     ap.add_argument("--kernel", choices=("flat", "ws"), default=None,
                     help="decode kernel for direct rows: the flat-stage kernel (default) or the "
                          "register-load kernel")
-    ap.add_argument("--only", choices=("prefill", "sparse", "batch"),
+    ap.add_argument("--only", choices=("prefill", "sparse", "batch", "token"),
                     help="run one secondary config alone and print its figures as one JSON "
                          "line (for profiling it without the cfg 2 cache)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -343,7 +397,8 @@ def main():
         stream = torch.cuda.current_stream()
         fn = {"prefill": lambda: bench_prefill(dev, stream, max(3, args.steps // 10)),
               "sparse": lambda: bench_sparse(dev, stream, args.steps),
-              "batch": lambda: bench_batch(dev, stream, args.steps)}[args.only]
+              "batch": lambda: bench_batch(dev, stream, args.steps),
+              "token": lambda: bench_token(dev, stream, args.steps)}[args.only]
         log(f"secondary config {args.only} alone")
         print(json.dumps({"only": args.only, "figures": fn()}), flush=True)
         return
@@ -442,7 +497,8 @@ def main():
                 return {"error": f"{type(e).__name__}: {e}"}
         res["secondary"] = {"prefill": guarded(lambda: bench_prefill(dev, stream, max(3, args.steps // 10))),
                             "sparse_decode": guarded(lambda: bench_sparse(dev, stream, args.steps)),
-                            "batched_block": guarded(lambda: bench_batch(dev, stream, args.steps))}
+                            "batched_block": guarded(lambda: bench_batch(dev, stream, args.steps)),
+                            "token_slice": guarded(lambda: bench_token(dev, stream, args.steps))}
     if not args.no_cpu_baseline:
         log("timing the CPU baseline (oracle) on one layer")
         res["cpu_baseline"] = cpu_baseline()

@@ -42,6 +42,7 @@ constexpr int kMaxHeads = 64;
 constexpr int kMaxDim = 128;
 constexpr int kQStride = kMaxDim + 4;   // query row stride in LDS for the four-thread form
 constexpr int kBins = 2048;
+constexpr int kSmallSelect = 16384;   // candidates one workgroup selects in LDS (the batched select's limit)
 
 __device__ inline unsigned ord_key(float s) {
     unsigned u = __float_as_uint(s);
@@ -648,6 +649,15 @@ int score_select(const float *q, const float *w, const void *keys, int kind, int
     }
     const int recent = n_recent < top_k ? n_recent : top_k;
     const int n_cand = n_comp - recent;
+    // Few candidates and positions only (the model's decode: a few thousand
+    // compressed rows): the batched pair with one sequence, four lanes per
+    // key and one workgroup's LDS radix select, two launches instead of six;
+    // the same scores and the same selection rule.
+    if (!mask && head_dim == kMaxDim && n_cand <= kSmallSelect) {
+        const long long row0 = 0;
+        return ds4hip_indexer_topk_positions_batch(q, w, keys, kind, &row0, &n_comp, 1, n_head, head_dim, top_k,
+                                                   n_recent, scores, pos_out, top_k, st);
+    }
     const unsigned need0 = (unsigned)(top_k - recent);
     const int n_chunks = (n_comp + kChunk - 1) / kChunk;
     unsigned *hists = scratch;

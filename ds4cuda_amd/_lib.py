@@ -34,7 +34,7 @@ SIGNATURES: dict[str, list] = {
         _vp, _i, _ll, _vp, _ll, _vp, _ll, _vp, _vp, _vp, _vp, _i, _vp, _ll, _vp, _ll, _vp, _i,
         _i, _i, _i, _i, _ll, _vp, _vp, _sz, _i, _vp],
     "ds4hip_flash_attn_prefill_fp8_workspace_size": [_i],
-    "ds4hip_flash_attn_prefill_fp8": [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _sz,
+    "ds4hip_flash_attn_prefill_fp8": [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _sz, _i,
                                       _vp],
     "ds4hip_tail_rope_yarn_f32": [_vp, _vp, _i, _i, _i, _i, _i, _vp],
     "ds4hip_tail_rope_yarn_inverse_f32": [_vp, _vp, _i, _i, _i, _i, _i, _vp],

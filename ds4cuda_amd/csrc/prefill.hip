@@ -188,12 +188,13 @@ __device__ inline void load_q(const PrefillArgs &A, int qi, int w, int n16, int 
 // The P fragments are read one row tile ahead of their MFMAs, and a
 // scheduling barrier closes every row tile so the compiler cannot hoist all
 // reads to the front (which would need 64 more VGPRs than exist).
-// P passed as f16 hi + lo halves (kPrefillPLo) or as one f16 with l summing the
-// rounded P. One f16 measured 2.44 against 3.0 ms at cfg 4 but a max error of
-// 1.75e-3 x RMS against the 2e-3 bar (the hi + lo form: 3.1e-4), too thin a
-// margin to be the default.
+// kPLo: P passed as f16 hi + lo halves (~22 bits, twice the P . V MFMAs);
+// otherwise one f16 with l summing the rounded P, so O stays an exactly
+// normalized average whose weights are off by at most 2^-11 relative.
+// The fixup kernel (prefill_fp8_kernel) always carries hi + lo.
 constexpr bool kPrefillPLo = true;
 
+template <bool kPLo>
 __device__ inline void pv_step(const half8_t (*phi)[64], const half8_t (*plo)[64], int lane,
                                uint32_t a0, uint32_t a1, float4_t (*o)[8]) {
 #pragma unroll
@@ -205,19 +206,19 @@ __device__ inline void pv_step(const half8_t (*phi)[64], const half8_t (*plo)[64
             read_vt4<4>(a0, a1, vb);
         half8_t ph[2], pl[2];
         ph[0] = phi[0][lane];
-        if (kPrefillPLo) pl[0] = plo[0][lane];
+        if (kPLo) pl[0] = plo[0][lane];
 #pragma unroll
         for (int rt8 = 0; rt8 < 8; ++rt8) {
             if (rt8 < 7) {
                 ph[(rt8 + 1) & 1] = phi[rt8 + 1][lane];
-                if (kPrefillPLo) pl[(rt8 + 1) & 1] = plo[rt8 + 1][lane];
+                if (kPLo) pl[(rt8 + 1) & 1] = plo[rt8 + 1][lane];
             }
             // hi products of the 4 dim tiles, then lo: dependent MFMAs 4 apart
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 o[rt8][4 * half + i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
                     ph[rt8 & 1], vb[i], o[rt8][4 * half + i], 0, 0, 0);
-            if (kPrefillPLo) {
+            if (kPLo) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
                     o[rt8][4 * half + i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
@@ -372,7 +373,7 @@ __global__ __launch_bounds__(256) void prefill_fp8_kernel(const PrefillArgs A) {
                 }
             }
             // ---- O += P . V ----
-            pv_step(phi, plo, lane, lds_addr(st) + va[0], lds_addr(st) + va[1], o);
+            pv_step<kPrefillPLo>(phi, plo, lane, lds_addr(st) + va[0], lds_addr(st) + va[1], o);
         }
         if (kFix && slow) {
             // a row's reference max moved: finish tile t with O rows rescaled
@@ -384,7 +385,7 @@ __global__ __launch_bounds__(256) void prefill_fp8_kernel(const PrefillArgs A) {
                 for (int dt = 0; dt < 8; ++dt) o[rt8][dt] *= al;
             }
             const uint8_t *st = stages[t & 1];
-            pv_step(phi, plo, lane, lds_addr(st) + va[0], lds_addr(st) + va[1], o);
+            pv_step<kPrefillPLo>(phi, plo, lane, lds_addr(st) + va[0], lds_addr(st) + va[1], o);
             load_q(A, q_ok ? qi : 0, w, n16, g, qf);
             ++t;
         }
@@ -480,7 +481,7 @@ __device__ inline void qk_tile(const uint8_t *st, const uint32_t *ka, const half
 // Softmax of one tile with the reference max fixed (set on the first tile):
 // writes P hi/lo for the wave's two row tiles and accumulates l. A score more
 // than 2^kLazy above the reference marks the wave failed.
-template <bool kFirst>
+template <bool kFirst, bool kPLo>
 __device__ inline void softmax_fixed(const float4_t (*acc)[2], float kq_log2, int key0, int qpos,
                                      int g, float *m_use, float *l_part, bool &failed,
                                      half8_t *hi_out, half8_t *lo_out) {
@@ -512,9 +513,9 @@ __device__ inline void softmax_fixed(const float4_t (*acc)[2], float kq_log2, in
                 big |= x > kLazy;
                 const float p = s2[kt][r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(x);
                 const half_t h = (half_t)p;
-                lsum += kPrefillPLo ? p : (float)h;
+                lsum += kPLo ? p : (float)h;
                 hi[4 * kt + r] = h;
-                lo[4 * kt + r] = (half_t)(p - (float)h);
+                if (kPLo) lo[4 * kt + r] = (half_t)(p - (float)h);
             }
         l_part[rt] += lsum;
         failed |= big;
@@ -527,6 +528,7 @@ __device__ inline void softmax_fixed(const float4_t (*acc)[2], float kq_log2, in
 // Iteration t: [barrier] S(t) = K(t) Q^T | dequantize tile t+1 (fetched one
 // iteration earlier), fetch tile t+2 | softmax(t) | O += P(t-1) V(t-1). Three f16 stages (t-1 for V, t for K,
 // t+1 being written) and two P buffers make every LDS hazard one barrier apart.
+template <bool kPLo>
 __global__ __launch_bounds__(256) void prefill_fast_kernel(const PrefillArgs A) {
     __shared__ __attribute__((aligned(16))) uint8_t stages[3][kStageB];
     __shared__ __attribute__((aligned(16))) half8_t pb[2][2][8][64];   // [buf][hi,lo][row tile][lane]
@@ -577,11 +579,11 @@ __global__ __launch_bounds__(256) void prefill_fast_kernel(const PrefillArgs A) 
         store_tile(stages[1], tid, R);
         load_raw(A, 2, n_all, tid, R);
         half8_t hi[2], lo[2];
-        softmax_fixed<true>(acc, A.kq_log2, 0, qpos, g, m_use, l_part, failed, hi, lo);
+        softmax_fixed<true, kPLo>(acc, A.kq_log2, 0, qpos, g, m_use, l_part, failed, hi, lo);
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt) {
             pb[0][0][2 * w + rt][lane] = hi[rt];
-            pb[0][1][2 * w + rt][lane] = lo[rt];
+            if (kPLo) pb[0][1][2 * w + rt][lane] = lo[rt];
         }
     }
     int sp = 0, sc = 1, sn = 2;   // stages of tiles t-1, t, t+1
@@ -593,14 +595,14 @@ __global__ __launch_bounds__(256) void prefill_fast_kernel(const PrefillArgs A) 
         store_tile(stages[sn], tid, R);
         load_raw(A, t + 2, n_all, tid, R);
         half8_t hi[2], lo[2];
-        softmax_fixed<false>(acc, A.kq_log2, t * kTile, qpos, g, m_use, l_part, failed, hi, lo);
+        softmax_fixed<false, kPLo>(acc, A.kq_log2, t * kTile, qpos, g, m_use, l_part, failed, hi, lo);
         const int pbuf = (t - 1) & 1;
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt) {
             pb[pbuf ^ 1][0][2 * w + rt][lane] = hi[rt];
-            pb[pbuf ^ 1][1][2 * w + rt][lane] = lo[rt];
+            if (kPLo) pb[pbuf ^ 1][1][2 * w + rt][lane] = lo[rt];
         }
-        pv_step(pb[pbuf][0], pb[pbuf][1], lane, lds_addr(stages[sp]) + va[0],
+        pv_step<kPLo>(pb[pbuf][0], pb[pbuf][1], lane, lds_addr(stages[sp]) + va[0],
                 lds_addr(stages[sp]) + va[1], o);
         const int tmp = sp;
         sp = sc;
@@ -610,7 +612,7 @@ __global__ __launch_bounds__(256) void prefill_fast_kernel(const PrefillArgs A) 
     lds_barrier();
     {
         const int pbuf = (n_tiles - 1) & 1;
-        pv_step(pb[pbuf][0], pb[pbuf][1], lane, lds_addr(stages[sp]) + va[0],
+        pv_step<kPLo>(pb[pbuf][0], pb[pbuf][1], lane, lds_addr(stages[sp]) + va[0],
                 lds_addr(stages[sp]) + va[1], o);
     }
 
@@ -666,9 +668,10 @@ extern "C" int ds4hip_flash_attn_prefill_fp8(const void *q, const float *sinks, 
                                              const uint8_t *codes, const int8_t *sexp,
                                              const uint16_t *tail, int n_q, int n_cached,
                                              int n_head, int head_dim, int n_rot,
-                                             void *workspace, size_t workspace_bytes,
+                                             void *workspace, size_t workspace_bytes, int exact_p,
                                              void *stream) {
     if (n_head != kH || head_dim != kD || n_rot != kRot || n_q < 0 || n_cached < 0 ||
+        (exact_p != 0 && exact_p != 1) ||
         (n_q > 0 && (!q || !sinks || !out || !codes || !sexp || !tail || !workspace ||
                      workspace_bytes < ds4hip_flash_attn_prefill_fp8_workspace_size(n_q))))
         return ds4hip_set_last_error(kEINVAL);
@@ -688,7 +691,10 @@ extern "C" int ds4hip_flash_attn_prefill_fp8(const void *q, const float *sinks, 
     const hipStream_t st = (hipStream_t)stream;
     hipLaunchKernelGGL(zero_i32_kernel, dim3((n_pairs + 255) / 256), dim3(256), 0, st, A.fail,
                        n_pairs);
-    hipLaunchKernelGGL(prefill_fast_kernel, dim3(n_pairs), dim3(256), 0, st, A);
+    if (exact_p)
+        hipLaunchKernelGGL(prefill_fast_kernel<true>, dim3(n_pairs), dim3(256), 0, st, A);
+    else
+        hipLaunchKernelGGL(prefill_fast_kernel<false>, dim3(n_pairs), dim3(256), 0, st, A);
     hipLaunchKernelGGL(prefill_fp8_kernel<true>, dim3(n_pairs), dim3(256), 0, st, A);
     return ds4hip_set_last_error(hip_status(hipGetLastError()));
 }

@@ -218,10 +218,11 @@ def flash_attn_decode_fp8(q, sinks, out, cache: Fp8KVCache, n_rows_per_prob, *, 
 
 
 def flash_attn_prefill_fp8(q, sinks, out, cache: Fp8KVCache, n_q, n_cached, row0=0,
-                           workspace=None, stream=None):
+                           workspace=None, exact_p=False, stream=None):
     """Causal chunked prefill: q [n_q, 64, 512] bf16, out [n_q, 64, 512] fp32;
     the sequence's rows start at cache row row0 and the chunk's own rows
-    (n_cached .. n_cached + n_q - 1) are already appended."""
+    (n_cached .. n_cached + n_q - 1) are already appended. exact_p: P as f16
+    hi + lo in P . V (default: one f16)."""
     _check(q, torch.bfloat16, n_q * N_HEAD * HEAD_DIM, "q")
     _check(sinks, torch.float32, N_HEAD, "sinks")
     _check(out, torch.float32, n_q * N_HEAD * HEAD_DIM, "out")
@@ -236,7 +237,7 @@ def flash_attn_prefill_fp8(q, sinks, out, cache: Fp8KVCache, n_q, n_cached, row0
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
     call("ds4hip_flash_attn_prefill_fp8", _ptr(q), _ptr(sinks), _ptr(out), _ptr(c), _ptr(s),
          _ptr(t), n_q, n_cached, N_HEAD, HEAD_DIM, N_ROT, _ptr(workspace), workspace.numel(),
-         _stream(stream))
+         int(bool(exact_p)), _stream(stream))
     return workspace
 
 

@@ -185,12 +185,15 @@ int ds4hip_flash_attn_decode_fp8(const void *q, int q_is_f32, long long q_stride
  * codes/sexp/tail point at the sequence's row 0. workspace holds
  * ds4hip_flash_attn_prefill_fp8_workspace_size(n_q) bytes (one flag per query
  * pair: pairs whose softmax range outgrows the fast kernel are redone by a
- * second, rescaling kernel in the same call). */
+ * second, rescaling kernel in the same call). exact_p: 0 passes P to the P . V
+ * MFMAs as one f16 (l sums the rounded values, so each output stays an exactly
+ * normalized average), 1 as f16 hi + lo halves (~22 bits, twice the P . V
+ * MFMAs). Per call; nothing is process-wide. */
 size_t ds4hip_flash_attn_prefill_fp8_workspace_size(int n_q);
 int ds4hip_flash_attn_prefill_fp8(const void *q, const float *sinks, float *out,
                                   const uint8_t *codes, const int8_t *sexp, const uint16_t *tail,
                                   int n_q, int n_cached, int n_head, int head_dim, int n_rot,
-                                  void *workspace, size_t workspace_bytes, void *stream);
+                                  void *workspace, size_t workspace_bytes, int exact_p, void *stream);
 
 /* ---- tail RoPE YaRN --------------------------------------------------------------- */
 

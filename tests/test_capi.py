@@ -91,7 +91,8 @@ def test_newer_entry_points_refuse_bad_arguments_on_the_host():
     assert dec([10], 100, DecodeOpts(2, 0)) == -22     # unknown P mode
     assert dec([10], 100, DecodeOpts(0, 7)) == -22     # unknown kernel
     assert dec([10], 100, row_idx=X, q=N) == -22       # (control: a null q is refused too)
-    assert l.ds4hip_flash_attn_prefill_fp8(N, N, N, N, N, N, 4, 8, 64, 512, 64, N, C.c_size_t(0), N) == -22
+    assert l.ds4hip_flash_attn_prefill_fp8(N, N, N, N, N, N, 4, 8, 64, 512, 64, N, C.c_size_t(0), 0, N) == -22
+    assert l.ds4hip_flash_attn_prefill_fp8(N, N, N, N, N, N, 0, 8, 64, 512, 64, N, C.c_size_t(0), 2, N) == -22
     assert l.ds4hip_flash_attn_decode_mixed_f32_noalloc(N, N, N, N, N, N, 64, -1, 0, 512, N) == -22
     assert l.ds4hip_mul_mm_f32_f32(N, N, N, 16, 32, 1, N, C.c_size_t(0), N) == -22
 

@@ -26,6 +26,12 @@ constexpr float kRmsEps = 1.0e-6f;    // cuda/compressor.cu:54
 constexpr int kNRot = 64;             // cuda/compressor.cu:55
 constexpr int kMaxIn = 8192;
 
+// One wave per output row of the two projections (rows [0, width) of w_kv,
+// then [0, width) of w_gate), four per workgroup: eight 16-byte weight chunks
+// per lane are in flight before their fmas (wave_rows_dot), which keeps the
+// weight stream busy without fewer workgroups than CUs. Then the APE row and
+// the state row (cuda/compressor.cu:78-110).
+constexpr int kCpRows = 1;
 template <bool kW32>
 __global__ __launch_bounds__(256) void comp_project_kernel(
         const float *__restrict__ x, const void *__restrict__ w_kv, const void *__restrict__ w_gate,
@@ -36,43 +42,38 @@ __global__ __launch_bounds__(256) void comp_project_kernel(
     for (int i = threadIdx.x; i < in_dim; i += 256) xs[i] = x[i];
     __syncthreads();
     const int lane = threadIdx.x & 63;
-    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);   // [0, 2*width)
-    if (r >= 2 * width) return;
-    const bool gate = r >= width;
-    const int o = gate ? r - width : r;
-    float acc = 0.0f;
-    if (kW32) {
-        const float *wr = static_cast<const float *>(gate ? w_gate : w_kv) + (size_t)o * in_dim;
-        for (int i = lane * 4; i < in_dim; i += 256) {
-            const float4_t v = *reinterpret_cast<const float4_t *>(wr + i);
-            acc = fmaf(v[0], xs[i], acc);
-            acc = fmaf(v[1], xs[i + 1], acc);
-            acc = fmaf(v[2], xs[i + 2], acc);
-            acc = fmaf(v[3], xs[i + 3], acc);
-        }
-    } else {
-        const uint16_t *wr = static_cast<const uint16_t *>(gate ? w_gate : w_kv) + (size_t)o * in_dim;
-        for (int i = lane * 8; i < in_dim; i += 512) {
-            const uint4_t v = *reinterpret_cast<const uint4_t *>(wr + i);
+    const int r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * kCpRows;   // rows of [0, 2*width)
+    if (r0 >= 2 * width) return;
+    const void *rows[kCpRows];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                acc = fmaf(f16_bits_to_f32((uint16_t)(v[k] & 0xFFFF)), xs[i + 2 * k], acc);
-                acc = fmaf(f16_bits_to_f32((uint16_t)(v[k] >> 16)), xs[i + 2 * k + 1], acc);
-            }
-        }
+    for (int k = 0; k < kCpRows; ++k) {
+        const int r = min(r0 + k, 2 * width - 1);
+        const bool gate = r >= width;
+        const size_t o = (size_t)(gate ? r - width : r) * in_dim;
+        rows[k] = kW32 ? static_cast<const void *>(static_cast<const float *>(gate ? w_gate : w_kv) + o)
+                       : static_cast<const void *>(static_cast<const uint16_t *>(gate ? w_gate : w_kv) + o);
     }
+    float acc[kCpRows] = {0.0f};
+    wave_rows_dot<kCpRows, 8, kW32>(rows, xs, in_dim, lane, acc);
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
-    if (lane == 0) {
-        const int row = ratio == 4 ? ratio + pos_mod : pos_mod;   // cuda/compressor.cu:85
-        const size_t off = (size_t)row * width + o;
-        if (gate) {
-            const float s = acc + f16_bits_to_f32(w_ape[(size_t)pos_mod * width + o]);
-            state_score[off] = s;
-            if (sc_cur) sc_cur[o] = s;
-        } else {
-            state_kv[off] = acc;
-            if (kv_cur) kv_cur[o] = acc;
+    for (int k = 0; k < kCpRows; ++k) {
+        float a = acc[k];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) a += __shfl_xor(a, off);
+        const int r = r0 + k;
+        if (lane == 0 && r < 2 * width) {
+            const bool gate = r >= width;
+            const int o = gate ? r - width : r;
+            const int row = ratio == 4 ? ratio + pos_mod : pos_mod;   // cuda/compressor.cu:85
+            const size_t off = (size_t)row * width + o;
+            if (gate) {
+                const float s = a + f16_bits_to_f32(w_ape[(size_t)pos_mod * width + o]);
+                state_score[off] = s;
+                if (sc_cur) sc_cur[o] = s;
+            } else {
+                state_kv[off] = a;
+                if (kv_cur) kv_cur[o] = a;
+            }
         }
     }
 }
@@ -270,7 +271,7 @@ int comp_step(bool is_attn, const float *x, const void *w_kv, const void *w_gate
     const int width = coff * head_dim_out;
     const int pos_mod = pos % ratio;
     const bool emit = ((pos + 1) % ratio) == 0;
-    const dim3 grid((2 * width + 3) / 4);
+    const dim3 grid((2 * width + 4 * kCpRows - 1) / (4 * kCpRows));
     if (w32)
         hipLaunchKernelGGL(comp_project_kernel<true>, grid, dim3(256), 0, st, x, w_kv, w_gate,
                            w_ape, in_dim, width, ratio, pos_mod, state_kv, state_score, kv_cur, sc_cur);

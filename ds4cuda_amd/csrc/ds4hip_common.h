@@ -134,6 +134,52 @@ __device__ inline float f16_bits_to_f32(uint16_t b) {
 
 __host__ inline int hip_status(hipError_t e) { return e == hipSuccess ? 0 : kHipErrBase - (int)e; }
 
+
+// ---- wave-per-rows GEMV ---------------------------------------------------------
+// acc[r] += dot(row r of W, x) for kRows rows held by one wave, x staged in LDS.
+// Each lane reads 16-byte chunks (8 f16 or 4 fp32 weights) of every row at
+// chunk index lane + 64 j; kUnroll chunks of each of the kRows rows are
+// loaded before any is used, so a wave keeps kRows * kUnroll loads in flight
+// and every x value read from LDS serves all kRows rows. in_dim must be a
+// multiple of the chunk width. The per-lane sums are left to the caller's
+// reduction (lane order is fixed, so results are reproducible).
+template <int kRows, int kUnroll, bool kF32>
+__device__ inline void wave_rows_dot(const void *const (&rows)[kRows], const float *xs, int in_dim, int lane,
+                                     float (&acc)[kRows]) {
+    constexpr int kPer = kF32 ? 4 : 8;
+    const int n_chunks = in_dim / kPer;
+    for (int c0 = lane; c0 < n_chunks; c0 += 64 * kUnroll) {
+        uint4_t v[kRows][kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const int c = c0 + 64 * u;
+#pragma unroll
+            for (int r = 0; r < kRows; ++r)
+                v[r][u] = c < n_chunks ? reinterpret_cast<const uint4_t *>(rows[r])[c] : uint4_t{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const int c = c0 + 64 * u;
+            if (c >= n_chunks) break;
+            float xv[kPer];
+#pragma unroll
+            for (int e = 0; e < kPer; ++e) xv[e] = xs[c * kPer + e];
+#pragma unroll
+            for (int r = 0; r < kRows; ++r) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    if (kF32) {
+                        acc[r] = fmaf(__uint_as_float(v[r][u][k]), xv[k], acc[r]);
+                    } else {
+                        acc[r] = fmaf(f16_bits_to_f32((uint16_t)(v[r][u][k] & 0xFFFF)), xv[2 * k], acc[r]);
+                        acc[r] = fmaf(f16_bits_to_f32((uint16_t)(v[r][u][k] >> 16)), xv[2 * k + 1], acc[r]);
+                    }
+                }
+            }
+        }
+    }
+}
+
 }  // namespace ds4hip
 
 // Library-internal launchers shared between translation units (rope_matvec.hip).

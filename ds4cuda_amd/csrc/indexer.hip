@@ -42,6 +42,7 @@ constexpr int kMaxHeads = 64;
 constexpr int kMaxDim = 128;
 constexpr int kQStride = kMaxDim + 4;   // query row stride in LDS for the four-thread form
 constexpr int kBins = 2048;
+constexpr int kBatchKeys = 128;   // keys per workgroup of the four-lane scorer
 constexpr int kSmallSelect = 16384;   // candidates one workgroup selects in LDS (the batched select's limit)
 
 __device__ inline unsigned ord_key(float s) {
@@ -249,12 +250,12 @@ template <int kKind>
 __device__ __attribute__((always_inline)) inline void score_chain4x2(const float *qs, const float *ws,
                                                                      const void *__restrict__ keys,
                                                                      int c0, int c1, int n_head, int part,
+                                                                     float *pbuf, int kl0, int kl1,
                                                                      float &s0, float &s1) {
     float k0[32], k1[32];
     load_key32<kKind>(keys, c0, part, k0);
     load_key32<kKind>(keys, c1, part, k1);
     float carry0 = 0.0f, carry1 = 0.0f;
-    HeadTree<5> t0, t1;
     const int n_leaves = (n_head + 31) & ~31;
     for (int i = 0; i < n_leaves + 3; ++i) {
         const int leaf = i - part;
@@ -276,13 +277,33 @@ __device__ __attribute__((always_inline)) inline void score_chain4x2(const float
         // lane l takes lane l-1's chains (row_shr:1; part 0 ignores them)
         carry0 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(d0), 0x111, 0xF, 0xF, false));
         carry1 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(d1), 0x111, 0xF, 0xF, false));
+        // the head's product, in leaf order, for the tree below
         if (part == 3 && in) {
-            t0.push(leaf, act ? head_partial(d0, ws[h]) : 0.0f);
-            t1.push(leaf, act ? head_partial(d1, ws[h]) : 0.0f);
+            pbuf[leaf * kBatchKeys + kl0] = act ? head_partial(d0, ws[h]) : 0.0f;
+            pbuf[leaf * kBatchKeys + kl1] = act ? head_partial(d1, ws[h]) : 0.0f;
         }
     }
-    s0 = t0.result();
-    s1 = t1.result();
+    // In leaf order the butterfly of a warp of heads is a balanced tree of
+    // adjacent pairs; warp 0 then combines the two warp sums.
+    if (part == 3) {
+        float w[2][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}};
+        for (int wv = 0; wv < n_leaves / 32; ++wv) {
+#pragma unroll
+            for (int z = 0; z < 2; ++z) {
+                const int kl = z ? kl1 : kl0;
+                float v[32];
+#pragma unroll
+                for (int t = 0; t < 32; ++t) v[t] = pbuf[(32 * wv + t) * kBatchKeys + kl];
+#pragma unroll
+                for (int n = 16; n >= 1; n >>= 1)
+#pragma unroll
+                    for (int t = 0; t < n; ++t) v[t] = v[2 * t] + v[2 * t + 1];
+                w[z][wv] = v[0];
+            }
+        }
+        s0 = (w[0][0] + 0.0f) + (w[0][1] + 0.0f);
+        s1 = (w[1][0] + 0.0f) + (w[1][1] + 0.0f);
+    }
 }
 
 // Any head_dim <= 128: the key row is zero-padded to 128 in registers and
@@ -811,6 +832,7 @@ __global__ __launch_bounds__(256) void score_batch_kernel(const BatchArgs A) {
     const int c = ((int)blockIdx.x - first) * (kSplit == 1 ? 256 : 128) + (int)threadIdx.x / kSplit;
     __shared__ __attribute__((aligned(16))) float qs[kMaxHeads * kQStride];
     __shared__ float ws[kMaxHeads];
+    __shared__ float pbuf[kSplit == 1 ? 1 : kMaxHeads * kBatchKeys];   // [leaf][key of the block]
     const float *qg = A.q + (size_t)s * A.n_head * kMaxDim;
     const float *wg = A.w + (size_t)s * A.n_head;
     if (kSplit == 1)
@@ -827,11 +849,91 @@ __global__ __launch_bounds__(256) void score_batch_kernel(const BatchArgs A) {
         // keys c and c + 64 of this block's 128
         const int c1 = c + 64;
         float s0, s1;
+        const int kl = (int)threadIdx.x / kSplit;   // the group's first key within the block
         score_chain4x2<kKind>(qs, ws, A.keys, (int)(k0 + c), (int)(k0 + (c1 < n ? c1 : c)), A.n_head,
-                              (int)threadIdx.x % kSplit, s0, s1);
+                              (int)threadIdx.x % kSplit, pbuf, kl, kl + 64, s0, s1);
         if (threadIdx.x % kSplit == kSplit - 1) {
             A.scores[k0 + c] = s0;
             if (c1 < n) A.scores[k0 + c1] = s1;
+        }
+    }
+}
+
+// Lane-per-head scorer (the reference's own layout, cuda/indexer_allowed.cu:
+// 68-171: one thread per head): lane h of a wave holds q_h in registers, the
+// block's keys sit in LDS as fp32 and are read by broadcast, and a wave scores
+// kHeadsKpw keys, two dot chains at a time. The head sum is the reference's
+// tree literally: an xor butterfly over each 32-lane half (offsets 16 .. 1),
+// then lane 0's and lane 32's warp sums combined as warp 0 combines them.
+// Many keys per launch need few registers per key; this form suits a few
+// thousand keys, where one thread per key would leave most CUs idle.
+constexpr int kHeadsKpw = 8;                    // keys per wave
+constexpr int kHeadsKpb = 4 * kHeadsKpw;        // keys per workgroup
+constexpr long long kHeadsMaxKeys = 8192;       // up to this many keys per launch (measured crossover range)
+template <int kKind>
+__global__ __launch_bounds__(256) void score_heads_kernel(const BatchArgs A) {
+    int s = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxSeq; ++i)
+        if (i < A.n_seq && (int)blockIdx.x >= A.blk0[i]) s = i;
+    int n = 0, first = 0;
+    long long k0 = 0;
+#pragma unroll
+    for (int i = 0; i < kMaxSeq; ++i)
+        if (i == s) {
+            n = A.n_comp[i];
+            k0 = A.key0[i];
+            first = A.blk0[i];
+        }
+    const int c0 = ((int)blockIdx.x - first) * kHeadsKpb;
+    __shared__ __attribute__((aligned(16))) float qs[kMaxHeads * kQStride];
+    __shared__ __attribute__((aligned(16))) float ks[kHeadsKpb * kMaxDim];
+    const float *qg = A.q + (size_t)s * A.n_head * kMaxDim;
+    stage_query<kQStride>(qs, qg, A.n_head);
+    // the block's keys, widened to fp32 (rows past n are zeros, never stored)
+    for (int i = threadIdx.x; i < kHeadsKpb * kMaxDim; i += 256) {
+        const int kr = i / kMaxDim, d = i % kMaxDim;
+        ks[i] = c0 + kr < n ? key_elem<kKind>(A.keys, (size_t)(k0 + c0 + kr) * kMaxDim + d) : 0.0f;
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int h = lane;
+    const bool live = h < A.n_head;
+    float q[kMaxDim];
+#pragma unroll
+    for (int v = 0; v < kMaxDim / 4; ++v) {
+        const float4_t t = *reinterpret_cast<const float4_t *>(qs + (live ? h : 0) * kQStride + 4 * v);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) q[4 * v + e] = t[e];
+    }
+    const float wh = live ? A.w[(size_t)s * A.n_head + h] : 0.0f;
+#pragma unroll 1
+    for (int kk = wave * kHeadsKpw; kk < (wave + 1) * kHeadsKpw; kk += 2) {
+        if (c0 + kk >= n) break;
+        float dot[2] = {0.0f, 0.0f};
+#pragma unroll
+        for (int v = 0; v < kMaxDim / 4; ++v) {
+            float4_t kv[2];
+#pragma unroll
+            for (int z = 0; z < 2; ++z) kv[z] = *reinterpret_cast<const float4_t *>(ks + (kk + z) * kMaxDim + 4 * v);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int z = 0; z < 2; ++z) dot[z] = fmaf(q[4 * v + e], kv[z][e], dot[z]);
+        }
+#pragma unroll
+        for (int z = 0; z < 2; ++z) {
+            // idle heads (the reference's threads h >= n_head) add +0.0f
+            float v = __int_as_float(__float_as_int(head_partial(dot[z], wh)) & (live ? ~0 : 0));
+#pragma unroll
+            for (int off = 16; off > 0; off >>= 1) v = v + __shfl_xor(v, off);
+            const float w0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+            const float w1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+            // warp 0's 8-lane butterfly over (w0, w1, 0, ...): lanes of an
+            // absent warp hold +0.0f, which (w1 + 0) reproduces
+            const float score = (w0 + 0.0f) + (w1 + 0.0f);
+            const int c = c0 + kk + z;
+            if (lane == 0 && c < n) A.scores[k0 + c] = score;
         }
     }
 }
@@ -961,9 +1063,14 @@ extern "C" int ds4hip_indexer_topk_positions_batch(
     A.top_k = top_k;
     A.n_recent = n_recent;
     A.pos_stride = pos_stride;
-    // four threads per key, two keys per thread group (128 keys per block)
-    const bool split = true;   // the chained four-thread form works for any n_head
-    const int keys_per_blk = split ? 128 : 256;
+    // Few keys in all: one wave per kHeadsKpw keys, lane = head
+    // (score_heads_kernel), which fills the chip where one group of lanes per
+    // key would not. Many keys: four chained lanes per key (score_batch_kernel).
+    long long n_scored = 0;
+    for (int s = 0; s < n_seq; ++s)
+        if (n_comp_host[s] > top_k) n_scored += n_comp_host[s];
+    const bool heads = n_scored <= kHeadsMaxKeys;
+    const int keys_per_blk = heads ? kHeadsKpb : 128;
     int blk = 0;
     for (int s = 0; s < kMaxSeq; ++s) {
         const int n = s < n_seq ? n_comp_host[s] : 0;
@@ -981,16 +1088,16 @@ extern "C" int ds4hip_indexer_topk_positions_batch(
         const dim3 g(blk), b(256);
         switch (key_kind) {
         case 0:
-            if (split) hipLaunchKernelGGL((score_batch_kernel<0, 4>), g, b, 0, st, A);
-            else hipLaunchKernelGGL((score_batch_kernel<0, 1>), g, b, 0, st, A);
+            if (heads) hipLaunchKernelGGL(score_heads_kernel<0>, g, b, 0, st, A);
+            else hipLaunchKernelGGL((score_batch_kernel<0, 4>), g, b, 0, st, A);
             break;
         case 1:
-            if (split) hipLaunchKernelGGL((score_batch_kernel<1, 4>), g, b, 0, st, A);
-            else hipLaunchKernelGGL((score_batch_kernel<1, 1>), g, b, 0, st, A);
+            if (heads) hipLaunchKernelGGL(score_heads_kernel<1>, g, b, 0, st, A);
+            else hipLaunchKernelGGL((score_batch_kernel<1, 4>), g, b, 0, st, A);
             break;
         default:
-            if (split) hipLaunchKernelGGL((score_batch_kernel<2, 4>), g, b, 0, st, A);
-            else hipLaunchKernelGGL((score_batch_kernel<2, 1>), g, b, 0, st, A);
+            if (heads) hipLaunchKernelGGL(score_heads_kernel<2>, g, b, 0, st, A);
+            else hipLaunchKernelGGL((score_batch_kernel<2, 4>), g, b, 0, st, A);
             break;
         }
     }

@@ -135,6 +135,11 @@ __device__ inline float wave_sum(float v) {
 // 256 threads = 4 waves, 2 rows per wave; x staged in LDS as fp32.
 constexpr int kMvMaxIn = 16384;
 
+// One wave per 4 rows (16 rows per workgroup): every weight chunk of the four
+// rows is loaded before the fmas that use it, and each x value read from LDS
+// serves the four rows (wave_rows_dot). Lane-strided fp32 partial sums, then
+// the wave's butterfly, as cuda/router.cu:69-97 reduces a warp's lanes.
+constexpr int kMvRows = 4;
 __global__ __launch_bounds__(256) void mv_f16_kernel(const uint16_t *__restrict__ w,
                                                      const float *__restrict__ x,
                                                      float *__restrict__ y, int out_dim,
@@ -144,25 +149,25 @@ __global__ __launch_bounds__(256) void mv_f16_kernel(const uint16_t *__restrict_
     __syncthreads();
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    for (int rr = 0; rr < 2; ++rr) {
-        const int row = (blockIdx.x * 4 + wave) * 2 + rr;
-        if (row >= out_dim) return;
-        const uint16_t *wr = w + (size_t)row * in_dim;
-        float acc = 0.0f;
-        if ((in_dim & 7) == 0) {
-            for (int i = lane * 8; i < in_dim; i += 512) {
-                const uint4_t v = *reinterpret_cast<const uint4_t *>(wr + i);
+    const int row0 = (blockIdx.x * 4 + wave) * kMvRows;
+    if (row0 >= out_dim) return;
+    float acc[kMvRows] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if ((in_dim & 7) == 0) {
+        const void *rows[kMvRows];
 #pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    acc = fmaf(f16_bits_to_f32((uint16_t)(v[k] & 0xFFFF)), xs[i + 2 * k], acc);
-                    acc = fmaf(f16_bits_to_f32((uint16_t)(v[k] >> 16)), xs[i + 2 * k + 1], acc);
-                }
-            }
-        } else {
-            for (int i = lane; i < in_dim; i += 64) acc = fmaf(f16_bits_to_f32(wr[i]), xs[i], acc);
+        for (int r = 0; r < kMvRows; ++r) rows[r] = w + (size_t)min(row0 + r, out_dim - 1) * in_dim;
+        wave_rows_dot<kMvRows, 2, false>(rows, xs, in_dim, lane, acc);
+    } else {
+#pragma unroll
+        for (int r = 0; r < kMvRows; ++r) {
+            const uint16_t *wr = w + (size_t)min(row0 + r, out_dim - 1) * in_dim;
+            for (int i = lane; i < in_dim; i += 64) acc[r] = fmaf(f16_bits_to_f32(wr[i]), xs[i], acc[r]);
         }
-        acc = wave_sum(acc);
-        if (lane == 0) y[row] = acc;
+    }
+#pragma unroll
+    for (int r = 0; r < kMvRows; ++r) {
+        const float a = wave_sum(acc[r]);
+        if (lane == 0 && row0 + r < out_dim) y[row0 + r] = a;
     }
 }
 
@@ -197,6 +202,20 @@ __device__ inline int dot4(int a, int b, int c) {
     return __builtin_amdgcn_sdot4(a, b, c, false);
 }
 
+// One wave per row. With an even block count (rows of n_blocks * 34 bytes stay
+// 4-byte aligned) a lane takes a pair of blocks, 68 bytes = 17 dwords, with
+// dword loads (two pairs per lane in flight): the f16 scale and the int8
+// values of the even block start at bytes 0 and 2 of the pair, those of the odd
+// block at bytes 66 and 34. Otherwise a lane reads one block as 17 halfwords.
+// Per block: the exact int32 dot of the int8 values, scaled by d_w * d_x in
+// fp32 (cuda/attn_out.cu:171-197).
+__device__ inline float q8_block_term(float dw, float dx, const uint32_t *q, const int *xb) {
+    int isum = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) isum = dot4((int)q[k], xb[k], isum);
+    return dw * dx * (float)isum;
+}
+
 __global__ __launch_bounds__(256) void mv_q8_kernel(const uint8_t *__restrict__ W,
                                                     const int8_t *__restrict__ xq,
                                                     const float *__restrict__ xscale,
@@ -211,17 +230,43 @@ __global__ __launch_bounds__(256) void mv_q8_kernel(const uint8_t *__restrict__ 
     const float *sg = xscale + (size_t)g * n_blocks;
     const uint8_t *wr = W + (size_t)row * n_blocks * 34;
     float acc = 0.0f;
-    for (int b = lane; b < n_blocks; b += 64) {
-        const uint16_t *blk = reinterpret_cast<const uint16_t *>(wr + (size_t)b * 34);
-        const float dw = f16_bits_to_f32(blk[0]);
-        int isum = 0;
-        const int *xb = reinterpret_cast<const int *>(xg + (size_t)b * 32);
+    if ((n_blocks & 1) == 0 && (reinterpret_cast<uintptr_t>(W) & 3) == 0) {
+        const int n_pairs = n_blocks / 2;
+        const uint32_t *wp = reinterpret_cast<const uint32_t *>(wr);
+        for (int p0 = lane; p0 < n_pairs; p0 += 128) {
+            uint32_t d[2][17];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const uint32_t wv = (uint32_t)blk[1 + 2 * k] | ((uint32_t)blk[2 + 2 * k] << 16);
-            isum = dot4((int)wv, xb[k], isum);
+            for (int u = 0; u < 2; ++u) {
+                const int p = min(p0 + 64 * u, n_pairs - 1);
+#pragma unroll
+                for (int k = 0; k < 17; ++k) d[u][k] = wp[(size_t)p * 17 + k];
+            }
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int p = p0 + 64 * u;
+                if (p >= n_pairs) break;
+                const int b = 2 * p;
+                uint32_t qe[8], qo[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    qe[k] = __builtin_amdgcn_alignbyte(d[u][k + 1], d[u][k], 2);   // bytes 2 + 4k ..
+                    qo[k] = d[u][k + 9];
+                }
+                const float dwe = f16_bits_to_f32((uint16_t)(d[u][0] & 0xFFFF));
+                const float dwo = f16_bits_to_f32((uint16_t)(d[u][8] >> 16));
+                acc += q8_block_term(dwe, sg[b], qe, reinterpret_cast<const int *>(xg + (size_t)b * 32));
+                acc += q8_block_term(dwo, sg[b + 1], qo, reinterpret_cast<const int *>(xg + (size_t)(b + 1) * 32));
+            }
         }
-        acc = fmaf(dw * sg[b], (float)isum, acc);
+    } else {
+        for (int b = lane; b < n_blocks; b += 64) {
+            const uint16_t *blk = reinterpret_cast<const uint16_t *>(wr + (size_t)b * 34);
+            const float dw = f16_bits_to_f32(blk[0]);
+            uint32_t q[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) q[k] = (uint32_t)blk[1 + 2 * k] | ((uint32_t)blk[2 + 2 * k] << 16);
+            acc += q8_block_term(dw, sg[b], q, reinterpret_cast<const int *>(xg + (size_t)b * 32));
+        }
     }
     acc = wave_sum(acc);
     if (lane == 0) y[row] = acc;
@@ -617,7 +662,8 @@ extern "C" int ds4hip_mul_mv_f16_f32(const uint16_t *w_f16, const float *x_f32, 
     if (!w_f16 || !x_f32 || !y_f32 || out_dim < 0 || in_dim <= 0 || in_dim > kMvMaxIn)
         return ds4hip_set_last_error(kEINVAL);
     if (out_dim == 0) return 0;
-    hipLaunchKernelGGL(mv_f16_kernel, dim3((out_dim + 7) / 8), dim3(256), in_dim * sizeof(float),
+    hipLaunchKernelGGL(mv_f16_kernel, dim3((out_dim + 4 * kMvRows - 1) / (4 * kMvRows)), dim3(256),
+                       in_dim * sizeof(float),
                        (hipStream_t)stream, w_f16, x_f32, y_f32, out_dim, in_dim);
     return ds4hip_set_last_error(hip_status(hipGetLastError()));
 }

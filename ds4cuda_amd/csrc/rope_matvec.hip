@@ -687,16 +687,17 @@ extern "C" int ds4hip_mul_mv_q8_0_q8_0_grouped_f32(const void *W, const float *x
     if (!W || !x || !y || n_groups <= 0 || rank <= 0 || group_dim <= 0 || group_dim % 32)
         return ds4hip_set_last_error(kEINVAL);
     const hipStream_t st = (hipStream_t)stream;
+    // the int8 activations and their scales live in the library's per-stream
+    // scratch: the reference's launcher of this name allocates nothing per call
     const size_t n = (size_t)n_groups * group_dim;
-    void *xq = nullptr, *xs = nullptr;
-    hipError_t e = hipMallocAsync(&xq, n, st);
-    if (e == hipSuccess) e = hipMallocAsync(&xs, n / 32 * sizeof(float), st);
-    if (e != hipSuccess) return ds4hip_set_last_error(hip_status(e));
-    int rc = launch_q8(static_cast<const uint8_t *>(W), x, y, n_groups, group_dim, rank,
-                       static_cast<int8_t *>(xq), static_cast<float *>(xs), true, st);
-    const hipError_t e1 = hipFreeAsync(xq, st), e2 = hipFreeAsync(xs, st);
-    if (!rc) rc = hip_status(e1 != hipSuccess ? e1 : e2);
-    return ds4hip_set_last_error(rc);
+    const size_t xs_off = (n + 255) & ~(size_t)255;
+    void *buf = nullptr;
+    const int e = stream_scratch(st, xs_off + n / 32 * sizeof(float), &buf);
+    if (e) return ds4hip_set_last_error(e);
+    int8_t *xq = static_cast<int8_t *>(buf);
+    float *xs = reinterpret_cast<float *>(static_cast<char *>(buf) + xs_off);
+    return ds4hip_set_last_error(launch_q8(static_cast<const uint8_t *>(W), x, y, n_groups,
+                                           group_dim, rank, xq, xs, true, st));
 }
 
 extern "C" int ds4hip_mul_mv_q8_0_q8_0_f32_prealloc(const void *W, const float *x, float *y,

@@ -166,9 +166,7 @@ def test_fp8_cfg2_scale_long_chunks(gpu):
     # ~170 tiles, so the softmax reference max is set long before the chunk's
     # largest score; two layers are checked against the oracle
     n_layer, n_kv = 43, 32768
-    x = torch.randn(n_layer * n_kv, 512, device=gpu, generator=torch.Generator(gpu).manual_seed(5))
-    pick = torch.rand(n_layer * n_kv, device=gpu, generator=torch.Generator(gpu).manual_seed(6)) < 0.01
-    x[pick] *= 8
+    x = synth.kv_rows_device(5, 0, n_layer * n_kv, gpu, outlier_frac=0.01)
     cache = ops.Fp8KVCache.empty(n_layer * n_kv, device=gpu)
     cache.append(x)
     bits, qf = q_bf16(41, n_layer)

@@ -40,22 +40,32 @@ def _compile(src: Path) -> Path:
 
 
 # Kernels whose copy ring counts outstanding vector-memory operations: a
-# register spill (scratch store) would break that count, so the build refuses it.
+# register spill (scratch access) inside the ring would break that count, so
+# the build refuses any scratch access that a path can reach while a copy is
+# outstanding (ds4cuda_amd/spill_check.py); spills outside the ring (before the
+# first copy, after a vmcnt(0)) are allowed.
 NO_SPILL_KERNELS = ("decode_fp8_kernelILb0E", "decode_flat_kernel")
 
 
 def check_spills(src: Path) -> None:
-    cmd = [HIPCC, *FLAGS, "-I", str(ROOT / "include"), "--cuda-device-only", "-c", str(src),
-           "-o", os.devnull, "-Rpass-analysis=kernel-resource-usage"]
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    name = None
-    for line in r.stderr.splitlines():
-        if "Function Name:" in line:
-            name = line.split("Function Name:")[1].split("[")[0].strip()
-        elif "VGPRs Spill:" in line and name and any(k in name for k in NO_SPILL_KERNELS):
-            n = int(line.split("VGPRs Spill:")[1].split("[")[0])
-            if n:
-                raise RuntimeError(f"{name} spills {n} VGPRs; its copy-ring waits require none")
+    import re
+    import tempfile
+    from .spill_check import ring_violations
+    with tempfile.TemporaryDirectory() as td:
+        out = Path(td) / "k.s"
+        cmd = [HIPCC, *FLAGS, "-I", str(ROOT / "include"), "--cuda-device-only", "-S", str(src),
+               "-o", str(out)]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"hipcc -S failed for {src.name}:\n{r.stderr}")
+        asm = out.read_text()
+    syms = sorted(set(re.findall(r"^(_Z\w+):", asm, re.M)))
+    for sym in syms:
+        if any(k in sym for k in NO_SPILL_KERNELS):
+            bad = ring_violations(asm, sym)
+            if bad:
+                raise RuntimeError(f"{sym}: {len(bad)} scratch accesses while ring copies may be "
+                                   f"outstanding (first: {bad[0]}); its copy-ring waits require none")
 
 
 def build_lib(verbose: bool = False) -> Path:

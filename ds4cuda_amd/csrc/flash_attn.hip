@@ -1635,9 +1635,14 @@ __device__ inline float xmax_16_32_raw(float v) {
 // copies from an SGPR base). The score scale log2(e)/sqrt(d) stays on S after
 // the MFMA: folded into Q it would make the bf16 values inexact in the two
 // E4M3 parts (a bf16 value's 8 significant bits split exactly into hi + lo).
-template <bool kPLo, bool kLean>
+template <bool kPLo, bool kLean, bool kQf32 = false>
 __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A) {
     static_assert(!kPLo, "the flat kernel passes P as one f16");
+    static_assert(kLean || !kQf32, "fp32 Q takes the lean form");
+    // Q parts on the scaled FP8 MFMA: a bf16 Q (8 significant bits) fits in
+    // two E4M3 parts; an fp32 Q takes three (about 12 bits: the score error of
+    // the dropped rest is ~2^-12 of |q| |k|)
+    constexpr int kParts = kQf32 ? 3 : 2;
     __shared__ __attribute__((aligned(16))) uint8_t stage[kFsStages][kFsSlot];
     __shared__ __attribute__((aligned(16))) uint8_t pws[2 * 4 * 64 * 16];   // [t & 1][head tile][lane] f16 x 8
     __shared__ __attribute__((aligned(16))) float alpha_s[2][kH];
@@ -1645,6 +1650,10 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
     __shared__ long long s_start[kMaxProb + 1];
     __shared__ long long s_rowbase[kMaxProb];
     __shared__ int s_badp[kMaxProb];
+    // kQf32: each producer lane's f16 hi + lo tail fragments of Q, read back
+    // per row half (held in registers they would push the producers past 256
+    // VGPRs): [wave][hi s0, hi s1, lo s0, lo s1][lane]
+    __shared__ __attribute__((aligned(16))) half8_t q_tail_s[kQf32 ? 4 * 4 * 64 : 1];
     stage_rowbase(A, s_rowbase, s_badp);
     stage_start(A, s_start);
 
@@ -1678,13 +1687,15 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
             // lo, each E4M3 codes with one E8M0 scale per head and k-step (a bf16
             // value has 8 significant bits: hi keeps 4, lo the rest). Dims >= 448
             // (the f16 RoPE tail) are zero here and take the f16 MFMA instead:
-            // qt[s] = dims 448 + 32 s + 8 q + [0, 8).
-            uint32_t qf8[4][2][8];
-            int qsc[2] = {0, 0};   // [part]: byte ks = E8M0 scale of k-step ks (the MFMA's op_sel picks it)
-            half8_t qt[2];
+            // qt[s] = dims 448 + 32 s + 8 q + [0, 8) (an fp32 Q: f16 hi qt + lo qtl;
+            // one f16 rounding there would dominate the error of the three parts).
+            uint32_t qf8[4][kParts][8];
+            int qsc[kParts] = {};   // [part]: byte ks = E8M0 scale of k-step ks (the MFMA's op_sel picks it)
+            half8_t qt[2], qtl[2];
             {
-                const uint16_t *qsrc = static_cast<const uint16_t *>(A.q) + (long long)p * A.q_stride +
-                                       (long long)(16 * d + j) * kD;
+                const long long qoff = (long long)p * A.q_stride + (long long)(16 * d + j) * kD;
+                const uint16_t *qsrc = static_cast<const uint16_t *>(A.q) + qoff;
+                const float *qsrc32 = static_cast<const float *>(A.q) + qoff;
 #pragma unroll
                 for (int ks = 0; ks < 4; ++ks) {
                     float x[32];
@@ -1693,17 +1704,31 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
                         const bool live = ks < 3 || hv == 0;
 #pragma unroll
                         for (int v = 0; v < 2; ++v) {
-                            uint4_t w = uint4_t{0, 0, 0, 0};
-                            if (live) w = *reinterpret_cast<const uint4_t *>(qsrc + 128 * ks + 64 * hv + 16 * q + 8 * v);
+                            const int off = 128 * ks + 64 * hv + 16 * q + 8 * v;
+                            if constexpr (kQf32) {
+                                float4_t a = float4_t{0, 0, 0, 0}, b = a;
+                                if (live) {
+                                    a = *reinterpret_cast<const float4_t *>(qsrc32 + off);
+                                    b = *reinterpret_cast<const float4_t *>(qsrc32 + off + 4);
+                                }
 #pragma unroll
-                            for (int i = 0; i < 4; ++i) {
-                                x[16 * hv + 8 * v + 2 * i] = bf16_to_f32((uint16_t)(w[i] & 0xFFFF));
-                                x[16 * hv + 8 * v + 2 * i + 1] = bf16_to_f32((uint16_t)(w[i] >> 16));
+                                for (int i = 0; i < 4; ++i) {
+                                    x[16 * hv + 8 * v + i] = a[i];
+                                    x[16 * hv + 8 * v + 4 + i] = b[i];
+                                }
+                            } else {
+                                uint4_t w = uint4_t{0, 0, 0, 0};
+                                if (live) w = *reinterpret_cast<const uint4_t *>(qsrc + off);
+#pragma unroll
+                                for (int i = 0; i < 4; ++i) {
+                                    x[16 * hv + 8 * v + 2 * i] = bf16_to_f32((uint16_t)(w[i] & 0xFFFF));
+                                    x[16 * hv + 8 * v + 2 * i + 1] = bf16_to_f32((uint16_t)(w[i] >> 16));
+                                }
                             }
                         }
                     }
 #pragma unroll
-                    for (int part = 0; part < 2; ++part) {
+                    for (int part = 0; part < kParts; ++part) {
                         float amax = 0.0f;
 #pragma unroll
                         for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(x[i]));
@@ -1721,7 +1746,7 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
                             pk = __builtin_amdgcn_cvt_pk_fp8_f32(x[4 * w] * inv, x[4 * w + 1] * inv, pk, false);
                             pk = __builtin_amdgcn_cvt_pk_fp8_f32(x[4 * w + 2] * inv, x[4 * w + 3] * inv, pk, true);
                             qf8[ks][part][w] = (uint32_t)pk;
-                            if (part == 0) {   // the residual goes to lo
+                            if (part < kParts - 1) {   // the residual goes to the next part
                                 x[4 * w] -= __builtin_amdgcn_cvt_f32_fp8(pk, 0) * sc;
                                 x[4 * w + 1] -= __builtin_amdgcn_cvt_f32_fp8(pk, 1) * sc;
                                 x[4 * w + 2] -= __builtin_amdgcn_cvt_f32_fp8(pk, 2) * sc;
@@ -1730,17 +1755,37 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
                         }
                     }
                 }
-                // tail dims 448 + 32 s2 + 8 q + [0, 8), bf16 -> f16
+                // tail dims 448 + 32 s2 + 8 q + [0, 8): bf16 -> f16, or fp32 -> f16 hi + lo
 #pragma unroll
                 for (int s2 = 0; s2 < 2; ++s2) {
-                    const uint4_t w = *reinterpret_cast<const uint4_t *>(qsrc + 448 + 32 * s2 + 8 * q);
                     half8_t h;
+                    if constexpr (kQf32) {
+                        const float4_t a = *reinterpret_cast<const float4_t *>(qsrc32 + 448 + 32 * s2 + 8 * q);
+                        const float4_t b = *reinterpret_cast<const float4_t *>(qsrc32 + 448 + 32 * s2 + 8 * q + 4);
+                        half8_t l;
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        h[2 * i] = (half_t)bf16_to_f32((uint16_t)(w[i] & 0xFFFF));
-                        h[2 * i + 1] = (half_t)bf16_to_f32((uint16_t)(w[i] >> 16));
+                        for (int i = 0; i < 4; ++i) {
+                            h[i] = (half_t)a[i];
+                            l[i] = (half_t)(a[i] - (float)h[i]);
+                            h[4 + i] = (half_t)b[i];
+                            l[4 + i] = (half_t)(b[i] - (float)h[4 + i]);
+                        }
+                        qtl[s2] = l;
+                    } else {
+                        const uint4_t w = *reinterpret_cast<const uint4_t *>(qsrc + 448 + 32 * s2 + 8 * q);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            h[2 * i] = (half_t)bf16_to_f32((uint16_t)(w[i] & 0xFFFF));
+                            h[2 * i + 1] = (half_t)bf16_to_f32((uint16_t)(w[i] >> 16));
+                        }
                     }
                     qt[s2] = h;
+                }
+                if constexpr (kQf32) {   // this lane's slots only: no other wave reads them
+                    const uint32_t qa = lds_addr(&q_tail_s[(d * 4) * 64]) + 16 * lane;
+                    asm volatile("ds_write_b128 %0, %1\n\tds_write_b128 %0, %2 offset:1024\n\t"
+                                 "ds_write_b128 %0, %3 offset:2048\n\tds_write_b128 %0, %4 offset:3072"
+                                 :: "v"(qa), "v"(qt[0]), "v"(qt[1]), "v"(qtl[0]), "v"(qtl[1]) : "memory");
                 }
             }
             float m_run = -INFINITY, l_run = 0.0f;   // head 16 d + j; l over this lane's rows
@@ -1755,11 +1800,14 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) s8[hh][r] = sa[hh][r] * A.kq_log2;
                 if (nv < kTile) {
+                    int ln = lane;   // opaque: the row numbers are not held through the loop
+                    asm volatile("" : "+v"(ln));
+                    const int rq = 4 * (ln >> 4);
 #pragma unroll
                     for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
                         for (int r = 0; r < 4; ++r)
-                            if (16 * hh + 4 * q + r >= nv) s8[hh][r] = -INFINITY;
+                            if (16 * hh + rq + r >= nv) s8[hh][r] = -INFINITY;
                 }
                 float tmax = -INFINITY;
                 if constexpr (kLean) {
@@ -1807,7 +1855,11 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
                 lds_st128(lds_addr(pws) + (uint32_t)(((b * 4 + d) * 64 + lane) * 16), pf);
                 l_run = l_run * alpha + psum;
                 m_run = m_new;
-                if (q == 0) lds_st32(lds_addr(&alpha_s[b][16 * d + j]), alpha);
+                if (q == 0) {
+                    int ln = lane;   // opaque, as above (q == 0: ln is the head's j)
+                    asm volatile("" : "+v"(ln));
+                    lds_st32(lds_addr(&alpha_s[b][16 * d]) + 4 * ln, alpha);
+                }
                 const int moved = __any(alpha != 1.0f) ? 1 : 0;
                 if (lane == 0) lds_st32(lds_addr(&rescale_s[b][d]), __int_as_float(moved));
             };
@@ -1842,8 +1894,20 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
                     const uint32_t ta = st + kFsTailOff + (16 * hh + j) * kFsTailRow;
                     lds_read_row(st + (16 * hh + j) * kFsCodeRow + 16 * q, ta + tpos0, ta + tpos1,
                                  st + kFsExpOff + (16 * hh + j) * 8, kc, kt, ke);
+                    half8_t qtv[2], qtlv[2];
+                    if constexpr (kQf32) {
+                        const uint32_t qa = lds_addr(&q_tail_s[(d * 4) * 64]) + 16 * ln;
+                        asm volatile("ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:1024\n\t"
+                                     "ds_read_b128 %2, %4 offset:2048\n\tds_read_b128 %3, %4 offset:3072"
+                                     : "=&v"(qtv[0]), "=&v"(qtv[1]), "=&v"(qtlv[0]), "=&v"(qtlv[1]) : "v"(qa));
+                    } else {
+                        qtv[0] = qt[0];
+                        qtv[1] = qt[1];
+                    }
                     if (hh == 0) pre();
                     lds_row_wait(kc, kt, ke);
+                    if constexpr (kQf32)   // landed with the wait
+                        asm volatile("" : "+v"(qtv[0]), "+v"(qtv[1]), "+v"(qtlv[0]), "+v"(qtlv[1]));
                     if (q < 2 && (d < 3 || q == 0)) {
                         if constexpr (kLean) {
                             const int e = __builtin_amdgcn_sbfe((int)ke[d >> 1], 8 * ((2 * d + q) & 3), 8);
@@ -1862,6 +1926,7 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
                     uint32_t scl = 0;
                     if constexpr (kLean)
                         scl = __builtin_amdgcn_perm(ke[1], ke[0], (q >> 1) ? 0x07050301u : 0x06040200u) ^ 0x80808080u;
+                    // two accumulation chains; the third part (fp32 Q) joins chain 0
                     float4_t c2[2] = {float4_t{0, 0, 0, 0}, float4_t{0, 0, 0, 0}};
                     static_for<4>([&](auto ksc) {
                         constexpr int ks = decltype(ksc)::value;
@@ -1872,16 +1937,26 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
                         if constexpr (ks < 3) k_hi = kc[2 * ks + 1];
                         const int8v av = __builtin_bit_cast(int8v, uint4x2_cat(kc[2 * ks], k_hi));
 #pragma unroll
-                        for (int part = 0; part < 2; ++part) {
-                            const int8v bv = __builtin_bit_cast(int8v, qf8v(qf8[ks][part]));
-                            c2[part] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                                av, bv, c2[part], 0, 0, kLean ? ks : 0, sa, ks, qsc[part]);
+                        for (int part = 0; part < kParts; ++part) {
+                            // k-step 3's dims 448.. are zeros: its upper 16 bytes are constants
+                            const uint8x_t qv = ks < 3 ? qf8v(qf8[ks][part])
+                                                       : uint8x_t{qf8[ks][part][0], qf8[ks][part][1],
+                                                                  qf8[ks][part][2], qf8[ks][part][3], 0, 0, 0, 0};
+                            const int8v bv = __builtin_bit_cast(int8v, qv);
+                            c2[part & 1] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                                av, bv, c2[part & 1], 0, 0, kLean ? ks : 0, sa, ks, qsc[part]);
                         }
                     });
-                    c2[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, kt[0]), qt[0],
+                    c2[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, kt[0]), qtv[0],
                                                                    c2[0], 0, 0, 0);
-                    c2[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, kt[1]), qt[1],
+                    c2[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, kt[1]), qtv[1],
                                                                    c2[1], 0, 0, 0);
+                    if constexpr (kQf32) {
+                        c2[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, kt[0]), qtlv[0],
+                                                                       c2[0], 0, 0, 0);
+                        c2[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, kt[1]), qtlv[1],
+                                                                       c2[1], 0, 0, 0);
+                    }
                     acc[hh] = c2[0] + c2[1];
                 }
             };
@@ -2369,6 +2444,9 @@ int launch(DecodeArgs &A, const Plan &pl, hipStream_t st, int phases = 3,
             else
                 launch_ws<0>(A, pl, st, o);
         }
+        else if (kFp8 && !A.phys && o.kernel != DS4HIP_DECODE_KERNEL_REGLOAD && !o.exact_p)
+            // fp32 Q over direct rows: the flat-stage kernel with Q in three FP8 parts
+            hipLaunchKernelGGL((decode_flat_kernel<false, true, true>), dim3(pl.n_wg), dim3(512), 0, st, A);
         else if (kFp8)
             hipLaunchKernelGGL(decode_fp8_kernel<kQf32>, dim3(pl.n_wg), dim3(256), 0, st, A);
         else if (A.f32_v_raw)

@@ -240,6 +240,38 @@ def test_fp8_flat_and_regload_kernels(gpu, counts):
         check(outs[1][p], outs[0][p])
 
 
+@pytest.mark.parametrize("counts", [[1], [33], [1000], [300, 0, 64, 1025, 7], [32768]])
+def test_fp8_fp32_q_kernels(gpu, counts):
+    """fp32 Q over direct rows: the flat-stage kernel (the default: Q in three
+    scaled FP8 parts, one f16 P) and the fp32-Q register kernel (Q as f16
+    hi + lo, P hi + lo; exact_p) against the oracle, which takes Q in fp32, at
+    the decode bar. Q ~ 2 N(0, 1), so scores span a wide range. Measured max
+    err / RMS: flat 4.9e-4 .. 1.0e-3, register kernel 5e-6 .. 4e-5. (With the
+    f16 tail of Q rounded once instead of hi + lo, the flat form read 4e-3.)"""
+    total = int(sum(counts))
+    base = np.concatenate([[0], np.cumsum(counts)[:-1]])
+    cache, (codes, sexp, tail) = make_cache(total, 71, gpu)
+    n = len(counts)
+    qf = synth.normal(72, 2, n * 64 * 512).reshape(n, 64, 512) * 2.0
+    sinks = sinks_for(73, n)
+    rb = torch.from_numpy(base.astype(np.int64)).to(gpu)
+    outs = {}
+    for exact in (False, True):
+        out = torch.zeros((n, 64, 512), dtype=torch.float32, device=gpu)
+        ops.flash_attn_decode_fp8(torch.from_numpy(qf).to(gpu), torch.from_numpy(sinks).to(gpu), out, cache,
+                                  counts, row_base=rb, exact_p=exact)
+        torch.cuda.synchronize()
+        outs[exact] = out.cpu().numpy()
+    for p, c in enumerate(counts):
+        if c == 0:
+            assert (outs[False][p] == 0).all() and (outs[True][p] == 0).all()
+            continue
+        rows = base[p] + np.arange(c)
+        ref = O.attn_decode_fp8(qf[p], codes, sexp, tail, rows, sinks[p], n_threads=8)
+        check(outs[False][p], ref)
+        check(outs[True][p], ref)
+
+
 @pytest.mark.parametrize("q_f32,paged", [(False, False), (True, False), (False, True)])
 def test_fp8_gathered_rows_outside_the_cache(gpu, q_f32, paged):
     """A row list (or page table) naming rows outside the cache: the kernels

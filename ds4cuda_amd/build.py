@@ -40,10 +40,11 @@ def _compile(src: Path) -> Path:
 
 
 # Kernels whose copy ring counts outstanding vector-memory operations: a
-# register spill (scratch access) inside the ring would break that count, so
-# the build refuses any scratch access that a path can reach while a copy is
-# outstanding (ds4cuda_amd/spill_check.py); spills outside the ring (before the
-# first copy, after a vmcnt(0)) are allowed.
+# register spill store inside the ring could complete ahead of older copies
+# and break that count, so the build refuses any spill store that a path can
+# reach while a copy is outstanding (ds4cuda_amd/spill_check.py). Spills
+# outside the ring (before the first copy, after a vmcnt(0)) and reloads
+# (in order with the copies) are allowed.
 NO_SPILL_KERNELS = ("decode_fp8_kernelILb0E", "decode_flat_kernel")
 
 
@@ -64,7 +65,7 @@ def check_spills(src: Path) -> None:
         if any(k in sym for k in NO_SPILL_KERNELS):
             bad = ring_violations(asm, sym)
             if bad:
-                raise RuntimeError(f"{sym}: {len(bad)} scratch accesses while ring copies may be "
+                raise RuntimeError(f"{sym}: {len(bad)} spill stores while ring copies may be "
                                    f"outstanding (first: {bad[0]}); its copy-ring waits require none")
 
 

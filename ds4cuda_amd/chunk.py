@@ -56,13 +56,14 @@ class ChunkLayer:
 
 
 def forward_chunk_attn(session, il, p0, attn_norm, q_lora_norm, q_cur, kv_rope, sinks, out,
-                       layer: ChunkLayer | None = None, workspace=None, stream=None):
+                       layer: ChunkLayer | None = None, workspace=None, exact_p=False, stream=None):
     """Attention slice of layer il for the n tokens at positions p0 .. p0+n-1
     of the session (n <= 128). attn_norm [n, 4096], q_lora_norm [n, 1024],
     q_cur [n, 64, 512], kv_rope [n, 512] fp32 (the producer's outputs, e.g.
     ops.attn_qkv_decode_f32 per token); sinks [64]; out [n, 64, 512] receives
-    each token's attention output (Step 13's kqv). Returns the workspace."""
-    from .ops import _check, decode_fp8_workspace_bytes
+    each token's attention output (Step 13's kqv). exact_p: the decode's P as
+    f16 hi + lo (as Session.decode). Returns the workspace."""
+    from .ops import _check, decode_fp8_workspace_bytes, decode_opts
     n = kv_rope.shape[0]
     if not 0 < n <= CHUNK_MAX:
         raise Ds4HipError("chunk of 1..128 tokens", -22)
@@ -161,7 +162,8 @@ def forward_chunk_attn(session, il, p0, attn_norm, q_lora_norm, q_cur, kv_rope, 
     call("ds4hip_flash_attn_decode_fp8", _ptr(q_cur), 1, N_HEAD * HEAD_DIM, _ptr(sinks), 0, _ptr(out),
          N_HEAD * HEAD_DIM, _vp(s.codes + rb * 448), _vp(s.sexp + rb * 8), _vp(s.tail + rb * 128),
          C.cast(counts, C.c_void_p), n, None, 0, _ptr(lists), stride, None, 0, 256, N_HEAD, HEAD_DIM,
-         N_ROT, C.c_longlong(session.rows_from(rb)), None, _ptr(workspace), workspace.numel(), 3, st)
+         N_ROT, C.c_longlong(session.rows_from(rb)), C.byref(decode_opts(exact_p)), _ptr(workspace),
+         workspace.numel(), 3, st)
     # the last token's selection stays in the layer's row list, where the
     # token-by-token loop leaves it
     if sel is not None and n_sel[-1] < n_comp[-1]:

@@ -1478,6 +1478,10 @@ constexpr int kFsExpOff = kFsTailOff + kTile * kFsTailRow; // 19456
 constexpr int kFsBytes = kFsExpOff + kTile * 8;           // 19712
 constexpr int kFsScaleOff = kFsBytes;                     // f16 2^e per [block][row]
 constexpr int kFsSlot = kFsBytes + 8 * kTile * 2;          // 20224
+// gathered rows: the physical rows of the tile kFsLead tiles later (32
+// int64, copied by consumer wave 0) ride in the stage after the scale table
+constexpr int kFsPhysOff = kFsSlot;
+constexpr int kFsSlotGather = kFsSlot + kTile * 8;         // 20480
 constexpr int kFsStages = 6;
 constexpr int kFsLead = 3;                                 // tiles copied ahead of the producers
 constexpr int kFsCodeChunks = kTile * (kFsCodeRow / 16);  // 960
@@ -1635,16 +1639,20 @@ __device__ inline float xmax_16_32_raw(float v) {
 // copies from an SGPR base). The score scale log2(e)/sqrt(d) stays on S after
 // the MFMA: folded into Q it would make the bf16 values inexact in the two
 // E4M3 parts (a bf16 value's 8 significant bits split exactly into hi + lo).
-template <bool kPLo, bool kLean, bool kQf32 = false>
+template <bool kPLo, bool kLean, bool kQf32 = false, bool kGather = false>
 __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A) {
-    static_assert(!kPLo, "the flat kernel passes P as one f16");
     static_assert(kLean || !kQf32, "fp32 Q takes the lean form");
     // Q parts on the scaled FP8 MFMA: a bf16 Q (8 significant bits) fits in
     // two E4M3 parts; an fp32 Q takes three (about 12 bits: the score error of
     // the dropped rest is ~2^-12 of |q| |k|)
     constexpr int kParts = kQf32 ? 3 : 2;
-    __shared__ __attribute__((aligned(16))) uint8_t stage[kFsStages][kFsSlot];
-    __shared__ __attribute__((aligned(16))) uint8_t pws[2 * 4 * 64 * 16];   // [t & 1][head tile][lane] f16 x 8
+    static_assert(kLean || !kGather, "gathered rows take the lean form");
+    // copies per consumer wave and tile: 5 of the tile, plus (gathered rows,
+    // consumer wave 0) one of the physical rows of a later tile
+    __shared__ __attribute__((aligned(16))) uint8_t stage[kFsStages][kGather ? kFsSlotGather : kFsSlot];
+    __shared__ int s_bad[2];
+    // P: [hi, lo (kPLo)][t & 1][head tile][lane] f16 x 8
+    __shared__ __attribute__((aligned(16))) uint8_t pws[(kPLo ? 2 : 1) * 2 * 4 * 64 * 16];
     __shared__ __attribute__((aligned(16))) float alpha_s[2][kH];
     __shared__ __attribute__((aligned(16))) int rescale_s[2][4];   // [t & 1][head tile]: some alpha != 1
     __shared__ long long s_start[kMaxProb + 1];
@@ -1655,6 +1663,7 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
     // VGPRs): [wave][hi s0, hi s1, lo s0, lo s1][lane]
     __shared__ __attribute__((aligned(16))) half8_t q_tail_s[kQf32 ? 4 * 4 * 64 : 1];
     stage_rowbase(A, s_rowbase, s_badp);
+    if (threadIdx.x < 2) s_bad[threadIdx.x] = 0;
     stage_start(A, s_start);
 
     const int lane = threadIdx.x & 63;
@@ -1677,6 +1686,7 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
         const long long slot = (long long)blockIdx.x * A.s_max + slot_s;
         const long long seg_r0 = s_rowbase[p] + r0;
         const int seg_last = (int)(r1 - 1 - r0);
+        if constexpr (kGather) scan_segment_rows(A, true, p, g0, seg_end, r0, r1, 0, slot_s, s_bad);
         // ---- the producers: QK^T on the scaled FP8 MFMA and the softmax, one
         // interval apart (interval u: QK(u) with softmax(u - 1) in its issue slots)
         auto produce = [&]() {
@@ -1853,6 +1863,7 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
                         psum = __builtin_amdgcn_fdot2(half2_t{pf[2 * i], pf[2 * i + 1]}, one2, psum, false);
                 }
                 lds_st128(lds_addr(pws) + (uint32_t)(((b * 4 + d) * 64 + lane) * 16), pf);
+                if constexpr (kPLo) lds_st128(lds_addr(pws) + 8192u + (uint32_t)(((b * 4 + d) * 64 + lane) * 16), pl);
                 l_run = l_run * alpha + psum;
                 m_run = m_new;
                 if (q == 0) {
@@ -2035,8 +2046,54 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
                     c_voff[k] = (uint32_t)c_row[k] * rb + c_off[k];
                 }
             }
+            // gathered rows: the copies of tile u from physical rows rr (this
+            // lane's 5 rows; unmarked, so a row outside the cache reads row 0 and
+            // the slot is marked bad), plus the physical rows of tile u + kFsLead
+            // into this wave's slot of the stage (32 int64, 4 bytes per lane),
+            // clamped inside the phys array (it has kTile rows of padding)
+            auto issue_rows = [&](int u, const long long (&rr)[5]) {
+                uint8_t *st = stage[u % kFsStages];
+#pragma unroll
+                for (int k = 0; k < 5; ++k) {
+                    const int n = 5 * c + k;
+                    if (n == 19)
+                        __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t *>(A.sexp) + rr[k] * 8 + c_off[k],
+                                                         st + kFsExpOff, 4, 0, 0);
+                    else if (n < kFsCodeChunks / 64)
+                        __builtin_amdgcn_global_load_lds(A.codes + rr[k] * kNope + c_off[k], st + 1024 * n, 16, 0, 0);
+                    else
+                        __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t *>(A.tail) + rr[k] * (2 * kRot) + c_off[k],
+                                                         st + 1024 * n, 16, 0, 0);
+                }
+                if (c == 0) {
+                    const long long gi = min(g0 + (long long)kTile * (u + kFsLead), A.total);
+                    int ln2 = lane;
+                    asm volatile("" : "+v"(ln2));
+                    __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t *>(A.phys + gi) + 4 * ln2,
+                                                     st + kFsPhysOff, 4, 0, 0);
+                }
+            };
             auto issue = [&](int u) {
                 uint8_t *st = stage[u % kFsStages];
+                if constexpr (kGather) {
+                    // tile u's rows rode in with tile u - kFsLead (landed: wave 0's wait
+                    // for that tile and the barrier after it have passed); rows past
+                    // the segment repeat its last row
+                    const uint32_t ph = lds_addr(stage[(u - kFsLead) % kFsStages] + kFsPhysOff);
+                    long long rr[5];
+                    const int last = seg_last - kTile * u;
+#pragma unroll
+                    for (int k = 0; k < 5; ++k) {
+                        const int e = max(min(c_row[k], last), 0);
+                        asm volatile("ds_read_b64 %0, %1" : "=v"(rr[k]) : "v"(ph + 8 * e));
+                    }
+                    asm volatile("s_waitcnt lgkmcnt(0)"
+                                 : "+v"(rr[0]), "+v"(rr[1]), "+v"(rr[2]), "+v"(rr[3]), "+v"(rr[4]) :: "memory");
+#pragma unroll
+                    for (int k = 0; k < 5; ++k) rr[k] = unmark_row(rr[k]);
+                    issue_rows(u, rr);
+                    return;
+                }
                 if constexpr (kLean) {
                     if (kTile * u + kTile - 1 <= seg_last) {
                         const uint32_t r0 = (uint32_t)(kTile * u);
@@ -2082,11 +2139,22 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
             // row's f16 block scale; the f16 tail through two transposing 16-bit
             // reads (lane (m, g) supplies row 4 g + (m >> 2), dims 4 (m & 3) + [0, 4)
             // of the chunk pair 2 nb', 2 nb' + 1 of dims 448 + 16 nb' + [0, 16)).
-            const uint32_t tr8_row = (uint32_t)((16 * ((j >> 1) >> 2) + 4 * q + ((j >> 1) & 3)) * kFsCodeRow +
-                                                128 * c + 8 * (j & 1));
+            // (the row offset is rebuilt per tile from an opaque lane id: held
+            // through the loop it is one more long-lived register)
+            auto tr8_row_of = [&]() {
+                int ln = lane;
+                asm volatile("" : "+v"(ln));
+                const int jj = ln & 15, qq = ln >> 4;
+                return (uint32_t)((16 * ((jj >> 1) >> 2) + 4 * qq + ((jj >> 1) & 3)) * kFsCodeRow +
+                                  128 * c + 8 * (jj & 1));
+            };
             auto pv = [&](int t) {
                 const int b = t & 1;
                 const uint32_t st = lds_addr(stage[t % kFsStages]);
+                const uint32_t tr8_row = tr8_row_of();
+                int lnp = lane;   // opaque, as tr8_row_of
+                asm volatile("" : "+v"(lnp));
+                const int qp = lnp >> 4;
                 half8_t pa[4];
                 uint4_t mv;         // the producers' rescale flags of tile t
                 uint2_t sc[2][2];   // [block of the quarter][row group]: f16 x 2 scale pairs
@@ -2097,12 +2165,19 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
                     "ds_read_b128 %2, %5 offset:2048\n\tds_read_b128 %3, %5 offset:3072\n\t"
                     "ds_read_b128 %4, %6"
                     : "=&v"(pa[0]), "=&v"(pa[1]), "=&v"(pa[2]), "=&v"(pa[3]), "=&v"(mv)
-                    : "v"(lds_addr(pws) + (uint32_t)((b * 4 * 64 + lane) * 16)),
+                    : "v"(lds_addr(pws) + (uint32_t)((b * 4 * 64 + lnp) * 16)),
                       "v"(lds_addr(&rescale_s[b][0])));
+                half8_t pl[4];   // kPLo: the lo halves of P, landed with the first wait below
+                if constexpr (kPLo)
+                    asm volatile(
+                        "ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:1024\n\t"
+                        "ds_read_b128 %2, %4 offset:2048\n\tds_read_b128 %3, %4 offset:3072"
+                        : "=&v"(pl[0]), "=&v"(pl[1]), "=&v"(pl[2]), "=&v"(pl[3])
+                        : "v"(lds_addr(pws) + 8192u + (uint32_t)((b * 4 * 64 + lnp) * 16)));
 #pragma unroll
                 for (int bb = 0; bb < 2; ++bb) {
                     if (kTailQ && bb == 1) continue;
-                    const uint32_t ta = st + kFsScaleOff + ((2 * c + bb) * kTile + 4 * q) * 2;
+                    const uint32_t ta = st + kFsScaleOff + ((2 * c + bb) * kTile + 4 * qp) * 2;
                     asm volatile("ds_read_b64 %0, %2\n\tds_read_b64 %1, %2 offset:32"
                                  : "=&v"(sc[bb][0]), "=&v"(sc[bb][1]) : "v"(ta));
                 }
@@ -2132,6 +2207,8 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
                                "+v"(sc[0][0]), "+v"(sc[0][1]), "+v"(sc[1][0]), "+v"(sc[1][1]),
                                "+v"(tb[0]), "+v"(tb[1]), "+v"(tb[2]), "+v"(tb[3]), "+v"(tt[0][0])
                              : "n"(kTailQ ? 8 : 4) : "memory");
+                if constexpr (kPLo)   // issued before the last reads: landed with that wait
+                    asm volatile("" : "+v"(pl[0]), "+v"(pl[1]), "+v"(pl[2]), "+v"(pl[3]));
                 // rare: a producer moved a reference point; the accumulators of
                 // its heads are rescaled by alpha (1 for the other heads)
                 if (__builtin_amdgcn_readfirstlane((int)(mv[0] | mv[1] | mv[2] | mv[3]))) {
@@ -2175,20 +2252,44 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
 #pragma unroll
                     for (int hb = 0; hb < 4; ++hb)
                         o[hb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[hb], vb, o[hb][nb], 0, 0, 0);
+                    if constexpr (kPLo) {
+#pragma unroll
+                        for (int hb = 0; hb < 4; ++hb)
+                            o[hb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[hb], vb, o[hb][nb], 0, 0, 0);
+                    }
                     vb = vn;
                 }
             };
+            // the tiles after the next kFsLead - 1 have landed (this wave's copies)
+            auto wait_ring = [&]() {
+                if (kGather && c == 0)
+                    asm volatile("s_waitcnt vmcnt(%0)" :: "n"(6 * (kFsLead - 1)) : "memory");
+                else
+                    asm volatile("s_waitcnt vmcnt(%0)" :: "n"(5 * (kFsLead - 1)) : "memory");
+            };
             // prologue: tiles 0 .. kFsLead - 1; tile 0 lands before the first barrier
+            if constexpr (kGather) {
+                // their rows straight from the phys array, all loaded before any copy
+                long long rr[kFsLead][5];
 #pragma unroll
-            for (int u = 0; u < kFsLead; ++u) issue(u);
-            asm volatile("s_waitcnt vmcnt(%0)" :: "n"(5 * (kFsLead - 1)) : "memory");
+                for (int u = 0; u < kFsLead; ++u)
+#pragma unroll
+                    for (int k = 0; k < 5; ++k)
+                        rr[u][k] = unmark_row(A.phys[g0 + min(kTile * u + c_row[k], seg_last)]);
+#pragma unroll
+                for (int u = 0; u < kFsLead; ++u) issue_rows(u, rr[u]);
+            } else {
+#pragma unroll
+                for (int u = 0; u < kFsLead; ++u) issue(u);
+            }
+            wait_ring();
             lds_barrier();
             // interval u: copies of u + kFsLead, P . V(u - 2); before the barrier
             // that ends it, tile u + 1 has landed (this wave's copies)
             for (int u = 0; u < n_tiles + 2; ++u) {
                 issue(u + kFsLead);
                 if (u >= 2) pv(u - 2);
-                asm volatile("s_waitcnt vmcnt(%0)" :: "n"(5 * (kFsLead - 1)) : "memory");
+                wait_ring();
                 lds_barrier();
             }
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -2214,8 +2315,13 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
                 else consume(std::false_type{});
             }
         }
-        // a segment with no rows (padding of the chunked row space) has no partial
-        if (threadIdx.x == 0) A.ws_prob[slot] = n_tiles > 0 ? (p | (s_badp[p] ? kBadSlot : 0)) : -1;
+        // a segment with no rows (padding of the chunked row space) has no partial;
+        // a bad row met by the segment's scan marks the slot (s_bad: the scan's
+        // atomics are ordered before this by the tile loop's barriers)
+        if (threadIdx.x == 0) {
+            A.ws_prob[slot] = n_tiles > 0 ? (p | ((s_badp[p] | s_bad[slot_s & 1]) ? kBadSlot : 0)) : -1;
+            s_bad[slot_s & 1] = 0;
+        }
         ++slot_s;
         g0 = seg_end;
         lds_barrier();   // the next segment reuses the stages
@@ -2417,6 +2523,10 @@ void launch_ws(const DecodeArgs &A, const Plan &pl, hipStream_t st, const ds4hip
         hipLaunchKernelGGL((decode_flat_kernel<false, true>), dim3(pl.n_wg), dim3(512), 0, st, A);
         return;
     }
+    if (kMode == 1 && o.kernel != DS4HIP_DECODE_KERNEL_REGLOAD && !o.exact_p) {
+        hipLaunchKernelGGL((decode_flat_kernel<false, true, false, true>), dim3(pl.n_wg), dim3(512), 0, st, A);
+        return;
+    }
     if (o.exact_p)
         hipLaunchKernelGGL((decode_ws_kernel<kMode, true>), dim3(pl.n_wg), dim3(512), 0, st, A);
     else
@@ -2444,9 +2554,14 @@ int launch(DecodeArgs &A, const Plan &pl, hipStream_t st, int phases = 3,
             else
                 launch_ws<0>(A, pl, st, o);
         }
-        else if (kFp8 && !A.phys && o.kernel != DS4HIP_DECODE_KERNEL_REGLOAD && !o.exact_p)
-            // fp32 Q over direct rows: the flat-stage kernel with Q in three FP8 parts
-            hipLaunchKernelGGL((decode_flat_kernel<false, true, true>), dim3(pl.n_wg), dim3(512), 0, st, A);
+        else if (kFp8 && o.kernel != DS4HIP_DECODE_KERNEL_REGLOAD) {
+            // fp32 Q: the flat-stage kernel with Q in three FP8 parts and, as
+            // every fp32-Q decode, P as f16 hi + lo
+            if (A.phys)
+                hipLaunchKernelGGL((decode_flat_kernel<true, true, true, true>), dim3(pl.n_wg), dim3(512), 0, st, A);
+            else
+                hipLaunchKernelGGL((decode_flat_kernel<true, true, true>), dim3(pl.n_wg), dim3(512), 0, st, A);
+        }
         else if (kFp8)
             hipLaunchKernelGGL(decode_fp8_kernel<kQf32>, dim3(pl.n_wg), dim3(256), 0, st, A);
         else if (A.f32_v_raw)

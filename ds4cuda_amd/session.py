@@ -170,12 +170,13 @@ class Session:
              C.byref(n), C.byref(sel))
         return ri.value, n.value, sel.value
 
-    def decode(self, il, q, sinks, out, n_selected=-1, workspace=None, stream=None):
+    def decode(self, il, q, sinks, out, n_selected=-1, workspace=None, exact_p=False, stream=None):
         """Decode attention of one query (q [64,512] bf16/fp32) over layer il's
         valid ring rows plus its first n_selected compressed rows (all n_comp
         when n_selected < 0; the selection written at layer_rows()' selected
-        address otherwise)."""
-        from .ops import HEAD_DIM, N_HEAD, N_ROT, decode_fp8_workspace_bytes
+        address otherwise). exact_p: P as f16 hi + lo (the register kernels)
+        instead of one f16 (the flat-stage kernel)."""
+        from .ops import HEAD_DIM, N_HEAD, N_ROT, decode_fp8_workspace_bytes, decode_opts
         ri, n, _ = self.layer_rows(il, n_selected)
         _check(q, q.dtype, N_HEAD * HEAD_DIM, "q")
         _check(sinks, torch.float32, N_HEAD, "sinks")
@@ -190,6 +191,6 @@ class Session:
              C.c_void_p(self.s.codes + rb * 448), C.c_void_p(self.s.sexp + rb * 8),
              C.c_void_p(self.s.tail + rb * 128), C.cast(counts, C.c_void_p), 1, None, 0,
              C.c_void_p(ri),
-             0, None, 0, 256, N_HEAD, HEAD_DIM, N_ROT, C.c_longlong(self.rows_from(rb)), None,
-             _ptr(workspace), workspace.numel(), 3, _stream(stream))
+             0, None, 0, 256, N_HEAD, HEAD_DIM, N_ROT, C.c_longlong(self.rows_from(rb)),
+             C.byref(decode_opts(exact_p)), _ptr(workspace), workspace.numel(), 3, _stream(stream))
         return workspace

@@ -3,15 +3,18 @@
 The FP8 decode kernels count their outstanding HBM -> LDS copies
 (global_load_lds) with hand-written `s_waitcnt vmcnt(N)`. A scratch access
 (register spill or reload) issued while such copies are in flight adds to
-the same counter, and a scratch store may complete ahead of older copies, so
-the hand-written waits would no longer prove that a stage has landed. A
-spill is harmless where no copy can be outstanding: before the first copy,
-or after a `s_waitcnt vmcnt(0)` on every path.
+the same counter. A reload is a load: loads return in issue order, so it can
+only make a later `vmcnt(N)` wait for more copies than it needs. A spill
+store is not ordered with the loads: it may complete ahead of older copies,
+and a hand-written wait would then no longer prove that a stage has landed.
+A spill store is harmless where no copy can be outstanding: before the first
+copy, or after a `s_waitcnt vmcnt(0)` on every path.
 
 `ring_violations(asm, kernel)` runs that check as a forward dataflow over the
 kernel's basic blocks: the state is "a copy may be outstanding", set by
 global_load_lds, cleared by `s_waitcnt vmcnt(0)`, joined (or) at block
-entries; any scratch_load / scratch_store reached in that state is reported.
+entries; any scratch_store reached in that state is reported (with
+loads=True, reloads too).
 """
 from __future__ import annotations
 
@@ -62,7 +65,7 @@ def _blocks(body: list[str]):
     return [b for b in blocks if b[0] is not None or b[1]]
 
 
-def ring_violations(asm: str, symbol: str) -> list[str]:
+def ring_violations(asm: str, symbol: str, loads: bool = False) -> list[str]:
     blocks = _blocks(kernel_body(asm, symbol))
     index = {lab: i for i, (lab, _) in enumerate(blocks) if lab}
     succ = []
@@ -87,7 +90,8 @@ def ring_violations(asm: str, symbol: str) -> list[str]:
                 state = True
             elif op == "s_waitcnt" and re.search(r"vmcnt\(0\)", ln):
                 state = False
-            elif op.startswith("scratch_") and state and report is not None:
+            elif (op.startswith("scratch_store") or (loads and op.startswith("scratch_load"))) \
+                    and state and report is not None:
                 report.append(ln)
         return state
 

@@ -5,8 +5,12 @@ token by token, cloned through save/load), a chunk of tokens through the
 driver and the same tokens one at a time (push, compressors, indexer
 selection, single-problem decode) give
 
-  * attention outputs within 1e-4 x RMS (the same rows and math; only the
-    split of the rows over workgroups differs), and on the window-only layer
+  * attention outputs with exact_p within 1e-4 x RMS (the same rows and
+    math; only the split of the rows over workgroups differs); the default
+    path's token outputs within the 2e-3 x RMS decode bar of those, per token
+    (an fp32 Q always passes P as f16 hi + lo, so today they agree to ~1e-5;
+    a one-f16-P path, which rounds P against a running max that depends on
+    the split, measured up to 2.4e-3 here), and on the window-only layer both
     within 2e-3 x RMS of the CPU oracle for the chunk's last token;
   * byte-identical sessions afterwards (ring rows, compressed rows, indexer
     keys, compressor states, counters), the staging rows aside.
@@ -59,8 +63,10 @@ def token_inputs(il, pos, gpu):
     return g(1, EMBD), g(2, 1024), g(3, NH * HD), g(4, HD)   # attn_norm, q_lora_norm, q_cur, kv_rope
 
 
-def one_token(s, il, pos, layer, sinks, out, gpu):
-    """The per-token loop's attention slice (Steps 11-13) on the session."""
+def one_token(s, il, pos, layer, sinks, out, gpu, out_fast=None):
+    """The per-token loop's attention slice (Steps 11-13) on the session; out
+    receives the decode with P as hi + lo (exact_p), out_fast (if given) the
+    default one-f16-P decode of the same rows."""
     x, qln, q, kv = token_inputs(il, pos, gpu)
     s.push_raw(il, kv)
     L = s.layer(il)
@@ -104,7 +110,9 @@ def one_token(s, il, pos, layer, sinks, out, gpu):
                 call("ds4hip_indexer_topk_positions", _ptr(q_idx), _ptr(w_idx), C.c_void_p(L.index_comp_kv), 0,
                      L.n_index_comp, NH, IHD, TOPK, 0, _ptr(scores), _ptr(select), None, C.c_void_p(sel), st)
                 n_sel = TOPK
-    s.decode(il, q, sinks, out, n_selected=n_sel)
+    s.decode(il, q, sinks, out, n_selected=n_sel, exact_p=True)
+    if out_fast is not None:
+        s.decode(il, q, sinks, out_fast, n_selected=n_sel)
 
 
 def layer_bytes(s, il):
@@ -136,37 +144,52 @@ def test_chunk_matches_token_loop(gpu, tmp_path, il):
     layer = layer_weights(il, gpu)
     sinks = torch.from_numpy(synth.normal(310, il, NH)).to(gpu)
     out1 = torch.empty(NH * HD, device=gpu)
+    out_fast = torch.empty(NH * HD, device=gpu)
     a = session.Session(1024)
     b = session.Session(1024)
+    c = session.Session(1024)
     try:
         for pos in range(HIST):
             one_token(a, il, pos, layer, sinks, out1, gpu)
         a.save(tmp_path / "h.kv")
         assert b.load(tmp_path / "h.kv")[0] == 0
-        # the chunk through the driver (session a)
+        assert c.load(tmp_path / "h.kv")[0] == 0
+        # the chunk through the driver (session a: hi + lo P; session c: default)
         ins = [token_inputs(il, HIST + t, gpu) for t in range(CHUNK)]
         stack = lambda k: torch.stack([x[k] for x in ins])
         attn_norm, qln, q_cur, kv = stack(0), stack(1), stack(2).reshape(CHUNK, NH, HD), stack(3)
         out_chunk = torch.empty((CHUNK, NH, HD), device=gpu)
-        forward_chunk_attn(a, il, HIST, attn_norm, qln, q_cur, kv, sinks, out_chunk, layer=layer)
+        out_chunk_fast = torch.empty((CHUNK, NH, HD), device=gpu)
+        forward_chunk_attn(a, il, HIST, attn_norm, qln, q_cur, kv, sinks, out_chunk, layer=layer, exact_p=True)
+        forward_chunk_attn(c, il, HIST, attn_norm, qln, q_cur, kv, sinks, out_chunk_fast, layer=layer)
         # the same tokens one at a time (session b)
-        ref = []
+        ref, ref_fast = [], []
         for t in range(CHUNK):
-            one_token(b, il, HIST + t, layer, sinks, out1, gpu)
+            one_token(b, il, HIST + t, layer, sinks, out1, gpu, out_fast)
             ref.append(out1.clone())
+            ref_fast.append(out_fast.clone())
         torch.cuda.synchronize()
         got = out_chunk.cpu().numpy().reshape(CHUNK, -1)
+        got_fast = out_chunk_fast.cpu().numpy().reshape(CHUNK, -1)
         exp = torch.stack(ref).cpu().numpy()
+        exp_fast = torch.stack(ref_fast).cpu().numpy()
         rms = np.sqrt(np.mean(exp.astype(np.float64) ** 2))
         err = np.abs(got - exp).max() / rms
+        # the decode bar holds per problem (each token is one): max err / RMS of its output
+        rms_t = np.sqrt(np.mean(exp.astype(np.float64) ** 2, axis=1))
+        e_fast = [float((np.abs(x - exp).max(axis=1) / rms_t).max()) for x in (got_fast, exp_fast)]
+        print(f"il {il}: default paths vs exact_p: chunk {e_fast[0]:.2e}, token loop {e_fast[1]:.2e}")
         assert err < 1e-4, err
+        assert max(e_fast) < 2e-3, e_fast
         if il == 0:   # oracle: the chunk's last token over its window (dequantized rows)
             win = np.stack([token_inputs(il, p, gpu)[3].cpu().numpy()
                             for p in range(HIST + CHUNK - 128, HIST + CHUNK)])
             deq = O.fp8_quant_rows(win)[3]
             ref_o = O.attn_decode_mixed_f32(q_cur[-1].cpu().numpy(), deq, None, None, sinks.cpu().numpy())
-            e_o = np.abs(got[-1].reshape(NH, HD) - ref_o).max() / np.sqrt(np.mean(ref_o.astype(np.float64) ** 2))
-            assert e_o < 2e-3, e_o
+            for g in (got, got_fast):
+                e_o = np.abs(g[-1].reshape(NH, HD) - ref_o).max() / np.sqrt(np.mean(ref_o.astype(np.float64) ** 2))
+                print(f"il 0: last token vs oracle {e_o:.2e}")
+                assert e_o < 2e-3, e_o
         ra, ca = layer_bytes(a, il), layer_bytes(b, il)
         assert ra[1] == ca[1]
         for x, y in zip(ra[0], ca[0]):
@@ -176,3 +199,4 @@ def test_chunk_matches_token_loop(gpu, tmp_path, il):
     finally:
         a.close()
         b.close()
+        c.close()

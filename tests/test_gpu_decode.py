@@ -74,7 +74,11 @@ def test_fp8_multi_problem_layers_and_fp32_q(gpu):
             check(got[p], ref)
 
 
-def test_fp8_sparse_rows_and_pages(gpu):
+@pytest.mark.parametrize("q_f32,exact", [(False, False), (False, True), (True, False), (True, True)])
+def test_fp8_sparse_rows_and_pages(gpu, q_f32, exact):
+    """Gathered rows through a page table: the flat-stage kernel with its rows
+    riding in the copy stream (default), or the register kernels (exact_p),
+    for bf16 and fp32 Q."""
     n_rows = 4096
     cache, (codes, sexp, tail) = make_cache(n_rows, 31, gpu)
     rng = np.random.default_rng(32)
@@ -84,12 +88,15 @@ def test_fp8_sparse_rows_and_pages(gpu):
                     np.sort(rng.choice(4096, 700, replace=False))]).astype(np.int32)
     counts = [700, 513]
     bits, qf = q_bf16(33, 2)
+    if q_f32:
+        qf = synth.normal(33, 5, 2 * 64 * 512).reshape(2, 64, 512) * 2.0
     sinks = sinks_for(34, 2)
     out = torch.zeros((2, 64, 512), dtype=torch.float32, device=gpu)
-    q = torch.from_numpy(bits.view(np.int16)).to(gpu).view(torch.bfloat16)
+    q = (torch.from_numpy(qf).to(gpu) if q_f32 else
+         torch.from_numpy(bits.view(np.int16)).to(gpu).view(torch.bfloat16))
     ops.flash_attn_decode_fp8(q, torch.from_numpy(sinks).to(gpu), out, cache, counts,
                               row_idx=torch.from_numpy(idx).to(gpu),
-                              page_table=torch.from_numpy(pt).to(gpu), page_rows=256)
+                              page_table=torch.from_numpy(pt).to(gpu), page_rows=256, exact_p=exact)
     torch.cuda.synchronize()
     for p in range(2):
         pos = idx[p, :counts[p]]

@@ -2519,12 +2519,15 @@ void carve(DecodeArgs &A, void *ws, const Plan &pl) {
 // producers have no registers left for a second P fragment).
 template <int kMode>
 void launch_ws(const DecodeArgs &A, const Plan &pl, hipStream_t st, const ds4hip_decode_opts &o) {
-    if (kMode == 0 && o.kernel != DS4HIP_DECODE_KERNEL_REGLOAD && !o.exact_p) {
-        hipLaunchKernelGGL((decode_flat_kernel<false, true>), dim3(pl.n_wg), dim3(512), 0, st, A);
-        return;
-    }
-    if (kMode == 1 && o.kernel != DS4HIP_DECODE_KERNEL_REGLOAD && !o.exact_p) {
-        hipLaunchKernelGGL((decode_flat_kernel<false, true, false, true>), dim3(pl.n_wg), dim3(512), 0, st, A);
+    if (kMode < 2 && o.kernel != DS4HIP_DECODE_KERNEL_REGLOAD) {
+        if (kMode == 0 && o.exact_p)
+            hipLaunchKernelGGL((decode_flat_kernel<true, true>), dim3(pl.n_wg), dim3(512), 0, st, A);
+        else if (kMode == 0)
+            hipLaunchKernelGGL((decode_flat_kernel<false, true>), dim3(pl.n_wg), dim3(512), 0, st, A);
+        else if (o.exact_p)
+            hipLaunchKernelGGL((decode_flat_kernel<true, true, false, true>), dim3(pl.n_wg), dim3(512), 0, st, A);
+        else
+            hipLaunchKernelGGL((decode_flat_kernel<false, true, false, true>), dim3(pl.n_wg), dim3(512), 0, st, A);
         return;
     }
     if (o.exact_p)

@@ -2414,6 +2414,95 @@ __global__ __launch_bounds__(128) void decode_merge_kernel(const DecodeArgs A) {
     *reinterpret_cast<float4_t *>(A.out + (long long)p * A.out_stride + h * kD + 4 * tid) = res;
 }
 
+// The merge for problems of many slots (a long problem split over many
+// workgroups): one block per (problem, head, half of the dims) combines the
+// partials with the sink. The per-slot scalars (problem id, running max, sum) are read with
+// vector loads, one slot per thread, so their latencies overlap; their scale
+// factors go through LDS. Each wave then accumulates its own quarter of the
+// slots (slot j to wave j mod 4, in slot order), thread t dims 4t..4t+3 of the
+// half, several slots' 16-byte loads in flight, and the four waves' sums are
+// added in wave order: a fixed order, so the result is deterministic.
+constexpr int kMergeThreads = 256;
+constexpr long long kMergeWideSlots = 8;   // chunks per problem above which the wide merge runs
+__global__ __launch_bounds__(kMergeThreads) void decode_merge_wide_kernel(const DecodeArgs A) {
+    __shared__ float s_sc[kMergeThreads];
+    __shared__ float s_red[kMergeThreads / 64];
+    __shared__ float4_t s_acc[3][64];
+    const int p = blockIdx.x;
+    const int h = blockIdx.y;
+    const int half = blockIdx.z;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const float sink = A.sinks[(long long)p * A.sinks_stride + h] * kLog2e;
+    const long long b0 = A.start[p], b1 = b0 + A.count[p];
+    long long s0 = 0, n_slot = 0;
+    if (b1 > b0) {
+        s0 = (b0 / A.chunk) * A.s_max;
+        n_slot = ((b1 - 1) / A.chunk) * A.s_max + A.s_max - s0;
+    }
+    auto block_reduce = [&](float v, bool is_max) {
+        for (int off = 32; off > 0; off >>= 1) {
+            const float o = __shfl_xor(v, off);
+            v = is_max ? fmaxf(v, o) : v + o;
+        }
+        __syncthreads();   // s_red's previous readers are done
+        if (lane == 0) s_red[wave] = v;
+        __syncthreads();
+        return is_max ? fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]))
+                      : (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+    };
+    float mx = sink;
+    int bad = 0;
+    for (long long i = tid; i < n_slot; i += kMergeThreads) {
+        const long long slot = s0 + i;
+        const float m = A.ws_ml[slot * 2 * kH + h];
+        const int pr = A.ws_prob[slot];
+        if ((pr & ~kBadSlot) == p) {
+            mx = fmaxf(mx, m);
+            bad |= pr & kBadSlot;
+        }
+    }
+    bad = __syncthreads_or(bad);
+    mx = block_reduce(mx, true);
+    float den_part = 0.0f;
+    float4_t acc = float4_t{0, 0, 0, 0};
+    const float *o_base = A.ws_o + h * kD + half * (kD / 2) + 4 * lane;
+    for (long long base = 0; base < n_slot; base += kMergeThreads) {
+        float sc = 0.0f;
+        if (base + tid < n_slot) {
+            const long long slot = s0 + base + tid;
+            const float m = A.ws_ml[slot * 2 * kH + h];
+            const float l = A.ws_ml[slot * 2 * kH + kH + h];
+            if ((A.ws_prob[slot] & ~kBadSlot) == p && m != -INFINITY) {
+                sc = __builtin_amdgcn_exp2f(m - mx);
+                den_part += l * sc;
+            }
+        }
+        __syncthreads();   // the previous batch's readers are done
+        s_sc[tid] = sc;
+        __syncthreads();
+        const int nb = (int)min((long long)kMergeThreads, n_slot - base);
+        const float *ob = o_base + (s0 + base) * (kH * kD);
+#pragma unroll 8
+        for (int jj = wave; jj < nb; jj += 4) {
+            const float c = s_sc[jj];
+            const float4_t o = *reinterpret_cast<const float4_t *>(ob + (long long)jj * (kH * kD));
+            acc = c != 0.0f ? acc + o * c : acc;   // a select: unused slots may hold anything
+        }
+    }
+    const float den = block_reduce(den_part, false) + __builtin_amdgcn_exp2f(sink - mx);
+    if (wave > 0) s_acc[wave - 1][lane] = acc;
+    __syncthreads();
+    if (wave == 0) {
+        acc = ((acc + s_acc[0][lane]) + s_acc[1][lane]) + s_acc[2][lane];
+        // a problem that met a row outside the cache gets NaN, never a plausible value
+        const float4_t res = bad ? float4_t{NAN, NAN, NAN, NAN} : acc * (1.0f / den);
+        *reinterpret_cast<float4_t *>(A.out + (long long)p * A.out_stride + h * kD + half * (kD / 2) +
+                                      4 * lane) = res;
+    }
+}
+
 // ---- host-side planning -----------------------------------------------------------
 
 int g_num_cus = 0;
@@ -2575,7 +2664,22 @@ int launch(DecodeArgs &A, const Plan &pl, hipStream_t st, int phases = 3,
         if (e) return e;
     }
     if (phases & 2)
-        hipLaunchKernelGGL(decode_merge_kernel, dim3(A.n_prob, kH), dim3(128), 0, st, A);
+    {
+        // problems of few slots (a long batch of problems, e.g. 43 layers over
+        // 256 workgroups) merge with one block per (problem, head); a problem
+        // split over many workgroups takes the wide merge, whose four waves
+        // per half of the dims keep more slots' loads in flight
+        long long max_slots = 0;   // chunks a problem spans
+        for (int p = 0; p < A.n_prob; ++p) {
+            const long long b0 = A.start[p], b1 = b0 + A.count[p];
+            if (b1 > b0)
+                max_slots = std::max(max_slots, (b1 - 1) / A.chunk - b0 / A.chunk + 1);
+        }
+        if (max_slots > kMergeWideSlots)
+            hipLaunchKernelGGL(decode_merge_wide_kernel, dim3(A.n_prob, kH, 2), dim3(kMergeThreads), 0, st, A);
+        else
+            hipLaunchKernelGGL(decode_merge_kernel, dim3(A.n_prob, kH), dim3(128), 0, st, A);
+    }
     return hip_status(hipGetLastError());
 }
 

@@ -645,10 +645,16 @@ int launch_scores(const float *q, const float *w, const void *keys, int kind, in
 
 // scores + selection. mask and/or pos_out; n_recent trailing positions are
 // always selected and take part in no comparison.
+size_t select_large_scratch_words(int n_comp);
 size_t select_scratch_bytes(int n_comp) {
     const size_t chunks = (size_t)(n_comp > 0 ? n_comp : 1) / kChunk + 1;
-    return (3 * kBins + 2 * chunks) * sizeof(unsigned);
+    return std::max((3 * kBins + 2 * chunks), select_large_scratch_words(n_comp)) * sizeof(unsigned);
 }
+
+int launch_select_large(const float *scores, int n_comp, int n_cand, unsigned need0, unsigned *scratch,
+                        int32_t *mask, int32_t *pos_out, hipStream_t st);
+size_t select_large_scratch_words(int n_comp);
+constexpr int kLargeSelectMax = 262144;   // candidates of the two-launch select (its LDS bitmaps)
 
 int score_select(const float *q, const float *w, const void *keys, int kind, int n_comp,
                  int n_head, int head_dim, int top_k, int n_recent, float *scores,
@@ -684,6 +690,16 @@ int score_select(const float *q, const float *w, const void *keys, int kind, int
     unsigned *hists = scratch;
     unsigned *chunk_gt = scratch + 3 * kBins;
     unsigned *chunk_eq = chunk_gt + n_chunks;
+    // up to kLargeSelectMax candidates (16-byte aligned scores): the level-1
+    // histogram in the score kernel, then the two-launch select
+    if (n_cand <= kLargeSelectMax && (reinterpret_cast<uintptr_t>(scores) & 15) == 0) {
+        // level-1 histogram, list counter and bitmap start at zero
+        const int nz = kBins + 1 + (n_cand + 31) / 32;
+        hipLaunchKernelGGL(zero_u32_kernel, dim3((nz + 255) / 256), dim3(256), 0, st, scratch, nz);
+        int rc = launch_scores(q, w, keys, kind, n_comp, n_head, head_dim, scores, scratch, n_cand, st);
+        if (rc) return rc;
+        return launch_select_large(scores, n_comp, n_cand, need0, scratch, mask, pos_out, st);
+    }
     hipLaunchKernelGGL(zero_u32_kernel, dim3(24), dim3(256), 0, st, hists, 3 * kBins);
     int rc = launch_scores(q, w, keys, kind, n_comp, n_head, head_dim, scores, hists, n_cand, st);
     if (rc) return rc;
@@ -1038,6 +1054,224 @@ __global__ __launch_bounds__(1024) void select_batch_kernel(const BatchArgs A) {
         }
     }
     for (int i = t; i < recent; i += 1024) out[tot_sel + i] = n_cand + i;
+}
+
+// ---- two-launch selection of a long candidate list ----------------------------------------
+//
+// After the score kernel's level-1 histogram (key bits 31..21):
+//  compact (one workgroup per 1024 candidates, coalesced): keys above the
+//    level-1 threshold bin set their bit in a global bitmap; keys in the bin
+//    are appended, unordered, to a global list of (key, index) pairs (one
+//    counter add per wave);
+//  finish (one 1024-thread workgroup): levels 2 (bits 20..10) and 3 (bits
+//    9..0) of the radix select over the listed keys give the exact threshold
+//    key T and the number of ties at T to take; listed keys above T join the
+//    bitmap (copied to LDS), keys equal to T go to a tie bitmap whose
+//    popcount scan ranks them by index, and the need_eq lowest join too; a
+//    popcount scan of the bitmap writes the positions in ascending order (and
+//    / or the 0/1 mask), then the forced recent window.
+// Two launches instead of four, and the full score list is read once more
+// instead of three times. The list has room for every candidate, so a
+// threshold bin of any size is handled (a large one only costs list reads).
+constexpr int kLargeBits = 262144;   // candidates the finishing workgroup's LDS bitmaps cover
+constexpr int kFinishPairs = 8192;   // listed keys it copies to LDS (a longer list is read from memory)
+
+__global__ __launch_bounds__(256) void compact_kernel(const float *__restrict__ scores, int n_cand,
+                                                      unsigned need0, const unsigned *__restrict__ hist1,
+                                                      unsigned *__restrict__ bitmap,
+                                                      unsigned *__restrict__ list_n,
+                                                      unsigned *__restrict__ list_key,
+                                                      int *__restrict__ list_idx) {
+    __shared__ unsigned scratch[256];
+    __shared__ unsigned s_bin, s_above;
+    if (need0 == 0) return;
+    find_bin(hist1, kBins, need0, &s_bin, &s_above, scratch);
+    const unsigned b1 = s_bin;
+    const int c = blockIdx.x * kChunk + 4 * threadIdx.x;
+    unsigned k[4];
+    if (c + 3 < n_cand) {
+        const float4_t v = *reinterpret_cast<const float4_t *>(scores + c);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) k[j] = ord_key(v[j]);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) k[j] = c + j < n_cand ? ord_key(scores[c + j]) : 0;
+    }
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    // in-bin keys: per-wave ballots, one counter add per workgroup (a counter
+    // add per wave would serialize ~1000 same-address atomics)
+    __shared__ unsigned s_wcnt[4][4], s_base;
+    unsigned long long bal[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const bool live = c + j < n_cand;
+        const unsigned hb = k[j] >> 21;
+        if (live && hb > b1) atomicOr(&bitmap[(c + j) >> 5], 1u << ((c + j) & 31));
+        bal[j] = __ballot(live && hb == b1);
+        if (lane == 0) s_wcnt[wv][j] = (unsigned)__popcll(bal[j]);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned tot = 0;
+        for (int w = 0; w < 4; ++w)
+            for (int j = 0; j < 4; ++j) {
+                const unsigned n = s_wcnt[w][j];
+                s_wcnt[w][j] = tot;   // exclusive prefix in (wave, j) order
+                tot += n;
+            }
+        s_base = tot ? atomicAdd(list_n, tot) : 0;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        if ((bal[j] >> lane) & 1) {
+            const unsigned o = s_base + s_wcnt[wv][j] + (unsigned)__popcll(bal[j] & ((1ULL << lane) - 1));
+            list_key[o] = k[j];
+            list_idx[o] = c + j;
+        }
+}
+
+__global__ __launch_bounds__(1024) void finish_kernel(int n_comp, int n_cand, unsigned need0,
+                                                      const unsigned *__restrict__ hist1,
+                                                      const unsigned *__restrict__ bitmap,
+                                                      const unsigned *__restrict__ list_n,
+                                                      const unsigned *__restrict__ list_key,
+                                                      const int *__restrict__ list_idx,
+                                                      int32_t *__restrict__ mask,
+                                                      int32_t *__restrict__ pos_out) {
+    __shared__ unsigned sel[kLargeBits / 32];
+    __shared__ unsigned tie[kLargeBits / 32];
+    __shared__ unsigned hist[kBins];
+    __shared__ unsigned lkey[kFinishPairs];
+    __shared__ int lidx[kFinishPairs];
+    __shared__ unsigned wsum[16];
+    __shared__ unsigned s_bin, s_above;
+    const int t = threadIdx.x;
+    const int n_words = (n_cand + 31) / 32;
+    // the independent loads first (bitmap, level-1 histogram, list length),
+    // so their latencies overlap; then the list, once
+    const unsigned np = need0 ? *list_n : 0;
+    if (need0)
+        for (int i = t; i < kBins; i += 1024) hist[i] = hist1[i];
+    for (int i = t; i < n_words; i += 1024) {
+        sel[i] = need0 ? bitmap[i] : 0;
+        tie[i] = 0;
+    }
+    const bool in_lds = np <= (unsigned)kFinishPairs;
+    if (in_lds)
+        for (unsigned i = t; i < np; i += 1024) {
+            lkey[i] = list_key[i];
+            lidx[i] = list_idx[i];
+        }
+    __syncthreads();
+    const unsigned *keys_l = in_lds ? lkey : list_key;
+    const int *idx_l = in_lds ? lidx : list_idx;
+    // the bin of histogram h (nb bins, high bin = larger keys) that holds the
+    // need-th largest key, and the count above it (thread t owns nb / 1024
+    // bins from the top)
+    auto find = [&](const unsigned *h, int nb, unsigned need) {
+        const int per = nb / 1024;
+        unsigned v = 0;
+        for (int i = 0; i < per; ++i) v += h[nb - 1 - t * per - i];
+        unsigned tot;
+        const unsigned ex = scan1024_excl(v, wsum, &tot);
+        if (ex < need && ex + v >= need) {
+            unsigned run = ex;
+            int b = nb - 1 - t * per;
+            for (int i = 0; i < per - 1; ++i, --b) {
+                if (run + h[b] >= need) break;
+                run += h[b];
+            }
+            s_bin = (unsigned)b;
+            s_above = run;
+        }
+        __syncthreads();
+    };
+    const int wpt = (n_words + 1023) / 1024;   // thread t owns words [t * wpt, (t + 1) * wpt)
+    const int w0 = t * wpt, w1 = min(w0 + wpt, n_words);
+    if (need0 > 0) {
+        find(hist, kBins, need0);
+        const unsigned b1 = s_bin;
+        unsigned need = need0 - s_above;
+        unsigned pref = b1 << 21, pmask = 0xFFE00000u;
+        for (int lvl = 0; lvl < 2; ++lvl) {
+            const int shift = lvl == 0 ? 10 : 0, nb = lvl == 0 ? kBins : 1024;
+            __syncthreads();   // the previous level's readers of s_bin are done
+            for (int i = t; i < nb; i += 1024) hist[i] = 0;
+            __syncthreads();
+            for (unsigned i = t; i < np; i += 1024) {
+                const unsigned k = keys_l[i];
+                if ((k & pmask) == pref) atomicAdd(&hist[(k >> shift) & (nb - 1)], 1u);
+            }
+            __syncthreads();
+            find(hist, nb, need);
+            pref |= s_bin << shift;
+            pmask |= (unsigned)(nb - 1) << shift;
+            need -= s_above;
+        }
+        const unsigned T = pref, need_eq = need;
+        for (unsigned i = t; i < np; i += 1024) {
+            const unsigned k = keys_l[i];
+            const int c = idx_l[i];
+            if (k > T) atomicOr(&sel[c >> 5], 1u << (c & 31));
+            else if (k == T) atomicOr(&tie[c >> 5], 1u << (c & 31));
+        }
+        __syncthreads();
+        // the need_eq ties of lowest index
+        unsigned nt = 0;
+        for (int w = w0; w < w1; ++w) nt += __popc(tie[w]);
+        unsigned tot;
+        unsigned rank = scan1024_excl(nt, wsum, &tot);
+        for (int w = w0; w < w1; ++w) {
+            unsigned bits = tie[w], add = 0;
+            while (bits && rank < need_eq) {
+                const unsigned low = bits & (0u - bits);
+                add |= low;
+                bits ^= low;
+                ++rank;
+            }
+            sel[w] |= add;   // this thread's words only
+        }
+        __syncthreads();
+    }
+    unsigned ns = 0;
+    for (int w = w0; w < w1; ++w) ns += __popc(sel[w]);
+    unsigned tot;
+    unsigned o = scan1024_excl(ns, wsum, &tot);
+    for (int w = w0; w < w1; ++w) {
+        unsigned bits = sel[w];
+        if (mask)
+            for (int b = 0; b < 32 && w * 32 + b < n_cand; ++b) mask[w * 32 + b] = (bits >> b) & 1u;
+        if (pos_out)
+            while (bits) {
+                const int b = __builtin_ctz(bits);
+                bits &= bits - 1;
+                pos_out[o++] = w * 32 + b;
+            }
+    }
+    for (int i = t; i < n_comp - n_cand; i += 1024) {
+        if (pos_out) pos_out[need0 + i] = n_cand + i;
+        if (mask) mask[n_cand + i] = 1;
+    }
+}
+
+// scratch: [hist1 kBins][list_n 1][bitmap words][list keys n_cand][list idx n_cand] (u32)
+size_t select_large_scratch_words(int n_comp) {
+    const size_t n = (size_t)(n_comp > 0 ? n_comp : 1);
+    return kBins + 1 + (n + 31) / 32 + 2 * n;
+}
+
+int launch_select_large(const float *scores, int n_comp, int n_cand, unsigned need0, unsigned *scratch,
+                        int32_t *mask, int32_t *pos_out, hipStream_t st) {
+    unsigned *hist1 = scratch, *list_n = scratch + kBins, *bitmap = list_n + 1;
+    const int n_words = (n_cand + 31) / 32;
+    unsigned *list_key = bitmap + n_words;
+    int *list_idx = reinterpret_cast<int *>(list_key + n_cand);
+    hipLaunchKernelGGL(compact_kernel, dim3((n_cand + kChunk - 1) / kChunk), dim3(256), 0, st, scores, n_cand,
+                       need0, hist1, bitmap, list_n, list_key, list_idx);
+    hipLaunchKernelGGL(finish_kernel, dim3(1), dim3(1024), 0, st, n_comp, n_cand, need0, hist1, bitmap, list_n,
+                       list_key, list_idx, mask, pos_out);
+    return hip_status(hipGetLastError());
 }
 
 }  // namespace

@@ -170,6 +170,54 @@ def test_indexer_positions_with_ties_and_recent(gpu):
     assert m.sum() == top_k and np.array_equal(np.nonzero(m)[0], ref_p)
 
 
+@pytest.mark.parametrize("case", ["spread", "bin_overflow", "zero_ties", "mask_only"])
+def test_indexer_large_select_edges(gpu, case):
+    """The one-workgroup selection of long candidate lists (more than 16384
+    candidates) with designed scores: one head, q = e_0, w = 1 and fp32 keys
+    give score = relu(key[0]) exactly. spread: few ties; bin_overflow: 40000
+    equal keys (the threshold bin holds more than the 8192 listed keys, so
+    the rescans run); zero_ties: half the keys relu to 0 and the selection
+    reaches into those ties; mask_only: the 0/1 mask alone. Positions and
+    mask bit-exact against the oracle's (score desc, index asc) rule."""
+    n_head, hd = 1, 128
+    rng = np.random.default_rng(11)
+    n_comp, top_k, recent = {"spread": (200000, 2048, 128), "bin_overflow": (40000, 1000, 16),
+                             "zero_ties": (50000, 26000, 64), "mask_only": (30000, 700, 0)}[case]
+    k = np.zeros((n_comp, hd), np.float32)
+    if case == "spread":
+        k[:, 0] = np.round(rng.standard_normal(n_comp) * 64) / 64   # ~400 levels: ties too
+    elif case == "bin_overflow":
+        k[:, 0] = 1.0
+    elif case == "zero_ties":
+        k[:, 0] = rng.standard_normal(n_comp)
+    else:
+        k[:, 0] = rng.standard_normal(n_comp)
+    k[:, 1:] = rng.standard_normal((n_comp, hd - 1)).astype(np.float32)
+    q = np.zeros(hd, np.float32)
+    q[0] = 1.0
+    w = np.ones(1, np.float32)
+    ref_s = np.zeros(n_comp, np.float32)
+    O.lib().orc_indexer_scores(P(q), P(w), P(k), C.c_int(0), C.c_int(n_comp), C.c_int(n_head),
+                               C.c_int(hd), P(ref_s))
+    assert np.array_equal(ref_s, np.maximum(k[:, 0], 0))
+    mask = torch.empty(n_comp, dtype=torch.int32, device=gpu)
+    if case == "mask_only":
+        ref_m = np.zeros(n_comp, np.int32)
+        O.lib().orc_topk_mask(P(ref_s), C.c_int(n_comp), C.c_int(top_k), P(ref_m))
+        ops.indexer_topk_positions(t(q, gpu), t(w, gpu), t(k, gpu), top_k, 0, mask=mask,
+                                   positions=torch.empty(top_k, dtype=torch.int32, device=gpu))
+        torch.cuda.synchronize()
+        assert np.array_equal(mask.cpu().numpy(), ref_m)
+        return
+    ref_p = np.zeros(top_k, np.int32)
+    O.lib().orc_topk_positions(P(ref_s), C.c_int(n_comp), C.c_int(top_k), C.c_int(recent), P(ref_p))
+    pos, _, scores = ops.indexer_topk_positions(t(q, gpu), t(w, gpu), t(k, gpu), top_k, recent, mask=mask)
+    torch.cuda.synchronize()
+    assert np.array_equal(scores.cpu().numpy().view(np.uint32), ref_s.view(np.uint32))
+    assert np.array_equal(pos.cpu().numpy(), ref_p)
+    assert np.array_equal(np.nonzero(mask.cpu().numpy())[0], ref_p)
+
+
 def test_short_circuit_and_scale(gpu):
     out = torch.zeros(100, dtype=torch.int32, device=gpu)
     ops.launch_indexer_allowed_short_circuit_i32(out, 100, 512)

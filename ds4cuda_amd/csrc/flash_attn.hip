@@ -1639,7 +1639,10 @@ __device__ inline float xmax_16_32_raw(float v) {
 // copies from an SGPR base). The score scale log2(e)/sqrt(d) stays on S after
 // the MFMA: folded into Q it would make the bf16 values inexact in the two
 // E4M3 parts (a bf16 value's 8 significant bits split exactly into hi + lo).
-template <bool kPLo, bool kLean, bool kQf32 = false, bool kGather = false>
+// kGather: 0 direct rows; 1 physical rows from the phys array (phys_kernel
+// ran: pages and / or row lists); 2 the int32 row list itself (no pages: row
+// = the problem's base + entry, clamped into the cache)
+template <bool kPLo, bool kLean, bool kQf32 = false, int kGather = 0>
 __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A) {
     static_assert(kLean || !kQf32, "fp32 Q takes the lean form");
     // Q parts on the scaled FP8 MFMA: a bf16 Q (8 significant bits) fits in
@@ -1686,7 +1689,8 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
         const long long slot = (long long)blockIdx.x * A.s_max + slot_s;
         const long long seg_r0 = s_rowbase[p] + r0;
         const int seg_last = (int)(r1 - 1 - r0);
-        if constexpr (kGather) scan_segment_rows(A, true, p, g0, seg_end, r0, r1, 0, slot_s, s_bad);
+        if constexpr (kGather != 0)
+            scan_segment_rows(A, kGather == 1, p, g0, seg_end, r0, r1, s_rowbase[p], slot_s, s_bad);
         // ---- the producers: QK^T on the scaled FP8 MFMA and the softmax, one
         // interval apart (interval u: QK(u) with softmax(u - 1) in its issue slots)
         auto produce = [&]() {
@@ -2066,13 +2070,23 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
                                                          st + 1024 * n, 16, 0, 0);
                 }
                 if (c == 0) {
-                    const long long gi = min(g0 + (long long)kTile * (u + kFsLead), A.total);
                     int ln2 = lane;
                     asm volatile("" : "+v"(ln2));
-                    __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t *>(A.phys + gi) + 4 * ln2,
-                                                     st + kFsPhysOff, 4, 0, 0);
+                    if constexpr (kGather == 1) {
+                        const long long gi = min(g0 + (long long)kTile * (u + kFsLead), A.total);
+                        __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t *>(A.phys + gi) + 4 * ln2,
+                                                         st + kFsPhysOff, 4, 0, 0);
+                    } else {
+                        // 32 int32 entries (lanes 32..63 repeat lanes 0..31), clamped
+                        // to the segment's last row: no entry past the problem's list
+                        const int e = min(kTile * (u + kFsLead) + (ln2 & 31), seg_last);
+                        __builtin_amdgcn_global_load_lds(
+                            reinterpret_cast<const uint8_t *>(A.row_idx + (long long)p * A.row_idx_stride + r0 + e),
+                            st + kFsPhysOff, 4, 0, 0);
+                    }
                 }
             };
+            const long long seg_base = s_rowbase[p];
             auto issue = [&](int u) {
                 uint8_t *st = stage[u % kFsStages];
                 if constexpr (kGather) {
@@ -2082,15 +2096,28 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
                     const uint32_t ph = lds_addr(stage[(u - kFsLead) % kFsStages] + kFsPhysOff);
                     long long rr[5];
                     const int last = seg_last - kTile * u;
+                    if constexpr (kGather == 1) {
 #pragma unroll
-                    for (int k = 0; k < 5; ++k) {
-                        const int e = max(min(c_row[k], last), 0);
-                        asm volatile("ds_read_b64 %0, %1" : "=v"(rr[k]) : "v"(ph + 8 * e));
+                        for (int k = 0; k < 5; ++k) {
+                            const int e = max(min(c_row[k], last), 0);
+                            asm volatile("ds_read_b64 %0, %1" : "=v"(rr[k]) : "v"(ph + 8 * e));
+                        }
+                        asm volatile("s_waitcnt lgkmcnt(0)"
+                                     : "+v"(rr[0]), "+v"(rr[1]), "+v"(rr[2]), "+v"(rr[3]), "+v"(rr[4]) :: "memory");
+#pragma unroll
+                        for (int k = 0; k < 5; ++k) rr[k] = unmark_row(rr[k]);
+                    } else {
+                        int ix[5];
+#pragma unroll
+                        for (int k = 0; k < 5; ++k) {
+                            const int e = max(min(c_row[k], last), 0);
+                            asm volatile("ds_read_b32 %0, %1" : "=v"(ix[k]) : "v"(ph + 4 * e));
+                        }
+                        asm volatile("s_waitcnt lgkmcnt(0)"
+                                     : "+v"(ix[0]), "+v"(ix[1]), "+v"(ix[2]), "+v"(ix[3]), "+v"(ix[4]) :: "memory");
+#pragma unroll
+                        for (int k = 0; k < 5; ++k) rr[k] = clamp_row(seg_base + ix[k], A.n_cache_rows);
                     }
-                    asm volatile("s_waitcnt lgkmcnt(0)"
-                                 : "+v"(rr[0]), "+v"(rr[1]), "+v"(rr[2]), "+v"(rr[3]), "+v"(rr[4]) :: "memory");
-#pragma unroll
-                    for (int k = 0; k < 5; ++k) rr[k] = unmark_row(rr[k]);
                     issue_rows(u, rr);
                     return;
                 }
@@ -2268,14 +2295,21 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
                     asm volatile("s_waitcnt vmcnt(%0)" :: "n"(5 * (kFsLead - 1)) : "memory");
             };
             // prologue: tiles 0 .. kFsLead - 1; tile 0 lands before the first barrier
-            if constexpr (kGather) {
-                // their rows straight from the phys array, all loaded before any copy
+            if constexpr (kGather != 0) {
+                // their rows straight from the phys array (or the row list), all
+                // loaded before any copy
                 long long rr[kFsLead][5];
 #pragma unroll
                 for (int u = 0; u < kFsLead; ++u)
 #pragma unroll
-                    for (int k = 0; k < 5; ++k)
-                        rr[u][k] = unmark_row(A.phys[g0 + min(kTile * u + c_row[k], seg_last)]);
+                    for (int k = 0; k < 5; ++k) {
+                        const int e = min(kTile * u + c_row[k], seg_last);
+                        if constexpr (kGather == 1)
+                            rr[u][k] = unmark_row(A.phys[g0 + e]);
+                        else
+                            rr[u][k] = clamp_row(seg_base + A.row_idx[(long long)p * A.row_idx_stride + r0 + e],
+                                                 A.n_cache_rows);
+                    }
 #pragma unroll
                 for (int u = 0; u < kFsLead; ++u) issue_rows(u, rr[u]);
             } else {
@@ -2614,9 +2648,9 @@ void launch_ws(const DecodeArgs &A, const Plan &pl, hipStream_t st, const ds4hip
         else if (kMode == 0)
             hipLaunchKernelGGL((decode_flat_kernel<false, true>), dim3(pl.n_wg), dim3(512), 0, st, A);
         else if (o.exact_p)
-            hipLaunchKernelGGL((decode_flat_kernel<true, true, false, true>), dim3(pl.n_wg), dim3(512), 0, st, A);
+            hipLaunchKernelGGL((decode_flat_kernel<true, true, false, 1>), dim3(pl.n_wg), dim3(512), 0, st, A);
         else
-            hipLaunchKernelGGL((decode_flat_kernel<false, true, false, true>), dim3(pl.n_wg), dim3(512), 0, st, A);
+            hipLaunchKernelGGL((decode_flat_kernel<false, true, false, 1>), dim3(pl.n_wg), dim3(512), 0, st, A);
         return;
     }
     if (o.exact_p)
@@ -2632,8 +2666,11 @@ int launch(DecodeArgs &A, const Plan &pl, hipStream_t st, int phases = 3,
     A.s_max = pl.s_max;
     A.kq_log2 = kLog2e / sqrtf((float)kD);
     if ((phases & 1) && pl.n_wg > 0) {
-        // bf16 Q with position lists but no pages: the kernel resolves the rows
-        const bool idx_only = kFp8 && !kQf32 && A.row_idx && !A.page_table;
+        // position lists without pages: the kernel resolves the rows itself
+        // (bf16 Q: decode_ws_kernel<2>; fp32 Q: the flat kernel's list form);
+        // the fp32 register kernel needs the phys pass for them
+        const bool flat_f32 = kQf32 && o.kernel != DS4HIP_DECODE_KERNEL_REGLOAD;
+        const bool idx_only = kFp8 && A.row_idx && !A.page_table && (!kQf32 || flat_f32);
         if (kFp8 && A.phys && !idx_only) {
             const long long n = A.total + kTile;
             hipLaunchKernelGGL(phys_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, A);
@@ -2649,10 +2686,12 @@ int launch(DecodeArgs &A, const Plan &pl, hipStream_t st, int phases = 3,
         else if (kFp8 && o.kernel != DS4HIP_DECODE_KERNEL_REGLOAD) {
             // fp32 Q: the flat-stage kernel with Q in three FP8 parts and, as
             // every fp32-Q decode, P as f16 hi + lo
-            if (A.phys)
-                hipLaunchKernelGGL((decode_flat_kernel<true, true, true, true>), dim3(pl.n_wg), dim3(512), 0, st, A);
+            if (idx_only)
+                hipLaunchKernelGGL((decode_flat_kernel<true, true, true, 2>), dim3(pl.n_wg), dim3(512), 0, st, A);
+            else if (A.phys)
+                hipLaunchKernelGGL((decode_flat_kernel<true, true, true, 1>), dim3(pl.n_wg), dim3(512), 0, st, A);
             else
-                hipLaunchKernelGGL((decode_flat_kernel<true, true, true>), dim3(pl.n_wg), dim3(512), 0, st, A);
+                hipLaunchKernelGGL((decode_flat_kernel<true, true, true, 0>), dim3(pl.n_wg), dim3(512), 0, st, A);
         }
         else if (kFp8)
             hipLaunchKernelGGL(decode_fp8_kernel<kQf32>, dim3(pl.n_wg), dim3(256), 0, st, A);

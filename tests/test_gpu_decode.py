@@ -74,11 +74,13 @@ def test_fp8_multi_problem_layers_and_fp32_q(gpu):
             check(got[p], ref)
 
 
+@pytest.mark.parametrize("paged", [True, False])
 @pytest.mark.parametrize("q_f32,exact", [(False, False), (False, True), (True, False), (True, True)])
-def test_fp8_sparse_rows_and_pages(gpu, q_f32, exact):
-    """Gathered rows through a page table: the flat-stage kernel with its rows
-    riding in the copy stream (default), or the register kernels (exact_p),
-    for bf16 and fp32 Q."""
+def test_fp8_sparse_rows_and_pages(gpu, q_f32, exact, paged):
+    """Gathered rows through a page table (the phys pass, then the flat-stage
+    kernel with the rows riding in its copy stream) or a plain position list
+    (fp32 Q: the flat kernel reads the list itself; bf16 Q: the register
+    kernel does), for bf16 and fp32 Q and both P forms."""
     n_rows = 4096
     cache, (codes, sexp, tail) = make_cache(n_rows, 31, gpu)
     rng = np.random.default_rng(32)
@@ -96,11 +98,12 @@ def test_fp8_sparse_rows_and_pages(gpu, q_f32, exact):
          torch.from_numpy(bits.view(np.int16)).to(gpu).view(torch.bfloat16))
     ops.flash_attn_decode_fp8(q, torch.from_numpy(sinks).to(gpu), out, cache, counts,
                               row_idx=torch.from_numpy(idx).to(gpu),
-                              page_table=torch.from_numpy(pt).to(gpu), page_rows=256, exact_p=exact)
+                              page_table=torch.from_numpy(pt).to(gpu) if paged else None, page_rows=256,
+                              exact_p=exact)
     torch.cuda.synchronize()
     for p in range(2):
         pos = idx[p, :counts[p]]
-        phys = pt[p][pos // 256] * 256 + pos % 256
+        phys = pt[p][pos // 256] * 256 + pos % 256 if paged else pos
         ref = O.attn_decode_fp8(qf[p], codes, sexp, tail, phys, sinks[p])
         check(out[p].cpu().numpy(), ref)
 

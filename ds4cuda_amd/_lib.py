@@ -39,6 +39,10 @@ SIGNATURES: dict[str, list] = {
     "ds4hip_tail_rope_yarn_f32": [_vp, _vp, _i, _i, _i, _i, _i, _vp],
     "ds4hip_tail_rope_yarn_inverse_f32": [_vp, _vp, _i, _i, _i, _i, _i, _vp],
     "ds4hip_mul_mv_f16_f32": [_vp, _vp, _vp, _i, _i, _vp],
+    "ds4hip_mul_mv_f16_scaled_f32": [_vp, _vp, _vp, _i, _i, C.c_float, _vp],
+    "ds4hip_mul_mv_f16_rope_f32": [_vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp],
+    "ds4hip_attn_out_decode_workspace_bytes": [_i, _i, _i, _i],
+    "ds4hip_attn_out_decode_f32": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _sz, _vp],
     "ds4hip_mul_mv_q8_0_q8_0_grouped_f32": [_vp, _vp, _vp, _i, _i, _i, _vp],
     "ds4hip_mul_mv_q8_0_q8_0_grouped_f32_prealloc": [_vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp],
     "ds4hip_mul_mv_q8_0_q8_0_f32_prealloc": [_vp, _vp, _vp, _i, _i, _vp, _vp, _vp],
@@ -98,7 +102,8 @@ RESTYPES = {"ds4hip_indexer_select_scratch_bytes": C.c_size_t,
             "ds4hip_session_state_arena_bytes": C.c_size_t,
             "ds4hip_mul_mm_workspace_bytes": C.c_size_t,
             "ds4hip_compressor_batch_scratch_bytes": C.c_size_t,
-            "ds4hip_attn_qkv_decode_workspace_bytes": C.c_size_t}
+            "ds4hip_attn_qkv_decode_workspace_bytes": C.c_size_t,
+            "ds4hip_attn_out_decode_workspace_bytes": C.c_size_t}
 
 _lib = None
 

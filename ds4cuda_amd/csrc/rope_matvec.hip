@@ -140,10 +140,25 @@ constexpr int kMvMaxIn = 16384;
 // serves the four rows (wave_rows_dot). Lane-strided fp32 partial sums, then
 // the wave's butterfly, as cuda/router.cu:69-97 reduces a warp's lanes.
 constexpr int kMvRows = 4;
+// Epilogues (each the arithmetic of the separate launch it replaces, so the
+// results are bit-identical to that pair of launches):
+//   kMvPlain: y = W x;
+//   kMvScale: y = (W x) * scale (the indexer's head weights, then
+//             ds4hip_scale_inplace_f32);
+//   kMvRope:  y = W x, then the forward tail RoPE of every head of head_dim
+//             rows (the indexer query, then ds4hip_tail_rope_yarn_f32): a
+//             wave's four rows hold two whole pairs, rotated before the store.
+enum { kMvPlain = 0, kMvScale = 1, kMvRope = 2 };
+struct MvEpilogue {
+    float scale = 1.0f;
+    int head_dim = 0, n_rot = 0, pos = 0;
+    RopeParams P{};
+};
+template <int kEpi>
 __global__ __launch_bounds__(256) void mv_f16_kernel(const uint16_t *__restrict__ w,
                                                      const float *__restrict__ x,
                                                      float *__restrict__ y, int out_dim,
-                                                     int in_dim) {
+                                                     int in_dim, MvEpilogue E) {
     extern __shared__ float xs[];
     for (int i = threadIdx.x; i < in_dim; i += 256) xs[i] = x[i];
     __syncthreads();
@@ -164,11 +179,22 @@ __global__ __launch_bounds__(256) void mv_f16_kernel(const uint16_t *__restrict_
             for (int i = lane; i < in_dim; i += 64) acc[r] = fmaf(f16_bits_to_f32(wr[i]), xs[i], acc[r]);
         }
     }
+    float a[kMvRows];
 #pragma unroll
-    for (int r = 0; r < kMvRows; ++r) {
-        const float a = wave_sum(acc[r]);
-        if (lane == 0 && row0 + r < out_dim) y[row0 + r] = a;
+    for (int r = 0; r < kMvRows; ++r) a[r] = wave_sum(acc[r]);
+    if (kEpi == kMvScale) {
+#pragma unroll
+        for (int r = 0; r < kMvRows; ++r) a[r] = a[r] * E.scale;
     }
+    if (kEpi == kMvRope) {
+        const int d0 = row0 % E.head_dim, n_nope = E.head_dim - E.n_rot;
+#pragma unroll
+        for (int r = 0; r < kMvRows; r += 2)
+            if (d0 + r >= n_nope) rope_pair(a[r], a[r + 1], (d0 + r - n_nope) / 2, E.pos, E.P, a[r], a[r + 1]);
+    }
+#pragma unroll
+    for (int r = 0; r < kMvRows; ++r)
+        if (lane == 0 && row0 + r < out_dim) y[row0 + r] = a[r];
 }
 
 // ---- Q8_0 activation quantization (cuda/attn_out.cu:119-145, dense_q8.cu) ---------------
@@ -270,6 +296,36 @@ __global__ __launch_bounds__(256) void mv_q8_kernel(const uint8_t *__restrict__ 
     }
     acc = wave_sum(acc);
     if (lane == 0) y[row] = acc;
+}
+
+// Steps 14 + 15a in one launch: the inverse tail RoPE of a head's attention
+// output and the Q8_0 quantization of the rotated row (one workgroup per
+// head, thread t on dims 2t and 2t + 1; a 32-dim block is 16 threads). The
+// rotation is rope_tail_kernel's and the quantization q8_quant_kernel's, in
+// registers, so the int8 values and scales equal those of the two launches.
+__global__ __launch_bounds__(256) void rope_q8_kernel(const float *__restrict__ x, int8_t *__restrict__ xq,
+                                                      float *__restrict__ xscale, int head_dim, int n_rot,
+                                                      int pos, RopeParams P) {
+    const int head = blockIdx.x;
+    const int t = threadIdx.x;
+    const int d = 2 * t;
+    if (d >= head_dim) return;
+    const float *xi = x + (size_t)head * head_dim;
+    float v0 = xi[d], v1 = xi[d + 1];
+    const int n_nope = head_dim - n_rot;
+    if (d >= n_nope) rope_pair(v0, v1, (d - n_nope) / 2, pos, P, v0, v1);
+    float a = fmaxf(fabsf(v0), fabsf(v1));
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, 16));
+    const float dq = a / 127.0f;
+    const float id = dq != 0.0f ? 1.0f / dq : 0.0f;
+    int q0 = (int)__builtin_rintf(v0 * id), q1 = (int)__builtin_rintf(v1 * id);
+    q0 = q0 > 127 ? 127 : (q0 < -128 ? -128 : q0);
+    q1 = q1 > 127 ? 127 : (q1 < -128 ? -128 : q1);
+    const size_t o = (size_t)head * head_dim + d;
+    xq[o] = (int8_t)q0;
+    xq[o + 1] = (int8_t)q1;
+    if ((t & 15) == 0) xscale[o / 32] = dq;
 }
 
 int launch_q8(const uint8_t *W, const float *x, float *y, int n_groups, int group_dim, int rank,
@@ -657,15 +713,46 @@ extern "C" int ds4hip_tail_rope_yarn_inverse_f32(const float *x_in, float *x_out
         launch_rope(x_in, x_out, n_heads, head_dim, n_rot, pos, il, true, (hipStream_t)stream));
 }
 
+namespace {
+template <int kEpi>
+int launch_mv_f16(const uint16_t *w_f16, const float *x_f32, float *y_f32, int out_dim, int in_dim,
+                  const MvEpilogue &E, hipStream_t st) {
+    if (!w_f16 || !x_f32 || !y_f32 || out_dim < 0 || in_dim <= 0 || in_dim > kMvMaxIn) return kEINVAL;
+    if (out_dim == 0) return 0;
+    hipLaunchKernelGGL(mv_f16_kernel<kEpi>, dim3((out_dim + 4 * kMvRows - 1) / (4 * kMvRows)), dim3(256),
+                       in_dim * sizeof(float), st, w_f16, x_f32, y_f32, out_dim, in_dim, E);
+    return hip_status(hipGetLastError());
+}
+}  // namespace
+
 extern "C" int ds4hip_mul_mv_f16_f32(const uint16_t *w_f16, const float *x_f32, float *y_f32,
                                      int out_dim, int in_dim, void *stream) {
-    if (!w_f16 || !x_f32 || !y_f32 || out_dim < 0 || in_dim <= 0 || in_dim > kMvMaxIn)
+    return ds4hip_set_last_error(
+        launch_mv_f16<kMvPlain>(w_f16, x_f32, y_f32, out_dim, in_dim, MvEpilogue{}, (hipStream_t)stream));
+}
+
+extern "C" int ds4hip_mul_mv_f16_scaled_f32(const uint16_t *w_f16, const float *x_f32, float *y_f32,
+                                            int out_dim, int in_dim, float scale, void *stream) {
+    MvEpilogue E;
+    E.scale = scale;
+    return ds4hip_set_last_error(
+        launch_mv_f16<kMvScale>(w_f16, x_f32, y_f32, out_dim, in_dim, E, (hipStream_t)stream));
+}
+
+extern "C" int ds4hip_mul_mv_f16_rope_f32(const uint16_t *w_f16, const float *x_f32, float *y_f32,
+                                          int n_heads, int head_dim, int n_rot, int pos, int il,
+                                          int in_dim, void *stream) {
+    // four rows per wave must hold whole pairs of one head's tail
+    if (n_heads <= 0 || head_dim <= 0 || head_dim % 4 || n_rot <= 0 || n_rot > 128 || n_rot % 4 ||
+        n_rot > head_dim)
         return ds4hip_set_last_error(kEINVAL);
-    if (out_dim == 0) return 0;
-    hipLaunchKernelGGL(mv_f16_kernel, dim3((out_dim + 4 * kMvRows - 1) / (4 * kMvRows)), dim3(256),
-                       in_dim * sizeof(float),
-                       (hipStream_t)stream, w_f16, x_f32, y_f32, out_dim, in_dim);
-    return ds4hip_set_last_error(hip_status(hipGetLastError()));
+    MvEpilogue E;
+    E.head_dim = head_dim;
+    E.n_rot = n_rot;
+    E.pos = pos;
+    E.P = rope_params(n_rot, il, false);
+    return ds4hip_set_last_error(launch_mv_f16<kMvRope>(w_f16, x_f32, y_f32, n_heads * head_dim, in_dim, E,
+                                                        (hipStream_t)stream));
 }
 
 extern "C" int ds4hip_mul_mv_q8_0_q8_0_grouped_f32_prealloc(const void *W, const float *x,
@@ -709,6 +796,66 @@ extern "C" int ds4hip_mul_mv_q8_0_q8_0_f32_prealloc(const void *W, const float *
     return ds4hip_set_last_error(launch_q8(static_cast<const uint8_t *>(W), x, y, 1, n_cols,
                                            n_rows, scratch_xq, scratch_xscale, false,
                                            (hipStream_t)stream));
+}
+
+// Steps 14-16 of one token (cuda/forward_layer.cu:1172-1210): inverse tail
+// RoPE + Q8_0 quantization (one launch), the grouped Q8_0 projection, the
+// quantization of its output and the dense Q8_0 projection. The same values as
+// ds4hip_tail_rope_yarn_inverse_f32 + the two _prealloc matvecs, one launch
+// fewer. Workspace: ds4hip_attn_out_decode_workspace_bytes.
+namespace {
+struct AttnOutWs {
+    int8_t *xq, *xq2;
+    float *xs, *low, *xs2;
+};
+size_t attn_out_ws(int n_head, int head_dim, int n_groups, int rank, char *base, AttnOutWs *w) {
+    auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    const size_t n = (size_t)n_head * head_dim, m = (size_t)n_groups * rank;
+    size_t off = 0;
+    const size_t o_xq = off; off += al(n);
+    const size_t o_xs = off; off += al(n / 32 * sizeof(float));
+    const size_t o_low = off; off += al(m * sizeof(float));
+    const size_t o_xq2 = off; off += al(m);
+    const size_t o_xs2 = off; off += al(m / 32 * sizeof(float));
+    if (w) {
+        w->xq = reinterpret_cast<int8_t *>(base + o_xq);
+        w->xs = reinterpret_cast<float *>(base + o_xs);
+        w->low = reinterpret_cast<float *>(base + o_low);
+        w->xq2 = reinterpret_cast<int8_t *>(base + o_xq2);
+        w->xs2 = reinterpret_cast<float *>(base + o_xs2);
+    }
+    return off;
+}
+}  // namespace
+
+extern "C" size_t ds4hip_attn_out_decode_workspace_bytes(int n_head, int head_dim, int n_groups, int rank) {
+    if (n_head <= 0 || head_dim <= 0 || n_groups <= 0 || rank <= 0) return 0;
+    return attn_out_ws(n_head, head_dim, n_groups, rank, nullptr, nullptr);
+}
+
+extern "C" int ds4hip_attn_out_decode_f32(const float *kqv, const void *w_out_a, const void *w_out_b,
+                                          float *out, int n_head, int head_dim, int n_rot, int pos, int il,
+                                          int n_groups, int rank, int out_dim, void *workspace,
+                                          size_t workspace_bytes, void *stream) {
+    if (!kqv || !w_out_a || !w_out_b || !out || !workspace || n_head <= 0 || head_dim <= 0 ||
+        head_dim % 32 || head_dim > 512 || n_rot <= 0 || n_rot > 128 || (n_rot & 1) || n_rot > head_dim ||
+        n_groups <= 0 || (n_head * head_dim) % n_groups || ((n_head * head_dim) / n_groups) % 32 || rank <= 0 ||
+        rank % 32 || (n_groups * rank) % 32 || out_dim <= 0 ||
+        workspace_bytes < attn_out_ws(n_head, head_dim, n_groups, rank, nullptr, nullptr))
+        return ds4hip_set_last_error(kEINVAL);
+    const hipStream_t st = (hipStream_t)stream;
+    AttnOutWs w;
+    attn_out_ws(n_head, head_dim, n_groups, rank, static_cast<char *>(workspace), &w);
+    const RopeParams P = rope_params(n_rot, il, true);
+    hipLaunchKernelGGL(rope_q8_kernel, dim3(n_head), dim3(256), 0, st, kqv, w.xq, w.xs, head_dim, n_rot, pos, P);
+    const int bpg = (n_head * head_dim) / n_groups / 32;
+    const int n_low = n_groups * rank;
+    hipLaunchKernelGGL(mv_q8_kernel, dim3((n_low + 3) / 4), dim3(256), 0, st,
+                       static_cast<const uint8_t *>(w_out_a), w.xq, w.xs, w.low, n_low, bpg, rank, 1);
+    int e = hip_status(hipGetLastError());
+    if (e) return ds4hip_set_last_error(e);
+    return ds4hip_set_last_error(launch_q8(static_cast<const uint8_t *>(w_out_b), w.low, out, 1, n_low, out_dim,
+                                           w.xq2, w.xs2, false, st));
 }
 
 extern "C" int ds4hip_mul_mm_bf16_f32(const uint16_t *W, const float *X, float *Y, int n_rows,

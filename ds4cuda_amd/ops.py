@@ -268,6 +268,51 @@ def launch_mul_mv_f16_f32(w_f16, x_f32, y_f32, out_dim, in_dim, stream=None):
          _stream(stream))
 
 
+def mul_mv_f16_scaled_f32(w_f16, x_f32, y_f32, out_dim, in_dim, scale, stream=None):
+    """launch_mul_mv_f16_f32 then every output times scale, in one launch."""
+    _check(w_f16, torch.int16, out_dim * in_dim, "w_f16")
+    _check(x_f32, torch.float32, in_dim, "x")
+    _check(y_f32, torch.float32, out_dim, "y")
+    call("ds4hip_mul_mv_f16_scaled_f32", _ptr(w_f16), _ptr(x_f32), _ptr(y_f32), out_dim, in_dim,
+         C.c_float(scale), _stream(stream))
+
+
+def mul_mv_f16_rope_f32(w_f16, x_f32, y_f32, n_heads, head_dim, n_rot, pos, il, in_dim, stream=None):
+    """launch_mul_mv_f16_f32 into n_heads rows of head_dim, then the forward
+    tail RoPE, in one launch."""
+    _check(w_f16, torch.int16, n_heads * head_dim * in_dim, "w_f16")
+    _check(x_f32, torch.float32, in_dim, "x")
+    _check(y_f32, torch.float32, n_heads * head_dim, "y")
+    call("ds4hip_mul_mv_f16_rope_f32", _ptr(w_f16), _ptr(x_f32), _ptr(y_f32), n_heads, head_dim, n_rot,
+         pos, il, in_dim, _stream(stream))
+
+
+def attn_out_decode_workspace(n_head, head_dim, n_groups, rank, device):
+    from ._lib import lib
+    nb = lib().ds4hip_attn_out_decode_workspace_bytes(n_head, head_dim, n_groups, rank)
+    return torch.empty(max(nb, 1), dtype=torch.uint8, device=device)
+
+
+def attn_out_decode_f32(kqv, w_out_a, w_out_b, out, n_head, head_dim, n_rot, pos, il, n_groups, rank,
+                        out_dim, workspace=None, stream=None):
+    """Steps 14-16: inverse tail RoPE of kqv [n_head, head_dim], the grouped
+    Q8_0 projection (n_groups x rank rows) and the dense Q8_0 projection to
+    out [out_dim]; the rotation and the first quantization in one launch."""
+    from ._lib import lib
+    group_dim = n_head * head_dim // n_groups
+    _check(kqv, torch.float32, n_head * head_dim, "kqv")
+    _check(w_out_a, torch.uint8, n_groups * rank * (group_dim // 32) * 34, "w_out_a")
+    _check(w_out_b, torch.uint8, out_dim * (n_groups * rank // 32) * 34, "w_out_b")
+    _check(out, torch.float32, out_dim, "out")
+    need = lib().ds4hip_attn_out_decode_workspace_bytes(n_head, head_dim, n_groups, rank)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=kqv.device)
+    _dev(workspace, "workspace", need)
+    call("ds4hip_attn_out_decode_f32", _ptr(kqv), _ptr(w_out_a), _ptr(w_out_b), _ptr(out), n_head, head_dim,
+         n_rot, pos, il, n_groups, rank, out_dim, _ptr(workspace), workspace.numel(), _stream(stream))
+    return workspace
+
+
 def launch_mul_mv_q8_0_q8_0_grouped_f32(W, x, y, n_groups, group_dim, rank, stream=None):
     _check(W, torch.uint8, n_groups * rank * (group_dim // 32) * 34, "W")
     _check(x, torch.float32, n_groups * group_dim, "x")

@@ -13,7 +13,9 @@ Per layer il at position pos:
       fp32 Q, with the layer's sinks;
   14. inverse tail RoPE;
   15. the grouped Q8_0 low-rank projection (8 groups x 4096 -> 1024);
-  16. the dense Q8_0 output projection (8192 -> 4096).
+  16. the dense Q8_0 output projection (8192 -> 4096)
+(Steps 14-16 through ds4hip_attn_out_decode_f32, the indexer query and head
+weights through the fused matvec launches: the same values, fewer launches).
 
 Every buffer is allocated up front, and step() neither allocates, nor
 synchronizes the host, nor writes memory with hipMemsetAsync, so capture()
@@ -176,10 +178,10 @@ class TokenSlice:
         self.q_idx, self.w_idx, self.scores = f(IDX_HEAD * IDX_DIM), f(IDX_HEAD), f(cap)
         self.select = torch.empty(lib().ds4hip_indexer_select_scratch_bytes(cap), dtype=torch.uint8,
                                   device=dev)
-        self.kqv, self.kqv_back = f(N_HEAD * HEAD_DIM), f(N_HEAD * HEAD_DIM)
-        self.low = f(N_OUT_GROUP * N_LORA_O)
-        self.xq = torch.empty(N_HEAD * HEAD_DIM, dtype=torch.int8, device=dev)
-        self.xscale = f(N_HEAD * HEAD_DIM // 32)
+        self.kqv = f(N_HEAD * HEAD_DIM)
+        self.out_ws = torch.empty(lib().ds4hip_attn_out_decode_workspace_bytes(N_HEAD, HEAD_DIM, N_OUT_GROUP,
+                                                                               N_LORA_O),
+                                  dtype=torch.uint8, device=dev)
         # the largest decode of any layer: the whole ring and every compressed row
         n_max = s.layers[0].cap_raw + cap
         self.dec_ws = torch.empty(decode_fp8_workspace_bytes([n_max]), dtype=torch.uint8, device=dev)
@@ -224,14 +226,12 @@ class TokenSlice:
                 L = s.layers[il]
                 if L.n_index_comp > self.top_k:
                     # Step 12c: indexer query, head weights, top-k into the row list
-                    call("ds4hip_mul_mv_f16_f32", _ptr(w["idx_q_b"]), _ptr(q_lora[il]), _ptr(self.q_idx),
-                         IDX_HEAD * IDX_DIM, Q_LORA, st)
-                    call("ds4hip_tail_rope_yarn_f32", _ptr(self.q_idx), _ptr(self.q_idx), IDX_HEAD, IDX_DIM,
-                         N_ROT, pos, il, st)
-                    call("ds4hip_mul_mv_f16_f32", _ptr(w["idx_proj"]), _ptr(x), _ptr(self.w_idx), IDX_HEAD,
-                         N_EMBD, st)
-                    call("ds4hip_scale_inplace_f32", _ptr(self.w_idx), IDX_HEAD,
-                         C.c_float(1.0 / np.sqrt(IDX_DIM * IDX_HEAD)), st)
+                    # the query with its RoPE, and the scaled head weights: one
+                    # launch each (the fused forms of the matvec + RoPE / scale pairs)
+                    call("ds4hip_mul_mv_f16_rope_f32", _ptr(w["idx_q_b"]), _ptr(q_lora[il]), _ptr(self.q_idx),
+                         IDX_HEAD, IDX_DIM, N_ROT, pos, il, Q_LORA, st)
+                    call("ds4hip_mul_mv_f16_scaled_f32", _ptr(w["idx_proj"]), _ptr(x), _ptr(self.w_idx), IDX_HEAD,
+                         N_EMBD, C.c_float(1.0 / np.sqrt(IDX_DIM * IDX_HEAD)), st)
                     _, _, sel = sess.layer_rows(il, self.top_k)
                     call("ds4hip_indexer_topk_positions", _ptr(self.q_idx), _ptr(self.w_idx),
                          _vp(L.index_comp_kv), 0, L.n_index_comp, IDX_HEAD, IDX_DIM, self.top_k, 0,
@@ -240,15 +240,11 @@ class TokenSlice:
             # Step 13
             sess.decode(il, q_cur[il].reshape(-1), w["sinks"], self.kqv, n_selected=n_sel,
                         workspace=self.dec_ws, stream=stream)
-            # Step 14
-            call("ds4hip_tail_rope_yarn_inverse_f32", _ptr(self.kqv), _ptr(self.kqv_back), N_HEAD, HEAD_DIM,
-                 N_ROT, pos, il, st)
-            # Steps 15, 16
-            call("ds4hip_mul_mv_q8_0_q8_0_grouped_f32_prealloc", _ptr(w["out_a"]), _ptr(self.kqv_back),
-                 _ptr(self.low), N_OUT_GROUP, HEAD_DIM * N_HEAD // N_OUT_GROUP, N_LORA_O, _ptr(self.xq),
-                 _ptr(self.xscale), st)
-            call("ds4hip_mul_mv_q8_0_q8_0_f32_prealloc", _ptr(w["out_b"]), _ptr(self.low), _ptr(out[il]),
-                 N_EMBD, N_OUT_GROUP * N_LORA_O, _ptr(self.xq), _ptr(self.xscale), st)
+            # Steps 14-16: inverse RoPE + quantization in one launch, then the
+            # grouped and the dense Q8_0 projections
+            call("ds4hip_attn_out_decode_f32", _ptr(self.kqv), _ptr(w["out_a"]), _ptr(w["out_b"]), _ptr(out[il]),
+                 N_HEAD, HEAD_DIM, N_ROT, pos, il, N_OUT_GROUP, N_LORA_O, N_EMBD, _ptr(self.out_ws),
+                 self.out_ws.numel(), st)
         s.pos = pos + 1
         s.n_tokens_processed = pos + 1
 

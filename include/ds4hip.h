@@ -219,8 +219,8 @@ int ds4hip_mul_mv_f16_f32(const uint16_t *w_f16, const float *x_f32, float *y_f3
 /* Replaces ds4cuda::launch_mul_mv_q8_0_q8_0_grouped_f32 (cuda/attn_out.cuh:86).
  * W: n_groups*rank rows of group_dim/32 block_q8_0 records (34 bytes: f16 d,
  * 32 int8). x: n_groups*group_dim fp32, quantized per 32 elements
- * (d = amax/127, fp32 scale). Row r reads group r / rank. Activation scratch is
- * stream-ordered (hipMallocAsync). */
+ * (d = amax/127, fp32 scale). Row r reads group r / rank. The activations
+ * live in the library's per-stream scratch: nothing is allocated per call. */
 int ds4hip_mul_mv_q8_0_q8_0_grouped_f32(const void *W, const float *x, float *y, int n_groups,
                                         int group_dim, int rank, void *stream);
 
@@ -237,6 +237,32 @@ int ds4hip_mul_mv_q8_0_q8_0_grouped_f32_prealloc(const void *W, const float *x, 
 int ds4hip_mul_mv_q8_0_q8_0_f32_prealloc(const void *W, const float *x, float *y, int n_rows,
                                          int n_cols, int8_t *scratch_xq, float *scratch_xscale,
                                          void *stream);
+
+/* Fused launches (no reference counterpart: each replaces a pair of the
+ * launchers above with the same arithmetic, so the results are bit-identical
+ * to the pair; for callers that count launches, e.g. a per-token slice):
+ *
+ * ds4hip_mul_mv_f16_scaled_f32: ds4hip_mul_mv_f16_f32, then every output times
+ * scale (the indexer head weights and their 1/sqrt(d * n_head) scale,
+ * cuda/forward_layer.cu:1054-1060).
+ *
+ * ds4hip_mul_mv_f16_rope_f32: ds4hip_mul_mv_f16_f32 into n_heads rows of
+ * head_dim, then ds4hip_tail_rope_yarn_f32 (the indexer query,
+ * cuda/forward_layer.cu:1046-1053). head_dim and n_rot multiples of 4.
+ *
+ * ds4hip_attn_out_decode_f32: Steps 14-16 (cuda/forward_layer.cu:1172-1210):
+ * ds4hip_tail_rope_yarn_inverse_f32 of kqv [n_head][head_dim], the grouped
+ * Q8_0 projection (n_groups groups, rank rows each) and the dense Q8_0
+ * projection to out_dim, with the rotation and the first quantization in one
+ * launch. Workspace: ds4hip_attn_out_decode_workspace_bytes. */
+int ds4hip_mul_mv_f16_scaled_f32(const uint16_t *w_f16, const float *x_f32, float *y_f32, int out_dim,
+                                 int in_dim, float scale, void *stream);
+int ds4hip_mul_mv_f16_rope_f32(const uint16_t *w_f16, const float *x_f32, float *y_f32, int n_heads,
+                               int head_dim, int n_rot, int pos, int il, int in_dim, void *stream);
+size_t ds4hip_attn_out_decode_workspace_bytes(int n_head, int head_dim, int n_groups, int rank);
+int ds4hip_attn_out_decode_f32(const float *kqv, const void *w_out_a, const void *w_out_b, float *out,
+                               int n_head, int head_dim, int n_rot, int pos, int il, int n_groups, int rank,
+                               int out_dim, void *workspace, size_t workspace_bytes, void *stream);
 
 /* Replaces ds4cuda::launch_rms_norm_f32 (cuda/norm.cuh:24): one row of n,
  * y = x * (1 / sqrtf(mean(x^2) + eps)) * w, fp32 accumulation. */

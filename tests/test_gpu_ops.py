@@ -296,3 +296,50 @@ def test_compressor_steps(gpu, is_attn, ratio, hd, il):
     assert n_emit >= 1
     print(f"compressor ratio {ratio} is_attn {is_attn}: {n_emit} emits, worst pre-quant "
           f"err/RMS {worst:.2e}, FP8 midpoint flips {flips}")
+
+
+@pytest.mark.parametrize("il", [0, 2])
+def test_fused_launches_equal_the_pairs(gpu, il):
+    """The fused entry points against the launcher pairs they replace, bit for
+    bit: the indexer query (f16 matvec + forward RoPE), the head weights
+    (f16 matvec + scale) and Steps 14-16 (inverse RoPE + grouped and dense
+    Q8_0 projections)."""
+    from ds4cuda_amd import token
+    g = torch.Generator(device=gpu)
+    g.manual_seed(123 + il)
+    pos = 300 + il
+    # indexer query: 64 heads x 128 from 1024
+    wq = token.f16_weights((64 * 128, 1024), g, gpu, 0.05)
+    xq = torch.randn(1024, generator=g, device=gpu)
+    a, b = torch.empty(64 * 128, device=gpu), torch.empty(64 * 128, device=gpu)
+    ops.launch_mul_mv_f16_f32(wq, xq, a, 64 * 128, 1024)
+    ops.launch_tail_rope_yarn_f32(a, a, 64, 128, 64, pos, il)
+    ops.mul_mv_f16_rope_f32(wq, xq, b, 64, 128, 64, pos, il, 1024)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    # head weights: 64 from 4096, scaled
+    wp = token.f16_weights((64, 4096), g, gpu)
+    x = torch.randn(4096, generator=g, device=gpu)
+    a, b = torch.empty(64, device=gpu), torch.empty(64, device=gpu)
+    sc = 1.0 / np.sqrt(128 * 64)
+    ops.launch_mul_mv_f16_f32(wp, x, a, 64, 4096)
+    ops.launch_scale_inplace_f32(a, 64, sc)
+    ops.mul_mv_f16_scaled_f32(wp, x, b, 64, 4096, sc)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    # Steps 14-16
+    wa = token.q8_weights(8 * 1024, 4096, g, gpu)
+    wb = token.q8_weights(4096, 8 * 1024, g, gpu)
+    kqv = torch.randn(64 * 512, generator=g, device=gpu)
+    back = torch.empty(64 * 512, device=gpu)
+    low = torch.empty(8 * 1024, device=gpu)
+    sq = torch.empty(64 * 512, dtype=torch.int8, device=gpu)
+    ss = torch.empty(64 * 512 // 32, device=gpu)
+    ref = torch.empty(4096, device=gpu)
+    ops.launch_tail_rope_yarn_inverse_f32(kqv, back, 64, 512, 64, pos, il)
+    ops.launch_mul_mv_q8_0_q8_0_grouped_f32_prealloc(wa, back, low, 8, 4096, 1024, sq, ss)
+    ops.launch_mul_mv_q8_0_q8_0_f32_prealloc(wb, low, ref, 4096, 8 * 1024, sq, ss)
+    out = torch.empty(4096, device=gpu)
+    ops.attn_out_decode_f32(kqv, wa, wb, out, 64, 512, 64, pos, il, 8, 1024, 4096)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)

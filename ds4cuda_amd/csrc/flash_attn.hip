@@ -50,7 +50,8 @@ constexpr int kNope = kD - kRot; // 448 FP8-coded dims, 7 scale blocks
 constexpr int kTile = 32;        // rows per tile
 constexpr int kVtStride = 40;    // halves per V^T line (32 rows + 8 pad)
 constexpr int kMaxProb = 128;
-constexpr int kMinChunk = 2 * kTile;
+constexpr int kMinChunk = 2 * kTile;       // the register-load kernels run tiles in pairs
+constexpr int kMinChunkFlat = kTile;       // the flat-stage kernel: one tile is a whole chunk
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazyLog2 = 8.0f;   // decode softmax: reference point slack (log2 units)
 constexpr int kFp8WgPerCu = 1;   // the FP8 kernel's LDS ring allows one workgroup per CU
@@ -2575,14 +2576,14 @@ constexpr long long kSegCostRows = 5 * kTile;
 // target_wg: workgroups to aim for (0: wg_per_cu per CU). with_phys: the
 // workspace also holds the physical-row array of gathered FP8 steps.
 Plan make_plan(const long long *count, int n_prob, int wg_per_cu, long long target_wg = 0,
-               bool with_phys = true) {
+               bool with_phys = true, int min_chunk = kMinChunk) {
     Plan pl;
     long long total = 0;
     for (int p = 0; p < n_prob; ++p) total += count[p];
     const long long target = target_wg > 0 ? target_wg : (long long)num_cus() * wg_per_cu;
     auto round_tile = [](long long x) { return ((x + kTile - 1) / kTile) * kTile; };
     long long chunk_a = total > 0 ? round_tile((total + target - 1) / target) : kTile;
-    if (chunk_a < kMinChunk) chunk_a = kMinChunk;
+    if (chunk_a < min_chunk) chunk_a = min_chunk;
     int smax_a = 1;
     {
         long long st = 0;
@@ -2729,7 +2730,8 @@ extern "C" int ds4hip_flash_attn_decode_fp8_workspace_size(const long long *n_ro
     if (!bytes || n_prob <= 0 || n_prob > kMaxProb || !n_rows_per_prob) return kEINVAL;
     for (int p = 0; p < n_prob; ++p)
         if (n_rows_per_prob[p] < 0) return kEINVAL;
-    *bytes = make_plan(n_rows_per_prob, n_prob, kFp8WgPerCu).ws_bytes;
+    // the flat kernel's shorter minimum chunk gives the most slots
+    *bytes = make_plan(n_rows_per_prob, n_prob, kFp8WgPerCu, 0, true, kMinChunkFlat).ws_bytes;
     return 0;
 }
 
@@ -2768,7 +2770,13 @@ extern "C" int ds4hip_flash_attn_decode_fp8(
         A.count[p] = n;
     }
     A.n_cache_rows = n_cache_rows;
-    const Plan pl = make_plan(n_rows_per_prob, n_prob, kFp8WgPerCu);
+    // short problems: the flat kernel takes one-tile chunks (more workgroups,
+    // a shorter chain each; the token slice's ~640-row decodes 88.1 -> 86.7
+    // us per layer); the register-load kernels keep two-tile chunks
+    const bool regload_kernel = o.kernel == DS4HIP_DECODE_KERNEL_REGLOAD ||
+                                (!q_is_f32 && row_idx && !page_table);
+    const Plan pl = make_plan(n_rows_per_prob, n_prob, kFp8WgPerCu, 0, true,
+                              regload_kernel ? kMinChunk : kMinChunkFlat);
     for (int p = 0; p <= n_prob; ++p) A.start[p] = pl.start[p];
     if (workspace_bytes < pl.ws_bytes) return ds4hip_set_last_error(kEINVAL);
     A.q = q;

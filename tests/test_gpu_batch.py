@@ -26,7 +26,7 @@ def test_mul_mm_f32(gpu, n_rows, n_cols, nb):
     close(Y.cpu().numpy(), X.astype(np.float64) @ W.astype(np.float64).T, 1e-5)
 
 
-@pytest.mark.parametrize("n_rows,n_cols,nb", [(100, 64, 1), (256, 4096, 3), (300, 2080, 5), (4096, 32768, 16)])
+@pytest.mark.parametrize("n_rows,n_cols,nb", [(100, 64, 1), (256, 4096, 3), (300, 2080, 5), (300, 2048, 7), (4096, 32768, 16)])
 def test_mul_mm_bf16_shapes(gpu, n_rows, n_cols, nb):
     W = synth.to_bf16_bits(synth.normal(52, 1, n_rows * n_cols) * 0.02).reshape(n_rows, n_cols)
     X = synth.normal(52, 2, nb * n_cols).reshape(nb, n_cols)

@@ -42,6 +42,8 @@ SIGNATURES: dict[str, list] = {
     "ds4hip_mul_mv_f16_scaled_f32": [_vp, _vp, _vp, _i, _i, C.c_float, _vp],
     "ds4hip_mul_mv_f16_rope_f32": [_vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp],
     "ds4hip_attn_out_decode_workspace_bytes": [_i, _i, _i, _i],
+    "ds4hip_token_prologue_f32": [_vp, _vp],
+    "ds4hip_compressor_emit_f32": [_i, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp],
     "ds4hip_attn_out_decode_f32": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _sz, _vp],
     "ds4hip_mul_mv_q8_0_q8_0_grouped_f32": [_vp, _vp, _vp, _i, _i, _i, _vp],
     "ds4hip_mul_mv_q8_0_q8_0_grouped_f32_prealloc": [_vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp],

@@ -13,6 +13,7 @@
 // after a barrier, since the pool read the state — shifts the ratio-4 ring.
 
 #include "ds4hip_common.h"
+#include "step_bodies.h"
 #include "../../include/ds4hip.h"
 
 #include <cmath>
@@ -24,14 +25,13 @@ namespace {
 constexpr float kNegInf = -1.0e30f;   // cuda/compressor.cu:53
 constexpr float kRmsEps = 1.0e-6f;    // cuda/compressor.cu:54
 constexpr int kNRot = 64;             // cuda/compressor.cu:55
-constexpr int kMaxIn = 8192;
+constexpr int kMaxIn = kCompMaxIn;
 
 // One wave per output row of the two projections (rows [0, width) of w_kv,
 // then [0, width) of w_gate), four per workgroup: eight 16-byte weight chunks
 // per lane are in flight before their fmas (wave_rows_dot), which keeps the
 // weight stream busy without fewer workgroups than CUs. Then the APE row and
 // the state row (cuda/compressor.cu:78-110).
-constexpr int kCpRows = 1;
 template <bool kW32>
 __global__ __launch_bounds__(256) void comp_project_kernel(
         const float *__restrict__ x, const void *__restrict__ w_kv, const void *__restrict__ w_gate,
@@ -41,41 +41,8 @@ __global__ __launch_bounds__(256) void comp_project_kernel(
     __shared__ float xs[kMaxIn];
     for (int i = threadIdx.x; i < in_dim; i += 256) xs[i] = x[i];
     __syncthreads();
-    const int lane = threadIdx.x & 63;
-    const int r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * kCpRows;   // rows of [0, 2*width)
-    if (r0 >= 2 * width) return;
-    const void *rows[kCpRows];
-#pragma unroll
-    for (int k = 0; k < kCpRows; ++k) {
-        const int r = min(r0 + k, 2 * width - 1);
-        const bool gate = r >= width;
-        const size_t o = (size_t)(gate ? r - width : r) * in_dim;
-        rows[k] = kW32 ? static_cast<const void *>(static_cast<const float *>(gate ? w_gate : w_kv) + o)
-                       : static_cast<const void *>(static_cast<const uint16_t *>(gate ? w_gate : w_kv) + o);
-    }
-    float acc[kCpRows] = {0.0f};
-    wave_rows_dot<kCpRows, 8, kW32>(rows, xs, in_dim, lane, acc);
-#pragma unroll
-    for (int k = 0; k < kCpRows; ++k) {
-        float a = acc[k];
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) a += __shfl_xor(a, off);
-        const int r = r0 + k;
-        if (lane == 0 && r < 2 * width) {
-            const bool gate = r >= width;
-            const int o = gate ? r - width : r;
-            const int row = ratio == 4 ? ratio + pos_mod : pos_mod;   // cuda/compressor.cu:85
-            const size_t off = (size_t)row * width + o;
-            if (gate) {
-                const float s = a + f16_bits_to_f32(w_ape[(size_t)pos_mod * width + o]);
-                state_score[off] = s;
-                if (sc_cur) sc_cur[o] = s;
-            } else {
-                state_kv[off] = a;
-                if (kv_cur) kv_cur[o] = a;
-            }
-        }
-    }
+    comp_project_rows<kW32>(xs, w_kv, w_gate, w_ape, in_dim, width, ratio, pos_mod, state_kv, state_score,
+                            kv_cur, sc_cur, blockIdx.x);
 }
 
 struct RopeArgs {
@@ -288,6 +255,19 @@ int comp_step(bool is_attn, const float *x, const void *w_kv, const void *w_gate
 }
 
 }  // namespace
+
+extern "C" int ds4hip_compressor_emit_f32(int is_attn, const float *w_norm_f32, int head_dim_out,
+                                          int compress_ratio, int pos, int il, float *state_kv, float *state_score,
+                                          float *emit_out, void *stream) {
+    if (!w_norm_f32 || !state_kv || !state_score || !emit_out || head_dim_out <= kNRot || head_dim_out > 512 ||
+        (head_dim_out % 64) || (compress_ratio != 4 && compress_ratio != 128) || pos < 0 ||
+        (pos + 1) % compress_ratio)
+        return ds4hip_set_last_error(kEINVAL);
+    hipLaunchKernelGGL(comp_emit_kernel, dim3(1), dim3(512), 0, (hipStream_t)stream, state_kv, state_score,
+                       w_norm_f32, emit_out, head_dim_out, compress_ratio, is_attn ? 1 : 0,
+                       rope_args(il, pos + 1 - compress_ratio));
+    return ds4hip_set_last_error(hip_status(hipGetLastError()));
+}
 
 extern "C" int ds4hip_compressor_decode_step_f32_prealloc(
         int is_attn, const float *x_f32, const uint16_t *w_kv_f16, const uint16_t *w_gate_f16,

@@ -16,6 +16,7 @@
 // exact in int32, scaled per 32-element block as the reference does.
 
 #include "ds4hip_common.h"
+#include "step_bodies.h"
 #include "../../include/ds4hip.h"
 
 #include <algorithm>
@@ -154,17 +155,14 @@ struct MvEpilogue {
     int head_dim = 0, n_rot = 0, pos = 0;
     RopeParams P{};
 };
+// Rows [16 vblock, 16 vblock + 16) of y = W x over the staged input xs, with
+// the epilogue kEpi.
 template <int kEpi>
-__global__ __launch_bounds__(256) void mv_f16_kernel(const uint16_t *__restrict__ w,
-                                                     const float *__restrict__ x,
-                                                     float *__restrict__ y, int out_dim,
-                                                     int in_dim, MvEpilogue E) {
-    extern __shared__ float xs[];
-    for (int i = threadIdx.x; i < in_dim; i += 256) xs[i] = x[i];
-    __syncthreads();
+__device__ inline void mv_f16_rows(const float *xs, const uint16_t *__restrict__ w, float *__restrict__ y,
+                                   int out_dim, int in_dim, const MvEpilogue &E, int vblock) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int row0 = (blockIdx.x * 4 + wave) * kMvRows;
+    const int row0 = (vblock * 4 + wave) * kMvRows;
     if (row0 >= out_dim) return;
     float acc[kMvRows] = {0.0f, 0.0f, 0.0f, 0.0f};
     if ((in_dim & 7) == 0) {
@@ -195,6 +193,17 @@ __global__ __launch_bounds__(256) void mv_f16_kernel(const uint16_t *__restrict_
 #pragma unroll
     for (int r = 0; r < kMvRows; ++r)
         if (lane == 0 && row0 + r < out_dim) y[row0 + r] = a[r];
+}
+
+template <int kEpi>
+__global__ __launch_bounds__(256) void mv_f16_kernel(const uint16_t *__restrict__ w,
+                                                     const float *__restrict__ x,
+                                                     float *__restrict__ y, int out_dim,
+                                                     int in_dim, MvEpilogue E) {
+    extern __shared__ float xs[];
+    for (int i = threadIdx.x; i < in_dim; i += 256) xs[i] = x[i];
+    __syncthreads();
+    mv_f16_rows<kEpi>(xs, w, y, out_dim, in_dim, E, blockIdx.x);
 }
 
 // ---- Q8_0 activation quantization (cuda/attn_out.cu:119-145, dense_q8.cu) ---------------
@@ -856,6 +865,106 @@ extern "C" int ds4hip_attn_out_decode_f32(const float *kqv, const void *w_out_a,
     if (e) return ds4hip_set_last_error(e);
     return ds4hip_set_last_error(launch_q8(static_cast<const uint8_t *>(w_out_b), w.low, out, 1, n_low, out_dim,
                                            w.xq2, w.xs2, false, st));
+}
+
+// ---- per-token layer prologue: Steps 11-12c's independent launches as one --------------
+//
+// The launches of a layer step that depend only on the layer's inputs (the
+// FP8 push of the token's KV row, the attention and the indexer compressor
+// projections, the indexer query with its RoPE and the scaled head weights)
+// run as one launch: its workgroup range is cut into the jobs' own grids, each
+// job's workgroups run that job's body (the same device code as its own
+// kernel, so the results are bit-identical), on the CUs at the same time
+// instead of one launch after another.
+namespace {
+constexpr int kPrologueRot = 64;   // the model's RoPE tail (the session's row layout)
+struct PrologueArgs {
+    ds4hip_token_prologue a;
+    int blk_push, blk_comp[2], blk_q, blk_hw;   // first workgroup of each job (blk_hw + n_hw = grid)
+    int width[2], pos_mod[2];
+    MvEpilogue eq, ehw;
+};
+
+__global__ __launch_bounds__(256) void token_prologue_kernel(const PrologueArgs P) {
+    __shared__ float xs[kCompMaxIn];
+    const ds4hip_token_prologue &a = P.a;
+    const int b = blockIdx.x;
+    auto stage = [&](const float *x, int n) {
+        for (int i = threadIdx.x; i < n; i += 256) xs[i] = x[i];
+        __syncthreads();
+    };
+    if (b < P.blk_comp[0]) {   // the FP8 push: one 64-lane row
+        if (threadIdx.x < 64)
+            fp8_row_body<false>(a.kv, nullptr, a.codes, a.sexp, a.tail, 0, a.head_dim, a.n_rot, a.kv_row,
+                                threadIdx.x);
+        return;
+    }
+    for (int c = 0; c < 2; ++c) {
+        const int end = c == 0 ? P.blk_comp[1] : P.blk_q;
+        if (b < end) {
+            stage(a.x, a.in_dim);
+            comp_project_rows<false>(xs, c ? a.comp1_w_kv : a.comp0_w_kv, c ? a.comp1_w_gate : a.comp0_w_gate,
+                                     c ? a.comp1_w_ape : a.comp0_w_ape, a.in_dim, P.width[c],
+                                     c ? a.comp1_ratio : a.comp0_ratio, P.pos_mod[c],
+                                     c ? a.comp1_state_kv : a.comp0_state_kv,
+                                     c ? a.comp1_state_score : a.comp0_state_score, nullptr, nullptr,
+                                     b - P.blk_comp[c]);
+            return;
+        }
+    }
+    if (b < P.blk_hw) {
+        stage(a.q_x, a.q_in);
+        mv_f16_rows<kMvRope>(xs, a.q_w, a.q_out, a.q_heads * a.q_head_dim, a.q_in, P.eq, b - P.blk_q);
+        return;
+    }
+    stage(a.x, a.in_dim);
+    mv_f16_rows<kMvScale>(xs, a.hw_w, a.hw_out, a.hw_rows, a.in_dim, P.ehw, b - P.blk_hw);
+}
+}  // namespace
+
+extern "C" int ds4hip_token_prologue_f32(const ds4hip_token_prologue *a, void *stream) {
+    if (!a || !a->kv || !a->codes || !a->sexp || !a->tail || a->kv_row < 0 || a->head_dim != 512 ||
+        a->n_rot != kPrologueRot || a->n_comp < 0 || a->n_comp > 2 ||
+        ((a->n_comp || a->hw_w) && (!a->x || a->in_dim <= 0 || a->in_dim > kCompMaxIn || a->in_dim % 8)))
+        return ds4hip_set_last_error(kEINVAL);
+    PrologueArgs P = {};
+    P.a = *a;
+    const int ratio[2] = {a->comp0_ratio, a->comp1_ratio};
+    const int hdo[2] = {a->comp0_head_dim_out, a->comp1_head_dim_out};
+    const int pos[2] = {a->comp0_pos, a->comp1_pos};
+    int blk = 1;   // workgroup 0: the FP8 push
+    for (int c = 0; c < 2; ++c) {
+        P.blk_comp[c] = blk;
+        if (c >= a->n_comp) continue;
+        const void *wk = c ? a->comp1_w_kv : a->comp0_w_kv, *wg = c ? a->comp1_w_gate : a->comp0_w_gate;
+        const void *wa = c ? a->comp1_w_ape : a->comp0_w_ape;
+        const float *sk = c ? a->comp1_state_kv : a->comp0_state_kv, *ss = c ? a->comp1_state_score : a->comp0_state_score;
+        if (!wk || !wg || !wa || !sk || !ss || (ratio[c] != 4 && ratio[c] != 128) || hdo[c] <= 64 ||
+            hdo[c] > 512 || hdo[c] % 64 || pos[c] < 0)
+            return ds4hip_set_last_error(kEINVAL);
+        P.width[c] = (ratio[c] == 4 ? 2 : 1) * hdo[c];
+        P.pos_mod[c] = pos[c] % ratio[c];
+        blk += (2 * P.width[c] + 3) / 4;
+    }
+    P.blk_q = blk;
+    if (a->q_w) {
+        if (!a->q_x || !a->q_out || a->q_heads <= 0 || a->q_head_dim <= 0 || a->q_head_dim % 4 || a->q_in <= 0 ||
+            a->q_in > kCompMaxIn || a->q_in % 8)
+            return ds4hip_set_last_error(kEINVAL);
+        P.eq.head_dim = a->q_head_dim;
+        P.eq.n_rot = kPrologueRot;
+        P.eq.pos = a->q_pos;
+        P.eq.P = rope_params(kPrologueRot, a->q_il, false);
+        blk += (a->q_heads * a->q_head_dim + 4 * kMvRows - 1) / (4 * kMvRows);
+    }
+    P.blk_hw = blk;
+    if (a->hw_w) {
+        if (!a->hw_out || a->hw_rows <= 0) return ds4hip_set_last_error(kEINVAL);
+        P.ehw.scale = a->hw_scale;
+        blk += (a->hw_rows + 4 * kMvRows - 1) / (4 * kMvRows);
+    }
+    hipLaunchKernelGGL(token_prologue_kernel, dim3(blk), dim3(256), 0, (hipStream_t)stream, P);
+    return ds4hip_set_last_error(hip_status(hipGetLastError()));
 }
 
 extern "C" int ds4hip_mul_mm_bf16_f32(const uint16_t *W, const float *X, float *Y, int n_rows,

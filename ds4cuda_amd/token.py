@@ -45,6 +45,19 @@ N_OUT_GROUP, N_LORA_O = 8, 1024
 Q8_BLOCK = 34
 
 
+class TokenPrologue(C.Structure):
+    """ds4hip_token_prologue (include/ds4hip.h): one layer step's independent
+    launches of Steps 11-12c as one."""
+    _vp_fields = lambda pre: [(pre + n, C.c_void_p) for n in ("w_kv", "w_gate", "w_ape", "state_kv", "state_score")] + \
+        [(pre + n, C.c_int) for n in ("head_dim_out", "ratio", "pos")]
+    _fields_ = [("kv", C.c_void_p), ("codes", C.c_void_p), ("sexp", C.c_void_p), ("tail", C.c_void_p),
+                ("kv_row", C.c_longlong), ("head_dim", C.c_int), ("n_rot", C.c_int), ("x", C.c_void_p),
+                ("in_dim", C.c_int), ("n_comp", C.c_int)] + _vp_fields("comp0_") + _vp_fields("comp1_") + \
+               [("q_w", C.c_void_p), ("q_x", C.c_void_p), ("q_out", C.c_void_p), ("q_heads", C.c_int),
+                ("q_head_dim", C.c_int), ("q_in", C.c_int), ("q_pos", C.c_int), ("q_il", C.c_int),
+                ("hw_w", C.c_void_p), ("hw_out", C.c_void_p), ("hw_rows", C.c_int), ("hw_scale", C.c_float)]
+
+
 def layer_ratio(il: int) -> int:
     """Compression ratio of layer il (cuda/rope.cu:123-126): 0 for il < 2,
     then 4 on even and 128 on odd layers."""
@@ -165,10 +178,14 @@ class TokenSlice:
     given per-layer weights (synthetic_weights' layout). top_k: the indexer's
     selection size (512 in the model)."""
 
-    def __init__(self, session: Session, weights, top_k: int = 512):
+    def __init__(self, session: Session, weights, top_k: int = 512, fused: bool = True):
         self.session = session
         self.w = weights
         self.top_k = top_k
+        # fused: each layer's push, compressor projections and indexer query /
+        # weights as one launch (ds4hip_token_prologue_f32); otherwise one
+        # launch each (the same values)
+        self.fused = fused
         s = session.s
         dev = weights[0]["sinks"].device
         cap = max(1, max(s.layers[il].cap_comp for il in range(N_LAYER)))
@@ -197,6 +214,9 @@ class TokenSlice:
         sess, s = self.session, self.session.s
         st = _stream(stream)
         for il in range(N_LAYER):
+            if self.fused:
+                self._layer_fused(il, pos, kv_rope, attn_norm, q_cur, q_lora, out, stream)
+                continue
             w = self.w[il]
             L = s.layers[il]
             r = L.compress_ratio
@@ -247,6 +267,65 @@ class TokenSlice:
                  self.out_ws.numel(), st)
         s.pos = pos + 1
         s.n_tokens_processed = pos + 1
+
+    def _layer_fused(self, il, pos, kv_rope, attn_norm, q_cur, q_lora, out, stream):
+        """One layer of step() with Steps 11-12c's independent launches as one."""
+        sess, s = self.session, self.session.s
+        st = _stream(stream)
+        w = self.w[il]
+        L = s.layers[il]
+        r = L.compress_ratio
+        x = attn_norm[il]
+        P = TokenPrologue()
+        # Step 11: the FP8 push, with the host bookkeeping of
+        # ds4hip_session_push_raw
+        P.kv, P.codes, P.sexp, P.tail = _ptr(kv_rope[il]), s.codes, s.sexp, s.tail
+        P.kv_row = L.row_base + L.cap_comp + L.raw_head
+        P.head_dim, P.n_rot = HEAD_DIM, N_ROT
+        L.raw_head = (L.raw_head + 1) % L.cap_raw
+        L.n_raw = min(L.n_raw + 1, L.cap_raw)
+        P.x, P.in_dim = _ptr(x), N_EMBD
+        emit = bool(r) and (pos + 1) % r == 0
+        if r:   # Step 12a (and 12b): the projections
+            P.n_comp = 2 if r == 4 else 1
+            P.comp0_w_kv, P.comp0_w_gate, P.comp0_w_ape = _ptr(w["comp_kv"]), _ptr(w["comp_gate"]), _ptr(w["comp_ape"])
+            P.comp0_state_kv, P.comp0_state_score = L.attn_state_kv, L.attn_state_score
+            P.comp0_head_dim_out, P.comp0_ratio, P.comp0_pos = HEAD_DIM, r, pos
+            if r == 4:
+                P.comp1_w_kv, P.comp1_w_gate, P.comp1_w_ape = _ptr(w["idx_kv"]), _ptr(w["idx_gate"]), _ptr(w["idx_ape"])
+                P.comp1_state_kv, P.comp1_state_score = L.index_state_kv, L.index_state_score
+                P.comp1_head_dim_out, P.comp1_ratio, P.comp1_pos = IDX_DIM, r, pos
+        # Step 12c runs when the indexer holds more than top_k keys after this step
+        select = r == 4 and L.n_index_comp + (1 if emit else 0) > self.top_k
+        if select:
+            P.q_w, P.q_x, P.q_out = _ptr(w["idx_q_b"]), _ptr(q_lora[il]), _ptr(self.q_idx)
+            P.q_heads, P.q_head_dim, P.q_in, P.q_pos, P.q_il = IDX_HEAD, IDX_DIM, Q_LORA, pos, il
+            P.hw_w, P.hw_out, P.hw_rows = _ptr(w["idx_proj"]), _ptr(self.w_idx), IDX_HEAD
+            P.hw_scale = 1.0 / np.sqrt(IDX_DIM * IDX_HEAD)
+        call("ds4hip_token_prologue_f32", C.byref(P), st)
+        if emit:   # the emits and their row pushes
+            call("ds4hip_compressor_emit_f32", 1, _ptr(w["comp_norm"]), HEAD_DIM, r, pos, il,
+                 _vp(L.attn_state_kv), _vp(L.attn_state_score), _ptr(self.emit), st)
+            sess.push_comp(il, self.emit, stream=stream)
+            if r == 4:
+                call("ds4hip_compressor_emit_f32", 0, _ptr(w["idx_norm"]), IDX_DIM, r, pos, il,
+                     _vp(L.index_state_kv), _vp(L.index_state_score), _ptr(self.emit_i), st)
+                sess.push_index_comp(il, self.emit_i, stream=stream)
+        n_sel = -1
+        L = s.layers[il]
+        if select:
+            _, _, sel = sess.layer_rows(il, self.top_k)
+            call("ds4hip_indexer_topk_positions", _ptr(self.q_idx), _ptr(self.w_idx),
+                 _vp(L.index_comp_kv), 0, L.n_index_comp, IDX_HEAD, IDX_DIM, self.top_k, 0,
+                 _ptr(self.scores), _ptr(self.select), None, _vp(sel), st)
+            n_sel = self.top_k
+        # Step 13
+        sess.decode(il, q_cur[il].reshape(-1), w["sinks"], self.kqv, n_selected=n_sel,
+                    workspace=self.dec_ws, stream=stream)
+        # Steps 14-16
+        call("ds4hip_attn_out_decode_f32", _ptr(self.kqv), _ptr(w["out_a"]), _ptr(w["out_b"]), _ptr(out[il]),
+             N_HEAD, HEAD_DIM, N_ROT, pos, il, N_OUT_GROUP, N_LORA_O, N_EMBD, _ptr(self.out_ws),
+             self.out_ws.numel(), st)
 
     def capture(self, pos, kv_rope, attn_norm, q_cur, q_lora, out):
         """Records step(pos, ...) into a HIP graph (torch.cuda.CUDAGraph) and

@@ -255,6 +255,54 @@ int ds4hip_mul_mv_q8_0_q8_0_f32_prealloc(const void *W, const float *x, float *y
  * Q8_0 projection (n_groups groups, rank rows each) and the dense Q8_0
  * projection to out_dim, with the rotation and the first quantization in one
  * launch. Workspace: ds4hip_attn_out_decode_workspace_bytes. */
+/* One layer step's independent launches of Steps 11-12c as one launch (no
+ * reference counterpart; for a per-token slice that counts launches). Jobs:
+ *   - the FP8 push: kv [head_dim] into cache row kv_row of codes / sexp / tail
+ *     (as ds4hip_fp8_kv_quantize_append of one row);
+ *   - n_comp (0..2) compressor projections over x [in_dim] with f16 weights
+ *     (the projection half of ds4hip_compressor_decode_step_f32_prealloc at
+ *     pos; the emit, on steps where (pos + 1) % ratio == 0, is
+ *     ds4hip_compressor_emit_f32 afterwards);
+ *   - if q_w: the indexer query, q_out = RoPE(q_w . q_x) (as
+ *     ds4hip_mul_mv_f16_rope_f32 with n_rot 64);
+ *   - if hw_w: the head weights, hw_out = (hw_w . x) * hw_scale (as
+ *     ds4hip_mul_mv_f16_scaled_f32).
+ * head_dim 512 and n_rot 64 (the session's rows). The results are
+ * bit-identical to those launches. in_dim, q_in <= 8192. */
+typedef struct ds4hip_token_prologue {
+    const float *kv;
+    uint8_t *codes;
+    int8_t *sexp;
+    uint16_t *tail;
+    long long kv_row;
+    int head_dim, n_rot;
+    const float *x;
+    int in_dim, n_comp;
+    const uint16_t *comp0_w_kv, *comp0_w_gate, *comp0_w_ape;
+    float *comp0_state_kv, *comp0_state_score;
+    int comp0_head_dim_out, comp0_ratio, comp0_pos;
+    const uint16_t *comp1_w_kv, *comp1_w_gate, *comp1_w_ape;
+    float *comp1_state_kv, *comp1_state_score;
+    int comp1_head_dim_out, comp1_ratio, comp1_pos;
+    const uint16_t *q_w;
+    const float *q_x;
+    float *q_out;
+    int q_heads, q_head_dim, q_in, q_pos, q_il;
+    const uint16_t *hw_w;
+    float *hw_out;
+    int hw_rows;
+    float hw_scale;
+} ds4hip_token_prologue;
+int ds4hip_token_prologue_f32(const ds4hip_token_prologue *a, void *stream);
+
+/* The emit half of ds4hip_compressor_decode_step_f32_prealloc for a step whose
+ * projection already ran (through ds4hip_token_prologue_f32): pool, RMSNorm,
+ * tail RoPE at pos + 1 - ratio, FP8 round trip (is_attn) and the ratio-4 ring
+ * shift, into emit_out [head_dim_out]. Only for (pos + 1) % ratio == 0. */
+int ds4hip_compressor_emit_f32(int is_attn, const float *w_norm_f32, int head_dim_out, int compress_ratio,
+                               int pos, int il, float *state_kv, float *state_score, float *emit_out,
+                               void *stream);
+
 int ds4hip_mul_mv_f16_scaled_f32(const uint16_t *w_f16, const float *x_f32, float *y_f32, int out_dim,
                                  int in_dim, float scale, void *stream);
 int ds4hip_mul_mv_f16_rope_f32(const uint16_t *w_f16, const float *x_f32, float *y_f32, int n_heads,

@@ -65,3 +65,40 @@ def test_token_slice_graph_replay_matches_eager(gpu):
     finally:
         a.close()
         b.close()
+
+
+def test_token_slice_fused_prologue_matches_separate_launches(gpu):
+    """fused=True (each layer's FP8 push, compressor projections and indexer
+    query / head weights as one launch) against fused=False (one launch
+    each): bit-identical outputs and arenas over positions 380-383, where
+    pos 383 emits on both the ratio-4 and the ratio-128 layers and, with
+    top_k 95, the ratio-4 layers' indexer first holds more than top_k keys
+    (95 before the emit, 96 after), so the selection starts on that step."""
+    pos0, topk = 380, 95
+    w = token.synthetic_weights(gpu)
+    a, b = session.Session(CTX), session.Session(CTX)
+    try:
+        token.fill_history(a, pos0)
+        token.fill_history(b, pos0)
+        assert a.layer(2).n_index_comp == topk
+        ta = token.TokenSlice(a, w, top_k=topk, fused=False)
+        tb = token.TokenSlice(b, w, top_k=topk, fused=True)
+        for pos in range(pos0, pos0 + 4):
+            x = inputs(pos, gpu)
+            oa, ob = torch.empty((43, 4096), device=gpu), torch.empty((43, 4096), device=gpu)
+            ta.step(pos, *x, oa)
+            tb.step(pos, *x, ob)
+            torch.cuda.synchronize()
+            e, r = oa.cpu().numpy(), ob.cpu().numpy()
+            assert np.isfinite(e).all()
+            assert np.array_equal(e.view(np.uint32), r.view(np.uint32)), pos
+            assert np.array_equal(arena(a), arena(b)), pos
+            for il in range(43):
+                la, lb = a.layer(il), b.layer(il)
+                assert (la.n_raw, la.raw_head, la.n_comp, la.n_index_comp) == \
+                       (lb.n_raw, lb.raw_head, lb.n_comp, lb.n_index_comp), (pos, il)
+        assert a.layer(2).n_index_comp == topk + 1
+        print(f"token slice fused == separate launches bit for bit, pos {pos0}-{pos0 + 3}")
+    finally:
+        a.close()
+        b.close()

@@ -31,6 +31,7 @@
 // contiguous 16-byte LDS read.
 
 #include "ds4hip_common.h"
+#include "q_prep.h"
 #include "../../include/ds4hip.h"
 
 #include <algorithm>
@@ -1643,7 +1644,7 @@ __device__ inline float xmax_16_32_raw(float v) {
 // kGather: 0 direct rows; 1 physical rows from the phys array (phys_kernel
 // ran: pages and / or row lists); 2 the int32 row list itself (no pages: row
 // = the problem's base + entry, clamped into the cache)
-template <bool kPLo, bool kLean, bool kQf32 = false, int kGather = 0>
+template <bool kPLo, bool kLean, int kQf32 = 0, int kGather = 0>
 __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A) {
     static_assert(kLean || !kQf32, "fp32 Q takes the lean form");
     // Q parts on the scaled FP8 MFMA: a bf16 Q (8 significant bits) fits in
@@ -1690,119 +1691,35 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
         const long long slot = (long long)blockIdx.x * A.s_max + slot_s;
         const long long seg_r0 = s_rowbase[p] + r0;
         const int seg_last = (int)(r1 - 1 - r0);
-        if constexpr (kGather != 0)
-            scan_segment_rows(A, kGather == 1, p, g0, seg_end, r0, r1, s_rowbase[p], slot_s, s_bad);
         // ---- the producers: QK^T on the scaled FP8 MFMA and the softmax, one
         // interval apart (interval u: QK(u) with softmax(u - 1) in its issue slots)
         auto produce = [&]() {
-            // Q of head 16 d + j as the B operand of the scaled FP8 MFMA. k-step ks
-            // covers dims 128 ks + [0, 128); the MFMA takes lane (j, q)'s 32 bytes
-            // as dims 128 ks + 16 q + [0, 16) and 128 ks + 64 + 16 q + [0, 16)
-            // (lane q supplies the scale of dims 128 ks + 32 q + [0, 32)). Q ~ hi +
-            // lo, each E4M3 codes with one E8M0 scale per head and k-step (a bf16
-            // value has 8 significant bits: hi keeps 4, lo the rest). Dims >= 448
-            // (the f16 RoPE tail) are zero here and take the f16 MFMA instead:
-            // qt[s] = dims 448 + 32 s + 8 q + [0, 8) (an fp32 Q: f16 hi qt + lo qtl;
-            // one f16 rounding there would dominate the error of the three parts).
+            // Q of head 16 d + j as the scaled FP8 MFMA's B operand (q_prep_lane),
+            // converted here or (kQf32 == 2) loaded as the prologue converted it
             uint32_t qf8[4][kParts][8];
-            int qsc[kParts] = {};   // [part]: byte ks = E8M0 scale of k-step ks (the MFMA's op_sel picks it)
+            int qsc[kParts];
             half8_t qt[2], qtl[2];
             {
-                const long long qoff = (long long)p * A.q_stride + (long long)(16 * d + j) * kD;
-                const uint16_t *qsrc = static_cast<const uint16_t *>(A.q) + qoff;
-                const float *qsrc32 = static_cast<const float *>(A.q) + qoff;
-#pragma unroll
-                for (int ks = 0; ks < 4; ++ks) {
-                    float x[32];
-#pragma unroll
-                    for (int hv = 0; hv < 2; ++hv) {
-                        const bool live = ks < 3 || hv == 0;
-#pragma unroll
-                        for (int v = 0; v < 2; ++v) {
-                            const int off = 128 * ks + 64 * hv + 16 * q + 8 * v;
-                            if constexpr (kQf32) {
-                                float4_t a = float4_t{0, 0, 0, 0}, b = a;
-                                if (live) {
-                                    a = *reinterpret_cast<const float4_t *>(qsrc32 + off);
-                                    b = *reinterpret_cast<const float4_t *>(qsrc32 + off + 4);
-                                }
-#pragma unroll
-                                for (int i = 0; i < 4; ++i) {
-                                    x[16 * hv + 8 * v + i] = a[i];
-                                    x[16 * hv + 8 * v + 4 + i] = b[i];
-                                }
-                            } else {
-                                uint4_t w = uint4_t{0, 0, 0, 0};
-                                if (live) w = *reinterpret_cast<const uint4_t *>(qsrc + off);
-#pragma unroll
-                                for (int i = 0; i < 4; ++i) {
-                                    x[16 * hv + 8 * v + 2 * i] = bf16_to_f32((uint16_t)(w[i] & 0xFFFF));
-                                    x[16 * hv + 8 * v + 2 * i + 1] = bf16_to_f32((uint16_t)(w[i] >> 16));
-                                }
-                            }
-                        }
-                    }
-#pragma unroll
-                    for (int part = 0; part < kParts; ++part) {
-                        float amax = 0.0f;
-#pragma unroll
-                        for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(x[i]));
-                        amax = xmax_16_32(amax);   // one scale for the head's 128 dims
-                        // scale 2^e with amax / 2^e in [128, 256): no E4M3 overflow
-                        int e = amax > 0.0f ? ((int)((__float_as_uint(amax) >> 23) & 0xFF) - 127 - 7) : 0;
-                        // kLean: the rows' E8M0 scales are 2^(e_row + 1) (byte e_row ^ 0x80),
-                        // so Q's scale carries the compensating 2^-1
-                        if constexpr (kLean) e = max(e, -126);
-                        const float inv = pow2f(-e), sc = pow2f(e);
-                        qsc[part] |= (e + (kLean ? 126 : 127)) << (8 * ks);
-#pragma unroll
-                        for (int w = 0; w < 8; ++w) {
-                            int pk = 0;
-                            pk = __builtin_amdgcn_cvt_pk_fp8_f32(x[4 * w] * inv, x[4 * w + 1] * inv, pk, false);
-                            pk = __builtin_amdgcn_cvt_pk_fp8_f32(x[4 * w + 2] * inv, x[4 * w + 3] * inv, pk, true);
-                            qf8[ks][part][w] = (uint32_t)pk;
-                            if (part < kParts - 1) {   // the residual goes to the next part
-                                x[4 * w] -= __builtin_amdgcn_cvt_f32_fp8(pk, 0) * sc;
-                                x[4 * w + 1] -= __builtin_amdgcn_cvt_f32_fp8(pk, 1) * sc;
-                                x[4 * w + 2] -= __builtin_amdgcn_cvt_f32_fp8(pk, 2) * sc;
-                                x[4 * w + 3] -= __builtin_amdgcn_cvt_f32_fp8(pk, 3) * sc;
-                            }
-                        }
-                    }
+                if constexpr (kQf32 == 2) {
+                    const uint4_t *src = reinterpret_cast<const uint4_t *>(static_cast<const uint32_t *>(A.q) +
+                                                                           (long long)p * A.q_stride);
+                    q_prep_load(src, 64 * d + lane, qf8, qsc, qt, qtl);
+                } else {
+                    const long long qoff = (long long)p * A.q_stride + (long long)(16 * d + j) * kD;
+                    const void *qrow = kQf32 ? static_cast<const void *>(static_cast<const float *>(A.q) + qoff)
+                                             : static_cast<const void *>(static_cast<const uint16_t *>(A.q) + qoff);
+                    q_prep_lane<kQf32 != 0, kLean>(qrow, q, qf8, qsc, qt, qtl);
                 }
-                // tail dims 448 + 32 s2 + 8 q + [0, 8): bf16 -> f16, or fp32 -> f16 hi + lo
-#pragma unroll
-                for (int s2 = 0; s2 < 2; ++s2) {
-                    half8_t h;
-                    if constexpr (kQf32) {
-                        const float4_t a = *reinterpret_cast<const float4_t *>(qsrc32 + 448 + 32 * s2 + 8 * q);
-                        const float4_t b = *reinterpret_cast<const float4_t *>(qsrc32 + 448 + 32 * s2 + 8 * q + 4);
-                        half8_t l;
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            h[i] = (half_t)a[i];
-                            l[i] = (half_t)(a[i] - (float)h[i]);
-                            h[4 + i] = (half_t)b[i];
-                            l[4 + i] = (half_t)(b[i] - (float)h[4 + i]);
-                        }
-                        qtl[s2] = l;
-                    } else {
-                        const uint4_t w = *reinterpret_cast<const uint4_t *>(qsrc + 448 + 32 * s2 + 8 * q);
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            h[2 * i] = (half_t)bf16_to_f32((uint16_t)(w[i] & 0xFFFF));
-                            h[2 * i + 1] = (half_t)bf16_to_f32((uint16_t)(w[i] >> 16));
-                        }
-                    }
-                    qt[s2] = h;
-                }
-                if constexpr (kQf32) {   // this lane's slots only: no other wave reads them
+                if constexpr (kQf32 != 0) {   // this lane's slots only: no other wave reads them
                     const uint32_t qa = lds_addr(&q_tail_s[(d * 4) * 64]) + 16 * lane;
                     asm volatile("ds_write_b128 %0, %1\n\tds_write_b128 %0, %2 offset:1024\n\t"
                                  "ds_write_b128 %0, %3 offset:2048\n\tds_write_b128 %0, %4 offset:3072"
                                  :: "v"(qa), "v"(qt[0]), "v"(qt[1]), "v"(qtl[0]), "v"(qtl[1]) : "memory");
                 }
             }
+            // stage 0 complete (the consumers' prologue copies); the Q work above
+            // ran under those copies
+            lds_barrier();
             float m_run = -INFINITY, l_run = 0.0f;   // head 16 d + j; l over this lane's rows
             // softmax of tile t (S^T in sa) for heads 16 d + [0, 16) -> P, alpha in LDS
             auto softmax = [&](int t, const float4_t (&sa)[2]) {
@@ -2088,6 +2005,15 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
                 }
             };
             const long long seg_base = s_rowbase[p];
+            // gathered rows: a row outside the cache seen by this lane (every row
+            // of the segment passes through some consumer lane's copies); the
+            // slot mark reads it after the producers' last barrier, which comes
+            // after every copy issue
+            bool cbad = false;
+            auto report_bad = [&]() {
+                if constexpr (kGather != 0)
+                    if (__builtin_expect(__any(cbad), 0) && lane == 0) s_bad[slot_s & 1] = 1;
+            };
             auto issue = [&](int u) {
                 uint8_t *st = stage[u % kFsStages];
                 if constexpr (kGather) {
@@ -2106,7 +2032,10 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
                         asm volatile("s_waitcnt lgkmcnt(0)"
                                      : "+v"(rr[0]), "+v"(rr[1]), "+v"(rr[2]), "+v"(rr[3]), "+v"(rr[4]) :: "memory");
 #pragma unroll
-                        for (int k = 0; k < 5; ++k) rr[k] = unmark_row(rr[k]);
+                        for (int k = 0; k < 5; ++k) {
+                            cbad |= rr[k] < 0;
+                            rr[k] = unmark_row(rr[k]);
+                        }
                     } else {
                         int ix[5];
 #pragma unroll
@@ -2117,7 +2046,11 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
                         asm volatile("s_waitcnt lgkmcnt(0)"
                                      : "+v"(ix[0]), "+v"(ix[1]), "+v"(ix[2]), "+v"(ix[3]), "+v"(ix[4]) :: "memory");
 #pragma unroll
-                        for (int k = 0; k < 5; ++k) rr[k] = clamp_row(seg_base + ix[k], A.n_cache_rows);
+                        for (int k = 0; k < 5; ++k) {
+                            const long long v = seg_base + ix[k];
+                            cbad |= v < 0 || v >= A.n_cache_rows;
+                            rr[k] = clamp_row(v, A.n_cache_rows);
+                        }
                     }
                     issue_rows(u, rr);
                     return;
@@ -2305,14 +2238,19 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
 #pragma unroll
                     for (int k = 0; k < 5; ++k) {
                         const int e = min(kTile * u + c_row[k], seg_last);
-                        if constexpr (kGather == 1)
-                            rr[u][k] = unmark_row(A.phys[g0 + e]);
-                        else
-                            rr[u][k] = clamp_row(seg_base + A.row_idx[(long long)p * A.row_idx_stride + r0 + e],
-                                                 A.n_cache_rows);
+                        if constexpr (kGather == 1) {
+                            const long long v = A.phys[g0 + e];
+                            cbad |= v < 0;
+                            rr[u][k] = unmark_row(v);
+                        } else {
+                            const long long v = seg_base + A.row_idx[(long long)p * A.row_idx_stride + r0 + e];
+                            cbad |= v < 0 || v >= A.n_cache_rows;
+                            rr[u][k] = clamp_row(v, A.n_cache_rows);
+                        }
                     }
 #pragma unroll
                 for (int u = 0; u < kFsLead; ++u) issue_rows(u, rr[u]);
+                report_bad();
             } else {
 #pragma unroll
                 for (int u = 0; u < kFsLead; ++u) issue(u);
@@ -2323,6 +2261,7 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
             // that ends it, tile u + 1 has landed (this wave's copies)
             for (int u = 0; u < n_tiles + 2; ++u) {
                 issue(u + kFsLead);
+                report_bad();
                 if (u >= 2) pv(u - 2);
                 wait_ring();
                 lds_barrier();
@@ -2343,16 +2282,15 @@ __global__ __launch_bounds__(512, 1) void decode_flat_kernel(const DecodeArgs A)
         };
         if (n_tiles > 0) {
             if (producer) {
-                lds_barrier();   // stage 0 complete (the consumers' prologue copies)
-                produce();
+                produce();   // its first barrier: stage 0 complete
             } else {
                 if (d == 3) consume(std::true_type{});
                 else consume(std::false_type{});
             }
         }
         // a segment with no rows (padding of the chunked row space) has no partial;
-        // a bad row met by the segment's scan marks the slot (s_bad: the scan's
-        // atomics are ordered before this by the tile loop's barriers)
+        // a gathered row outside the cache, met by a consumer's copies, marks the
+        // slot (s_bad: written before the tile loop's last barrier)
         if (threadIdx.x == 0) {
             A.ws_prob[slot] = n_tiles > 0 ? (p | ((s_badp[p] | s_bad[slot_s & 1]) ? kBadSlot : 0)) : -1;
             s_bad[slot_s & 1] = 0;
@@ -2660,9 +2598,10 @@ void launch_ws(const DecodeArgs &A, const Plan &pl, hipStream_t st, const ds4hip
         hipLaunchKernelGGL((decode_ws_kernel<kMode, false>), dim3(pl.n_wg), dim3(512), 0, st, A);
 }
 
+// q_pre: an fp32 Q already converted by q_prep_lane (ds4hip_flash_attn_q_prep_f32)
 template <bool kFp8, bool kQf32>
 int launch(DecodeArgs &A, const Plan &pl, hipStream_t st, int phases = 3,
-           const ds4hip_decode_opts &o = ds4hip_decode_opts{0, 0}) {
+           const ds4hip_decode_opts &o = ds4hip_decode_opts{0, 0}, bool q_pre = false) {
     A.chunk = pl.chunk;
     A.s_max = pl.s_max;
     A.kq_log2 = kLog2e / sqrtf((float)kD);
@@ -2687,12 +2626,18 @@ int launch(DecodeArgs &A, const Plan &pl, hipStream_t st, int phases = 3,
         else if (kFp8 && o.kernel != DS4HIP_DECODE_KERNEL_REGLOAD) {
             // fp32 Q: the flat-stage kernel with Q in three FP8 parts and, as
             // every fp32-Q decode, P as f16 hi + lo
-            if (idx_only)
-                hipLaunchKernelGGL((decode_flat_kernel<true, true, true, 2>), dim3(pl.n_wg), dim3(512), 0, st, A);
+            if (q_pre && idx_only)
+                hipLaunchKernelGGL((decode_flat_kernel<true, true, 2, 2>), dim3(pl.n_wg), dim3(512), 0, st, A);
+            else if (q_pre && A.phys)
+                hipLaunchKernelGGL((decode_flat_kernel<true, true, 2, 1>), dim3(pl.n_wg), dim3(512), 0, st, A);
+            else if (q_pre)
+                hipLaunchKernelGGL((decode_flat_kernel<true, true, 2, 0>), dim3(pl.n_wg), dim3(512), 0, st, A);
+            else if (idx_only)
+                hipLaunchKernelGGL((decode_flat_kernel<true, true, 1, 2>), dim3(pl.n_wg), dim3(512), 0, st, A);
             else if (A.phys)
-                hipLaunchKernelGGL((decode_flat_kernel<true, true, true, 1>), dim3(pl.n_wg), dim3(512), 0, st, A);
+                hipLaunchKernelGGL((decode_flat_kernel<true, true, 1, 1>), dim3(pl.n_wg), dim3(512), 0, st, A);
             else
-                hipLaunchKernelGGL((decode_flat_kernel<true, true, true, 0>), dim3(pl.n_wg), dim3(512), 0, st, A);
+                hipLaunchKernelGGL((decode_flat_kernel<true, true, 1, 0>), dim3(pl.n_wg), dim3(512), 0, st, A);
         }
         else if (kFp8)
             hipLaunchKernelGGL(decode_fp8_kernel<kQf32>, dim3(pl.n_wg), dim3(256), 0, st, A);
@@ -2751,6 +2696,12 @@ extern "C" int ds4hip_flash_attn_decode_fp8(
     if ((o.exact_p != 0 && o.exact_p != 1) ||
         (o.kernel != DS4HIP_DECODE_KERNEL_AUTO && o.kernel != DS4HIP_DECODE_KERNEL_REGLOAD))
         return ds4hip_set_last_error(kEINVAL);
+    // q_is_f32 2: the converted form (only the flat-stage kernel reads it); its
+    // problems kQPrepWords apart at least
+    if (q_is_f32 < 0 || q_is_f32 > 2 ||
+        (q_is_f32 == 2 && (o.kernel == DS4HIP_DECODE_KERNEL_REGLOAD || (n_prob > 1 && q_stride < kQPrepWords) ||
+                           q_stride % 4 || reinterpret_cast<uintptr_t>(q) % 16)))
+        return ds4hip_set_last_error(kEINVAL);
     int page_shift = 0;
     if (page_table) {
         if (page_rows <= 0 || (page_rows & (page_rows - 1)) || page_table_stride <= 0)
@@ -2800,10 +2751,38 @@ extern "C" int ds4hip_flash_attn_decode_fp8(
     carve(A, workspace, pl);
     if (!row_idx && !page_table) A.phys = nullptr;
     const hipStream_t st = (hipStream_t)stream;
-    const int rc = q_is_f32 ? launch<true, true>(A, pl, st, phases, o)
+    const int rc = q_is_f32 ? launch<true, true>(A, pl, st, phases, o, q_is_f32 == 2)
                             : launch<true, false>(A, pl, st, phases, o);
     return ds4hip_set_last_error(rc);
 }
+
+namespace {
+// one 256-thread block per problem: producer lane (wave d, lane) of the flat
+// kernel converts its fragments of Q
+__global__ __launch_bounds__(256) void q_prep_kernel(const float *q, long long q_stride, uint32_t *out,
+                                                     long long out_stride) {
+    const int d = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    uint32_t qf8[4][3][8];
+    int qsc[3];
+    half8_t qt[2], qtl[2];
+    q_prep_lane<true, true>(q + (long long)blockIdx.x * q_stride + (long long)(16 * d + (lane & 15)) * kD, lane >> 4,
+                            qf8, qsc, qt, qtl);
+    q_prep_store(reinterpret_cast<uint4_t *>(out + (long long)blockIdx.x * out_stride), threadIdx.x, qf8, qsc, qt,
+                 qtl);
+}
+}  // namespace
+
+extern "C" int ds4hip_flash_attn_q_prep_f32(const float *q, long long q_stride, int n_prob, void *out,
+                                            long long out_stride, void *stream) {
+    if (!q || !out || n_prob <= 0 || n_prob > kMaxProb || (n_prob > 1 && (q_stride < kH * kD || out_stride < kQPrepWords)) ||
+        (reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out)) % 16 || q_stride % 4 || out_stride % 4)
+        return ds4hip_set_last_error(kEINVAL);
+    hipLaunchKernelGGL(q_prep_kernel, dim3(n_prob), dim3(256), 0, (hipStream_t)stream, q, q_stride,
+                       static_cast<uint32_t *>(out), out_stride);
+    return ds4hip_set_last_error(hip_status(hipGetLastError()));
+}
+
+extern "C" long long ds4hip_flash_attn_q_prep_words(void) { return kQPrepWords; }
 
 // fp32 launchers of the reference (cuda/flash_attn.cuh:73,142). The split-K
 // partials live in a workspace: the caller's (the _prealloc forms), or the

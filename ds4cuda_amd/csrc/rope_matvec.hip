@@ -17,6 +17,7 @@
 
 #include "ds4hip_common.h"
 #include "step_bodies.h"
+#include "q_prep.h"
 #include "../../include/ds4hip.h"
 
 #include <algorithm>
@@ -880,7 +881,7 @@ namespace {
 constexpr int kPrologueRot = 64;   // the model's RoPE tail (the session's row layout)
 struct PrologueArgs {
     ds4hip_token_prologue a;
-    int blk_push, blk_comp[2], blk_q, blk_hw;   // first workgroup of each job (blk_hw + n_hw = grid)
+    int blk_push, blk_comp[2], blk_q, blk_hw, blk_qp;   // first workgroup of each job (blk_qp + n_qp = grid)
     int width[2], pos_mod[2];
     MvEpilogue eq, ehw;
 };
@@ -917,8 +918,18 @@ __global__ __launch_bounds__(256) void token_prologue_kernel(const PrologueArgs 
         mv_f16_rows<kMvRope>(xs, a.q_w, a.q_out, a.q_heads * a.q_head_dim, a.q_in, P.eq, b - P.blk_q);
         return;
     }
-    stage(a.x, a.in_dim);
-    mv_f16_rows<kMvScale>(xs, a.hw_w, a.hw_out, a.hw_rows, a.in_dim, P.ehw, b - P.blk_hw);
+    if (b < P.blk_qp) {
+        stage(a.x, a.in_dim);
+        mv_f16_rows<kMvScale>(xs, a.hw_w, a.hw_out, a.hw_rows, a.in_dim, P.ehw, b - P.blk_hw);
+        return;
+    }
+    // the decode query: producer lane (wave d, lane) of the flat decode kernel
+    const int d = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    uint32_t qf8[4][3][8];
+    int qsc[3];
+    half8_t qt[2], qtl[2];
+    q_prep_lane<true, true>(a.qp_q + (16 * d + (lane & 15)) * 512, lane >> 4, qf8, qsc, qt, qtl);
+    q_prep_store(static_cast<uint4_t *>(a.qp_out), threadIdx.x, qf8, qsc, qt, qtl);
 }
 }  // namespace
 
@@ -962,6 +973,12 @@ extern "C" int ds4hip_token_prologue_f32(const ds4hip_token_prologue *a, void *s
         if (!a->hw_out || a->hw_rows <= 0) return ds4hip_set_last_error(kEINVAL);
         P.ehw.scale = a->hw_scale;
         blk += (a->hw_rows + 4 * kMvRows - 1) / (4 * kMvRows);
+    }
+    P.blk_qp = blk;
+    if (a->qp_q) {
+        if (!a->qp_out || (reinterpret_cast<uintptr_t>(a->qp_q) | reinterpret_cast<uintptr_t>(a->qp_out)) % 16)
+            return ds4hip_set_last_error(kEINVAL);
+        blk += 1;
     }
     hipLaunchKernelGGL(token_prologue_kernel, dim3(blk), dim3(256), 0, (hipStream_t)stream, P);
     return ds4hip_set_last_error(hip_status(hipGetLastError()));

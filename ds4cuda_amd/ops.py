@@ -14,7 +14,7 @@ from dataclasses import dataclass
 
 import torch
 
-from ._lib import Ds4HipError, call
+from ._lib import Ds4HipError, call, lib
 
 N_HEAD = 64
 HEAD_DIM = 512
@@ -180,12 +180,42 @@ def decode_fp8_workspace_bytes(n_rows_per_prob) -> int:
     return out.value
 
 
+def q_prep_words() -> int:
+    """32-bit words of one problem's converted query (flash_attn_q_prep_f32)."""
+    return lib().ds4hip_flash_attn_q_prep_words()
+
+
+def flash_attn_q_prep_f32(q, out=None, stream=None):
+    """q [n_prob, 64, 512] fp32 -> int32 [n_prob, q_prep_words()]: the form
+    the FP8 decode's flat-stage kernel builds from an fp32 Q at its start;
+    passing it as q to flash_attn_decode_fp8 (or Session.decode) gives the
+    fp32-Q results bit for bit without that work."""
+    n_prob = q.numel() // (N_HEAD * HEAD_DIM)
+    _check(q, torch.float32, n_prob * N_HEAD * HEAD_DIM, "q")
+    w = q_prep_words()
+    if out is None:
+        out = torch.empty((n_prob, w), dtype=torch.int32, device=q.device)
+    _check(out, torch.int32, n_prob * w, "out")
+    call("ds4hip_flash_attn_q_prep_f32", _ptr(q), N_HEAD * HEAD_DIM, n_prob, _ptr(out), w, _stream(stream))
+    return out
+
+
+def _q_mode(q):
+    """(q_is_f32 argument, problem stride) of a decode query tensor."""
+    if q.dtype == torch.int32:
+        return 2, q_prep_words()
+    if q.dtype not in (torch.bfloat16, torch.float32):
+        raise Ds4HipError("q must be bf16, fp32 or a converted fp32 query (int32)", -22)
+    return int(q.dtype == torch.float32), N_HEAD * HEAD_DIM
+
+
 def flash_attn_decode_fp8(q, sinks, out, cache: Fp8KVCache, n_rows_per_prob, *, row_base=None,
                           row_base_stride=0, row_idx=None, page_table=None, page_rows=256,
                           workspace=None, phases=3, exact_p=False, kernel="auto", stream=None):
     """Decode attention of n_prob single-query problems over the FP8 cache.
 
-    q [n_prob, 64, 512] bf16 or fp32; sinks [n_prob, 64] fp32; out
+    q [n_prob, 64, 512] bf16 or fp32 (or int32 [n_prob, q_prep_words()], a
+    converted fp32 Q from flash_attn_q_prep_f32); sinks [n_prob, 64] fp32; out
     [n_prob, 64, 512] fp32; n_rows_per_prob: host ints. Row r of problem p is
     position row_idx[p, r] (or r), mapped through page_table[p] (pages of
     page_rows rows) or offset by row_base[p] (int64 tensor) / p*row_base_stride.
@@ -193,9 +223,8 @@ def flash_attn_decode_fp8(q, sinks, out, cache: Fp8KVCache, n_rows_per_prob, *, 
     (the register-load kernel for direct rows too).
     """
     n_prob = len(n_rows_per_prob)
-    if q.dtype not in (torch.bfloat16, torch.float32):
-        raise Ds4HipError("q must be bf16 or fp32", -22)
-    _check(q, q.dtype, n_prob * N_HEAD * HEAD_DIM, "q")
+    q_mode, q_stride = _q_mode(q)
+    _check(q, q.dtype, n_prob * q_stride, "q")
     _check(sinks, torch.float32, n_prob * N_HEAD, "sinks")
     _check(out, torch.float32, n_prob * N_HEAD * HEAD_DIM, "out")
     _check(row_base, torch.int64, n_prob, "row_base")
@@ -206,9 +235,8 @@ def flash_attn_decode_fp8(q, sinks, out, cache: Fp8KVCache, n_rows_per_prob, *, 
     if workspace is None or workspace.numel() < need:
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
     _dev(workspace, "workspace", need)
-    call("ds4hip_flash_attn_decode_fp8", _ptr(q), int(q.dtype == torch.float32),
-         N_HEAD * HEAD_DIM, _ptr(sinks), N_HEAD, _ptr(out), N_HEAD * HEAD_DIM,
-         _ptr(cache.codes), _ptr(cache.sexp), _ptr(cache.tail), C.cast(counts, C.c_void_p),
+    call("ds4hip_flash_attn_decode_fp8", _ptr(q), q_mode, q_stride, _ptr(sinks), N_HEAD, _ptr(out),
+         N_HEAD * HEAD_DIM, _ptr(cache.codes), _ptr(cache.sexp), _ptr(cache.tail), C.cast(counts, C.c_void_p),
          n_prob, _ptr(row_base), int(row_base_stride), _ptr(row_idx),
          row_idx.shape[-1] if row_idx is not None else 0, _ptr(page_table),
          page_table.shape[-1] if page_table is not None else 0, int(page_rows), N_HEAD,

@@ -171,14 +171,16 @@ class Session:
         return ri.value, n.value, sel.value
 
     def decode(self, il, q, sinks, out, n_selected=-1, workspace=None, exact_p=False, stream=None):
-        """Decode attention of one query (q [64,512] bf16/fp32) over layer il's
+        """Decode attention of one query (q [64,512] bf16/fp32, or an fp32 one
+        converted by ops.flash_attn_q_prep_f32 / the token prologue) over layer il's
         valid ring rows plus its first n_selected compressed rows (all n_comp
         when n_selected < 0; the selection written at layer_rows()' selected
         address otherwise). exact_p: P as f16 hi + lo (the register kernels)
         instead of one f16 (the flat-stage kernel)."""
-        from .ops import HEAD_DIM, N_HEAD, N_ROT, decode_fp8_workspace_bytes, decode_opts
+        from .ops import HEAD_DIM, N_HEAD, _q_mode, decode_fp8_workspace_bytes, decode_opts, N_ROT
         ri, n, _ = self.layer_rows(il, n_selected)
-        _check(q, q.dtype, N_HEAD * HEAD_DIM, "q")
+        q_mode, q_stride = _q_mode(q)
+        _check(q, q.dtype, q_stride, "q")
         _check(sinks, torch.float32, N_HEAD, "sinks")
         _check(out, torch.float32, N_HEAD * HEAD_DIM, "out")
         counts = (C.c_longlong * 1)(n)
@@ -186,8 +188,7 @@ class Session:
         if workspace is None or workspace.numel() < need:
             workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
         rb = self.layer(il).row_base      # the layer's rows start at its row_base
-        call("ds4hip_flash_attn_decode_fp8", _ptr(q), int(q.dtype == torch.float32),
-             N_HEAD * HEAD_DIM, _ptr(sinks), N_HEAD, _ptr(out), N_HEAD * HEAD_DIM,
+        call("ds4hip_flash_attn_decode_fp8", _ptr(q), q_mode, q_stride, _ptr(sinks), N_HEAD, _ptr(out), N_HEAD * HEAD_DIM,
              C.c_void_p(self.s.codes + rb * 448), C.c_void_p(self.s.sexp + rb * 8),
              C.c_void_p(self.s.tail + rb * 128), C.cast(counts, C.c_void_p), 1, None, 0,
              C.c_void_p(ri),

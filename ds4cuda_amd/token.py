@@ -36,7 +36,7 @@ import numpy as np
 import torch
 
 from ._lib import Ds4HipError, call, lib
-from .ops import _check, _ptr, _stream, decode_fp8_workspace_bytes
+from .ops import _check, _ptr, _stream, decode_fp8_workspace_bytes, q_prep_words
 from .session import N_LAYER, Session
 
 N_HEAD, HEAD_DIM, N_ROT, IDX_DIM, IDX_HEAD, N_EMBD = 64, 512, 64, 128, 64, 4096
@@ -55,7 +55,8 @@ class TokenPrologue(C.Structure):
                 ("in_dim", C.c_int), ("n_comp", C.c_int)] + _vp_fields("comp0_") + _vp_fields("comp1_") + \
                [("q_w", C.c_void_p), ("q_x", C.c_void_p), ("q_out", C.c_void_p), ("q_heads", C.c_int),
                 ("q_head_dim", C.c_int), ("q_in", C.c_int), ("q_pos", C.c_int), ("q_il", C.c_int),
-                ("hw_w", C.c_void_p), ("hw_out", C.c_void_p), ("hw_rows", C.c_int), ("hw_scale", C.c_float)]
+                ("hw_w", C.c_void_p), ("hw_out", C.c_void_p), ("hw_rows", C.c_int), ("hw_scale", C.c_float),
+                ("qp_q", C.c_void_p), ("qp_out", C.c_void_p)]
 
 
 def layer_ratio(il: int) -> int:
@@ -196,6 +197,7 @@ class TokenSlice:
         self.select = torch.empty(lib().ds4hip_indexer_select_scratch_bytes(cap), dtype=torch.uint8,
                                   device=dev)
         self.kqv = f(N_HEAD * HEAD_DIM)
+        self.q_pre = torch.empty(q_prep_words(), dtype=torch.int32, device=dev)   # fused: Step 13's query
         self.out_ws = torch.empty(lib().ds4hip_attn_out_decode_workspace_bytes(N_HEAD, HEAD_DIM, N_OUT_GROUP,
                                                                                N_LORA_O),
                                   dtype=torch.uint8, device=dev)
@@ -302,6 +304,8 @@ class TokenSlice:
             P.q_heads, P.q_head_dim, P.q_in, P.q_pos, P.q_il = IDX_HEAD, IDX_DIM, Q_LORA, pos, il
             P.hw_w, P.hw_out, P.hw_rows = _ptr(w["idx_proj"]), _ptr(self.w_idx), IDX_HEAD
             P.hw_scale = 1.0 / np.sqrt(IDX_DIM * IDX_HEAD)
+        # the decode query, converted for Step 13's kernel
+        P.qp_q, P.qp_out = _ptr(q_cur[il]), _ptr(self.q_pre)
         call("ds4hip_token_prologue_f32", C.byref(P), st)
         if emit:   # the emits and their row pushes
             call("ds4hip_compressor_emit_f32", 1, _ptr(w["comp_norm"]), HEAD_DIM, r, pos, il,
@@ -320,8 +324,7 @@ class TokenSlice:
                  _ptr(self.scores), _ptr(self.select), None, _vp(sel), st)
             n_sel = self.top_k
         # Step 13
-        sess.decode(il, q_cur[il].reshape(-1), w["sinks"], self.kqv, n_selected=n_sel,
-                    workspace=self.dec_ws, stream=stream)
+        sess.decode(il, self.q_pre, w["sinks"], self.kqv, n_selected=n_sel, workspace=self.dec_ws, stream=stream)
         # Steps 14-16
         call("ds4hip_attn_out_decode_f32", _ptr(self.kqv), _ptr(w["out_a"]), _ptr(w["out_b"]), _ptr(out[il]),
              N_HEAD, HEAD_DIM, N_ROT, pos, il, N_OUT_GROUP, N_LORA_O, N_EMBD, _ptr(self.out_ws),

@@ -142,7 +142,10 @@ typedef struct ds4hip_decode_opts {
  * independent single-query problems in one launch pair — layers of one token,
  * or sequences of a batch:
  *   q      problem p at q + p*q_stride elements, [64][512], bf16 bits
- *          (q_is_f32 = 0) or fp32 (q_is_f32 = 1)
+ *          (q_is_f32 = 0) or fp32 (q_is_f32 = 1), or (q_is_f32 = 2) an fp32 Q
+ *          as ds4hip_flash_attn_q_prep_f32 wrote it (q_stride in 32-bit
+ *          words; same results as q_is_f32 = 1 on the unconverted Q, bit for
+ *          bit; not with DS4HIP_DECODE_KERNEL_REGLOAD)
  *   sinks  sinks + p*sinks_stride, [64] fp32
  *   out    out + p*out_stride, [64][512] fp32
  *   n_rows_per_prob  HOST array [n_prob] of row counts (n_prob <= 128)
@@ -172,6 +175,17 @@ int ds4hip_flash_attn_decode_fp8(const void *q, int q_is_f32, long long q_stride
                                  int page_table_stride, int page_rows, int n_head, int head_dim,
                                  int n_rot, long long n_cache_rows, const ds4hip_decode_opts *opts,
                                  void *workspace, size_t workspace_bytes, int phases, void *stream);
+
+/* The fp32 queries of n_prob decode problems (q + p*q_stride floats,
+ * [64][512]) converted to the form the FP8 decode's flat-stage kernel computes
+ * from them at its start (three E4M3 parts with per-head E8M0 scales, f16 hi +
+ * lo RoPE tail), written to out + p*out_stride 32-bit words
+ * (ds4hip_flash_attn_q_prep_words() words each, 16-byte aligned). Decoding
+ * with q_is_f32 = 2 then skips that work. Additive: no counterpart in the
+ * reference, whose decode takes the fp32 Q (cuda/flash_attn.cuh:9-26). */
+int ds4hip_flash_attn_q_prep_f32(const float *q, long long q_stride, int n_prob, void *out,
+                                 long long out_stride, void *stream);
+long long ds4hip_flash_attn_q_prep_words(void);
 
 /* ---- chunked prefill ------------------------------------------------------------- */
 
@@ -266,7 +280,9 @@ int ds4hip_mul_mv_q8_0_q8_0_f32_prealloc(const void *W, const float *x, float *y
  *   - if q_w: the indexer query, q_out = RoPE(q_w . q_x) (as
  *     ds4hip_mul_mv_f16_rope_f32 with n_rot 64);
  *   - if hw_w: the head weights, hw_out = (hw_w . x) * hw_scale (as
- *     ds4hip_mul_mv_f16_scaled_f32).
+ *     ds4hip_mul_mv_f16_scaled_f32);
+ *   - if qp_q: the layer's decode query qp_q [64][512] fp32 converted for
+ *     the decode into qp_out (as ds4hip_flash_attn_q_prep_f32 of one problem).
  * head_dim 512 and n_rot 64 (the session's rows). The results are
  * bit-identical to those launches. in_dim, q_in <= 8192. */
 typedef struct ds4hip_token_prologue {
@@ -292,6 +308,8 @@ typedef struct ds4hip_token_prologue {
     float *hw_out;
     int hw_rows;
     float hw_scale;
+    const float *qp_q;
+    void *qp_out;
 } ds4hip_token_prologue;
 int ds4hip_token_prologue_f32(const ds4hip_token_prologue *a, void *stream);
 

@@ -284,13 +284,52 @@ def test_fp8_fp32_q_kernels(gpu, counts):
         check(outs[True][p], ref)
 
 
-@pytest.mark.parametrize("q_f32,paged", [(False, False), (True, False), (False, True)])
+@pytest.mark.parametrize("form", ["direct", "list", "pages"])
+def test_fp8_converted_q_equals_fp32_q(gpu, form):
+    """An fp32 Q converted ahead (flash_attn_q_prep_f32, int32 form) decodes
+    to the fp32-Q results bit for bit: direct rows over four problems (one
+    empty, one a single row, one ragged), a position list and pages (the phys
+    pass), both with problems of one and of several workgroups."""
+    rng = np.random.default_rng(95)
+    if form == "direct":
+        counts = [1, 0, 3000, 777]
+        total = int(sum(counts))
+        cache, _ = make_cache(total, 96, gpu)
+        base = np.concatenate([[0], np.cumsum(counts)[:-1]])
+        kw = dict(row_base=torch.from_numpy(base.astype(np.int64)).to(gpu))
+    else:
+        cache, _ = make_cache(4096, 96, gpu)
+        counts = [700, 33]
+        idx = np.stack([np.sort(rng.choice(4096, 700, replace=False)) for _ in range(2)]).astype(np.int32)
+        kw = dict(row_idx=torch.from_numpy(idx).to(gpu))
+        if form == "pages":
+            pt = np.stack([rng.permutation(16), rng.permutation(16)]).astype(np.int32)
+            kw.update(page_table=torch.from_numpy(pt).to(gpu), page_rows=256)
+    n = len(counts)
+    qf = torch.from_numpy(synth.normal(97, 2, n * 64 * 512).reshape(n, 64, 512) * 2.0).to(gpu)
+    sinks = torch.from_numpy(sinks_for(98, n)).to(gpu)
+    qp = ops.flash_attn_q_prep_f32(qf)
+    assert qp.shape == (n, ops.q_prep_words()) and qp.dtype == torch.int32
+    outs = []
+    for q in (qf, qp):
+        out = torch.zeros((n, 64, 512), dtype=torch.float32, device=gpu)
+        ops.flash_attn_decode_fp8(q, sinks, out, cache, counts, **kw)
+        torch.cuda.synchronize()
+        outs.append(out.cpu().numpy())
+    assert np.isfinite(outs[0]).all()
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+
+
+@pytest.mark.parametrize("q_f32,paged", [(False, False), (True, False), (False, True), ("pre", False),
+                                         ("pre", True)])
 def test_fp8_gathered_rows_outside_the_cache(gpu, q_f32, paged):
     """A row list (or page table) naming rows outside the cache: the kernels
     read no such row, finish normally and write NaN for every output of that
     problem; the other problems of the launch are unaffected. Paths: bf16 Q
     with a row list (resolved in the partial kernel), fp32 Q with a row list
-    and bf16 Q with pages (both resolved by the phys pass)."""
+    and bf16 Q with pages (both resolved by the phys pass); "pre": the fp32 Q
+    converted ahead (flash_attn_q_prep_f32), where the flat kernel's copy
+    issue detects the bad rows."""
     n_rows = 1024
     cache, (codes, sexp, tail) = make_cache(n_rows, 81, gpu)
     n_prob, n_list = 3, 300
@@ -313,6 +352,8 @@ def test_fp8_gathered_rows_outside_the_cache(gpu, q_f32, paged):
     sinks = sinks_for(84, n_prob)
     q = (torch.from_numpy(qf).to(gpu) if q_f32 else
          torch.from_numpy(bits.view(np.int16)).to(gpu).view(torch.bfloat16))
+    if q_f32 == "pre":
+        q = ops.flash_attn_q_prep_f32(q)
     out = torch.zeros((n_prob, 64, 512), dtype=torch.float32, device=gpu)
     kw = dict(row_idx=torch.from_numpy(bad).to(gpu))
     if paged:

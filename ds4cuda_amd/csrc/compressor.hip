@@ -38,8 +38,8 @@ __global__ __launch_bounds__(256) void comp_project_kernel(
         const uint16_t *__restrict__ w_ape, int in_dim, int width, int ratio, int pos_mod,
         float *__restrict__ state_kv, float *__restrict__ state_score, float *__restrict__ kv_cur,
         float *__restrict__ sc_cur) {
-    __shared__ float xs[kMaxIn];
-    for (int i = threadIdx.x; i < in_dim; i += 256) xs[i] = x[i];
+    __shared__ __attribute__((aligned(16))) float xs[kMaxIn];
+    stage_to_lds(xs, x, in_dim);
     __syncthreads();
     comp_project_rows<kW32>(xs, w_kv, w_gate, w_ape, in_dim, width, ratio, pos_mod, state_kv, state_score,
                             kv_cur, sc_cur, blockIdx.x);

@@ -135,6 +135,31 @@ __device__ inline float f16_bits_to_f32(uint16_t b) {
 __host__ inline int hip_status(hipError_t e) { return e == hipSuccess ? 0 : kHipErrBase - (int)e; }
 
 
+// x[0, n) into LDS xs by a 256-thread block: 16-byte loads, eight per thread
+// issued before any is written, so a block pays one memory latency per 8192
+// floats instead of one per 256 (a loop of dependent 4-byte copies). Ends
+// without a barrier.
+__device__ inline void stage_to_lds(float *xs, const float *x, int n) {
+    if (((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(xs)) & 15) == 0 && (n & 3) == 0) {
+        const int n4 = n >> 2;
+        const float4_t *x4 = reinterpret_cast<const float4_t *>(x);
+        float4_t *s4 = reinterpret_cast<float4_t *>(xs);
+        for (int b = 0; b < n4; b += 256 * 8) {
+            float4_t v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)   // clamped, not branched: no wait between the loads
+                v[u] = x4[min(b + 256 * u + (int)threadIdx.x, n4 - 1)];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int i = b + 256 * u + (int)threadIdx.x;
+                if (i < n4) s4[i] = v[u];
+            }
+        }
+    } else {
+        for (int i = threadIdx.x; i < n; i += 256) xs[i] = x[i];
+    }
+}
+
 // ---- wave-per-rows GEMV ---------------------------------------------------------
 // acc[r] += dot(row r of W, x) for kRows rows held by one wave, x staged in LDS.
 // Each lane reads 16-byte chunks (8 f16 or 4 fp32 weights) of every row at

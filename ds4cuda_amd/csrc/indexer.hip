@@ -72,7 +72,7 @@ __device__ inline void stage_query(float *qs, const float *q, int n_head) {
 #pragma unroll
     for (int i = 0; i < kMaxHeads * kMaxDim / 4 / 256; ++i) {
         const int k = (int)threadIdx.x + 256 * i;
-        v[i] = k < n4 ? reinterpret_cast<const float4_t *>(q)[k] : float4_t{0, 0, 0, 0};
+        v[i] = reinterpret_cast<const float4_t *>(q)[min(k, n4 - 1)];   // clamped: no branch between the loads
     }
 #pragma unroll
     for (int i = 0; i < kMaxHeads * kMaxDim / 4 / 256; ++i) {
@@ -370,7 +370,7 @@ __global__ __launch_bounds__(256) void score_kernel(const float *__restrict__ q,
     const int c = blockIdx.x * 256 + threadIdx.x;
     float s = 0.0f;
     {
-        for (int i = threadIdx.x; i < n_head * head_dim; i += 256) qs[i] = q[i];
+        stage_to_lds(qs, q, n_head * head_dim);
         for (int i = threadIdx.x; i < n_head; i += 256) ws[i] = w[i];
         __syncthreads();
         if (c < n_comp) s = score_any<kKind>(qs, ws, keys, c, n_head, head_dim);
@@ -906,10 +906,44 @@ __global__ __launch_bounds__(256) void score_heads_kernel(const BatchArgs A) {
     __shared__ __attribute__((aligned(16))) float ks[kHeadsKpb * kMaxDim];
     const float *qg = A.q + (size_t)s * A.n_head * kMaxDim;
     stage_query<kQStride>(qs, qg, A.n_head);
-    // the block's keys, widened to fp32 (rows past n are zeros, never stored)
-    for (int i = threadIdx.x; i < kHeadsKpb * kMaxDim; i += 256) {
-        const int kr = i / kMaxDim, d = i % kMaxDim;
-        ks[i] = c0 + kr < n ? key_elem<kKind>(A.keys, (size_t)(k0 + c0 + kr) * kMaxDim + d) : 0.0f;
+    // the block's keys, widened to fp32 (rows past n are zeros, never stored):
+    // 16-byte loads, all issued before any is used (rows past n load row
+    // n - 1, so there is no branch between them)
+    constexpr int kEsz = kKind == 0 ? 4 : 2;
+    constexpr int kPer = 16 / kEsz;                    // elements per load
+    constexpr int kRowVecs = kMaxDim / kPer;
+    constexpr int kLoads = kHeadsKpb * kRowVecs / 256;
+    const int rows_here = min(n - c0, kHeadsKpb);
+    const char *kbase = static_cast<const char *>(A.keys) + (size_t)(k0 + c0) * kMaxDim * kEsz;
+    if (rows_here > 0 && (reinterpret_cast<uintptr_t>(kbase) & 15) == 0) {
+        uint4_t kv[kLoads];
+#pragma unroll
+        for (int u = 0; u < kLoads; ++u) {
+            const int vi = (int)threadIdx.x + 256 * u;
+            const int kr = min(vi / kRowVecs, rows_here - 1);
+            kv[u] = reinterpret_cast<const uint4_t *>(kbase)[kr * kRowVecs + vi % kRowVecs];
+        }
+#pragma unroll
+        for (int u = 0; u < kLoads; ++u) {
+            const int vi = (int)threadIdx.x + 256 * u;
+            const bool in = vi / kRowVecs < rows_here;
+            float f[kPer];
+#pragma unroll
+            for (int e = 0; e < kPer; ++e) {
+                const uint32_t w = kv[u][e * kEsz / 4];
+                const uint16_t h = (uint16_t)(e & 1 ? w >> 16 : w & 0xFFFF);
+                f[e] = kKind == 0 ? __uint_as_float(kv[u][e]) : (kKind == 1 ? f16_bits_to_f32(h) : bf16_to_f32(h));
+                f[e] = in ? f[e] : 0.0f;
+            }
+#pragma unroll
+            for (int e = 0; e < kPer; e += 4)
+                *reinterpret_cast<float4_t *>(ks + vi * kPer + e) = float4_t{f[e], f[e + 1], f[e + 2], f[e + 3]};
+        }
+    } else {
+        for (int i = threadIdx.x; i < kHeadsKpb * kMaxDim; i += 256) {
+            const int kr = i / kMaxDim, d = i % kMaxDim;
+            ks[i] = c0 + kr < n ? key_elem<kKind>(A.keys, (size_t)(k0 + c0 + kr) * kMaxDim + d) : 0.0f;
+        }
     }
     __syncthreads();
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;

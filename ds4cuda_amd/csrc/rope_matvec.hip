@@ -201,8 +201,8 @@ __global__ __launch_bounds__(256) void mv_f16_kernel(const uint16_t *__restrict_
                                                      const float *__restrict__ x,
                                                      float *__restrict__ y, int out_dim,
                                                      int in_dim, MvEpilogue E) {
-    extern __shared__ float xs[];
-    for (int i = threadIdx.x; i < in_dim; i += 256) xs[i] = x[i];
+    extern __shared__ __attribute__((aligned(16))) float xs[];
+    stage_to_lds(xs, x, in_dim);
     __syncthreads();
     mv_f16_rows<kEpi>(xs, w, y, out_dim, in_dim, E, blockIdx.x);
 }
@@ -887,11 +887,11 @@ struct PrologueArgs {
 };
 
 __global__ __launch_bounds__(256) void token_prologue_kernel(const PrologueArgs P) {
-    __shared__ float xs[kCompMaxIn];
+    __shared__ __attribute__((aligned(16))) float xs[kCompMaxIn];
     const ds4hip_token_prologue &a = P.a;
     const int b = blockIdx.x;
     auto stage = [&](const float *x, int n) {
-        for (int i = threadIdx.x; i < n; i += 256) xs[i] = x[i];
+        stage_to_lds(xs, x, n);
         __syncthreads();
     };
     if (b < P.blk_comp[0]) {   // the FP8 push: one 64-lane row
@@ -955,7 +955,7 @@ extern "C" int ds4hip_token_prologue_f32(const ds4hip_token_prologue *a, void *s
             return ds4hip_set_last_error(kEINVAL);
         P.width[c] = (ratio[c] == 4 ? 2 : 1) * hdo[c];
         P.pos_mod[c] = pos[c] % ratio[c];
-        blk += (2 * P.width[c] + 3) / 4;
+        blk += (2 * P.width[c] + 4 * kCpRows - 1) / (4 * kCpRows);
     }
     P.blk_q = blk;
     if (a->q_w) {

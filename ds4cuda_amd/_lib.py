@@ -47,6 +47,7 @@ SIGNATURES: dict[str, list] = {
     "ds4hip_flash_attn_q_prep_words": [],
     "ds4hip_compressor_emit_f32": [_i, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp],
     "ds4hip_attn_out_decode_f32": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _sz, _vp],
+    "ds4hip_attn_out_decode_q8_f32": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _sz, _vp],
     "ds4hip_mul_mv_q8_0_q8_0_grouped_f32": [_vp, _vp, _vp, _i, _i, _i, _vp],
     "ds4hip_mul_mv_q8_0_q8_0_grouped_f32_prealloc": [_vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp],
     "ds4hip_mul_mv_q8_0_q8_0_f32_prealloc": [_vp, _vp, _vp, _i, _i, _vp, _vp, _vp],

@@ -32,6 +32,7 @@
 
 #include "ds4hip_common.h"
 #include "q_prep.h"
+#include "rope.h"
 #include "../../include/ds4hip.h"
 
 #include <algorithm>
@@ -101,7 +102,62 @@ struct DecodeArgs {
     float *ws_o;                     // [slot][64][512]
     float *ws_ml;                    // [slot][2][64]
     int *ws_prob;                    // [slot]
+    // merge output in the rotated Q8_0 form (DS4HIP_DECODE_OUT_ROPE_Q8)
+    int out_q8;
+    int rope_pos;
+    RopeParams rope;
+    int8_t *q8_out;
+    float *q8_scale;
 };
+
+// The rotation coefficients of dims dim0 .. dim0 + 3 for merge_store (out_q8
+// and tail dims only), computed at the merge's start, under its loads.
+struct MergeRope {
+    float c[2], s[2];
+};
+__device__ inline MergeRope merge_rope(const DecodeArgs &A, int dim0) {
+    MergeRope r = {{1.0f, 1.0f}, {0.0f, 0.0f}};
+    constexpr int kNope = kD - kRot;
+    if (A.out_q8 && dim0 >= kNope) {
+        rope_cs((dim0 - kNope) / 2, A.rope_pos, A.rope, r.c[0], r.s[0]);
+        rope_cs((dim0 + 2 - kNope) / 2, A.rope_pos, A.rope, r.c[1], r.s[1]);
+    }
+    // here, not sunk next to their use at the end
+    asm volatile("" : "+v"(r.c[0]), "+v"(r.c[1]), "+v"(r.s[0]), "+v"(r.s[1]));
+    return r;
+}
+
+// The merge's result for dims dim0 .. dim0 + 3 of head h of problem p: into
+// out, or (out_q8) rotated by the inverse tail RoPE and quantized as Q8_0,
+// with the arithmetic of rope_q8_kernel. The 8 lanes of a 32-dim block are
+// consecutive lanes of one wave, all present.
+__device__ inline void merge_store(const DecodeArgs &A, int p, int h, int dim0, float4_t res, const MergeRope &R) {
+    const long long o = (long long)p * (kH * kD) + h * kD + dim0;
+    if (!A.out_q8) {
+        *reinterpret_cast<float4_t *>(A.out + (long long)p * A.out_stride + h * kD + dim0) = res;
+        return;
+    }
+    float v[4] = {res[0], res[1], res[2], res[3]};
+    constexpr int kNope = kD - kRot;
+    if (dim0 >= kNope) {
+        rope_apply(v[0], v[1], R.c[0], R.s[0], v[0], v[1]);
+        rope_apply(v[2], v[3], R.c[1], R.s[1], v[2], v[3]);
+    }
+    float a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+#pragma unroll
+    for (int off = 4; off > 0; off >>= 1) a = fmaxf(a, __shfl_xor(a, off));
+    const float dq = a / 127.0f;
+    const float id = dq != 0.0f ? 1.0f / dq : 0.0f;
+    uint32_t packed = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        int q = (int)__builtin_rintf(v[i] * id);
+        q = q > 127 ? 127 : (q < -128 ? -128 : q);
+        packed |= (uint32_t)(q & 0xFF) << (8 * i);
+    }
+    *reinterpret_cast<uint32_t *>(A.q8_out + o) = packed;
+    if ((dim0 & 31) == 0) A.q8_scale[o / 32] = dq;
+}
 
 // bytes [0,1] (kHi = false) or [2,3] (kHi = true) of w, times scale, to f16
 template <bool kHi>
@@ -2333,6 +2389,7 @@ __global__ __launch_bounds__(128) void decode_merge_kernel(const DecodeArgs A) {
     const int h = blockIdx.y;
     const int tid = threadIdx.x;
     const float sink = A.sinks[(long long)p * A.sinks_stride + h] * kLog2e;
+    const MergeRope R = merge_rope(A, 4 * tid);
     const long long b0 = A.start[p], b1 = b0 + A.count[p];
     long long s0 = 0, n_slot = 0;
     if (b1 > b0) {
@@ -2384,7 +2441,7 @@ __global__ __launch_bounds__(128) void decode_merge_kernel(const DecodeArgs A) {
     }
     // a problem that met a row outside the cache gets NaN, never a plausible value
     const float4_t res = bad ? float4_t{NAN, NAN, NAN, NAN} : acc * (1.0f / den);
-    *reinterpret_cast<float4_t *>(A.out + (long long)p * A.out_stride + h * kD + 4 * tid) = res;
+    merge_store(A, p, h, 4 * tid, res, R);
 }
 
 // The merge for problems of many slots (a long problem split over many
@@ -2408,6 +2465,7 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_wide_kernel(const 
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const float sink = A.sinks[(long long)p * A.sinks_stride + h] * kLog2e;
+    const MergeRope R = merge_rope(A, half * (kD / 2) + 4 * lane);
     const long long b0 = A.start[p], b1 = b0 + A.count[p];
     long long s0 = 0, n_slot = 0;
     if (b1 > b0) {
@@ -2471,8 +2529,7 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_wide_kernel(const 
         acc = ((acc + s_acc[0][lane]) + s_acc[1][lane]) + s_acc[2][lane];
         // a problem that met a row outside the cache gets NaN, never a plausible value
         const float4_t res = bad ? float4_t{NAN, NAN, NAN, NAN} : acc * (1.0f / den);
-        *reinterpret_cast<float4_t *>(A.out + (long long)p * A.out_stride + h * kD + half * (kD / 2) +
-                                      4 * lane) = res;
+        merge_store(A, p, h, half * (kD / 2) + 4 * lane, res, R);
     }
 }
 
@@ -2692,9 +2749,12 @@ extern "C" int ds4hip_flash_attn_decode_fp8(
     if (phases < 1 || phases > 3 || n_head != kH || head_dim != kD || n_rot != kRot || n_prob <= 0 || n_prob > kMaxProb ||
         !n_rows_per_prob || !q || !sinks || !out || !codes || !sexp || !tail || !workspace || n_cache_rows <= 0)
         return ds4hip_set_last_error(kEINVAL);
-    const ds4hip_decode_opts o = opts ? *opts : ds4hip_decode_opts{0, DS4HIP_DECODE_KERNEL_AUTO};
+    const ds4hip_decode_opts o = opts ? *opts : ds4hip_decode_opts{};
     if ((o.exact_p != 0 && o.exact_p != 1) ||
-        (o.kernel != DS4HIP_DECODE_KERNEL_AUTO && o.kernel != DS4HIP_DECODE_KERNEL_REGLOAD))
+        (o.kernel != DS4HIP_DECODE_KERNEL_AUTO && o.kernel != DS4HIP_DECODE_KERNEL_REGLOAD) ||
+        (o.out_form != DS4HIP_DECODE_OUT_F32 && o.out_form != DS4HIP_DECODE_OUT_ROPE_Q8) ||
+        (o.out_form == DS4HIP_DECODE_OUT_ROPE_Q8 &&
+         (!o.q8_out || !o.q8_scale || o.out_pos < 0 || o.out_il < 0 || reinterpret_cast<uintptr_t>(o.q8_out) % 4)))
         return ds4hip_set_last_error(kEINVAL);
     // q_is_f32 2: the converted form (only the flat-stage kernel reads it); its
     // problems kQPrepWords apart at least
@@ -2750,6 +2810,13 @@ extern "C" int ds4hip_flash_attn_decode_fp8(
     A.total = A.start[n_prob];
     carve(A, workspace, pl);
     if (!row_idx && !page_table) A.phys = nullptr;
+    if (o.out_form == DS4HIP_DECODE_OUT_ROPE_Q8) {
+        A.out_q8 = 1;
+        A.rope_pos = o.out_pos;
+        A.rope = rope_params(kRot, o.out_il, true);
+        A.q8_out = o.q8_out;
+        A.q8_scale = o.q8_scale;
+    }
     const hipStream_t st = (hipStream_t)stream;
     const int rc = q_is_f32 ? launch<true, true>(A, pl, st, phases, o, q_is_f32 == 2)
                             : launch<true, false>(A, pl, st, phases, o);

@@ -18,6 +18,7 @@
 #include "ds4hip_common.h"
 #include "step_bodies.h"
 #include "q_prep.h"
+#include "rope.h"
 #include "../../include/ds4hip.h"
 
 #include <algorithm>
@@ -28,67 +29,6 @@ using namespace ds4hip;
 namespace {
 
 // ---- tail RoPE YaRN ---------------------------------------------------------------
-
-struct RopeParams {
-    float theta_scale;
-    float freq_scale;
-    float ext_factor;
-    float attn_factor;
-    float corr_low;
-    float corr_high;
-    float sin_sign;
-};
-
-// cuda/rope.cu:123-126
-int compress_ratio_of(int il) { return il < 2 ? 0 : ((il & 1) == 0 ? 4 : 128); }
-
-// cuda/rope.cu:214-250 (host-side parameter routing)
-RopeParams rope_params(int n_rot, int il, bool inverse) {
-    constexpr float kFreqBase = 10000.0f, kScale = 16.0f, kBetaFast = 32.0f, kBetaSlow = 1.0f;
-    constexpr float kCompressBase = 160000.0f;
-    constexpr int kOrigCtx = 65536;
-    const bool compressed = compress_ratio_of(il) != 0;
-    RopeParams P;
-    const float freq_base = compressed ? kCompressBase : kFreqBase;
-    P.freq_scale = compressed ? 1.0f / kScale : 1.0f;
-    P.ext_factor = compressed ? 1.0f : 0.0f;
-    P.attn_factor = 1.0f;
-    if (P.ext_factor != 0.0f) P.attn_factor /= 1.0f + 0.1f * logf(1.0f / P.freq_scale);
-    P.corr_low = P.corr_high = 0.0f;
-    if (P.ext_factor != 0.0f) {
-        const float pi = 3.14159265358979323846f;
-        auto corr_dim = [&](float target) {
-            return (float)n_rot * logf((float)kOrigCtx / (target * 2.0f * pi)) /
-                   (2.0f * logf(freq_base));
-        };
-        P.corr_low = fmaxf(0.0f, floorf(corr_dim(kBetaFast)));
-        P.corr_high = fminf((float)(n_rot - 1), ceilf(corr_dim(kBetaSlow)));
-    }
-    P.theta_scale = powf(freq_base, -2.0f / (float)n_rot);
-    P.sin_sign = inverse ? -1.0f : 1.0f;
-    return P;
-}
-
-// Rotation of pair t (dims n_nope + 2t, n_nope + 2t + 1) at position pos.
-__device__ inline void rope_pair(float x0, float x1, int t, int pos, const RopeParams &P, float &y0,
-                                 float &y1) {
-    float theta_extrap = (float)pos;
-    for (int k = 0; k < t; ++k) theta_extrap *= P.theta_scale;   // running product (rope.cu:172-177)
-    const float theta_interp = P.freq_scale * theta_extrap;
-    float theta = theta_interp;
-    float mscale = P.attn_factor;
-    if (P.ext_factor != 0.0f) {
-        // cuda/rope.cu:130-133 ramp, then the YaRN mix
-        const float y = ((float)((2 * t) / 2) - P.corr_low) / fmaxf(0.001f, P.corr_high - P.corr_low);
-        const float ramp_mix = (1.0f - fminf(1.0f, fmaxf(0.0f, y))) * P.ext_factor;
-        theta = theta_interp * (1.0f - ramp_mix) + theta_extrap * ramp_mix;
-        mscale *= 1.0f + 0.1f * logf(1.0f / P.freq_scale);
-    }
-    const float c = cosf(theta) * mscale;
-    const float s = P.sin_sign * sinf(theta) * mscale;
-    y0 = x0 * c - x1 * s;
-    y1 = x0 * s + x1 * c;
-}
 
 // pos_dev (optional): position per group of heads_per_pos consecutive heads.
 __global__ __launch_bounds__(64) void rope_tail_kernel(const float *__restrict__ x_in,
@@ -252,60 +192,118 @@ __device__ inline float q8_block_term(float dw, float dx, const uint32_t *q, con
     return dw * dx * (float)isum;
 }
 
+// kR rows per wave, all their weight loads in flight before any is used;
+// row r's sum is accumulated exactly as with one row per wave.
+template <int kR>
+__device__ inline void q8_rows(const uint8_t *__restrict__ W, const int8_t *__restrict__ xq,
+                               const float *__restrict__ xscale, const int (&row)[kR], int n_blocks, int rank,
+                               int grouped, int lane, float (&out)[kR]) {
+    const int8_t *xg[kR];
+    const float *sg[kR];
+    const uint8_t *wr[kR];
+    float acc[kR];
+#pragma unroll
+    for (int r = 0; r < kR; ++r) {
+        const int g = grouped ? row[r] / rank : 0;
+        xg[r] = xq + (size_t)g * n_blocks * 32;
+        sg[r] = xscale + (size_t)g * n_blocks;
+        wr[r] = W + (size_t)row[r] * n_blocks * 34;
+        acc[r] = 0.0f;
+    }
+    if ((n_blocks & 1) == 0 && (reinterpret_cast<uintptr_t>(W) & 3) == 0) {
+        const int n_pairs = n_blocks / 2;
+        for (int p0 = lane; p0 < n_pairs; p0 += 128) {
+            uint32_t d[kR][2][17];
+#pragma unroll
+            for (int r = 0; r < kR; ++r)
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const int p = min(p0 + 64 * u, n_pairs - 1);
+                    const uint32_t *wp = reinterpret_cast<const uint32_t *>(wr[r]);
+#pragma unroll
+                    for (int k = 0; k < 17; ++k) d[r][u][k] = wp[(size_t)p * 17 + k];
+                }
+#pragma unroll
+            for (int r = 0; r < kR; ++r)
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const int p = p0 + 64 * u;
+                    if (p >= n_pairs) break;
+                    const int b = 2 * p;
+                    uint32_t qe[8], qo[8];
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) {
+                        qe[k] = __builtin_amdgcn_alignbyte(d[r][u][k + 1], d[r][u][k], 2);   // bytes 2 + 4k ..
+                        qo[k] = d[r][u][k + 9];
+                    }
+                    const float dwe = f16_bits_to_f32((uint16_t)(d[r][u][0] & 0xFFFF));
+                    const float dwo = f16_bits_to_f32((uint16_t)(d[r][u][8] >> 16));
+                    acc[r] += q8_block_term(dwe, sg[r][b], qe, reinterpret_cast<const int *>(xg[r] + (size_t)b * 32));
+                    acc[r] += q8_block_term(dwo, sg[r][b + 1], qo,
+                                            reinterpret_cast<const int *>(xg[r] + (size_t)(b + 1) * 32));
+                }
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < kR; ++r)
+            for (int b = lane; b < n_blocks; b += 64) {
+                const uint16_t *blk = reinterpret_cast<const uint16_t *>(wr[r] + (size_t)b * 34);
+                const float dw = f16_bits_to_f32(blk[0]);
+                uint32_t q[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) q[k] = (uint32_t)blk[1 + 2 * k] | ((uint32_t)blk[2 + 2 * k] << 16);
+                acc[r] += q8_block_term(dw, sg[r][b], q, reinterpret_cast<const int *>(xg[r] + (size_t)b * 32));
+            }
+    }
+#pragma unroll
+    for (int r = 0; r < kR; ++r) out[r] = wave_sum(acc[r]);
+}
+
 __global__ __launch_bounds__(256) void mv_q8_kernel(const uint8_t *__restrict__ W,
                                                     const int8_t *__restrict__ xq,
                                                     const float *__restrict__ xscale,
                                                     float *__restrict__ y, int n_rows,
                                                     int n_blocks, int rank, int grouped) {
     const int lane = threadIdx.x & 63;
+    const int row[1] = {(int)blockIdx.x * 4 + (int)(threadIdx.x >> 6)};
+    if (row[0] >= n_rows) return;
+    float acc[1];
+    q8_rows<1>(W, xq, xscale, row, n_blocks, rank, grouped, lane, acc);
+    if (lane == 0) y[row[0]] = acc[0];
+}
+
+// mv_q8_kernel and q8_quant_kernel of its output in one launch: a 1024-thread
+// workgroup computes 32 consecutive rows (two per wave), then quantizes them
+// as one Q8_0 block (q8_quant_kernel's arithmetic) into yq / yscale. n_rows a
+// multiple of 32.
+__global__ __launch_bounds__(1024) void mv_q8_quant_kernel(const uint8_t *__restrict__ W,
+                                                           const int8_t *__restrict__ xq,
+                                                           const float *__restrict__ xscale,
+                                                           int8_t *__restrict__ yq, float *__restrict__ yscale,
+                                                           int n_blocks, int rank, int grouped) {
+    __shared__ float s_y[32];
+    const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int row = blockIdx.x * 4 + wave;
-    if (row >= n_rows) return;
-    const int g = grouped ? row / rank : 0;
-    const int8_t *xg = xq + (size_t)g * n_blocks * 32;
-    const float *sg = xscale + (size_t)g * n_blocks;
-    const uint8_t *wr = W + (size_t)row * n_blocks * 34;
-    float acc = 0.0f;
-    if ((n_blocks & 1) == 0 && (reinterpret_cast<uintptr_t>(W) & 3) == 0) {
-        const int n_pairs = n_blocks / 2;
-        const uint32_t *wp = reinterpret_cast<const uint32_t *>(wr);
-        for (int p0 = lane; p0 < n_pairs; p0 += 128) {
-            uint32_t d[2][17];
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const int p = min(p0 + 64 * u, n_pairs - 1);
-#pragma unroll
-                for (int k = 0; k < 17; ++k) d[u][k] = wp[(size_t)p * 17 + k];
-            }
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const int p = p0 + 64 * u;
-                if (p >= n_pairs) break;
-                const int b = 2 * p;
-                uint32_t qe[8], qo[8];
-#pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    qe[k] = __builtin_amdgcn_alignbyte(d[u][k + 1], d[u][k], 2);   // bytes 2 + 4k ..
-                    qo[k] = d[u][k + 9];
-                }
-                const float dwe = f16_bits_to_f32((uint16_t)(d[u][0] & 0xFFFF));
-                const float dwo = f16_bits_to_f32((uint16_t)(d[u][8] >> 16));
-                acc += q8_block_term(dwe, sg[b], qe, reinterpret_cast<const int *>(xg + (size_t)b * 32));
-                acc += q8_block_term(dwo, sg[b + 1], qo, reinterpret_cast<const int *>(xg + (size_t)(b + 1) * 32));
-            }
-        }
-    } else {
-        for (int b = lane; b < n_blocks; b += 64) {
-            const uint16_t *blk = reinterpret_cast<const uint16_t *>(wr + (size_t)b * 34);
-            const float dw = f16_bits_to_f32(blk[0]);
-            uint32_t q[8];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) q[k] = (uint32_t)blk[1 + 2 * k] | ((uint32_t)blk[2 + 2 * k] << 16);
-            acc += q8_block_term(dw, sg[b], q, reinterpret_cast<const int *>(xg + (size_t)b * 32));
-        }
+    const int row[2] = {(int)blockIdx.x * 32 + 2 * wave, (int)blockIdx.x * 32 + 2 * wave + 1};
+    float acc[2];
+    q8_rows<2>(W, xq, xscale, row, n_blocks, rank, grouped, lane, acc);
+    if (lane == 0) {
+        s_y[2 * wave] = acc[0];
+        s_y[2 * wave + 1] = acc[1];
     }
-    acc = wave_sum(acc);
-    if (lane == 0) y[row] = acc;
+    __syncthreads();
+    if (threadIdx.x >= 32) return;
+    const int l = threadIdx.x;
+    const float v = s_y[l];
+    float a = fabsf(v);
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, 32));
+    const float d = a / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    int q = (int)__builtin_rintf(v * id);
+    q = q > 127 ? 127 : (q < -128 ? -128 : q);
+    yq[(size_t)blockIdx.x * 32 + l] = (int8_t)q;
+    if (l == 0) yscale[blockIdx.x] = d;
 }
 
 // Steps 14 + 15a in one launch: the inverse tail RoPE of a head's attention
@@ -843,14 +841,32 @@ extern "C" size_t ds4hip_attn_out_decode_workspace_bytes(int n_head, int head_di
     return attn_out_ws(n_head, head_dim, n_groups, rank, nullptr, nullptr);
 }
 
+namespace {
+bool attn_out_shape_ok(int n_head, int head_dim, int n_groups, int rank, int out_dim) {
+    return n_head > 0 && head_dim > 0 && head_dim % 32 == 0 && head_dim <= 512 && n_groups > 0 &&
+           (n_head * head_dim) % n_groups == 0 && ((n_head * head_dim) / n_groups) % 32 == 0 && rank > 0 &&
+           rank % 32 == 0 && out_dim > 0;
+}
+// Steps 15-16 from the quantized attention output: the grouped projection
+// with the quantization of its output, then the dense one
+void attn_out_projections(const int8_t *xq, const float *xs, const void *w_out_a, const void *w_out_b, float *out,
+                          int n_head, int head_dim, int n_groups, int rank, int out_dim, const AttnOutWs &w,
+                          hipStream_t st) {
+    const int bpg = (n_head * head_dim) / n_groups / 32;
+    const int n_low = n_groups * rank;
+    hipLaunchKernelGGL(mv_q8_quant_kernel, dim3(n_low / 32), dim3(1024), 0, st,
+                       static_cast<const uint8_t *>(w_out_a), xq, xs, w.xq2, w.xs2, bpg, rank, 1);
+    hipLaunchKernelGGL(mv_q8_kernel, dim3((out_dim + 3) / 4), dim3(256), 0, st, static_cast<const uint8_t *>(w_out_b),
+                       w.xq2, w.xs2, out, out_dim, n_low / 32, out_dim, 0);
+}
+}  // namespace
+
 extern "C" int ds4hip_attn_out_decode_f32(const float *kqv, const void *w_out_a, const void *w_out_b,
                                           float *out, int n_head, int head_dim, int n_rot, int pos, int il,
                                           int n_groups, int rank, int out_dim, void *workspace,
                                           size_t workspace_bytes, void *stream) {
-    if (!kqv || !w_out_a || !w_out_b || !out || !workspace || n_head <= 0 || head_dim <= 0 ||
-        head_dim % 32 || head_dim > 512 || n_rot <= 0 || n_rot > 128 || (n_rot & 1) || n_rot > head_dim ||
-        n_groups <= 0 || (n_head * head_dim) % n_groups || ((n_head * head_dim) / n_groups) % 32 || rank <= 0 ||
-        rank % 32 || (n_groups * rank) % 32 || out_dim <= 0 ||
+    if (!kqv || !w_out_a || !w_out_b || !out || !workspace || !attn_out_shape_ok(n_head, head_dim, n_groups, rank, out_dim) ||
+        n_rot <= 0 || n_rot > 128 || (n_rot & 1) || n_rot > head_dim ||
         workspace_bytes < attn_out_ws(n_head, head_dim, n_groups, rank, nullptr, nullptr))
         return ds4hip_set_last_error(kEINVAL);
     const hipStream_t st = (hipStream_t)stream;
@@ -858,14 +874,23 @@ extern "C" int ds4hip_attn_out_decode_f32(const float *kqv, const void *w_out_a,
     attn_out_ws(n_head, head_dim, n_groups, rank, static_cast<char *>(workspace), &w);
     const RopeParams P = rope_params(n_rot, il, true);
     hipLaunchKernelGGL(rope_q8_kernel, dim3(n_head), dim3(256), 0, st, kqv, w.xq, w.xs, head_dim, n_rot, pos, P);
-    const int bpg = (n_head * head_dim) / n_groups / 32;
-    const int n_low = n_groups * rank;
-    hipLaunchKernelGGL(mv_q8_kernel, dim3((n_low + 3) / 4), dim3(256), 0, st,
-                       static_cast<const uint8_t *>(w_out_a), w.xq, w.xs, w.low, n_low, bpg, rank, 1);
-    int e = hip_status(hipGetLastError());
-    if (e) return ds4hip_set_last_error(e);
-    return ds4hip_set_last_error(launch_q8(static_cast<const uint8_t *>(w_out_b), w.low, out, 1, n_low, out_dim,
-                                           w.xq2, w.xs2, false, st));
+    attn_out_projections(w.xq, w.xs, w_out_a, w_out_b, out, n_head, head_dim, n_groups, rank, out_dim, w, st);
+    return ds4hip_set_last_error(hip_status(hipGetLastError()));
+}
+
+extern "C" int ds4hip_attn_out_decode_q8_f32(const int8_t *xq, const float *xscale, const void *w_out_a,
+                                             const void *w_out_b, float *out, int n_head, int head_dim, int n_groups,
+                                             int rank, int out_dim, void *workspace, size_t workspace_bytes,
+                                             void *stream) {
+    if (!xq || !xscale || !w_out_a || !w_out_b || !out || !workspace ||
+        !attn_out_shape_ok(n_head, head_dim, n_groups, rank, out_dim) ||
+        workspace_bytes < attn_out_ws(n_head, head_dim, n_groups, rank, nullptr, nullptr))
+        return ds4hip_set_last_error(kEINVAL);
+    const hipStream_t st = (hipStream_t)stream;
+    AttnOutWs w;
+    attn_out_ws(n_head, head_dim, n_groups, rank, static_cast<char *>(workspace), &w);
+    attn_out_projections(xq, xscale, w_out_a, w_out_b, out, n_head, head_dim, n_groups, rank, out_dim, w, st);
+    return ds4hip_set_last_error(hip_status(hipGetLastError()));
 }
 
 // ---- per-token layer prologue: Steps 11-12c's independent launches as one --------------

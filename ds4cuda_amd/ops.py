@@ -159,17 +159,26 @@ def launch_flash_attn_decode_mixed_f32_prealloc(Q, raw_kv, comp_kv, comp_allowed
 
 
 class DecodeOpts(C.Structure):
-    """ds4hip_decode_opts: per-call P precision and kernel choice."""
-    _fields_ = [("exact_p", C.c_int), ("kernel", C.c_int)]
+    """ds4hip_decode_opts: per-call P precision, kernel choice and merge output form."""
+    _fields_ = [("exact_p", C.c_int), ("kernel", C.c_int), ("out_form", C.c_int), ("out_pos", C.c_int),
+                ("out_il", C.c_int), ("q8_out", C.c_void_p), ("q8_scale", C.c_void_p)]
 
 
 _KERNELS = {"auto": 0, "regload": 1}
 
 
-def decode_opts(exact_p=False, kernel="auto"):
+def decode_opts(exact_p=False, kernel="auto", rope_q8=None):
+    """rope_q8: None (the merge writes out) or (q8_out int8, q8_scale fp32,
+    pos, il): the merge writes the inverse-RoPE'd rows in Q8_0 form instead
+    (DS4HIP_DECODE_OUT_ROPE_Q8), the input of attn_out_decode_q8_f32."""
     if kernel not in _KERNELS:
         raise Ds4HipError(f"kernel must be one of {sorted(_KERNELS)}", -22)
-    return DecodeOpts(int(bool(exact_p)), _KERNELS[kernel])
+    if rope_q8 is None:
+        return DecodeOpts(int(bool(exact_p)), _KERNELS[kernel])
+    xq, xs, pos, il = rope_q8
+    _check(xq, torch.int8, None, "q8_out")
+    _check(xs, torch.float32, None, "q8_scale")
+    return DecodeOpts(int(bool(exact_p)), _KERNELS[kernel], 1, int(pos), int(il), _ptr(xq), _ptr(xs))
 
 
 def decode_fp8_workspace_bytes(n_rows_per_prob) -> int:
@@ -211,7 +220,7 @@ def _q_mode(q):
 
 def flash_attn_decode_fp8(q, sinks, out, cache: Fp8KVCache, n_rows_per_prob, *, row_base=None,
                           row_base_stride=0, row_idx=None, page_table=None, page_rows=256,
-                          workspace=None, phases=3, exact_p=False, kernel="auto", stream=None):
+                          workspace=None, phases=3, exact_p=False, kernel="auto", rope_q8=None, stream=None):
     """Decode attention of n_prob single-query problems over the FP8 cache.
 
     q [n_prob, 64, 512] bf16 or fp32 (or int32 [n_prob, q_prep_words()], a
@@ -220,7 +229,7 @@ def flash_attn_decode_fp8(q, sinks, out, cache: Fp8KVCache, n_rows_per_prob, *, 
     position row_idx[p, r] (or r), mapped through page_table[p] (pages of
     page_rows rows) or offset by row_base[p] (int64 tensor) / p*row_base_stride.
     exact_p: P as f16 hi + lo instead of one f16; kernel: "auto" or "regload"
-    (the register-load kernel for direct rows too).
+    (the register-load kernel for direct rows too); rope_q8: see decode_opts.
     """
     n_prob = len(n_rows_per_prob)
     q_mode, q_stride = _q_mode(q)
@@ -240,7 +249,7 @@ def flash_attn_decode_fp8(q, sinks, out, cache: Fp8KVCache, n_rows_per_prob, *, 
          n_prob, _ptr(row_base), int(row_base_stride), _ptr(row_idx),
          row_idx.shape[-1] if row_idx is not None else 0, _ptr(page_table),
          page_table.shape[-1] if page_table is not None else 0, int(page_rows), N_HEAD,
-         HEAD_DIM, N_ROT, C.c_longlong(cache.n_rows), C.byref(decode_opts(exact_p, kernel)),
+         HEAD_DIM, N_ROT, C.c_longlong(cache.n_rows), C.byref(decode_opts(exact_p, kernel, rope_q8)),
          _ptr(workspace), workspace.numel(), int(phases), _stream(stream))
     return workspace
 
@@ -338,6 +347,26 @@ def attn_out_decode_f32(kqv, w_out_a, w_out_b, out, n_head, head_dim, n_rot, pos
     _dev(workspace, "workspace", need)
     call("ds4hip_attn_out_decode_f32", _ptr(kqv), _ptr(w_out_a), _ptr(w_out_b), _ptr(out), n_head, head_dim,
          n_rot, pos, il, n_groups, rank, out_dim, _ptr(workspace), workspace.numel(), _stream(stream))
+    return workspace
+
+
+def attn_out_decode_q8_f32(xq, xscale, w_out_a, w_out_b, out, n_head, head_dim, n_groups, rank, out_dim,
+                           workspace=None, stream=None):
+    """attn_out_decode_f32 after its first step: from the rotated Q8_0
+    attention output (xq int8 [n_head*head_dim], xscale fp32 [/32]) that a
+    decode merge writes with decode_opts(rope_q8=...)."""
+    group_dim = n_head * head_dim // n_groups
+    _check(xq, torch.int8, n_head * head_dim, "xq")
+    _check(xscale, torch.float32, n_head * head_dim // 32, "xscale")
+    _check(w_out_a, torch.uint8, n_groups * rank * (group_dim // 32) * 34, "w_out_a")
+    _check(w_out_b, torch.uint8, out_dim * (n_groups * rank // 32) * 34, "w_out_b")
+    _check(out, torch.float32, out_dim, "out")
+    need = lib().ds4hip_attn_out_decode_workspace_bytes(n_head, head_dim, n_groups, rank)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=xq.device)
+    _dev(workspace, "workspace", need)
+    call("ds4hip_attn_out_decode_q8_f32", _ptr(xq), _ptr(xscale), _ptr(w_out_a), _ptr(w_out_b), _ptr(out), n_head,
+         head_dim, n_groups, rank, out_dim, _ptr(workspace), workspace.numel(), _stream(stream))
     return workspace
 
 

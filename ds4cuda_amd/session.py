@@ -170,13 +170,15 @@ class Session:
              C.byref(n), C.byref(sel))
         return ri.value, n.value, sel.value
 
-    def decode(self, il, q, sinks, out, n_selected=-1, workspace=None, exact_p=False, stream=None):
+    def decode(self, il, q, sinks, out, n_selected=-1, workspace=None, exact_p=False, rope_q8=None,
+               stream=None):
         """Decode attention of one query (q [64,512] bf16/fp32, or an fp32 one
         converted by ops.flash_attn_q_prep_f32 / the token prologue) over layer il's
         valid ring rows plus its first n_selected compressed rows (all n_comp
         when n_selected < 0; the selection written at layer_rows()' selected
         address otherwise). exact_p: P as f16 hi + lo (the register kernels)
-        instead of one f16 (the flat-stage kernel)."""
+        instead of one f16 (the flat-stage kernel). rope_q8: see
+        ops.decode_opts (the merge writes the rotated Q8_0 rows instead of out)."""
         from .ops import HEAD_DIM, N_HEAD, _q_mode, decode_fp8_workspace_bytes, decode_opts, N_ROT
         ri, n, _ = self.layer_rows(il, n_selected)
         q_mode, q_stride = _q_mode(q)
@@ -193,5 +195,6 @@ class Session:
              C.c_void_p(self.s.tail + rb * 128), C.cast(counts, C.c_void_p), 1, None, 0,
              C.c_void_p(ri),
              0, None, 0, 256, N_HEAD, HEAD_DIM, N_ROT, C.c_longlong(self.rows_from(rb)),
-             C.byref(decode_opts(exact_p)), _ptr(workspace), workspace.numel(), 3, _stream(stream))
+             C.byref(decode_opts(exact_p, rope_q8=rope_q8)), _ptr(workspace), workspace.numel(), 3,
+             _stream(stream))
         return workspace

@@ -198,6 +198,9 @@ class TokenSlice:
                                   device=dev)
         self.kqv = f(N_HEAD * HEAD_DIM)
         self.q_pre = torch.empty(q_prep_words(), dtype=torch.int32, device=dev)   # fused: Step 13's query
+        # fused: Step 13's output as the merge writes it (rotated, Q8_0)
+        self.kq8 = torch.empty(N_HEAD * HEAD_DIM, dtype=torch.int8, device=dev)
+        self.kq8s = f(N_HEAD * HEAD_DIM // 32)
         self.out_ws = torch.empty(lib().ds4hip_attn_out_decode_workspace_bytes(N_HEAD, HEAD_DIM, N_OUT_GROUP,
                                                                                N_LORA_O),
                                   dtype=torch.uint8, device=dev)
@@ -323,11 +326,13 @@ class TokenSlice:
                  _vp(L.index_comp_kv), 0, L.n_index_comp, IDX_HEAD, IDX_DIM, self.top_k, 0,
                  _ptr(self.scores), _ptr(self.select), None, _vp(sel), st)
             n_sel = self.top_k
-        # Step 13
-        sess.decode(il, self.q_pre, w["sinks"], self.kqv, n_selected=n_sel, workspace=self.dec_ws, stream=stream)
-        # Steps 14-16
-        call("ds4hip_attn_out_decode_f32", _ptr(self.kqv), _ptr(w["out_a"]), _ptr(w["out_b"]), _ptr(out[il]),
-             N_HEAD, HEAD_DIM, N_ROT, pos, il, N_OUT_GROUP, N_LORA_O, N_EMBD, _ptr(self.out_ws),
+        # Step 13, its merge writing Step 14's inverse RoPE and the first Q8_0
+        # quantization of Step 15
+        sess.decode(il, self.q_pre, w["sinks"], self.kqv, n_selected=n_sel, workspace=self.dec_ws,
+                    rope_q8=(self.kq8, self.kq8s, pos, il), stream=stream)
+        # Steps 15-16
+        call("ds4hip_attn_out_decode_q8_f32", _ptr(self.kq8), _ptr(self.kq8s), _ptr(w["out_a"]), _ptr(w["out_b"]),
+             _ptr(out[il]), N_HEAD, HEAD_DIM, N_OUT_GROUP, N_LORA_O, N_EMBD, _ptr(self.out_ws),
              self.out_ws.numel(), st)
 
     def capture(self, pos, kv_rope, attn_norm, q_cur, q_lora, out):

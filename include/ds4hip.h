@@ -133,9 +133,23 @@ typedef struct ds4hip_decode_opts {
      * flat-stage kernel, everything else the register-load kernel;
      * DS4HIP_DECODE_KERNEL_REGLOAD: the register-load kernel for direct rows too. */
     int kernel;
+    /* What the merge writes. DS4HIP_DECODE_OUT_F32 (default): out.
+     * DS4HIP_DECODE_OUT_ROPE_Q8: instead of out, each head's row after the
+     * inverse tail RoPE (n_rot dims at position out_pos with layer out_il's
+     * parameters, as ds4hip_tail_rope_yarn_inverse_f32) in Q8_0 form: int8
+     * values at q8_out + p*n_head*head_dim and one fp32 scale per 32 values at
+     * q8_scale + p*n_head*head_dim/32 (the quantization of
+     * ds4hip_attn_out_decode_f32's first step, bit for bit) — the input of
+     * ds4hip_attn_out_decode_q8_f32. */
+    int out_form;
+    int out_pos, out_il;
+    int8_t *q8_out;
+    float *q8_scale;
 } ds4hip_decode_opts;
 #define DS4HIP_DECODE_KERNEL_AUTO 0
 #define DS4HIP_DECODE_KERNEL_REGLOAD 1
+#define DS4HIP_DECODE_OUT_F32 0
+#define DS4HIP_DECODE_OUT_ROPE_Q8 1
 
 /* Decode attention over the FP8 cache (additive: the FP8-cache form of
  * cuda/flash_attn.cuh:9-26,90-117, which take fp32 rows). Solves n_prob
@@ -264,6 +278,11 @@ int ds4hip_mul_mv_q8_0_q8_0_f32_prealloc(const void *W, const float *x, float *y
  * head_dim, then ds4hip_tail_rope_yarn_f32 (the indexer query,
  * cuda/forward_layer.cu:1046-1053). head_dim and n_rot multiples of 4.
  *
+ * ds4hip_attn_out_decode_q8_f32: ds4hip_attn_out_decode_f32 after its
+ * first step, from the rotated Q8_0 attention output (a decode merge's
+ * DS4HIP_DECODE_OUT_ROPE_Q8 form: xq [n_head*head_dim] int8, xscale
+ * [n_head*head_dim/32]); the same results bit for bit.
+ *
  * ds4hip_attn_out_decode_f32: Steps 14-16 (cuda/forward_layer.cu:1172-1210):
  * ds4hip_tail_rope_yarn_inverse_f32 of kqv [n_head][head_dim], the grouped
  * Q8_0 projection (n_groups groups, rank rows each) and the dense Q8_0
@@ -329,6 +348,9 @@ size_t ds4hip_attn_out_decode_workspace_bytes(int n_head, int head_dim, int n_gr
 int ds4hip_attn_out_decode_f32(const float *kqv, const void *w_out_a, const void *w_out_b, float *out,
                                int n_head, int head_dim, int n_rot, int pos, int il, int n_groups, int rank,
                                int out_dim, void *workspace, size_t workspace_bytes, void *stream);
+int ds4hip_attn_out_decode_q8_f32(const int8_t *xq, const float *xscale, const void *w_out_a, const void *w_out_b,
+                                  float *out, int n_head, int head_dim, int n_groups, int rank, int out_dim,
+                                  void *workspace, size_t workspace_bytes, void *stream);
 
 /* Replaces ds4cuda::launch_rms_norm_f32 (cuda/norm.cuh:24): one row of n,
  * y = x * (1 / sqrtf(mean(x^2) + eps)) * w, fp32 accumulation. */

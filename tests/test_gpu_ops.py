@@ -343,3 +343,45 @@ def test_fused_launches_equal_the_pairs(gpu, il):
     ops.attn_out_decode_f32(kqv, wa, wb, out, 64, 512, 64, pos, il, 8, 1024, 4096)
     torch.cuda.synchronize()
     assert torch.equal(out, ref)
+
+
+@pytest.mark.parametrize("n_rows,il", [(200, 0), (5000, 2), (3000, 3)])
+def test_decode_merge_rope_q8_output(gpu, n_rows, il):
+    """The decode merge's rotated Q8_0 output (decode_opts rope_q8) against
+    the fp32 merge output rotated by the inverse tail RoPE launcher and
+    quantized by the grouped Q8_0 launcher: int8 values and scales bit for
+    bit, and Steps 15-16 from it (attn_out_decode_q8_f32) equal to
+    attn_out_decode_f32 from the fp32 output. 200 rows take the narrow merge,
+    3000 and 5000 the wide one; layers 0, 2, 3 cover the three RoPE
+    parameter sets."""
+    from ds4cuda_amd import synth, token
+    g = torch.Generator(device=gpu)
+    g.manual_seed(77 + il)
+    pos = 4000 + il
+    x = synth.kv_rows(78 + il, 1, n_rows)
+    cache = ops.Fp8KVCache.empty(n_rows, device=gpu)
+    cache.append(torch.from_numpy(x).to(gpu))
+    q = torch.randn((1, 64, 512), generator=g, device=gpu) * 2.0
+    sinks = torch.randn((1, 64), generator=g, device=gpu)
+    kqv = torch.empty((1, 64, 512), device=gpu)
+    ops.flash_attn_decode_fp8(q, sinks, kqv, cache, [n_rows])
+    xq = torch.empty(64 * 512, dtype=torch.int8, device=gpu)
+    xs = torch.empty(64 * 512 // 32, device=gpu)
+    ops.flash_attn_decode_fp8(q, sinks, torch.empty_like(kqv), cache, [n_rows], rope_q8=(xq, xs, pos, il))
+    back = torch.empty(64 * 512, device=gpu)
+    ops.launch_tail_rope_yarn_inverse_f32(kqv.reshape(-1), back, 64, 512, 64, pos, il)
+    wa = token.q8_weights(8 * 1024, 4096, g, gpu)
+    wb = token.q8_weights(4096, 8 * 1024, g, gpu)
+    low = torch.empty(8 * 1024, device=gpu)
+    sq = torch.empty(64 * 512, dtype=torch.int8, device=gpu)
+    ss = torch.empty(64 * 512 // 32, device=gpu)
+    ops.launch_mul_mv_q8_0_q8_0_grouped_f32_prealloc(wa, back, low, 8, 4096, 1024, sq, ss)
+    ref = torch.empty(4096, device=gpu)
+    ops.attn_out_decode_f32(kqv.reshape(-1), wa, wb, ref, 64, 512, 64, pos, il, 8, 1024, 4096)
+    got = torch.empty(4096, device=gpu)
+    ops.attn_out_decode_q8_f32(xq, xs, wa, wb, got, 64, 512, 8, 1024, 4096)
+    torch.cuda.synchronize()
+    assert torch.equal(xq, sq)
+    assert np.array_equal(xs.cpu().numpy().view(np.uint32), ss.cpu().numpy().view(np.uint32))
+    assert torch.isfinite(ref).all()
+    assert np.array_equal(got.cpu().numpy().view(np.uint32), ref.cpu().numpy().view(np.uint32))

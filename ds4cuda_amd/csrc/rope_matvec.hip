@@ -272,25 +272,29 @@ __global__ __launch_bounds__(256) void mv_q8_kernel(const uint8_t *__restrict__ 
     if (lane == 0) y[row[0]] = acc[0];
 }
 
-// mv_q8_kernel and q8_quant_kernel of its output in one launch: a 1024-thread
-// workgroup computes 32 consecutive rows (two per wave), then quantizes them
-// as one Q8_0 block (q8_quant_kernel's arithmetic) into yq / yscale. n_rows a
-// multiple of 32.
-__global__ __launch_bounds__(1024) void mv_q8_quant_kernel(const uint8_t *__restrict__ W,
-                                                           const int8_t *__restrict__ xq,
-                                                           const float *__restrict__ xscale,
-                                                           int8_t *__restrict__ yq, float *__restrict__ yscale,
-                                                           int n_blocks, int rank, int grouped) {
+// mv_q8_kernel and q8_quant_kernel of its output in one launch: a workgroup
+// of 32 / kRpw waves computes 32 consecutive rows (kRpw per wave), then
+// quantizes them as one Q8_0 block (q8_quant_kernel's arithmetic) into yq /
+// yscale. n_rows a multiple of 32.
+constexpr int kQuantRpw = 2;   // rows per wave (1024-thread workgroups)
+template <int kRpw>
+__global__ __launch_bounds__(64 * 32 / kRpw) void mv_q8_quant_kernel(const uint8_t *__restrict__ W,
+                                                                     const int8_t *__restrict__ xq,
+                                                                     const float *__restrict__ xscale,
+                                                                     int8_t *__restrict__ yq,
+                                                                     float *__restrict__ yscale, int n_blocks,
+                                                                     int rank, int grouped) {
     __shared__ float s_y[32];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int row[2] = {(int)blockIdx.x * 32 + 2 * wave, (int)blockIdx.x * 32 + 2 * wave + 1};
-    float acc[2];
-    q8_rows<2>(W, xq, xscale, row, n_blocks, rank, grouped, lane, acc);
-    if (lane == 0) {
-        s_y[2 * wave] = acc[0];
-        s_y[2 * wave + 1] = acc[1];
-    }
+    int row[kRpw];
+#pragma unroll
+    for (int r = 0; r < kRpw; ++r) row[r] = (int)blockIdx.x * 32 + kRpw * wave + r;
+    float acc[kRpw];
+    q8_rows<kRpw>(W, xq, xscale, row, n_blocks, rank, grouped, lane, acc);
+    if (lane == 0)
+#pragma unroll
+        for (int r = 0; r < kRpw; ++r) s_y[kRpw * wave + r] = acc[r];
     __syncthreads();
     if (threadIdx.x >= 32) return;
     const int l = threadIdx.x;
@@ -854,7 +858,7 @@ void attn_out_projections(const int8_t *xq, const float *xs, const void *w_out_a
                           hipStream_t st) {
     const int bpg = (n_head * head_dim) / n_groups / 32;
     const int n_low = n_groups * rank;
-    hipLaunchKernelGGL(mv_q8_quant_kernel, dim3(n_low / 32), dim3(1024), 0, st,
+    hipLaunchKernelGGL(mv_q8_quant_kernel<kQuantRpw>, dim3(n_low / 32), dim3(64 * 32 / kQuantRpw), 0, st,
                        static_cast<const uint8_t *>(w_out_a), xq, xs, w.xq2, w.xs2, bpg, rank, 1);
     hipLaunchKernelGGL(mv_q8_kernel, dim3((out_dim + 3) / 4), dim3(256), 0, st, static_cast<const uint8_t *>(w_out_b),
                        w.xq2, w.xs2, out, out_dim, n_low / 32, out_dim, 0);

@@ -96,43 +96,47 @@ struct MvEpilogue {
     int head_dim = 0, n_rot = 0, pos = 0;
     RopeParams P{};
 };
-// Rows [16 vblock, 16 vblock + 16) of y = W x over the staged input xs, with
-// the epilogue kEpi.
-template <int kEpi>
+// Rows [4 kRows vblock, 4 kRows (vblock + 1)) of y = W x over the staged
+// input xs (kRows per wave, kUnroll chunks of each in flight), with the
+// epilogue kEpi (kMvRope: kRows even). Each row's sum is the same for any
+// kRows and kUnroll: a lane takes chunks lane, lane + 64, ... in that order.
+template <int kEpi, int kRows = kMvRows, int kUnroll = 2>
 __device__ inline void mv_f16_rows(const float *xs, const uint16_t *__restrict__ w, float *__restrict__ y,
                                    int out_dim, int in_dim, const MvEpilogue &E, int vblock) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int row0 = (vblock * 4 + wave) * kMvRows;
+    const int row0 = (vblock * 4 + wave) * kRows;
     if (row0 >= out_dim) return;
-    float acc[kMvRows] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if ((in_dim & 7) == 0) {
-        const void *rows[kMvRows];
+    float acc[kRows];
 #pragma unroll
-        for (int r = 0; r < kMvRows; ++r) rows[r] = w + (size_t)min(row0 + r, out_dim - 1) * in_dim;
-        wave_rows_dot<kMvRows, 2, false>(rows, xs, in_dim, lane, acc);
+    for (int r = 0; r < kRows; ++r) acc[r] = 0.0f;
+    if ((in_dim & 7) == 0) {
+        const void *rows[kRows];
+#pragma unroll
+        for (int r = 0; r < kRows; ++r) rows[r] = w + (size_t)min(row0 + r, out_dim - 1) * in_dim;
+        wave_rows_dot<kRows, kUnroll, false>(rows, xs, in_dim, lane, acc);
     } else {
 #pragma unroll
-        for (int r = 0; r < kMvRows; ++r) {
+        for (int r = 0; r < kRows; ++r) {
             const uint16_t *wr = w + (size_t)min(row0 + r, out_dim - 1) * in_dim;
             for (int i = lane; i < in_dim; i += 64) acc[r] = fmaf(f16_bits_to_f32(wr[i]), xs[i], acc[r]);
         }
     }
-    float a[kMvRows];
+    float a[kRows];
 #pragma unroll
-    for (int r = 0; r < kMvRows; ++r) a[r] = wave_sum(acc[r]);
+    for (int r = 0; r < kRows; ++r) a[r] = wave_sum(acc[r]);
     if (kEpi == kMvScale) {
 #pragma unroll
-        for (int r = 0; r < kMvRows; ++r) a[r] = a[r] * E.scale;
+        for (int r = 0; r < kRows; ++r) a[r] = a[r] * E.scale;
     }
     if (kEpi == kMvRope) {
         const int d0 = row0 % E.head_dim, n_nope = E.head_dim - E.n_rot;
 #pragma unroll
-        for (int r = 0; r < kMvRows; r += 2)
+        for (int r = 0; r < kRows; r += 2)
             if (d0 + r >= n_nope) rope_pair(a[r], a[r + 1], (d0 + r - n_nope) / 2, E.pos, E.P, a[r], a[r + 1]);
     }
 #pragma unroll
-    for (int r = 0; r < kMvRows; ++r)
+    for (int r = 0; r < kRows; ++r)
         if (lane == 0 && row0 + r < out_dim) y[row0 + r] = a[r];
 }
 
@@ -910,23 +914,51 @@ namespace {
 constexpr int kPrologueRot = 64;   // the model's RoPE tail (the session's row layout)
 struct PrologueArgs {
     ds4hip_token_prologue a;
-    int blk_push, blk_comp[2], blk_q, blk_hw, blk_qp;   // first workgroup of each job (blk_qp + n_qp = grid)
+    // first workgroup of each job, in launch order: the query conversion (4
+    // workgroups, one per k-step; first, as the longest chains), the push, the
+    // head weights (one row per wave: a short chain), the projections, the
+    // indexer query (blk_q + n_q = grid)
+    int blk_push, blk_hw, blk_comp[2], blk_q;
     int width[2], pos_mod[2];
     MvEpilogue eq, ehw;
 };
 
+// xs: the staged input vector, sized by the launch to the longest one (a
+// static 8192-float array would leave fewer workgroups per CU than the grid)
 __global__ __launch_bounds__(256) void token_prologue_kernel(const PrologueArgs P) {
-    __shared__ __attribute__((aligned(16))) float xs[kCompMaxIn];
+    extern __shared__ __attribute__((aligned(16))) float xs[];
     const ds4hip_token_prologue &a = P.a;
     const int b = blockIdx.x;
     auto stage = [&](const float *x, int n) {
         stage_to_lds(xs, x, n);
         __syncthreads();
     };
-    if (b < P.blk_comp[0]) {   // the FP8 push: one 64-lane row
+    if (b < P.blk_push) {
+        // the decode query, k-step b: producer lane (wave d, lane) of the flat
+        // decode kernel; the k-step-3 workgroup also writes the f16 tail
+        const int d = threadIdx.x >> 6, lane = threadIdx.x & 63;
+        const float *qrow = a.qp_q + (16 * d + (lane & 15)) * 512;
+        uint4_t *dst = static_cast<uint4_t *>(a.qp_out);
+        uint32_t qf8[3][8];
+        int sc[3];
+        q_prep_ks<true, true>(qrow, lane >> 4, b, qf8, sc);
+        q_prep_store_ks(dst, threadIdx.x, b, qf8, sc);
+        if (b == 3) {
+            half8_t qt[2], qtl[2];
+            q_prep_tail<true>(qrow, lane >> 4, qt, qtl);
+            q_prep_store_tail(dst, threadIdx.x, qt, qtl);
+        }
+        return;
+    }
+    if (b < P.blk_hw) {   // the FP8 push: one 64-lane row
         if (threadIdx.x < 64)
             fp8_row_body<false>(a.kv, nullptr, a.codes, a.sexp, a.tail, 0, a.head_dim, a.n_rot, a.kv_row,
                                 threadIdx.x);
+        return;
+    }
+    if (b < P.blk_comp[0]) {
+        stage(a.x, a.in_dim);
+        mv_f16_rows<kMvScale, 1, 8>(xs, a.hw_w, a.hw_out, a.hw_rows, a.in_dim, P.ehw, b - P.blk_hw);
         return;
     }
     for (int c = 0; c < 2; ++c) {
@@ -942,23 +974,8 @@ __global__ __launch_bounds__(256) void token_prologue_kernel(const PrologueArgs 
             return;
         }
     }
-    if (b < P.blk_hw) {
-        stage(a.q_x, a.q_in);
-        mv_f16_rows<kMvRope>(xs, a.q_w, a.q_out, a.q_heads * a.q_head_dim, a.q_in, P.eq, b - P.blk_q);
-        return;
-    }
-    if (b < P.blk_qp) {
-        stage(a.x, a.in_dim);
-        mv_f16_rows<kMvScale>(xs, a.hw_w, a.hw_out, a.hw_rows, a.in_dim, P.ehw, b - P.blk_hw);
-        return;
-    }
-    // the decode query: producer lane (wave d, lane) of the flat decode kernel
-    const int d = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    uint32_t qf8[4][3][8];
-    int qsc[3];
-    half8_t qt[2], qtl[2];
-    q_prep_lane<true, true>(a.qp_q + (16 * d + (lane & 15)) * 512, lane >> 4, qf8, qsc, qt, qtl);
-    q_prep_store(static_cast<uint4_t *>(a.qp_out), threadIdx.x, qf8, qsc, qt, qtl);
+    stage(a.q_x, a.q_in);
+    mv_f16_rows<kMvRope>(xs, a.q_w, a.q_out, a.q_heads * a.q_head_dim, a.q_in, P.eq, b - P.blk_q);
 }
 }  // namespace
 
@@ -969,10 +986,25 @@ extern "C" int ds4hip_token_prologue_f32(const ds4hip_token_prologue *a, void *s
         return ds4hip_set_last_error(kEINVAL);
     PrologueArgs P = {};
     P.a = *a;
+    int blk = 0;
+    if (a->qp_q) {
+        if (!a->qp_out || (reinterpret_cast<uintptr_t>(a->qp_q) | reinterpret_cast<uintptr_t>(a->qp_out)) % 16)
+            return ds4hip_set_last_error(kEINVAL);
+        blk += 4;
+    }
+    P.blk_push = blk;
+    blk += 1;   // one workgroup: the FP8 push
+    int xs_floats = 4;   // the longest staged vector
+    if (a->n_comp || a->hw_w) xs_floats = std::max(xs_floats, a->in_dim);
+    P.blk_hw = blk;
+    if (a->hw_w) {
+        if (!a->hw_out || a->hw_rows <= 0) return ds4hip_set_last_error(kEINVAL);
+        P.ehw.scale = a->hw_scale;
+        blk += (a->hw_rows + 3) / 4;   // one row per wave
+    }
     const int ratio[2] = {a->comp0_ratio, a->comp1_ratio};
     const int hdo[2] = {a->comp0_head_dim_out, a->comp1_head_dim_out};
     const int pos[2] = {a->comp0_pos, a->comp1_pos};
-    int blk = 1;   // workgroup 0: the FP8 push
     for (int c = 0; c < 2; ++c) {
         P.blk_comp[c] = blk;
         if (c >= a->n_comp) continue;
@@ -996,20 +1028,10 @@ extern "C" int ds4hip_token_prologue_f32(const ds4hip_token_prologue *a, void *s
         P.eq.pos = a->q_pos;
         P.eq.P = rope_params(kPrologueRot, a->q_il, false);
         blk += (a->q_heads * a->q_head_dim + 4 * kMvRows - 1) / (4 * kMvRows);
+        xs_floats = std::max(xs_floats, a->q_in);
     }
-    P.blk_hw = blk;
-    if (a->hw_w) {
-        if (!a->hw_out || a->hw_rows <= 0) return ds4hip_set_last_error(kEINVAL);
-        P.ehw.scale = a->hw_scale;
-        blk += (a->hw_rows + 4 * kMvRows - 1) / (4 * kMvRows);
-    }
-    P.blk_qp = blk;
-    if (a->qp_q) {
-        if (!a->qp_out || (reinterpret_cast<uintptr_t>(a->qp_q) | reinterpret_cast<uintptr_t>(a->qp_out)) % 16)
-            return ds4hip_set_last_error(kEINVAL);
-        blk += 1;
-    }
-    hipLaunchKernelGGL(token_prologue_kernel, dim3(blk), dim3(256), 0, (hipStream_t)stream, P);
+    hipLaunchKernelGGL(token_prologue_kernel, dim3(blk), dim3(256), (size_t)xs_floats * sizeof(float),
+                       (hipStream_t)stream, P);
     return ds4hip_set_last_error(hip_status(hipGetLastError()));
 }
 

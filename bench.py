@@ -43,7 +43,7 @@ TRAFFIC_BYTES_PER_LAUNCH = {"ws": 882340981, "flat": 882148944}
 TRAFFIC_MEASURED_AT = {"ws": "22db79c", "flat": "dedad2c"}   # commit whose partial kernel was counted
 DECODE_KERNEL = "flat"
 KERNEL_LABEL = {"ws": "decode_ws_kernel<0, false> (direct rows, register loads, one f16 P)",
-                "flat": "decode_flat_kernel<false, true> (direct rows, DMA-fed flat LDS stages, one f16 P)"}
+                "flat": "decode_flat_kernel<false, true, 0, 0> (direct rows, DMA-fed flat LDS stages, one f16 P)"}
 
 
 def bytes_per_layer():

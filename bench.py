@@ -39,8 +39,8 @@ COPY_BYTES = 1 << 30                               # --copy-calibration: 1 GiB r
 # profiles/decode_flat_kernel_cfg2_traffic.md (flat kernel) and
 # profiles/decode_ws_kernel_cfg2_traffic.md (register-load kernel).
 # Re-measure after a kernel change.
-TRAFFIC_BYTES_PER_LAUNCH = {"ws": 882340981, "flat": 882148944}
-TRAFFIC_MEASURED_AT = {"ws": "22db79c", "flat": "dedad2c"}   # commit whose partial kernel was counted
+TRAFFIC_BYTES_PER_LAUNCH = {"ws": 882340981, "flat": 882271833}
+TRAFFIC_MEASURED_AT = {"ws": "22db79c", "flat": "36157d5"}   # commit whose partial kernel was counted
 DECODE_KERNEL = "flat"
 KERNEL_LABEL = {"ws": "decode_ws_kernel<0, false> (direct rows, register loads, one f16 P)",
                 "flat": "decode_flat_kernel<false, true, 0, 0> (direct rows, DMA-fed flat LDS stages, one f16 P)"}

@@ -2398,13 +2398,24 @@ __global__ __launch_bounds__(128) void decode_merge_kernel(const DecodeArgs A) {
     }
     float mx = sink;
     int bad = 0;
+    // the first 128 slots' scalars are kept for the second pass (one round
+    // trip for them instead of two)
+    float m_first = -INFINITY, l_first = 0.0f;
+    bool ok_first = false;
     for (long long i = tid; i < n_slot; i += 128) {
         const long long slot = s0 + i;
         const float m = A.ws_ml[slot * 2 * kH + h];
+        const float l = A.ws_ml[slot * 2 * kH + kH + h];
         const int pr = A.ws_prob[slot];
-        if ((pr & ~kBadSlot) == p) {
+        const bool ok = (pr & ~kBadSlot) == p;
+        if (ok) {
             mx = fmaxf(mx, m);
             bad |= pr & kBadSlot;
+        }
+        if (i == tid) {
+            m_first = m;
+            l_first = l;
+            ok_first = ok;
         }
     }
     bad = __syncthreads_or(bad);
@@ -2418,9 +2429,10 @@ __global__ __launch_bounds__(128) void decode_merge_kernel(const DecodeArgs A) {
         float sc = 0.0f, dl = 0.0f;
         if (base + tid < n_slot) {
             const long long slot = s0 + base + tid;
-            const float m = A.ws_ml[slot * 2 * kH + h];
-            const float l = A.ws_ml[slot * 2 * kH + kH + h];
-            if ((A.ws_prob[slot] & ~kBadSlot) == p && m != -INFINITY) {
+            const float m = base == 0 ? m_first : A.ws_ml[slot * 2 * kH + h];
+            const float l = base == 0 ? l_first : A.ws_ml[slot * 2 * kH + kH + h];
+            const bool ok = base == 0 ? ok_first : (A.ws_prob[slot] & ~kBadSlot) == p;
+            if (ok && m != -INFINITY) {
                 sc = __builtin_amdgcn_exp2f(m - mx);
                 dl = l * sc;
             }
@@ -2485,13 +2497,23 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_wide_kernel(const 
     };
     float mx = sink;
     int bad = 0;
+    // the first kMergeThreads slots' scalars are kept for the second pass
+    float m_first = -INFINITY, l_first = 0.0f;
+    bool ok_first = false;
     for (long long i = tid; i < n_slot; i += kMergeThreads) {
         const long long slot = s0 + i;
         const float m = A.ws_ml[slot * 2 * kH + h];
+        const float l = A.ws_ml[slot * 2 * kH + kH + h];
         const int pr = A.ws_prob[slot];
-        if ((pr & ~kBadSlot) == p) {
+        const bool ok = (pr & ~kBadSlot) == p;
+        if (ok) {
             mx = fmaxf(mx, m);
             bad |= pr & kBadSlot;
+        }
+        if (i == tid) {
+            m_first = m;
+            l_first = l;
+            ok_first = ok;
         }
     }
     bad = __syncthreads_or(bad);
@@ -2503,9 +2525,10 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_wide_kernel(const 
         float sc = 0.0f;
         if (base + tid < n_slot) {
             const long long slot = s0 + base + tid;
-            const float m = A.ws_ml[slot * 2 * kH + h];
-            const float l = A.ws_ml[slot * 2 * kH + kH + h];
-            if ((A.ws_prob[slot] & ~kBadSlot) == p && m != -INFINITY) {
+            const float m = base == 0 ? m_first : A.ws_ml[slot * 2 * kH + h];
+            const float l = base == 0 ? l_first : A.ws_ml[slot * 2 * kH + kH + h];
+            const bool ok = base == 0 ? ok_first : (A.ws_prob[slot] & ~kBadSlot) == p;
+            if (ok && m != -INFINITY) {
                 sc = __builtin_amdgcn_exp2f(m - mx);
                 den_part += l * sc;
             }

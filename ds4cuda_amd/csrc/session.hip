@@ -325,16 +325,31 @@ extern "C" int ds4hip_session_state_reset(ds4hip_session_state *s, void *stream)
     return ds4hip_set_last_error(init_buffers(s, (hipStream_t)stream));
 }
 
+namespace {
+// the ring row of the next raw push, and the counters after it
+long long raw_row(const ds4hip_layer_state *L) { return L->row_base + L->cap_comp + L->raw_head; }
+void advance_raw(ds4hip_layer_state *L) {
+    L->raw_head = (L->raw_head + 1) % L->cap_raw;
+    if (L->n_raw < L->cap_raw) ++L->n_raw;
+}
+}  // namespace
+
 extern "C" int ds4hip_session_push_raw(ds4hip_session_state *s, int il, const float *kv_cur,
                                        void *stream) {
     if (!layer_ok(s, il) || !kv_cur) return ds4hip_set_last_error(kEINVAL);
     ds4hip_layer_state *L = &s->layers[il];
-    const long long row = L->row_base + L->cap_comp + L->raw_head;
     const int rc = ds4hip_fp8_kv_quantize_append(kv_cur, 1, DS4HIP_HEAD_DIM, DS4HIP_N_ROT, s->codes,
-                                                 s->sexp, s->tail, row, nullptr, stream);
+                                                 s->sexp, s->tail, raw_row(L), nullptr, stream);
     if (rc) return rc;
-    L->raw_head = (L->raw_head + 1) % L->cap_raw;
-    if (L->n_raw < L->cap_raw) ++L->n_raw;
+    advance_raw(L);
+    return 0;
+}
+
+extern "C" int ds4hip_session_claim_raw_row(ds4hip_session_state *s, int il, long long *row_out) {
+    if (!layer_ok(s, il) || !row_out) return ds4hip_set_last_error(kEINVAL);
+    ds4hip_layer_state *L = &s->layers[il];
+    *row_out = raw_row(L);
+    advance_raw(L);
     return 0;
 }
 

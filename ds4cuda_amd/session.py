@@ -112,6 +112,13 @@ class Session:
         _check(kv_cur, torch.float32, 512, "kv_cur")
         call("ds4hip_session_push_raw", C.byref(self.s), il, _ptr(kv_cur), _stream(stream))
 
+    def claim_raw_row(self, il) -> int:
+        """Arena row of the next raw push, with the ring counters advanced
+        (for a push written by the caller's own launch)."""
+        row = C.c_longlong()
+        call("ds4hip_session_claim_raw_row", C.byref(self.s), il, C.byref(row))
+        return row.value
+
     def push_comp(self, il, row, stream=None):
         _check(row, torch.float32, 512, "row")
         call("ds4hip_session_push_comp", C.byref(self.s), il, _ptr(row), _stream(stream))

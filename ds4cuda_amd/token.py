@@ -282,13 +282,10 @@ class TokenSlice:
         r = L.compress_ratio
         x = attn_norm[il]
         P = TokenPrologue()
-        # Step 11: the FP8 push, with the host bookkeeping of
-        # ds4hip_session_push_raw
+        # Step 11: the FP8 push into the ring row the session hands out
         P.kv, P.codes, P.sexp, P.tail = _ptr(kv_rope[il]), s.codes, s.sexp, s.tail
-        P.kv_row = L.row_base + L.cap_comp + L.raw_head
+        P.kv_row = sess.claim_raw_row(il)
         P.head_dim, P.n_rot = HEAD_DIM, N_ROT
-        L.raw_head = (L.raw_head + 1) % L.cap_raw
-        L.n_raw = min(L.n_raw + 1, L.cap_raw)
         P.x, P.in_dim = _ptr(x), N_EMBD
         emit = bool(r) and (pos + 1) % r == 0
         if r:   # Step 12a (and 12b): the projections

@@ -115,6 +115,12 @@ int ds4hip_session_state_reset(ds4hip_session_state *s, void *stream);
  * oldest row once the ring is full). */
 int ds4hip_session_push_raw(ds4hip_session_state *s, int il, const float *kv_cur, void *stream);
 
+/* The ring bookkeeping of ds4hip_session_push_raw without the write: the
+ * arena row (in codes / sexp / tail) the next raw row goes to, with the ring
+ * counters advanced, for a caller that writes the row in a launch of its own
+ * (ds4hip_token_prologue_f32). No counterpart in the reference. */
+int ds4hip_session_claim_raw_row(ds4hip_session_state *s, int il, long long *row_out);
+
 /* Quantizes an emitted compressed row [512] into the next compressed slot;
  * -28 when full, -22 on a layer without compression. */
 int ds4hip_session_push_comp(ds4hip_session_state *s, int il, const float *row, void *stream);

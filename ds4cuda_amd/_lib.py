@@ -43,6 +43,8 @@ SIGNATURES: dict[str, list] = {
     "ds4hip_mul_mv_f16_rope_f32": [_vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp],
     "ds4hip_attn_out_decode_workspace_bytes": [_i, _i, _i, _i],
     "ds4hip_token_prologue_f32": [_vp, _vp],
+    "ds4hip_compressor_pair_batch_scratch_bytes": [_i, _i, _i, _i, _i],
+    "ds4hip_compressor_pair_step_batch_w32": [_i, _vp, _i, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _sz, _vp],
     "ds4hip_session_claim_raw_row": [_vp, _i, C.POINTER(_ll)],
     "ds4hip_flash_attn_q_prep_f32": [_vp, _ll, _i, _vp, _ll, _vp],
     "ds4hip_flash_attn_q_prep_words": [],
@@ -110,7 +112,8 @@ RESTYPES = {"ds4hip_indexer_select_scratch_bytes": C.c_size_t,
             "ds4hip_compressor_batch_scratch_bytes": C.c_size_t,
             "ds4hip_attn_qkv_decode_workspace_bytes": C.c_size_t,
             "ds4hip_attn_out_decode_workspace_bytes": C.c_size_t,
-            "ds4hip_flash_attn_q_prep_words": C.c_longlong}
+            "ds4hip_flash_attn_q_prep_words": C.c_longlong,
+            "ds4hip_compressor_pair_batch_scratch_bytes": C.c_size_t}
 
 _lib = None
 

@@ -48,7 +48,7 @@ class BatchedAttentionBlock:
     max_pos: largest position a step may decode (sizes the caches)."""
 
     def __init__(self, weights, n_seq, max_pos, in_dim=4096, out_dim=4096, page_rows=256,
-                 top_k=2048, il=2, device="cuda", page_seed=6):
+                 top_k=2048, il=2, device="cuda", page_seed=6, fused=True):
         if n_seq > 16:
             raise Ds4HipError("at most 16 sequences per batched block", -22)
         self.w = weights
@@ -75,6 +75,10 @@ class BatchedAttentionBlock:
         self.emit_i = torch.zeros((B, IDX_DIM), device=device)
         self.scratch = ops.compressor_batch_scratch(B, in_dim, HEAD_DIM, RATIO, device)
         self.scratch_i = ops.compressor_batch_scratch(B, in_dim, IDX_DIM, RATIO, device)
+        # fused: both compressors in three launches (ds4hip_compressor_pair_step_batch_w32,
+        # the same results) instead of six
+        self.fused = fused
+        self.scratch_pair = ops.compressor_pair_scratch(B, in_dim, HEAD_DIM, IDX_DIM, RATIO, device)
         self.mm_ws = ops.mul_mm_workspace(out_dim, N_HEAD * HEAD_DIM, B, device)
         self.scores = torch.empty(self.key_trash + 1, device=device)
         self.out = torch.empty((B, N_HEAD, HEAD_DIM), device=device)
@@ -152,14 +156,24 @@ class BatchedAttentionBlock:
         scaled), sinks [B, 64] fp32. Returns y [B, out_dim] fp32."""
         P = self.plan(pos)
         w, B = self.w, self.B
-        ops.compressor_decode_step_batch_w32(True, x, w["w_kv"], w["w_gate"], w["ape"], w["wn"],
-                                             self.in_dim, HEAD_DIM, RATIO, P["pos_host"],
-                                             P["pos_dev"], self.il, self.st_kv, self.st_sc,
-                                             8 * 1024, self.emit, self.scratch, stream=stream)
-        ops.compressor_decode_step_batch_w32(False, x, w["wi_kv"], w["wi_gate"], w["ape_i"],
-                                             w["wn_i"], self.in_dim, IDX_DIM, RATIO, P["pos_host"],
-                                             P["pos_dev"], self.il, self.sti_kv, self.sti_sc,
-                                             8 * 256, self.emit_i, self.scratch_i, stream=stream)
+        if self.fused:
+            ops.compressor_pair_step_batch_w32(
+                x, self.in_dim, RATIO, P["pos_host"], P["pos_dev"], self.il,
+                dict(w_kv=w["w_kv"], w_gate=w["w_gate"], w_ape=w["ape"], w_norm=w["wn"], head_dim_out=HEAD_DIM,
+                     state_kv=self.st_kv, state_score=self.st_sc, state_stride=8 * 1024, emit_out=self.emit),
+                dict(w_kv=w["wi_kv"], w_gate=w["wi_gate"], w_ape=w["ape_i"], w_norm=w["wn_i"],
+                     head_dim_out=IDX_DIM, state_kv=self.sti_kv, state_score=self.sti_sc, state_stride=8 * 256,
+                     emit_out=self.emit_i),
+                self.scratch_pair, stream=stream)
+        else:
+            ops.compressor_decode_step_batch_w32(True, x, w["w_kv"], w["w_gate"], w["ape"], w["wn"],
+                                                 self.in_dim, HEAD_DIM, RATIO, P["pos_host"],
+                                                 P["pos_dev"], self.il, self.st_kv, self.st_sc,
+                                                 8 * 1024, self.emit, self.scratch, stream=stream)
+            ops.compressor_decode_step_batch_w32(False, x, w["wi_kv"], w["wi_gate"], w["ape_i"],
+                                                 w["wn_i"], self.in_dim, IDX_DIM, RATIO, P["pos_host"],
+                                                 P["pos_dev"], self.il, self.sti_kv, self.sti_sc,
+                                                 8 * 256, self.emit_i, self.scratch_i, stream=stream)
         self.cache.append(kv_cur, dst_rows=P["dst_raw"], stream=stream)
         self.cache.append(self.emit, dst_rows=P["dst_emit"], stream=stream)
         call("ds4hip_rows_scatter_f32", _ptr(self.emit_i), B, IDX_DIM, _ptr(self.keys),

@@ -192,13 +192,10 @@ __global__ __launch_bounds__(512) void comp_emit_kernel(float *__restrict__ stat
 // Sums the n_kg k-group partials of both projections in group order (the
 // same result on every run), adds the APE row to the gate and writes the
 // state row. P: kv partials [n_kg][n_seq][width], then gate partials likewise.
-__global__ __launch_bounds__(256) void comp_batch_update_kernel(
-        const float *__restrict__ P, int n_kg, const uint16_t *__restrict__ w_ape,
-        const int *__restrict__ pos, int n_seq, int width, int ratio, float *__restrict__ state_kv,
-        float *__restrict__ state_score, long long state_stride) {
-    const int b = blockIdx.y;
-    const int o = blockIdx.x * 256 + threadIdx.x;
-    if (o >= width) return;
+__device__ inline void batch_update_body(const float *__restrict__ P, int n_kg, const uint16_t *__restrict__ w_ape,
+                                         const int *__restrict__ pos, int n_seq, int width, int ratio,
+                                         float *__restrict__ state_kv, float *__restrict__ state_score,
+                                         long long state_stride, int b, int o) {
     const size_t n = (size_t)n_seq * width, j = (size_t)b * width + o;
     float kv = P[j], sc = P[(size_t)n_kg * n + j];
     for (int g = 1; g < n_kg; ++g) {
@@ -210,6 +207,39 @@ __global__ __launch_bounds__(256) void comp_batch_update_kernel(
     const size_t off = (size_t)b * state_stride + (size_t)row * width + o;
     state_kv[off] = kv;
     state_score[off] = sc + f16_bits_to_f32(w_ape[(size_t)pm * width + o]);
+}
+
+__global__ __launch_bounds__(256) void comp_batch_update_kernel(
+        const float *__restrict__ P, int n_kg, const uint16_t *__restrict__ w_ape,
+        const int *__restrict__ pos, int n_seq, int width, int ratio, float *__restrict__ state_kv,
+        float *__restrict__ state_score, long long state_stride) {
+    const int o = blockIdx.x * 256 + threadIdx.x;
+    if (o >= width) return;
+    batch_update_body(P, n_kg, w_ape, pos, n_seq, width, ratio, state_kv, state_score, state_stride, blockIdx.y, o);
+}
+
+// The two compressors of a layer: job 0 (attention) on workgroups x <
+// blk1, job 1 (indexer) on the rest
+struct PairJob {
+    const float *P;
+    int n_kg, width, head_dim;
+    const uint16_t *w_ape;
+    const float *w_norm;
+    float *state_kv, *state_score, *emit_out;
+    long long state_stride;
+};
+struct PairArgs {
+    PairJob j[2];
+    int blk1;
+};
+__global__ __launch_bounds__(256) void comp_pair_update_kernel(const PairArgs A, const int *__restrict__ pos,
+                                                               int n_seq, int ratio) {
+    const int job = (int)blockIdx.x >= A.blk1 ? 1 : 0;
+    const PairJob &J = A.j[job];
+    const int o = ((int)blockIdx.x - (job ? A.blk1 : 0)) * 256 + threadIdx.x;
+    if (o >= J.width) return;
+    batch_update_body(J.P, J.n_kg, J.w_ape, pos, n_seq, J.width, ratio, J.state_kv, J.state_score, J.state_stride,
+                      blockIdx.y, o);
 }
 
 // One workgroup per sequence; sequences whose position does not close a
@@ -224,6 +254,19 @@ __global__ __launch_bounds__(512) void comp_batch_emit_kernel(
     R.pos = p + 1 - ratio;
     emit_body(state_kv + (size_t)b * state_stride, state_score + (size_t)b * state_stride, w_norm,
               emit_out + (size_t)b * head_dim, head_dim, ratio, is_attn, R);
+}
+
+// workgroup x: sequence x % n_seq of job x / n_seq (job 0 attention, 1 the indexer)
+__global__ __launch_bounds__(512) void comp_pair_emit_kernel(const PairArgs A, int n_seq, int ratio, RopeArgs R,
+                                                             const int *__restrict__ pos) {
+    const int job = (int)blockIdx.x >= n_seq ? 1 : 0;
+    const int b = (int)blockIdx.x - job * n_seq;
+    const int p = pos[b];
+    if ((p + 1) % ratio) return;
+    const PairJob &J = A.j[job];
+    R.pos = p + 1 - ratio;
+    emit_body(J.state_kv + (size_t)b * J.state_stride, J.state_score + (size_t)b * J.state_stride, J.w_norm,
+              J.emit_out + (size_t)b * J.head_dim, J.head_dim, ratio, job == 0 ? 1 : 0, R);
 }
 
 int comp_step(bool is_attn, const float *x, const void *w_kv, const void *w_gate, bool w32,
@@ -357,5 +400,91 @@ extern "C" int ds4hip_compressor_decode_step_batch_w32(
         hipLaunchKernelGGL(comp_batch_emit_kernel, dim3(n_seq), dim3(512), 0, st, state_kv,
                            state_score, state_stride, w_norm_f32, emit_out, head_dim_out, ratio,
                            is_attn ? 1 : 0, rope_args(il, 0), pos_dev);
+    return ds4hip_set_last_error(hip_status(hipGetLastError()));
+}
+
+namespace {
+// scratch floats of one job's two projections' partials
+size_t pair_job_floats(int n_seq, int in_dim, int head_dim_out, int ratio) {
+    const int width = (ratio == 4 ? 2 : 1) * head_dim_out;
+    return (size_t)2 * ds4hip_mm_k_groups(width, in_dim, 2) * n_seq * width;
+}
+bool pair_job_ok(const ds4hip_compressor_batch_job *j, int ratio) {
+    const int coff = ratio == 4 ? 2 : 1;
+    return j && j->w_kv_f32 && j->w_gate_f32 && j->w_ape_f16 && j->w_norm_f32 && j->state_kv &&
+           j->state_score && j->emit_out && j->head_dim_out > kNRot && j->head_dim_out <= 512 &&
+           j->head_dim_out % 64 == 0 && j->state_stride >= (long long)coff * ratio * coff * j->head_dim_out;
+}
+}  // namespace
+
+extern "C" size_t ds4hip_compressor_pair_batch_scratch_bytes(int n_seq, int in_dim, int attn_head_dim_out,
+                                                            int index_head_dim_out, int compress_ratio) {
+    if (n_seq <= 0 || in_dim <= 0 || attn_head_dim_out <= 0 || index_head_dim_out <= 0 ||
+        (compress_ratio != 4 && compress_ratio != 128))
+        return 0;
+    return (pair_job_floats(n_seq, in_dim, attn_head_dim_out, compress_ratio) +
+            pair_job_floats(n_seq, in_dim, index_head_dim_out, compress_ratio)) *
+           sizeof(float);
+}
+
+extern "C" int ds4hip_compressor_pair_step_batch_w32(int n_seq, const float *x_f32, int in_dim, int compress_ratio,
+                                                     const int *pos_host, const int *pos_dev, int il,
+                                                     const ds4hip_compressor_batch_job *attn,
+                                                     const ds4hip_compressor_batch_job *index,
+                                                     int *emitted_out_host, float *scratch, size_t scratch_bytes,
+                                                     void *stream) {
+    const int ratio = compress_ratio;
+    if (n_seq <= 0 || n_seq > 16 || !x_f32 || !pos_host || !pos_dev || !scratch || in_dim <= 0 || in_dim % 32 ||
+        (ratio != 4 && ratio != 128) || !pair_job_ok(attn, ratio) || !pair_job_ok(index, ratio) ||
+        scratch_bytes < ds4hip_compressor_pair_batch_scratch_bytes(n_seq, in_dim, attn->head_dim_out,
+                                                                   index->head_dim_out, ratio))
+        return ds4hip_set_last_error(kEINVAL);
+    bool any = false;
+    for (int b = 0; b < n_seq; ++b) {
+        if (pos_host[b] < 0) return ds4hip_set_last_error(kEINVAL);
+        const bool e = ((pos_host[b] + 1) % ratio) == 0;
+        if (emitted_out_host) emitted_out_host[b] = e ? 1 : 0;
+        any |= e;
+    }
+    const hipStream_t st = (hipStream_t)stream;
+    const int coff = ratio == 4 ? 2 : 1;
+    const ds4hip_compressor_batch_job *jobs[2] = {attn, index};
+    PairArgs A = {};
+    // each job's partials as its own ds4hip_compressor_decode_step_batch_w32
+    // call lays them out (its k-slice, kv then gate), so the sums are the same
+    const float *W[4];
+    float *part[4];
+    int rows[4], ks[4];
+    float *base = scratch;
+    for (int k = 0; k < 2; ++k) {
+        const int width = coff * jobs[k]->head_dim_out;
+        const int n_kg = ds4hip_mm_k_groups(width, in_dim, 2);
+        PairJob &J = A.j[k];
+        J.P = base;
+        J.n_kg = n_kg;
+        J.width = width;
+        J.head_dim = jobs[k]->head_dim_out;
+        J.w_ape = jobs[k]->w_ape_f16;
+        J.w_norm = jobs[k]->w_norm_f32;
+        J.state_kv = jobs[k]->state_kv;
+        J.state_score = jobs[k]->state_score;
+        J.emit_out = jobs[k]->emit_out;
+        J.state_stride = jobs[k]->state_stride;
+        W[2 * k] = jobs[k]->w_kv_f32;
+        W[2 * k + 1] = jobs[k]->w_gate_f32;
+        part[2 * k] = base;
+        part[2 * k + 1] = base + (size_t)n_kg * n_seq * width;
+        rows[2 * k] = rows[2 * k + 1] = width;
+        ks[2 * k] = ks[2 * k + 1] = ds4hip_mm_kslice(width, in_dim, 2);
+        base += (size_t)2 * n_kg * n_seq * width;
+    }
+    int rc = ds4hip_mm_f32_parts_mats(W, part, rows, ks, 4, x_f32, in_dim, n_seq, st);
+    if (rc) return ds4hip_set_last_error(rc);
+    A.blk1 = (A.j[0].width + 255) / 256;
+    hipLaunchKernelGGL(comp_pair_update_kernel, dim3(A.blk1 + (A.j[1].width + 255) / 256, n_seq), dim3(256), 0, st,
+                       A, pos_dev, n_seq, ratio);
+    if (any)
+        hipLaunchKernelGGL(comp_pair_emit_kernel, dim3(2 * n_seq), dim3(512), 0, st, A, n_seq, ratio,
+                           rope_args(il, 0), pos_dev);
     return ds4hip_set_last_error(hip_status(hipGetLastError()));
 }

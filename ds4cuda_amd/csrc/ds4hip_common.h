@@ -217,6 +217,12 @@ int ds4hip_mm_k_groups(int n_rows, int n_cols, int n_mats);
 int ds4hip_mm_f32_parts(const float *W, const float *X, float *part, int n_rows, int n_cols,
                         int n_batch, hipStream_t st, const float *W2 = nullptr,
                         float *part2 = nullptr);
+// The k-slice (columns per wave) ds4hip_mm_f32_parts uses for that shape, and
+// up to four matrices of their own row counts and k-slices over one X in one
+// launch (matrix z's partials exactly as a launch of it alone with ks[z]).
+int ds4hip_mm_kslice(int n_rows, int n_cols, int n_mats);
+int ds4hip_mm_f32_parts_mats(const float *const *W, float *const *part, const int *n_rows, const int *ks,
+                             int n_mats, const float *X, int n_cols, int n_batch, hipStream_t st);
 
 // Records the last failing status for the void-returning C++ shims.
 extern "C" int ds4hip_set_last_error(int code);

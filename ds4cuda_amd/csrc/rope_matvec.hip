@@ -565,19 +565,28 @@ __device__ inline void mm_compute(const MmFrag<kF32W> &f, bool bok, float4_t *ac
 // the k-group's partial to Y + blockIdx.y * n_batch * n_rows (no atomics): the
 // k-groups are summed afterwards in k order, so the result is the same on
 // every run.
+// Up to four matrices over the same X and column count, one per blockIdx.z,
+// each with its own row count and k-slice (workgroups past a matrix's row
+// tiles or k-groups exit at once).
+struct MmMats {
+    const void *W[4];
+    float *Y[4];
+    int n_rows[4];
+    int ks[4];
+};
+
 template <bool kF32W>
-__global__ __launch_bounds__(256) void mm_stream_kernel(const void *__restrict__ Wv0,
-                                                        const void *__restrict__ Wv1,
-                                                        const float *__restrict__ X,
-                                                        float *__restrict__ Y0,
-                                                        float *__restrict__ Y1, int n_rows,
-                                                        int n_cols, int n_batch, int kslice) {
+__global__ __launch_bounds__(256) void mm_stream_kernel(const MmMats M, const float *__restrict__ X, int n_cols,
+                                                        int n_batch) {
     constexpr int kDepth = 4;   // 32-column steps in flight
     __shared__ float4_t red[4][4][64];   // [wave][row tile][lane]
-    const void *Wv = blockIdx.z ? Wv1 : Wv0;
-    float *Y = blockIdx.z ? Y1 : Y0;
+    const void *Wv = M.W[blockIdx.z];
+    float *Y = M.Y[blockIdx.z];
+    const int n_rows = M.n_rows[blockIdx.z];
+    const int kslice = M.ks[blockIdx.z];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r0 = blockIdx.x * 64;
+    if (r0 >= n_rows || (long long)blockIdx.y * 4 * kslice >= n_cols) return;   // workgroup-uniform
     const int i = lane & 15, q = lane >> 4;
     const int k0 = (blockIdx.y * 4 + wave) * kslice;
     const int k1 = min(k0 + kslice, n_cols);
@@ -648,14 +657,30 @@ int mm_kslice(int n_rows, int n_cols, int n_mats) {
 }
 
 template <bool kF32W>
+int mm_launch_mats(const MmMats &M, int n_mats, const float *X, int n_cols, int n_batch, hipStream_t st) {
+    int max_rows = 0, max_kg = 0;
+    for (int z = 0; z < n_mats; ++z) {
+        max_rows = std::max(max_rows, M.n_rows[z]);
+        max_kg = std::max(max_kg, (n_cols + 4 * M.ks[z] - 1) / (4 * M.ks[z]));
+    }
+    const dim3 grid((max_rows + 63) / 64, max_kg, n_mats);
+    hipLaunchKernelGGL(mm_stream_kernel<kF32W>, grid, dim3(256), 0, st, M, X, n_cols, n_batch);
+    return hip_status(hipGetLastError());
+}
+
+template <bool kF32W>
 int mm_launch(const void *W, const float *X, float *part, int n_rows, int n_cols, int n_batch,
               hipStream_t st, const void *W2 = nullptr, float *part2 = nullptr) {
     const int n_mats = W2 ? 2 : 1;
-    const int ks = mm_kslice(n_rows, n_cols, n_mats);
-    const dim3 grid((n_rows + 63) / 64, (n_cols + 4 * ks - 1) / (4 * ks), n_mats);
-    hipLaunchKernelGGL(mm_stream_kernel<kF32W>, grid, dim3(256), 0, st, W, W2 ? W2 : W, X, part,
-                       part2 ? part2 : part, n_rows, n_cols, n_batch, ks);
-    return hip_status(hipGetLastError());
+    MmMats M = {};
+    M.W[0] = W;
+    M.Y[0] = part;
+    M.n_rows[0] = n_rows;
+    M.W[1] = W2;
+    M.Y[1] = part2;
+    M.n_rows[1] = n_rows;
+    M.ks[0] = M.ks[1] = mm_kslice(n_rows, n_cols, n_mats);
+    return mm_launch_mats<kF32W>(M, n_mats, X, n_cols, n_batch, st);
 }
 
 // Projection into Y through k-group partials in ws (skipped when one k-group
@@ -681,6 +706,24 @@ int ds4hip_mm_k_groups(int n_rows, int n_cols, int n_mats) {
     const int ks = mm_kslice(n_rows, n_cols, n_mats);
     return (n_cols + 4 * ks - 1) / (4 * ks);
 }
+
+int ds4hip_mm_f32_parts_mats(const float *const *W, float *const *part, const int *n_rows, const int *ks,
+                             int n_mats, const float *X, int n_cols, int n_batch, hipStream_t st) {
+    if (!W || !part || !n_rows || !ks || n_mats < 1 || n_mats > 4 || !X || n_cols <= 0 || n_cols % 32 ||
+        n_batch <= 0 || n_batch > 16)
+        return kEINVAL;
+    MmMats M = {};
+    for (int z = 0; z < n_mats; ++z) {
+        if (!W[z] || !part[z] || n_rows[z] <= 0 || ks[z] <= 0 || ks[z] % 32) return kEINVAL;
+        M.W[z] = W[z];
+        M.Y[z] = part[z];
+        M.n_rows[z] = n_rows[z];
+        M.ks[z] = ks[z];
+    }
+    return mm_launch_mats<true>(M, n_mats, X, n_cols, n_batch, st);
+}
+
+int ds4hip_mm_kslice(int n_rows, int n_cols, int n_mats) { return mm_kslice(n_rows, n_cols, n_mats); }
 
 int ds4hip_mm_f32_parts(const float *W, const float *X, float *part, int n_rows, int n_cols,
                         int n_batch, hipStream_t st, const float *W2, float *part2) {

@@ -601,6 +601,45 @@ def compressor_decode_step_batch_w32(is_attn, x, w_kv, w_gate, w_ape, w_norm, in
     return list(em)
 
 
+class CompressorBatchJob(C.Structure):
+    """ds4hip_compressor_batch_job: one compressor of compressor_pair_step_batch_w32."""
+    _fields_ = [("w_kv_f32", C.c_void_p), ("w_gate_f32", C.c_void_p), ("w_ape_f16", C.c_void_p),
+                ("w_norm_f32", C.c_void_p), ("head_dim_out", C.c_int), ("state_kv", C.c_void_p),
+                ("state_score", C.c_void_p), ("state_stride", C.c_longlong), ("emit_out", C.c_void_p)]
+
+
+def compressor_pair_scratch(n_seq, in_dim, attn_head_dim_out, index_head_dim_out, ratio, device):
+    """Scratch tensor (uint8) for compressor_pair_step_batch_w32."""
+    nb = lib().ds4hip_compressor_pair_batch_scratch_bytes(n_seq, in_dim, attn_head_dim_out, index_head_dim_out,
+                                                          ratio)
+    return torch.empty(nb, dtype=torch.uint8, device=device)
+
+
+def compressor_pair_step_batch_w32(x, in_dim, ratio, pos, pos_dev, il, attn, index, scratch, stream=None):
+    """A layer's attention and indexer compressors for len(pos) sequences in
+    three launches; attn / index: dicts of w_kv, w_gate, w_ape, w_norm,
+    head_dim_out, state_kv, state_score, state_stride, emit_out (the
+    arguments of compressor_decode_step_batch_w32). Returns the host emit flags."""
+    n = len(pos)
+    ph = (C.c_int * n)(*[int(p) for p in pos])
+    em = (C.c_int * n)()
+    _check(pos_dev, torch.int32, n, "pos_dev")
+    _check(x, torch.float32, n * in_dim, "x")
+    jobs = []
+    for j in (attn, index):
+        for k in ("w_kv", "w_gate", "w_norm", "state_kv", "state_score", "emit_out"):
+            _check(j[k], torch.float32, None, k)
+        _check(j["w_ape"], j["w_ape"].dtype, None, "w_ape")
+        jobs.append(CompressorBatchJob(_ptr(j["w_kv"]), _ptr(j["w_gate"]), _ptr(j["w_ape"]), _ptr(j["w_norm"]),
+                                       int(j["head_dim_out"]), _ptr(j["state_kv"]), _ptr(j["state_score"]),
+                                       int(j["state_stride"]), _ptr(j["emit_out"])))
+    _check(scratch, torch.uint8, None, "scratch")
+    call("ds4hip_compressor_pair_step_batch_w32", n, _ptr(x), in_dim, ratio, C.cast(ph, C.c_void_p), _ptr(pos_dev),
+         il, C.byref(jobs[0]), C.byref(jobs[1]), C.cast(em, C.c_void_p), _ptr(scratch), scratch.numel(),
+         _stream(stream))
+    return list(em)
+
+
 def launch_rms_norm_f32(x, w, y, n, eps=1e-6, stream=None):
     _check(x, torch.float32, n, "x")
     _check(w, torch.float32, n, "w")

@@ -521,6 +521,31 @@ int ds4hip_compressor_decode_step_batch_w32(int is_attn, int n_seq, const float 
                                             int *emitted_out_host, float *scratch,
                                             size_t scratch_bytes, void *stream);
 
+/* One layer's two batched compressors at once (no reference counterpart; the
+ * reference runs them one after the other, cuda/forward_layer.cu:1021-1072):
+ * the attention compressor (is_attn = 1) and the indexer's (is_attn = 0),
+ * same x, ratio and positions, in three launches instead of six (both
+ * projections, both state updates, both emits). Each job's arguments mean
+ * what they mean in ds4hip_compressor_decode_step_batch_w32, and the results
+ * equal two calls of it bit for bit. scratch:
+ * ds4hip_compressor_pair_batch_scratch_bytes(...) bytes. */
+typedef struct ds4hip_compressor_batch_job {
+    const float *w_kv_f32, *w_gate_f32;
+    const uint16_t *w_ape_f16;
+    const float *w_norm_f32;
+    int head_dim_out;
+    float *state_kv, *state_score;
+    long long state_stride;
+    float *emit_out;
+} ds4hip_compressor_batch_job;
+size_t ds4hip_compressor_pair_batch_scratch_bytes(int n_seq, int in_dim, int attn_head_dim_out,
+                                                  int index_head_dim_out, int compress_ratio);
+int ds4hip_compressor_pair_step_batch_w32(int n_seq, const float *x_f32, int in_dim, int compress_ratio,
+                                          const int *pos_host, const int *pos_dev, int il,
+                                          const ds4hip_compressor_batch_job *attn,
+                                          const ds4hip_compressor_batch_job *index, int *emitted_out_host,
+                                          float *scratch, size_t scratch_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -240,3 +240,43 @@ def test_batched_block_graph_replay(gpu):
         torch.cuda.synchronize()
         assert torch.equal(blk.y, eager[k]), k
         _ = (blk.y * 2).sum().item()   # eager work between replays
+
+
+def test_batched_block_compressor_pair_equals_two_steps(gpu):
+    """fused=True (both compressors in three launches,
+    ds4hip_compressor_pair_step_batch_w32) against fused=False (two
+    ds4hip_compressor_decode_step_batch_w32 calls): the block output, both
+    compressors' states and emitted rows bit for bit over three steps (with
+    emits: sequence 2 emits on the first step, others later)."""
+    nb = 4
+    ctx = np.array([700, 1301, 2046, 4099])
+    pos = (ctx - 1).astype(np.int64)
+    w = make_weights(gpu)
+    blks = [BatchedAttentionBlock(w, nb, int(pos.max()) + 4, device=gpu, fused=f) for f in (True, False)]
+    for blk in blks:
+        for b in range(nb):
+            n = int(pos[b]) // 4
+            blk.load_history(b, torch.from_numpy(synth.kv_rows(81, b, n)).to(gpu),
+                             torch.from_numpy(synth.kv_rows(82, b, SWA)).to(gpu),
+                             np.arange(pos[b] - SWA + 1, pos[b] + 1),
+                             torch.from_numpy(synth.normal(83, b, n * 128).reshape(n, 128)).to(gpu))
+    g = lambda s, shape: torch.from_numpy(synth.normal(85, s, int(np.prod(shape))).reshape(shape)).to(gpu)
+    n_emit = 0
+    for step in range(3):
+        p = pos + step
+        x, kv_cur = g(10 * step + 1, (nb, IN)), g(10 * step + 2, (nb, 512))
+        q = g(10 * step + 3, (nb, 64, 512)).to(torch.bfloat16)
+        q_idx = g(10 * step + 4, (nb, 64, 128))
+        w_idx = g(10 * step + 5, (nb, 64)) / float(np.sqrt(128 * 64))
+        sinks = g(10 * step + 6, (nb, 64))
+        ys = [blk.step(p, x, kv_cur, q, q_idx, w_idx, sinks).clone() for blk in blks]
+        torch.cuda.synchronize()
+        n_emit += int(sum((int(v) + 1) % 4 == 0 for v in p))
+        assert torch.isfinite(ys[0]).all()
+        assert torch.equal(ys[0], ys[1]), step
+        for name in ("st_kv", "st_sc", "sti_kv", "sti_sc", "emit", "emit_i"):
+            assert torch.equal(getattr(blks[0], name), getattr(blks[1], name)), (step, name)
+        # the key rows (the last one is the trash row that every non-emitting
+        # sequence writes at once: its content is whichever write lands last)
+        assert torch.equal(blks[0].keys[:-1], blks[1].keys[:-1]), step
+    assert n_emit >= 2

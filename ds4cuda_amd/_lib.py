@@ -43,6 +43,7 @@ SIGNATURES: dict[str, list] = {
     "ds4hip_mul_mv_f16_rope_f32": [_vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp],
     "ds4hip_attn_out_decode_workspace_bytes": [_i, _i, _i, _i],
     "ds4hip_token_prologue_f32": [_vp, _vp],
+    "ds4hip_batch_rows_push_f32": [_vp, _vp, _vp, _vp, _i, _i, _vp],
     "ds4hip_compressor_pair_batch_scratch_bytes": [_i, _i, _i, _i, _i],
     "ds4hip_compressor_pair_step_batch_w32": [_i, _vp, _i, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _sz, _vp],
     "ds4hip_session_claim_raw_row": [_vp, _i, C.POINTER(_ll)],

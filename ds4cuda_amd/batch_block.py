@@ -75,8 +75,9 @@ class BatchedAttentionBlock:
         self.emit_i = torch.zeros((B, IDX_DIM), device=device)
         self.scratch = ops.compressor_batch_scratch(B, in_dim, HEAD_DIM, RATIO, device)
         self.scratch_i = ops.compressor_batch_scratch(B, in_dim, IDX_DIM, RATIO, device)
-        # fused: both compressors in three launches (ds4hip_compressor_pair_step_batch_w32,
-        # the same results) instead of six
+        # fused: both compressors in three launches (ds4hip_compressor_pair_step_batch_w32)
+        # instead of six, and the three row pushes in one (ds4hip_batch_rows_push_f32);
+        # the same results
         self.fused = fused
         self.scratch_pair = ops.compressor_pair_scratch(B, in_dim, HEAD_DIM, IDX_DIM, RATIO, device)
         self.mm_ws = ops.mul_mm_workspace(out_dim, N_HEAD * HEAD_DIM, B, device)
@@ -174,10 +175,14 @@ class BatchedAttentionBlock:
                                                  w["wn_i"], self.in_dim, IDX_DIM, RATIO, P["pos_host"],
                                                  P["pos_dev"], self.il, self.sti_kv, self.sti_sc,
                                                  8 * 256, self.emit_i, self.scratch_i, stream=stream)
-        self.cache.append(kv_cur, dst_rows=P["dst_raw"], stream=stream)
-        self.cache.append(self.emit, dst_rows=P["dst_emit"], stream=stream)
-        call("ds4hip_rows_scatter_f32", _ptr(self.emit_i), B, IDX_DIM, _ptr(self.keys),
-             _ptr(P["dst_key"]), _stream(stream))
+        if self.fused:   # the three row pushes in one launch
+            ops.batch_rows_push_f32(self.cache, ((kv_cur, P["dst_raw"]), (self.emit, P["dst_emit"])), self.emit_i,
+                                    self.keys, P["dst_key"], stream=stream)
+        else:
+            self.cache.append(kv_cur, dst_rows=P["dst_raw"], stream=stream)
+            self.cache.append(self.emit, dst_rows=P["dst_emit"], stream=stream)
+            call("ds4hip_rows_scatter_f32", _ptr(self.emit_i), B, IDX_DIM, _ptr(self.keys),
+                 _ptr(P["dst_key"]), _stream(stream))
         self.rowlist = P["rowlist"]
         ops.indexer_topk_positions_batch(q_idx, w_idx, self.keys, self.key_row0, P["n_comp"],
                                          self.top_k, 0, self.scores, self.rowlist,

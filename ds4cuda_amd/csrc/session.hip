@@ -28,6 +28,7 @@
 
 #include "../../include/ds4hip_session.h"
 #include "ds4hip_common.h"
+#include "step_bodies.h"
 
 using namespace ds4hip;
 
@@ -407,9 +408,7 @@ __global__ __launch_bounds__(256) void rows_scatter_kernel(const float *__restri
                                                            const long long *__restrict__ dst_rows) {
     const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r >= n_rows) return;
-    const float4_t *s = reinterpret_cast<const float4_t *>(src + (size_t)r * width);
-    float4_t *d = reinterpret_cast<float4_t *>(dst + (size_t)dst_rows[r] * width);
-    for (int i = threadIdx.x & 63; i < width / 4; i += 64) d[i] = s[i];
+    row_copy_body(src, r, width, dst, dst_rows, threadIdx.x & 63);
 }
 }  // namespace
 

@@ -136,4 +136,13 @@ __device__ inline void comp_project_rows(const float *xs, const void *__restrict
     }
 }
 
+// Row r of src [n][width] fp32 to row dst_rows[r] of dst, by one 64-lane
+// wave (lane t: 16-byte chunks t, t + 64, ...). width % 4 == 0.
+__device__ inline void row_copy_body(const float *__restrict__ src, int r, int width, float *__restrict__ dst,
+                                     const long long *__restrict__ dst_rows, int t) {
+    const float4_t *s = reinterpret_cast<const float4_t *>(src + (size_t)r * width);
+    float4_t *d = reinterpret_cast<float4_t *>(dst + (size_t)dst_rows[r] * width);
+    for (int i = t; i < width / 4; i += 64) d[i] = s[i];
+}
+
 }  // namespace ds4hip

@@ -601,6 +601,31 @@ def compressor_decode_step_batch_w32(is_attn, x, w_kv, w_gate, w_ape, w_norm, in
     return list(em)
 
 
+class RowsPush(C.Structure):
+    """ds4hip_rows_push: two FP8 appends and one fp32 row scatter in one launch."""
+    _fields_ = [("fp8_src", C.c_void_p * 2), ("fp8_n", C.c_int * 2), ("fp8_dst", C.c_void_p * 2),
+                ("f32_src", C.c_void_p), ("f32_n", C.c_int), ("f32_width", C.c_int), ("f32_dst", C.c_void_p),
+                ("f32_dst_rows", C.c_void_p)]
+
+
+def batch_rows_push_f32(cache, fp8_sets, f32_src, f32_dst, f32_dst_rows, stream=None):
+    """fp8_sets: two (rows [n, 512] fp32, dst_rows int64 [n]) appended to the
+    FP8 cache; f32_src [m, w] rows copied to f32_dst rows f32_dst_rows (int64 [m])."""
+    p = RowsPush()
+    for k, (rows, dst) in enumerate(fp8_sets):
+        n = rows.shape[0]
+        _check(rows, torch.float32, n * HEAD_DIM, "fp8 rows")
+        _check(dst, torch.int64, n, "fp8 dst_rows")
+        p.fp8_src[k], p.fp8_n[k], p.fp8_dst[k] = _ptr(rows), n, _ptr(dst)
+    m, w = f32_src.shape
+    _check(f32_src, torch.float32, m * w, "f32_src")
+    _check(f32_dst, torch.float32, None, "f32_dst")
+    _check(f32_dst_rows, torch.int64, m, "f32_dst_rows")
+    p.f32_src, p.f32_n, p.f32_width, p.f32_dst, p.f32_dst_rows = _ptr(f32_src), m, w, _ptr(f32_dst), _ptr(f32_dst_rows)
+    call("ds4hip_batch_rows_push_f32", C.byref(p), _ptr(cache.codes), _ptr(cache.sexp), _ptr(cache.tail), HEAD_DIM,
+         N_ROT, _stream(stream))
+
+
 class CompressorBatchJob(C.Structure):
     """ds4hip_compressor_batch_job: one compressor of compressor_pair_step_batch_w32."""
     _fields_ = [("w_kv_f32", C.c_void_p), ("w_gate_f32", C.c_void_p), ("w_ape_f16", C.c_void_p),

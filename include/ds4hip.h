@@ -58,6 +58,24 @@ int ds4hip_fp8_kv_quantize_append(const float *kv_in, int n_rows, int head_dim, 
                                   uint8_t *codes, int8_t *sexp, uint16_t *tail,
                                   long long row0, const long long *dst_rows, void *stream);
 
+/* The row pushes of a batched step in one launch (no reference counterpart):
+ * two FP8 appends (rows fp8_src[k] [fp8_n[k]][head_dim] fp32 to cache rows
+ * fp8_dst[k][r], as ds4hip_fp8_kv_quantize_append) and one fp32 row scatter
+ * (as ds4hip_rows_scatter_f32: f32_src row r to f32_dst row f32_dst_rows[r],
+ * f32_width floats). A set with n = 0 is skipped. The results equal the
+ * three separate calls. */
+typedef struct ds4hip_rows_push {
+    const float *fp8_src[2];
+    int fp8_n[2];
+    const long long *fp8_dst[2];
+    const float *f32_src;
+    int f32_n, f32_width;
+    float *f32_dst;
+    const long long *f32_dst_rows;
+} ds4hip_rows_push;
+int ds4hip_batch_rows_push_f32(const ds4hip_rows_push *p, uint8_t *codes, int8_t *sexp, uint16_t *tail,
+                               int head_dim, int n_rot, void *stream);
+
 /* ---- decode attention ------------------------------------------------------------- */
 
 /* Replaces ds4cuda::launch_flash_attn_decode_raw_f32 (cuda/flash_attn.cuh:73).

@@ -244,10 +244,12 @@ def test_batched_block_graph_replay(gpu):
 
 def test_batched_block_compressor_pair_equals_two_steps(gpu):
     """fused=True (both compressors in three launches,
-    ds4hip_compressor_pair_step_batch_w32) against fused=False (two
-    ds4hip_compressor_decode_step_batch_w32 calls): the block output, both
-    compressors' states and emitted rows bit for bit over three steps (with
-    emits: sequence 2 emits on the first step, others later)."""
+    ds4hip_compressor_pair_step_batch_w32, and the row pushes in one,
+    ds4hip_batch_rows_push_f32) against fused=False (two
+    ds4hip_compressor_decode_step_batch_w32 calls, two FP8 appends and a row
+    scatter): the block output, both compressors' states, emitted rows, key
+    rows and FP8 cache bit for bit over three steps (with emits: sequence 2
+    emits on the first step, others later)."""
     nb = 4
     ctx = np.array([700, 1301, 2046, 4099])
     pos = (ctx - 1).astype(np.int64)
@@ -279,4 +281,6 @@ def test_batched_block_compressor_pair_equals_two_steps(gpu):
         # the key rows (the last one is the trash row that every non-emitting
         # sequence writes at once: its content is whichever write lands last)
         assert torch.equal(blks[0].keys[:-1], blks[1].keys[:-1]), step
+        for name in ("codes", "sexp", "tail"):   # the cache, its trash row aside
+            assert torch.equal(getattr(blks[0].cache, name)[:-1], getattr(blks[1].cache, name)[:-1]), (step, name)
     assert n_emit >= 2

@@ -76,8 +76,8 @@ class BatchedAttentionBlock:
         self.scratch = ops.compressor_batch_scratch(B, in_dim, HEAD_DIM, RATIO, device)
         self.scratch_i = ops.compressor_batch_scratch(B, in_dim, IDX_DIM, RATIO, device)
         # fused: both compressors in three launches (ds4hip_compressor_pair_step_batch_w32)
-        # instead of six, and the three row pushes in one (ds4hip_batch_rows_push_f32);
-        # the same results
+        # instead of six, the three row pushes in one (ds4hip_batch_rows_push_f32), and
+        # the inverse RoPE in the decode's merge; the same results
         self.fused = fused
         self.scratch_pair = ops.compressor_pair_scratch(B, in_dim, HEAD_DIM, IDX_DIM, RATIO, device)
         self.mm_ws = ops.mul_mm_workspace(out_dim, N_HEAD * HEAD_DIM, B, device)
@@ -187,11 +187,17 @@ class BatchedAttentionBlock:
         ops.indexer_topk_positions_batch(q_idx, w_idx, self.keys, self.key_row0, P["n_comp"],
                                          self.top_k, 0, self.scores, self.rowlist,
                                          pos_offset=SWA, stream=stream)
-        ops.flash_attn_decode_fp8(q, sinks, self.out, self.cache, P["counts"],
-                                  row_idx=self.rowlist, page_table=self.page_table,
-                                  page_rows=self.page_rows, workspace=P["ws"], stream=stream)
-        ops.tail_rope_yarn_batch_f32(self.out, self.out, B, N_HEAD, HEAD_DIM, N_ROT,
-                                     P["pos_dev"], self.il, inverse=True, stream=stream)
+        if self.fused:   # the merge writes the inverse-RoPE'd rows
+            ops.flash_attn_decode_fp8(q, sinks, self.out, self.cache, P["counts"],
+                                      row_idx=self.rowlist, page_table=self.page_table,
+                                      page_rows=self.page_rows, workspace=P["ws"],
+                                      rope_out=(P["pos_dev"], self.il), stream=stream)
+        else:
+            ops.flash_attn_decode_fp8(q, sinks, self.out, self.cache, P["counts"],
+                                      row_idx=self.rowlist, page_table=self.page_table,
+                                      page_rows=self.page_rows, workspace=P["ws"], stream=stream)
+            ops.tail_rope_yarn_batch_f32(self.out, self.out, B, N_HEAD, HEAD_DIM, N_ROT,
+                                         P["pos_dev"], self.il, inverse=True, stream=stream)
         ops.mul_mm_bf16_f32(w["w_out"], self.out, self.y, self.out_dim, N_HEAD * HEAD_DIM, B,
                             workspace=self.mm_ws, stream=stream)
         return self.y

@@ -102,25 +102,29 @@ struct DecodeArgs {
     float *ws_o;                     // [slot][64][512]
     float *ws_ml;                    // [slot][2][64]
     int *ws_prob;                    // [slot]
-    // merge output in the rotated Q8_0 form (DS4HIP_DECODE_OUT_ROPE_Q8)
-    int out_q8;
+    // merge output form (DS4HIP_DECODE_OUT_*): 0 fp32 rows, 1 rotated Q8_0,
+    // 2 rotated fp32; rotation position rope_pos_dev[p] or rope_pos
+    int out_form;
     int rope_pos;
+    const int *rope_pos_dev;
     RopeParams rope;
     int8_t *q8_out;
     float *q8_scale;
 };
 
-// The rotation coefficients of dims dim0 .. dim0 + 3 for merge_store (out_q8
-// and tail dims only), computed at the merge's start, under its loads.
+// The rotation coefficients of dims dim0 .. dim0 + 3 of problem p for
+// merge_store (rotated forms and tail dims only), computed at the merge's
+// start, under its loads.
 struct MergeRope {
     float c[2], s[2];
 };
-__device__ inline MergeRope merge_rope(const DecodeArgs &A, int dim0) {
+__device__ inline MergeRope merge_rope(const DecodeArgs &A, int p, int dim0) {
     MergeRope r = {{1.0f, 1.0f}, {0.0f, 0.0f}};
     constexpr int kNope = kD - kRot;
-    if (A.out_q8 && dim0 >= kNope) {
-        rope_cs((dim0 - kNope) / 2, A.rope_pos, A.rope, r.c[0], r.s[0]);
-        rope_cs((dim0 + 2 - kNope) / 2, A.rope_pos, A.rope, r.c[1], r.s[1]);
+    if (A.out_form && dim0 >= kNope) {
+        const int pos = A.rope_pos_dev ? A.rope_pos_dev[p] : A.rope_pos;
+        rope_cs((dim0 - kNope) / 2, pos, A.rope, r.c[0], r.s[0]);
+        rope_cs((dim0 + 2 - kNope) / 2, pos, A.rope, r.c[1], r.s[1]);
     }
     // here, not sunk next to their use at the end
     asm volatile("" : "+v"(r.c[0]), "+v"(r.c[1]), "+v"(r.s[0]), "+v"(r.s[1]));
@@ -128,13 +132,15 @@ __device__ inline MergeRope merge_rope(const DecodeArgs &A, int dim0) {
 }
 
 // The merge's result for dims dim0 .. dim0 + 3 of head h of problem p: into
-// out, or (out_q8) rotated by the inverse tail RoPE and quantized as Q8_0,
-// with the arithmetic of rope_q8_kernel. The 8 lanes of a 32-dim block are
-// consecutive lanes of one wave, all present.
+// out, or rotated by the inverse tail RoPE (rope_tail_kernel's arithmetic)
+// into out (out_form 2) or quantized as Q8_0 with the arithmetic of
+// rope_q8_kernel (out_form 1). The 8 lanes of a 32-dim block are consecutive
+// lanes of one wave, all present.
 __device__ inline void merge_store(const DecodeArgs &A, int p, int h, int dim0, float4_t res, const MergeRope &R) {
     const long long o = (long long)p * (kH * kD) + h * kD + dim0;
-    if (!A.out_q8) {
-        *reinterpret_cast<float4_t *>(A.out + (long long)p * A.out_stride + h * kD + dim0) = res;
+    float4_t *dst = reinterpret_cast<float4_t *>(A.out + (long long)p * A.out_stride + h * kD + dim0);
+    if (!A.out_form) {
+        *dst = res;
         return;
     }
     float v[4] = {res[0], res[1], res[2], res[3]};
@@ -142,6 +148,10 @@ __device__ inline void merge_store(const DecodeArgs &A, int p, int h, int dim0, 
     if (dim0 >= kNope) {
         rope_apply(v[0], v[1], R.c[0], R.s[0], v[0], v[1]);
         rope_apply(v[2], v[3], R.c[1], R.s[1], v[2], v[3]);
+    }
+    if (A.out_form == 2) {
+        *dst = float4_t{v[0], v[1], v[2], v[3]};
+        return;
     }
     float a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
 #pragma unroll
@@ -2389,7 +2399,7 @@ __global__ __launch_bounds__(128) void decode_merge_kernel(const DecodeArgs A) {
     const int h = blockIdx.y;
     const int tid = threadIdx.x;
     const float sink = A.sinks[(long long)p * A.sinks_stride + h] * kLog2e;
-    const MergeRope R = merge_rope(A, 4 * tid);
+    const MergeRope R = merge_rope(A, p, 4 * tid);
     const long long b0 = A.start[p], b1 = b0 + A.count[p];
     long long s0 = 0, n_slot = 0;
     if (b1 > b0) {
@@ -2477,7 +2487,7 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_wide_kernel(const 
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const float sink = A.sinks[(long long)p * A.sinks_stride + h] * kLog2e;
-    const MergeRope R = merge_rope(A, half * (kD / 2) + 4 * lane);
+    const MergeRope R = merge_rope(A, p, half * (kD / 2) + 4 * lane);
     const long long b0 = A.start[p], b1 = b0 + A.count[p];
     long long s0 = 0, n_slot = 0;
     if (b1 > b0) {
@@ -2775,9 +2785,11 @@ extern "C" int ds4hip_flash_attn_decode_fp8(
     const ds4hip_decode_opts o = opts ? *opts : ds4hip_decode_opts{};
     if ((o.exact_p != 0 && o.exact_p != 1) ||
         (o.kernel != DS4HIP_DECODE_KERNEL_AUTO && o.kernel != DS4HIP_DECODE_KERNEL_REGLOAD) ||
-        (o.out_form != DS4HIP_DECODE_OUT_F32 && o.out_form != DS4HIP_DECODE_OUT_ROPE_Q8) ||
+        (o.out_form != DS4HIP_DECODE_OUT_F32 && o.out_form != DS4HIP_DECODE_OUT_ROPE_Q8 &&
+         o.out_form != DS4HIP_DECODE_OUT_ROPE_F32) ||
+        (o.out_form != DS4HIP_DECODE_OUT_F32 && (o.out_pos < 0 || o.out_il < 0)) ||
         (o.out_form == DS4HIP_DECODE_OUT_ROPE_Q8 &&
-         (!o.q8_out || !o.q8_scale || o.out_pos < 0 || o.out_il < 0 || reinterpret_cast<uintptr_t>(o.q8_out) % 4)))
+         (!o.q8_out || !o.q8_scale || reinterpret_cast<uintptr_t>(o.q8_out) % 4)))
         return ds4hip_set_last_error(kEINVAL);
     // q_is_f32 2: the converted form (only the flat-stage kernel reads it); its
     // problems kQPrepWords apart at least
@@ -2833,9 +2845,10 @@ extern "C" int ds4hip_flash_attn_decode_fp8(
     A.total = A.start[n_prob];
     carve(A, workspace, pl);
     if (!row_idx && !page_table) A.phys = nullptr;
-    if (o.out_form == DS4HIP_DECODE_OUT_ROPE_Q8) {
-        A.out_q8 = 1;
+    if (o.out_form != DS4HIP_DECODE_OUT_F32) {
+        A.out_form = o.out_form == DS4HIP_DECODE_OUT_ROPE_Q8 ? 1 : 2;
         A.rope_pos = o.out_pos;
+        A.rope_pos_dev = o.out_pos_dev;
         A.rope = rope_params(kRot, o.out_il, true);
         A.q8_out = o.q8_out;
         A.q8_scale = o.q8_scale;

@@ -161,18 +161,25 @@ def launch_flash_attn_decode_mixed_f32_prealloc(Q, raw_kv, comp_kv, comp_allowed
 class DecodeOpts(C.Structure):
     """ds4hip_decode_opts: per-call P precision, kernel choice and merge output form."""
     _fields_ = [("exact_p", C.c_int), ("kernel", C.c_int), ("out_form", C.c_int), ("out_pos", C.c_int),
-                ("out_il", C.c_int), ("q8_out", C.c_void_p), ("q8_scale", C.c_void_p)]
+                ("out_il", C.c_int), ("q8_out", C.c_void_p), ("q8_scale", C.c_void_p),
+                ("out_pos_dev", C.c_void_p)]
 
 
 _KERNELS = {"auto": 0, "regload": 1}
 
 
-def decode_opts(exact_p=False, kernel="auto", rope_q8=None):
+def decode_opts(exact_p=False, kernel="auto", rope_q8=None, rope_out=None):
     """rope_q8: None (the merge writes out) or (q8_out int8, q8_scale fp32,
     pos, il): the merge writes the inverse-RoPE'd rows in Q8_0 form instead
-    (DS4HIP_DECODE_OUT_ROPE_Q8), the input of attn_out_decode_q8_f32."""
+    (DS4HIP_DECODE_OUT_ROPE_Q8), the input of attn_out_decode_q8_f32.
+    rope_out: (pos_dev int32 [n_prob], il): out holds the rows after the
+    inverse tail RoPE at each problem's position (DS4HIP_DECODE_OUT_ROPE_F32)."""
     if kernel not in _KERNELS:
         raise Ds4HipError(f"kernel must be one of {sorted(_KERNELS)}", -22)
+    if rope_out is not None:
+        pos_dev, il = rope_out
+        _check(pos_dev, torch.int32, None, "out_pos_dev")
+        return DecodeOpts(int(bool(exact_p)), _KERNELS[kernel], 2, 0, int(il), None, None, _ptr(pos_dev))
     if rope_q8 is None:
         return DecodeOpts(int(bool(exact_p)), _KERNELS[kernel])
     xq, xs, pos, il = rope_q8
@@ -220,7 +227,8 @@ def _q_mode(q):
 
 def flash_attn_decode_fp8(q, sinks, out, cache: Fp8KVCache, n_rows_per_prob, *, row_base=None,
                           row_base_stride=0, row_idx=None, page_table=None, page_rows=256,
-                          workspace=None, phases=3, exact_p=False, kernel="auto", rope_q8=None, stream=None):
+                          workspace=None, phases=3, exact_p=False, kernel="auto", rope_q8=None, rope_out=None,
+                          stream=None):
     """Decode attention of n_prob single-query problems over the FP8 cache.
 
     q [n_prob, 64, 512] bf16 or fp32 (or int32 [n_prob, q_prep_words()], a
@@ -229,7 +237,7 @@ def flash_attn_decode_fp8(q, sinks, out, cache: Fp8KVCache, n_rows_per_prob, *, 
     position row_idx[p, r] (or r), mapped through page_table[p] (pages of
     page_rows rows) or offset by row_base[p] (int64 tensor) / p*row_base_stride.
     exact_p: P as f16 hi + lo instead of one f16; kernel: "auto" or "regload"
-    (the register-load kernel for direct rows too); rope_q8: see decode_opts.
+    (the register-load kernel for direct rows too); rope_q8, rope_out: see decode_opts.
     """
     n_prob = len(n_rows_per_prob)
     q_mode, q_stride = _q_mode(q)
@@ -249,7 +257,7 @@ def flash_attn_decode_fp8(q, sinks, out, cache: Fp8KVCache, n_rows_per_prob, *, 
          n_prob, _ptr(row_base), int(row_base_stride), _ptr(row_idx),
          row_idx.shape[-1] if row_idx is not None else 0, _ptr(page_table),
          page_table.shape[-1] if page_table is not None else 0, int(page_rows), N_HEAD,
-         HEAD_DIM, N_ROT, C.c_longlong(cache.n_rows), C.byref(decode_opts(exact_p, kernel, rope_q8)),
+         HEAD_DIM, N_ROT, C.c_longlong(cache.n_rows), C.byref(decode_opts(exact_p, kernel, rope_q8, rope_out)),
          _ptr(workspace), workspace.numel(), int(phases), _stream(stream))
     return workspace
 

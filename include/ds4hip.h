@@ -158,16 +158,21 @@ typedef struct ds4hip_decode_opts {
      * values at q8_out + p*n_head*head_dim and one fp32 scale per 32 values at
      * q8_scale + p*n_head*head_dim/32 (the quantization of
      * ds4hip_attn_out_decode_f32's first step, bit for bit) — the input of
-     * ds4hip_attn_out_decode_q8_f32. */
+     * ds4hip_attn_out_decode_q8_f32. DS4HIP_DECODE_OUT_ROPE_F32: out, each
+     * head's row after that inverse tail RoPE (ds4hip_tail_rope_yarn_batch_f32
+     * of out, bit for bit). out_pos_dev (device int32 [n_prob], may be NULL):
+     * problem p's position, in place of out_pos. */
     int out_form;
     int out_pos, out_il;
     int8_t *q8_out;
     float *q8_scale;
+    const int *out_pos_dev;
 } ds4hip_decode_opts;
 #define DS4HIP_DECODE_KERNEL_AUTO 0
 #define DS4HIP_DECODE_KERNEL_REGLOAD 1
 #define DS4HIP_DECODE_OUT_F32 0
 #define DS4HIP_DECODE_OUT_ROPE_Q8 1
+#define DS4HIP_DECODE_OUT_ROPE_F32 2
 
 /* Decode attention over the FP8 cache (additive: the FP8-cache form of
  * cuda/flash_attn.cuh:9-26,90-117, which take fp32 rows). Solves n_prob

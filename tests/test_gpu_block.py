@@ -244,10 +244,10 @@ def test_batched_block_graph_replay(gpu):
 
 def test_batched_block_compressor_pair_equals_two_steps(gpu):
     """fused=True (both compressors in three launches,
-    ds4hip_compressor_pair_step_batch_w32, and the row pushes in one,
-    ds4hip_batch_rows_push_f32) against fused=False (two
-    ds4hip_compressor_decode_step_batch_w32 calls, two FP8 appends and a row
-    scatter): the block output, both compressors' states, emitted rows, key
+    ds4hip_compressor_pair_step_batch_w32, the row pushes in one,
+    ds4hip_batch_rows_push_f32, and the inverse RoPE in the decode merge)
+    against fused=False (two ds4hip_compressor_decode_step_batch_w32 calls,
+    two FP8 appends and a row scatter, a RoPE launch): the block output, both compressors' states, emitted rows, key
     rows and FP8 cache bit for bit over three steps (with emits: sequence 2
     emits on the first step, others later)."""
     nb = 4

@@ -385,3 +385,31 @@ def test_decode_merge_rope_q8_output(gpu, n_rows, il):
     assert np.array_equal(xs.cpu().numpy().view(np.uint32), ss.cpu().numpy().view(np.uint32))
     assert torch.isfinite(ref).all()
     assert np.array_equal(got.cpu().numpy().view(np.uint32), ref.cpu().numpy().view(np.uint32))
+
+
+@pytest.mark.parametrize("counts", [[200, 50, 130], [3000, 700, 4000]])
+def test_decode_merge_rope_f32_output(gpu, counts):
+    """The decode merge's rotated fp32 output (decode_opts rope_out: per
+    problem positions from a device array) against the fp32 merge output
+    rotated by the batched inverse tail RoPE launcher, bit for bit; the first
+    counts take the narrow merge, the second the wide one."""
+    from ds4cuda_amd import synth
+    n, il = len(counts), 2
+    total = int(sum(counts))
+    x = synth.kv_rows(91, 1, total)
+    cache = ops.Fp8KVCache.empty(total, device=gpu)
+    cache.append(torch.from_numpy(x).to(gpu))
+    base = torch.tensor(np.concatenate([[0], np.cumsum(counts)[:-1]]), dtype=torch.int64, device=gpu)
+    g = torch.Generator(device=gpu)
+    g.manual_seed(92)
+    q = torch.randn((n, 64, 512), generator=g, device=gpu).to(torch.bfloat16)
+    sinks = torch.randn((n, 64), generator=g, device=gpu)
+    pos = torch.tensor([4000, 17, 65000][:n], dtype=torch.int32, device=gpu)
+    ref = torch.empty((n, 64, 512), device=gpu)
+    ops.flash_attn_decode_fp8(q, sinks, ref, cache, counts, row_base=base)
+    ops.tail_rope_yarn_batch_f32(ref, ref, n, 64, 512, 64, pos, il, inverse=True)
+    got = torch.empty((n, 64, 512), device=gpu)
+    ops.flash_attn_decode_fp8(q, sinks, got, cache, counts, row_base=base, rope_out=(pos, il))
+    torch.cuda.synchronize()
+    assert torch.isfinite(ref).all()
+    assert np.array_equal(got.cpu().numpy().view(np.uint32), ref.cpu().numpy().view(np.uint32))

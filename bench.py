@@ -344,7 +344,7 @@ def bench_batch(dev, stream, steps):
                         "top-2048 selection, decode, inverse RoPE, bf16 attn_out 32768->4096 "
                         "(BASELINE configs[4])",
             "us_per_step_layer": round(ms * 1e3, 2), "us_per_step_layer_eager": round(ms_eager * 1e3, 2),
-            "timing": ("HIP graph replay of the step (us_per_step_layer_eager: 13 launches from Python)"
+            "timing": ("HIP graph replay of the step (us_per_step_layer_eager: the same launches from Python)"
                        if graph_error is None else f"eager step (graph capture failed: {graph_error})"),
             "bytes": b,
             "gbs": round(b / (ms * 1e-3) / 1e9, 1),

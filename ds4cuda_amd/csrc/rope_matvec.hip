@@ -559,7 +559,7 @@ __device__ inline void mm_compute(const MmFrag<kF32W> &f, bool bok, float4_t *ac
     }
 }
 
-// grid.z selects one of two (W, Y) pairs with the same shape and X. The four
+// grid.z selects the (W, Y) pair (MmMats, below). The four
 // waves of a workgroup take the same 64 rows and four consecutive k-slices;
 // their partial sums are added in LDS in wave order, and the workgroup stores
 // the k-group's partial to Y + blockIdx.y * n_batch * n_rows (no atomics): the

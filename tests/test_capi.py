@@ -91,6 +91,23 @@ def test_newer_entry_points_refuse_bad_arguments_on_the_host():
     assert dec([10], 100, DecodeOpts(2, 0)) == -22     # unknown P mode
     assert dec([10], 100, DecodeOpts(0, 7)) == -22     # unknown kernel
     assert dec([10], 100, row_idx=X, q=N) == -22       # (control: a null q is refused too)
+    assert dec([10], 100, DecodeOpts(0, 0, 3)) == -22  # unknown merge output form
+    assert dec([10], 100, DecodeOpts(0, 0, 1)) == -22  # Q8_0 output form without its buffers
+    assert dec([10], 100, DecodeOpts(0, 0, 2, -1)) == -22   # rotated output at a negative position
+    c1 = (C.c_longlong * 1)(10)
+    # a converted Q (q_is_f32 = 2) is read by the flat kernel only
+    assert l.ds4hip_flash_attn_decode_fp8(X, 2, C.c_longlong(0), X, C.c_longlong(0), X, C.c_longlong(0), X, X, X,
+                                          c1, 1, N, C.c_longlong(0), N, C.c_longlong(0), N, 0, 256, 64, 512, 64,
+                                          C.c_longlong(100), C.byref(DecodeOpts(0, 1)), X, ws_sz, 3, N) == -22
+    # the fused entry points' argument checks
+    assert l.ds4hip_flash_attn_q_prep_f32(N, C.c_longlong(0), 1, N, C.c_longlong(0), N) == -22
+    assert l.ds4hip_token_prologue_f32(N, N) == -22
+    assert l.ds4hip_compressor_emit_f32(1, X, 512, 4, 2, 0, X, X, X, N) == -22   # (pos + 1) % 4 != 0
+    assert l.ds4hip_attn_out_decode_q8_f32(N, N, N, N, N, 64, 512, 8, 1024, 4096, N, C.c_size_t(0), N) == -22
+    assert l.ds4hip_compressor_pair_step_batch_w32(1, N, 4096, 4, N, N, 0, N, N, N, N, C.c_size_t(0), N) == -22
+    assert l.ds4hip_compressor_pair_batch_scratch_bytes(16, 4096, 512, 128, 3) == 0   # ratio 3
+    assert l.ds4hip_batch_rows_push_f32(N, N, N, N, 512, 64, N) == -22
+    assert l.ds4hip_session_claim_raw_row(N, 0, N) == -22
     assert l.ds4hip_flash_attn_prefill_fp8(N, N, N, N, N, N, 4, 8, 64, 512, 64, N, C.c_size_t(0), 0, N) == -22
     assert l.ds4hip_flash_attn_prefill_fp8(N, N, N, N, N, N, 0, 8, 64, 512, 64, N, C.c_size_t(0), 2, N) == -22
     assert l.ds4hip_flash_attn_decode_mixed_f32_noalloc(N, N, N, N, N, N, 64, -1, 0, 512, N) == -22

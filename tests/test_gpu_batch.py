@@ -175,3 +175,45 @@ def test_indexer_batch_positions(gpu, key_kind):
         ref = np.zeros(top_k, np.int32)
         O.lib().orc_topk_positions(P(sc), C.c_int(n), C.c_int(top_k), C.c_int(recent), P(ref))
         assert np.array_equal(got[s, :top_k], ref), s
+
+
+@pytest.mark.parametrize("case", ["levels", "zero_ties", "all_equal", "recent_only"])
+def test_indexer_batch_select_edges(gpu, case):
+    """The batched selection (one workgroup per sequence, keys in LDS) at the
+    boundaries of its keys-per-thread count (1 to 9 candidates per thread),
+    with designed scores: one head, q = e_0, w = 1 and fp32 keys
+    give score = relu(key[0]) exactly. levels: ~20 score levels (ties
+    everywhere); zero_ties: most keys relu to 0 and the selection reaches into
+    them; all_equal: every key ties; recent_only: the recent window is the
+    whole top-k (nothing selected). Positions bit-exact against the oracle's
+    (score desc, index asc) rule."""
+    top_k, recent = 512, 512 if case == "recent_only" else 64
+    # n = 513 .. 9064: 449, 1024, 1025, 2048, 2049, 4096, 4097 and 9000 candidates
+    n_comp = [513, 1088, 1089, 2112, 2113, 4160, 4161, 9064]
+    n_seq = len(n_comp)
+    row0 = np.concatenate([[0], np.cumsum(n_comp)[:-1]]) + 3
+    n_rows = int(row0[-1] + n_comp[-1])
+    rng = np.random.default_rng(23)
+    k = rng.standard_normal((n_rows, 128)).astype(np.float32)
+    if case in ("levels", "recent_only"):
+        k[:, 0] = np.round(rng.standard_normal(n_rows) * 4) / 4
+    elif case == "zero_ties":
+        k[:, 0] = rng.standard_normal(n_rows) - 1.5
+    else:
+        k[:, 0] = 0.5
+    q = np.zeros((n_seq, 1, 128), np.float32)
+    q[:, 0, 0] = 1.0
+    w = np.ones((n_seq, 1), np.float32)
+    scores = torch.zeros(n_rows, device=gpu)
+    pos = torch.full((n_seq, top_k), -1, dtype=torch.int32, device=gpu)
+    ops.indexer_topk_positions_batch(t(q, gpu), t(w, gpu), t(k, gpu), row0, n_comp, top_k, recent,
+                                     scores, pos)
+    torch.cuda.synchronize()
+    got = pos.cpu().numpy()
+    for s in range(n_seq):
+        n = n_comp[s]
+        sc = np.maximum(k[row0[s]:row0[s] + n, 0], 0).astype(np.float32)
+        assert np.array_equal(scores.cpu().numpy()[row0[s]:row0[s] + n], sc)
+        ref = np.zeros(top_k, np.int32)
+        O.lib().orc_topk_positions(P(sc), C.c_int(n), C.c_int(top_k), C.c_int(recent), P(ref))
+        assert np.array_equal(got[s], ref), (s, n)

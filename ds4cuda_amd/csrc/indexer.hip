@@ -898,7 +898,9 @@ __global__ __launch_bounds__(256) void score_batch_kernel(const BatchArgs A) {
 // then lane 0's and lane 32's warp sums combined as warp 0 combines them.
 // Many keys per launch need few registers per key; this form suits a few
 // thousand keys, where one thread per key would leave most CUs idle.
-constexpr int kHeadsKpw = 8;                    // keys per wave
+// Two keys per wave (one pair of chains) gives the most workgroups; eight
+// measured 135 us slower per token over 43 layers at context 4096.
+constexpr int kHeadsKpw = 2;                    // keys per wave
 constexpr int kHeadsKpb = 4 * kHeadsKpw;        // keys per workgroup
 constexpr long long kHeadsMaxKeys = 8192;       // up to this many keys per launch (measured crossover range)
 template <int kKind>
@@ -927,7 +929,7 @@ __global__ __launch_bounds__(256) void score_heads_kernel(const BatchArgs A) {
     constexpr int kEsz = kKind == 0 ? 4 : 2;
     constexpr int kPer = 16 / kEsz;                    // elements per load
     constexpr int kRowVecs = kMaxDim / kPer;
-    constexpr int kLoads = kHeadsKpb * kRowVecs / 256;
+    constexpr int kLoads = (kHeadsKpb * kRowVecs + 255) / 256;
     const int rows_here = min(n - c0, kHeadsKpb);
     const char *kbase = static_cast<const char *>(A.keys) + (size_t)(k0 + c0) * kMaxDim * kEsz;
     if (rows_here > 0 && (reinterpret_cast<uintptr_t>(kbase) & 15) == 0) {
@@ -941,6 +943,7 @@ __global__ __launch_bounds__(256) void score_heads_kernel(const BatchArgs A) {
 #pragma unroll
         for (int u = 0; u < kLoads; ++u) {
             const int vi = (int)threadIdx.x + 256 * u;
+            if (vi >= kHeadsKpb * kRowVecs) break;   // a block of few bf16 rows: fewer vectors than threads
             const bool in = vi / kRowVecs < rows_here;
             float f[kPer];
 #pragma unroll

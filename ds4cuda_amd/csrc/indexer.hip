@@ -256,22 +256,23 @@ __device__ inline void load_key32(const void *__restrict__ keys, int c, int part
 }
 
 // Two keys (c0, c1) per group of four lanes: their chains are independent,
-// which gives the VALU two dependency chains to interleave. Scores are valid
-// in part 3.
-template <int kKind>
+// which gives the VALU two dependency chains to interleave. The group runs
+// kLeaves consecutive leaves (heads, in bit-reversed order within their
+// warp), from leaf0, of the reference's block (a whole warp: 32), and part 3
+// returns their subtree of the warp's butterfly for both keys.
+template <int kKind, int kLeaves>
 __device__ __attribute__((always_inline)) inline void score_chain4x2(const float *qs, const float *ws,
                                                                      const void *__restrict__ keys,
                                                                      int c0, int c1, int n_head, int part,
-                                                                     float *pbuf, int kl0, int kl1,
-                                                                     float &s0, float &s1) {
+                                                                     float *pbuf, int kl0, int kl1, int leaf0,
+                                                                     float &w0, float &w1) {
     float k0[32], k1[32];
     load_key32<kKind>(keys, c0, part, k0);
     load_key32<kKind>(keys, c1, part, k1);
     float carry0 = 0.0f, carry1 = 0.0f;
-    const int n_leaves = (n_head + 31) & ~31;
-    for (int i = 0; i < n_leaves + 3; ++i) {
-        const int leaf = i - part;
-        const bool in = leaf >= 0 && leaf < n_leaves;
+    for (int i = 0; i < kLeaves + 3; ++i) {
+        const int leaf = leaf0 + i - part;
+        const bool in = i - part >= 0 && i - part < kLeaves;
         const int h = in ? head_of_leaf(leaf) : 0;
         const bool act = in && h < n_head;
         const float4_t *qv = reinterpret_cast<const float4_t *>(qs + (act ? h : 0) * kQStride + 32 * part);
@@ -296,25 +297,20 @@ __device__ __attribute__((always_inline)) inline void score_chain4x2(const float
         }
     }
     // In leaf order the butterfly of a warp of heads is a balanced tree of
-    // adjacent pairs; warp 0 then combines the two warp sums.
+    // adjacent pairs.
     if (part == 3) {
-        float w[2][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}};
-        for (int wv = 0; wv < n_leaves / 32; ++wv) {
 #pragma unroll
-            for (int z = 0; z < 2; ++z) {
-                const int kl = z ? kl1 : kl0;
-                float v[32];
+        for (int z = 0; z < 2; ++z) {
+            const int kl = z ? kl1 : kl0;
+            float v[kLeaves];
 #pragma unroll
-                for (int t = 0; t < 32; ++t) v[t] = pbuf[(32 * wv + t) * kBatchKeys + kl];
+            for (int t = 0; t < kLeaves; ++t) v[t] = pbuf[(leaf0 + t) * kBatchKeys + kl];
 #pragma unroll
-                for (int n = 16; n >= 1; n >>= 1)
+            for (int n = kLeaves / 2; n >= 1; n >>= 1)
 #pragma unroll
-                    for (int t = 0; t < n; ++t) v[t] = v[2 * t] + v[2 * t + 1];
-                w[z][wv] = v[0];
-            }
+                for (int t = 0; t < n; ++t) v[t] = v[2 * t] + v[2 * t + 1];
+            (z ? w1 : w0) = v[0];
         }
-        s0 = (w[0][0] + 0.0f) + (w[0][1] + 0.0f);
-        s1 = (w[1][0] + 0.0f) + (w[1][1] + 0.0f);
     }
 }
 
@@ -842,8 +838,16 @@ struct BatchArgs {
 };
 
 // kSplit threads per key (1 or 4); blocks of 256 threads cover 256 / kSplit keys.
-template <int kKind, int kSplit>
-__global__ __launch_bounds__(256) void score_batch_kernel(const BatchArgs A) {
+// Four chained lanes per key, two keys per lane group, 128 keys per
+// workgroup of 2 x 256 threads: thread group g runs the leaves of warp g of
+// the reference's block (heads 32 g .. 32 g + 31) for the same keys, so a
+// wave's chain is half as long and the launch has twice the waves (cfg-5
+// layer-step 195.5 -> 187.2 us; four groups of 16 leaves measured the same);
+// the two warp sums meet in LDS for warp 0's combine.
+constexpr int kGroups = 2;
+template <int kKind>
+__global__ __launch_bounds__(256 * kGroups) void score_batch_kernel(const BatchArgs A) {
+    constexpr int kLeaves = kMaxHeads / kGroups;
     int s = 0;
 #pragma unroll
     for (int i = 1; i < kMaxSeq; ++i)
@@ -860,32 +864,38 @@ __global__ __launch_bounds__(256) void score_batch_kernel(const BatchArgs A) {
 #pragma unroll
     for (int i = 0; i < kMaxSeq; ++i)
         if (i == s) first = A.blk0[i];
-    const int c = ((int)blockIdx.x - first) * (kSplit == 1 ? 256 : 128) + (int)threadIdx.x / kSplit;
+    const int grp = (int)threadIdx.x >> 8, tl = (int)threadIdx.x & 255;
+    const int c = ((int)blockIdx.x - first) * kBatchKeys + tl / 4;
     __shared__ __attribute__((aligned(16))) float qs[kMaxHeads * kQStride];
     __shared__ float ws[kMaxHeads];
-    __shared__ float pbuf[kSplit == 1 ? 1 : kMaxHeads * kBatchKeys];   // [leaf][key of the block]
+    __shared__ float pbuf[kMaxHeads * kBatchKeys];   // [leaf][key of the block]
+    __shared__ float sub[kGroups][kBatchKeys];       // subtree sums per key of the block
     const float *qg = A.q + (size_t)s * A.n_head * kMaxDim;
     const float *wg = A.w + (size_t)s * A.n_head;
-    if (kSplit == 1)
-        stage_query(qs, qg, A.n_head);
-    else
-        stage_query<kQStride>(qs, qg, A.n_head);
-    for (int i = threadIdx.x; i < A.n_head; i += 256) ws[i] = wg[i];
-    if (kSplit == 1) pad_heads(qs, ws, A.n_head);
+    if (grp == 0) stage_query<kQStride>(qs, qg, A.n_head);
+    for (int i = threadIdx.x; i < A.n_head; i += 256 * kGroups) ws[i] = wg[i];
     __syncthreads();
-    if (c >= n) return;   // the kSplit lanes of a key leave together
-    if (kSplit == 1) {
-        A.scores[k0 + c] = score_lds<kKind>(qs, ws, A.keys, (int)(k0 + c), A.n_head);
-    } else {
-        // keys c and c + 64 of this block's 128
-        const int c1 = c + 64;
-        float s0, s1;
-        const int kl = (int)threadIdx.x / kSplit;   // the group's first key within the block
-        score_chain4x2<kKind>(qs, ws, A.keys, (int)(k0 + c), (int)(k0 + (c1 < n ? c1 : c)), A.n_head,
-                              (int)threadIdx.x % kSplit, pbuf, kl, kl + 64, s0, s1);
-        if (threadIdx.x % kSplit == kSplit - 1) {
-            A.scores[k0 + c] = s0;
-            if (c1 < n) A.scores[k0 + c1] = s1;
+    const int part = tl % 4;
+    const int kl = tl / 4;   // the group's first key within the block; the second is kl + 64
+    const int c1 = c + 64;
+    const int n_leaves = (A.n_head + 31) & ~31;   // an absent warp 1 adds +0.0f
+    const int leaf0 = grp * kLeaves;
+    float s0 = 0.0f, s1 = 0.0f;
+    if (c < n && leaf0 < n_leaves)
+        score_chain4x2<kKind, kLeaves>(qs, ws, A.keys, (int)(k0 + c), (int)(k0 + (c1 < n ? c1 : c)), A.n_head,
+                                       part, pbuf, kl, kl + 64, leaf0, s0, s1);
+    if (part == 3) {
+        sub[grp][kl] = s0;
+        sub[grp][kl + 64] = s1;
+    }
+    __syncthreads();
+    if (grp == 0 && part == 3 && c < n) {
+#pragma unroll
+        for (int z = 0; z < 2; ++z) {
+            const int k = kl + 64 * z;
+            const float w0 = sub[0][k], w1 = sub[1][k];
+            // warp 0's 8-lane butterfly over (w0, w1, 0, ..., 0)
+            if (z == 0 || c1 < n) A.scores[k0 + c + 64 * z] = (w0 + 0.0f) + (w1 + 0.0f);
         }
     }
 }
@@ -1427,15 +1437,15 @@ extern "C" int ds4hip_indexer_topk_positions_batch(
         switch (key_kind) {
         case 0:
             if (heads) hipLaunchKernelGGL(score_heads_kernel<0>, g, b, 0, st, A);
-            else hipLaunchKernelGGL((score_batch_kernel<0, 4>), g, b, 0, st, A);
+            else hipLaunchKernelGGL(score_batch_kernel<0>, g, dim3(256 * kGroups), 0, st, A);
             break;
         case 1:
             if (heads) hipLaunchKernelGGL(score_heads_kernel<1>, g, b, 0, st, A);
-            else hipLaunchKernelGGL((score_batch_kernel<1, 4>), g, b, 0, st, A);
+            else hipLaunchKernelGGL(score_batch_kernel<1>, g, dim3(256 * kGroups), 0, st, A);
             break;
         default:
             if (heads) hipLaunchKernelGGL(score_heads_kernel<2>, g, b, 0, st, A);
-            else hipLaunchKernelGGL((score_batch_kernel<2, 4>), g, b, 0, st, A);
+            else hipLaunchKernelGGL(score_batch_kernel<2>, g, dim3(256 * kGroups), 0, st, A);
             break;
         }
     }

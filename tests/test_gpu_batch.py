@@ -136,12 +136,15 @@ def test_compressor_batch_matches_per_sequence(gpu):
           f"FP8 midpoint flips {flips}")
 
 
+@pytest.mark.parametrize("sizes", ["few", "many"])
 @pytest.mark.parametrize("key_kind", [0, 1, 2])
-def test_indexer_batch_positions(gpu, key_kind):
+def test_indexer_batch_positions(gpu, key_kind, sizes):
     """Batched scorer + selection for fp32 (0), f16 (1) and bf16 (2) keys:
-    scores and positions bit-exact against the oracle per sequence."""
-    n_seq, top_k, recent = 6, 512, 64
-    n_comp = [100, 512, 513, 2000, 4000, 3]
+    scores and positions bit-exact against the oracle per sequence. few: up
+    to 8192 keys scored in all (the lane-per-head scorer); many: more (the
+    four-lane scorer)."""
+    n_comp = [100, 512, 513, 2000, 4000, 3] + ([5000, 700] if sizes == "many" else [])
+    n_seq, top_k, recent = len(n_comp), 512, 64
     row0 = np.concatenate([[0], np.cumsum(n_comp)[:-1]]) + 10
     n_rows = int(row0[-1] + n_comp[-1])
     kf = synth.normal(55, 1, n_rows * 128).reshape(n_rows, 128)

@@ -1096,7 +1096,16 @@ __global__ __launch_bounds__(1024) void select_batch_kernel(const BatchArgs A) {
     const int recent = A.n_recent < A.top_k ? A.n_recent : A.top_k;
     const int n_cand = n - recent;
     const unsigned need0 = (unsigned)(A.top_k - recent);
-    for (int i = t; i < n_cand; i += 1024) keys[i] = ord_key(A.scores[k0 + i]);
+    // four loads in flight per thread (clamped, not branched): a strided copy
+    // loop would wait for each load in turn
+    for (int b = 0; b < n_cand; b += 4096) {
+        unsigned v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = ord_key(A.scores[k0 + min(b + 1024 * u + t, n_cand - 1)]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (b + 1024 * u + t < n_cand) keys[b + 1024 * u + t] = v[u];
+    }
     // radix select of the need0-th largest key, 8 bits at a time. Two
     // histograms alternate by pass, so a pass is two barriers: every wave
     // reads the whole histogram (4 bins per lane) and finds the threshold

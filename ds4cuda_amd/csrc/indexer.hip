@@ -912,7 +912,10 @@ __global__ __launch_bounds__(256 * kGroups) void score_batch_kernel(const BatchA
 // measured 135 us slower per token over 43 layers at context 4096.
 constexpr int kHeadsKpw = 2;                    // keys per wave
 constexpr int kHeadsKpb = 4 * kHeadsKpw;        // keys per workgroup
-constexpr long long kHeadsMaxKeys = 8192;       // up to this many keys per launch (measured crossover range)
+// Up to this many keys per launch. Measured (one sequence, 64 heads, fp32
+// keys): this form 5.2 / 8.6 / 12.4 / 22.0 us at 1500 / 3000 / 6000 / 12000
+// keys, the four-lane form 19.3 / 19.6 / 20.0 us at 3000 / 6000 / 12000.
+constexpr long long kHeadsMaxKeys = 10240;
 template <int kKind>
 __global__ __launch_bounds__(256) void score_heads_kernel(const BatchArgs A) {
     int s = 0;

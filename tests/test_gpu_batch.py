@@ -141,7 +141,7 @@ def test_compressor_batch_matches_per_sequence(gpu):
 def test_indexer_batch_positions(gpu, key_kind, sizes):
     """Batched scorer + selection for fp32 (0), f16 (1) and bf16 (2) keys:
     scores and positions bit-exact against the oracle per sequence. few: up
-    to 8192 keys scored in all (the lane-per-head scorer); many: more (the
+    to 10240 keys scored in all (the lane-per-head scorer); many: more (the
     four-lane scorer)."""
     n_comp = [100, 512, 513, 2000, 4000, 3] + ([5000, 700] if sizes == "many" else [])
     n_seq, top_k, recent = len(n_comp), 512, 64

@@ -845,8 +845,10 @@ struct BatchArgs {
 // layer-step 195.5 -> 187.2 us; four groups of 16 leaves measured the same);
 // the two warp sums meet in LDS for warp 0's combine.
 constexpr int kGroups = 2;
+constexpr int kHalf = kBatchKeys / 2;            // a lane group's second key: kl + kHalf
+constexpr int kGroupThreads = 4 * kHalf;         // threads of one leaf group
 template <int kKind>
-__global__ __launch_bounds__(256 * kGroups) void score_batch_kernel(const BatchArgs A) {
+__global__ __launch_bounds__(kGroupThreads * kGroups) void score_batch_kernel(const BatchArgs A) {
     constexpr int kLeaves = kMaxHeads / kGroups;
     int s = 0;
 #pragma unroll
@@ -864,7 +866,7 @@ __global__ __launch_bounds__(256 * kGroups) void score_batch_kernel(const BatchA
 #pragma unroll
     for (int i = 0; i < kMaxSeq; ++i)
         if (i == s) first = A.blk0[i];
-    const int grp = (int)threadIdx.x >> 8, tl = (int)threadIdx.x & 255;
+    const int grp = (int)threadIdx.x / kGroupThreads, tl = (int)threadIdx.x % kGroupThreads;
     const int c = ((int)blockIdx.x - first) * kBatchKeys + tl / 4;
     __shared__ __attribute__((aligned(16))) float qs[kMaxHeads * kQStride];
     __shared__ float ws[kMaxHeads];
@@ -872,30 +874,30 @@ __global__ __launch_bounds__(256 * kGroups) void score_batch_kernel(const BatchA
     __shared__ float sub[kGroups][kBatchKeys];       // subtree sums per key of the block
     const float *qg = A.q + (size_t)s * A.n_head * kMaxDim;
     const float *wg = A.w + (size_t)s * A.n_head;
-    if (grp == 0) stage_query<kQStride>(qs, qg, A.n_head);
-    for (int i = threadIdx.x; i < A.n_head; i += 256 * kGroups) ws[i] = wg[i];
+    if (threadIdx.x < 256) stage_query<kQStride>(qs, qg, A.n_head);
+    for (int i = threadIdx.x; i < A.n_head; i += kGroupThreads * kGroups) ws[i] = wg[i];
     __syncthreads();
     const int part = tl % 4;
-    const int kl = tl / 4;   // the group's first key within the block; the second is kl + 64
-    const int c1 = c + 64;
+    const int kl = tl / 4;   // the group's first key within the block; the second is kl + kHalf
+    const int c1 = c + kHalf;
     const int n_leaves = (A.n_head + 31) & ~31;   // an absent warp 1 adds +0.0f
     const int leaf0 = grp * kLeaves;
     float s0 = 0.0f, s1 = 0.0f;
     if (c < n && leaf0 < n_leaves)
         score_chain4x2<kKind, kLeaves>(qs, ws, A.keys, (int)(k0 + c), (int)(k0 + (c1 < n ? c1 : c)), A.n_head,
-                                       part, pbuf, kl, kl + 64, leaf0, s0, s1);
+                                       part, pbuf, kl, kl + kHalf, leaf0, s0, s1);
     if (part == 3) {
         sub[grp][kl] = s0;
-        sub[grp][kl + 64] = s1;
+        sub[grp][kl + kHalf] = s1;
     }
     __syncthreads();
     if (grp == 0 && part == 3 && c < n) {
 #pragma unroll
         for (int z = 0; z < 2; ++z) {
-            const int k = kl + 64 * z;
+            const int k = kl + kHalf * z;
             const float w0 = sub[0][k], w1 = sub[1][k];
             // warp 0's 8-lane butterfly over (w0, w1, 0, ..., 0)
-            if (z == 0 || c1 < n) A.scores[k0 + c + 64 * z] = (w0 + 0.0f) + (w1 + 0.0f);
+            if (z == 0 || c1 < n) A.scores[k0 + c + kHalf * z] = (w0 + 0.0f) + (w1 + 0.0f);
         }
     }
 }
@@ -1430,7 +1432,7 @@ extern "C" int ds4hip_indexer_topk_positions_batch(
     for (int s = 0; s < n_seq; ++s)
         if (n_comp_host[s] > top_k) n_scored += n_comp_host[s];
     const bool heads = n_scored <= kHeadsMaxKeys;
-    const int keys_per_blk = heads ? kHeadsKpb : 128;
+    const int keys_per_blk = heads ? kHeadsKpb : kBatchKeys;
     int blk = 0;
     for (int s = 0; s < kMaxSeq; ++s) {
         const int n = s < n_seq ? n_comp_host[s] : 0;
@@ -1449,15 +1451,15 @@ extern "C" int ds4hip_indexer_topk_positions_batch(
         switch (key_kind) {
         case 0:
             if (heads) hipLaunchKernelGGL(score_heads_kernel<0>, g, b, 0, st, A);
-            else hipLaunchKernelGGL(score_batch_kernel<0>, g, dim3(256 * kGroups), 0, st, A);
+            else hipLaunchKernelGGL(score_batch_kernel<0>, g, dim3(kGroupThreads * kGroups), 0, st, A);
             break;
         case 1:
             if (heads) hipLaunchKernelGGL(score_heads_kernel<1>, g, b, 0, st, A);
-            else hipLaunchKernelGGL(score_batch_kernel<1>, g, dim3(256 * kGroups), 0, st, A);
+            else hipLaunchKernelGGL(score_batch_kernel<1>, g, dim3(kGroupThreads * kGroups), 0, st, A);
             break;
         default:
             if (heads) hipLaunchKernelGGL(score_heads_kernel<2>, g, b, 0, st, A);
-            else hipLaunchKernelGGL(score_batch_kernel<2>, g, dim3(256 * kGroups), 0, st, A);
+            else hipLaunchKernelGGL(score_batch_kernel<2>, g, dim3(kGroupThreads * kGroups), 0, st, A);
             break;
         }
     }
